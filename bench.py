@@ -1,0 +1,228 @@
+"""LUT layer forward+backward benchmark (BASELINE config 3 by default).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3|1|4] [--no-cpu-baseline]
+
+A step is one forward + backward of the dense LUT layer through its autograd
+function (LUTForwardFN via LUTLayer.__call__ and Tensor.backward) on one batch
+of synthetic, HBM-resident input: the same work the reference's
+LUTLayer.forward/backward_step perform (check_detectors, fill_outputs,
+propagate_through_detectors, gather_w_gradients) plus the layer's own
+allocations.  Per-kernel GPU times come from HIP events recorded on the launch
+stream inside the timed region.  The CPU baseline is the C oracle (a serial
+restatement of the reference's CPU path) timed on one host core on a bounded
+batch of the same workload.
+
+Prints one JSON line on stdout; progress goes to stderr.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0  # MI355X HBM3E peak
+
+CONFIGS = {
+    # name: (B, I, T, Nc, O, x_dist, cpu_sample_B)
+    1: (64, 784, 256, 6, 10, "uniform", 64),
+    3: (1024, 4096, 8192, 8, 1024, "normal", 16),
+}
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def g_model_bytes(B, I, T, Nc, O, w=4):
+    """Algorithmic bytes per kernel family, gather model: every logical row
+    access counts once per use."""
+    return {
+        "check_detectors": B * I * 4 + T * Nc * 8 + B * T * 12,
+        "fill_outputs_fc": B * T * O * w + B * O * 4,
+        "propagate_fc": 2 * B * T * O * 4 + B * O * 4 + B * T * 12 + B * I * 4 + T * Nc * 8,
+        "gather_w_gradients_fc": 2 * B * T * O * 4,
+    }
+
+
+def compulsory_bytes(B, I, T, Nc, O):
+    """Unique bytes a step must move at least: the tables read in forward and
+    backward, and the weight gradient written once."""
+    E = 1 << Nc
+    return 3 * T * E * O * 4 + 2 * B * I * 4 + 2 * B * O * 4 + B * T * 12
+
+
+def make_anchors(T, I, Nc, seed, device):
+    """Nc distinct (a1, a2) pairs per table: 2*Nc distinct inputs drawn without
+    replacement per table, paired in order."""
+    import torch
+    g = torch.Generator(device=device).manual_seed(seed)
+    perm = torch.rand(T, I, device=device, generator=g).argsort(dim=1)[:, :2 * Nc]
+    return perm.to(torch.int32).reshape(-1).contiguous()
+
+
+def load_traffic(kernel, config):
+    path = os.path.join(ROOT, "profiles", f"pmc_{kernel}_config{config}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
+def cpu_baseline(x, anchors, W, go, B_full, I, T, Nc, O, sample_B):
+    """Times the C oracle on one host core over the first sample_B samples:
+    forward (indices + gather-sum) and backward (propagate + weight gradient),
+    including the caller-side zero-fill of out, x_grad and w_grad that the
+    reference's LUTLayer performs (LUTLayer.py:631,851,864)."""
+    import numpy as np
+    import oracle
+    E = 1 << Nc
+    log(f"cpu baseline: copying tables to host ({W.numel() * 4 / 1e9:.1f} GB)")
+    Wn = W.cpu().numpy()
+    xn = x[:sample_B * I].cpu().numpy()
+    gn = go[:sample_B * O].cpu().numpy()
+    an = anchors.cpu().numpy()
+    wg = np.empty(T * E * O, np.float32)
+    times = []
+    zero_fill = []
+    for rep in range(4):
+        t0 = time.perf_counter()
+        out = np.zeros(sample_B * O, np.float32)
+        idx, md, mi = oracle.check_detectors(xn, an, sample_B, I, T, Nc)
+        oracle.fill_outputs_fc(Wn, idx, sample_B, O, T, E, out=out)
+        xg = np.zeros(sample_B * I, np.float32)
+        tz = time.perf_counter()
+        wg.fill(0.0)
+        zero_fill.append(time.perf_counter() - tz)
+        oracle.propagate_fc(Wn, gn, idx, md, mi, an, sample_B, I, O, T, Nc, E, x_grad=xg)
+        oracle.gather_wgrad_fc(gn, idx, wg, sample_B, O, T, E)
+        dt = time.perf_counter() - t0
+        log(f"cpu baseline rep {rep}: {dt:.2f} s")
+        if rep > 0:
+            times.append(dt)
+    med = float(np.median(times))
+    return {
+        "value": sample_B / med,
+        "unit": "samples/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"config workload at batch {sample_B} of {B_full} (same tables, anchors, inputs); "
+                   f"median of 3 timed steps after 1 warm-up; step {med:.3f} s of which w_grad "
+                   f"zero-fill {float(np.median(zero_fill[1:])):.3f} s"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build's LUT path runs on a single MI355X "
+              "(the multi-GPU table-parallel design is described, not built).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from spiky_amd import LUTLayer
+
+    B, I, T, Nc, O, xdist, cpu_B = CONFIGS[args.config]
+    E = 1 << Nc
+    dev = torch.device("cuda:0")
+    log(f"config {args.config}: B={B} I={I} T={T} Nc={Nc} O={O}")
+    anchors = make_anchors(T, I, Nc, 1, dev)
+    layer = LUTLayer(I, Nc, T, O, _explicit_anchors=anchors, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(2)
+    with torch.no_grad():
+        layer._weights.normal_(0.0, 0.01, generator=gen)
+    gx = torch.Generator(device=dev).manual_seed(0)
+    x = (torch.randn(B, 1, I, device=dev, generator=gx) if xdist == "normal"
+         else torch.rand(B, 1, I, device=dev, generator=gx))
+    x.requires_grad_(True)
+    gg = torch.Generator(device=dev).manual_seed(3)
+    go = torch.randn(B, 1, O, device=dev, generator=gg)
+    dm = layer._lut_dm
+
+    def step():
+        layer._weights.grad = None
+        x.grad = None
+        y = layer(x)
+        y.backward(go)
+
+    log("warmup")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    dm.get_kernel_times(reset=True)
+    dm.set_kernel_timing(True)
+    log(f"timing {args.steps} steps")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    dm.set_kernel_timing(False)
+    ktimes = dm.get_kernel_times(reset=True)
+    ms_per_step = (t1 - t0) * 1e3 / args.steps
+    value = B / (ms_per_step / 1e3)
+    log(f"{ms_per_step:.3f} ms/step, {value:.1f} samples/s; kernels {ktimes}")
+
+    gbytes = g_model_bytes(B, I, T, Nc, O)
+    per_kernel = {}
+    for name, (cnt, tot) in ktimes.items():
+        ms = tot / max(cnt, 1)
+        b = gbytes.get(name)
+        per_kernel[name] = {"ms_per_launch": round(ms, 4),
+                            "gbs_g_model": round(b / (ms * 1e-3) / 1e9, 1) if b else None}
+    dom = max(ktimes.items(), key=lambda kv: kv[1][1])[0]
+    dom_ms = ktimes[dom][1] / ktimes[dom][0]
+    achieved = gbytes[dom] / (dom_ms * 1e-3) / 1e9
+    step_g = sum(gbytes.values())
+    roofline = {
+        "bound": "hbm",
+        "kernel": dom,
+        "achieved": round(achieved, 1),
+        "peak": PEAK_HBM_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / PEAK_HBM_GBS, 4),
+        "traffic": load_traffic(dom, args.config),
+        "algorithmic_bytes_per_launch": gbytes[dom],
+        "ms_per_launch": round(dom_ms, 4),
+        "step_g_model_frac": round(step_g / (ms_per_step * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+        "step_compulsory_frac": round(compulsory_bytes(B, I, T, Nc, O) / (ms_per_step * 1e-3) / 1e9
+                                      / PEAK_HBM_GBS, 4),
+        "kernels": per_kernel,
+    }
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(x.detach().reshape(-1), layer._detector_anchors, layer._weights.detach(),
+                           go.reshape(-1), B, I, T, Nc, O, cpu_B)
+    res = {
+        "metric": "LUT fwd+bwd samples/sec at 8192 tables; achieved HBM GB/s vs peak",
+        "value": round(value, 1),
+        "unit": "samples/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 (fp64 partial sums)",
+        "data": "synthetic (seeded N(0,1) inputs and grads, N(0,0.01) tables, anchors without replacement)",
+        "config": {"workload": f"BASELINE config {args.config}: dense LUT layer fwd+bwd", "batch": B,
+                   "n_inputs": I, "n_tables": T, "anchors_per_table": Nc, "n_outputs": O,
+                   "table_bytes": T * E * O * 4, "parallelism": "single GPU"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,161 @@
+/*
+ * spiky_lut.h -- C ABI of the MI355X-native LUT-layer hot path.
+ *
+ * One opaque manager object stands for one reference `LUTDataManagerF` /
+ * `LUTDataManagerI` (spiky_cuda/lut/lut.cu:16-128, pybind at lut.cu:1476-1656).
+ * The caller (Python via ctypes, or any FFI) owns every tensor: weights,
+ * anchors, activations and gradients are plain device pointers, sizes are
+ * plain integers, streams are `hipStream_t` passed as `void *`.  Nothing in
+ * these signatures depends on torch.
+ *
+ * Conventions (all as in the reference):
+ *   - weights  : fp32 [n_detectors * 2^n_anchors][n_outputs]   (row = t*E + idx)
+ *   - anchors  : int32 pairs [n_detectors][n_anchors][2]; -1 marks an unused pair
+ *   - input    : fp32 [batch][n_inputs];  output fp32 [batch][n_outputs]
+ *   - idx / min_deltas / min_delta_indices : [batch][n_detectors]
+ *   - outputs, input gradients and weight gradients are ACCUMULATED INTO, so
+ *     callers pass zeroed buffers (reference LUTLayer.py:631,851,864).  Entry
+ *     points with an `overwrite_*` flag may instead be told the buffer holds
+ *     garbage and is to be written, which skips the zero-fill pass.
+ *   - int32 summation managers keep partial sums as int32 fixed point
+ *     (DENOMINATOR32 = 0xFFFFF scaled by int_rescaler) inside the fp32 buffers
+ *     and convert back to fp32 before returning (lut_runtime_kernels_logic.proto:200-213).
+ *
+ * Return codes: SPIKY_OK, SPIKY_VALUE_ERROR (the reference raises ValueError),
+ * SPIKY_RUNTIME_ERROR (RuntimeError: HIP failures, bad device state).  The
+ * message of the last failure on the calling thread is spiky_lut_last_error().
+ */
+#ifndef SPIKY_LUT_H
+#define SPIKY_LUT_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SPIKY_OK 0
+#define SPIKY_VALUE_ERROR 1
+#define SPIKY_RUNTIME_ERROR 2
+
+typedef struct spiky_lut_manager spiky_lut_manager;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *spiky_lut_last_error(void);
+
+/* Library version string. */
+const char *spiky_lut_version(void);
+
+/* Replaces LUTDataManagerF/I::LUTDataManagerF/I (lut.cu:16-128; validation
+ * lut.cu:47-76).  summation_int32 != 0 gives the LUTDataManagerI behaviour
+ * with the given int_rescaler (aux/lut_I.cu:1-2). */
+int spiky_lut_create(uint32_t n_inputs, uint32_t n_outputs, uint32_t n_detectors,
+                     uint32_t n_anchors_per_detector, uint32_t sequence_length,
+                     uint32_t positional_dim, uint64_t initial_synapse_capacity,
+                     uint32_t forward_group_size, uint32_t backward_group_size,
+                     int summation_int32, double int_rescaler, spiky_lut_manager **out);
+
+/* Replaces the pybind destructor (lut.cu ~LUTDataManager). */
+void spiky_lut_destroy(spiky_lut_manager *m);
+
+/* Replaces register_synapse_meta (lut.cu:148-206). */
+int spiky_lut_register_synapse_meta(spiky_lut_manager *m, float learning_rate,
+                                    float min_synaptic_weight, float max_synaptic_weight,
+                                    float initial_noise_level, float initial_weight,
+                                    uint32_t *out_meta_index);
+
+/* Replaces initialize_neurons (lut.cu:208-243). */
+int spiky_lut_initialize_neurons(spiky_lut_manager *m, int is_fully_connected);
+
+/* Replaces get_number_of_lookup_neurons / get_weights_dimension /
+ * get_max_forward_groups_per_neuron / get_number_of_synapses
+ * (lut.cu:266-301). */
+uint64_t spiky_lut_n_lookup_neurons(const spiky_lut_manager *m);
+uint64_t spiky_lut_weights_dimension(const spiky_lut_manager *m);
+uint32_t spiky_lut_max_forward_groups_per_neuron(const spiky_lut_manager *m);
+uint64_t spiky_lut_n_synapses(const spiky_lut_manager *m);
+
+/* Replaces forward_step (lut.cu:629-716 -> lut_runtime.cu:76-211):
+ * check_detectors(_eval) then fill_outputs_non_seq_{fc,sparse}.
+ * min_deltas == NULL selects eval mode (lut_runtime.cu:104). */
+int spiky_lut_forward_step(spiky_lut_manager *m, const float *weights, uint32_t batch_size,
+                           const float *input, const int32_t *anchors, float *output,
+                           int32_t *lookup_indices, float cmp_eps, float *min_deltas,
+                           int32_t *min_delta_indices, void *stream);
+
+/* int8 tables with a per-detector fp32 scale, forward (eval or train).
+ * Weight of row entry = scales[t] * (float)q8[...] in fp32.  Fully connected
+ * managers only.  The int8 form has no counterpart in the reference (its
+ * tables are fp32, lut.h:55); it reuses forward_step's index and summation
+ * semantics (lut_runtime.cu:76-211) on the dequantised weight. */
+int spiky_lut_forward_step_i8(spiky_lut_manager *m, const int8_t *q8, const float *scales,
+                              uint32_t batch_size, const float *input, const int32_t *anchors,
+                              float *output, int32_t *lookup_indices, float cmp_eps,
+                              float *min_deltas, int32_t *min_delta_indices, void *stream);
+
+/* Replaces backward_backprop (lut.cu:1030-1088 -> lut_runtime.cu:213-397):
+ * propagate_through_detectors_non_seq_* into input_grad and
+ * gather_w_gradients_non_seq_* into weight_grad.  external_lr >= 0 selects the
+ * Internal policy: the weight update -lr*external_lr*g is applied to `weights`
+ * in place and weight_grad must be NULL (lut_runtime.cu:236-238).
+ * overwrite_weight_grad != 0 tells the library weight_grad holds garbage to be
+ * overwritten (no reference counterpart: it fuses the caller's zeros_like,
+ * LUTLayer.py:864, into the gradient kernel). */
+int spiky_lut_backward_backprop(spiky_lut_manager *m, float *weights, uint32_t batch_size,
+                                const float *output_grad, const int32_t *anchors,
+                                const int32_t *lookup_indices, const float *min_deltas,
+                                const int32_t *min_delta_indices, float *input_grad,
+                                double external_lr, float *weight_grad,
+                                int overwrite_weight_grad, void *stream);
+
+/* Replaces add_lookup_connections + compile for sparse managers
+ * (lut.cu:560-627) with this build's CSR: lookup neuron n owns synapses
+ * [syn_offsets[n], syn_offsets[n+1]) whose targets are output indices in
+ * syn_targets.  Host pointers; the library keeps a device copy.  The weight
+ * tensor of a sparse manager has one fp32 per synapse in the same order. */
+int spiky_lut_set_sparse_connectivity(spiky_lut_manager *m, const int64_t *syn_offsets,
+                                      const int32_t *syn_targets, uint64_t n_synapses);
+
+/* Replaces prepare_detectors_compact (lut_compile_time_kernels_logic.proto:70-125)
+ * over a CSR of each detector's ascending input list.  Host pointers.
+ * Returns SPIKY_VALUE_ERROR ("Some detectors have <= 1 input synapses",
+ * lut.cu:537-550) if a detector has fewer than two inputs. */
+int spiky_lut_decode_anchors_compact(const uint32_t *encoded_pairs, uint32_t n_detectors,
+                                     uint32_t max_pairs_per_detector, uint32_t n_anchors,
+                                     const int64_t *in_offsets, const int32_t *in_ids,
+                                     int32_t *anchors_out);
+
+/* Receptive-field index builder: replaces the reference's spatial growth
+ * engine for one GrowthCommand with probability p (synapse_growth.py:11-55,
+ * synapse_growth_kernels_logic.proto:69-374; inclusion test in fp32 at
+ * proto:229-256).  Host pointers.  Sources are visited in ascending id order;
+ * out_offsets[i]..out_offsets[i+1] delimit the ascending target ids of the
+ * i-th source in that order.  Call once with out_targets == NULL to get
+ * *out_total, then again with capacity >= *out_total.  cuboid = x1,y1,z1,x2,y2,z2
+ * relative to the source.  max_per_source == 0 means unbounded. */
+int spiky_grow_cuboid(uint32_t n_src, const int32_t *src_ids, const float *src_xyz,
+                      uint32_t n_tgt, const int32_t *tgt_ids, const float *tgt_xyz,
+                      const float *cuboid, float p, uint64_t seed, uint32_t max_per_source,
+                      int64_t *out_offsets, int32_t *out_targets, uint64_t capacity,
+                      uint64_t *out_total);
+
+/* Replaces get_profiling_stats / reset_profiler (lut.cu:1274-1290):
+ * per-operation call counts and host wall-clock (stream-ordered calls are
+ * timed only up to launch, since nothing here synchronises). */
+int spiky_lut_profiling_stats(const spiky_lut_manager *m, char *buf, uint64_t buf_len);
+void spiky_lut_reset_profiler(spiky_lut_manager *m);
+
+/* GPU-side timing of every launch with HIP events recorded on the launch
+ * stream (no reference counterpart: the reference's profiler times on the host
+ * after a device-wide synchronisation, misc.h:170-194).  While enabled, each
+ * kernel family's launches are bracketed by events; spiky_lut_kernel_times
+ * waits for the recorded events and writes one line "name count total_ms" per
+ * family (reset != 0 clears the totals). */
+int spiky_lut_set_kernel_timing(spiky_lut_manager *m, int enable);
+int spiky_lut_kernel_times(spiky_lut_manager *m, char *buf, uint64_t buf_len, int reset);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPIKY_LUT_H */

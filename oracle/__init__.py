@@ -1,0 +1,170 @@
+"""CPU oracle for the LUT hot path -- TEST INFRASTRUCTURE ONLY.
+
+Thin numpy/ctypes wrapper over ``liblut_oracle.so`` (built from
+``lut_oracle.c`` by ``oracle/Makefile``).  Only ``tests/``,
+``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg import
+this package, and only as the checker; the product (``spiky_amd``) never does.
+
+Every function restates the reference's single-threaded NO_CUDA path
+(``spiky_cuda/misc/misc.h:119-129``); the per-function citations live in the
+C source.  Arrays are numpy; outputs are accumulated into (as the reference
+does), so pass zero-filled arrays for a plain result.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liblut_oracle.so")
+_lib = None
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+_u32p = np.ctypeslib.ndpointer(dtype=np.uint32, flags="C_CONTIGUOUS")
+_i64p = np.ctypeslib.ndpointer(dtype=np.int64, flags="C_CONTIGUOUS")
+_i8p = np.ctypeslib.ndpointer(dtype=np.int8, flags="C_CONTIGUOUS")
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+_f64 = ctypes.c_double
+_int = ctypes.c_int
+
+
+def build():
+    """Compile liblut_oracle.so with the committed Makefile."""
+    subprocess.check_call(["make", "-s", "-C", _HERE])
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        L.oracle_decode_anchors_compact.argtypes = [_u32p, _i64, _i64, _i64, _i64p, _i32p, _i32p]
+        L.oracle_decode_anchors_compact.restype = _i64
+        L.oracle_check_detectors.argtypes = [_f32p, _i64, _i64, _i32p, _i64, _i64, _f32, _i32p, _vp, _vp]
+        L.oracle_fill_outputs_fc.argtypes = [_vp, _vp, _vp, _i32p, _f32p, _i64, _i64, _i64, _i64, _i64, _int, _f64]
+        L.oracle_convert_int_to_float.argtypes = [_f32p, _i64, _f64]
+        L.oracle_propagate_fc.argtypes = [_f32p, _f32p, _i32p, _f32p, _i32p, _i32p, _f32p,
+                                          _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _f64]
+        L.oracle_gather_wgrad_fc.argtypes = [_f32p, _i32p, _f32p, _i64, _i64, _i64, _i64, _i64,
+                                             _f32, _f32, _int, _f64]
+        L.oracle_fill_outputs_sparse.argtypes = [_f32p, _i32p, _i64p, _i32p, _f32p, _i64, _i64, _i64,
+                                                 _i64, _int, _f64]
+        L.oracle_propagate_sparse.argtypes = [_f32p, _f32p, _i32p, _f32p, _i32p, _i32p, _i64p, _i32p,
+                                              _f32p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                              _int, _f64]
+        L.oracle_gather_wgrad_sparse.argtypes = [_f32p, _i32p, _i64p, _i32p, _f32p, _i64, _i64, _i64,
+                                                 _i64, _f32, _f32, _int, _f64]
+        _lib = L
+    return _lib
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+# ---------------------------------------------------------------- anchors
+def decode_anchors_compact(encoded_pairs, n_detectors, max_pairs_per_detector, n_anchors,
+                           in_offsets, in_ids):
+    """Compact anchor decode; returns (anchors int32 [N_t*Nc*2], n_errors)."""
+    out = np.zeros(n_detectors * n_anchors * 2, dtype=np.int32)
+    err = lib().oracle_decode_anchors_compact(
+        _c(encoded_pairs, np.int64).astype(np.uint32), n_detectors, max_pairs_per_detector,
+        n_anchors, _c(in_offsets, np.int64), _c(in_ids, np.int32), out)
+    return out, int(err)
+
+
+# ---------------------------------------------------------------- FC path
+def check_detectors(x, anchors, batch, n_inputs, n_detectors, n_anchors, cmp_eps=0.0, train=True):
+    x = _c(x, np.float32)
+    anchors = _c(anchors, np.int32)
+    idx = np.zeros(batch * n_detectors, dtype=np.int32)
+    md = np.zeros(batch * n_detectors, dtype=np.float32) if train else None
+    mi = np.zeros(batch * n_detectors, dtype=np.int32) if train else None
+    lib().oracle_check_detectors(x, batch, n_inputs, anchors, n_detectors, n_anchors,
+                                 float(cmp_eps), idx, _ptr(md), _ptr(mi))
+    return (idx, md, mi) if train else idx
+
+
+def fill_outputs_fc(w, idx, batch, n_outputs, n_detectors, n_entries, dgs=32,
+                    out=None, int_mode=False, int_rescaler=1.0, q8=None, scales=None):
+    """Forward row gather-sum.  In int mode the result is the int32 accumulator
+    (reinterpretation of `out`); call convert_int_to_float for the fp32 view."""
+    if out is None:
+        out = np.zeros(batch * n_outputs, dtype=np.float32)
+    if q8 is not None:
+        q8 = _c(q8, np.int8)
+        scales = _c(scales, np.float32)
+        w = None
+    else:
+        w = _c(w, np.float32)
+    lib().oracle_fill_outputs_fc(_ptr(w), _ptr(q8), _ptr(scales), _c(idx, np.int32), out,
+                                 batch, n_outputs, n_detectors, n_entries, dgs,
+                                 int(int_mode), float(int_rescaler))
+    return out
+
+
+def convert_int_to_float(buf, int_rescaler):
+    lib().oracle_convert_int_to_float(buf, buf.size, float(int_rescaler))
+    return buf
+
+
+def propagate_fc(w, g, idx, md, mi, anchors, batch, n_inputs, n_outputs, n_detectors,
+                 n_anchors, n_entries, ogs=32, x_grad=None, int_mode=False, int_rescaler=1.0):
+    if x_grad is None:
+        x_grad = np.zeros(batch * n_inputs, dtype=np.float32)
+    lib().oracle_propagate_fc(_c(w, np.float32), _c(g, np.float32), _c(idx, np.int32),
+                              _c(md, np.float32), _c(mi, np.int32), _c(anchors, np.int32), x_grad,
+                              batch, n_inputs, n_outputs, n_detectors, n_anchors, n_entries, ogs,
+                              int(int_mode), float(int_rescaler))
+    return x_grad
+
+
+def gather_wgrad_fc(g, idx, target, batch, n_outputs, n_detectors, n_entries, ogs=32,
+                    first_meta_lr=1.0, external_lr=-1.0, int_mode=False, int_rescaler=1.0):
+    lib().oracle_gather_wgrad_fc(_c(g, np.float32), _c(idx, np.int32), target, batch, n_outputs,
+                                 n_detectors, n_entries, ogs, float(first_meta_lr),
+                                 float(external_lr), int(int_mode), float(int_rescaler))
+    return target
+
+
+# ---------------------------------------------------------------- sparse path
+def fill_outputs_sparse(w, idx, syn_offsets, syn_targets, batch, n_outputs, n_detectors,
+                        n_entries, out=None, int_mode=False, int_rescaler=1.0):
+    if out is None:
+        out = np.zeros(batch * n_outputs, dtype=np.float32)
+    lib().oracle_fill_outputs_sparse(_c(w, np.float32), _c(idx, np.int32), _c(syn_offsets, np.int64),
+                                     _c(syn_targets, np.int32), out, batch, n_outputs, n_detectors,
+                                     n_entries, int(int_mode), float(int_rescaler))
+    return out
+
+
+def propagate_sparse(w, g, idx, md, mi, anchors, syn_offsets, syn_targets, batch, n_inputs,
+                     n_outputs, n_detectors, n_anchors, n_entries, fgs, max_groups,
+                     x_grad=None, int_mode=False, int_rescaler=1.0):
+    if x_grad is None:
+        x_grad = np.zeros(batch * n_inputs, dtype=np.float32)
+    lib().oracle_propagate_sparse(_c(w, np.float32), _c(g, np.float32), _c(idx, np.int32),
+                                  _c(md, np.float32), _c(mi, np.int32), _c(anchors, np.int32),
+                                  _c(syn_offsets, np.int64), _c(syn_targets, np.int32), x_grad,
+                                  batch, n_inputs, n_outputs, n_detectors, n_anchors, n_entries,
+                                  fgs, max_groups, int(int_mode), float(int_rescaler))
+    return x_grad
+
+
+def gather_wgrad_sparse(g, idx, syn_offsets, syn_targets, target, batch, n_outputs, n_detectors,
+                        n_entries, first_meta_lr=1.0, external_lr=-1.0, int_mode=False,
+                        int_rescaler=1.0):
+    lib().oracle_gather_wgrad_sparse(_c(g, np.float32), _c(idx, np.int32), _c(syn_offsets, np.int64),
+                                     _c(syn_targets, np.int32), target, batch, n_outputs,
+                                     n_detectors, n_entries, float(first_meta_lr),
+                                     float(external_lr), int(int_mode), float(int_rescaler))
+    return target

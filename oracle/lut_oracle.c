@@ -1,0 +1,383 @@
+/*
+ * lut_oracle.c -- CPU restatement of the reference's LUT hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker the parity tests and
+ * bench.py's cpu_baseline leg use.  Nothing in the product (spiky_amd/) links,
+ * loads or calls it.
+ *
+ * Every function restates the reference's NO_CUDA (device == -1) semantics:
+ * the kernel body runs in serial loops blockIdx.y -> blockIdx.x -> threadIdx.x
+ * (spiky_cuda/misc/misc.h:119-129), so a flat item index i = blockIdx.x*TPB +
+ * threadIdx.x is visited in ascending order for every batch row in turn.  The
+ * arithmetic (fp64 partial sums, fp32 commits, int32 fixed-point payloads) and
+ * the rounding points follow the cited lines exactly.
+ *
+ * Pinning (what checks these functions independently of this file) is listed
+ * per function in tests/test_oracle_*.py; functions with no such check say
+ * "parity unpinned" here.
+ *
+ * Types: anchors are int32 pairs [n_detectors][n_anchors][2]; the value -1
+ * (0xFFFFFFFF) marks an unused pair, as NeuronIndex_t max does in the
+ * reference (lut_runtime_kernels_logic.proto:1076-1079).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+/* spiky_cuda/misc/misc.h:90 */
+#define OR_EPS 0.00000000000000001
+/* spiky_cuda/misc/misc.h:98-99 */
+#define OR_DENOM32 1048575.0
+#define OR_DENOM32_RECIPROC 9.536752259018191e-07
+
+/* ROUNDED_COMPARISON_GREATER(delta, 0.0, cmp_eps), misc.h:16 */
+static inline int rounded_greater0(float d, float cmp_eps)
+{
+    if (cmp_eps == 0.0f) return d > 0.0f;
+    return (fabsf(d) < cmp_eps) ? 0 : (d > 0.0f);
+}
+
+/* int32 add with two's-complement wrap (what atomicAdd on int does, and what
+ * the CPU build's `+=` produces on x86 in practice). */
+static inline int32_t wrap_add(int32_t a, int32_t b)
+{
+    return (int32_t)((uint32_t)a + (uint32_t)b);
+}
+
+static inline int32_t *as_i32(float *p) { return (int32_t *)(void *)p; }
+
+/* ------------------------------------------------------------------------ */
+/* Anchor decode, compact mode: lut_compile_time_kernels_logic.proto:70-125. */
+/* inputs_of_detector: CSR (offsets[n_det+1], ids[]) of each detector's      */
+/* ascending input list (the CPU order of the backward synapse list).        */
+/* Returns the number of detectors with <= 1 input (the reference's error    */
+/* counter, lut.cu:537-550); such detectors are left untouched.              */
+/* ------------------------------------------------------------------------ */
+int64_t oracle_decode_anchors_compact(
+    const uint32_t *encoded_pairs, int64_t n_detectors, int64_t max_pairs_per_detector,
+    int64_t n_anchors, const int64_t *in_offsets, const int32_t *in_ids,
+    int32_t *anchors_out)
+{
+    int64_t errors = 0;
+    for (int64_t i = 0; i < n_detectors; i++) {
+        const uint32_t *codes = encoded_pairs + i * max_pairs_per_detector;
+        int32_t *dst = anchors_out + i * n_anchors * 2;
+        uint32_t n_syn = (uint32_t)(in_offsets[i + 1] - in_offsets[i]);
+        const int32_t *ids = in_ids + in_offsets[i];
+        if (n_syn <= 1) { errors++; continue; }
+        uint32_t max_codes = n_syn * (n_syn - 1);
+        for (int64_t j = 0; j < n_anchors; j++) {
+            uint32_t c = codes[j] % max_codes;
+            uint32_t a1 = c / (n_syn - 1);
+            uint32_t a2 = c % (n_syn - 1);
+            if (a2 >= a1) a2++;
+            dst[2 * j] = ids[a1];
+            dst[2 * j + 1] = ids[a2];
+        }
+    }
+    return errors;
+}
+
+/* ------------------------------------------------------------------------ */
+/* check_detectors_logic (train) proto:1099-1158 and check_detectors_eval    */
+/* proto:1050-1097.  w_min_deltas == NULL selects eval.                      */
+/* ------------------------------------------------------------------------ */
+void oracle_check_detectors(
+    const float *x, int64_t batch, int64_t n_inputs,
+    const int32_t *anchors, int64_t n_detectors, int64_t n_anchors, float cmp_eps,
+    int32_t *w_idx, float *w_min_deltas, int32_t *w_min_idx)
+{
+    for (int64_t b = 0; b < batch; b++) {
+        const float *xb = x + b * n_inputs;
+        for (int64_t t = 0; t < n_detectors; t++) {
+            const int32_t *ap = anchors + t * n_anchors * 2;
+            int32_t li = 0;
+            float md = 0.0f;
+            int32_t mi = -1;
+            for (int64_t k = 0; k < n_anchors; k++) {
+                int32_t a1 = ap[2 * k], a2 = ap[2 * k + 1];
+                if (a1 == -1 || a2 == -1) continue;
+                float d = xb[a1] - xb[a2];
+                if (rounded_greater0(d, cmp_eps)) li |= (1 << k);
+                if (mi == -1 || fabsf(d) < fabsf(md)) { md = d; mi = (int32_t)k; }
+            }
+            w_idx[b * n_detectors + t] = li;
+            if (w_min_deltas) {
+                w_min_deltas[b * n_detectors + t] = md;
+                w_min_idx[b * n_detectors + t] = mi;
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* fill_outputs_non_seq_fc_logic, proto:1214-1299.  Item i = blk*O + o, so   */
+/* for each sample the blocks of `dgs` detectors are committed in ascending  */
+/* block order.  Each block: fp64 sum of the selected weights in ascending   */
+/* detector order, then one fp32 commit (float mode) or one int32 payload    */
+/* trunc(sum*DENOM32*int_rescaler) (int mode, proto:1276-1285).              */
+/* W layout [n_detectors][n_entries][O] (row = t*E + idx), proto:1233-1270.  */
+/* If q8 != NULL the table is int8 with a per-detector fp32 scale and the    */
+/* weight is the fp32 product scale[t]*(float)q (the int8 mapping of the     */
+/* integer path; the reference itself stores fp32 weights only).             */
+/* ------------------------------------------------------------------------ */
+static inline double weight_at(const float *w, const int8_t *q8, const float *scales,
+                               int64_t t, int64_t off)
+{
+    if (q8) return (double)(scales[t] * (float)q8[off]);
+    return (double)w[off];
+}
+
+void oracle_fill_outputs_fc(
+    const float *w, const int8_t *q8, const float *scales,
+    const int32_t *idx, float *out, int64_t batch, int64_t n_outputs,
+    int64_t n_detectors, int64_t n_entries, int64_t dgs, int int_mode, double int_rescaler)
+{
+    int64_t n_blocks = (n_detectors + dgs - 1) / dgs;
+    for (int64_t b = 0; b < batch; b++) {
+        const int32_t *ib = idx + b * n_detectors;
+        float *ob = out + b * n_outputs;
+        for (int64_t blk = 0; blk < n_blocks; blk++) {
+            int64_t t0 = blk * dgs;
+            int64_t t1 = t0 + dgs < n_detectors ? t0 + dgs : n_detectors;
+            for (int64_t o = 0; o < n_outputs; o++) {
+                double s = 0.0;
+                for (int64_t t = t0; t < t1; t++) {
+                    int64_t off = (t * n_entries + ib[t]) * n_outputs + o;
+                    s += weight_at(w, q8, scales, t, off);
+                }
+                if (int_mode) {
+                    int32_t p = (int32_t)(s * OR_DENOM32 * int_rescaler);
+                    as_i32(ob)[o] = wrap_add(as_i32(ob)[o], p);
+                } else {
+                    ob[o] += (float)s;
+                }
+            }
+        }
+    }
+}
+
+/* convert_integers_to_floats_logic, proto:200-213: in-place int32 -> fp32. */
+void oracle_convert_int_to_float(float *buf, int64_t n, double int_rescaler)
+{
+    for (int64_t i = 0; i < n; i++) {
+        double y = (double)as_i32(buf)[i] * OR_DENOM32_RECIPROC;
+        buf[i] = (float)(y / int_rescaler);
+    }
+}
+
+/* du = sign(u)*0.5/(1+|u|)^2 with sign(u<=0) = -1, evaluated as the         */
+/* reference does: proto:1458-1465.                                          */
+static inline double du_of_margin(float md)
+{
+    double du = (double)md;
+    if (du > 0) {
+        du = 1.0 / (1.0 + fabs(du));
+        du *= 0.5 * du;
+    } else {
+        du = 1.0 / (1.0 + fabs(du));
+        du *= -0.5 * du;
+    }
+    return du;
+}
+
+/* propagate_through_detector, proto:821-867 (CPU branch). */
+static inline void push_input_grad(float *xg, int32_t a1, int32_t a2, double du,
+                                   int int_mode, double int_rescaler)
+{
+    if (!(fabs(du) > OR_EPS)) return;
+    if (int_mode) {
+        int32_t d = (int32_t)(du * OR_DENOM32 * int_rescaler);
+        as_i32(xg)[a1] = wrap_add(as_i32(xg)[a1], d);
+        as_i32(xg)[a2] = wrap_add(as_i32(xg)[a2], (int32_t)(0u - (uint32_t)d));
+    } else {
+        /* float += double: one rounding through double (C semantics) */
+        xg[a1] = (float)((double)xg[a1] + du);
+        xg[a2] = (float)((double)xg[a2] - du);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* propagate_through_detectors_non_seq_fc_logic, proto:1421-1499, with       */
+/* accumulate_pair_of_gradient_sums_fc proto:474-582 (CPU branch 575-581).   */
+/* Item i = t*n_ob + ob.  A detector whose min-index is -1 (no valid anchor) */
+/* contributes nothing (the reference shifts by -1 there, which is UB).      */
+/* ------------------------------------------------------------------------ */
+void oracle_propagate_fc(
+    const float *w, const float *g, const int32_t *idx, const float *min_deltas,
+    const int32_t *min_idx, const int32_t *anchors, float *x_grad,
+    int64_t batch, int64_t n_inputs, int64_t n_outputs, int64_t n_detectors,
+    int64_t n_anchors, int64_t n_entries, int64_t ogs, int int_mode, double int_rescaler)
+{
+    int64_t n_ob = (n_outputs + ogs - 1) / ogs;
+    for (int64_t b = 0; b < batch; b++) {
+        const float *gb = g + b * n_outputs;
+        float *xg = x_grad + b * n_inputs;
+        for (int64_t t = 0; t < n_detectors; t++) {
+            int32_t li = idx[b * n_detectors + t];
+            int32_t mi = min_idx[b * n_detectors + t];
+            float md = min_deltas[b * n_detectors + t];
+            for (int64_t ob = 0; ob < n_ob; ob++) {
+                if (mi < 0) continue;
+                double du = du_of_margin(md);
+                int64_t main_row = t * n_entries + li;
+                int64_t alt_row = t * n_entries + (li ^ (1 << mi));
+                int64_t o0 = ob * ogs;
+                int64_t o1 = o0 + ogs < n_outputs ? o0 + ogs : n_outputs;
+                double ms = 0.0, as = 0.0;
+                for (int64_t o = o0; o < o1; o++) {
+                    double gg = (double)gb[o];
+                    ms += (double)w[main_row * n_outputs + o] * gg;
+                    as += (double)w[alt_row * n_outputs + o] * gg;
+                }
+                du *= ms - as;
+                const int32_t *ap = anchors + (t * n_anchors + mi) * 2;
+                push_input_grad(xg, ap[0], ap[1], du, int_mode, int_rescaler);
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* gather_w_gradients_non_seq_fc_logic proto:1547-1585 with                  */
+/* gather_weight_gradients_fc proto:716-819 (CPU branch 792-818).            */
+/* lr = (double)first_meta_lr, times -external_lr when external_lr >= 0      */
+/* (then `target` is the weight tensor itself: in-place SGD,                 */
+/* lut_runtime.cu:342-361).                                                  */
+/* ------------------------------------------------------------------------ */
+void oracle_gather_wgrad_fc(
+    const float *g, const int32_t *idx, float *target,
+    int64_t batch, int64_t n_outputs, int64_t n_detectors, int64_t n_entries, int64_t ogs,
+    float first_meta_lr, float external_lr, int int_mode, double int_rescaler)
+{
+    int64_t n_ob = (n_outputs + ogs - 1) / ogs;
+    double lr = (double)first_meta_lr;
+    if (external_lr >= 0) lr *= -(double)external_lr;
+    for (int64_t b = 0; b < batch; b++) {
+        const float *gb = g + b * n_outputs;
+        for (int64_t t = 0; t < n_detectors; t++) {
+            int64_t row = t * n_entries + idx[b * n_detectors + t];
+            for (int64_t ob = 0; ob < n_ob; ob++) {
+                int64_t o0 = ob * ogs;
+                int64_t o1 = o0 + ogs < n_outputs ? o0 + ogs : n_outputs;
+                for (int64_t o = o0; o < o1; o++) {
+                    double gg = (double)gb[o];
+                    if (!(fabs(gg) > OR_EPS)) continue;
+                    if (int_mode) {
+                        int32_t d = (int32_t)(gg * lr * OR_DENOM32 * int_rescaler);
+                        as_i32(target)[row * n_outputs + o] =
+                            wrap_add(as_i32(target)[row * n_outputs + o], d);
+                    } else {
+                        target[row * n_outputs + o] += (float)(gg * lr);
+                    }
+                }
+            }
+        }
+    }
+}
+
+/* ======================================================================== */
+/* Sparse (ProjectionLUTLayer) path over this build's CSR layout:            */
+/*   syn_offsets[n_lookup+1]  - synapses of lookup neuron n = t*E + e        */
+/*   syn_targets[n_syn]       - output index of each synapse                 */
+/*   weights[n_syn]           - one fp32 weight per synapse                  */
+/* A neuron's synapses split into forward groups of `fgs` in list order      */
+/* (the reference's ForwardSynapseGroup, connections_manager.h:39-66).       */
+/* ======================================================================== */
+
+/* fill_outputs_non_seq_sparse_logic proto:1160-1212 + fire_single_synapse_group
+ * proto:215-313: per synapse one fp32 commit of (float)(double)w, items ordered
+ * (t, group) ascending, synapses in list order. */
+void oracle_fill_outputs_sparse(
+    const float *w, const int32_t *idx, const int64_t *syn_offsets, const int32_t *syn_targets,
+    float *out, int64_t batch, int64_t n_outputs, int64_t n_detectors, int64_t n_entries,
+    int int_mode, double int_rescaler)
+{
+    for (int64_t b = 0; b < batch; b++) {
+        float *ob = out + b * n_outputs;
+        for (int64_t t = 0; t < n_detectors; t++) {
+            int64_t n = t * n_entries + idx[b * n_detectors + t];
+            for (int64_t s = syn_offsets[n]; s < syn_offsets[n + 1]; s++) {
+                int32_t tg = syn_targets[s];
+                double wt = (double)w[s];
+                if (int_mode) {
+                    int32_t p = (int32_t)(wt * OR_DENOM32 * int_rescaler);
+                    as_i32(ob)[tg] = wrap_add(as_i32(ob)[tg], p);
+                } else {
+                    ob[tg] += (float)wt;
+                }
+            }
+        }
+    }
+}
+
+/* propagate_through_detectors_non_seq_sparse_logic proto:1303-1419 with
+ * accumulate_grad_sum_sparse proto:315-395.  Group `grp` of the main neuron
+ * and group `grp` of the alt neuron (each only if it exists), then one du per
+ * (t, grp), grp < max_groups. */
+void oracle_propagate_sparse(
+    const float *w, const float *g, const int32_t *idx, const float *min_deltas,
+    const int32_t *min_idx, const int32_t *anchors, const int64_t *syn_offsets,
+    const int32_t *syn_targets, float *x_grad, int64_t batch, int64_t n_inputs,
+    int64_t n_outputs, int64_t n_detectors, int64_t n_anchors, int64_t n_entries,
+    int64_t fgs, int64_t max_groups, int int_mode, double int_rescaler)
+{
+    for (int64_t b = 0; b < batch; b++) {
+        const float *gb = g + b * n_outputs;
+        float *xg = x_grad + b * n_inputs;
+        for (int64_t t = 0; t < n_detectors; t++) {
+            int32_t li = idx[b * n_detectors + t];
+            int32_t mi = min_idx[b * n_detectors + t];
+            float md = min_deltas[b * n_detectors + t];
+            for (int64_t grp = 0; grp < max_groups; grp++) {
+                if (mi < 0) continue;
+                double du = du_of_margin(md);
+                int64_t nm = t * n_entries + li;
+                int64_t na = t * n_entries + (li ^ (1 << mi));
+                double ms = 0.0, as = 0.0;
+                int64_t s0 = syn_offsets[nm] + grp * fgs;
+                if (s0 < syn_offsets[nm + 1]) {
+                    int64_t s1 = s0 + fgs < syn_offsets[nm + 1] ? s0 + fgs : syn_offsets[nm + 1];
+                    for (int64_t s = s0; s < s1; s++)
+                        ms += (double)w[s] * (double)gb[syn_targets[s]];
+                }
+                s0 = syn_offsets[na] + grp * fgs;
+                if (s0 < syn_offsets[na + 1]) {
+                    int64_t s1 = s0 + fgs < syn_offsets[na + 1] ? s0 + fgs : syn_offsets[na + 1];
+                    for (int64_t s = s0; s < s1; s++)
+                        as += (double)w[s] * (double)gb[syn_targets[s]];
+                }
+                du *= ms - as;
+                const int32_t *ap = anchors + (t * n_anchors + mi) * 2;
+                push_input_grad(xg, ap[0], ap[1], du, int_mode, int_rescaler);
+            }
+        }
+    }
+}
+
+/* gather_w_gradients_non_seq_sparse_logic proto:1501-1545 with
+ * gather_weight_gradients_sparse proto:584-714. */
+void oracle_gather_wgrad_sparse(
+    const float *g, const int32_t *idx, const int64_t *syn_offsets, const int32_t *syn_targets,
+    float *target, int64_t batch, int64_t n_outputs, int64_t n_detectors, int64_t n_entries,
+    float first_meta_lr, float external_lr, int int_mode, double int_rescaler)
+{
+    double lr = (double)first_meta_lr;
+    if (external_lr >= 0) lr *= -(double)external_lr;
+    for (int64_t b = 0; b < batch; b++) {
+        const float *gb = g + b * n_outputs;
+        for (int64_t t = 0; t < n_detectors; t++) {
+            int64_t n = t * n_entries + idx[b * n_detectors + t];
+            for (int64_t s = syn_offsets[n]; s < syn_offsets[n + 1]; s++) {
+                double gg = (double)gb[syn_targets[s]];
+                if (!(fabs(gg) > OR_EPS)) continue;
+                if (int_mode) {
+                    int32_t d = (int32_t)(gg * lr * OR_DENOM32 * int_rescaler);
+                    as_i32(target)[s] = wrap_add(as_i32(target)[s], d);
+                } else {
+                    target[s] += (float)(gg * lr);
+                }
+            }
+        }
+    }
+}

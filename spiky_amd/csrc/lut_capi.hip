@@ -1,0 +1,669 @@
+// lut_capi.hip -- the C ABI of include/spiky_lut.h: one manager object per
+// LUT layer (the reference's LUTDataManagerF/I, spiky_cuda/lut/lut.cu), host
+// validation with the reference's error texts, and dispatch to the kernels on
+// the caller's HIP stream.  Nothing here synchronises the device.
+#include "../../include/spiky_lut.h"
+#include "lut_kernels.h"
+
+#include <algorithm>
+#include <chrono>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace {
+
+thread_local std::string g_last_error;
+
+struct ValueError : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+void check_hip(hipError_t e, const char *what) {
+    if (e != hipSuccess) {
+        throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+    }
+}
+
+template <typename F>
+int guarded(F &&f) {
+    try {
+        f();
+        g_last_error.clear();
+        return SPIKY_OK;
+    } catch (const ValueError &e) {
+        g_last_error = e.what();
+        return SPIKY_VALUE_ERROR;
+    } catch (const std::exception &e) {
+        g_last_error = e.what();
+        return SPIKY_RUNTIME_ERROR;
+    }
+}
+
+struct DeviceBuffer {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+    int device = -1;
+    void release() {
+        if (ptr) {
+            int cur = 0;
+            (void)hipGetDevice(&cur);
+            (void)hipSetDevice(device);
+            (void)hipFree(ptr);
+            (void)hipSetDevice(cur);
+        }
+        ptr = nullptr;
+        bytes = 0;
+        device = -1;
+    }
+    // Make sure at least `need` bytes exist on the current device.
+    void *ensure(size_t need) {
+        int cur = 0;
+        check_hip(hipGetDevice(&cur), "hipGetDevice");
+        if (ptr && device == cur && bytes >= need) return ptr;
+        release();
+        if (need == 0) return nullptr;
+        check_hip(hipMalloc(&ptr, need), "hipMalloc(scratch)");
+        bytes = need;
+        device = cur;
+        return ptr;
+    }
+    // Upload host data (re-uploads when the current device changed).
+    void *upload(const void *host, size_t n, bool force) {
+        int cur = 0;
+        check_hip(hipGetDevice(&cur), "hipGetDevice");
+        if (!force && ptr && device == cur && bytes == n) return ptr;
+        release();
+        if (n == 0) return nullptr;
+        check_hip(hipMalloc(&ptr, n), "hipMalloc(connectivity)");
+        bytes = n;
+        device = cur;
+        check_hip(hipMemcpy(ptr, host, n, hipMemcpyHostToDevice), "hipMemcpy(connectivity)");
+        return ptr;
+    }
+};
+
+struct OpStat {
+    uint64_t count = 0;
+    double total_ms = 0.0;
+};
+
+class ScopedTimer {
+  public:
+    ScopedTimer(std::map<std::string, OpStat> &stats, const char *name)
+        : stats_(stats), name_(name), t0_(std::chrono::steady_clock::now()) {}
+    ~ScopedTimer() {
+        const double ms =
+            std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0_).count();
+        OpStat &s = stats_[name_];
+        s.count++;
+        s.total_ms += ms;
+    }
+
+  private:
+    std::map<std::string, OpStat> &stats_;
+    const char *name_;
+    std::chrono::steady_clock::time_point t0_;
+};
+
+}  // namespace
+
+struct spiky_lut_manager {
+    uint32_t n_inputs, n_outputs, n_detectors, n_anchors, sequence_length, positional_dim;
+    uint64_t initial_synapse_capacity;
+    uint32_t forward_group_size, backward_group_size;
+    bool int_mode;
+    double int_rescaler;
+    uint64_t n_lookup;
+    std::vector<std::vector<float>> metas;  // lr, min, max, noise, init
+    int fully_connected = -1;               // -1: neurons not initialised
+    bool context_active = false;            // set by the first forward (lut.cu:664-694)
+
+    // sparse connectivity (host master copy + device copies)
+    bool has_connectivity = false;
+    std::vector<int64_t> syn_offsets;
+    std::vector<int32_t> syn_targets;
+    std::vector<int64_t> in_offsets;
+    std::vector<int32_t> in_pairs;
+    bool uniform = false;
+    uint32_t max_groups = 0;
+    DeviceBuffer d_syn_offsets, d_syn_targets, d_in_offsets, d_in_pairs;
+    bool dirty = true;
+
+    DeviceBuffer scratch;
+    std::map<std::string, OpStat> stats;
+
+    // optional per-launch GPU timing with HIP events on the launch stream
+    bool timing = false;
+    struct Pending {
+        const char *name;
+        hipEvent_t start, stop;
+    };
+    std::vector<Pending> pending;
+    std::vector<hipEvent_t> event_pool;
+    std::map<std::string, OpStat> kernel_stats;
+
+    hipEvent_t take_event() {
+        if (!event_pool.empty()) {
+            hipEvent_t e = event_pool.back();
+            event_pool.pop_back();
+            return e;
+        }
+        hipEvent_t e;
+        check_hip(hipEventCreate(&e), "hipEventCreate");
+        return e;
+    }
+
+    template <typename F>
+    void timed(const char *name, hipStream_t st, F &&launch) {
+        if (!timing) {
+            launch();
+            return;
+        }
+        Pending p{name, take_event(), take_event()};
+        check_hip(hipEventRecord(p.start, st), "hipEventRecord");
+        launch();
+        check_hip(hipEventRecord(p.stop, st), "hipEventRecord");
+        pending.push_back(p);
+    }
+
+    void collect() {
+        for (auto &p : pending) {
+            check_hip(hipEventSynchronize(p.stop), "hipEventSynchronize");
+            float ms = 0.f;
+            check_hip(hipEventElapsedTime(&ms, p.start, p.stop), "hipEventElapsedTime");
+            OpStat &k = kernel_stats[p.name];
+            k.count++;
+            k.total_ms += ms;
+            event_pool.push_back(p.start);
+            event_pool.push_back(p.stop);
+        }
+        pending.clear();
+    }
+
+    void release_events() {
+        for (auto &p : pending) {
+            (void)hipEventDestroy(p.start);
+            (void)hipEventDestroy(p.stop);
+        }
+        pending.clear();
+        for (auto e : event_pool) (void)hipEventDestroy(e);
+        event_pool.clear();
+    }
+
+    uint32_t n_entries() const { return 1u << n_anchors; }
+
+    spiky::FcShape shape(uint32_t batch) const {
+        spiky::FcShape s;
+        s.batch = batch;
+        s.n_inputs = n_inputs;
+        s.n_outputs = n_outputs;
+        s.n_detectors = n_detectors;
+        s.n_anchors = n_anchors;
+        s.n_entries = n_entries();
+        s.dgs = backward_group_size;
+        s.ogs = forward_group_size;
+        return s;
+    }
+
+    void sync_connectivity() {
+        d_syn_offsets.upload(syn_offsets.data(), syn_offsets.size() * sizeof(int64_t), dirty);
+        d_syn_targets.upload(syn_targets.data(), syn_targets.size() * sizeof(int32_t), dirty);
+        if (uniform) {
+            d_in_offsets.upload(in_offsets.data(), in_offsets.size() * sizeof(int64_t), dirty);
+            d_in_pairs.upload(in_pairs.data(), in_pairs.size() * sizeof(int32_t), dirty);
+        }
+        dirty = false;
+    }
+};
+
+namespace {
+
+void require_manager(const spiky_lut_manager *m) {
+    if (!m) throw ValueError("null manager");
+}
+
+void require_initialized(const spiky_lut_manager *m) {
+    if (m->fully_connected < 0) throw ValueError("neurons are not initialized (call initialize_neurons first)");
+    if (m->fully_connected == 0 && !m->has_connectivity)
+        throw ValueError("sparse connectivity is not compiled (call compile first)");
+}
+
+hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+}  // namespace
+
+extern "C" {
+
+const char *spiky_lut_last_error(void) { return g_last_error.c_str(); }
+
+const char *spiky_lut_version(void) { return "spiky_amd-lut 0.1 (gfx950)"; }
+
+int spiky_lut_create(uint32_t n_inputs, uint32_t n_outputs, uint32_t n_detectors,
+                     uint32_t n_anchors_per_detector, uint32_t sequence_length,
+                     uint32_t positional_dim, uint64_t initial_synapse_capacity,
+                     uint32_t forward_group_size, uint32_t backward_group_size,
+                     int summation_int32, double int_rescaler, spiky_lut_manager **out) {
+    return guarded([&] {
+        if (!out) throw ValueError("null output handle");
+        *out = nullptr;
+        // lut.cu:47-76
+        if (n_inputs == 0) throw ValueError("n_inputs == 0");
+        if (n_outputs == 0) throw ValueError("n_outputs == 0");
+        if (n_detectors == 0) throw ValueError("n_detectors == 0");
+        if (n_anchors_per_detector == 0) throw ValueError("n_anchors_per_detector == 0");
+        if (sequence_length == 0) throw ValueError("sequence_length == 0");
+        if (forward_group_size == 0) throw ValueError("forward_group_size == 0");
+        if (forward_group_size > 2047) throw ValueError("forward_group_size > MAX_SYNAPSE_GROUP_SIZE");
+        if (forward_group_size > 1024) throw ValueError("forward_group_size > LUT_RUNTIME_KERNELS_TPB");
+        if (backward_group_size == 0) throw ValueError("backward_group_size == 0");
+        if (backward_group_size > 2047) throw ValueError("backward_group_size > MAX_SYNAPSE_GROUP_SIZE");
+        const uint32_t bits = n_anchors_per_detector +
+                              (sequence_length > 1 ? n_anchors_per_detector + positional_dim : 0);
+        if (bits > 30) throw ValueError("lookup index does not fit: too many anchors per detector");
+        if (summation_int32 && !(int_rescaler > 0.0)) throw ValueError("int_rescaler must be > 0");
+        auto *m = new spiky_lut_manager();
+        m->n_inputs = n_inputs;
+        m->n_outputs = n_outputs;
+        m->n_detectors = n_detectors;
+        m->n_anchors = n_anchors_per_detector;
+        m->sequence_length = sequence_length;
+        m->positional_dim = positional_dim;
+        m->initial_synapse_capacity = initial_synapse_capacity;
+        m->forward_group_size = forward_group_size;
+        m->backward_group_size = backward_group_size;
+        m->int_mode = summation_int32 != 0;
+        m->int_rescaler = summation_int32 ? int_rescaler : 0.0;
+        m->n_lookup = (uint64_t)n_detectors << bits;  // lut.cu:42
+        *out = m;
+    });
+}
+
+void spiky_lut_destroy(spiky_lut_manager *m) {
+    if (!m) return;
+    m->release_events();
+    m->scratch.release();
+    m->d_syn_offsets.release();
+    m->d_syn_targets.release();
+    m->d_in_offsets.release();
+    m->d_in_pairs.release();
+    delete m;
+}
+
+int spiky_lut_register_synapse_meta(spiky_lut_manager *m, float learning_rate,
+                                    float min_synaptic_weight, float max_synaptic_weight,
+                                    float initial_noise_level, float initial_weight,
+                                    uint32_t *out_meta_index) {
+    return guarded([&] {
+        require_manager(m);
+        // lut.cu:148-206
+        if (m->fully_connected >= 0)
+            throw ValueError("can't register new synapse metas after neurons were initialized");
+        if (learning_rate < 0.0f) throw ValueError("learning_rate < 0");
+        if (learning_rate > 1.0f) throw ValueError("learning_rate > 1");
+        if (m->int_mode) {
+            const float recip = (float)(1.0 / 1048575.0);
+            if (learning_rate > 0.0f && (learning_rate * m->int_rescaler) < recip)
+                throw ValueError("too small value for 'learning_rate' (less than smallest distinguishable fraction)");
+        }
+        if (min_synaptic_weight > max_synaptic_weight) throw ValueError("min_synaptic_weight > max_synaptic_weight");
+        if (initial_weight < min_synaptic_weight) throw ValueError("initial_weight < min_synaptic_weight");
+        if (initial_weight > max_synaptic_weight) throw ValueError("initial_weight > max_synaptic_weight");
+        std::vector<float> meta = {learning_rate, min_synaptic_weight, max_synaptic_weight,
+                                   initial_noise_level, initial_weight};
+        for (size_t i = 0; i < m->metas.size(); i++) {
+            if (m->metas[i] == meta) {
+                if (out_meta_index) *out_meta_index = (uint32_t)i;
+                return;
+            }
+        }
+        if (m->metas.size() >= 256) throw ValueError("too many different synapse metas");
+        m->metas.push_back(meta);
+        if (out_meta_index) *out_meta_index = (uint32_t)(m->metas.size() - 1);
+    });
+}
+
+int spiky_lut_initialize_neurons(spiky_lut_manager *m, int is_fully_connected) {
+    return guarded([&] {
+        require_manager(m);
+        if (m->metas.empty()) throw ValueError("no synapse metas were registered");
+        if (is_fully_connected && m->metas.size() > 1)
+            throw ValueError("fully connected mode is not compatible with multiple synapse metas");
+        m->fully_connected = is_fully_connected ? 1 : 0;
+    });
+}
+
+uint64_t spiky_lut_n_lookup_neurons(const spiky_lut_manager *m) { return m ? m->n_lookup : 0; }
+
+uint64_t spiky_lut_weights_dimension(const spiky_lut_manager *m) {
+    if (!m) return 0;
+    if (m->fully_connected == 1) return m->n_lookup * m->n_outputs;
+    return m->has_connectivity ? (uint64_t)m->syn_targets.size() : 0;
+}
+
+uint32_t spiky_lut_max_forward_groups_per_neuron(const spiky_lut_manager *m) {
+    if (!m) return 0;
+    if (m->fully_connected == 1)
+        return (m->n_outputs + m->forward_group_size - 1) / m->forward_group_size;  // lut.cu:225
+    return m->max_groups;
+}
+
+uint64_t spiky_lut_n_synapses(const spiky_lut_manager *m) {
+    if (!m) return 0;
+    if (m->fully_connected == 1) return 0;  // lut.cu n_synapses stays 0 in FC mode
+    return (uint64_t)m->syn_targets.size();
+}
+
+int spiky_lut_set_sparse_connectivity(spiky_lut_manager *m, const int64_t *syn_offsets,
+                                      const int32_t *syn_targets, uint64_t n_synapses) {
+    return guarded([&] {
+        require_manager(m);
+        if (m->fully_connected != 0) throw ValueError("can't add lookup connections in fully connected mode");
+        if (m->sequence_length != 1) throw ValueError("sparse connectivity needs sequence_length == 1");
+        if (!syn_offsets || (n_synapses && !syn_targets)) throw ValueError("null connectivity arrays");
+        const uint64_t nl = m->n_lookup;
+        if (syn_offsets[0] != 0 || (uint64_t)syn_offsets[nl] != n_synapses)
+            throw ValueError("syn_offsets must start at 0 and end at n_synapses");
+        uint32_t max_groups = 0;
+        for (uint64_t n = 0; n < nl; n++) {
+            const int64_t len = syn_offsets[n + 1] - syn_offsets[n];
+            if (len < 0) throw ValueError("syn_offsets must be non-decreasing");
+            max_groups = std::max<uint32_t>(
+                max_groups, (uint32_t)((len + m->forward_group_size - 1) / m->forward_group_size));
+        }
+        for (uint64_t s = 0; s < n_synapses; s++)
+            if (syn_targets[s] < 0 || (uint32_t)syn_targets[s] >= m->n_outputs)
+                throw ValueError("synapse target out of range");
+        m->syn_offsets.assign(syn_offsets, syn_offsets + nl + 1);
+        m->syn_targets.assign(syn_targets, syn_targets + n_synapses);
+        m->max_groups = max_groups;
+        // uniform topology: all lookup neurons of a detector share one ordered target list
+        const uint32_t E = m->n_entries();
+        bool uniform = true;
+        for (uint32_t t = 0; t < m->n_detectors && uniform; t++) {
+            const uint64_t n0 = (uint64_t)t * E;
+            const int64_t len0 = syn_offsets[n0 + 1] - syn_offsets[n0];
+            for (uint32_t e = 1; e < E && uniform; e++) {
+                const uint64_t n = n0 + e;
+                if (syn_offsets[n + 1] - syn_offsets[n] != len0) { uniform = false; break; }
+                if (std::memcmp(syn_targets + syn_offsets[n], syn_targets + syn_offsets[n0],
+                                (size_t)len0 * sizeof(int32_t)) != 0)
+                    uniform = false;
+            }
+        }
+        m->uniform = uniform;
+        m->in_offsets.clear();
+        m->in_pairs.clear();
+        if (uniform) {
+            std::vector<int64_t> cnt(m->n_outputs + 1, 0);
+            for (uint32_t t = 0; t < m->n_detectors; t++) {
+                const uint64_t n0 = (uint64_t)t * E;
+                for (int64_t s = syn_offsets[n0]; s < syn_offsets[n0 + 1]; s++) cnt[syn_targets[s] + 1]++;
+            }
+            for (uint32_t j = 0; j < m->n_outputs; j++) cnt[j + 1] += cnt[j];
+            m->in_offsets = cnt;
+            m->in_pairs.assign((size_t)cnt[m->n_outputs] * 2, 0);
+            std::vector<int64_t> pos(cnt.begin(), cnt.end() - 1);
+            for (uint32_t t = 0; t < m->n_detectors; t++) {
+                const uint64_t n0 = (uint64_t)t * E;
+                for (int64_t s = syn_offsets[n0]; s < syn_offsets[n0 + 1]; s++) {
+                    const int64_t p = pos[syn_targets[s]]++;
+                    m->in_pairs[2 * p] = (int32_t)t;
+                    m->in_pairs[2 * p + 1] = (int32_t)(s - syn_offsets[n0]);
+                }
+            }
+        }
+        m->has_connectivity = true;
+        m->dirty = true;
+    });
+}
+
+int spiky_lut_forward_step(spiky_lut_manager *m, const float *weights, uint32_t batch_size,
+                           const float *input, const int32_t *anchors, float *output,
+                           int32_t *lookup_indices, float cmp_eps, float *min_deltas,
+                           int32_t *min_delta_indices, void *stream) {
+    return guarded([&] {
+        require_manager(m);
+        if (batch_size == 0) throw ValueError("batch_size == 0");
+        if (m->sequence_length != 1)
+            throw ValueError("forward_step should only be called when sequence_length == 1");
+        require_initialized(m);
+        if (!weights || !input || !anchors || !output || !lookup_indices)
+            throw ValueError("null tensor pointer");
+        if ((min_deltas == nullptr) != (min_delta_indices == nullptr))
+            throw ValueError("w_min_anchor_deltas and w_min_anchor_delta_indices must be given together");
+        ScopedTimer timer(m->stats, min_deltas ? "lut::runtime::forward_non_seq"
+                                               : "lut::runtime::forward_non_seq_eval");
+        m->context_active = true;
+        const hipStream_t st = as_stream(stream);
+        const spiky::FcShape s = m->shape(batch_size);
+        m->timed("check_detectors", st, [&] {
+            check_hip(spiky::launch_check_detectors(s, input, anchors, cmp_eps, lookup_indices,
+                                                    min_deltas, min_delta_indices, st),
+                      "check_detectors");
+        });
+        if (m->fully_connected == 1) {
+            m->timed("fill_outputs_fc", st, [&] {
+                check_hip(spiky::launch_fill_fc_f32(s, weights, lookup_indices, output, m->int_mode,
+                                                    m->int_rescaler, st),
+                          "fill_outputs_fc");
+            });
+        } else {
+            m->sync_connectivity();
+            spiky::SparseShape ss{s, m->max_groups};
+            const int64_t *off = (const int64_t *)m->d_syn_offsets.ptr;
+            if (m->uniform) {
+                m->timed("fill_outputs_sparse", st, [&] {
+                    check_hip(spiky::launch_fill_sparse_uniform(
+                                  ss, weights, lookup_indices, off, (const int64_t *)m->d_in_offsets.ptr,
+                                  (const int32_t *)m->d_in_pairs.ptr, output, m->int_mode,
+                                  m->int_rescaler, st),
+                              "fill_outputs_sparse");
+                });
+            } else {
+                m->timed("fill_outputs_sparse", st, [&] {
+                    check_hip(spiky::launch_fill_sparse_atomic(ss, weights, lookup_indices, off,
+                                                               (const int32_t *)m->d_syn_targets.ptr,
+                                                               output, m->int_mode, m->int_rescaler, st),
+                              "fill_outputs_sparse");
+                });
+            }
+        }
+    });
+}
+
+int spiky_lut_forward_step_i8(spiky_lut_manager *m, const int8_t *q8, const float *scales,
+                              uint32_t batch_size, const float *input, const int32_t *anchors,
+                              float *output, int32_t *lookup_indices, float cmp_eps,
+                              float *min_deltas, int32_t *min_delta_indices, void *stream) {
+    return guarded([&] {
+        require_manager(m);
+        if (batch_size == 0) throw ValueError("batch_size == 0");
+        if (m->sequence_length != 1)
+            throw ValueError("forward_step should only be called when sequence_length == 1");
+        require_initialized(m);
+        if (m->fully_connected != 1) throw ValueError("int8 tables need a fully connected manager");
+        if (!q8 || !scales || !input || !anchors || !output || !lookup_indices)
+            throw ValueError("null tensor pointer");
+        if ((min_deltas == nullptr) != (min_delta_indices == nullptr))
+            throw ValueError("w_min_anchor_deltas and w_min_anchor_delta_indices must be given together");
+        ScopedTimer timer(m->stats, "lut::runtime::forward_non_seq_i8");
+        m->context_active = true;
+        const hipStream_t st = as_stream(stream);
+        const spiky::FcShape s = m->shape(batch_size);
+        m->timed("check_detectors", st, [&] {
+            check_hip(spiky::launch_check_detectors(s, input, anchors, cmp_eps, lookup_indices,
+                                                    min_deltas, min_delta_indices, st),
+                      "check_detectors");
+        });
+        m->timed("fill_outputs_fc_i8", st, [&] {
+            check_hip(spiky::launch_fill_fc_i8(s, q8, scales, lookup_indices, output, m->int_mode,
+                                               m->int_rescaler, st),
+                      "fill_outputs_fc_i8");
+        });
+    });
+}
+
+int spiky_lut_backward_backprop(spiky_lut_manager *m, float *weights, uint32_t batch_size,
+                                const float *output_grad, const int32_t *anchors,
+                                const int32_t *lookup_indices, const float *min_deltas,
+                                const int32_t *min_delta_indices, float *input_grad,
+                                double external_lr, float *weight_grad,
+                                int overwrite_weight_grad, void *stream) {
+    return guarded([&] {
+        require_manager(m);
+        // lut.cu:1044-1049 and lut_runtime.cu:228-238
+        if (batch_size == 0) throw ValueError("batch_size == 0");
+        if (!m->context_active) throw ValueError("no active context");
+        if (m->sequence_length != 1)
+            throw ValueError("backward_backprop should only be called when sequence_length == 1");
+        require_initialized(m);
+        const float ext = (float)external_lr;  // the reference narrows it to fp32 (lut.cu:1082)
+        if (ext >= 0.0f && weight_grad != nullptr)
+            throw ValueError("in internal weight gradients mode w_weights_gradients should be nullptr");
+        if (ext >= 0.0f && m->int_mode)
+            throw ValueError("summation dtype torch.int32 can't be combined with GradientType.Internal");
+        if (!weights || !output_grad || !anchors || !lookup_indices || !min_deltas ||
+            !min_delta_indices || !input_grad)
+            throw ValueError("null tensor pointer");
+        ScopedTimer timer(m->stats, "lut::runtime::backward_non_seq::backprop");
+        const hipStream_t st = as_stream(stream);
+        const spiky::FcShape s = m->shape(batch_size);
+        // gather_weight_gradients_*: lr = meta lr, times -external_lr in Internal mode (proto:731-734)
+        double lr = (double)m->metas[0][0];
+        if (ext >= 0.0f) lr *= -(double)ext;
+        float *target = (ext >= 0.0f) ? weights : weight_grad;
+        const bool overwrite = overwrite_weight_grad != 0 && target == weight_grad;
+        if (m->fully_connected == 1) {
+            m->timed("propagate_fc", st, [&] {
+                check_hip(spiky::launch_propagate_fc(s, weights, output_grad, lookup_indices, min_deltas,
+                                                     min_delta_indices, anchors, input_grad, m->int_mode,
+                                                     m->int_rescaler, st),
+                          "propagate_through_detectors_fc");
+            });
+            if (m->int_mode)
+                check_hip(spiky::launch_convert_i2f(input_grad, (uint64_t)batch_size * m->n_inputs,
+                                                    m->int_rescaler, st),
+                          "convert_integers_to_floats");
+            if (target) {
+                const size_t need = spiky::wgrad_fc_scratch_bytes(s);
+                void *scr = need ? m->scratch.ensure(need) : nullptr;
+                m->timed("gather_w_gradients_fc", st, [&] {
+                    check_hip(spiky::launch_wgrad_fc(s, output_grad, lookup_indices, target, lr,
+                                                     m->int_mode, m->int_rescaler, overwrite, scr, st),
+                              "gather_w_gradients_fc");
+                });
+            }
+        } else {
+            m->sync_connectivity();
+            spiky::SparseShape ss{s, m->max_groups};
+            const int64_t *off = (const int64_t *)m->d_syn_offsets.ptr;
+            const int32_t *tg = (const int32_t *)m->d_syn_targets.ptr;
+            m->timed("propagate_sparse", st, [&] {
+                check_hip(spiky::launch_propagate_sparse(ss, weights, output_grad, lookup_indices,
+                                                         min_deltas, min_delta_indices, anchors, off, tg,
+                                                         input_grad, m->int_mode, m->int_rescaler, st),
+                          "propagate_through_detectors_sparse");
+            });
+            if (m->int_mode)
+                check_hip(spiky::launch_convert_i2f(input_grad, (uint64_t)batch_size * m->n_inputs,
+                                                    m->int_rescaler, st),
+                          "convert_integers_to_floats");
+            if (target) {
+                const uint64_t n_syn = m->syn_targets.size();
+                if (overwrite) check_hip(spiky::launch_zero(target, n_syn, st), "zero w_grad");
+                void *scr = m->scratch.ensure(spiky::wgrad_sparse_scratch_bytes(ss));
+                m->timed("gather_w_gradients_sparse", st, [&] {
+                    check_hip(spiky::launch_wgrad_sparse(ss, output_grad, lookup_indices, off, tg, target,
+                                                         lr, m->int_mode, m->int_rescaler, scr, n_syn, st),
+                              "gather_w_gradients_sparse");
+                });
+            }
+        }
+    });
+}
+
+int spiky_lut_decode_anchors_compact(const uint32_t *encoded_pairs, uint32_t n_detectors,
+                                     uint32_t max_pairs_per_detector, uint32_t n_anchors,
+                                     const int64_t *in_offsets, const int32_t *in_ids,
+                                     int32_t *anchors_out) {
+    return guarded([&] {
+        if (!encoded_pairs || !in_offsets || !anchors_out) throw ValueError("null pointer");
+        if (max_pairs_per_detector < n_anchors)
+            throw ValueError("max_pairs_per_detector < n_anchors_per_detector");
+        // lut_compile_time_kernels_logic.proto:70-125 (compact decode); lut.cu:537-550 (error)
+        uint64_t errors = 0;
+        for (uint32_t i = 0; i < n_detectors; i++) {
+            const uint32_t *codes = encoded_pairs + (size_t)i * max_pairs_per_detector;
+            const int64_t len = in_offsets[i + 1] - in_offsets[i];
+            if (len <= 1) { errors++; continue; }
+            const uint32_t n_syn = (uint32_t)len;
+            const uint32_t max_codes = n_syn * (n_syn - 1);
+            const int32_t *ids = in_ids + in_offsets[i];
+            int32_t *dst = anchors_out + (size_t)i * n_anchors * 2;
+            for (uint32_t j = 0; j < n_anchors; j++) {
+                const uint32_t c = codes[j] % max_codes;
+                uint32_t a1 = c / (n_syn - 1);
+                uint32_t a2 = c % (n_syn - 1);
+                if (a2 >= a1) a2++;
+                dst[2 * j] = ids[a1];
+                dst[2 * j + 1] = ids[a2];
+            }
+        }
+        if (errors) throw ValueError("Some detectors have <= 1 input synapses");
+    });
+}
+
+int spiky_lut_profiling_stats(const spiky_lut_manager *m, char *buf, uint64_t buf_len) {
+    return guarded([&] {
+        require_manager(m);
+        std::string s;
+        for (const auto &kv : m->stats) {
+            char line[256];
+            std::snprintf(line, sizeof(line), "%s: %.3f ms / %llu = %.3f ms\n", kv.first.c_str(),
+                          kv.second.total_ms, (unsigned long long)kv.second.count,
+                          kv.second.count ? kv.second.total_ms / kv.second.count : 0.0);
+            s += line;
+        }
+        if (buf && buf_len) {
+            std::strncpy(buf, s.c_str(), buf_len - 1);
+            buf[buf_len - 1] = 0;
+        }
+    });
+}
+
+void spiky_lut_reset_profiler(spiky_lut_manager *m) {
+    if (m) m->stats.clear();
+}
+
+int spiky_lut_set_kernel_timing(spiky_lut_manager *m, int enable) {
+    return guarded([&] {
+        require_manager(m);
+        m->collect();
+        m->timing = enable != 0;
+    });
+}
+
+int spiky_lut_kernel_times(spiky_lut_manager *m, char *buf, uint64_t buf_len, int reset) {
+    return guarded([&] {
+        require_manager(m);
+        m->collect();
+        std::string s;
+        for (const auto &kv : m->kernel_stats) {
+            char line[256];
+            std::snprintf(line, sizeof(line), "%s %llu %.6f\n", kv.first.c_str(),
+                          (unsigned long long)kv.second.count, kv.second.total_ms);
+            s += line;
+        }
+        if (buf && buf_len) {
+            std::strncpy(buf, s.c_str(), buf_len - 1);
+            buf[buf_len - 1] = 0;
+        }
+        if (reset) m->kernel_stats.clear();
+    });
+}
+
+}  // extern "C"

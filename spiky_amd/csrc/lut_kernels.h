@@ -1,0 +1,106 @@
+// lut_kernels.h -- launchers of the LUT hot-path kernels (gfx950 / CDNA4).
+//
+// Internal to libspiky_lut.so; the public C ABI is include/spiky_lut.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace spiky {
+
+// spiky_cuda/misc/misc.h:90 (EPS) and misc.h:98-99 (DENOMINATOR32 and its reciprocal)
+constexpr double kEps = 0.00000000000000001;
+constexpr double kDenom32 = 1048575.0;
+constexpr double kDenom32Reciproc = 9.536752259018191e-07;
+
+struct FcShape {
+    uint32_t batch;
+    uint32_t n_inputs;
+    uint32_t n_outputs;
+    uint32_t n_detectors;
+    uint32_t n_anchors;
+    uint32_t n_entries;  // 2^n_anchors
+    uint32_t dgs;        // detectors per fp64 partial sum (backward_group_size)
+    uint32_t ogs;        // outputs per gradient dot block (forward_group_size)
+};
+
+// check_detectors(_eval): lookup index, and in train mode the min-margin anchor.
+hipError_t launch_check_detectors(const FcShape &s, const float *x, const int32_t *anchors,
+                                  float cmp_eps, int32_t *idx, float *min_deltas,
+                                  int32_t *min_idx, hipStream_t st);
+
+// Row gather-sum over fp32 tables (int_mode: int32 fixed-point accumulation).
+hipError_t launch_fill_fc_f32(const FcShape &s, const float *w, const int32_t *idx, float *out,
+                              bool int_mode, double int_rescaler, hipStream_t st);
+
+// Row gather-sum over int8 tables with a per-detector fp32 scale.
+hipError_t launch_fill_fc_i8(const FcShape &s, const int8_t *q8, const float *scales,
+                             const int32_t *idx, float *out, bool int_mode, double int_rescaler,
+                             hipStream_t st);
+
+// Min-margin input gradient.
+hipError_t launch_propagate_fc(const FcShape &s, const float *w, const float *g,
+                               const int32_t *idx, const float *min_deltas,
+                               const int32_t *min_idx, const int32_t *anchors, float *x_grad,
+                               bool int_mode, double int_rescaler, hipStream_t st);
+
+// Scratch bytes the bucketed weight-gradient path needs (0 if it does not apply).
+size_t wgrad_fc_scratch_bytes(const FcShape &s);
+
+// Table-row gradient: target[row, o] += lr * g[b, o] for every sample b hitting row.
+// scratch may be null when wgrad_fc_scratch_bytes() is 0.
+hipError_t launch_wgrad_fc(const FcShape &s, const float *g, const int32_t *idx, float *target,
+                           double lr, bool int_mode, double int_rescaler, bool overwrite,
+                           void *scratch, hipStream_t st);
+
+// int32 fixed point -> fp32, in place.
+hipError_t launch_convert_i2f(float *buf, uint64_t n, double int_rescaler, hipStream_t st);
+
+// Stable counting sort of samples by lookup index (one wavefront per table):
+// offsets [n_detectors][E+1], samples [n_detectors][batch].
+hipError_t launch_bucket_samples(const FcShape &s, const int32_t *idx, int32_t *offsets,
+                                 int32_t *samples, hipStream_t st);
+
+// Zero n floats with a kernel (graph-capture safe, unlike hipMemsetAsync).
+hipError_t launch_zero(float *buf, uint64_t n, hipStream_t st);
+
+// ---- sparse (CSR) path ---------------------------------------------------
+// Lookup neuron n = t*E + e owns synapses [syn_offsets[n], syn_offsets[n+1]);
+// syn_targets holds output indices; the weight tensor has one fp32 per synapse.
+struct SparseShape {
+    FcShape fc;            // n_outputs, n_detectors, n_entries ... as above
+    uint32_t max_groups;   // max forward groups (of fc.ogs synapses) per lookup neuron
+};
+
+// Output-major index for the exact forward, valid when every lookup neuron of
+// a detector has the same target list ("uniform" topology, ProjectionLUTLayer):
+// for output j, in_pairs[in_offsets[j] .. in_offsets[j+1]) are (t, k) pairs in
+// ascending (t, k): synapse k of detector t's neurons targets j.
+hipError_t launch_fill_sparse_uniform(const SparseShape &s, const float *w, const int32_t *idx,
+                                      const int64_t *syn_offsets, const int64_t *in_offsets,
+                                      const int32_t *in_pairs, float *out, bool int_mode,
+                                      double int_rescaler, hipStream_t st);
+
+// Generic forward: one thread per (b, t, group), fp32 (or int32) atomics.
+hipError_t launch_fill_sparse_atomic(const SparseShape &s, const float *w, const int32_t *idx,
+                                     const int64_t *syn_offsets, const int32_t *syn_targets,
+                                     float *out, bool int_mode, double int_rescaler,
+                                     hipStream_t st);
+
+hipError_t launch_propagate_sparse(const SparseShape &s, const float *w, const float *g,
+                                   const int32_t *idx, const float *min_deltas,
+                                   const int32_t *min_idx, const int32_t *anchors,
+                                   const int64_t *syn_offsets, const int32_t *syn_targets,
+                                   float *x_grad, bool int_mode, double int_rescaler,
+                                   hipStream_t st);
+
+// Scratch: the same bucket arrays as the FC path.
+size_t wgrad_sparse_scratch_bytes(const SparseShape &s);
+
+hipError_t launch_wgrad_sparse(const SparseShape &s, const float *g, const int32_t *idx,
+                               const int64_t *syn_offsets, const int32_t *syn_targets,
+                               float *target, double lr, bool int_mode, double int_rescaler,
+                               void *scratch, uint64_t n_synapses, hipStream_t st);
+
+}  // namespace spiky

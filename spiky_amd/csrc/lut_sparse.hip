@@ -1,0 +1,294 @@
+// lut_sparse.hip -- sparse (ProjectionLUTLayer) LUT kernels for gfx950.
+//
+// Connectivity is this build's CSR (see lut_kernels.h): lookup neuron
+// n = t*E + e owns synapses [syn_offsets[n], syn_offsets[n+1]) with output
+// indices syn_targets[s] and one fp32 weight w[s] each.  A neuron's synapses
+// form forward groups of `ogs` (forward_group_size) in list order, the unit of
+// the reference's ForwardSynapseGroup (connections_manager.h:39-66).
+//
+//   k_fill_sparse_uniform  one thread per (b, output): walks the outputs'
+//                          incoming (detector, slot) pairs in ascending order,
+//                          which is the reference CPU path's commit order, so the
+//                          fp32 result is bit-identical to it (no atomics).
+//   k_fill_sparse_atomic   one thread per (b, t, group): the reference's own
+//                          decomposition with fp32/int32 atomics (any topology).
+//   k_propagate_sparse     one thread per (b, t, group): main/alt group dots in
+//                          fp64 and the min-margin anchor update.
+//   k_wgrad_sparse_rowsum  one thread per synapse: sums lr*g over the samples
+//                          bucketed on its lookup neuron, ascending (bit-identical
+//                          to the reference CPU path), and writes it once.
+#include "lut_kernels.h"
+
+#include <algorithm>
+
+namespace spiky {
+namespace {
+
+constexpr int kBlock = 256;
+
+__device__ __forceinline__ int32_t wrap_add(int32_t a, int32_t b) {
+    return (int32_t)((uint32_t)a + (uint32_t)b);
+}
+
+__device__ __forceinline__ double du_of_margin(float md) {
+    double du = (double)md;
+    double r = 1.0 / (1.0 + fabs(du));
+    return (du > 0) ? r * (0.5 * r) : r * (-0.5 * r);
+}
+
+uint32_t blocks_for(uint64_t n) { return (uint32_t)((n + kBlock - 1) / kBlock); }
+
+// fill_outputs_non_seq_sparse_logic (lut_runtime_kernels_logic.proto:1160-1212)
+// with fire_single_synapse_group (proto:215-313): every synapse commits
+// (float)(double)w, or the int32 payload trunc(w*DENOM32*int_rescaler).
+template <bool INT_MODE>
+__global__ __launch_bounds__(kBlock) void k_fill_sparse_uniform(
+    const float *__restrict__ w, const int32_t *__restrict__ idx,
+    const int64_t *__restrict__ syn_offsets, const int64_t *__restrict__ in_offsets,
+    const int2 *__restrict__ in_pairs, float *__restrict__ out, uint32_t batch,
+    uint32_t n_outputs, uint32_t n_detectors, uint32_t n_entries, double int_rescaler) {
+    const uint64_t item = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (item >= (uint64_t)batch * n_outputs) return;
+    const uint32_t b = (uint32_t)(item / n_outputs);
+    const uint32_t j = (uint32_t)(item % n_outputs);
+    const int32_t *ib = idx + (size_t)b * n_detectors;
+    float acc = out[item];
+    int32_t iacc = __float_as_int(acc);
+    const uint32_t emask = n_entries - 1;
+    for (int64_t p = in_offsets[j]; p < in_offsets[j + 1]; p++) {
+        const int2 tk = in_pairs[p];
+        const uint32_t n = (uint32_t)tk.x * n_entries + ((uint32_t)ib[tk.x] & emask);
+        const double wt = (double)w[syn_offsets[n] + tk.y];
+        if (INT_MODE)
+            iacc = wrap_add(iacc, (int32_t)(wt * kDenom32 * int_rescaler));
+        else
+            acc += (float)wt;
+    }
+    if (INT_MODE)
+        out[item] = (float)(((double)iacc * kDenom32Reciproc) / int_rescaler);
+    else
+        out[item] = acc;
+}
+
+template <bool INT_MODE>
+__global__ __launch_bounds__(kBlock) void k_fill_sparse_atomic(
+    const float *__restrict__ w, const int32_t *__restrict__ idx,
+    const int64_t *__restrict__ syn_offsets, const int32_t *__restrict__ syn_targets,
+    float *__restrict__ out, uint32_t n_outputs, uint32_t n_detectors, uint32_t n_entries,
+    uint32_t ogs, uint32_t max_groups, uint64_t n_items, double int_rescaler) {
+    const uint64_t item = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (item >= n_items) return;
+    const uint32_t grp = (uint32_t)(item % max_groups);
+    const uint64_t bt = item / max_groups;
+    const uint32_t t = (uint32_t)(bt % n_detectors);
+    const uint32_t b = (uint32_t)(bt / n_detectors);
+    const uint32_t n = t * n_entries + ((uint32_t)idx[bt] & (n_entries - 1));
+    const int64_t s0 = syn_offsets[n] + (int64_t)grp * ogs;
+    const int64_t s1 = min(s0 + (int64_t)ogs, syn_offsets[n + 1]);
+    float *ob = out + (size_t)b * n_outputs;
+    for (int64_t s = s0; s < s1; s++) {
+        const uint32_t tg = (uint32_t)syn_targets[s];
+        if (tg >= n_outputs) continue;
+        const double wt = (double)w[s];
+        if (INT_MODE)
+            atomicAdd(reinterpret_cast<int32_t *>(ob + tg), (int32_t)(wt * kDenom32 * int_rescaler));
+        else
+            unsafeAtomicAdd(ob + tg, (float)wt);
+    }
+}
+
+// propagate_through_detectors_non_seq_sparse_logic (proto:1303-1419) with
+// accumulate_grad_sum_sparse (proto:315-395).
+template <bool INT_MODE>
+__global__ __launch_bounds__(kBlock) void k_propagate_sparse(
+    const float *__restrict__ w, const float *__restrict__ g, const int32_t *__restrict__ idx,
+    const float *__restrict__ md, const int32_t *__restrict__ mi, const int2 *__restrict__ anchors,
+    const int64_t *__restrict__ syn_offsets, const int32_t *__restrict__ syn_targets,
+    float *__restrict__ x_grad, uint32_t n_inputs, uint32_t n_outputs, uint32_t n_detectors,
+    uint32_t n_anchors, uint32_t n_entries, uint32_t ogs, uint32_t max_groups, uint64_t n_items,
+    double int_rescaler) {
+    const uint64_t item = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (item >= n_items) return;
+    const uint32_t grp = (uint32_t)(item % max_groups);
+    const uint64_t bt = item / max_groups;
+    const uint32_t t = (uint32_t)(bt % n_detectors);
+    const uint32_t b = (uint32_t)(bt / n_detectors);
+    const int32_t m = mi[bt];
+    if (m < 0 || (uint32_t)m >= n_anchors) return;
+    const uint32_t r = (uint32_t)idx[bt] & (n_entries - 1);
+    const uint32_t nm = t * n_entries + r;
+    const uint32_t na = t * n_entries + (r ^ (1u << m));
+    const float *gb = g + (size_t)b * n_outputs;
+    double ms = 0.0, as = 0.0;
+    {
+        const int64_t s0 = syn_offsets[nm] + (int64_t)grp * ogs;
+        const int64_t s1 = min(s0 + (int64_t)ogs, syn_offsets[nm + 1]);
+        for (int64_t s = s0; s < s1; s++) {
+            const uint32_t tg = (uint32_t)syn_targets[s];
+            if (tg < n_outputs) ms += (double)w[s] * (double)gb[tg];
+        }
+    }
+    {
+        const int64_t s0 = syn_offsets[na] + (int64_t)grp * ogs;
+        const int64_t s1 = min(s0 + (int64_t)ogs, syn_offsets[na + 1]);
+        for (int64_t s = s0; s < s1; s++) {
+            const uint32_t tg = (uint32_t)syn_targets[s];
+            if (tg < n_outputs) as += (double)w[s] * (double)gb[tg];
+        }
+    }
+    const double du = du_of_margin(md[bt]) * (ms - as);
+    if (!(fabs(du) > kEps)) return;
+    const int2 a = anchors[(size_t)t * n_anchors + m];
+    if ((uint32_t)a.x >= n_inputs || (uint32_t)a.y >= n_inputs) return;
+    float *xg = x_grad + (size_t)b * n_inputs;
+    if (INT_MODE) {
+        const int32_t d = (int32_t)(du * kDenom32 * int_rescaler);
+        atomicAdd(reinterpret_cast<int32_t *>(xg + a.x), d);
+        atomicAdd(reinterpret_cast<int32_t *>(xg + a.y), (int32_t)(0u - (uint32_t)d));
+    } else {
+        unsafeAtomicAdd(xg + a.x, (float)du);
+        unsafeAtomicAdd(xg + a.y, (float)(-du));
+    }
+}
+
+// gather_w_gradients_non_seq_sparse_logic (proto:1501-1545) with
+// gather_weight_gradients_sparse (proto:584-714), one thread per synapse.
+// The neuron of synapse s is found by binary search in syn_offsets.
+template <bool INT_MODE>
+__global__ __launch_bounds__(kBlock) void k_wgrad_sparse_rowsum(
+    const float *__restrict__ g, const int32_t *__restrict__ offsets,
+    const int32_t *__restrict__ samples, const int64_t *__restrict__ syn_offsets,
+    const int32_t *__restrict__ syn_targets, float *__restrict__ target, uint32_t batch,
+    uint32_t n_outputs, uint32_t n_entries, uint64_t n_lookup, uint64_t n_synapses, double lr,
+    double int_rescaler) {
+    const uint64_t s = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (s >= n_synapses) return;
+    // largest n with syn_offsets[n] <= s
+    uint64_t lo = 0, hi = n_lookup;
+    while (hi - lo > 1) {
+        const uint64_t mid = (lo + hi) / 2;
+        if ((uint64_t)syn_offsets[mid] <= s) lo = mid; else hi = mid;
+    }
+    const uint32_t t = (uint32_t)(lo / n_entries);
+    const uint32_t e = (uint32_t)(lo % n_entries);
+    const int32_t *off_t = offsets + (size_t)t * (n_entries + 1);
+    const int32_t beg = off_t[e], end = off_t[e + 1];
+    const uint32_t tg = (uint32_t)syn_targets[s];
+    if (beg == end || tg >= n_outputs) {
+        if (INT_MODE) {
+            const double y = (double)__float_as_int(target[s]) * kDenom32Reciproc;
+            target[s] = (float)(y / int_rescaler);
+        }
+        return;
+    }
+    const int32_t *smp = samples + (size_t)t * batch;
+    float acc = target[s];
+    int32_t iacc = __float_as_int(acc);
+    for (int32_t k = beg; k < end; k++) {
+        const double gg = (double)g[(size_t)smp[k] * n_outputs + tg];
+        if (!(fabs(gg) > kEps)) continue;
+        if (INT_MODE)
+            iacc = wrap_add(iacc, (int32_t)(gg * lr * kDenom32 * int_rescaler));
+        else
+            acc += (float)(gg * lr);
+    }
+    if (INT_MODE)
+        target[s] = (float)(((double)iacc * kDenom32Reciproc) / int_rescaler);
+    else
+        target[s] = acc;
+}
+
+}  // namespace
+
+hipError_t launch_fill_sparse_uniform(const SparseShape &s, const float *w, const int32_t *idx,
+                                      const int64_t *syn_offsets, const int64_t *in_offsets,
+                                      const int32_t *in_pairs, float *out, bool int_mode,
+                                      double int_rescaler, hipStream_t st) {
+    const uint64_t n = (uint64_t)s.fc.batch * s.fc.n_outputs;
+    if (n == 0) return hipSuccess;
+    const int2 *pairs = reinterpret_cast<const int2 *>(in_pairs);
+    if (int_mode)
+        hipLaunchKernelGGL(k_fill_sparse_uniform<true>, dim3(blocks_for(n)), dim3(kBlock), 0, st,
+                           w, idx, syn_offsets, in_offsets, pairs, out, s.fc.batch, s.fc.n_outputs,
+                           s.fc.n_detectors, s.fc.n_entries, int_rescaler);
+    else
+        hipLaunchKernelGGL(k_fill_sparse_uniform<false>, dim3(blocks_for(n)), dim3(kBlock), 0, st,
+                           w, idx, syn_offsets, in_offsets, pairs, out, s.fc.batch, s.fc.n_outputs,
+                           s.fc.n_detectors, s.fc.n_entries, int_rescaler);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_sparse_atomic(const SparseShape &s, const float *w, const int32_t *idx,
+                                     const int64_t *syn_offsets, const int32_t *syn_targets,
+                                     float *out, bool int_mode, double int_rescaler,
+                                     hipStream_t st) {
+    const uint64_t n_items = (uint64_t)s.fc.batch * s.fc.n_detectors * s.max_groups;
+    if (n_items == 0) return hipSuccess;
+    if (int_mode)
+        hipLaunchKernelGGL(k_fill_sparse_atomic<true>, dim3(blocks_for(n_items)), dim3(kBlock), 0,
+                           st, w, idx, syn_offsets, syn_targets, out, s.fc.n_outputs,
+                           s.fc.n_detectors, s.fc.n_entries, s.fc.ogs, s.max_groups, n_items,
+                           int_rescaler);
+    else
+        hipLaunchKernelGGL(k_fill_sparse_atomic<false>, dim3(blocks_for(n_items)), dim3(kBlock), 0,
+                           st, w, idx, syn_offsets, syn_targets, out, s.fc.n_outputs,
+                           s.fc.n_detectors, s.fc.n_entries, s.fc.ogs, s.max_groups, n_items,
+                           int_rescaler);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || !int_mode) return e;
+    return launch_convert_i2f(out, (uint64_t)s.fc.batch * s.fc.n_outputs, int_rescaler, st);
+}
+
+hipError_t launch_propagate_sparse(const SparseShape &s, const float *w, const float *g,
+                                   const int32_t *idx, const float *min_deltas,
+                                   const int32_t *min_idx, const int32_t *anchors,
+                                   const int64_t *syn_offsets, const int32_t *syn_targets,
+                                   float *x_grad, bool int_mode, double int_rescaler,
+                                   hipStream_t st) {
+    const uint64_t n_items = (uint64_t)s.fc.batch * s.fc.n_detectors * s.max_groups;
+    if (n_items == 0) return hipSuccess;
+    const int2 *ap = reinterpret_cast<const int2 *>(anchors);
+    if (int_mode)
+        hipLaunchKernelGGL(k_propagate_sparse<true>, dim3(blocks_for(n_items)), dim3(kBlock), 0,
+                           st, w, g, idx, min_deltas, min_idx, ap, syn_offsets, syn_targets,
+                           x_grad, s.fc.n_inputs, s.fc.n_outputs, s.fc.n_detectors,
+                           s.fc.n_anchors, s.fc.n_entries, s.fc.ogs, s.max_groups, n_items,
+                           int_rescaler);
+    else
+        hipLaunchKernelGGL(k_propagate_sparse<false>, dim3(blocks_for(n_items)), dim3(kBlock), 0,
+                           st, w, g, idx, min_deltas, min_idx, ap, syn_offsets, syn_targets,
+                           x_grad, s.fc.n_inputs, s.fc.n_outputs, s.fc.n_detectors,
+                           s.fc.n_anchors, s.fc.n_entries, s.fc.ogs, s.max_groups, n_items,
+                           int_rescaler);
+    return hipGetLastError();
+}
+
+size_t wgrad_sparse_scratch_bytes(const SparseShape &s) {
+    return ((size_t)s.fc.n_detectors * (s.fc.n_entries + 1) +
+            (size_t)s.fc.n_detectors * s.fc.batch) * sizeof(int32_t);
+}
+
+hipError_t launch_wgrad_sparse(const SparseShape &s, const float *g, const int32_t *idx,
+                               const int64_t *syn_offsets, const int32_t *syn_targets,
+                               float *target, double lr, bool int_mode, double int_rescaler,
+                               void *scratch, uint64_t n_synapses, hipStream_t st) {
+    if (n_synapses == 0) return hipSuccess;
+    int32_t *offsets = reinterpret_cast<int32_t *>(scratch);
+    int32_t *samples = offsets + (size_t)s.fc.n_detectors * (s.fc.n_entries + 1);
+    hipError_t e = launch_bucket_samples(s.fc, idx, offsets, samples, st);
+    if (e != hipSuccess) return e;
+    const uint64_t n_lookup = (uint64_t)s.fc.n_detectors * s.fc.n_entries;
+    if (int_mode)
+        hipLaunchKernelGGL(k_wgrad_sparse_rowsum<true>, dim3(blocks_for(n_synapses)), dim3(kBlock),
+                           0, st, g, offsets, samples, syn_offsets, syn_targets, target,
+                           s.fc.batch, s.fc.n_outputs, s.fc.n_entries, n_lookup, n_synapses, lr,
+                           int_rescaler);
+    else
+        hipLaunchKernelGGL(k_wgrad_sparse_rowsum<false>, dim3(blocks_for(n_synapses)),
+                           dim3(kBlock), 0, st, g, offsets, samples, syn_offsets, syn_targets,
+                           target, s.fc.batch, s.fc.n_outputs, s.fc.n_entries, n_lookup,
+                           n_synapses, lr, int_rescaler);
+    return hipGetLastError();
+}
+
+}  // namespace spiky

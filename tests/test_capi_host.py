@@ -1,0 +1,184 @@
+"""CPU-side checks of the drop-in boundary: the C-ABI library loads and exports
+every entry point include/spiky_lut.h declares; host-side validation raises the
+reference's exception types and messages; the receptive-field builder obeys
+the invariants the reference's own structural tests check
+(src/spiky/lut/tests/test_lut_forward_simple.py:163-219).  No GPU is touched."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    text = open(os.path.join(ROOT, "include", "spiky_lut.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(spiky_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from spiky_amd import _native
+    L = _native.lib()
+    names = header_functions()
+    assert len(names) >= 20
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+    # and the Python binding binds each of them
+    assert set(names) <= set(_native.exported_symbols())
+    assert b"gfx950" in L.spiky_lut_version()
+
+
+def test_constructor_validation():
+    from spiky_amd import LUTDataManagerF, LUTDataManagerI
+    with pytest.raises(ValueError, match="n_inputs == 0"):
+        LUTDataManagerF(0, 1, 1, 1, 1, 0, 0, 32, 32)
+    with pytest.raises(ValueError, match="forward_group_size > MAX_SYNAPSE_GROUP_SIZE"):
+        LUTDataManagerF(4, 1, 1, 1, 1, 0, 0, 4096, 32)
+    with pytest.raises(ValueError, match="backward_group_size == 0"):
+        LUTDataManagerF(4, 1, 1, 1, 1, 0, 0, 32, 0)
+    dm = LUTDataManagerI(4, 2, 3, 2, 1, 0, 0, 32, 32, 0.5)
+    assert dm.get_summations_data_type() == "int32"
+    assert dm.get_smallest_distinguishable_fraction() == pytest.approx((1.0 / 0xFFFFF) / 0.5)
+    assert dm.get_number_of_lookup_neurons() == 3 * 4
+    with pytest.raises(ValueError, match="learning_rate > 1"):
+        dm.register_synapse_meta(1.5, 0, 1, 0, 0)
+    assert dm.register_synapse_meta(1.0, 0, 1, 0, 0) == 0
+    assert dm.register_synapse_meta(1.0, 0, 1, 0, 0) == 0  # identical meta is reused
+    dm.initialize_neurons(True)
+    with pytest.raises(ValueError, match="can't register new synapse metas"):
+        dm.register_synapse_meta(0.5, 0, 1, 0, 0)
+    assert dm.get_weights_dimension() == 12 * 2
+    assert dm.get_max_forward_groups_per_neuron() == 1
+
+
+def test_backward_without_forward_is_value_error():
+    """lut.cu:1047-1049: backward before any forward raises 'no active context'.
+    Called through the C ABI directly; the check precedes any device access."""
+    from spiky_amd import _native
+    L = _native.lib()
+    h = ctypes.c_void_p()
+    _native.check(L.spiky_lut_create(8, 4, 4, 2, 1, 0, 0, 32, 32, 0, 0.0, ctypes.byref(h)))
+    try:
+        _native.check(L.spiky_lut_register_synapse_meta(h, 1.0, 0.0, 1.0, 0.0, 0.0, None))
+        _native.check(L.spiky_lut_initialize_neurons(h, 1))
+        dummy = ctypes.c_void_p(16)
+        with pytest.raises(ValueError, match="no active context"):
+            _native.check(L.spiky_lut_backward_backprop(h, dummy, 1, dummy, dummy, dummy, dummy, dummy,
+                                                        dummy, -1.0, dummy, 0, None))
+        with pytest.raises(ValueError, match="batch_size == 0"):
+            _native.check(L.spiky_lut_forward_step(h, dummy, 0, dummy, dummy, dummy, dummy, 0.0,
+                                                   None, None, None))
+    finally:
+        L.spiky_lut_destroy(h)
+
+
+def test_cpu_compute_is_refused():
+    """There is no CPU fallback: compute on a CPU-resident layer raises."""
+    from spiky_amd import LUTLayer
+    layer = LUTLayer(16, 3, 8, 4, random_seed=1)
+    with pytest.raises(RuntimeError, match="HIP devices only"):
+        layer(torch.rand(2, 1, 16))
+
+
+def test_tensor_checks():
+    from spiky_amd.lut.lut_data_manager import check_tensor
+    with pytest.raises(RuntimeError, match="must be flat"):
+        check_tensor(torch.zeros(2, 2), "t", True, -1)
+    with pytest.raises(RuntimeError, match="must have dtype int32"):
+        check_tensor(torch.zeros(2), "t", False, -1)
+    with pytest.raises(RuntimeError, match="must be contiguous"):
+        check_tensor(torch.zeros(4)[::2], "t", True, -1)
+
+
+def test_anchor_decode_matches_oracle(oracle):
+    """The library's host decode equals the oracle's on random lists."""
+    from spiky_amd import _native
+    rng = np.random.default_rng(0)
+    T, n, Nc = 50, 30, 6
+    ids = np.sort(rng.choice(1000, size=(T, n)), axis=1).astype(np.int32).reshape(-1)
+    offs = np.arange(T + 1, dtype=np.int64) * n
+    codes = rng.integers(0, 2 ** 31 - 1, size=T * n).astype(np.uint32)
+    out = np.zeros(T * Nc * 2, np.int32)
+    vp = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    _native.check(_native.lib().spiky_lut_decode_anchors_compact(vp(codes), T, n, Nc, vp(offs),
+                                                                 vp(ids), vp(out)))
+    ref, err = oracle.decode_anchors_compact(codes.astype(np.int64), T, n, Nc, offs, ids)
+    assert err == 0 and np.array_equal(out, ref)
+
+
+def test_fc_layer_anchors_are_the_reference_compact_draw():
+    """LUTLayer(random_seed=s) anchors = compact decode of
+    torch.randint(I*(I-1), [N_t, I], generator=manual_seed(s)) over the list
+    0..I-1 (reference LUTLayer.py:373-407, proto:101-117)."""
+    from spiky_amd import LUTLayer
+    I, T, Nc = 20, 6, 3
+    layer = LUTLayer(I, Nc, T, 4, random_seed=123)
+    g = torch.Generator().manual_seed(123)
+    codes = torch.randint(I * (I - 1), [T, I], dtype=torch.int32, generator=g).numpy()
+    expect = []
+    for t in range(T):
+        for k in range(Nc):
+            c = int(codes[t, k]) % (I * (I - 1))
+            a1, a2 = divmod(c, I - 1)
+            if a2 >= a1:
+                a2 += 1
+            expect += [a1, a2]
+    assert layer._detector_anchors.tolist() == expect
+
+
+def test_chunk_roundtrip():
+    from spiky_amd.util.chunk_of_connections import (build_connections, parse_connections,
+                                                     repeat_connections_incrementing_source)
+    src = [3, 7]
+    offs = [0, 5, 6]
+    tg = [10, 11, 12, 13, 14, 99]
+    ch = build_connections(src, offs, tg, 2)
+    s, t = parse_connections(ch.get_connections(), 2)
+    assert list(zip(s.tolist(), t.tolist())) == [(3, 10), (3, 11), (3, 12), (3, 13), (3, 14), (7, 99)]
+    rep = repeat_connections_incrementing_source(ch, 3)
+    s, t = parse_connections(rep.get_connections(), 2)
+    pairs = set(zip(s.tolist(), t.tolist()))
+    assert (5, 14) in pairs and (9, 99) in pairs and len(pairs) == 18
+
+
+def test_projection_builder_invariants():
+    """Every anchor lies in its detector's receptive rectangle around the group
+    centre; every lookup neuron of a group has the group's targets, which lie
+    in the projection rectangle around the scaled centre and in the output mask."""
+    from spiky_amd import ProjectionLUTLayer
+    H = W = 28
+    OH, OW = 20, 20
+    rh, rw, ph, pw = 5, 5, 4, 4
+    groups, per = 30, 6
+    out_mask = torch.ones(OH, OW, dtype=torch.bool)
+    out_mask[:, :3] = False
+    layer = ProjectionLUTLayer((H, W), (OH, OW), 4, groups, per, (rh, rw), (ph, pw),
+                               output_sparsity_mask=out_mask, random_seed=9)
+    E = 16
+    centers = layer._group_centers * torch.tensor([H / OH, W / OW])  # back to input scale
+    anchors = layer._export_anchors()
+    for t in range(groups * per):
+        cx, cy = centers[t // per].tolist()
+        for a in anchors[t].reshape(-1).tolist():
+            y, x = divmod(a, W)
+            assert abs(x - cx) <= (rw - 1) / 2 + 1e-3 and abs(y - cy) <= (rh - 1) / 2 + 1e-3
+    offs, tg = layer._lut_dm.lookup_connectivity()
+    for grp in range(groups):
+        n0 = grp * per * E
+        base = tg[offs[n0]:offs[n0 + 1]]
+        assert len(base) > 0 and list(base) == sorted(base)
+        for n in range(n0, n0 + per * E):
+            assert np.array_equal(tg[offs[n]:offs[n + 1]], base)
+        cx, cy = layer._group_centers[grp].tolist()
+        for o in base.tolist():
+            y, x = divmod(o, OW)
+            assert out_mask[y, x]
+            assert abs(x - cx) <= pw / 2 + 1e-3 and abs(y - cy) <= ph / 2 + 1e-3
+        # and no output inside the rectangle (and the mask) is missing
+        inside = [y * OW + x for y in range(OH) for x in range(OW)
+                  if out_mask[y, x] and abs(x - cx) <= pw / 2 and abs(y - cy) <= ph / 2]
+        assert set(inside) <= set(base.tolist())

@@ -1,0 +1,210 @@
+"""GPU parity of the fully connected LUT path against the CPU oracle.
+
+Bars (fixed by the task's north star):
+  * lookup indices, min-margin values and indices: bit-exact;
+  * forward output: bit-exact (the kernel keeps the reference CPU path's block
+    grouping and commit order);
+  * weight gradient: bit-exact (table-major bucketed kernel, ascending samples);
+  * int32 summation (forward, input and weight gradients): bit-exact;
+  * fp32 input gradient: the reference commits it with atomics, so only a
+    tolerance applies: |gpu - cpu| <= 1e-5 * max|x_grad[b, :]| per sample row.
+"""
+import numpy as np
+import pytest
+import torch
+
+from spiky_amd import LUTDataManagerF, LUTDataManagerI
+
+pytestmark = pytest.mark.gpu
+
+XG_RTOL = 1e-5
+
+
+def make_dm(I, O, T, Nc, fgs=32, bgs=32, int_rescaler=None, lr=1.0):
+    if int_rescaler is None:
+        dm = LUTDataManagerF(I, O, T, Nc, 1, 0, 0, fgs, bgs)
+    else:
+        dm = LUTDataManagerI(I, O, T, Nc, 1, 0, 0, fgs, bgs, int_rescaler)
+    dm.register_synapse_meta(lr, -10.0, 10.0, 0.0, 0.0)
+    dm.initialize_neurons(True)
+    dm.to_device(0)
+    return dm
+
+
+def make_inputs(seed, B, I, T, Nc, O, x_normal=False):
+    g = torch.Generator().manual_seed(seed)
+    E = 1 << Nc
+    x = torch.randn(B * I, generator=g) if x_normal else torch.rand(B * I, generator=g)
+    anchors = torch.stack([torch.randperm(I, generator=g)[:2] for _ in range(T * Nc)]).to(torch.int32).flatten()
+    W = torch.randn(T * E * O, generator=g) * 0.01
+    go = torch.randn(B * O, generator=g)
+    return x, anchors, W, go
+
+
+def xg_close(gpu, cpu, B, I):
+    gpu = gpu.reshape(B, I)
+    cpu = cpu.reshape(B, I)
+    scale = np.abs(cpu).max(axis=1, keepdims=True) + 1e-30
+    err = np.abs(gpu - cpu)
+    assert np.all(err <= XG_RTOL * scale), f"max rel err {np.max(err / scale)}"
+
+
+def run_fc(oracle, B, I, T, Nc, O, fgs=32, bgs=32, cmp_eps=0.0, seed=0, int_rescaler=None, lr=1.0):
+    dev = torch.device("cuda:0")
+    E = 1 << Nc
+    int_mode = int_rescaler is not None
+    x, anchors, W, go = make_inputs(seed, B, I, T, Nc, O)
+    dm = make_dm(I, O, T, Nc, fgs, bgs, int_rescaler, lr)
+    xd, ad, Wd, gd = x.to(dev), anchors.to(dev), W.to(dev), go.to(dev)
+    out = torch.zeros(B * O, device=dev)
+    idx = torch.empty(B * T, dtype=torch.int32, device=dev)
+    md = torch.empty(B * T, device=dev)
+    mi = torch.empty(B * T, dtype=torch.int32, device=dev)
+    print(f"[fc] B={B} I={I} T={T} Nc={Nc} O={O} fgs={fgs} bgs={bgs} int={int_mode}", flush=True)
+    dm.forward_step(Wd, B, xd, ad, out, idx, cmp_eps, None, md, mi)
+    xg = torch.zeros(B * I, device=dev)
+    wg = torch.empty(T * E * O, device=dev)
+    dm.backward_backprop(Wd, B, gd, ad, idx, md, mi, xg, -1.0, wg, None,
+                         overwrite_weights_gradients=True)
+    wg_acc = torch.zeros(T * E * O, device=dev)
+    xg2 = torch.zeros(B * I, device=dev)
+    dm.backward_backprop(Wd, B, gd, ad, idx, md, mi, xg2, -1.0, wg_acc, None)
+    torch.cuda.synchronize()
+    # oracle
+    xn, an, Wn, gn = x.numpy(), anchors.numpy(), W.numpy(), go.numpy()
+    ridx, rmd, rmi = oracle.check_detectors(xn, an, B, I, T, Nc, cmp_eps)
+    rout = oracle.fill_outputs_fc(Wn, ridx, B, O, T, E, dgs=bgs, int_mode=int_mode,
+                                  int_rescaler=int_rescaler or 1.0)
+    if int_mode:
+        oracle.convert_int_to_float(rout, int_rescaler)
+    rxg = oracle.propagate_fc(Wn, gn, ridx, rmd, rmi, an, B, I, O, T, Nc, E, ogs=fgs,
+                              int_mode=int_mode, int_rescaler=int_rescaler or 1.0)
+    if int_mode:
+        oracle.convert_int_to_float(rxg, int_rescaler)
+    rwg = np.zeros(T * E * O, np.float32)
+    oracle.gather_wgrad_fc(gn, ridx, rwg, B, O, T, E, ogs=fgs, first_meta_lr=lr, int_mode=int_mode,
+                           int_rescaler=int_rescaler or 1.0)
+    if int_mode:
+        oracle.convert_int_to_float(rwg, int_rescaler)
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    assert np.array_equal(md.cpu().numpy(), rmd)
+    assert np.array_equal(mi.cpu().numpy(), rmi)
+    assert np.array_equal(out.cpu().numpy(), rout)
+    if int_mode:
+        assert np.array_equal(xg.cpu().numpy(), rxg)
+        assert np.array_equal(xg2.cpu().numpy(), rxg)
+    else:
+        xg_close(xg.cpu().numpy(), rxg, B, I)
+        xg_close(xg2.cpu().numpy(), rxg, B, I)
+    assert np.array_equal(wg.cpu().numpy(), rwg)
+    assert np.array_equal(wg_acc.cpu().numpy(), rwg)
+
+
+def test_config1_full(oracle, cuda_device):
+    run_fc(oracle, 64, 784, 256, 6, 10)
+
+
+def test_config3_shrunk(oracle, cuda_device):
+    run_fc(oracle, 16, 512, 256, 8, 1024, seed=1)
+
+
+def test_unusual_group_sizes(oracle, cuda_device):
+    # the reference's own tests use odd block sizes (test_lut_transformer_small.py:287-291)
+    run_fc(oracle, 7, 50, 70, 5, 37, fgs=4, bgs=24, seed=2)
+
+
+def test_wide_outputs_and_eps(oracle, cuda_device):
+    run_fc(oracle, 5, 64, 40, 3, 1536, seed=3, cmp_eps=0.05)
+
+
+def test_single_sample_single_table(oracle, cuda_device):
+    run_fc(oracle, 1, 2, 1, 1, 1, seed=4)
+
+
+def test_learning_rate(oracle, cuda_device):
+    run_fc(oracle, 9, 32, 33, 4, 64, seed=5, lr=0.25)
+
+
+def test_int32_summation(oracle, cuda_device):
+    run_fc(oracle, 8, 64, 100, 4, 48, seed=6, int_rescaler=0.5)
+    run_fc(oracle, 8, 64, 100, 4, 10, seed=7, int_rescaler=0.001)
+
+
+def test_eval_mode(oracle, cuda_device):
+    dev = cuda_device
+    B, I, T, Nc, O = 6, 100, 64, 6, 96
+    x, anchors, W, _ = make_inputs(8, B, I, T, Nc, O)
+    dm = make_dm(I, O, T, Nc)
+    out = torch.zeros(B * O, device=dev)
+    idx = torch.empty(B * T, dtype=torch.int32, device=dev)
+    dm.forward_step(W.to(dev), B, x.to(dev), anchors.to(dev), out, idx)
+    ridx = oracle.check_detectors(x.numpy(), anchors.numpy(), B, I, T, Nc, train=False)
+    rout = oracle.fill_outputs_fc(W.numpy(), ridx, B, O, T, 1 << Nc)
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    assert np.array_equal(out.cpu().numpy(), rout)
+
+
+def test_internal_policy_sgd(oracle, cuda_device):
+    dev = cuda_device
+    B, I, T, Nc, O = 5, 40, 50, 4, 64
+    E = 1 << Nc
+    x, anchors, W, go = make_inputs(9, B, I, T, Nc, O)
+    dm = make_dm(I, O, T, Nc, lr=0.5)
+    Wd = W.to(dev)
+    out = torch.zeros(B * O, device=dev)
+    idx = torch.empty(B * T, dtype=torch.int32, device=dev)
+    md = torch.empty(B * T, device=dev)
+    mi = torch.empty(B * T, dtype=torch.int32, device=dev)
+    dm.forward_step(Wd, B, x.to(dev), anchors.to(dev), out, idx, 0.0, None, md, mi)
+    xg = torch.zeros(B * I, device=dev)
+    dm.backward_backprop(Wd, B, go.to(dev), anchors.to(dev), idx, md, mi, xg, 0.1, None)
+    with pytest.raises(ValueError):
+        dm.backward_backprop(Wd, B, go.to(dev), anchors.to(dev), idx, md, mi, xg, 0.1,
+                             torch.zeros_like(Wd))
+    ridx, rmd, rmi = oracle.check_detectors(x.numpy(), anchors.numpy(), B, I, T, Nc)
+    rxg = oracle.propagate_fc(W.numpy(), go.numpy(), ridx, rmd, rmi, anchors.numpy(), B, I, O, T,
+                              Nc, E)
+    rW = W.numpy().copy()
+    oracle.gather_wgrad_fc(go.numpy(), ridx, rW, B, O, T, E, first_meta_lr=0.5,
+                           external_lr=np.float32(0.1))
+    xg_close(xg.cpu().numpy(), rxg, B, I)
+    assert np.array_equal(Wd.cpu().numpy(), rW)
+
+
+def test_int8_tables(oracle, cuda_device):
+    dev = cuda_device
+    B, I, T, Nc, O = 12, 256, 96, 6, 128
+    E = 1 << Nc
+    g = torch.Generator().manual_seed(10)
+    x = torch.randn(B * I, generator=g)
+    anchors = torch.stack([torch.randperm(I, generator=g)[:2] for _ in range(T * Nc)]).to(torch.int32).flatten()
+    q = torch.randint(-127, 128, (T * E * O,), generator=g, dtype=torch.int8)
+    sc = torch.rand(T, generator=g) * 0.009 + 0.001
+    for resc in (None, 1.0):
+        dm = make_dm(I, O, T, Nc, int_rescaler=resc)
+        out = torch.zeros(B * O, device=dev)
+        idx = torch.empty(B * T, dtype=torch.int32, device=dev)
+        dm.forward_step_i8(q.to(dev), sc.to(dev), B, x.to(dev), anchors.to(dev), out, idx)
+        ridx = oracle.check_detectors(x.numpy(), anchors.numpy(), B, I, T, Nc, train=False)
+        rout = oracle.fill_outputs_fc(None, ridx, B, O, T, E, q8=q.numpy(), scales=sc.numpy(),
+                                      int_mode=resc is not None, int_rescaler=resc or 1.0)
+        if resc is not None:
+            oracle.convert_int_to_float(rout, resc)
+        assert np.array_equal(idx.cpu().numpy(), ridx)
+        assert np.array_equal(out.cpu().numpy(), rout)
+
+
+def test_errors_on_device(cuda_device):
+    dev = cuda_device
+    dm = make_dm(8, 4, 4, 2)
+    W = torch.zeros(4 * 4 * 4, device=dev)
+    with pytest.raises(ValueError, match="no active context"):
+        dm.backward_backprop(W, 1, torch.zeros(4, device=dev), torch.zeros(16, dtype=torch.int32, device=dev),
+                             torch.zeros(4, dtype=torch.int32, device=dev), torch.zeros(4, device=dev),
+                             torch.zeros(4, dtype=torch.int32, device=dev), torch.zeros(8, device=dev), -1.0)
+    with pytest.raises(RuntimeError, match="must be on CUDA"):
+        dm.forward_step(W.cpu(), 1, torch.zeros(8, device=dev), torch.zeros(16, dtype=torch.int32, device=dev),
+                        torch.zeros(4, device=dev), torch.zeros(4, dtype=torch.int32, device=dev))
+    with pytest.raises(ValueError, match="batch_size == 0"):
+        dm.forward_step(W, 0, torch.zeros(8, device=dev), torch.zeros(16, dtype=torch.int32, device=dev),
+                        torch.zeros(4, device=dev), torch.zeros(4, dtype=torch.int32, device=dev))

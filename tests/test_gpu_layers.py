@@ -1,0 +1,159 @@
+"""GPU parity at the layer level (LUTLayer / ProjectionLUTLayer through the
+LUTForwardFN autograd function) and at BASELINE config 3's full size."""
+import numpy as np
+import pytest
+import torch
+
+from spiky_amd import GradientPolicy, GradientType, LUTLayer, ProjectionLUTLayer
+
+pytestmark = pytest.mark.gpu
+
+
+def _xg_close(gpu, cpu, B, I, rtol=1e-5):
+    gpu = np.asarray(gpu).reshape(B, I)
+    cpu = np.asarray(cpu).reshape(B, I)
+    scale = np.abs(cpu).max(axis=1, keepdims=True) + 1e-30
+    assert np.all(np.abs(gpu - cpu) <= rtol * scale)
+
+
+def test_lut_layer_autograd(oracle, cuda_device):
+    dev = cuda_device
+    B, I, T, Nc, O = 32, 784, 256, 6, 10
+    torch.manual_seed(0)
+    layer = LUTLayer(I, Nc, T, O, random_seed=11).to(dev)
+    with torch.no_grad():
+        layer._weights.normal_(0.0, 0.01)
+    x = torch.rand(B, 1, I, device=dev, requires_grad=True)
+    y = layer(x)
+    g = torch.randn_like(y)
+    y.backward(g)
+    E = 1 << Nc
+    an = layer._detector_anchors.cpu().numpy()
+    Wn = layer._weights.detach().cpu().numpy()
+    xn = x.detach().cpu().numpy().reshape(-1)
+    gn = g.cpu().numpy().reshape(-1)
+    ridx, rmd, rmi = oracle.check_detectors(xn, an, B, I, T, Nc)
+    rout = oracle.fill_outputs_fc(Wn, ridx, B, O, T, E)
+    rxg = oracle.propagate_fc(Wn, gn, ridx, rmd, rmi, an, B, I, O, T, Nc, E)
+    rwg = np.zeros(T * E * O, np.float32)
+    oracle.gather_wgrad_fc(gn, ridx, rwg, B, O, T, E)
+    assert np.array_equal(y.detach().cpu().numpy().reshape(-1), rout)
+    _xg_close(x.grad.cpu().numpy(), rxg, B, I)
+    assert np.array_equal(layer._weights.grad.cpu().numpy(), rwg)
+
+
+def test_lut_layer_sparse_and_normalized_policies(oracle, cuda_device):
+    dev = cuda_device
+    B, I, T, Nc, O = 8, 64, 32, 4, 16
+    for policy in (GradientPolicy(GradientType.Sparse), GradientPolicy(GradientType.Dense, normalized=True)):
+        layer = LUTLayer(I, Nc, T, O, random_seed=3, weights_gradient_policy=policy).to(dev)
+        with torch.no_grad():
+            layer._weights.normal_(0.0, 0.01)
+        x = torch.rand(B, 1, I, device=dev)
+        y = layer(x)
+        y.backward(torch.ones_like(y))
+        E = 1 << Nc
+        ridx, _, _ = oracle.check_detectors(x.cpu().numpy().reshape(-1),
+                                            layer._detector_anchors.cpu().numpy(), B, I, T, Nc)
+        rwg = np.zeros(T * E * O, np.float32)
+        oracle.gather_wgrad_fc(np.ones(B * O, np.float32), ridx, rwg, B, O, T, E)
+        got = layer._weights.grad
+        got = got.to_dense() if got.is_sparse else got
+        if policy.normalized:
+            rwg = rwg / max(np.abs(rwg).max(), 1e-16)
+        np.testing.assert_allclose(got.cpu().numpy(), rwg, rtol=1e-6, atol=0)
+
+
+def test_projection_layer_sparse_parity(oracle, cuda_device):
+    dev = cuda_device
+    torch.manual_seed(1)
+    layer = ProjectionLUTLayer((28, 28), (24, 24), 5, 36, 8, (5, 5), (4, 4), random_seed=5).to(dev)
+    with torch.no_grad():
+        layer._weights.normal_(0.0, 0.01)
+    B = 16
+    T, Nc, I, O = layer.n_detectors(), 5, 784, 576
+    E = 1 << Nc
+    x = torch.rand(B, 1, 28, 28, device=dev)
+    x = x * (torch.rand_like(x) > 0.8)
+    x.requires_grad_(True)
+    y = layer(x)
+    g = torch.randn_like(y)
+    y.backward(g)
+    offs, tg = layer._lut_dm.lookup_connectivity()
+    an = layer._detector_anchors.cpu().numpy()
+    Wn = layer._weights.detach().cpu().numpy()
+    xn = x.detach().cpu().numpy().reshape(-1)
+    gn = g.cpu().numpy().reshape(-1)
+    ridx, rmd, rmi = oracle.check_detectors(xn, an, B, I, T, Nc)
+    rout = oracle.fill_outputs_sparse(Wn, ridx, offs, tg, B, O, T, E)
+    maxg = layer._lut_dm.get_max_forward_groups_per_neuron()
+    rxg = oracle.propagate_sparse(Wn, gn, ridx, rmd, rmi, an, offs, tg, B, I, O, T, Nc, E, 32, maxg)
+    rwg = np.zeros(Wn.size, np.float32)
+    oracle.gather_wgrad_sparse(gn, ridx, offs, tg, rwg, B, O, T, E)
+    assert np.array_equal(y.detach().cpu().numpy().reshape(-1), rout)
+    _xg_close(x.grad.cpu().numpy(), rxg, B, I)
+    assert np.array_equal(layer._weights.grad.cpu().numpy(), rwg)
+
+
+@pytest.mark.parametrize("B", [1024])
+def test_config3_full_size(oracle, cuda_device, B):
+    """BASELINE config 3 at its real size.  The oracle cannot hold the whole
+    problem in seconds, so parity is checked on slices the arithmetic allows:
+    every sample's forward output depends only on its own rows (gathered
+    host-side into an E=1 table), every table's weight gradient only on that
+    table, every sample's input gradient only on its main and flipped rows."""
+    dev = cuda_device
+    I, T, Nc, O = 4096, 8192, 8, 1024
+    E = 1 << Nc
+    from spiky_amd import LUTDataManagerF
+    dm = LUTDataManagerF(I, O, T, Nc, 1, 0, 0, 32, 32)
+    dm.register_synapse_meta(1.0, -1.0, 1.0, 0.0, 0.0)
+    dm.initialize_neurons(True)
+    dm.to_device(0)
+    gen = torch.Generator(device=dev).manual_seed(3)
+    x = torch.randn(B * I, device=dev, generator=gen)
+    W = torch.randn(T * E * O, device=dev, generator=gen) * 0.01
+    go = torch.randn(B * O, device=dev, generator=gen)
+    ga = torch.Generator().manual_seed(4)
+    anchors = torch.stack([torch.randperm(I, generator=ga)[:2] for _ in range(T * Nc)]).to(torch.int32).flatten()
+    ad = anchors.to(dev)
+    out = torch.zeros(B * O, device=dev)
+    idx = torch.empty(B * T, dtype=torch.int32, device=dev)
+    md = torch.empty(B * T, device=dev)
+    mi = torch.empty(B * T, dtype=torch.int32, device=dev)
+    print("[config3] forward", flush=True)
+    dm.forward_step(W, B, x, ad, out, idx, 0.0, None, md, mi)
+    xg = torch.zeros(B * I, device=dev)
+    wg = torch.empty(T * E * O, device=dev)
+    print("[config3] backward", flush=True)
+    dm.backward_backprop(W, B, go, ad, idx, md, mi, xg, -1.0, wg, None, overwrite_weights_gradients=True)
+    torch.cuda.synchronize()
+    # every table's gradient rows sum to the batch's gradient sum (each sample hits one row per table)
+    colsum = go.view(B, O).double().sum(0)
+    per_table = wg.view(T, E, O).double().sum(1)
+    assert torch.allclose(per_table, colsum.expand(T, O), rtol=0, atol=1e-3)
+    xs = x.view(B, I)
+    samples = [0, 513, B - 1]
+    an = anchors.numpy()
+    ridx, rmd, rmi = oracle.check_detectors(xs[samples].cpu().numpy().reshape(-1), an, len(samples), I, T, Nc)
+    assert np.array_equal(idx.view(B, T)[samples].cpu().numpy().reshape(-1), ridx)
+    assert np.array_equal(md.view(B, T)[samples].cpu().numpy().reshape(-1), rmd)
+    assert np.array_equal(mi.view(B, T)[samples].cpu().numpy().reshape(-1), rmi)
+    Wv = W.view(T, E, O)
+    tt = torch.arange(T, device=dev)
+    for s in samples:
+        rows = Wv[tt, idx.view(B, T)[s].long()].cpu().numpy().reshape(-1)       # [T][O], E=1
+        r = oracle.fill_outputs_fc(rows, np.zeros((1, T), np.int32), 1, O, T, 1, dgs=32)
+        assert np.array_equal(out.view(B, O)[s].cpu().numpy(), r)
+        li = idx.view(B, T)[s].long()
+        alt = li ^ (1 << mi.view(B, T)[s].long())
+        pair = torch.stack([Wv[tt, li], Wv[tt, alt]], 1).cpu().numpy().reshape(-1)  # [T][2][O]
+        a_sub = anchors.view(T, Nc, 2)[torch.arange(T), mi.view(B, T)[s].cpu().long()].numpy().reshape(-1)
+        rxg = oracle.propagate_fc(pair, go.view(B, O)[s].cpu().numpy(), np.zeros(T, np.int32),
+                                  md.view(B, T)[s].cpu().numpy(), np.zeros(T, np.int32), a_sub, 1, I,
+                                  O, T, 1, 2, ogs=32)
+        _xg_close(xg.view(B, I)[s].cpu().numpy(), rxg, 1, I)
+    for t in (0, 4097, T - 1):
+        r = np.zeros(E * O, np.float32)
+        oracle.gather_wgrad_fc(go.cpu().numpy(), idx.view(B, T)[:, t].cpu().numpy().copy(), r, B, O, 1, E)
+        assert np.array_equal(wg.view(T, E * O)[t].cpu().numpy(), r)
