@@ -64,11 +64,31 @@ def make_anchors(T, I, Nc, seed, device):
 
 
 def load_traffic(kernel, config):
-    path = os.path.join(ROOT, "profiles", f"pmc_{kernel}_config{config}.json")
+    """HBM bytes per launch of `kernel`, from the committed rocprofv3 counter
+    summary (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the copy-kernel
+    calibration factor).  Lines read "<kernel> <bytes>"; None when absent."""
+    path = os.path.join(ROOT, "profiles", f"hbm_traffic_config{config}.txt")
     if not os.path.exists(path):
         return None
     with open(path) as f:
-        return json.load(f).get("hbm_bytes_per_launch")
+        for line in f:
+            parts = line.split()
+            if len(parts) == 2 and parts[0] == kernel and not line.startswith("#"):
+                return float(parts[1])
+    return None
+
+
+def calibrate_copy(mib):
+    """A plain device-to-device copy of `mib` MiB, five times: the known-size
+    kernel the FETCH_SIZE / WRITE_SIZE counters are scaled against."""
+    import torch
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copied {mib} MiB x5 ({n * 4} bytes read and written per copy)")
 
 
 def cpu_baseline(x, anchors, W, go, B_full, I, T, Nc, O, sample_B):
@@ -121,7 +141,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="only run a plain copy of this many MiB (counter calibration) and exit")
     args = ap.parse_args()
+    if args.calibrate_copy_mib:
+        calibrate_copy(args.calibrate_copy_mib)
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build's LUT path runs on a single MI355X "
               "(the multi-GPU table-parallel design is described, not built).", file=sys.stderr)

@@ -135,6 +135,14 @@ struct RowLoad<int8_t, 1> {
     __device__ static void load(const int8_t *p, float *v) { v[0] = (float)p[0]; }
 };
 template <>
+struct RowLoad<int8_t, 2> {
+    __device__ static void load(const int8_t *p, float *v) {
+        const char2 q = *reinterpret_cast<const char2 *>(p);
+        v[0] = (float)q.x;
+        v[1] = (float)q.y;
+    }
+};
+template <>
 struct RowLoad<int8_t, 4> {
     __device__ static void load(const int8_t *p, float *v) {
         const char4 q = *reinterpret_cast<const char4 *>(p);
@@ -145,7 +153,29 @@ struct RowLoad<int8_t, 4> {
     }
 };
 
-template <typename WT, int VEC, bool INT_MODE, bool SCALED, int DGS>
+// Column slices and XCDs.  A launch covers the outputs in `n_slices` slices of
+// 64*VEC columns; workgroup i works on slice i % n_slices.  The hardware hands
+// workgroup i to XCD i % 8, so with 8 (or 16) slices every XCD owns whole
+// slices and sees every sample's accesses to them: table rows (forward,
+// propagate) and gradient rows (weight gradient) are then re-used from that
+// XCD's L2 instead of being fetched once per sample from HBM.
+constexpr int kWPB = kBlock / kWave;  // wavefronts per workgroup
+
+// Floats per lane such that the slices number at least 8 (one per XCD).
+uint32_t pick_vec(uint32_t n_outputs) {
+    if (n_outputs % 4 == 0 && n_outputs >= 64u * 4u * 8u) return 4;
+    if (n_outputs % 2 == 0 && n_outputs >= 64u * 2u * 8u) return 2;
+    return 1;
+}
+
+// Forward gather-sum.  Wavefront = SPW samples x one column slice; each lane
+// owns VEC columns of every sample and walks the tables in ascending order,
+// with an fp64 partial per block of `dgs` tables and an fp32 (or int32) running
+// sum -- the reference CPU path's exact commit order, so the output is
+// bit-identical to it.  U tables x SPW samples of row loads are issued before
+// the ordered adds.  Sample and column indices past the end are clamped to
+// valid memory for the loads and masked at the store.
+template <typename WT, int VEC, int SPW, int U, bool INT_MODE, bool SCALED>
 __global__ __launch_bounds__(kBlock) void k_fill_fc(
     const WT *__restrict__ w, const float *__restrict__ scales, const int32_t *__restrict__ idx,
     float *__restrict__ out, uint32_t batch, uint32_t n_outputs, uint32_t n_detectors,
@@ -153,96 +183,110 @@ __global__ __launch_bounds__(kBlock) void k_fill_fc(
     const uint32_t lane = threadIdx.x & (kWave - 1);
     const uint32_t wave = uniform(threadIdx.x / kWave);
     const uint32_t slice = blockIdx.x % n_slices;
-    const uint32_t b = (blockIdx.x / n_slices) * (kBlock / kWave) + wave;
-    if (b >= batch) return;
+    const uint32_t b0 = ((blockIdx.x / n_slices) * kWPB + wave) * SPW;
+    if (b0 >= batch) return;
     const uint32_t c = (slice * kWave + lane) * VEC;
     const bool active = c < n_outputs;
+    const uint32_t cc = active ? c : 0u;
     const uint32_t emask = n_entries - 1;
-    const int32_t *ib = idx + (size_t)b * n_detectors;
-    float *ob = out + (size_t)b * n_outputs + c;
-
-    float run[VEC];
-    int32_t irun[VEC];
+    const int32_t *ib[SPW];
+    bool live[SPW];
 #pragma unroll
-    for (int v = 0; v < VEC; v++) {
-        run[v] = 0.0f;
-        irun[v] = 0;
-        if (active) {
-            if (INT_MODE)
-                irun[v] = __float_as_int(ob[v]);
-            else
-                run[v] = ob[v];
+    for (int s = 0; s < SPW; s++) {
+        live[s] = b0 + s < batch;
+        ib[s] = idx + (size_t)(live[s] ? b0 + s : b0) * n_detectors;
+    }
+
+    float run[SPW][VEC];
+    int32_t irun[SPW][VEC];
+#pragma unroll
+    for (int s = 0; s < SPW; s++) {
+#pragma unroll
+        for (int v = 0; v < VEC; v++) {
+            run[s][v] = 0.0f;
+            irun[s][v] = 0;
+            if (active && live[s]) {
+                const float o = out[(size_t)(b0 + s) * n_outputs + c + v];
+                if (INT_MODE)
+                    irun[s][v] = __float_as_int(o);
+                else
+                    run[s][v] = o;
+            }
         }
     }
 
-    const uint32_t block_len = DGS > 0 ? (uint32_t)DGS : dgs;
-    for (uint32_t t0 = 0; t0 < n_detectors; t0 += block_len) {
-        const uint32_t t1 = min(t0 + block_len, n_detectors);
-        double acc[VEC];
+    for (uint32_t t0 = 0; t0 < n_detectors; t0 += dgs) {
+        const uint32_t t1 = min(t0 + dgs, n_detectors);
+        double acc[SPW][VEC];
 #pragma unroll
-        for (int v = 0; v < VEC; v++) acc[v] = 0.0;
-        if (DGS > 0 && t1 - t0 == (uint32_t)DGS) {
-            // full block: issue all DGS row loads before the ordered adds
-            constexpr int kD = DGS > 0 ? DGS : 1;
-            float vals[kD][VEC];
+        for (int s = 0; s < SPW; s++)
 #pragma unroll
-            for (int k = 0; k < kD; k++) {
-                const uint32_t t = t0 + k;
-                const uint32_t r = (uint32_t)ib[t] & emask;
-                const WT *p = w + ((size_t)t * n_entries + r) * n_outputs + c;
-                if (active) RowLoad<WT, VEC>::load(p, vals[k]);
-                else {
+            for (int v = 0; v < VEC; v++) acc[s][v] = 0.0;
+        uint32_t t = t0;
+        for (; t + U <= t1; t += U) {
+            float vals[U][SPW][VEC];
 #pragma unroll
-                    for (int v = 0; v < VEC; v++) vals[k][v] = 0.0f;
+            for (int u = 0; u < U; u++) {
+                const WT *wt = w + (size_t)(t + u) * n_entries * n_outputs + cc;
+#pragma unroll
+                for (int s = 0; s < SPW; s++) {
+                    const uint32_t r = (uint32_t)ib[s][t + u] & emask;
+                    RowLoad<WT, VEC>::load(wt + (size_t)r * n_outputs, vals[u][s]);
                 }
                 if (SCALED) {
-                    const float sc = scales[t];
+                    const float sc = scales[t + u];
 #pragma unroll
-                    for (int v = 0; v < VEC; v++) vals[k][v] = sc * vals[k][v];
+                    for (int s = 0; s < SPW; s++)
+#pragma unroll
+                        for (int v = 0; v < VEC; v++) vals[u][s][v] = sc * vals[u][s][v];
                 }
             }
 #pragma unroll
-            for (int k = 0; k < kD; k++) {
+            for (int u = 0; u < U; u++)
 #pragma unroll
-                for (int v = 0; v < VEC; v++) acc[v] += (double)vals[k][v];
+                for (int s = 0; s < SPW; s++)
+#pragma unroll
+                    for (int v = 0; v < VEC; v++) acc[s][v] += (double)vals[u][s][v];
+        }
+        for (; t < t1; t++) {
+            const WT *wt = w + (size_t)t * n_entries * n_outputs + cc;
+            float vals[SPW][VEC];
+#pragma unroll
+            for (int s = 0; s < SPW; s++) {
+                const uint32_t r = (uint32_t)ib[s][t] & emask;
+                RowLoad<WT, VEC>::load(wt + (size_t)r * n_outputs, vals[s]);
             }
-        } else {
-#pragma unroll 8
-            for (uint32_t t = t0; t < t1; t++) {
-                const uint32_t r = (uint32_t)ib[t] & emask;
-                const WT *p = w + ((size_t)t * n_entries + r) * n_outputs + c;
-                float vals[VEC];
-                if (active) RowLoad<WT, VEC>::load(p, vals);
-                else {
+            const float sc = SCALED ? scales[t] : 1.0f;
 #pragma unroll
-                    for (int v = 0; v < VEC; v++) vals[v] = 0.0f;
-                }
-                if (SCALED) {
-                    const float sc = scales[t];
+            for (int s = 0; s < SPW; s++)
 #pragma unroll
-                    for (int v = 0; v < VEC; v++) vals[v] = sc * vals[v];
-                }
-#pragma unroll
-                for (int v = 0; v < VEC; v++) acc[v] += (double)vals[v];
-            }
+                for (int v = 0; v < VEC; v++)
+                    acc[s][v] += (double)(SCALED ? sc * vals[s][v] : vals[s][v]);
         }
 #pragma unroll
-        for (int v = 0; v < VEC; v++) {
-            if (INT_MODE)
-                irun[v] = wrap_add(irun[v], (int32_t)(acc[v] * kDenom32 * int_rescaler));
-            else
-                run[v] += (float)acc[v];
-        }
+        for (int s = 0; s < SPW; s++)
+#pragma unroll
+            for (int v = 0; v < VEC; v++) {
+                if (INT_MODE)
+                    irun[s][v] = wrap_add(irun[s][v], (int32_t)(acc[s][v] * kDenom32 * int_rescaler));
+                else
+                    run[s][v] += (float)acc[s][v];
+            }
     }
     if (!active) return;
 #pragma unroll
-    for (int v = 0; v < VEC; v++) {
-        if (INT_MODE) {
-            // convert_integers_to_floats_logic, proto:200-213
-            const double y = (double)irun[v] * kDenom32Reciproc;
-            ob[v] = (float)(y / int_rescaler);
-        } else {
-            ob[v] = run[v];
+    for (int s = 0; s < SPW; s++) {
+        if (!live[s]) continue;
+        float *ob = out + (size_t)(b0 + s) * n_outputs + c;
+#pragma unroll
+        for (int v = 0; v < VEC; v++) {
+            if (INT_MODE) {
+                // convert_integers_to_floats_logic, proto:200-213
+                const double y = (double)irun[s][v] * kDenom32Reciproc;
+                ob[v] = (float)(y / int_rescaler);
+            } else {
+                ob[v] = run[s][v];
+            }
         }
     }
 }
@@ -251,21 +295,21 @@ template <typename WT, int VEC, bool INT_MODE, bool SCALED>
 hipError_t launch_fill_variant(const FcShape &s, const WT *w, const float *scales,
                                const int32_t *idx, float *out, double int_rescaler,
                                hipStream_t st) {
-    const uint32_t cols_per_wave = kWave * VEC;
-    const uint32_t n_slices = (s.n_outputs + cols_per_wave - 1) / cols_per_wave;
-    const uint32_t waves_per_block = kBlock / kWave;
-    const uint32_t b_groups = (s.batch + waves_per_block - 1) / waves_per_block;
+    const uint32_t n_slices = (s.n_outputs + kWave * VEC - 1) / (kWave * VEC);
+    // several samples per wavefront once the batch is large enough to fill the chip
+    const uint32_t spw = s.batch >= 512 ? 4 : 1;
+    const uint32_t b_groups = (s.batch + kWPB * spw - 1) / (kWPB * spw);
     const uint64_t grid = (uint64_t)n_slices * b_groups;
     if (grid == 0) return hipSuccess;
-    if (s.dgs == 32) {
-        hipLaunchKernelGGL((k_fill_fc<WT, VEC, INT_MODE, SCALED, 32>), dim3((uint32_t)grid),
+    if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
+    if (spw == 4)
+        hipLaunchKernelGGL((k_fill_fc<WT, VEC, 4, 8, INT_MODE, SCALED>), dim3((uint32_t)grid),
                            dim3(kBlock), 0, st, w, scales, idx, out, s.batch, s.n_outputs,
                            s.n_detectors, s.n_entries, s.dgs, n_slices, int_rescaler);
-    } else {
-        hipLaunchKernelGGL((k_fill_fc<WT, VEC, INT_MODE, SCALED, 0>), dim3((uint32_t)grid),
+    else
+        hipLaunchKernelGGL((k_fill_fc<WT, VEC, 1, 16, INT_MODE, SCALED>), dim3((uint32_t)grid),
                            dim3(kBlock), 0, st, w, scales, idx, out, s.batch, s.n_outputs,
                            s.n_detectors, s.n_entries, s.dgs, n_slices, int_rescaler);
-    }
     return hipGetLastError();
 }
 
@@ -320,12 +364,13 @@ __global__ __launch_bounds__(kBlock) void k_propagate_fc_exact(
 }
 
 // ---------------------------------------------------------------------------
-// propagate, fast fp32-summation form: one wavefront per (sample, table chunk).
-// Lane l owns columns (j*64 + l)*4 .. +3 for j < NJ.  The per-table result
-// du * (sum_o W_main*g - sum_o W_alt*g) is reduced over the whole row in fp64
-// and committed as one fp32 atomic pair per (b, t); the reference commits one
-// pair per 32-output block, which differs only in fp32 rounding of the
-// committed values (the blocks' du terms are summed in fp64 here first).
+// propagate, fp32-summation form over column slices.  Wavefront = SPW samples
+// x one column slice (slice -> XCD as in the forward).  For every (sample,
+// table) the lane-partial fp64 dot  sum_c (W_main[c] - W_alt[c]) * g[c]  over
+// the slice is reduced across the wavefront, scaled by du(min margin), and
+// committed as one pair of fp32 atomics per (sample, table, slice).  The
+// reference commits one pair per 32-output block (forward_group_size); the
+// slice commit differs from it only in fp32 rounding of the committed terms.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ double wave_sum(double v) {
 #pragma unroll
@@ -333,72 +378,81 @@ __device__ __forceinline__ double wave_sum(double v) {
     return v;
 }
 
-template <int NJ>
-__global__ __launch_bounds__(kBlock) void k_propagate_fc_fast(
+template <int VEC, int SPW, int U>
+__global__ __launch_bounds__(kBlock) void k_propagate_fc_slices(
     const float *__restrict__ w, const float *__restrict__ g, const int32_t *__restrict__ idx,
     const float *__restrict__ md, const int32_t *__restrict__ mi, const int2 *__restrict__ anchors,
     float *__restrict__ x_grad, uint32_t batch, uint32_t n_inputs, uint32_t n_outputs,
-    uint32_t n_detectors, uint32_t n_anchors, uint32_t n_entries, uint32_t n_chunks,
-    uint32_t tables_per_chunk) {
+    uint32_t n_detectors, uint32_t n_anchors, uint32_t n_entries, uint32_t n_slices) {
+    static_assert(U * SPW <= kWave, "one committing lane per (sample, table)");
     const uint32_t lane = threadIdx.x & (kWave - 1);
     const uint32_t wave = uniform(threadIdx.x / kWave);
-    const uint32_t chunk = blockIdx.x % n_chunks;
-    const uint32_t b = (blockIdx.x / n_chunks) * (kBlock / kWave) + wave;
-    if (b >= batch) return;
-    const uint32_t t_begin = chunk * tables_per_chunk;
-    const uint32_t t_end = min(t_begin + tables_per_chunk, n_detectors);
+    const uint32_t slice = blockIdx.x % n_slices;
+    const uint32_t b0 = ((blockIdx.x / n_slices) * kWPB + wave) * SPW;
+    if (b0 >= batch) return;
+    const uint32_t c = (slice * kWave + lane) * VEC;
+    const bool active = c < n_outputs;
+    const uint32_t cc = active ? c : 0u;
     const uint32_t emask = n_entries - 1;
 
-    double gd[NJ][4];
-    bool act[NJ];
+    uint32_t bs[SPW];
+    double gd[SPW][VEC];
 #pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        const uint32_t c = (j * kWave + lane) * 4;
-        act[j] = c < n_outputs;
-        float4 gv = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (act[j]) gv = *reinterpret_cast<const float4 *>(g + (size_t)b * n_outputs + c);
-        gd[j][0] = gv.x;
-        gd[j][1] = gv.y;
-        gd[j][2] = gv.z;
-        gd[j][3] = gv.w;
+    for (int s = 0; s < SPW; s++) {
+        bs[s] = (b0 + s < batch) ? b0 + s : b0;
+        float gv[VEC];
+        RowLoad<float, VEC>::load(g + (size_t)bs[s] * n_outputs + cc, gv);
+#pragma unroll
+        for (int v = 0; v < VEC; v++) gd[s][v] = active ? (double)gv[v] : 0.0;
     }
-    const int32_t *ib = idx + (size_t)b * n_detectors;
-    const int32_t *mib = mi + (size_t)b * n_detectors;
-    const float *mdb = md + (size_t)b * n_detectors;
-    float *xg = x_grad + (size_t)b * n_inputs;
+    // the committing lane j = u*SPW + s handles (sample b0+s, table t+u)
+    const uint32_t my_s = lane % SPW;
+    const uint32_t my_u = lane / SPW;
+    const bool my_live = lane < (uint32_t)(U * SPW) && b0 + my_s < batch;
+    const uint32_t my_b = b0 + (my_live ? my_s : 0u);
 
-    for (uint32_t t = t_begin; t < t_end; t++) {
-        const int32_t m = mib[t];
-        const bool valid = m >= 0 && (uint32_t)m < n_anchors;
-        const uint32_t r = (uint32_t)ib[t] & emask;
-        const uint32_t ra = valid ? (r ^ (1u << m)) : r;
-        const float *wm = w + ((size_t)t * n_entries + r) * n_outputs;
-        const float *wa = w + ((size_t)t * n_entries + ra) * n_outputs;
-        double dm = 0.0, da = 0.0;
+    for (uint32_t t = 0; t < n_detectors; t += U) {
+        float mv[U][SPW][VEC], av[U][SPW][VEC];
 #pragma unroll
-        for (int j = 0; j < NJ; j++) {
-            if (act[j]) {
-                const uint32_t c = (j * kWave + lane) * 4;
-                const float4 a = *reinterpret_cast<const float4 *>(wm + c);
-                const float4 e = *reinterpret_cast<const float4 *>(wa + c);
-                dm += (double)a.x * gd[j][0];
-                dm += (double)a.y * gd[j][1];
-                dm += (double)a.z * gd[j][2];
-                dm += (double)a.w * gd[j][3];
-                da += (double)e.x * gd[j][0];
-                da += (double)e.y * gd[j][1];
-                da += (double)e.z * gd[j][2];
-                da += (double)e.w * gd[j][3];
+        for (int u = 0; u < U; u++) {
+            const uint32_t tt = min(t + u, n_detectors - 1);
+            const float *wt = w + (size_t)tt * n_entries * n_outputs + cc;
+#pragma unroll
+            for (int s = 0; s < SPW; s++) {
+                const size_t bt = (size_t)bs[s] * n_detectors + tt;
+                const int32_t m = mi[bt];
+                const uint32_t r = (uint32_t)idx[bt] & emask;
+                const uint32_t ra = (m >= 0 && (uint32_t)m < n_anchors) ? (r ^ (1u << m)) : r;
+                RowLoad<float, VEC>::load(wt + (size_t)r * n_outputs, mv[u][s]);
+                RowLoad<float, VEC>::load(wt + (size_t)ra * n_outputs, av[u][s]);
             }
         }
-        const double diff = wave_sum(dm - da);
-        if (valid && lane == 0) {
-            const double du = du_of_margin(mdb[t]) * diff;
-            if (fabs(du) > kEps) {
-                const int2 a = anchors[(size_t)t * n_anchors + m];
-                if ((uint32_t)a.x < n_inputs && (uint32_t)a.y < n_inputs) {
-                    unsafeAtomicAdd(xg + a.x, (float)du);
-                    unsafeAtomicAdd(xg + a.y, (float)(-du));
+        double mine = 0.0;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+#pragma unroll
+            for (int s = 0; s < SPW; s++) {
+                double p = 0.0;
+#pragma unroll
+                for (int v = 0; v < VEC; v++)
+                    p += ((double)mv[u][s][v] - (double)av[u][s][v]) * gd[s][v];
+                p = wave_sum(p);
+                if (lane == (uint32_t)(u * SPW + s)) mine = p;
+            }
+        }
+        const uint32_t my_t = t + my_u;
+        if (my_live && my_t < n_detectors) {
+            const size_t bt = (size_t)my_b * n_detectors + my_t;
+            const int32_t m = mi[bt];
+            if (m >= 0 && (uint32_t)m < n_anchors) {
+                const double du = du_of_margin(md[bt]) * mine;
+                if (fabs(du) > kEps) {
+                    const int2 a = anchors[(size_t)my_t * n_anchors + m];
+                    if ((uint32_t)a.x < n_inputs && (uint32_t)a.y < n_inputs) {
+                        float *xg = x_grad + (size_t)my_b * n_inputs;
+                        unsafeAtomicAdd(xg + a.x, (float)du);
+                        unsafeAtomicAdd(xg + a.y, (float)(-du));
+                    }
                 }
             }
         }
@@ -497,70 +551,106 @@ __global__ __launch_bounds__(kWave) void k_bucket_samples(
     }
 }
 
-// One wavefront per table row: target[row, :] (+)= sum over the row's bucket.
-// Lane l owns columns (j*64 + l)*VEC .. +VEC-1 for j < NJ.
-template <int NJ, int VEC, bool INT_MODE, bool OVERWRITE>
-__global__ __launch_bounds__(kBlock) void k_wgrad_rowsum(
+// Table-major weight gradient over column slices.  Wavefront = `rpw`
+// consecutive rows of one table x one column slice (slice -> XCD, so each XCD
+// only ever reads its own column slice of g, which stays in its L2).  The
+// rows' buckets are contiguous in the table's sorted sample list, so the
+// wavefront walks that list in flat batches of KB samples (KB gradient rows in
+// flight) and closes a row whenever the walk crosses its bucket end.  Within a
+// row the samples are added in ascending order into an fp32 (or int32) sum
+// starting from the target value (or zero when overwriting): the reference
+// CPU path's order, so the result is bit-identical to it, and each target
+// element is written exactly once with no atomics.
+template <int VEC, int KB, bool INT_MODE, bool OVERWRITE>
+__global__ __launch_bounds__(kBlock) void k_wgrad_slices(
     const float *__restrict__ g, const int32_t *__restrict__ offsets,
     const int32_t *__restrict__ samples, float *__restrict__ target, uint32_t batch,
-    uint32_t n_outputs, uint32_t n_entries, uint64_t n_rows, double lr, double int_rescaler) {
+    uint32_t n_outputs, uint32_t n_entries, uint32_t n_detectors, uint32_t n_slices, uint32_t rpw,
+    double lr, double int_rescaler) {
     const uint32_t lane = threadIdx.x & (kWave - 1);
-    const uint64_t wave0 = (uint64_t)blockIdx.x * (kBlock / kWave) + uniform(threadIdx.x / kWave);
-    const uint64_t n_waves = (uint64_t)gridDim.x * (kBlock / kWave);
-    for (uint64_t row = wave0; row < n_rows; row += n_waves) {
-        const uint32_t t = (uint32_t)(row / n_entries);
-        const uint32_t e = (uint32_t)(row % n_entries);
-        const int32_t *off_t = offsets + (size_t)t * (n_entries + 1);
-        const int32_t beg = off_t[e];
-        const int32_t end = off_t[e + 1];
-        if (!OVERWRITE && !INT_MODE && beg == end) continue;
-        const int32_t *smp = samples + (size_t)t * batch;
-        float *trow = target + row * n_outputs;
+    const uint32_t wave = uniform(threadIdx.x / kWave);
+    const uint32_t slice = blockIdx.x % n_slices;
+    const uint64_t unit = (uint64_t)(blockIdx.x / n_slices) * kWPB + wave;
+    const uint32_t groups = n_entries / rpw;
+    const uint64_t t64 = unit / groups;
+    if (t64 >= n_detectors) return;
+    const uint32_t t = (uint32_t)t64;
+    const uint32_t e0 = (uint32_t)(unit % groups) * rpw;
+    const uint32_t c = (slice * kWave + lane) * VEC;
+    const bool active = c < n_outputs;
+    const uint32_t cc = active ? c : 0u;
+
+    // lane i <= rpw holds the start of bucket e0 + i
+    const int32_t *off_t = offsets + (size_t)t * (n_entries + 1) + e0;
+    const int32_t offv = lane <= rpw ? off_t[lane] : 0;
+    const int32_t *smp = samples + (size_t)t * batch;
+    float *tb = target + ((size_t)t * n_entries + e0) * n_outputs + cc;
+    const int32_t kbeg = __builtin_amdgcn_readfirstlane(offv);
+    const int32_t kend = __builtin_amdgcn_readlane(offv, rpw);
+
+    float acc[VEC];
+    int32_t iacc[VEC];
+    auto init = [&](uint32_t e) {
 #pragma unroll
-        for (int j = 0; j < NJ; j++) {
-            const uint32_t c = (j * kWave + lane) * VEC;
-            if (c >= n_outputs) continue;
-            float acc[VEC];
-            int32_t iacc[VEC];
+        for (int q = 0; q < VEC; q++) {
+            acc[q] = 0.0f;
+            iacc[q] = 0;
+        }
+        if (!OVERWRITE) {
+            float v[VEC];
+            RowLoad<float, VEC>::load(tb + (size_t)e * n_outputs, v);
 #pragma unroll
             for (int q = 0; q < VEC; q++) {
-                acc[q] = 0.0f;
-                iacc[q] = 0;
+                acc[q] = v[q];
+                iacc[q] = __float_as_int(v[q]);
             }
-            if (!OVERWRITE) {
-                float v[VEC];
-                RowLoad<float, VEC>::load(trow + c, v);
-#pragma unroll
-                for (int q = 0; q < VEC; q++) {
-                    acc[q] = v[q];
-                    iacc[q] = __float_as_int(v[q]);
-                }
-            }
-            for (int32_t k = beg; k < end; k++) {
-                const uint32_t b = (uint32_t)smp[k];
-                float gs[VEC];
-                RowLoad<float, VEC>::load(g + (size_t)b * n_outputs + c, gs);
-#pragma unroll
-                for (int q = 0; q < VEC; q++) {
-                    const double gg = (double)gs[q];
-                    if (fabs(gg) > kEps) {
-                        if (INT_MODE)
-                            iacc[q] = wrap_add(iacc[q], (int32_t)(gg * lr * kDenom32 * int_rescaler));
-                        else
-                            acc[q] += (float)(gg * lr);
-                    }
-                }
-            }
-            float res[VEC];
-#pragma unroll
-            for (int q = 0; q < VEC; q++)
-                res[q] = INT_MODE ? (float)(((double)iacc[q] * kDenom32Reciproc) / int_rescaler) : acc[q];
-            if (VEC == 4)
-                *reinterpret_cast<float4 *>(trow + c) = make_float4(res[0], res[1], res[2], res[3]);
-            else
-#pragma unroll
-                for (int q = 0; q < VEC; q++) trow[c + q] = res[q];
         }
+    };
+    auto store = [&](uint32_t e) {
+        if (!active) return;
+        float *p = tb + (size_t)e * n_outputs;
+#pragma unroll
+        for (int q = 0; q < VEC; q++)
+            p[q] = INT_MODE ? (float)(((double)iacc[q] * kDenom32Reciproc) / int_rescaler) : acc[q];
+    };
+
+    uint32_t e = 0;
+    int32_t row_end = __builtin_amdgcn_readlane(offv, 1);
+    init(0);
+    for (int32_t k0 = kbeg; k0 < kend; k0 += KB) {
+        float gv[KB][VEC];
+#pragma unroll
+        for (int j = 0; j < KB; j++) {
+            const int32_t kk = min(k0 + j, kend - 1);
+            const uint32_t b = (uint32_t)smp[kk];
+            RowLoad<float, VEC>::load(g + (size_t)b * n_outputs + cc, gv[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < KB; j++) {
+            if (k0 + j >= kend) break;
+            while (k0 + j >= row_end) {
+                store(e);
+                e++;
+                row_end = __builtin_amdgcn_readlane(offv, e + 1);
+                init(e);
+            }
+#pragma unroll
+            for (int q = 0; q < VEC; q++) {
+                const double gg = (double)gv[j][q];
+                if (fabs(gg) > kEps) {
+                    if (INT_MODE)
+                        iacc[q] = wrap_add(iacc[q], (int32_t)(gg * lr * kDenom32 * int_rescaler));
+                    else
+                        acc[q] += (float)(gg * lr);
+                }
+            }
+        }
+    }
+    for (;;) {
+        store(e);
+        e++;
+        if (e >= rpw) break;
+        init(e);
     }
 }
 
@@ -579,9 +669,9 @@ __global__ __launch_bounds__(kBlock) void k_convert_i2f(float *__restrict__ buf,
 
 uint32_t blocks_for(uint64_t n) { return (uint32_t)((n + kBlock - 1) / kBlock); }
 
+// The bucketed weight gradient needs the per-table bucket counters in LDS.
 bool rowsum_applies(const FcShape &s) {
-    const uint32_t vec = (s.n_outputs % 4 == 0) ? 4 : 1;
-    return s.n_outputs <= 16u * 64u * vec && s.n_entries <= 4096 && s.batch <= 0x7fffffffu;
+    return s.n_entries <= 4096 && s.batch <= 0x7fffffffu;
 }
 
 }  // namespace
@@ -607,33 +697,33 @@ hipError_t launch_check_detectors(const FcShape &s, const float *x, const int32_
 
 hipError_t launch_fill_fc_f32(const FcShape &s, const float *w, const int32_t *idx, float *out,
                               bool int_mode, double int_rescaler, hipStream_t st) {
-    if (s.n_outputs % 2 == 0) {
-        if (int_mode)
-            return launch_fill_variant<float, 2, true, false>(s, w, nullptr, idx, out,
-                                                              int_rescaler, st);
-        return launch_fill_variant<float, 2, false, false>(s, w, nullptr, idx, out, int_rescaler,
-                                                           st);
+#define SPIKY_FILL_F32(V)                                                                        \
+    return int_mode ? launch_fill_variant<float, V, true, false>(s, w, nullptr, idx, out,        \
+                                                                 int_rescaler, st)               \
+                    : launch_fill_variant<float, V, false, false>(s, w, nullptr, idx, out,       \
+                                                                  int_rescaler, st)
+    switch (pick_vec(s.n_outputs)) {
+        case 4: SPIKY_FILL_F32(4);
+        case 2: SPIKY_FILL_F32(2);
+        default: SPIKY_FILL_F32(1);
     }
-    if (int_mode)
-        return launch_fill_variant<float, 1, true, false>(s, w, nullptr, idx, out, int_rescaler,
-                                                          st);
-    return launch_fill_variant<float, 1, false, false>(s, w, nullptr, idx, out, int_rescaler, st);
+#undef SPIKY_FILL_F32
 }
 
 hipError_t launch_fill_fc_i8(const FcShape &s, const int8_t *q8, const float *scales,
                              const int32_t *idx, float *out, bool int_mode, double int_rescaler,
                              hipStream_t st) {
-    if (s.n_outputs % 4 == 0) {
-        if (int_mode)
-            return launch_fill_variant<int8_t, 4, true, true>(s, q8, scales, idx, out,
-                                                              int_rescaler, st);
-        return launch_fill_variant<int8_t, 4, false, true>(s, q8, scales, idx, out, int_rescaler,
-                                                           st);
+#define SPIKY_FILL_I8(V)                                                                         \
+    return int_mode ? launch_fill_variant<int8_t, V, true, true>(s, q8, scales, idx, out,        \
+                                                                 int_rescaler, st)               \
+                    : launch_fill_variant<int8_t, V, false, true>(s, q8, scales, idx, out,       \
+                                                                  int_rescaler, st)
+    switch (pick_vec(s.n_outputs)) {
+        case 4: SPIKY_FILL_I8(4);
+        case 2: SPIKY_FILL_I8(2);
+        default: SPIKY_FILL_I8(1);
     }
-    if (int_mode)
-        return launch_fill_variant<int8_t, 1, true, true>(s, q8, scales, idx, out, int_rescaler,
-                                                          st);
-    return launch_fill_variant<int8_t, 1, false, true>(s, q8, scales, idx, out, int_rescaler, st);
+#undef SPIKY_FILL_I8
 }
 
 hipError_t launch_propagate_fc(const FcShape &s, const float *w, const float *g,
@@ -641,24 +731,31 @@ hipError_t launch_propagate_fc(const FcShape &s, const float *w, const float *g,
                                const int32_t *min_idx, const int32_t *anchors, float *x_grad,
                                bool int_mode, double int_rescaler, hipStream_t st) {
     const int2 *ap = reinterpret_cast<const int2 *>(anchors);
-    const uint32_t nj = (s.n_outputs + 255) / 256;
-    const bool fast = !int_mode && s.n_outputs % 4 == 0 && nj <= 4 && s.n_detectors >= 64;
-    if (fast) {
-        const uint32_t n_chunks = std::min<uint32_t>(8, s.n_detectors);
-        const uint32_t tpc = (s.n_detectors + n_chunks - 1) / n_chunks;
-        const uint32_t b_groups = (s.batch + 3) / 4;
-        const uint64_t grid = (uint64_t)n_chunks * b_groups;
-#define SPIKY_PROP_FAST(NJ)                                                                      \
-    hipLaunchKernelGGL(k_propagate_fc_fast<NJ>, dim3((uint32_t)grid), dim3(kBlock), 0, st, w, g, \
-                       idx, min_deltas, min_idx, ap, x_grad, s.batch, s.n_inputs, s.n_outputs,  \
-                       s.n_detectors, s.n_anchors, s.n_entries, n_chunks, tpc)
-        switch (nj) {
-            case 1: SPIKY_PROP_FAST(1); break;
-            case 2: SPIKY_PROP_FAST(2); break;
-            case 3: SPIKY_PROP_FAST(3); break;
-            default: SPIKY_PROP_FAST(4); break;
+    if (!int_mode && s.n_outputs >= 256) {
+        const uint32_t vec = pick_vec(s.n_outputs);
+        const uint32_t n_slices = (s.n_outputs + kWave * vec - 1) / (kWave * vec);
+        const uint32_t spw = s.batch >= 512 ? 4 : 1;
+        const uint32_t b_groups = (s.batch + kWPB * spw - 1) / (kWPB * spw);
+        const uint64_t grid = (uint64_t)n_slices * b_groups;
+        if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
+#define SPIKY_PROP(V, SPW, U)                                                                     \
+    hipLaunchKernelGGL((k_propagate_fc_slices<V, SPW, U>), dim3((uint32_t)grid), dim3(kBlock), 0, \
+                       st, w, g, idx, min_deltas, min_idx, ap, x_grad, s.batch, s.n_inputs,       \
+                       s.n_outputs, s.n_detectors, s.n_anchors, s.n_entries, n_slices)
+        if (spw == 4) {
+            switch (vec) {
+                case 4: SPIKY_PROP(4, 4, 4); break;
+                case 2: SPIKY_PROP(2, 4, 4); break;
+                default: SPIKY_PROP(1, 4, 4); break;
+            }
+        } else {
+            switch (vec) {
+                case 4: SPIKY_PROP(4, 1, 8); break;
+                case 2: SPIKY_PROP(2, 1, 8); break;
+                default: SPIKY_PROP(1, 1, 8); break;
+            }
         }
-#undef SPIKY_PROP_FAST
+#undef SPIKY_PROP
         return hipGetLastError();
     }
     const uint32_t n_ob = (s.n_outputs + s.ogs - 1) / s.ogs;
@@ -691,41 +788,29 @@ hipError_t launch_wgrad_fc(const FcShape &s, const float *g, const int32_t *idx,
         int32_t *samples = offsets + (size_t)s.n_detectors * (s.n_entries + 1);
         hipError_t e = launch_bucket_samples(s, idx, offsets, samples, st);
         if (e != hipSuccess) return e;
-        const uint64_t n_rows = (uint64_t)s.n_detectors * s.n_entries;
-        const uint64_t want = (n_rows + 3) / 4;
-        const uint32_t grid = (uint32_t)std::min<uint64_t>(want, 65536);
-        const uint32_t vec = (s.n_outputs % 4 == 0) ? 4 : 1;
-        const uint32_t nj = (s.n_outputs + 64 * vec - 1) / (64 * vec);
-#define SPIKY_ROWSUM(NJ, V, IM, OW)                                                               \
-    hipLaunchKernelGGL((k_wgrad_rowsum<NJ, V, IM, OW>), dim3(grid), dim3(kBlock), 0, st, g,        \
-                       offsets, samples, target, s.batch, s.n_outputs, s.n_entries, n_rows, lr,  \
-                       int_rescaler)
-#define SPIKY_ROWSUM_NJ(IM, OW)                                          \
-    if (vec == 4) {                                                      \
-        switch (nj) {                                                    \
-            case 1: SPIKY_ROWSUM(1, 4, IM, OW); break;                   \
-            case 2: SPIKY_ROWSUM(2, 4, IM, OW); break;                   \
-            case 3: SPIKY_ROWSUM(3, 4, IM, OW); break;                   \
-            case 4: SPIKY_ROWSUM(4, 4, IM, OW); break;                   \
-            case 5: case 6: case 7: case 8: SPIKY_ROWSUM(8, 4, IM, OW); break; \
-            default: SPIKY_ROWSUM(16, 4, IM, OW); break;                 \
-        }                                                                \
-    } else {                                                             \
-        switch (nj) {                                                    \
-            case 1: SPIKY_ROWSUM(1, 1, IM, OW); break;                   \
-            case 2: SPIKY_ROWSUM(2, 1, IM, OW); break;                   \
-            case 3: case 4: SPIKY_ROWSUM(4, 1, IM, OW); break;           \
-            case 5: case 6: case 7: case 8: SPIKY_ROWSUM(8, 1, IM, OW); break; \
-            default: SPIKY_ROWSUM(16, 1, IM, OW); break;                 \
-        }                                                                \
+        const uint32_t vec = pick_vec(s.n_outputs);
+        const uint32_t n_slices = (s.n_outputs + kWave * vec - 1) / (kWave * vec);
+        const uint32_t rpw = std::min<uint32_t>(s.n_entries, 16);
+        const uint64_t units = (uint64_t)s.n_detectors * (s.n_entries / rpw);
+        const uint64_t grid = (uint64_t)n_slices * ((units + kWPB - 1) / kWPB);
+        if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
+#define SPIKY_WG(V, IM, OW)                                                                       \
+    hipLaunchKernelGGL((k_wgrad_slices<V, 8, IM, OW>), dim3((uint32_t)grid), dim3(kBlock), 0, st, \
+                       g, offsets, samples, target, s.batch, s.n_outputs, s.n_entries,            \
+                       s.n_detectors, n_slices, rpw, lr, int_rescaler)
+#define SPIKY_WG_V(IM, OW)                     \
+    switch (vec) {                             \
+        case 4: SPIKY_WG(4, IM, OW); break;    \
+        case 2: SPIKY_WG(2, IM, OW); break;    \
+        default: SPIKY_WG(1, IM, OW); break;   \
     }
         if (int_mode) {
-            if (overwrite) { SPIKY_ROWSUM_NJ(true, true) } else { SPIKY_ROWSUM_NJ(true, false) }
+            if (overwrite) { SPIKY_WG_V(true, true) } else { SPIKY_WG_V(true, false) }
         } else {
-            if (overwrite) { SPIKY_ROWSUM_NJ(false, true) } else { SPIKY_ROWSUM_NJ(false, false) }
+            if (overwrite) { SPIKY_WG_V(false, true) } else { SPIKY_WG_V(false, false) }
         }
-#undef SPIKY_ROWSUM_NJ
-#undef SPIKY_ROWSUM
+#undef SPIKY_WG_V
+#undef SPIKY_WG
         return hipGetLastError();
     }
     // generic atomic fallback: the caller must have zeroed target when overwrite was asked for

@@ -108,6 +108,25 @@ def test_config3_shrunk(oracle, cuda_device):
     run_fc(oracle, 16, 512, 256, 8, 1024, seed=1)
 
 
+def test_large_batch_ragged_slices(oracle, cuda_device):
+    # 4 samples per wavefront with a ragged last wavefront; 16 column slices, the
+    # last one partly inactive (1000 = 15*64 + 40)
+    run_fc(oracle, 515, 256, 40, 5, 1000, seed=11)
+
+
+def test_large_batch_two_columns_per_lane(oracle, cuda_device):
+    # 2 columns per lane; block sizes that do not divide the table count or the unroll
+    run_fc(oracle, 600, 128, 24, 4, 1024, fgs=16, bgs=7, seed=12)
+
+
+def test_large_batch_four_columns_per_lane(oracle, cuda_device):
+    run_fc(oracle, 520, 96, 16, 3, 2048, seed=13)
+
+
+def test_large_batch_int32_summation(oracle, cuda_device):
+    run_fc(oracle, 530, 64, 20, 4, 512, seed=14, int_rescaler=0.5)
+
+
 def test_unusual_group_sizes(oracle, cuda_device):
     # the reference's own tests use odd block sizes (test_lut_transformer_small.py:287-291)
     run_fc(oracle, 7, 50, 70, 5, 37, fgs=4, bgs=24, seed=2)
@@ -171,9 +190,10 @@ def test_internal_policy_sgd(oracle, cuda_device):
     assert np.array_equal(Wd.cpu().numpy(), rW)
 
 
-def test_int8_tables(oracle, cuda_device):
+@pytest.mark.parametrize("B,O", [(12, 128), (517, 1024)])
+def test_int8_tables(oracle, cuda_device, B, O):
     dev = cuda_device
-    B, I, T, Nc, O = 12, 256, 96, 6, 128
+    I, T, Nc = 256, 96, 6
     E = 1 << Nc
     g = torch.Generator().manual_seed(10)
     x = torch.randn(B * I, generator=g)
