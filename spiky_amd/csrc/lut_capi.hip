@@ -133,7 +133,9 @@ struct spiky_lut_manager {
     DeviceBuffer d_syn_offsets, d_syn_targets, d_in_offsets, d_in_pairs;
     bool dirty = true;
 
-    DeviceBuffer scratch;
+    // forward and backward keep separate scratch so that calls issued on
+    // different streams never share a buffer
+    DeviceBuffer scratch_fwd, scratch;
     std::map<std::string, OpStat> stats;
 
     // optional per-launch GPU timing with HIP events on the launch stream
@@ -286,6 +288,7 @@ void spiky_lut_destroy(spiky_lut_manager *m) {
     if (!m) return;
     m->release_events();
     m->scratch.release();
+    m->scratch_fwd.release();
     m->d_syn_offsets.release();
     m->d_syn_targets.release();
     m->d_in_offsets.release();
@@ -446,11 +449,20 @@ int spiky_lut_forward_step(spiky_lut_manager *m, const float *weights, uint32_t 
                       "check_detectors");
         });
         if (m->fully_connected == 1) {
-            m->timed("fill_outputs_fc", st, [&] {
-                check_hip(spiky::launch_fill_fc_f32(s, weights, lookup_indices, output, m->int_mode,
-                                                    m->int_rescaler, st),
-                          "fill_outputs_fc");
-            });
+            if (spiky::tm_fill_applies(s)) {
+                void *scr = m->scratch_fwd.ensure(spiky::tm_fill_scratch_bytes(s));
+                m->timed("fill_outputs_fc", st, [&] {
+                    check_hip(spiky::launch_fill_tm(s, weights, lookup_indices, output, m->int_mode,
+                                                    m->int_rescaler, scr, st),
+                              "fill_outputs_fc");
+                });
+            } else {
+                m->timed("fill_outputs_fc", st, [&] {
+                    check_hip(spiky::launch_fill_fc_f32(s, weights, lookup_indices, output,
+                                                        m->int_mode, m->int_rescaler, st),
+                              "fill_outputs_fc");
+                });
+            }
         } else {
             m->sync_connectivity();
             spiky::SparseShape ss{s, m->max_groups};
@@ -538,19 +550,32 @@ int spiky_lut_backward_backprop(spiky_lut_manager *m, float *weights, uint32_t b
         float *target = (ext >= 0.0f) ? weights : weight_grad;
         const bool overwrite = overwrite_weight_grad != 0 && target == weight_grad;
         if (m->fully_connected == 1) {
+            // one scratch: [propagate partials | weight-gradient buckets], used in stream order
+            const bool tm = !m->int_mode && spiky::tm_propagate_applies(s);
+            const size_t prop_bytes =
+                tm ? ((spiky::tm_propagate_scratch_bytes(s) + 255) & ~(size_t)255) : 0;
+            const size_t wg_bytes = target ? spiky::wgrad_fc_scratch_bytes(s) : 0;
+            uint8_t *scr_all = (prop_bytes + wg_bytes)
+                                   ? reinterpret_cast<uint8_t *>(m->scratch.ensure(prop_bytes + wg_bytes))
+                                   : nullptr;
             m->timed("propagate_fc", st, [&] {
-                check_hip(spiky::launch_propagate_fc(s, weights, output_grad, lookup_indices, min_deltas,
-                                                     min_delta_indices, anchors, input_grad, m->int_mode,
-                                                     m->int_rescaler, st),
-                          "propagate_through_detectors_fc");
+                if (tm)
+                    check_hip(spiky::launch_propagate_tm(s, weights, output_grad, lookup_indices,
+                                                         min_deltas, min_delta_indices, anchors,
+                                                         input_grad, scr_all, st),
+                              "propagate_through_detectors_fc");
+                else
+                    check_hip(spiky::launch_propagate_fc(s, weights, output_grad, lookup_indices,
+                                                         min_deltas, min_delta_indices, anchors,
+                                                         input_grad, m->int_mode, m->int_rescaler, st),
+                              "propagate_through_detectors_fc");
             });
             if (m->int_mode)
                 check_hip(spiky::launch_convert_i2f(input_grad, (uint64_t)batch_size * m->n_inputs,
                                                     m->int_rescaler, st),
                           "convert_integers_to_floats");
             if (target) {
-                const size_t need = spiky::wgrad_fc_scratch_bytes(s);
-                void *scr = need ? m->scratch.ensure(need) : nullptr;
+                void *scr = wg_bytes ? scr_all + prop_bytes : nullptr;
                 m->timed("gather_w_gradients_fc", st, [&] {
                     check_hip(spiky::launch_wgrad_fc(s, output_grad, lookup_indices, target, lr,
                                                      m->int_mode, m->int_rescaler, overwrite, scr, st),

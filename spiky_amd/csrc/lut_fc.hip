@@ -34,6 +34,7 @@
 #include "lut_kernels.h"
 
 #include <algorithm>
+#include <cmath>
 
 namespace spiky {
 namespace {
@@ -551,22 +552,28 @@ __global__ __launch_bounds__(kWave) void k_bucket_samples(
     }
 }
 
-// Table-major weight gradient over column slices.  Wavefront = `rpw`
+// Table-major weight gradient over column slices.  Wavefront = `rpw` (<= 63)
 // consecutive rows of one table x one column slice (slice -> XCD, so each XCD
 // only ever reads its own column slice of g, which stays in its L2).  The
 // rows' buckets are contiguous in the table's sorted sample list, so the
 // wavefront walks that list in flat batches of KB samples (KB gradient rows in
-// flight) and closes a row whenever the walk crosses its bucket end.  Within a
+// flight, double-buffered) and closes a row whenever the walk crosses its
+// bucket end.  Within a
 // row the samples are added in ascending order into an fp32 (or int32) sum
 // starting from the target value (or zero when overwriting): the reference
 // CPU path's order, so the result is bit-identical to it, and each target
 // element is written exactly once with no atomics.
-template <int VEC, int KB, bool INT_MODE, bool OVERWRITE>
+//
+// LR1: the learning rate is exactly 1, so the reference's committed value
+// (float)((double)g * lr) is g itself and its test |(double)g| > EPS is
+// |g| >= eps_f, the smallest float above EPS: the sum stays in fp32 and is
+// bit-identical to the general form.
+template <int VEC, int KB, bool INT_MODE, bool OVERWRITE, bool LR1>
 __global__ __launch_bounds__(kBlock) void k_wgrad_slices(
     const float *__restrict__ g, const int32_t *__restrict__ offsets,
     const int32_t *__restrict__ samples, float *__restrict__ target, uint32_t batch,
     uint32_t n_outputs, uint32_t n_entries, uint32_t n_detectors, uint32_t n_slices, uint32_t rpw,
-    double lr, double int_rescaler) {
+    double lr, double int_rescaler, float eps_f) {
     const uint32_t lane = threadIdx.x & (kWave - 1);
     const uint32_t wave = uniform(threadIdx.x / kWave);
     const uint32_t slice = blockIdx.x % n_slices;
@@ -617,31 +624,54 @@ __global__ __launch_bounds__(kBlock) void k_wgrad_slices(
     uint32_t e = 0;
     int32_t row_end = __builtin_amdgcn_readlane(offv, 1);
     init(0);
-    for (int32_t k0 = kbeg; k0 < kend; k0 += KB) {
-        float gv[KB][VEC];
+    // samples are walked in chunks of up to 64 ids (one vector load), and each
+    // chunk in batches of KB gradient rows, the next batch loading while the
+    // current one is added
+    for (int32_t k = kbeg; k < kend; k += kWave) {
+        const int32_t n = min((int32_t)kWave, kend - k);
+        const int32_t idv = smp[k + min((int32_t)lane, n - 1)];
+        float cur[KB][VEC], nxt[KB][VEC];
 #pragma unroll
         for (int j = 0; j < KB; j++) {
-            const int32_t kk = min(k0 + j, kend - 1);
-            const uint32_t b = (uint32_t)smp[kk];
-            RowLoad<float, VEC>::load(g + (size_t)b * n_outputs + cc, gv[j]);
+            const uint32_t b = (uint32_t)__builtin_amdgcn_readlane(idv, min(j, n - 1));
+            RowLoad<float, VEC>::load(g + (size_t)b * n_outputs + cc, nxt[j]);
         }
+        for (int32_t j0 = 0; j0 < n; j0 += KB) {
 #pragma unroll
-        for (int j = 0; j < KB; j++) {
-            if (k0 + j >= kend) break;
-            while (k0 + j >= row_end) {
-                store(e);
-                e++;
-                row_end = __builtin_amdgcn_readlane(offv, e + 1);
-                init(e);
+            for (int j = 0; j < KB; j++)
+#pragma unroll
+                for (int q = 0; q < VEC; q++) cur[j][q] = nxt[j][q];
+            if (j0 + KB < n) {
+#pragma unroll
+                for (int j = 0; j < KB; j++) {
+                    const uint32_t b =
+                        (uint32_t)__builtin_amdgcn_readlane(idv, min(j0 + KB + j, n - 1));
+                    RowLoad<float, VEC>::load(g + (size_t)b * n_outputs + cc, nxt[j]);
+                }
             }
 #pragma unroll
-            for (int q = 0; q < VEC; q++) {
-                const double gg = (double)gv[j][q];
-                if (fabs(gg) > kEps) {
-                    if (INT_MODE)
-                        iacc[q] = wrap_add(iacc[q], (int32_t)(gg * lr * kDenom32 * int_rescaler));
-                    else
-                        acc[q] += (float)(gg * lr);
+            for (int j = 0; j < KB; j++) {
+                if (j0 + j >= n) break;
+                const int32_t kk = k + j0 + j;
+                while (kk >= row_end) {
+                    store(e);
+                    e++;
+                    row_end = __builtin_amdgcn_readlane(offv, e + 1);
+                    init(e);
+                }
+#pragma unroll
+                for (int q = 0; q < VEC; q++) {
+                    if (LR1 && !INT_MODE) {
+                        if (fabsf(cur[j][q]) >= eps_f) acc[q] += cur[j][q];
+                    } else {
+                        const double gg = (double)cur[j][q];
+                        if (fabs(gg) > kEps) {
+                            if (INT_MODE)
+                                iacc[q] = wrap_add(iacc[q], (int32_t)(gg * lr * kDenom32 * int_rescaler));
+                            else
+                                acc[q] += (float)(gg * lr);
+                        }
+                    }
                 }
             }
         }
@@ -668,6 +698,14 @@ __global__ __launch_bounds__(kBlock) void k_convert_i2f(float *__restrict__ buf,
 }
 
 uint32_t blocks_for(uint64_t n) { return (uint32_t)((n + kBlock - 1) / kBlock); }
+
+// Smallest float f with (double)f > EPS: |g| >= f is the reference's test
+// |(double)g| > EPS for a float g (misc.h:90).
+float smallest_float_above_eps() {
+    float f = (float)kEps;
+    if ((double)f <= kEps) f = std::nextafter(f, INFINITY);
+    return f;
+}
 
 // The bucketed weight gradient needs the per-table bucket counters in LDS.
 bool rowsum_applies(const FcShape &s) {
@@ -788,26 +826,31 @@ hipError_t launch_wgrad_fc(const FcShape &s, const float *g, const int32_t *idx,
         int32_t *samples = offsets + (size_t)s.n_detectors * (s.n_entries + 1);
         hipError_t e = launch_bucket_samples(s, idx, offsets, samples, st);
         if (e != hipSuccess) return e;
-        const uint32_t vec = pick_vec(s.n_outputs);
+        // 4 columns per lane once that still leaves 4 slices (two XCDs per slice)
+        const uint32_t vec = (s.n_outputs % 4 == 0 && s.n_outputs >= 1024) ? 4 : pick_vec(s.n_outputs);
         const uint32_t n_slices = (s.n_outputs + kWave * vec - 1) / (kWave * vec);
-        const uint32_t rpw = std::min<uint32_t>(s.n_entries, 16);
+        const uint32_t rpw = std::min<uint32_t>(s.n_entries, 32);
         const uint64_t units = (uint64_t)s.n_detectors * (s.n_entries / rpw);
         const uint64_t grid = (uint64_t)n_slices * ((units + kWPB - 1) / kWPB);
         if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
-#define SPIKY_WG(V, IM, OW)                                                                       \
-    hipLaunchKernelGGL((k_wgrad_slices<V, 8, IM, OW>), dim3((uint32_t)grid), dim3(kBlock), 0, st, \
-                       g, offsets, samples, target, s.batch, s.n_outputs, s.n_entries,            \
-                       s.n_detectors, n_slices, rpw, lr, int_rescaler)
-#define SPIKY_WG_V(IM, OW)                     \
-    switch (vec) {                             \
-        case 4: SPIKY_WG(4, IM, OW); break;    \
-        case 2: SPIKY_WG(2, IM, OW); break;    \
-        default: SPIKY_WG(1, IM, OW); break;   \
+        const bool lr1 = !int_mode && lr == 1.0;
+        const float eps_f = smallest_float_above_eps();
+#define SPIKY_WG(V, IM, OW, L1)                                                                   \
+    hipLaunchKernelGGL((k_wgrad_slices<V, 8, IM, OW, L1>), dim3((uint32_t)grid), dim3(kBlock), 0, \
+                       st, g, offsets, samples, target, s.batch, s.n_outputs, s.n_entries,        \
+                       s.n_detectors, n_slices, rpw, lr, int_rescaler, eps_f)
+#define SPIKY_WG_V(IM, OW, L1)                     \
+    switch (vec) {                                 \
+        case 4: SPIKY_WG(4, IM, OW, L1); break;    \
+        case 2: SPIKY_WG(2, IM, OW, L1); break;    \
+        default: SPIKY_WG(1, IM, OW, L1); break;   \
     }
         if (int_mode) {
-            if (overwrite) { SPIKY_WG_V(true, true) } else { SPIKY_WG_V(true, false) }
+            if (overwrite) { SPIKY_WG_V(true, true, false) } else { SPIKY_WG_V(true, false, false) }
+        } else if (lr1) {
+            if (overwrite) { SPIKY_WG_V(false, true, true) } else { SPIKY_WG_V(false, false, true) }
         } else {
-            if (overwrite) { SPIKY_WG_V(false, true) } else { SPIKY_WG_V(false, false) }
+            if (overwrite) { SPIKY_WG_V(false, true, false) } else { SPIKY_WG_V(false, false, false) }
         }
 #undef SPIKY_WG_V
 #undef SPIKY_WG

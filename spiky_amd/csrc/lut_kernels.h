@@ -62,6 +62,22 @@ hipError_t launch_convert_i2f(float *buf, uint64_t n, double int_rescaler, hipSt
 hipError_t launch_bucket_samples(const FcShape &s, const int32_t *idx, int32_t *offsets,
                                  int32_t *samples, hipStream_t st);
 
+// ---- table-major fully connected path (lut_tm.hip) ------------------------
+// Forward gather-sum through per-block partials in scratch; bit-identical to
+// launch_fill_fc_f32.  Applies to fp32 tables with E <= 256 and O % 4 == 0.
+bool tm_fill_applies(const FcShape &s);
+size_t tm_fill_scratch_bytes(const FcShape &s);
+hipError_t launch_fill_tm(const FcShape &s, const float *w, const int32_t *idx, float *out,
+                          bool int_mode, double int_rescaler, void *scratch, hipStream_t st);
+
+// fp32-summation min-margin input gradient through per-slice partial dots.
+bool tm_propagate_applies(const FcShape &s);
+size_t tm_propagate_scratch_bytes(const FcShape &s);
+hipError_t launch_propagate_tm(const FcShape &s, const float *w, const float *g,
+                               const int32_t *idx, const float *min_deltas,
+                               const int32_t *min_idx, const int32_t *anchors, float *x_grad,
+                               void *scratch, hipStream_t st);
+
 // Zero n floats with a kernel (graph-capture safe, unlike hipMemsetAsync).
 hipError_t launch_zero(float *buf, uint64_t n, hipStream_t st);
 

@@ -1,0 +1,685 @@
+// lut_tm.hip -- table-major ("stage once, serve every sample") kernels for the
+// fully connected LUT layer on gfx950.
+//
+// A work unit is (block of `dgs` tables, slice of 32 output columns, chunk of
+// samples).  The unit streams its tables' 128-byte row chunks (all E rows of a
+// table, 32 KiB at E = 256) from HBM into LDS exactly once, double-buffered
+// through registers, and 1024 threads then serve every sample of the chunk
+// from LDS.  Each table byte therefore crosses HBM once per sample chunk
+// instead of once per sample that hits its row, which is what makes the
+// gather compulsory-traffic bound.
+//
+// Thread layout inside a unit: wavefront w (0..15), lane l: sample
+// w*8 + l/8 (+128*i for i < SPT), column quad l%8 (columns slice*32 + 4*(l%8)
+// .. +3).  The 8 lanes of one sample read one 128-byte LDS row, so the read is
+// free of bank conflicts.
+//
+// Forward: the unit writes, for every sample, the fp32 (or int32 fixed-point)
+// commit value of its table block -- (float)(fp64 sum over the block's tables,
+// ascending) -- into a partial buffer; k_fill_commit then adds the blocks in
+// ascending order onto the output.  That is exactly the reference CPU path's
+// arithmetic (lut_runtime_kernels_logic.proto:1214-1299 run serially,
+// misc.h:119-129), so the output stays bit-identical to it.
+//
+// Propagate: the unit writes, for every (sample, table), the fp64 dot of its
+// 32 columns, sum_c (W[main][c] - W[alt][c]) * g[c], rounded to fp32, into a
+// partial buffer [slice][table][sample]; k_propagate_reduce sums the slices in
+// a fixed order and scales by du(min margin) into du[sample][table], and
+// k_propagate_scatter accumulates the input gradient of a few samples in LDS
+// before adding it to HBM once (no global atomics).
+#include "lut_kernels.h"
+
+namespace spiky {
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kTmThreads = 1024;
+constexpr int kTmCols = 32;
+constexpr int kTmPass = (kTmThreads / kWave) * 8;  // samples per pass of SPT = 1
+constexpr int kTmMaxEntries = 256;
+constexpr int kTmPF = 2;  // tables per pipeline stage
+
+// native vector types: they stay in registers across the staging loop, where
+// HIP's struct-based float4 is demoted to scratch memory
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ double du_of_margin(float md) {
+    double du = (double)md;
+    double r = 1.0 / (1.0 + fabs(du));
+    return (du > 0) ? r * (0.5 * r) : r * (-0.5 * r);
+}
+
+__device__ __forceinline__ int32_t wrap_add(int32_t a, int32_t b) {
+    return (int32_t)((uint32_t)a + (uint32_t)b);
+}
+
+// DPP lane exchange of an fp64 value (two 32-bit moves on the VALU).
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const unsigned long long u = (unsigned long long)__double_as_longlong(v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xF, 0xF, false);
+    return __longlong_as_double((long long)(((unsigned long long)(uint32_t)hi << 32) |
+                                            (unsigned long long)(uint32_t)lo));
+}
+constexpr int kDppHalfMirror = 0x141;  // lane l of 8 <-> 7 - l
+constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]
+
+// One reduce-scatter step over a lane pairing: the pair sums its N items and
+// each lane keeps half of them (the lane with `upper` set keeps the upper
+// half); with N == 1 both lanes keep the single sum.
+template <int CTRL, int N>
+__device__ __forceinline__ void rs_step(double (&v)[8], bool upper) {
+    if (N == 1) {
+        v[0] += dpp_f64<CTRL>(v[0]);
+        return;
+    }
+    constexpr int M = N / 2;
+#pragma unroll
+    for (int j = 0; j < M; j++) {
+        const double send = upper ? v[j] : v[M + j];
+        const double keep = upper ? v[M + j] : v[j];
+        v[j] = keep + dpp_f64<CTRL>(send);
+    }
+}
+
+// Sums item j (< N) of the 8 lanes of every lane group; afterwards lane l of
+// the group holds the sum of item rs_item<N>(l) in v[0], and rs_writer<N>(l)
+// marks one lane per item.
+template <int N>
+__device__ __forceinline__ void reduce_scatter8(double (&v)[8], uint32_t l) {
+    const bool h = l >= 4, b0 = l & 1, b1 = (l >> 1) & 1;
+    rs_step<kDppHalfMirror, N>(v, h);
+    rs_step<kDppXor1, (N >= 2 ? N / 2 : 1)>(v, b0);
+    rs_step<kDppXor2, (N >= 4 ? N / 4 : 1)>(v, b1);
+}
+template <int N>
+__device__ __forceinline__ uint32_t rs_item(uint32_t l) {
+    const uint32_t h = l >= 4, b0 = l & 1, b1 = (l >> 1) & 1;
+    return (N >= 2 ? h * (N / 2) : 0) + (N >= 4 ? b0 * (N / 4) : 0) + (N >= 8 ? b1 * (N / 8) : 0);
+}
+template <int N>
+__device__ __forceinline__ bool rs_writer(uint32_t l) {
+    const uint32_t h = l >= 4, b0 = l & 1, b1 = (l >> 1) & 1;
+    return (N >= 2 || !h) && (N >= 4 || !b0) && (N >= 8 || !b1);
+}
+
+// LDS image of one table in a stage: E rows x 128 bytes, then one key per
+// sample of the chunk (u8 row index for the forward, u16 main|alt<<8 for the
+// propagate).
+template <typename KEY, int SPT>
+struct StageLayout {
+    static constexpr int kKeys = kTmPass * SPT;
+    static constexpr int kTableBytes = kTmMaxEntries * 128 + kKeys * (int)sizeof(KEY);
+    static constexpr int kStageBytes = kTmPF * kTableBytes;
+};
+
+// Each thread's share of one stage: row chunks c = tid and tid + 1024 (E <= 256
+// rows x 8 chunks of 16 bytes), and for the first kKeyPieces threads one
+// 16-byte piece of the stage's key row.
+template <typename KEY, int SPT>
+struct KeyPieces {
+    static constexpr int kPer = 16 / (int)sizeof(KEY);
+    static constexpr int kCount = StageLayout<KEY, SPT>::kKeys / kPer;
+};
+
+template <typename KEY, int SPT>
+__device__ __forceinline__ void stage_load(f32x4 (&rows)[kTmPF][2], u32x4 (&keys)[kTmPF],
+                                           const float *__restrict__ w,
+                                           const KEY *__restrict__ keys_t, uint32_t tid,
+                                           uint32_t t_first, uint32_t nt, uint32_t n_entries,
+                                           uint32_t n_outputs, uint32_t col0, uint32_t batch,
+                                           uint32_t b_base) {
+    constexpr int kPer = KeyPieces<KEY, SPT>::kPer;
+#pragma unroll
+    for (int p = 0; p < kTmPF; p++) {
+        const uint32_t t = t_first + min((uint32_t)p, nt - 1);
+        const float *wt = w + (size_t)t * n_entries * n_outputs;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t c = tid + (uint32_t)h * kTmThreads;
+            const uint32_t row = (c >> 3) & (n_entries - 1);
+            uint32_t col = col0 + (c & 7) * 4;
+            if (col >= n_outputs) col = 0;
+            rows[p][h] = *reinterpret_cast<const f32x4 *>(wt + (size_t)row * n_outputs + col);
+        }
+        if ((int)tid < KeyPieces<KEY, SPT>::kCount) {
+            // keys of samples b_base + tid*kPer .. +kPer-1 (zero past the batch)
+            const uint32_t b = b_base + tid * kPer;
+            const KEY *src = keys_t + (size_t)t * batch + b;
+            if (b + kPer <= batch && batch % kPer == 0) {
+                keys[p] = *reinterpret_cast<const u32x4 *>(src);
+            } else {
+                uint32_t wd[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+                for (int q = 0; q < kPer; q++) {
+                    const uint32_t v = (b + q < batch) ? (uint32_t)src[q] : 0u;
+                    wd[q / (4 / (int)sizeof(KEY))] |= v << (8 * sizeof(KEY) * (q % (4 / (int)sizeof(KEY))));
+                }
+                keys[p] = u32x4{wd[0], wd[1], wd[2], wd[3]};
+            }
+        }
+    }
+}
+
+template <typename KEY, int SPT>
+__device__ __forceinline__ void stage_store(const f32x4 (&rows)[kTmPF][2],
+                                            const u32x4 (&keys)[kTmPF], uint8_t *stage,
+                                            uint32_t tid) {
+#pragma unroll
+    for (int p = 0; p < kTmPF; p++) {
+        uint8_t *tb = stage + p * StageLayout<KEY, SPT>::kTableBytes;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t c = tid + (uint32_t)h * kTmThreads;
+            *reinterpret_cast<f32x4 *>(tb + c * 16) = rows[p][h];
+        }
+        if ((int)tid < KeyPieces<KEY, SPT>::kCount)
+            *reinterpret_cast<u32x4 *>(tb + kTmMaxEntries * 128 + tid * 16) = keys[p];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Forward partials.  part[k][b][o] = commit value of table block k for (b, o).
+// ---------------------------------------------------------------------------
+template <int SPT, bool INT_MODE>
+__global__ __launch_bounds__(kTmThreads) void k_fill_tm(
+    const float *__restrict__ w, const uint8_t *__restrict__ idx_t, uint32_t *__restrict__ part,
+    uint32_t batch, uint32_t n_outputs, uint32_t n_detectors, uint32_t n_entries, uint32_t dgs,
+    uint32_t n_slices, uint32_t n_chunks, double int_rescaler) {
+    using L = StageLayout<uint8_t, SPT>;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * L::kStageBytes];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & (kWave - 1);
+    const uint32_t wave = tid / kWave;
+    const uint32_t slice = blockIdx.x % n_slices;
+    const uint32_t rest = blockIdx.x / n_slices;
+    const uint32_t chunk = rest % n_chunks;
+    const uint32_t k = rest / n_chunks;
+    const uint32_t t0 = k * dgs;
+    const uint32_t t1 = min(t0 + dgs, n_detectors);
+    const uint32_t b_base = chunk * (kTmPass * SPT);
+    const uint32_t col0 = slice * kTmCols;
+    const uint32_t q = lane & 7;
+    const uint32_t col = col0 + q * 4;
+    const uint32_t emask = n_entries - 1;
+    const uint32_t s_loc0 = wave * 8 + (lane >> 3);
+
+    double acc[SPT][4];
+#pragma unroll
+    for (int i = 0; i < SPT; i++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) acc[i][c] = 0.0;
+
+    const uint32_t nt_all = t1 - t0;
+    const uint32_t n_stages = (nt_all + kTmPF - 1) / kTmPF;
+    f32x4 rows[kTmPF][2];
+    u32x4 keys4[kTmPF];
+    stage_load<uint8_t, SPT>(rows, keys4, w, idx_t, tid, t0, min((uint32_t)kTmPF, nt_all), n_entries,
+                             n_outputs, col0, batch, b_base);
+    for (uint32_t st = 0; st < n_stages; st++) {
+        uint8_t *stage = smem + (st & 1) * L::kStageBytes;
+        stage_store<uint8_t, SPT>(rows, keys4, stage, tid);
+        const uint32_t ts = t0 + st * kTmPF;
+        const uint32_t nt = min((uint32_t)kTmPF, t1 - ts);
+        if (st + 1 < n_stages) {
+            const uint32_t tn = ts + kTmPF;
+            stage_load<uint8_t, SPT>(rows, keys4, w, idx_t, tid, tn, min((uint32_t)kTmPF, t1 - tn),
+                                     n_entries, n_outputs, col0, batch, b_base);
+        }
+        __syncthreads();
+        for (uint32_t p = 0; p < nt; p++) {
+            const uint8_t *tb = stage + p * L::kTableBytes;
+            const uint8_t *keys = tb + kTmMaxEntries * 128;
+#pragma unroll
+            for (int i = 0; i < SPT; i++) {
+                const uint32_t r = (uint32_t)keys[s_loc0 + kTmPass * i] & emask;
+                const f32x4 v = *reinterpret_cast<const f32x4 *>(tb + r * 128 + q * 16);
+                acc[i][0] += (double)v.x;
+                acc[i][1] += (double)v.y;
+                acc[i][2] += (double)v.z;
+                acc[i][3] += (double)v.w;
+            }
+        }
+    }
+    if (col >= n_outputs) return;
+#pragma unroll
+    for (int i = 0; i < SPT; i++) {
+        const uint32_t b = b_base + s_loc0 + kTmPass * i;
+        if (b >= batch) continue;
+        uint4 o;
+        if (INT_MODE) {
+            o.x = (uint32_t)(int32_t)(acc[i][0] * kDenom32 * int_rescaler);
+            o.y = (uint32_t)(int32_t)(acc[i][1] * kDenom32 * int_rescaler);
+            o.z = (uint32_t)(int32_t)(acc[i][2] * kDenom32 * int_rescaler);
+            o.w = (uint32_t)(int32_t)(acc[i][3] * kDenom32 * int_rescaler);
+        } else {
+            o.x = __float_as_uint((float)acc[i][0]);
+            o.y = __float_as_uint((float)acc[i][1]);
+            o.z = __float_as_uint((float)acc[i][2]);
+            o.w = __float_as_uint((float)acc[i][3]);
+        }
+        *reinterpret_cast<uint4 *>(part + ((size_t)k * batch + b) * n_outputs + col) = o;
+    }
+}
+
+// out[b][o] (+)= sum over blocks k ascending of part[k][b][o] (fp32 or int32).
+template <bool INT_MODE>
+__global__ __launch_bounds__(256) void k_fill_commit(const uint32_t *__restrict__ part,
+                                                     float *__restrict__ out, uint64_t n_quads,
+                                                     uint32_t n_blocks, uint64_t stride,
+                                                     double int_rescaler) {
+    const uint64_t qd = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (qd >= n_quads) return;
+    float4 *op = reinterpret_cast<float4 *>(out) + qd;
+    const uint4 *pp = reinterpret_cast<const uint4 *>(part) + qd;
+    const uint64_t s4 = stride / 4;
+    float4 run = *op;
+    int32_t ir[4] = {__float_as_int(run.x), __float_as_int(run.y), __float_as_int(run.z),
+                     __float_as_int(run.w)};
+    uint32_t k = 0;
+    constexpr int kU = 8;
+    for (; k + kU <= n_blocks; k += kU) {
+        uint4 v[kU];
+#pragma unroll
+        for (int u = 0; u < kU; u++) v[u] = pp[(k + u) * s4];
+#pragma unroll
+        for (int u = 0; u < kU; u++) {
+            if (INT_MODE) {
+                ir[0] = wrap_add(ir[0], (int32_t)v[u].x);
+                ir[1] = wrap_add(ir[1], (int32_t)v[u].y);
+                ir[2] = wrap_add(ir[2], (int32_t)v[u].z);
+                ir[3] = wrap_add(ir[3], (int32_t)v[u].w);
+            } else {
+                run.x += __uint_as_float(v[u].x);
+                run.y += __uint_as_float(v[u].y);
+                run.z += __uint_as_float(v[u].z);
+                run.w += __uint_as_float(v[u].w);
+            }
+        }
+    }
+    for (; k < n_blocks; k++) {
+        const uint4 v = pp[k * s4];
+        if (INT_MODE) {
+            ir[0] = wrap_add(ir[0], (int32_t)v.x);
+            ir[1] = wrap_add(ir[1], (int32_t)v.y);
+            ir[2] = wrap_add(ir[2], (int32_t)v.z);
+            ir[3] = wrap_add(ir[3], (int32_t)v.w);
+        } else {
+            run.x += __uint_as_float(v.x);
+            run.y += __uint_as_float(v.y);
+            run.z += __uint_as_float(v.z);
+            run.w += __uint_as_float(v.w);
+        }
+    }
+    if (INT_MODE) {
+        // convert_integers_to_floats_logic, proto:200-213
+        run.x = (float)(((double)ir[0] * kDenom32Reciproc) / int_rescaler);
+        run.y = (float)(((double)ir[1] * kDenom32Reciproc) / int_rescaler);
+        run.z = (float)(((double)ir[2] * kDenom32Reciproc) / int_rescaler);
+        run.w = (float)(((double)ir[3] * kDenom32Reciproc) / int_rescaler);
+    }
+    *op = run;
+}
+
+// ---------------------------------------------------------------------------
+// Propagate partials.  dpart[s][t][b] = fp32(sum over slice s's columns of
+// (W[t][main] - W[t][alt]) * g[b]) in fp64.  Key = main | alt << 8.
+// ---------------------------------------------------------------------------
+template <int SPT>
+__global__ __launch_bounds__(kTmThreads) void k_propagate_tm(
+    const float *__restrict__ w, const float *__restrict__ g, const uint16_t *__restrict__ key_t,
+    float *__restrict__ dpart, uint32_t batch, uint32_t n_outputs, uint32_t n_detectors,
+    uint32_t n_entries, uint32_t tpu, uint32_t n_slices, uint32_t n_chunks) {
+    using L = StageLayout<uint16_t, SPT>;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * L::kStageBytes];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & (kWave - 1);
+    const uint32_t wave = tid / kWave;
+    const uint32_t slice = blockIdx.x % n_slices;
+    const uint32_t rest = blockIdx.x / n_slices;
+    const uint32_t chunk = rest % n_chunks;
+    const uint32_t k = rest / n_chunks;
+    const uint32_t t0 = k * tpu;
+    const uint32_t t1 = min(t0 + tpu, n_detectors);
+    const uint32_t b_base = chunk * (kTmPass * SPT);
+    const uint32_t col0 = slice * kTmCols;
+    const uint32_t q = lane & 7;
+    const uint32_t col = col0 + q * 4;
+    const bool active = col < n_outputs;
+    const uint32_t emask = n_entries - 1;
+    const uint32_t s_loc0 = wave * 8 + (lane >> 3);
+
+    f32x4 gv[SPT];
+#pragma unroll
+    for (int i = 0; i < SPT; i++) {
+        const uint32_t b = min(b_base + s_loc0 + kTmPass * i, batch - 1);
+        gv[i] = active ? *reinterpret_cast<const f32x4 *>(g + (size_t)b * n_outputs + col)
+                       : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    const uint32_t nt_all = t1 - t0;
+    const uint32_t n_stages = (nt_all + kTmPF - 1) / kTmPF;
+    f32x4 rows[kTmPF][2];
+    u32x4 keys4[kTmPF];
+    stage_load<uint16_t, SPT>(rows, keys4, w, key_t, tid, t0, min((uint32_t)kTmPF, nt_all), n_entries,
+                              n_outputs, col0, batch, b_base);
+    for (uint32_t st = 0; st < n_stages; st++) {
+        uint8_t *stage = smem + (st & 1) * L::kStageBytes;
+        stage_store<uint16_t, SPT>(rows, keys4, stage, tid);
+        const uint32_t ts = t0 + st * kTmPF;
+        const uint32_t nt = min((uint32_t)kTmPF, t1 - ts);
+        if (st + 1 < n_stages) {
+            const uint32_t tn = ts + kTmPF;
+            stage_load<uint16_t, SPT>(rows, keys4, w, key_t, tid, tn, min((uint32_t)kTmPF, t1 - tn),
+                                      n_entries, n_outputs, col0, batch, b_base);
+        }
+        __syncthreads();
+        for (uint32_t p = 0; p < nt; p++) {
+            const uint8_t *tb = stage + p * L::kTableBytes;
+            const uint16_t *keys = reinterpret_cast<const uint16_t *>(tb + kTmMaxEntries * 128);
+            const uint32_t t = ts + p;
+            double dv[8];
+#pragma unroll
+            for (int i = 0; i < SPT; i++) {
+                // keep at most 4 samples' row reads in flight (128-VGPR budget)
+                if (i == 4) __builtin_amdgcn_sched_barrier(0);
+                const uint32_t key = keys[s_loc0 + kTmPass * i];
+                const uint32_t rm = key & emask;
+                const uint32_t ra = (key >> 8) & emask;
+                const f32x4 a = *reinterpret_cast<const f32x4 *>(tb + rm * 128 + q * 16);
+                const f32x4 e = *reinterpret_cast<const f32x4 *>(tb + ra * 128 + q * 16);
+                double d = ((double)a.x - (double)e.x) * (double)gv[i].x;
+                d += ((double)a.y - (double)e.y) * (double)gv[i].y;
+                d += ((double)a.z - (double)e.z) * (double)gv[i].z;
+                d += ((double)a.w - (double)e.w) * (double)gv[i].w;
+                dv[i] = d;
+            }
+            // the 8 lanes of a sample group each hold a 4-column piece of the
+            // SPT dots; after the reduce-scatter lane q holds sample rs_item's sum
+            reduce_scatter8<SPT>(dv, q);
+            const uint32_t b = b_base + s_loc0 + kTmPass * rs_item<SPT>(q);
+            if (rs_writer<SPT>(q) && b < batch)
+                dpart[((size_t)slice * n_detectors + t) * batch + b] = (float)dv[0];
+        }
+    }
+}
+
+// du[b][t] = sum over slices s ascending of du(min margin of (b, t)) *
+// dpart[s][t][b] (fp64), or 0 when the min-margin index is unused.  One
+// workgroup per 64 tables x 64 samples tile; md / mi and du pass through LDS so
+// that every global access is coalesced.
+__global__ __launch_bounds__(256) void k_propagate_reduce(const float *__restrict__ dpart,
+                                                          const float *__restrict__ md,
+                                                          const int32_t *__restrict__ mi,
+                                                          float *__restrict__ du_out,
+                                                          uint32_t batch, uint32_t n_detectors,
+                                                          uint32_t n_anchors, uint32_t n_slices,
+                                                          bool per_slice_eps) {
+    __shared__ float s_md[64][65];
+    __shared__ int32_t s_mi[64][65];
+    __shared__ float s_du[64][65];
+    const uint32_t tb = blockIdx.x * 64;
+    const uint32_t bb = blockIdx.y * 64;
+    const uint32_t tx = threadIdx.x & 63;
+    const uint32_t ty = threadIdx.x >> 6;
+    for (uint32_t r = ty; r < 64; r += 4) {
+        const uint32_t b = bb + r, t = tb + tx;
+        if (b < batch && t < n_detectors) {
+            s_md[r][tx] = md[(size_t)b * n_detectors + t];
+            s_mi[r][tx] = mi[(size_t)b * n_detectors + t];
+        }
+    }
+    __syncthreads();
+    // thread (tx = sample, r = table): coalesced over samples
+    for (uint32_t r = ty; r < 64; r += 4) {
+        const uint32_t t = tb + r, b = bb + tx;
+        float du = 0.0f;
+        if (b < batch && t < n_detectors) {
+            const int32_t m = s_mi[tx][r];
+            if (m >= 0 && (uint32_t)m < n_anchors) {
+                // slice terms du(margin) * dot; with per_slice_eps (slices are the
+                // reference's 32-output blocks) each term is dropped unless
+                // |term| > EPS, as the reference's per-block commit does
+                // (proto:833-863, misc.h:90)
+                const double dm = du_of_margin(s_md[tx][r]);
+                double acc = 0.0;
+                const float *p = dpart + (size_t)t * batch + b;
+                const size_t stride = (size_t)n_detectors * batch;
+                uint32_t s = 0;
+                for (; s + 8 <= n_slices; s += 8) {
+                    float v[8];
+#pragma unroll
+                    for (int u = 0; u < 8; u++) v[u] = p[(s + u) * stride];
+#pragma unroll
+                    for (int u = 0; u < 8; u++) {
+                        const double term = dm * (double)v[u];
+                        if (!per_slice_eps || fabs(term) > kEps) acc += term;
+                    }
+                }
+                for (; s < n_slices; s++) {
+                    const double term = dm * (double)p[s * stride];
+                    if (!per_slice_eps || fabs(term) > kEps) acc += term;
+                }
+                if (fabs(acc) > kEps) du = (float)acc;
+            }
+        }
+        s_du[tx][r] = du;
+    }
+    __syncthreads();
+    for (uint32_t r = ty; r < 64; r += 4) {
+        const uint32_t b = bb + r, t = tb + tx;
+        if (b < batch && t < n_detectors) du_out[(size_t)b * n_detectors + t] = s_du[r][tx];
+    }
+}
+
+// x_grad[b][a1] += du, x_grad[b][a2] -= du for every table with |du| > EPS
+// (propagate_through_detector, proto:821-867).  One workgroup per group of
+// samples; their input-gradient rows are accumulated in LDS and added to HBM
+// once.
+constexpr int kScatterThreads = 1024;
+constexpr int kScatterLds = 64 * 1024;
+
+__global__ __launch_bounds__(kScatterThreads) void k_propagate_scatter(
+    const float *__restrict__ du_in, const int32_t *__restrict__ mi,
+    const int2 *__restrict__ anchors, float *__restrict__ x_grad, uint32_t batch,
+    uint32_t n_inputs, uint32_t n_detectors, uint32_t n_anchors, uint32_t samples_per_group) {
+    __shared__ float xg[kScatterLds / 4];
+    const uint32_t b0 = blockIdx.x * samples_per_group;
+    const uint32_t nb = min(samples_per_group, batch - b0);
+    const uint32_t n_el = nb * n_inputs;
+    for (uint32_t i = threadIdx.x; i < n_el; i += kScatterThreads) xg[i] = 0.0f;
+    __syncthreads();
+    const uint64_t n_pairs = (uint64_t)nb * n_detectors;
+    const size_t base = (size_t)b0 * n_detectors;
+    for (uint64_t p = threadIdx.x; p < n_pairs; p += kScatterThreads) {
+        const float du = du_in[base + p];
+        if (du == 0.0f) continue;
+        const int32_t m = mi[base + p];
+        const uint32_t t = (uint32_t)(p % n_detectors);
+        const uint32_t bl = (uint32_t)(p / n_detectors);
+        if (m < 0 || (uint32_t)m >= n_anchors) continue;
+        const int2 a = anchors[(size_t)t * n_anchors + m];
+        if ((uint32_t)a.x >= n_inputs || (uint32_t)a.y >= n_inputs) continue;
+        atomicAdd(&xg[bl * n_inputs + a.x], du);
+        atomicAdd(&xg[bl * n_inputs + a.y], -du);
+    }
+    __syncthreads();
+    float *dst = x_grad + (size_t)b0 * n_inputs;
+    for (uint32_t i = threadIdx.x; i < n_el; i += kScatterThreads) dst[i] += xg[i];
+}
+
+// keys_t[t][b] = idx[b][t] (u8), through a 64x64 LDS tile.
+__global__ __launch_bounds__(256) void k_transpose_idx(const int32_t *__restrict__ idx,
+                                                       uint8_t *__restrict__ idx_t,
+                                                       uint32_t batch, uint32_t n_detectors) {
+    __shared__ uint8_t tile[64][65];
+    const uint32_t tb = blockIdx.x * 64;  // table tile
+    const uint32_t bb = blockIdx.y * 64;  // sample tile
+    const uint32_t tx = threadIdx.x & 63;
+    const uint32_t ty = threadIdx.x >> 6;
+    for (uint32_t r = ty; r < 64; r += 4) {
+        const uint32_t b = bb + r, t = tb + tx;
+        if (b < batch && t < n_detectors) tile[r][tx] = (uint8_t)idx[(size_t)b * n_detectors + t];
+    }
+    __syncthreads();
+    for (uint32_t r = ty; r < 64; r += 4) {
+        const uint32_t t = tb + r, b = bb + tx;
+        if (b < batch && t < n_detectors) idx_t[(size_t)t * batch + b] = tile[tx][r];
+    }
+}
+
+// keys_t[t][b] = main | alt << 8 with alt = main ^ (1 << min_idx) (main when
+// the min-margin index is unused), through a 64x64 LDS tile.
+__global__ __launch_bounds__(256) void k_transpose_keys(const int32_t *__restrict__ idx,
+                                                        const int32_t *__restrict__ mi,
+                                                        uint16_t *__restrict__ key_t,
+                                                        uint32_t batch, uint32_t n_detectors,
+                                                        uint32_t n_anchors, uint32_t n_entries) {
+    __shared__ uint16_t tile[64][65];
+    const uint32_t tb = blockIdx.x * 64;
+    const uint32_t bb = blockIdx.y * 64;
+    const uint32_t tx = threadIdx.x & 63;
+    const uint32_t ty = threadIdx.x >> 6;
+    for (uint32_t r = ty; r < 64; r += 4) {
+        const uint32_t b = bb + r, t = tb + tx;
+        if (b < batch && t < n_detectors) {
+            const size_t bt = (size_t)b * n_detectors + t;
+            const uint32_t rm = (uint32_t)idx[bt] & (n_entries - 1);
+            const int32_t m = mi[bt];
+            const uint32_t ra = (m >= 0 && (uint32_t)m < n_anchors) ? (rm ^ (1u << m)) : rm;
+            tile[r][tx] = (uint16_t)(rm | (ra << 8));
+        }
+    }
+    __syncthreads();
+    for (uint32_t r = ty; r < 64; r += 4) {
+        const uint32_t t = tb + r, b = bb + tx;
+        if (b < batch && t < n_detectors) key_t[(size_t)t * batch + b] = tile[tx][r];
+    }
+}
+
+uint32_t tm_spt(uint32_t batch) {
+    if (batch <= (uint32_t)kTmPass) return 1;
+    if (batch <= 2u * kTmPass) return 2;
+    if (batch <= 4u * kTmPass) return 4;
+    return 8;
+}
+
+}  // namespace
+
+bool tm_fill_applies(const FcShape &s) {
+    const uint64_t n_blocks = (s.n_detectors + s.dgs - 1) / s.dgs;
+    return s.batch >= 256 && s.n_entries <= (uint32_t)kTmMaxEntries && s.n_outputs % 4 == 0 &&
+           s.n_outputs >= 64 && s.dgs >= 8 &&
+           n_blocks * s.batch * s.n_outputs * 4 <= (4ull << 30);
+}
+
+size_t tm_fill_scratch_bytes(const FcShape &s) {
+    const uint64_t n_blocks = (s.n_detectors + s.dgs - 1) / s.dgs;
+    const size_t keys = ((size_t)s.n_detectors * s.batch + 255) & ~(size_t)255;
+    return keys + (size_t)n_blocks * s.batch * s.n_outputs * 4;
+}
+
+hipError_t launch_fill_tm(const FcShape &s, const float *w, const int32_t *idx, float *out,
+                          bool int_mode, double int_rescaler, void *scratch, hipStream_t st) {
+    uint8_t *idx_t = reinterpret_cast<uint8_t *>(scratch);
+    const size_t keys = ((size_t)s.n_detectors * s.batch + 255) & ~(size_t)255;
+    uint32_t *part = reinterpret_cast<uint32_t *>(reinterpret_cast<uint8_t *>(scratch) + keys);
+    hipLaunchKernelGGL(k_transpose_idx, dim3((s.n_detectors + 63) / 64, (s.batch + 63) / 64),
+                       dim3(256), 0, st, idx, idx_t, s.batch, s.n_detectors);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const uint32_t spt = tm_spt(s.batch);
+    const uint32_t n_chunks = (s.batch + kTmPass * spt - 1) / (kTmPass * spt);
+    const uint32_t n_slices = (s.n_outputs + kTmCols - 1) / kTmCols;
+    const uint32_t n_blocks = (s.n_detectors + s.dgs - 1) / s.dgs;
+    const uint64_t grid = (uint64_t)n_blocks * n_chunks * n_slices;
+    if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
+#define SPIKY_TM(SPT, IM)                                                                        \
+    hipLaunchKernelGGL((k_fill_tm<SPT, IM>), dim3((uint32_t)grid), dim3(kTmThreads), 0, st, w,  \
+                       idx_t, part, s.batch, s.n_outputs, s.n_detectors, s.n_entries, s.dgs,   \
+                       n_slices, n_chunks, int_rescaler)
+    switch (spt) {
+        case 1: if (int_mode) SPIKY_TM(1, true); else SPIKY_TM(1, false); break;
+        case 2: if (int_mode) SPIKY_TM(2, true); else SPIKY_TM(2, false); break;
+        case 4: if (int_mode) SPIKY_TM(4, true); else SPIKY_TM(4, false); break;
+        default: if (int_mode) SPIKY_TM(8, true); else SPIKY_TM(8, false); break;
+    }
+#undef SPIKY_TM
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const uint64_t n_quads = (uint64_t)s.batch * s.n_outputs / 4;
+    const uint64_t stride = (uint64_t)s.batch * s.n_outputs;
+    const uint32_t cgrid = (uint32_t)((n_quads + 255) / 256);
+    if (int_mode)
+        hipLaunchKernelGGL(k_fill_commit<true>, dim3(cgrid), dim3(256), 0, st, part, out, n_quads,
+                           n_blocks, stride, int_rescaler);
+    else
+        hipLaunchKernelGGL(k_fill_commit<false>, dim3(cgrid), dim3(256), 0, st, part, out,
+                           n_quads, n_blocks, stride, int_rescaler);
+    return hipGetLastError();
+}
+
+bool tm_propagate_applies(const FcShape &s) {
+    const uint64_t n_slices = (s.n_outputs + kTmCols - 1) / kTmCols;
+    return s.batch >= 256 && s.n_entries <= (uint32_t)kTmMaxEntries && s.n_outputs % 4 == 0 &&
+           s.n_outputs >= 64 && s.n_inputs * 4 <= (uint32_t)kScatterLds &&
+           n_slices * s.batch * s.n_detectors * 4 <= (4ull << 30);
+}
+
+// scratch: keys [T][B] u16 | partial dots [slices][T][B] f32 | du [B][T] f32
+size_t tm_propagate_scratch_bytes(const FcShape &s) {
+    const uint64_t n_slices = (s.n_outputs + kTmCols - 1) / kTmCols;
+    const size_t keys = ((size_t)s.n_detectors * s.batch * 2 + 255) & ~(size_t)255;
+    return keys + (size_t)(n_slices + 1) * s.batch * s.n_detectors * 4;
+}
+
+hipError_t launch_propagate_tm(const FcShape &s, const float *w, const float *g,
+                               const int32_t *idx, const float *min_deltas,
+                               const int32_t *min_idx, const int32_t *anchors, float *x_grad,
+                               void *scratch, hipStream_t st) {
+    uint16_t *key_t = reinterpret_cast<uint16_t *>(scratch);
+    const size_t keys = ((size_t)s.n_detectors * s.batch * 2 + 255) & ~(size_t)255;
+    float *dpart = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(scratch) + keys);
+    hipLaunchKernelGGL(k_transpose_keys, dim3((s.n_detectors + 63) / 64, (s.batch + 63) / 64),
+                       dim3(256), 0, st, idx, min_idx, key_t, s.batch, s.n_detectors,
+                       s.n_anchors, s.n_entries);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const uint32_t spt = tm_spt(s.batch);
+    const uint32_t n_chunks = (s.batch + kTmPass * spt - 1) / (kTmPass * spt);
+    const uint32_t n_slices = (s.n_outputs + kTmCols - 1) / kTmCols;
+    const uint32_t tpu = 32;
+    const uint32_t n_units = (s.n_detectors + tpu - 1) / tpu;
+    const uint64_t grid = (uint64_t)n_units * n_chunks * n_slices;
+    if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
+#define SPIKY_PTM(SPT)                                                                            \
+    hipLaunchKernelGGL((k_propagate_tm<SPT>), dim3((uint32_t)grid), dim3(kTmThreads), 0, st, w, g, \
+                       key_t, dpart, s.batch, s.n_outputs, s.n_detectors, s.n_entries, tpu,       \
+                       n_slices, n_chunks)
+    switch (spt) {
+        case 1: SPIKY_PTM(1); break;
+        case 2: SPIKY_PTM(2); break;
+        case 4: SPIKY_PTM(4); break;
+        default: SPIKY_PTM(8); break;
+    }
+#undef SPIKY_PTM
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    float *du = dpart + (size_t)n_slices * s.batch * s.n_detectors;
+    hipLaunchKernelGGL(k_propagate_reduce, dim3((s.n_detectors + 63) / 64, (s.batch + 63) / 64),
+                       dim3(256), 0, st, dpart, min_deltas, min_idx, du, s.batch, s.n_detectors,
+                       s.n_anchors, n_slices, s.ogs == (uint32_t)kTmCols);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const uint32_t spg = std::max<uint32_t>(1, std::min<uint32_t>(16, kScatterLds / 4 / s.n_inputs));
+    const uint32_t groups = (s.batch + spg - 1) / spg;
+    hipLaunchKernelGGL(k_propagate_scatter, dim3(groups), dim3(kScatterThreads), 0, st, du,
+                       min_idx, reinterpret_cast<const int2 *>(anchors), x_grad, s.batch,
+                       s.n_inputs, s.n_detectors, s.n_anchors, spg);
+    return hipGetLastError();
+}
+
+}  // namespace spiky

@@ -41,19 +41,27 @@ def make_inputs(seed, B, I, T, Nc, O, x_normal=False):
     return x, anchors, W, go
 
 
-def xg_close(gpu, cpu, B, I):
+def xg_close(gpu, cpu, B, I, T=8192, n_ob=32):
+    """|gpu - cpu| <= 1e-5 * max|x_grad[b, :]| + T * n_ob * 1e-17.  The absolute
+    term bounds the terms the reference drops as |du| <= EPS = 1e-17 per
+    (table, 32-output block) (misc.h:90, proto:833-863) where a kernel that
+    commits wider sums applies the same cut to the sum instead."""
     gpu = gpu.reshape(B, I)
     cpu = cpu.reshape(B, I)
-    scale = np.abs(cpu).max(axis=1, keepdims=True) + 1e-30
+    scale = np.abs(cpu).max(axis=1, keepdims=True)
     err = np.abs(gpu - cpu)
-    assert np.all(err <= XG_RTOL * scale), f"max rel err {np.max(err / scale)}"
+    bound = XG_RTOL * scale + T * n_ob * 1e-17
+    assert np.all(err <= bound), f"max excess {np.max(err - bound)}"
 
 
-def run_fc(oracle, B, I, T, Nc, O, fgs=32, bgs=32, cmp_eps=0.0, seed=0, int_rescaler=None, lr=1.0):
+def run_fc(oracle, B, I, T, Nc, O, fgs=32, bgs=32, cmp_eps=0.0, seed=0, int_rescaler=None, lr=1.0,
+           edit_grad=None):
     dev = torch.device("cuda:0")
     E = 1 << Nc
     int_mode = int_rescaler is not None
     x, anchors, W, go = make_inputs(seed, B, I, T, Nc, O)
+    if edit_grad is not None:
+        go = edit_grad(go)
     dm = make_dm(I, O, T, Nc, fgs, bgs, int_rescaler, lr)
     xd, ad, Wd, gd = x.to(dev), anchors.to(dev), W.to(dev), go.to(dev)
     out = torch.zeros(B * O, device=dev)
@@ -90,12 +98,13 @@ def run_fc(oracle, B, I, T, Nc, O, fgs=32, bgs=32, cmp_eps=0.0, seed=0, int_resc
     assert np.array_equal(md.cpu().numpy(), rmd)
     assert np.array_equal(mi.cpu().numpy(), rmi)
     assert np.array_equal(out.cpu().numpy(), rout)
+    n_ob = (O + fgs - 1) // fgs
     if int_mode:
         assert np.array_equal(xg.cpu().numpy(), rxg)
         assert np.array_equal(xg2.cpu().numpy(), rxg)
     else:
-        xg_close(xg.cpu().numpy(), rxg, B, I)
-        xg_close(xg2.cpu().numpy(), rxg, B, I)
+        xg_close(xg.cpu().numpy(), rxg, B, I, T, n_ob)
+        xg_close(xg2.cpu().numpy(), rxg, B, I, T, n_ob)
     assert np.array_equal(wg.cpu().numpy(), rwg)
     assert np.array_equal(wg_acc.cpu().numpy(), rwg)
 
@@ -123,8 +132,30 @@ def test_large_batch_four_columns_per_lane(oracle, cuda_device):
     run_fc(oracle, 520, 96, 16, 3, 2048, seed=13)
 
 
+def test_table_major_two_sample_chunks(oracle, cuda_device):
+    # 256-entry tables staged in LDS, a second sample chunk of 6 samples, and a
+    # last column slice of 4 columns (100 = 3*32 + 4)
+    run_fc(oracle, 1030, 300, 40, 8, 100, seed=15)
+
+
 def test_large_batch_int32_summation(oracle, cuda_device):
     run_fc(oracle, 530, 64, 20, 4, 512, seed=14, int_rescaler=0.5)
+
+
+def test_weight_gradient_eps_edge(oracle, cuda_device):
+    # gradient values on both sides of the reference's |g| > 1e-17 cut (misc.h:90),
+    # through the lr == 1 fp32 path (O = 1024: four columns per lane)
+    eps = np.float32(1e-17)
+    edge = np.array([eps, -eps, np.nextafter(eps, np.float32(1)), np.nextafter(eps, np.float32(0)),
+                     -np.nextafter(eps, np.float32(1)), 0.0, -0.0, 1e-30, 1e-16], np.float32)
+
+    def edit(go):
+        g = go.numpy().copy()
+        g[: g.size // 2] = np.resize(edge, g.size // 2)
+        return torch.from_numpy(g)
+
+    run_fc(oracle, 40, 64, 24, 4, 1024, seed=16, edit_grad=edit)
+    run_fc(oracle, 40, 64, 24, 4, 1024, seed=16, edit_grad=edit, lr=0.5)
 
 
 def test_unusual_group_sizes(oracle, cuda_device):
@@ -186,7 +217,7 @@ def test_internal_policy_sgd(oracle, cuda_device):
     rW = W.numpy().copy()
     oracle.gather_wgrad_fc(go.numpy(), ridx, rW, B, O, T, E, first_meta_lr=0.5,
                            external_lr=np.float32(0.1))
-    xg_close(xg.cpu().numpy(), rxg, B, I)
+    xg_close(xg.cpu().numpy(), rxg, B, I, T, 2)
     assert np.array_equal(Wd.cpu().numpy(), rW)
 
 
