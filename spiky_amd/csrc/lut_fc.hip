@@ -34,7 +34,6 @@
 #include "lut_kernels.h"
 
 #include <algorithm>
-#include <cmath>
 
 namespace spiky {
 namespace {
@@ -552,28 +551,98 @@ __global__ __launch_bounds__(kWave) void k_bucket_samples(
     }
 }
 
+// Commit values of the weight gradient, one per (sample, output): what the
+// reference adds to a table row for that sample (gather_weight_gradients_fc,
+// proto:731-790): (float)((double)g * lr) if |(double)g| > EPS, or the int32
+// payload (int32)(g * lr * DENOM32 * int_rescaler) for int32 summation.  A
+// skipped term becomes -0.0f (float) or 0 (int), which leaves any sum
+// unchanged bit for bit (x + -0.0f == x for every x, including +-0.0).
+template <bool INT_MODE>
+__global__ __launch_bounds__(kBlock) void k_wgrad_commit_values(
+    const float *__restrict__ g, uint32_t *__restrict__ cv, uint64_t n, double lr,
+    double int_rescaler) {
+    const uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (i >= n) return;
+    const double gg = (double)g[i];
+    uint32_t v;
+    if (INT_MODE)
+        v = fabs(gg) > kEps ? (uint32_t)(int32_t)(gg * lr * kDenom32 * int_rescaler) : 0u;
+    else
+        v = fabs(gg) > kEps ? __float_as_uint((float)(gg * lr)) : 0x80000000u;
+    cv[i] = v;
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+template <int VEC>
+struct CvLoad;
+template <>
+struct CvLoad<1> {
+    __device__ static void load(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, uint32_t *v) {
+        v[0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+    }
+};
+template <>
+struct CvLoad<2> {
+    __device__ static void load(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, uint32_t *v) {
+        const u32x2 q = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+        v[0] = q.x;
+        v[1] = q.y;
+    }
+};
+template <>
+struct CvLoad<4> {
+    __device__ static void load(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, uint32_t *v) {
+        const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+        v[0] = q.x;
+        v[1] = q.y;
+        v[2] = q.z;
+        v[3] = q.w;
+    }
+};
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Non-temporal store of VEC floats (one instruction).
+template <int VEC>
+struct NtStore;
+template <>
+struct NtStore<1> {
+    __device__ static void store(float *p, const float *v) { __builtin_nontemporal_store(v[0], p); }
+};
+template <>
+struct NtStore<2> {
+    __device__ static void store(float *p, const float *v) {
+        __builtin_nontemporal_store(f32x2{v[0], v[1]}, reinterpret_cast<f32x2 *>(p));
+    }
+};
+template <>
+struct NtStore<4> {
+    __device__ static void store(float *p, const float *v) {
+        __builtin_nontemporal_store(f32x4{v[0], v[1], v[2], v[3]}, reinterpret_cast<f32x4 *>(p));
+    }
+};
+
 // Table-major weight gradient over column slices.  Wavefront = `rpw` (<= 63)
 // consecutive rows of one table x one column slice (slice -> XCD, so each XCD
-// only ever reads its own column slice of g, which stays in its L2).  The
-// rows' buckets are contiguous in the table's sorted sample list, so the
-// wavefront walks that list in flat batches of KB samples (KB gradient rows in
-// flight, double-buffered) and closes a row whenever the walk crosses its
-// bucket end.  Within a
-// row the samples are added in ascending order into an fp32 (or int32) sum
-// starting from the target value (or zero when overwriting): the reference
-// CPU path's order, so the result is bit-identical to it, and each target
-// element is written exactly once with no atomics.
-//
-// LR1: the learning rate is exactly 1, so the reference's committed value
-// (float)((double)g * lr) is g itself and its test |(double)g| > EPS is
-// |g| >= eps_f, the smallest float above EPS: the sum stays in fp32 and is
-// bit-identical to the general form.
-template <int VEC, int KB, bool INT_MODE, bool OVERWRITE, bool LR1>
+// only ever reads its own column slice of the commit values, which stays in its
+// L2).  The rows' buckets are contiguous in the table's sorted sample list, so
+// the wavefront walks that list in batches of KB samples (the next batch
+// loading while the current one is added, ping-pong) and closes a row whenever
+// the walk crosses its bucket end.  Within a row the commit values are added in
+// ascending sample order into an fp32 (or int32) sum starting from the target
+// value (or zero when overwriting): the reference CPU path's order, so the
+// result is bit-identical to it, and each target element is written exactly
+// once with no atomics.  Commit-value rows are read with buffer loads whose row
+// offset is a scalar register, so a sample costs VEC adds and one lane read.
+template <int VEC, int KB, bool INT_MODE, bool OVERWRITE>
 __global__ __launch_bounds__(kBlock) void k_wgrad_slices(
-    const float *__restrict__ g, const int32_t *__restrict__ offsets,
+    const uint32_t *__restrict__ cv, const int32_t *__restrict__ offsets,
     const int32_t *__restrict__ samples, float *__restrict__ target, uint32_t batch,
     uint32_t n_outputs, uint32_t n_entries, uint32_t n_detectors, uint32_t n_slices, uint32_t rpw,
-    double lr, double int_rescaler, float eps_f) {
+    double int_rescaler) {
     const uint32_t lane = threadIdx.x & (kWave - 1);
     const uint32_t wave = uniform(threadIdx.x / kWave);
     const uint32_t slice = blockIdx.x % n_slices;
@@ -586,6 +655,10 @@ __global__ __launch_bounds__(kBlock) void k_wgrad_slices(
     const uint32_t c = (slice * kWave + lane) * VEC;
     const bool active = c < n_outputs;
     const uint32_t cc = active ? c : 0u;
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)cv, (short)0, (int)(batch * n_outputs * 4u), 0x00020000);
+    const uint32_t voff = cc * 4u;
+    const uint32_t row_bytes = n_outputs * 4u;
 
     // lane i <= rpw holds the start of bucket e0 + i
     const int32_t *off_t = offsets + (size_t)t * (n_entries + 1) + e0;
@@ -595,60 +668,45 @@ __global__ __launch_bounds__(kBlock) void k_wgrad_slices(
     const int32_t kbeg = __builtin_amdgcn_readfirstlane(offv);
     const int32_t kend = __builtin_amdgcn_readlane(offv, rpw);
 
-    float acc[VEC];
-    int32_t iacc[VEC];
+    uint32_t acc[VEC];
     auto init = [&](uint32_t e) {
 #pragma unroll
-        for (int q = 0; q < VEC; q++) {
-            acc[q] = 0.0f;
-            iacc[q] = 0;
-        }
+        for (int q = 0; q < VEC; q++) acc[q] = 0u;  // +0.0f / int 0
         if (!OVERWRITE) {
             float v[VEC];
             RowLoad<float, VEC>::load(tb + (size_t)e * n_outputs, v);
 #pragma unroll
-            for (int q = 0; q < VEC; q++) {
-                acc[q] = v[q];
-                iacc[q] = __float_as_int(v[q]);
-            }
+            for (int q = 0; q < VEC; q++) acc[q] = __float_as_uint(v[q]);
         }
     };
+    // the rows are written once and not re-read here: non-temporal stores keep
+    // them from evicting the commit values this XCD re-reads from its L2
     auto store = [&](uint32_t e) {
         if (!active) return;
         float *p = tb + (size_t)e * n_outputs;
+        float v[VEC];
 #pragma unroll
         for (int q = 0; q < VEC; q++)
-            p[q] = INT_MODE ? (float)(((double)iacc[q] * kDenom32Reciproc) / int_rescaler) : acc[q];
+            v[q] = INT_MODE ? (float)(((double)(int32_t)acc[q] * kDenom32Reciproc) / int_rescaler)
+                            : __uint_as_float(acc[q]);
+        NtStore<VEC>::store(p, v);
     };
 
     uint32_t e = 0;
     int32_t row_end = __builtin_amdgcn_readlane(offv, 1);
     init(0);
-    // samples are walked in chunks of up to 64 ids (one vector load), and each
-    // chunk in batches of KB gradient rows, the next batch loading while the
-    // current one is added
     for (int32_t k = kbeg; k < kend; k += kWave) {
         const int32_t n = min((int32_t)kWave, kend - k);
         const int32_t idv = smp[k + min((int32_t)lane, n - 1)];
-        float cur[KB][VEC], nxt[KB][VEC];
+        uint32_t va[KB][VEC], vb[KB][VEC];
+        auto load = [&](uint32_t (&v)[KB][VEC], int32_t j0) {
 #pragma unroll
-        for (int j = 0; j < KB; j++) {
-            const uint32_t b = (uint32_t)__builtin_amdgcn_readlane(idv, min(j, n - 1));
-            RowLoad<float, VEC>::load(g + (size_t)b * n_outputs + cc, nxt[j]);
-        }
-        for (int32_t j0 = 0; j0 < n; j0 += KB) {
-#pragma unroll
-            for (int j = 0; j < KB; j++)
-#pragma unroll
-                for (int q = 0; q < VEC; q++) cur[j][q] = nxt[j][q];
-            if (j0 + KB < n) {
-#pragma unroll
-                for (int j = 0; j < KB; j++) {
-                    const uint32_t b =
-                        (uint32_t)__builtin_amdgcn_readlane(idv, min(j0 + KB + j, n - 1));
-                    RowLoad<float, VEC>::load(g + (size_t)b * n_outputs + cc, nxt[j]);
-                }
+            for (int j = 0; j < KB; j++) {
+                const uint32_t b = (uint32_t)__builtin_amdgcn_readlane(idv, min(j0 + j, n - 1));
+                CvLoad<VEC>::load(rsrc, voff, b * row_bytes, v[j]);
             }
+        };
+        auto add = [&](const uint32_t (&v)[KB][VEC], int32_t j0) {
 #pragma unroll
             for (int j = 0; j < KB; j++) {
                 if (j0 + j >= n) break;
@@ -661,19 +719,26 @@ __global__ __launch_bounds__(kBlock) void k_wgrad_slices(
                 }
 #pragma unroll
                 for (int q = 0; q < VEC; q++) {
-                    if (LR1 && !INT_MODE) {
-                        if (fabsf(cur[j][q]) >= eps_f) acc[q] += cur[j][q];
-                    } else {
-                        const double gg = (double)cur[j][q];
-                        if (fabs(gg) > kEps) {
-                            if (INT_MODE)
-                                iacc[q] = wrap_add(iacc[q], (int32_t)(gg * lr * kDenom32 * int_rescaler));
-                            else
-                                acc[q] += (float)(gg * lr);
-                        }
-                    }
+                    if (INT_MODE)
+                        acc[q] = acc[q] + v[j][q];
+                    else
+                        acc[q] = __float_as_uint(__uint_as_float(acc[q]) + __uint_as_float(v[j][q]));
                 }
             }
+        };
+        int32_t j0 = 0;
+        load(va, 0);
+        for (;;) {
+            const bool more_b = j0 + KB < n;
+            if (more_b) load(vb, j0 + KB);
+            add(va, j0);
+            j0 += KB;
+            if (!more_b) break;
+            const bool more_a = j0 + KB < n;
+            if (more_a) load(va, j0 + KB);
+            add(vb, j0);
+            j0 += KB;
+            if (!more_a) break;
         }
     }
     for (;;) {
@@ -699,17 +764,10 @@ __global__ __launch_bounds__(kBlock) void k_convert_i2f(float *__restrict__ buf,
 
 uint32_t blocks_for(uint64_t n) { return (uint32_t)((n + kBlock - 1) / kBlock); }
 
-// Smallest float f with (double)f > EPS: |g| >= f is the reference's test
-// |(double)g| > EPS for a float g (misc.h:90).
-float smallest_float_above_eps() {
-    float f = (float)kEps;
-    if ((double)f <= kEps) f = std::nextafter(f, INFINITY);
-    return f;
-}
-
-// The bucketed weight gradient needs the per-table bucket counters in LDS.
+// The bucketed weight gradient needs the per-table bucket counters in LDS and
+// byte offsets of the commit values within 32 bits (buffer loads).
 bool rowsum_applies(const FcShape &s) {
-    return s.n_entries <= 4096 && s.batch <= 0x7fffffffu;
+    return s.n_entries <= 4096 && (uint64_t)s.batch * s.n_outputs * 4 < 0x7fffffffull;
 }
 
 }  // namespace
@@ -812,9 +870,11 @@ hipError_t launch_propagate_fc(const FcShape &s, const float *w, const float *g,
     return hipGetLastError();
 }
 
+// scratch: bucket offsets [T][E+1] | sorted samples [T][B] | commit values [B][O]
 size_t wgrad_fc_scratch_bytes(const FcShape &s) {
     if (!rowsum_applies(s)) return 0;
-    return ((size_t)s.n_detectors * (s.n_entries + 1) + (size_t)s.n_detectors * s.batch) *
+    return ((size_t)s.n_detectors * (s.n_entries + 1) + (size_t)s.n_detectors * s.batch +
+            (size_t)s.batch * s.n_outputs) *
            sizeof(int32_t);
 }
 
@@ -833,24 +893,30 @@ hipError_t launch_wgrad_fc(const FcShape &s, const float *g, const int32_t *idx,
         const uint64_t units = (uint64_t)s.n_detectors * (s.n_entries / rpw);
         const uint64_t grid = (uint64_t)n_slices * ((units + kWPB - 1) / kWPB);
         if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
-        const bool lr1 = !int_mode && lr == 1.0;
-        const float eps_f = smallest_float_above_eps();
-#define SPIKY_WG(V, IM, OW, L1)                                                                   \
-    hipLaunchKernelGGL((k_wgrad_slices<V, 8, IM, OW, L1>), dim3((uint32_t)grid), dim3(kBlock), 0, \
-                       st, g, offsets, samples, target, s.batch, s.n_outputs, s.n_entries,        \
-                       s.n_detectors, n_slices, rpw, lr, int_rescaler, eps_f)
-#define SPIKY_WG_V(IM, OW, L1)                     \
-    switch (vec) {                                 \
-        case 4: SPIKY_WG(4, IM, OW, L1); break;    \
-        case 2: SPIKY_WG(2, IM, OW, L1); break;    \
-        default: SPIKY_WG(1, IM, OW, L1); break;   \
+        uint32_t *cv = reinterpret_cast<uint32_t *>(samples + (size_t)s.n_detectors * s.batch);
+        const uint64_t n_cv = (uint64_t)s.batch * s.n_outputs;
+        if (int_mode)
+            hipLaunchKernelGGL(k_wgrad_commit_values<true>, dim3(blocks_for(n_cv)), dim3(kBlock), 0,
+                               st, g, cv, n_cv, lr, int_rescaler);
+        else
+            hipLaunchKernelGGL(k_wgrad_commit_values<false>, dim3(blocks_for(n_cv)), dim3(kBlock), 0,
+                               st, g, cv, n_cv, lr, int_rescaler);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+#define SPIKY_WG(V, IM, OW)                                                                       \
+    hipLaunchKernelGGL((k_wgrad_slices<V, 8, IM, OW>), dim3((uint32_t)grid), dim3(kBlock), 0, st, \
+                       cv, offsets, samples, target, s.batch, s.n_outputs, s.n_entries,           \
+                       s.n_detectors, n_slices, rpw, int_rescaler)
+#define SPIKY_WG_V(IM, OW)                     \
+    switch (vec) {                             \
+        case 4: SPIKY_WG(4, IM, OW); break;    \
+        case 2: SPIKY_WG(2, IM, OW); break;    \
+        default: SPIKY_WG(1, IM, OW); break;   \
     }
         if (int_mode) {
-            if (overwrite) { SPIKY_WG_V(true, true, false) } else { SPIKY_WG_V(true, false, false) }
-        } else if (lr1) {
-            if (overwrite) { SPIKY_WG_V(false, true, true) } else { SPIKY_WG_V(false, false, true) }
+            if (overwrite) { SPIKY_WG_V(true, true) } else { SPIKY_WG_V(true, false) }
         } else {
-            if (overwrite) { SPIKY_WG_V(false, true, false) } else { SPIKY_WG_V(false, false, false) }
+            if (overwrite) { SPIKY_WG_V(false, true) } else { SPIKY_WG_V(false, false) }
         }
 #undef SPIKY_WG_V
 #undef SPIKY_WG

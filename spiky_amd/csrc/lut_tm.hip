@@ -261,7 +261,10 @@ __global__ __launch_bounds__(kTmThreads) void k_fill_tm(
             o.z = __float_as_uint((float)acc[i][2]);
             o.w = __float_as_uint((float)acc[i][3]);
         }
-        *reinterpret_cast<uint4 *>(part + ((size_t)k * batch + b) * n_outputs + col) = o;
+        // written once, read once by the commit kernel: non-temporal
+        __builtin_nontemporal_store(
+            u32x4{o.x, o.y, o.z, o.w},
+            reinterpret_cast<u32x4 *>(part + ((size_t)k * batch + b) * n_outputs + col));
     }
 }
 
@@ -402,7 +405,8 @@ __global__ __launch_bounds__(kTmThreads) void k_propagate_tm(
             reduce_scatter8<SPT>(dv, q);
             const uint32_t b = b_base + s_loc0 + kTmPass * rs_item<SPT>(q);
             if (rs_writer<SPT>(q) && b < batch)
-                dpart[((size_t)slice * n_detectors + t) * batch + b] = (float)dv[0];
+                __builtin_nontemporal_store((float)dv[0],
+                                            dpart + ((size_t)slice * n_detectors + t) * batch + b);
         }
     }
 }
