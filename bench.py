@@ -207,6 +207,7 @@ def main():
     dom = max(ktimes.items(), key=lambda kv: kv[1][1])[0]
     dom_ms = ktimes[dom][1] / ktimes[dom][0]
     achieved = gbytes[dom] / (dom_ms * 1e-3) / 1e9
+    traffic = load_traffic(dom, args.config)
     step_g = sum(gbytes.values())
     roofline = {
         "bound": "hbm",
@@ -215,7 +216,10 @@ def main():
         "peak": PEAK_HBM_GBS,
         "unit": "GB/s",
         "frac": round(achieved / PEAK_HBM_GBS, 4),
-        "traffic": load_traffic(dom, args.config),
+        "traffic": traffic,
+        # measured HBM bytes (rocprofv3 counters, profiles/) over the same launch time
+        "traffic_gbs": round(traffic / (dom_ms * 1e-3) / 1e9, 1) if traffic else None,
+        "traffic_frac": round(traffic / (dom_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4) if traffic else None,
         "algorithmic_bytes_per_launch": gbytes[dom],
         "ms_per_launch": round(dom_ms, 4),
         "step_g_model_frac": round(step_g / (ms_per_step * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),

@@ -405,8 +405,9 @@ __global__ __launch_bounds__(kTmThreads) void k_propagate_tm(
             reduce_scatter8<SPT>(dv, q);
             const uint32_t b = b_base + s_loc0 + kTmPass * rs_item<SPT>(q);
             if (rs_writer<SPT>(q) && b < batch)
-                __builtin_nontemporal_store((float)dv[0],
-                                            dpart + ((size_t)slice * n_detectors + t) * batch + b);
+                // 4-byte pieces of 4 KiB table rows: plain stores, so that L2
+                // merges them into full lines before they reach HBM
+                dpart[((size_t)slice * n_detectors + t) * batch + b] = (float)dv[0];
         }
     }
 }
