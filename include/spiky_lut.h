@@ -108,6 +108,38 @@ int spiky_lut_backward_backprop(spiky_lut_manager *m, float *weights, uint32_t b
                                 double external_lr, float *weight_grad,
                                 int overwrite_weight_grad, void *stream);
 
+/* Replaces forward_step_concat (lut.cu pybind 1556-1575 -> lut_runtime.cu:399-593):
+ * check_detectors_seq(_eval) over the batch_size*S rows of input [B][S][I],
+ * check_positional_embeddings(_eval) over positional_embeddings [(S-1)][T][Npe]
+ * (unused when positional_dim == 0), then fill_outputs_fully_connected_seq into
+ * output [B][S][O].  Lookup indices / min deltas / min indices are [B][S][T];
+ * positional ones [(S-1)][T].  min_deltas == NULL selects eval mode, and then
+ * the three min-delta arguments must all be NULL.  Fully connected managers with
+ * sequence_length > 1 only. */
+int spiky_lut_forward_step_concat(spiky_lut_manager *m, const float *weights, uint32_t batch_size,
+                                  const float *input, const int32_t *anchors, float *output,
+                                  int32_t *lookup_indices, float cmp_eps,
+                                  const float *positional_embeddings,
+                                  int32_t *positional_lookup_indices, float *min_deltas,
+                                  int32_t *min_delta_indices, float *positional_min_deltas,
+                                  int32_t *positional_min_delta_indices, void *stream);
+
+/* Replaces backward_backprop_concat (lut.cu pybind 1620-1636 ->
+ * lut_runtime.cu:595-850): propagate_through_detectors_seq_fc into input_grad
+ * [B][S][I] and positional_grad [(S-1)][T][Npe], and gather_w_gradients_seq_fc
+ * into weight_grad (external_lr < 0) or, for the Internal policy
+ * (external_lr >= 0, weight_grad NULL), the in-place update of weights.
+ * overwrite_weight_grad as for spiky_lut_backward_backprop. */
+int spiky_lut_backward_backprop_concat(spiky_lut_manager *m, float *weights, uint32_t batch_size,
+                                       const float *output_grad, const int32_t *anchors,
+                                       const int32_t *lookup_indices, const float *min_deltas,
+                                       const int32_t *min_delta_indices, float *input_grad,
+                                       double external_lr, const int32_t *positional_lookup_indices,
+                                       const float *positional_min_deltas,
+                                       const int32_t *positional_min_delta_indices,
+                                       float *positional_grad, float *weight_grad,
+                                       int overwrite_weight_grad, void *stream);
+
 /* Replaces add_lookup_connections + compile for sparse managers
  * (lut.cu:560-627) with this build's CSR: lookup neuron n owns synapses
  * [syn_offsets[n], syn_offsets[n+1]) whose targets are output indices in

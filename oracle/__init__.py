@@ -59,6 +59,14 @@ def lib():
                                               _int, _f64]
         L.oracle_gather_wgrad_sparse.argtypes = [_f32p, _i32p, _i64p, _i32p, _f32p, _i64, _i64, _i64,
                                                  _i64, _f32, _f32, _int, _f64]
+        L.oracle_check_pe.argtypes = [_f32p, _i64, _i64, _i64, _f32, _i32p, _vp, _vp]
+        L.oracle_fill_outputs_seq.argtypes = [_f32p, _i32p, _vp, _f32p, _i64, _i64, _i64, _i64, _i64,
+                                              _i64, _int, _f64]
+        L.oracle_propagate_seq.argtypes = [_f32p, _f32p, _i32p, _f32p, _i32p, _vp, _vp, _vp, _i32p,
+                                           _f32p, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                           _i64, _int, _f64]
+        L.oracle_gather_wgrad_seq.argtypes = [_f32p, _i32p, _vp, _f32p, _i64, _i64, _i64, _i64, _i64,
+                                              _i64, _i64, _f32, _f32, _int, _f64]
         _lib = L
     return _lib
 
@@ -167,4 +175,56 @@ def gather_wgrad_sparse(g, idx, syn_offsets, syn_targets, target, batch, n_outpu
                                      _c(syn_targets, np.int32), target, batch, n_outputs,
                                      n_detectors, n_entries, float(first_meta_lr),
                                      float(external_lr), int(int_mode), float(int_rescaler))
+    return target
+
+
+# ---------------------------------------------------------------- sequence-concat path
+def check_pe(pe, seq_len, n_detectors, positional_dim, cmp_eps=0.0, train=True):
+    """Positional lookup indices [(S-1)][T] (and min margins in train mode)."""
+    n = (seq_len - 1) * n_detectors
+    pidx = np.zeros(n, dtype=np.int32)
+    pmd = np.zeros(n, dtype=np.float32) if train else None
+    pmi = np.zeros(n, dtype=np.int32) if train else None
+    lib().oracle_check_pe(_c(pe, np.float32), seq_len, n_detectors, positional_dim, float(cmp_eps),
+                          pidx, _ptr(pmd), _ptr(pmi))
+    return (pidx, pmd, pmi) if train else pidx
+
+
+def fill_outputs_seq(w, idx, pidx, batch, n_outputs, n_detectors, seq_len, n_anchors,
+                     positional_dim, out=None, int_mode=False, int_rescaler=1.0):
+    if out is None:
+        out = np.zeros(batch * seq_len * n_outputs, dtype=np.float32)
+    pidx = None if pidx is None else _c(pidx, np.int32)
+    lib().oracle_fill_outputs_seq(_c(w, np.float32), _c(idx, np.int32), _ptr(pidx), out, batch,
+                                  n_outputs, n_detectors, seq_len, n_anchors, positional_dim,
+                                  int(int_mode), float(int_rescaler))
+    return out
+
+
+def propagate_seq(w, g, idx, md, mi, pidx, pmd, pmi, anchors, batch, n_inputs, n_outputs,
+                  n_detectors, seq_len, n_anchors, positional_dim, ogs=32, x_grad=None,
+                  pe_grad=None, int_mode=False, int_rescaler=1.0):
+    """Returns (x_grad [B*S*I], pe_grad [(S-1)*T*Npe] or None)."""
+    if x_grad is None:
+        x_grad = np.zeros(batch * seq_len * n_inputs, dtype=np.float32)
+    if pe_grad is None and positional_dim > 0:
+        pe_grad = np.zeros((seq_len - 1) * n_detectors * positional_dim, dtype=np.float32)
+    pidx, pmd, pmi = (None if a is None else _c(a, dt) for a, dt in
+                      ((pidx, np.int32), (pmd, np.float32), (pmi, np.int32)))
+    lib().oracle_propagate_seq(_c(w, np.float32), _c(g, np.float32), _c(idx, np.int32),
+                               _c(md, np.float32), _c(mi, np.int32), _ptr(pidx), _ptr(pmd),
+                               _ptr(pmi), _c(anchors, np.int32), x_grad, _ptr(pe_grad), batch,
+                               n_inputs, n_outputs, n_detectors, seq_len, n_anchors,
+                               positional_dim, ogs, int(int_mode), float(int_rescaler))
+    return x_grad, pe_grad
+
+
+def gather_wgrad_seq(g, idx, pidx, target, batch, n_outputs, n_detectors, seq_len, n_anchors,
+                     positional_dim, ogs=32, first_meta_lr=1.0, external_lr=-1.0,
+                     int_mode=False, int_rescaler=1.0):
+    pidx = None if pidx is None else _c(pidx, np.int32)
+    lib().oracle_gather_wgrad_seq(_c(g, np.float32), _c(idx, np.int32), _ptr(pidx), target, batch,
+                                  n_outputs, n_detectors, seq_len, n_anchors, positional_dim, ogs,
+                                  float(first_meta_lr), float(external_lr), int(int_mode),
+                                  float(int_rescaler))
     return target

@@ -381,3 +381,202 @@ void oracle_gather_wgrad_sparse(
         }
     }
 }
+
+/* ======================================================================== */
+/* Sequence-concat mode (LUTTransformer attention).                          */
+/* Layouts: x [B][S][I]; idx / md / mi [B][S][T]; pe [(S-1)][T][Npe];        */
+/* pidx / pmd / pmi [(S-1)][T]; out / g [B][S][O];                           */
+/* W [T][2^(2Nc+Npe)][O] with row (Q << (Nc+Npe)) | (K << Npe) | PE.         */
+/* check_detectors_seq(_eval) (proto:1589-1707) is check_detectors over the  */
+/* B*S rows of x, which is what the callers use.                             */
+/* ======================================================================== */
+
+/* check_positional_embeddings(_eval)_logic, proto:1709-1805.  pmd / pmi     */
+/* may be NULL (eval).                                                       */
+void oracle_check_pe(
+    const float *pe, int64_t seq_len, int64_t n_detectors, int64_t positional_dim,
+    float cmp_eps, int32_t *pidx, float *pmd, int32_t *pmi)
+{
+    for (int64_t it = 0; it < (seq_len - 1) * n_detectors; it++) {
+        const float *v = pe + it * positional_dim;
+        int32_t li = 0, mk = -1;
+        float mind = 0.0f;
+        for (int64_t d = 0; d < positional_dim; d++) {
+            if (rounded_greater0(v[d], cmp_eps)) li |= (1 << d);
+            if (mk == -1 || fabsf(v[d]) < fabsf(mind)) {
+                mind = v[d];
+                mk = (int32_t)d;
+            }
+        }
+        pidx[it] = li;
+        if (pmd) pmd[it] = mind;
+        if (pmi) pmi[it] = mk;
+    }
+}
+
+static inline int64_t seq_row(int32_t q, int32_t k, int32_t p, int64_t n_anchors, int64_t pd)
+{
+    return ((int64_t)q << (n_anchors + pd)) | ((int64_t)k << pd) | (int64_t)p;
+}
+
+/* fill_outputs_fully_connected_seq_logic, proto:1807-1904.  Serial order:   */
+/* for b: item ((j-1)*T + t)*O + o ascending; each item commits the fp64 sum */
+/* over i < j once (fp32, or the int32 payload).                             */
+void oracle_fill_outputs_seq(
+    const float *w, const int32_t *idx, const int32_t *pidx, float *out,
+    int64_t batch, int64_t n_outputs, int64_t n_detectors, int64_t seq_len,
+    int64_t n_anchors, int64_t positional_dim, int int_mode, double int_rescaler)
+{
+    const int64_t nlpd = (int64_t)1 << (2 * n_anchors + positional_dim);
+    for (int64_t b = 0; b < batch; b++) {
+        for (int64_t j = 1; j < seq_len; j++) {
+            for (int64_t t = 0; t < n_detectors; t++) {
+                int32_t q = idx[(b * seq_len + j) * n_detectors + t];
+                for (int64_t o = 0; o < n_outputs; o++) {
+                    double ws = 0.0;
+                    for (int64_t i = 0; i < j; i++) {
+                        int32_t k = idx[(b * seq_len + i) * n_detectors + t];
+                        int32_t p = positional_dim > 0 ? pidx[(j - i - 1) * n_detectors + t] : 0;
+                        int64_t row = t * nlpd + seq_row(q, k, p, n_anchors, positional_dim);
+                        ws += (double)w[row * n_outputs + o];
+                    }
+                    float *dst = out + (b * seq_len + j) * n_outputs + o;
+                    if (int_mode)
+                        *as_i32(dst) = wrap_add(*as_i32(dst), (int32_t)(ws * OR_DENOM32 * int_rescaler));
+                    else
+                        *dst += (float)ws;
+                }
+            }
+        }
+    }
+}
+
+/* Visits the causal pairs in the reference CPU path's serial order for the  */
+/* seq backward kernels (lut_runtime.cu:630-637, proto:3653-3689):           */
+/* b -> output block -> tile (ti row-major, tiles with ti > tj skipped) ->   */
+/* detector -> thread (i = ti*32 + tid%32, j = tj*32 + tid/32, i < j).       */
+#define OR_TILE 32
+#define FOR_SEQ_PAIRS(B, S, NOB, T, ...)                                               \
+    do {                                                                               \
+        int64_t tgw_ = ((S) + OR_TILE - 1) / OR_TILE;                                  \
+        for (int64_t b = 0; b < (B); b++)                                              \
+            for (int64_t ob = 0; ob < (NOB); ob++)                                     \
+                for (int64_t tile_ = 0; tile_ < tgw_ * tgw_; tile_++) {                \
+                    int64_t ti_ = tile_ / tgw_, tj_ = tile_ % tgw_;                    \
+                    if (ti_ > tj_) continue;                                           \
+                    for (int64_t t = 0; t < (T); t++)                                  \
+                        for (int64_t tid_ = 0; tid_ < OR_TILE * OR_TILE; tid_++) {     \
+                            int64_t i = ti_ * OR_TILE + tid_ % OR_TILE;                \
+                            int64_t j = tj_ * OR_TILE + tid_ / OR_TILE;                \
+                            if (i >= j || j >= (S)) continue;                          \
+                            __VA_ARGS__                                                \
+                        }                                                              \
+                }                                                                      \
+    } while (0)
+
+static inline double block_dot(const float *w, int64_t row, const float *gj, int64_t n_outputs,
+                               int64_t o0, int64_t o1)
+{
+    double s = 0.0;
+    for (int64_t o = o0; o < o1; o++) s += (double)w[row * n_outputs + o] * (double)gj[o];
+    return s;
+}
+
+/* propagate_through_detectors_seq_fc_logic, proto:3629-3835, with           */
+/* accumulate_pair_of_gradient_sums_fc / accumulate_grad_sum_fc (proto:396-  */
+/* 582), propagate_through_detector (proto:821-867) and                      */
+/* update_positional_gradients (proto:1016-1046, no EPS cut).  Per (pair,    */
+/* detector, output block): flip Q's min anchor if |dQ| < |dK| else K's; the */
+/* positional flip applies when |dPE| is strictly the smallest.  pe_grad may */
+/* be NULL when positional_dim == 0.                                         */
+void oracle_propagate_seq(
+    const float *w, const float *g, const int32_t *idx, const float *md, const int32_t *mi,
+    const int32_t *pidx, const float *pmd, const int32_t *pmi, const int32_t *anchors,
+    float *x_grad, float *pe_grad, int64_t batch, int64_t n_inputs, int64_t n_outputs,
+    int64_t n_detectors, int64_t seq_len, int64_t n_anchors, int64_t positional_dim, int64_t ogs,
+    int int_mode, double int_rescaler)
+{
+    const int64_t nlpd = (int64_t)1 << (2 * n_anchors + positional_dim);
+    const int64_t n_ob = (n_outputs + ogs - 1) / ogs;
+    const int64_t pd = positional_dim;
+    FOR_SEQ_PAIRS(batch, seq_len, n_ob, n_detectors, {
+        int64_t o0 = ob * ogs, o1 = o0 + ogs < n_outputs ? o0 + ogs : n_outputs;
+        int64_t ko = (b * seq_len + i) * n_detectors + t, qo = (b * seq_len + j) * n_detectors + t;
+        int32_t K = idx[ko], Q = idx[qo];
+        int32_t km = mi[ko], qm = mi[qo];
+        float kd = md[ko], qd = md[qo];
+        int32_t P = 0, pm = -1;
+        float pdl = 0.0f;
+        int64_t pe_off = (j - i - 1) * n_detectors + t;
+        if (pd > 0) {
+            P = pidx[pe_off];
+            pm = pmi[pe_off];
+            pdl = pmd[pe_off];
+        }
+        const float *gj = g + (b * seq_len + j) * n_outputs;
+        int64_t main_row = t * nlpd + seq_row(Q, K, P, n_anchors, pd);
+        int64_t alt_row, src_pos;
+        int32_t flip;
+        double du;
+        if (fabsf(qd) < fabsf(kd)) {
+            alt_row = t * nlpd + seq_row(qm >= 0 ? Q ^ (1 << qm) : Q, K, P, n_anchors, pd);
+            du = du_of_margin(qd);
+            flip = qm;
+            src_pos = j;
+        } else {
+            alt_row = t * nlpd + seq_row(Q, km >= 0 ? K ^ (1 << km) : K, P, n_anchors, pd);
+            du = du_of_margin(kd);
+            flip = km;
+            src_pos = i;
+        }
+        double ms = block_dot(w, main_row, gj, n_outputs, o0, o1);
+        double as = block_dot(w, alt_row, gj, n_outputs, o0, o1);
+        du *= ms - as;
+        if (flip >= 0) {
+            const int32_t *ap = anchors + (t * n_anchors + flip) * 2;
+            push_input_grad(x_grad + (b * seq_len + src_pos) * n_inputs, ap[0], ap[1], du, int_mode,
+                            int_rescaler);
+        }
+        if (pd > 0 && fabsf(pdl) < fabsf(qd) && fabsf(pdl) < fabsf(kd) && pm >= 0) {
+            int64_t pe_row = t * nlpd + seq_row(Q, K, P ^ (1 << pm), n_anchors, pd);
+            double dpe = du_of_margin(pdl) * (ms - block_dot(w, pe_row, gj, n_outputs, o0, o1));
+            float *dst = pe_grad + pe_off * pd + pm;
+            if (int_mode)
+                *as_i32(dst) = wrap_add(*as_i32(dst), (int32_t)(dpe * OR_DENOM32 * int_rescaler));
+            else
+                *dst = (float)((double)*dst + dpe);
+        }
+    });
+}
+
+/* gather_w_gradients_seq_fc_cpu_logic, proto:3944-4045, with                */
+/* gather_weight_gradients_fc (proto:716-819, CPU branch 792-818): every     */
+/* causal pair (i < j) adds (float)(g[b][j][o] * lr) to its row (|g| > EPS). */
+void oracle_gather_wgrad_seq(
+    const float *g, const int32_t *idx, const int32_t *pidx, float *target,
+    int64_t batch, int64_t n_outputs, int64_t n_detectors, int64_t seq_len, int64_t n_anchors,
+    int64_t positional_dim, int64_t ogs, float first_meta_lr, float external_lr, int int_mode,
+    double int_rescaler)
+{
+    const int64_t nlpd = (int64_t)1 << (2 * n_anchors + positional_dim);
+    const int64_t n_ob = (n_outputs + ogs - 1) / ogs;
+    double lr = (double)first_meta_lr;
+    if (external_lr >= 0) lr *= -(double)external_lr;
+    FOR_SEQ_PAIRS(batch, seq_len, n_ob, n_detectors, {
+        int64_t o0 = ob * ogs, o1 = o0 + ogs < n_outputs ? o0 + ogs : n_outputs;
+        int32_t K = idx[(b * seq_len + i) * n_detectors + t];
+        int32_t Q = idx[(b * seq_len + j) * n_detectors + t];
+        int32_t P = positional_dim > 0 ? pidx[(j - i - 1) * n_detectors + t] : 0;
+        int64_t row = t * nlpd + seq_row(Q, K, P, n_anchors, positional_dim);
+        const float *gj = g + (b * seq_len + j) * n_outputs;
+        for (int64_t o = o0; o < o1; o++) {
+            double gg = (double)gj[o];
+            if (!(fabs(gg) > OR_EPS)) continue;
+            float *dst = target + row * n_outputs + o;
+            if (int_mode)
+                *as_i32(dst) = wrap_add(*as_i32(dst), (int32_t)(gg * lr * OR_DENOM32 * int_rescaler));
+            else
+                *dst += (float)(gg * lr);
+        }
+    });
+}

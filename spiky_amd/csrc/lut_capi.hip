@@ -611,6 +611,117 @@ int spiky_lut_backward_backprop(spiky_lut_manager *m, float *weights, uint32_t b
     });
 }
 
+static spiky::SeqShape seq_shape(const spiky_lut_manager *m, uint32_t batch) {
+    spiky::SeqShape s;
+    s.batch = batch;
+    s.seq = m->sequence_length;
+    s.n_inputs = m->n_inputs;
+    s.n_outputs = m->n_outputs;
+    s.n_detectors = m->n_detectors;
+    s.n_anchors = m->n_anchors;
+    s.pe_dim = m->positional_dim;
+    s.dgs = m->backward_group_size;
+    s.ogs = m->forward_group_size;
+    return s;
+}
+
+static void require_seq(const spiky_lut_manager *m, uint32_t batch_size, const char *what) {
+    if (batch_size == 0) throw ValueError("batch_size == 0");
+    // lut_runtime.cu:438-440 / 620-622
+    if (m->sequence_length <= 1)
+        throw ValueError(std::string(what) + " should only be called when sequence_length > 1");
+    require_initialized(m);
+    if (m->fully_connected != 1)
+        throw ValueError("sequence mode is built for fully connected managers only");
+    if (2 * m->n_anchors + m->positional_dim > 24)
+        throw ValueError("2 * n_anchors_per_detector + positional_dim > 24 is not supported");
+    if ((uint64_t)batch_size * m->sequence_length > 0x7fffffffull)
+        throw ValueError("batch_size * sequence_length is too large");
+}
+
+int spiky_lut_forward_step_concat(spiky_lut_manager *m, const float *weights, uint32_t batch_size,
+                                  const float *input, const int32_t *anchors, float *output,
+                                  int32_t *lookup_indices, float cmp_eps,
+                                  const float *positional_embeddings,
+                                  int32_t *positional_lookup_indices, float *min_deltas,
+                                  int32_t *min_delta_indices, float *positional_min_deltas,
+                                  int32_t *positional_min_delta_indices, void *stream) {
+    return guarded([&] {
+        require_manager(m);
+        require_seq(m, batch_size, "forward_step_concat");
+        if (!weights || !input || !anchors || !output || !lookup_indices)
+            throw ValueError("null tensor pointer");
+        const bool train = min_deltas != nullptr;
+        if ((min_delta_indices != nullptr) != train)
+            throw ValueError("w_min_anchor_deltas and w_min_anchor_delta_indices must be given together");
+        if (m->positional_dim > 0) {
+            // lut.cu:737-777
+            if (!positional_embeddings) throw ValueError("r_positional_embeddings must be provided when positional_dim > 0");
+            if (!positional_lookup_indices) throw ValueError("w_positional_lookup_indices must be provided when positional_dim > 0");
+            if (train && (!positional_min_deltas || !positional_min_delta_indices))
+                throw ValueError("positional min deltas must be provided in training mode when positional_dim > 0");
+        }
+        ScopedTimer timer(m->stats, train ? "lut::runtime::forward_seq" : "lut::runtime::forward_seq_eval");
+        m->context_active = true;
+        const hipStream_t st = as_stream(stream);
+        const spiky::SeqShape s = seq_shape(m, batch_size);
+        void *scr = m->scratch_fwd.ensure(spiky::seq_scratch_bytes(s, false));
+        m->timed("fill_outputs_seq", st, [&] {
+            check_hip(spiky::launch_forward_seq(s, weights, input, anchors, positional_embeddings,
+                                                output, lookup_indices, positional_lookup_indices,
+                                                min_deltas, min_delta_indices, positional_min_deltas,
+                                                positional_min_delta_indices, cmp_eps, m->int_mode,
+                                                m->int_rescaler, scr, st),
+                      "forward_step_concat");
+        });
+    });
+}
+
+int spiky_lut_backward_backprop_concat(spiky_lut_manager *m, float *weights, uint32_t batch_size,
+                                       const float *output_grad, const int32_t *anchors,
+                                       const int32_t *lookup_indices, const float *min_deltas,
+                                       const int32_t *min_delta_indices, float *input_grad,
+                                       double external_lr, const int32_t *positional_lookup_indices,
+                                       const float *positional_min_deltas,
+                                       const int32_t *positional_min_delta_indices,
+                                       float *positional_grad, float *weight_grad,
+                                       int overwrite_weight_grad, void *stream) {
+    return guarded([&] {
+        require_manager(m);
+        if (batch_size == 0) throw ValueError("batch_size == 0");
+        if (!m->context_active) throw ValueError("no active context");
+        require_seq(m, batch_size, "backward_backprop_concat");
+        const float ext = (float)external_lr;
+        if (ext >= 0.0f && weight_grad != nullptr)
+            throw ValueError("in internal weight gradients mode w_weights_gradients should be nullptr");
+        if (ext >= 0.0f && m->int_mode)
+            throw ValueError("summation dtype torch.int32 can't be combined with GradientType.Internal");
+        if (!weights || !output_grad || !anchors || !lookup_indices || !min_deltas ||
+            !min_delta_indices || !input_grad)
+            throw ValueError("null tensor pointer");
+        if (m->positional_dim > 0 && (!positional_lookup_indices || !positional_min_deltas ||
+                                      !positional_min_delta_indices || !positional_grad))
+            throw ValueError("positional tensors must be provided when positional_dim > 0");
+        ScopedTimer timer(m->stats, "lut::runtime::backward_seq");
+        const hipStream_t st = as_stream(stream);
+        const spiky::SeqShape s = seq_shape(m, batch_size);
+        double lr = (double)m->metas[0][0];
+        if (ext >= 0.0f) lr *= -(double)ext;
+        float *target = (ext >= 0.0f) ? weights : weight_grad;
+        const bool overwrite = overwrite_weight_grad != 0 && target == weight_grad;
+        void *scr = m->scratch.ensure(spiky::seq_scratch_bytes(s, true));
+        m->timed("backward_seq", st, [&] {
+            check_hip(spiky::launch_backward_seq(s, weights, output_grad, anchors, lookup_indices,
+                                                 min_deltas, min_delta_indices,
+                                                 positional_lookup_indices, positional_min_deltas,
+                                                 positional_min_delta_indices, input_grad,
+                                                 positional_grad, target, lr, overwrite, m->int_mode,
+                                                 m->int_rescaler, scr, st),
+                      "backward_backprop_concat");
+        });
+    });
+}
+
 int spiky_lut_decode_anchors_compact(const uint32_t *encoded_pairs, uint32_t n_detectors,
                                      uint32_t max_pairs_per_detector, uint32_t n_anchors,
                                      const int64_t *in_offsets, const int32_t *in_ids,

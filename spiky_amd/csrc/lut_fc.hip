@@ -943,6 +943,18 @@ hipError_t launch_wgrad_fc(const FcShape &s, const float *g, const int32_t *idx,
                               int_rescaler, st);
 }
 
+hipError_t launch_wgrad_commit_values(const float *g, uint32_t *cv, uint64_t n, double lr,
+                                      bool int_mode, double int_rescaler, hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    if (int_mode)
+        hipLaunchKernelGGL(k_wgrad_commit_values<true>, dim3(blocks_for(n)), dim3(kBlock), 0, st, g,
+                           cv, n, lr, int_rescaler);
+    else
+        hipLaunchKernelGGL(k_wgrad_commit_values<false>, dim3(blocks_for(n)), dim3(kBlock), 0, st, g,
+                           cv, n, lr, int_rescaler);
+    return hipGetLastError();
+}
+
 hipError_t launch_bucket_samples(const FcShape &s, const int32_t *idx, int32_t *offsets,
                                  int32_t *samples, hipStream_t st) {
     if (s.n_detectors == 0) return hipSuccess;

@@ -78,6 +78,40 @@ hipError_t launch_propagate_tm(const FcShape &s, const float *w, const float *g,
                                const int32_t *min_idx, const int32_t *anchors, float *x_grad,
                                void *scratch, hipStream_t st);
 
+// Commit values of the weight gradient for every (row, output) of g
+// (lut_fc.hip k_wgrad_commit_values).
+hipError_t launch_wgrad_commit_values(const float *g, uint32_t *cv, uint64_t n, double lr,
+                                      bool int_mode, double int_rescaler, hipStream_t st);
+
+// ---- sequence-concat path (lut_seq.hip) ------------------------------------
+struct SeqShape {
+    uint32_t batch;
+    uint32_t seq;          // sequence length S (> 1)
+    uint32_t n_inputs;
+    uint32_t n_outputs;
+    uint32_t n_detectors;
+    uint32_t n_anchors;
+    uint32_t pe_dim;       // positional_dim (0: no positional embedding)
+    uint32_t dgs;
+    uint32_t ogs;
+};
+size_t seq_scratch_bytes(const SeqShape &s, bool backward);
+// check_detectors_seq(_eval) + check_positional_embeddings(_eval) +
+// fill_outputs_fully_connected_seq; md == null selects eval mode.
+hipError_t launch_forward_seq(const SeqShape &s, const float *w, const float *x,
+                              const int32_t *anchors, const float *pe, float *out, int32_t *idx,
+                              int32_t *pidx, float *md, int32_t *mi, float *pmd, int32_t *pmi,
+                              float cmp_eps, bool int_mode, double int_rescaler, void *scratch,
+                              hipStream_t st);
+// propagate_through_detectors_seq_fc + gather_w_gradients_seq_fc; target is the
+// weight gradient (or the weights for the Internal policy, lr folded in), or null.
+hipError_t launch_backward_seq(const SeqShape &s, float *w, const float *g, const int32_t *anchors,
+                               const int32_t *idx, const float *md, const int32_t *mi,
+                               const int32_t *pidx, const float *pmd, const int32_t *pmi,
+                               float *x_grad, float *pe_grad, float *target, double lr,
+                               bool overwrite, bool int_mode, double int_rescaler, void *scratch,
+                               hipStream_t st);
+
 // Zero n floats with a kernel (graph-capture safe, unlike hipMemsetAsync).
 hipError_t launch_zero(float *buf, uint64_t n, hipStream_t st);
 

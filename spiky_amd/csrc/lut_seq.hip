@@ -1,0 +1,893 @@
+// lut_seq.hip -- sequence-concat LUT kernels (LUTTransformer attention) for gfx950.
+//
+// Layouts (caller-owned, as in the reference): x [B][S][I]; idx / md / mi
+// [B][S][T]; positional embeddings [(S-1)][T][Npe]; pidx / pmd / pmi
+// [(S-1)][T]; out / g [B][S][O]; W [T][2^(2Nc+Npe)][O] with row
+// (Q << (Nc+Npe)) | (K << Npe) | PE, where Q is the later position's index,
+// K the earlier one's and PE the index of their distance - 1
+// (lut_runtime_kernels_logic.proto:1807-1904, lut.cu:42).
+//
+// Kernels:
+//   k_check_pe          one thread per (distance, table): sign bits of the
+//                       positional embedding and its min-|value| dimension.
+//   k_seq_pack          idx / mi / md -> one 8-byte record per (t, b, s), so a
+//                       wavefront's walk over positions reads contiguous memory.
+//   k_fill_seq          one wavefront per (sample, later position j, column
+//                       slice): tables in ascending order, pairs i < j summed in
+//                       fp64 and committed once per table -- the reference CPU
+//                       path's order, so the output is bit-identical to it.
+//   k_propagate_seq     fp32 summation: one wavefront per (sample, table, j); for
+//                       8 pairs at a time it reads the main, flipped and
+//                       PE-flipped rows, reduces the dots with a DPP
+//                       reduce-scatter, keeps the Q-flip terms of (b, t, j) in
+//                       registers and adds K-flip and positional terms with fp64
+//                       atomics into small per-(b, t, position) buffers.
+//   k_propagate_seq_exact  int32 summation (and any shape): the reference's own
+//                       decomposition, one thread per (pair, table, output block)
+//                       with sequential block dots and integer payloads, so the
+//                       int32 accumulators are bit-identical.
+//   k_seq_xgrad         x_grad[b][s][anchor] +-= du(b, t, s) for every table.
+//   k_wgrad_seq_lds     one workgroup per (table, Q value, column slice): the
+//                       gradient of that sub-table slice (2^(Nc+Npe) rows x C
+//                       columns, <= 128 KiB) is accumulated in LDS from every
+//                       (b, j) whose Q is that value and written to HBM once.
+#include "lut_kernels.h"
+
+#include <algorithm>
+
+namespace spiky {
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kBlock = 256;
+constexpr int kWPB = kBlock / kWave;
+
+__device__ __forceinline__ uint32_t uniform(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+
+__device__ __forceinline__ int32_t wrap_add(int32_t a, int32_t b) {
+    return (int32_t)((uint32_t)a + (uint32_t)b);
+}
+
+__device__ __forceinline__ bool rounded_greater0(float d, float cmp_eps) {
+    if (cmp_eps == 0.0f) return d > 0.0f;
+    return (fabsf(d) < cmp_eps) ? false : (d > 0.0f);
+}
+
+__device__ __forceinline__ double du_of_margin(float md) {
+    double du = (double)md;
+    double r = 1.0 / (1.0 + fabs(du));
+    return (du > 0) ? r * (0.5 * r) : r * (-0.5 * r);
+}
+
+// DPP lane exchange of an fp64 value.
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const unsigned long long u = (unsigned long long)__double_as_longlong(v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xF, 0xF, false);
+    return __longlong_as_double((long long)(((unsigned long long)(uint32_t)hi << 32) |
+                                            (unsigned long long)(uint32_t)lo));
+}
+
+// Record of one (table, sample, position): x = md bits, y = idx | (mi & 0xff) << 16.
+__device__ __forceinline__ uint32_t rec_idx(uint2 r) { return r.y & 0xFFFFu; }
+__device__ __forceinline__ int32_t rec_mi(uint2 r) {
+    const uint32_t m = (r.y >> 16) & 0xFFu;
+    return m == 0xFFu ? -1 : (int32_t)m;
+}
+__device__ __forceinline__ float rec_md(uint2 r) { return __uint_as_float(r.x); }
+
+// ---------------------------------------------------------------------------
+// check_positional_embeddings(_eval)_logic, proto:1709-1805
+template <bool TRAIN>
+__global__ __launch_bounds__(kBlock) void k_check_pe(const float *__restrict__ pe, uint32_t n_items,
+                                                     uint32_t pe_dim, float cmp_eps,
+                                                     int32_t *__restrict__ pidx,
+                                                     float *__restrict__ pmd,
+                                                     int32_t *__restrict__ pmi) {
+    const uint32_t it = blockIdx.x * kBlock + threadIdx.x;
+    if (it >= n_items) return;
+    const float *v = pe + (size_t)it * pe_dim;
+    int32_t li = 0, mk = -1;
+    float mind = 0.0f;
+    for (uint32_t d = 0; d < pe_dim; d++) {
+        const float x = v[d];
+        if (rounded_greater0(x, cmp_eps)) li |= (1 << d);
+        if (TRAIN && (mk == -1 || fabsf(x) < fabsf(mind))) {
+            mind = x;
+            mk = (int32_t)d;
+        }
+    }
+    pidx[it] = li;
+    if (TRAIN) {
+        pmd[it] = mind;
+        pmi[it] = mk;
+    }
+}
+
+// pack[t][b][s] from idx / md / mi [b][s][t] (md / mi may be null: eval).
+__global__ __launch_bounds__(kBlock) void k_seq_pack(const int32_t *__restrict__ idx,
+                                                     const float *__restrict__ md,
+                                                     const int32_t *__restrict__ mi,
+                                                     uint2 *__restrict__ pack, uint32_t n_rows,
+                                                     uint32_t n_detectors) {
+    __shared__ uint2 tile[64][65];
+    const uint32_t tb = blockIdx.x * 64;  // tables
+    const uint32_t rb = blockIdx.y * 64;  // rows b*S + s
+    const uint32_t tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    for (uint32_t r = ty; r < 64; r += 4) {
+        const uint32_t row = rb + r, t = tb + tx;
+        if (row < n_rows && t < n_detectors) {
+            const size_t o = (size_t)row * n_detectors + t;
+            const uint32_t m = mi ? (uint32_t)(mi[o] < 0 ? 0xFF : mi[o] & 0xFF) : 0xFFu;
+            tile[r][tx] = make_uint2(md ? __float_as_uint(md[o]) : 0u,
+                                     ((uint32_t)idx[o] & 0xFFFFu) | (m << 16));
+        }
+    }
+    __syncthreads();
+    for (uint32_t r = ty; r < 64; r += 4) {
+        const uint32_t t = tb + r, row = rb + tx;
+        if (row < n_rows && t < n_detectors) pack[(size_t)t * n_rows + row] = tile[tx][r];
+    }
+}
+
+// ppack[t][d] from pidx / pmd / pmi [d][t]; all zero (PE index 0) without PE.
+__global__ __launch_bounds__(kBlock) void k_seq_pack_pe(const int32_t *__restrict__ pidx,
+                                                        const float *__restrict__ pmd,
+                                                        const int32_t *__restrict__ pmi,
+                                                        uint2 *__restrict__ ppack, uint32_t n_dist,
+                                                        uint32_t n_detectors) {
+    const uint32_t it = blockIdx.x * kBlock + threadIdx.x;
+    if (it >= n_dist * n_detectors) return;
+    const uint32_t t = it / n_dist, d = it % n_dist;
+    uint2 r = make_uint2(0u, 0xFFu << 16);
+    if (pidx) {
+        const size_t o = (size_t)d * n_detectors + t;
+        const uint32_t m = pmi ? (uint32_t)(pmi[o] < 0 ? 0xFF : pmi[o] & 0xFF) : 0xFFu;
+        r = make_uint2(pmd ? __float_as_uint(pmd[o]) : 0u, ((uint32_t)pidx[o] & 0xFFFFu) | (m << 16));
+    }
+    ppack[it] = r;
+}
+
+// ---------------------------------------------------------------------------
+// fill_outputs_fully_connected_seq_logic (proto:1807-1904), re-scheduled.
+template <int VEC>
+struct Ld;
+template <>
+struct Ld<1> {
+    __device__ static void f(const float *p, float *v) { v[0] = p[0]; }
+};
+template <>
+struct Ld<2> {
+    __device__ static void f(const float *p, float *v) {
+        const float2 q = *reinterpret_cast<const float2 *>(p);
+        v[0] = q.x;
+        v[1] = q.y;
+    }
+};
+template <>
+struct Ld<4> {
+    __device__ static void f(const float *p, float *v) {
+        const float4 q = *reinterpret_cast<const float4 *>(p);
+        v[0] = q.x;
+        v[1] = q.y;
+        v[2] = q.z;
+        v[3] = q.w;
+    }
+};
+
+template <int VEC, bool INT_MODE>
+__global__ __launch_bounds__(kBlock) void k_fill_seq(
+    const float *__restrict__ w, const uint2 *__restrict__ pack, const uint2 *__restrict__ ppack,
+    float *__restrict__ out, uint32_t batch, uint32_t seq, uint32_t n_outputs,
+    uint32_t n_detectors, uint32_t n_anchors, uint32_t pe_dim, uint32_t n_slices,
+    double int_rescaler) {
+    const uint32_t lane = threadIdx.x & (kWave - 1);
+    const uint32_t wave = uniform(threadIdx.x / kWave);
+    const uint32_t slice = blockIdx.x % n_slices;
+    const uint32_t unit = (blockIdx.x / n_slices) * kWPB + wave;
+    const uint32_t per_b = seq - 1;
+    const uint32_t b = unit / per_b;
+    if (b >= batch) return;
+    const uint32_t j = seq - 1 - unit % per_b;  // long rows first
+    const uint32_t c = (slice * kWave + lane) * VEC;
+    const bool active = c < n_outputs;
+    const uint32_t cc = active ? c : 0u;
+    const uint32_t n_rows = batch * seq;
+    const uint32_t sub_rows = 1u << (n_anchors + pe_dim);  // rows per (table, Q)
+    float *ob = out + ((size_t)b * seq + j) * n_outputs + c;
+    float run[VEC];
+    int32_t irun[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; v++) {
+        run[v] = 0.0f;
+        irun[v] = 0;
+        if (active) {
+            if (INT_MODE)
+                irun[v] = __float_as_int(ob[v]);
+            else
+                run[v] = ob[v];
+        }
+    }
+    for (uint32_t t = 0; t < n_detectors; t++) {
+        const uint2 *kp = pack + (size_t)t * n_rows + (size_t)b * seq;
+        const uint2 *pp = ppack + (size_t)t * (seq - 1);
+        const uint32_t q = rec_idx(kp[j]);
+        const float *sub = w + ((size_t)t * (1u << n_anchors) + q) * sub_rows * n_outputs + cc;
+        double acc[VEC];
+#pragma unroll
+        for (int v = 0; v < VEC; v++) acc[v] = 0.0;
+        for (uint32_t i0 = 0; i0 < j; i0 += 8) {
+            const uint32_t n = min(8u, j - i0);
+            float vals[8][VEC];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const uint32_t i = i0 + min((uint32_t)u, n - 1);
+                const uint32_t row = (rec_idx(kp[i]) << pe_dim) | rec_idx(pp[j - i - 1]);
+                Ld<VEC>::f(sub + (size_t)(row & (sub_rows - 1)) * n_outputs, vals[u]);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                if ((uint32_t)u < n) {
+#pragma unroll
+                    for (int v = 0; v < VEC; v++) acc[v] += (double)vals[u][v];
+                }
+            }
+        }
+        if (j == 0) continue;
+#pragma unroll
+        for (int v = 0; v < VEC; v++) {
+            if (INT_MODE)
+                irun[v] = wrap_add(irun[v], (int32_t)(acc[v] * kDenom32 * int_rescaler));
+            else
+                run[v] += (float)acc[v];
+        }
+    }
+    if (!active) return;
+#pragma unroll
+    for (int v = 0; v < VEC; v++)
+        ob[v] = INT_MODE ? (float)(((double)irun[v] * kDenom32Reciproc) / int_rescaler) : run[v];
+}
+
+// ---------------------------------------------------------------------------
+// propagate_through_detectors_seq_fc_logic (proto:3629-3835), fp32 summation.
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppXor1 = 0xB1;
+constexpr int kDppXor2 = 0x4E;
+
+template <int CTRL>
+__device__ __forceinline__ void rs16_step(double (&v)[16], int m, bool upper) {
+    for (int jj = 0; jj < m; jj++) {
+        const double send = upper ? v[jj] : v[m + jj];
+        const double keep = upper ? v[m + jj] : v[jj];
+        v[jj] = keep + dpp_f64<CTRL>(send);
+    }
+}
+
+// 16 items per lane, the 8 lanes of a group hold column pieces: afterwards lane
+// l holds the group sums of items 2u, 2u+1 with u = 4*(l>=4) + 2*(l&1) + ((l>>1)&1)
+// in v[0], v[1].
+__device__ __forceinline__ uint32_t rs_pair(uint32_t l) {
+    return 4u * (l >= 4 ? 1u : 0u) + 2u * (l & 1u) + ((l >> 1) & 1u);
+}
+
+template <int NJ>
+__global__ __launch_bounds__(kBlock) void k_propagate_seq(
+    const float *__restrict__ w, const float *__restrict__ g, const uint2 *__restrict__ pack,
+    const uint2 *__restrict__ ppack, double *__restrict__ dq, double *__restrict__ dk,
+    double *__restrict__ dpe, uint32_t batch, uint32_t seq, uint32_t n_outputs,
+    uint32_t n_detectors, uint32_t n_anchors, uint32_t pe_dim) {
+    const uint32_t lane = threadIdx.x & (kWave - 1);
+    const uint32_t wave = uniform(threadIdx.x / kWave);
+    const uint32_t unit = blockIdx.x * kWPB + wave;
+    const uint32_t per_bt = seq - 1;
+    const uint32_t bt = unit / per_bt;
+    if (bt >= batch * n_detectors) return;
+    const uint32_t j = seq - 1 - unit % per_bt;  // long rows first
+    const uint32_t b = bt / n_detectors, t = bt % n_detectors;
+    const uint32_t n_rows = batch * seq;
+    const uint32_t kbits = n_anchors + pe_dim;
+    const uint32_t pmask = (1u << pe_dim) - 1;
+    const uint2 *kp = pack + (size_t)t * n_rows + (size_t)b * seq;
+    const uint2 *pp = ppack + (size_t)t * (seq - 1);
+    const float *wt = w + (size_t)t * (1u << (n_anchors + kbits)) * n_outputs;
+
+    float gv[NJ][4];
+    bool act[NJ];
+#pragma unroll
+    for (int jj = 0; jj < NJ; jj++) {
+        const uint32_t c = (jj * kWave + lane) * 4;
+        act[jj] = c < n_outputs;
+        float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (act[jj]) q = *reinterpret_cast<const float4 *>(g + ((size_t)b * seq + j) * n_outputs + c);
+        gv[jj][0] = q.x;
+        gv[jj][1] = q.y;
+        gv[jj][2] = q.z;
+        gv[jj][3] = q.w;
+    }
+    const uint2 qr = kp[j];
+    const uint32_t Q = rec_idx(qr);
+    const int32_t qm = rec_mi(qr);
+    const float qd = rec_md(qr);
+    const uint32_t l8 = lane & 7;
+    const uint32_t my_u = rs_pair(l8);
+    double q_acc = 0.0;
+
+    for (uint32_t i0 = 0; i0 < j; i0 += 8) {
+        const uint32_t n = min(8u, j - i0);
+        double items[16];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const uint32_t i = i0 + min((uint32_t)u, n - 1);
+            const uint2 kr = kp[i];
+            const uint2 pr = pp[j - i - 1];
+            const uint32_t K = rec_idx(kr), P = rec_idx(pr) & pmask;
+            const int32_t km = rec_mi(kr), pm = rec_mi(pr);
+            const float kd = rec_md(kr), pdl = rec_md(pr);
+            const bool qflip = fabsf(qd) < fabsf(kd);
+            const int32_t fm = qflip ? qm : km;
+            const uint32_t main_row = (Q << kbits) | (K << pe_dim) | P;
+            uint32_t alt_row = main_row;
+            if (fm >= 0) alt_row = qflip ? (main_row ^ (1u << (fm + kbits))) : (main_row ^ (1u << (fm + pe_dim)));
+            const bool peflip = pe_dim > 0 && pm >= 0 && fabsf(pdl) < fabsf(qd) && fabsf(pdl) < fabsf(kd);
+            const uint32_t pe_row = peflip ? (main_row ^ (1u << pm)) : main_row;
+            double d1 = 0.0, d2 = 0.0;
+#pragma unroll
+            for (int jj = 0; jj < NJ; jj++) {
+                if (!act[jj]) continue;
+                const uint32_t c = (jj * kWave + lane) * 4;
+                const float4 m = *reinterpret_cast<const float4 *>(wt + (size_t)main_row * n_outputs + c);
+                const float4 a = *reinterpret_cast<const float4 *>(wt + (size_t)alt_row * n_outputs + c);
+                d1 += ((double)m.x - (double)a.x) * (double)gv[jj][0];
+                d1 += ((double)m.y - (double)a.y) * (double)gv[jj][1];
+                d1 += ((double)m.z - (double)a.z) * (double)gv[jj][2];
+                d1 += ((double)m.w - (double)a.w) * (double)gv[jj][3];
+                if (peflip) {
+                    const float4 e = *reinterpret_cast<const float4 *>(wt + (size_t)pe_row * n_outputs + c);
+                    d2 += ((double)m.x - (double)e.x) * (double)gv[jj][0];
+                    d2 += ((double)m.y - (double)e.y) * (double)gv[jj][1];
+                    d2 += ((double)m.z - (double)e.z) * (double)gv[jj][2];
+                    d2 += ((double)m.w - (double)e.w) * (double)gv[jj][3];
+                }
+            }
+            items[2 * u] = d1;
+            items[2 * u + 1] = d2;
+        }
+        // reduce-scatter inside each 8-lane group, then sum the 8 groups
+        rs16_step<kDppHalfMirror>(items, 8, l8 >= 4);
+        rs16_step<kDppXor1>(items, 4, (l8 & 1) != 0);
+        rs16_step<kDppXor2>(items, 2, ((l8 >> 1) & 1) != 0);
+#pragma unroll
+        for (int s = 8; s < kWave; s <<= 1) {
+            items[0] += __shfl_xor(items[0], s, kWave);
+            items[1] += __shfl_xor(items[1], s, kWave);
+        }
+        // lanes 0..7 hold the totals of pair my_u
+        if (lane < 8 && my_u < n) {
+            const uint32_t i = i0 + my_u;
+            const uint2 kr = kp[i];
+            const uint2 pr = pp[j - i - 1];
+            const int32_t km = rec_mi(kr), pm = rec_mi(pr);
+            const float kd = rec_md(kr), pdl = rec_md(pr);
+            const bool qflip = fabsf(qd) < fabsf(kd);
+            const int32_t fm = qflip ? qm : km;
+            if (fm >= 0) {
+                const double du = du_of_margin(qflip ? qd : kd) * items[0];
+                if (qflip)
+                    q_acc += du;
+                else
+                    atomicAdd(dk + ((size_t)b * n_detectors + t) * seq + i, du);
+            }
+            if (pe_dim > 0 && pm >= 0 && fabsf(pdl) < fabsf(qd) && fabsf(pdl) < fabsf(kd))
+                atomicAdd(dpe + ((size_t)(j - i - 1) * n_detectors + t) * pe_dim + pm,
+                          du_of_margin(pdl) * items[1]);
+        }
+    }
+    // the wave's Q-flip total for (b, t, j): lanes 0..7 hold the pieces
+    double s = lane < 8 ? q_acc : 0.0;
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) s += __shfl_xor(s, o, kWave);
+    if (lane == 0) dq[((size_t)b * n_detectors + t) * seq + j] = s;
+}
+
+// Exact decomposition: one thread per (b, t, pair, output block).
+template <bool INT_MODE>
+__global__ __launch_bounds__(kBlock) void k_propagate_seq_exact(
+    const float *__restrict__ w, const float *__restrict__ g, const uint2 *__restrict__ pack,
+    const uint2 *__restrict__ ppack, const int2 *__restrict__ anchors, float *__restrict__ x_grad,
+    float *__restrict__ pe_grad, uint32_t batch, uint32_t seq, uint32_t n_inputs,
+    uint32_t n_outputs, uint32_t n_detectors, uint32_t n_anchors, uint32_t pe_dim, uint32_t ogs,
+    uint32_t n_ob, uint64_t n_items, double int_rescaler) {
+    const uint64_t item = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (item >= n_items) return;
+    const uint64_t n_pairs = (uint64_t)seq * (seq - 1) / 2;
+    const uint32_t ob = (uint32_t)(item % n_ob);
+    const uint64_t r1 = item / n_ob;
+    const uint64_t p = r1 % n_pairs;
+    const uint64_t r2 = r1 / n_pairs;
+    const uint32_t t = (uint32_t)(r2 % n_detectors);
+    const uint32_t b = (uint32_t)(r2 / n_detectors);
+    // pair p -> (i < j): j is the largest with j*(j-1)/2 <= p
+    uint32_t j = (uint32_t)((1.0 + sqrt(1.0 + 8.0 * (double)p)) * 0.5);
+    while ((uint64_t)j * (j - 1) / 2 > p) j--;
+    while ((uint64_t)(j + 1) * j / 2 <= p) j++;
+    const uint32_t i = (uint32_t)(p - (uint64_t)j * (j - 1) / 2);
+    const uint32_t n_rows = batch * seq;
+    const uint32_t kbits = n_anchors + pe_dim;
+    const uint32_t pmask = (1u << pe_dim) - 1;
+    const uint2 *kp = pack + (size_t)t * n_rows + (size_t)b * seq;
+    const uint2 qr = kp[j], kr = kp[i];
+    const uint2 pr = ppack[(size_t)t * (seq - 1) + (j - i - 1)];
+    const uint32_t Q = rec_idx(qr), K = rec_idx(kr), P = rec_idx(pr) & pmask;
+    const int32_t qm = rec_mi(qr), km = rec_mi(kr), pm = rec_mi(pr);
+    const float qd = rec_md(qr), kd = rec_md(kr), pdl = rec_md(pr);
+    const bool qflip = fabsf(qd) < fabsf(kd);
+    const int32_t fm = qflip ? qm : km;
+    const uint32_t main_row = (Q << kbits) | (K << pe_dim) | P;
+    const uint32_t alt_row = fm < 0 ? main_row
+                                    : (qflip ? (main_row ^ (1u << (fm + kbits)))
+                                             : (main_row ^ (1u << (fm + pe_dim))));
+    const float *wt = w + (size_t)t * (1u << (n_anchors + kbits)) * n_outputs;
+    const float *gj = g + ((size_t)b * seq + j) * n_outputs;
+    const uint32_t o0 = ob * ogs, o1 = min(o0 + ogs, n_outputs);
+    double ms = 0.0, as = 0.0;
+    for (uint32_t o = o0; o < o1; o++) {
+        const double gg = (double)gj[o];
+        ms += (double)wt[(size_t)main_row * n_outputs + o] * gg;
+        as += (double)wt[(size_t)alt_row * n_outputs + o] * gg;
+    }
+    if (fm >= 0) {
+        const double du = du_of_margin(qflip ? qd : kd) * (ms - as);
+        if (fabs(du) > kEps) {
+            const int2 a = anchors[(size_t)t * n_anchors + fm];
+            if ((uint32_t)a.x < n_inputs && (uint32_t)a.y < n_inputs) {
+                float *xg = x_grad + ((size_t)b * seq + (qflip ? j : i)) * n_inputs;
+                if (INT_MODE) {
+                    const int32_t d = (int32_t)(du * kDenom32 * int_rescaler);
+                    atomicAdd(reinterpret_cast<int32_t *>(xg + a.x), d);
+                    atomicAdd(reinterpret_cast<int32_t *>(xg + a.y), (int32_t)(0u - (uint32_t)d));
+                } else {
+                    unsafeAtomicAdd(xg + a.x, (float)du);
+                    unsafeAtomicAdd(xg + a.y, (float)(-du));
+                }
+            }
+        }
+    }
+    if (pe_dim > 0 && pm >= 0 && fabsf(pdl) < fabsf(qd) && fabsf(pdl) < fabsf(kd)) {
+        const uint32_t pe_row = main_row ^ (1u << pm);
+        double es = 0.0;
+        for (uint32_t o = o0; o < o1; o++)
+            es += (double)wt[(size_t)pe_row * n_outputs + o] * (double)gj[o];
+        const double dpe = du_of_margin(pdl) * (ms - es);
+        float *dst = pe_grad + ((size_t)(j - i - 1) * n_detectors + t) * pe_dim + pm;
+        if (INT_MODE)
+            atomicAdd(reinterpret_cast<int32_t *>(dst), (int32_t)(dpe * kDenom32 * int_rescaler));
+        else
+            unsafeAtomicAdd(dst, (float)dpe);
+    }
+}
+
+// x_grad[b][s][a1] += du, [a2] -= du with du = dq + dk of (b, t, s) and the
+// min anchor of (b, s, t) (both the Q flips at s and the K flips at s flip
+// that anchor), dropped unless |du| > EPS.
+__global__ __launch_bounds__(kBlock) void k_seq_xgrad(const double *__restrict__ dq,
+                                                      const double *__restrict__ dk,
+                                                      const uint2 *__restrict__ pack,
+                                                      const int2 *__restrict__ anchors,
+                                                      float *__restrict__ x_grad, uint32_t batch,
+                                                      uint32_t seq, uint32_t n_inputs,
+                                                      uint32_t n_detectors, uint32_t n_anchors) {
+    const uint64_t it = (uint64_t)blockIdx.x * kBlock + threadIdx.x;  // (b, t, s)
+    const uint64_t n = (uint64_t)batch * n_detectors * seq;
+    if (it >= n) return;
+    const uint32_t s = (uint32_t)(it % seq);
+    const uint32_t t = (uint32_t)((it / seq) % n_detectors);
+    const uint32_t b = (uint32_t)(it / ((uint64_t)seq * n_detectors));
+    const double du = dq[it] + dk[it];
+    if (!(fabs(du) > kEps)) return;
+    const int32_t m = rec_mi(pack[(size_t)t * batch * seq + (size_t)b * seq + s]);
+    if (m < 0 || (uint32_t)m >= n_anchors) return;
+    const int2 a = anchors[(size_t)t * n_anchors + m];
+    if ((uint32_t)a.x >= n_inputs || (uint32_t)a.y >= n_inputs) return;
+    float *xg = x_grad + ((size_t)b * seq + s) * n_inputs;
+    unsafeAtomicAdd(xg + a.x, (float)du);
+    unsafeAtomicAdd(xg + a.y, (float)(-du));
+}
+
+// pe_grad (+)= fp32(accumulated fp64 terms).
+__global__ __launch_bounds__(kBlock) void k_seq_pe_commit(const double *__restrict__ dpe,
+                                                          float *__restrict__ pe_grad, uint32_t n) {
+    const uint32_t i = blockIdx.x * kBlock + threadIdx.x;
+    if (i < n) pe_grad[i] = (float)((double)pe_grad[i] + dpe[i]);
+}
+
+__global__ __launch_bounds__(kBlock) void k_zero64(double *__restrict__ p, uint64_t n) {
+    const uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (i < n) p[i] = 0.0;
+}
+
+// ---------------------------------------------------------------------------
+// gather_w_gradients_seq_fc (proto:3944-4304), one workgroup per (table t,
+// Q value q, column slice).  cv holds the commit values of every (b, s)
+// (k_wgrad_commit_values); samples / offsets are the (b, s) rows of each table
+// bucketed by their index (k_bucket_samples).
+constexpr int kSeqWgThreads = 1024;
+constexpr int kSeqWgAccWords = 32768;  // 128 KiB accumulator
+constexpr int kSeqWgKeys = 8192;       // K indices of up to 8192 (b, s) rows at a time
+constexpr int kSeqWgPe = 1024;
+
+template <bool INT_MODE, bool OVERWRITE>
+__global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_lds(
+    const uint32_t *__restrict__ cv, const int32_t *__restrict__ offsets,
+    const int32_t *__restrict__ samples, const uint2 *__restrict__ pack,
+    const uint2 *__restrict__ ppack, float *__restrict__ target, uint32_t batch, uint32_t seq,
+    uint32_t n_outputs, uint32_t n_detectors, uint32_t n_anchors, uint32_t pe_dim,
+    uint32_t cols, uint32_t n_slices, double int_rescaler) {
+    __shared__ uint32_t acc[kSeqWgAccWords];
+    __shared__ uint16_t ktab[kSeqWgKeys];
+    __shared__ uint16_t ptab[kSeqWgPe];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t slice = blockIdx.x % n_slices;
+    const uint32_t tq = blockIdx.x / n_slices;
+    const uint32_t n_q = 1u << n_anchors;
+    const uint32_t t = tq / n_q, q = tq % n_q;
+    const uint32_t sub_rows = 1u << (n_anchors + pe_dim);
+    const uint32_t pmask = (1u << pe_dim) - 1;
+    const uint32_t n_rows = batch * seq;
+    const uint32_t col0 = slice * cols;
+    const uint32_t lanes_per_item = cols / 4;
+    const uint32_t items_per_pass = kSeqWgThreads / lanes_per_item;
+    const uint32_t my_item = tid / lanes_per_item;
+    const uint32_t my_q4 = tid % lanes_per_item;
+    const uint32_t c = col0 + my_q4 * 4;
+    const bool active = c < n_outputs;
+    for (uint32_t k = tid; k < sub_rows * cols; k += kSeqWgThreads) acc[k] = 0u;
+    for (uint32_t d = tid; d + 1 < seq; d += kSeqWgThreads)
+        ptab[d] = (uint16_t)(rec_idx(ppack[(size_t)t * (seq - 1) + d]) & pmask);
+    const int32_t *off_t = offsets + (size_t)t * (n_q + 1);
+    const int32_t beg = off_t[q], end = off_t[q + 1];
+    const int32_t *smp = samples + (size_t)t * n_rows;
+    const uint2 *kp = pack + (size_t)t * n_rows;
+    const uint32_t rows_per_chunk = (kSeqWgKeys / seq) * seq;
+    // the bucket is ascending in (b, s): walk it in chunks of whole samples
+    int32_t k0 = beg;
+    for (uint32_t r0 = 0; r0 < n_rows && k0 < end; r0 += rows_per_chunk) {
+        const uint32_t r1 = min(r0 + rows_per_chunk, n_rows);
+        __syncthreads();
+        for (uint32_t r = r0 + tid; r < r1; r += kSeqWgThreads) ktab[r - r0] = (uint16_t)rec_idx(kp[r]);
+        __syncthreads();
+        // first bucket position at or past row r1 (uniform binary search)
+        int32_t lo = k0, hi = end;
+        while (lo < hi) {
+            const int32_t mid = lo + (hi - lo) / 2;
+            if ((uint32_t)smp[mid] < r1) lo = mid + 1; else hi = mid;
+        }
+        const int32_t k1 = lo;
+        for (int32_t kb = k0; kb < k1; kb += (int32_t)items_per_pass) {
+            const int32_t k = kb + (int32_t)my_item;
+            if (k >= k1 || !active) continue;
+            const uint32_t r = (uint32_t)smp[k];
+            const uint32_t bl = r / seq - r0 / seq, j = r % seq;
+            const uint4 v = *reinterpret_cast<const uint4 *>(cv + (size_t)r * n_outputs + c);
+            const uint16_t *kt = ktab + (size_t)bl * seq;
+            for (uint32_t i = 0; i < j; i++) {
+                const uint32_t row = ((uint32_t)kt[i] << pe_dim) | ptab[j - i - 1];
+                uint32_t *a = acc + (row & (sub_rows - 1)) * cols + my_q4 * 4;
+                if (INT_MODE) {
+                    atomicAdd(a + 0, v.x);
+                    atomicAdd(a + 1, v.y);
+                    atomicAdd(a + 2, v.z);
+                    atomicAdd(a + 3, v.w);
+                } else {
+                    atomicAdd(reinterpret_cast<float *>(a + 0), __uint_as_float(v.x));
+                    atomicAdd(reinterpret_cast<float *>(a + 1), __uint_as_float(v.y));
+                    atomicAdd(reinterpret_cast<float *>(a + 2), __uint_as_float(v.z));
+                    atomicAdd(reinterpret_cast<float *>(a + 3), __uint_as_float(v.w));
+                }
+            }
+        }
+        k0 = k1;
+    }
+    __syncthreads();
+    // write the sub-table slice: rows q*sub_rows .. of table t
+    float *dst = target + ((size_t)t * n_q + q) * sub_rows * n_outputs;
+    for (uint32_t k = tid; k < sub_rows * lanes_per_item; k += kSeqWgThreads) {
+        const uint32_t row = k / lanes_per_item, qq = k % lanes_per_item;
+        const uint32_t cc = col0 + qq * 4;
+        if (cc >= n_outputs) continue;
+        const uint32_t *a = acc + row * cols + qq * 4;
+        float *p = dst + (size_t)row * n_outputs + cc;
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            if (INT_MODE) {
+                int32_t iv = (int32_t)a[e];
+                if (!OVERWRITE) iv = wrap_add(iv, __float_as_int(p[e]));
+                o[e] = (float)(((double)iv * kDenom32Reciproc) / int_rescaler);
+            } else {
+                o[e] = __uint_as_float(a[e]);
+                if (!OVERWRITE) o[e] = p[e] + o[e];
+            }
+        }
+        *reinterpret_cast<float4 *>(p) = make_float4(o[0], o[1], o[2], o[3]);
+    }
+}
+
+// Fallback weight gradient: one thread per (b, t, j, output) with global atomics.
+template <bool INT_MODE>
+__global__ __launch_bounds__(kBlock) void k_wgrad_seq_atomic(
+    const uint32_t *__restrict__ cv, const uint2 *__restrict__ pack, const uint2 *__restrict__ ppack,
+    float *__restrict__ target, uint32_t batch, uint32_t seq, uint32_t n_outputs,
+    uint32_t n_detectors, uint32_t n_anchors, uint32_t pe_dim, uint64_t n_items) {
+    const uint64_t it = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (it >= n_items) return;
+    const uint32_t o = (uint32_t)(it % n_outputs);
+    const uint64_t r = it / n_outputs;
+    const uint32_t j = (uint32_t)(r % seq);
+    const uint32_t t = (uint32_t)((r / seq) % n_detectors);
+    const uint32_t b = (uint32_t)(r / ((uint64_t)seq * n_detectors));
+    const uint32_t n_rows = batch * seq;
+    const uint32_t kbits = n_anchors + pe_dim;
+    const uint32_t pmask = (1u << pe_dim) - 1;
+    const uint2 *kp = pack + (size_t)t * n_rows + (size_t)b * seq;
+    const uint32_t Q = rec_idx(kp[j]);
+    const uint32_t v = cv[((size_t)b * seq + j) * n_outputs + o];
+    float *wt = target + (size_t)t * (1u << (n_anchors + kbits)) * n_outputs;
+    for (uint32_t i = 0; i < j; i++) {
+        const uint32_t row = (Q << kbits) | (rec_idx(kp[i]) << pe_dim) |
+                             (rec_idx(ppack[(size_t)t * (seq - 1) + (j - i - 1)]) & pmask);
+        float *p = wt + (size_t)row * n_outputs + o;
+        if (INT_MODE)
+            atomicAdd(reinterpret_cast<int32_t *>(p), (int32_t)v);
+        else
+            unsafeAtomicAdd(p, __uint_as_float(v));
+    }
+}
+
+uint32_t blocks_for(uint64_t n) { return (uint32_t)((n + kBlock - 1) / kBlock); }
+
+uint32_t seq_vec(uint32_t n_outputs) {
+    if (n_outputs % 4 == 0 && n_outputs >= 64u * 4u * 4u) return 4;
+    if (n_outputs % 2 == 0 && n_outputs >= 64u * 2u * 4u) return 2;
+    return 1;
+}
+
+// Columns of a weight-gradient LDS slice (0: the LDS path does not apply).
+uint32_t seq_wg_cols(const SeqShape &s) {
+    const uint64_t sub_rows = 1ull << (s.n_anchors + s.pe_dim);
+    if (s.n_outputs % 4 != 0 || s.seq > (uint32_t)kSeqWgKeys || s.seq - 1 > (uint32_t)kSeqWgPe ||
+        s.n_anchors > 12)
+        return 0;
+    uint32_t cols = 32;
+    while (cols >= 4 && sub_rows * cols > (uint64_t)kSeqWgAccWords) cols /= 2;
+    if (cols < 4) return 0;
+    while (cols > 4 && cols / 2 >= s.n_outputs) cols /= 2;
+    return cols;
+}
+
+}  // namespace
+
+// scratch: pack [T][B*S] | ppack [T][S-1] | dq, dk [B][T][S] f64 | dpe [(S-1)][T][Npe] f64 |
+//          bucket offsets [T][2^Nc+1] | samples [T][B*S] | commit values [B*S][O]
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+size_t seq_scratch_bytes(const SeqShape &s, bool backward) {
+    const size_t rows = (size_t)s.batch * s.seq;
+    size_t n = align256(rows * s.n_detectors * 8) + align256((size_t)s.n_detectors * (s.seq - 1) * 8);
+    if (!backward) return n;
+    n += 2 * align256(rows * s.n_detectors * 8);
+    n += align256((size_t)(s.seq - 1) * s.n_detectors * std::max<uint32_t>(s.pe_dim, 1) * 8);
+    n += align256((size_t)s.n_detectors * ((1u << s.n_anchors) + 1) * 4);
+    n += align256((size_t)s.n_detectors * rows * 4);
+    n += align256(rows * s.n_outputs * 4);
+    return n;
+}
+
+hipError_t launch_forward_seq(const SeqShape &s, const float *w, const float *x,
+                              const int32_t *anchors, const float *pe, float *out, int32_t *idx,
+                              int32_t *pidx, float *md, int32_t *mi, float *pmd, int32_t *pmi,
+                              float cmp_eps, bool int_mode, double int_rescaler, void *scratch,
+                              hipStream_t st) {
+    const uint32_t rows = s.batch * s.seq;
+    FcShape fs{};
+    fs.batch = rows;
+    fs.n_inputs = s.n_inputs;
+    fs.n_outputs = s.n_outputs;
+    fs.n_detectors = s.n_detectors;
+    fs.n_anchors = s.n_anchors;
+    fs.n_entries = 1u << s.n_anchors;
+    fs.dgs = s.dgs;
+    fs.ogs = s.ogs;
+    hipError_t e = launch_check_detectors(fs, x, anchors, cmp_eps, idx, md, mi, st);
+    if (e != hipSuccess) return e;
+    const uint32_t n_pe = (s.seq - 1) * s.n_detectors;
+    if (s.pe_dim > 0) {
+        if (md)
+            hipLaunchKernelGGL(k_check_pe<true>, dim3(blocks_for(n_pe)), dim3(kBlock), 0, st, pe,
+                               n_pe, s.pe_dim, cmp_eps, pidx, pmd, pmi);
+        else
+            hipLaunchKernelGGL(k_check_pe<false>, dim3(blocks_for(n_pe)), dim3(kBlock), 0, st, pe,
+                               n_pe, s.pe_dim, cmp_eps, pidx, (float *)nullptr, (int32_t *)nullptr);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    uint8_t *sp = reinterpret_cast<uint8_t *>(scratch);
+    uint2 *pack = reinterpret_cast<uint2 *>(sp);
+    uint2 *ppack = reinterpret_cast<uint2 *>(sp + align256((size_t)rows * s.n_detectors * 8));
+    hipLaunchKernelGGL(k_seq_pack, dim3((s.n_detectors + 63) / 64, (rows + 63) / 64), dim3(kBlock),
+                       0, st, idx, (const float *)nullptr, (const int32_t *)nullptr, pack, rows,
+                       s.n_detectors);
+    hipLaunchKernelGGL(k_seq_pack_pe, dim3(blocks_for(n_pe)), dim3(kBlock), 0, st,
+                       s.pe_dim > 0 ? pidx : (const int32_t *)nullptr, (const float *)nullptr,
+                       (const int32_t *)nullptr, ppack, s.seq - 1, s.n_detectors);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const uint32_t vec = seq_vec(s.n_outputs);
+    const uint32_t n_slices = (s.n_outputs + kWave * vec - 1) / (kWave * vec);
+    const uint64_t units = (uint64_t)s.batch * (s.seq - 1);
+    const uint64_t grid = (uint64_t)n_slices * ((units + kWPB - 1) / kWPB);
+    if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
+#define SPIKY_FSEQ(V, IM)                                                                         \
+    hipLaunchKernelGGL((k_fill_seq<V, IM>), dim3((uint32_t)grid), dim3(kBlock), 0, st, w, pack,    \
+                       ppack, out, s.batch, s.seq, s.n_outputs, s.n_detectors, s.n_anchors,        \
+                       s.pe_dim, n_slices, int_rescaler)
+    switch (vec) {
+        case 4: if (int_mode) SPIKY_FSEQ(4, true); else SPIKY_FSEQ(4, false); break;
+        case 2: if (int_mode) SPIKY_FSEQ(2, true); else SPIKY_FSEQ(2, false); break;
+        default: if (int_mode) SPIKY_FSEQ(1, true); else SPIKY_FSEQ(1, false); break;
+    }
+#undef SPIKY_FSEQ
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    // position 0 has no earlier token; in int mode its int32 accumulator still
+    // needs the epilogue
+    if (int_mode) {
+        for (uint32_t b = 0; b < s.batch; b++) {
+            e = launch_convert_i2f(out + (size_t)b * s.seq * s.n_outputs, s.n_outputs, int_rescaler, st);
+            if (e != hipSuccess) return e;
+        }
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_backward_seq(const SeqShape &s, float *w, const float *g, const int32_t *anchors,
+                               const int32_t *idx, const float *md, const int32_t *mi,
+                               const int32_t *pidx, const float *pmd, const int32_t *pmi,
+                               float *x_grad, float *pe_grad, float *target, double lr,
+                               bool overwrite, bool int_mode, double int_rescaler, void *scratch,
+                               hipStream_t st) {
+    const uint32_t rows = s.batch * s.seq;
+    const uint32_t n_pe = (s.seq - 1) * s.n_detectors;
+    uint8_t *sp = reinterpret_cast<uint8_t *>(scratch);
+    size_t off = 0;
+    uint2 *pack = reinterpret_cast<uint2 *>(sp + off);
+    off += align256((size_t)rows * s.n_detectors * 8);
+    uint2 *ppack = reinterpret_cast<uint2 *>(sp + off);
+    off += align256((size_t)s.n_detectors * (s.seq - 1) * 8);
+    double *dq = reinterpret_cast<double *>(sp + off);
+    off += align256((size_t)rows * s.n_detectors * 8);
+    double *dk = reinterpret_cast<double *>(sp + off);
+    off += align256((size_t)rows * s.n_detectors * 8);
+    double *dpe = reinterpret_cast<double *>(sp + off);
+    const size_t n_dpe = (size_t)n_pe * std::max<uint32_t>(s.pe_dim, 1);
+    off += align256(n_dpe * 8);
+    int32_t *offsets = reinterpret_cast<int32_t *>(sp + off);
+    off += align256((size_t)s.n_detectors * ((1u << s.n_anchors) + 1) * 4);
+    int32_t *samples = reinterpret_cast<int32_t *>(sp + off);
+    off += align256((size_t)s.n_detectors * rows * 4);
+    uint32_t *cv = reinterpret_cast<uint32_t *>(sp + off);
+
+    hipLaunchKernelGGL(k_seq_pack, dim3((s.n_detectors + 63) / 64, (rows + 63) / 64), dim3(kBlock),
+                       0, st, idx, md, mi, pack, rows, s.n_detectors);
+    hipLaunchKernelGGL(k_seq_pack_pe, dim3(blocks_for(n_pe)), dim3(kBlock), 0, st,
+                       s.pe_dim > 0 ? pidx : (const int32_t *)nullptr, pmd, pmi, ppack, s.seq - 1,
+                       s.n_detectors);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int2 *ap = reinterpret_cast<const int2 *>(anchors);
+
+    // input and positional gradients
+    const uint32_t nj = (s.n_outputs + 255) / 256;
+    if (!int_mode && s.n_outputs % 4 == 0 && nj <= 4) {
+        const uint64_t n_acc = (uint64_t)rows * s.n_detectors;
+        hipLaunchKernelGGL(k_zero64, dim3(blocks_for(n_acc)), dim3(kBlock), 0, st, dq, n_acc);
+        hipLaunchKernelGGL(k_zero64, dim3(blocks_for(n_acc)), dim3(kBlock), 0, st, dk, n_acc);
+        hipLaunchKernelGGL(k_zero64, dim3(blocks_for(n_dpe)), dim3(kBlock), 0, st, dpe, (uint64_t)n_dpe);
+        const uint64_t units = (uint64_t)s.batch * s.n_detectors * (s.seq - 1);
+        const uint64_t grid = (units + kWPB - 1) / kWPB;
+        if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
+#define SPIKY_PSEQ(NJ)                                                                            \
+    hipLaunchKernelGGL(k_propagate_seq<NJ>, dim3((uint32_t)grid), dim3(kBlock), 0, st, w, g, pack, \
+                       ppack, dq, dk, dpe, s.batch, s.seq, s.n_outputs, s.n_detectors, s.n_anchors, \
+                       s.pe_dim)
+        switch (nj) {
+            case 1: SPIKY_PSEQ(1); break;
+            case 2: SPIKY_PSEQ(2); break;
+            case 3: SPIKY_PSEQ(3); break;
+            default: SPIKY_PSEQ(4); break;
+        }
+#undef SPIKY_PSEQ
+        hipLaunchKernelGGL(k_seq_xgrad, dim3(blocks_for(n_acc)), dim3(kBlock), 0, st, dq, dk, pack,
+                           ap, x_grad, s.batch, s.seq, s.n_inputs, s.n_detectors, s.n_anchors);
+        if (s.pe_dim > 0)
+            hipLaunchKernelGGL(k_seq_pe_commit, dim3(blocks_for(n_dpe)), dim3(kBlock), 0, st, dpe,
+                               pe_grad, (uint32_t)n_dpe);
+    } else {
+        const uint32_t n_ob = (s.n_outputs + s.ogs - 1) / s.ogs;
+        const uint64_t n_items = (uint64_t)s.batch * s.n_detectors * ((uint64_t)s.seq * (s.seq - 1) / 2) * n_ob;
+        if (n_items > 0) {
+            if (n_items / kBlock > 0x7fffffffull) return hipErrorInvalidConfiguration;
+            if (int_mode)
+                hipLaunchKernelGGL(k_propagate_seq_exact<true>, dim3(blocks_for(n_items)), dim3(kBlock),
+                                   0, st, w, g, pack, ppack, ap, x_grad, pe_grad, s.batch, s.seq,
+                                   s.n_inputs, s.n_outputs, s.n_detectors, s.n_anchors, s.pe_dim,
+                                   s.ogs, n_ob, n_items, int_rescaler);
+            else
+                hipLaunchKernelGGL(k_propagate_seq_exact<false>, dim3(blocks_for(n_items)),
+                                   dim3(kBlock), 0, st, w, g, pack, ppack, ap, x_grad, pe_grad,
+                                   s.batch, s.seq, s.n_inputs, s.n_outputs, s.n_detectors,
+                                   s.n_anchors, s.pe_dim, s.ogs, n_ob, n_items, int_rescaler);
+        }
+        if (int_mode) {
+            e = launch_convert_i2f(x_grad, (uint64_t)rows * s.n_inputs, int_rescaler, st);
+            if (e != hipSuccess) return e;
+            if (s.pe_dim > 0) {
+                e = launch_convert_i2f(pe_grad, (uint64_t)n_pe * s.pe_dim, int_rescaler, st);
+                if (e != hipSuccess) return e;
+            }
+        }
+    }
+    e = hipGetLastError();
+    if (e != hipSuccess || target == nullptr) return e;
+
+    // weight gradient (or the in-place update of the weights)
+    FcShape fs{};
+    fs.batch = rows;
+    fs.n_inputs = s.n_inputs;
+    fs.n_outputs = s.n_outputs;
+    fs.n_detectors = s.n_detectors;
+    fs.n_anchors = s.n_anchors;
+    fs.n_entries = 1u << s.n_anchors;
+    fs.dgs = s.dgs;
+    fs.ogs = s.ogs;
+    e = launch_wgrad_commit_values(g, cv, (uint64_t)rows * s.n_outputs, lr, int_mode, int_rescaler, st);
+    if (e != hipSuccess) return e;
+    const uint32_t cols = seq_wg_cols(s);
+    if (cols > 0) {
+        e = launch_bucket_samples(fs, idx, offsets, samples, st);
+        if (e != hipSuccess) return e;
+        const uint32_t n_slices = (s.n_outputs + cols - 1) / cols;
+        const uint64_t grid = (uint64_t)s.n_detectors * (1u << s.n_anchors) * n_slices;
+        if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
+#define SPIKY_WSEQ(IM, OW)                                                                            \
+    hipLaunchKernelGGL((k_wgrad_seq_lds<IM, OW>), dim3((uint32_t)grid), dim3(kSeqWgThreads), 0, st, cv, \
+                       offsets, samples, pack, ppack, target, s.batch, s.seq, s.n_outputs,            \
+                       s.n_detectors, s.n_anchors, s.pe_dim, cols, n_slices, int_rescaler)
+        if (int_mode) {
+            if (overwrite) SPIKY_WSEQ(true, true); else SPIKY_WSEQ(true, false);
+        } else {
+            if (overwrite) SPIKY_WSEQ(false, true); else SPIKY_WSEQ(false, false);
+        }
+#undef SPIKY_WSEQ
+        return hipGetLastError();
+    }
+    const uint64_t n_w = (uint64_t)s.n_detectors * (1ull << (2 * s.n_anchors + s.pe_dim)) * s.n_outputs;
+    if (overwrite) {
+        e = launch_zero(target, n_w, st);
+        if (e != hipSuccess) return e;
+    }
+    const uint64_t n_items = (uint64_t)rows * s.n_detectors * s.n_outputs;
+    if (int_mode)
+        hipLaunchKernelGGL(k_wgrad_seq_atomic<true>, dim3(blocks_for(n_items)), dim3(kBlock), 0, st,
+                           cv, pack, ppack, target, s.batch, s.seq, s.n_outputs, s.n_detectors,
+                           s.n_anchors, s.pe_dim, n_items);
+    else
+        hipLaunchKernelGGL(k_wgrad_seq_atomic<false>, dim3(blocks_for(n_items)), dim3(kBlock), 0, st,
+                           cv, pack, ppack, target, s.batch, s.seq, s.n_outputs, s.n_detectors,
+                           s.n_anchors, s.pe_dim, n_items);
+    e = hipGetLastError();
+    if (e != hipSuccess || !int_mode) return e;
+    return launch_convert_i2f(target, n_w, int_rescaler, st);
+}
+
+}  // namespace spiky

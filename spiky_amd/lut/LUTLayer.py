@@ -467,6 +467,97 @@ class LUTLayerBasic(nn.Module):
         result = () if external_output else (x_grad.view(source_x_shape),)
         return result + (target_w_grad,)
 
+    def forward_step_concat(self, x, pos_embeddings, output=None):
+        """Sequence-concat forward (reference LUTLayer.py:677-777)."""
+        if not (len(x.shape) == len(self.input_shape()) + 2 and tuple(x.shape[2:]) == tuple(self.input_shape())):
+            raise ValueError(f"Input x has invalid shape {x.shape}; expected "
+                             f"{(x.shape[0], 'S', *self.input_shape())} input_shape={self.input_shape()}")
+        assert self._concatenation_product
+        assert x.device == self.device
+        batch_size, sequence_length = x.shape[0], x.shape[1]
+        assert sequence_length == self._sequence_length, \
+            f"Input sequence_length {sequence_length} does not match constructor sequence_length {self._sequence_length}"
+        x = x.contiguous().view(-1)
+        external_output = output is not None
+        if not external_output:
+            output = torch.zeros([batch_size * sequence_length * self._n_outputs], dtype=torch.float32,
+                                 device=self.device)
+        n_items = batch_size * sequence_length * self._n_detectors
+        lookup_indices = torch.empty([n_items], dtype=torch.int32, device=self.device)
+        min_anchor_deltas = min_anchor_delta_indices = None
+        if self.training:
+            min_anchor_deltas = torch.empty([n_items], dtype=torch.float32, device=self.device)
+            min_anchor_delta_indices = torch.empty([n_items], dtype=torch.int32, device=self.device)
+        pli = pmd = pmi = None
+        if self._positional_dim > 0:
+            n_pe = (sequence_length - 1) * self._n_detectors
+            pli = torch.empty([n_pe], dtype=torch.int32, device=self.device)
+            if self.training:
+                pmd = torch.empty([n_pe], dtype=torch.float32, device=self.device)
+                pmi = torch.empty([n_pe], dtype=torch.int32, device=self.device)
+            pos_embeddings = pos_embeddings.contiguous()
+        self._lut_dm.forward_step_concat(self._weights, batch_size, x, self._detector_anchors, output,
+                                         lookup_indices, self._shared_context._cmp_eps, pos_embeddings,
+                                         pli, min_anchor_deltas, min_anchor_delta_indices, pmd, pmi)
+        result = () if external_output else \
+            (output.view((batch_size, sequence_length) + tuple(self.output_shape())),)
+        if not self.training:
+            return None if external_output else result[0]
+        shp = (batch_size, sequence_length, self._n_detectors)
+        pshp = (sequence_length - 1, self._n_detectors)
+        return result + (lookup_indices.view(shp), min_anchor_deltas.view(shp),
+                         min_anchor_delta_indices.view(shp),
+                         None if pli is None else pli.view(pshp),
+                         None if pmd is None else pmd.view(pshp),
+                         None if pmi is None else pmi.view(pshp))
+
+    def backward_step_concat(self, x, grad_output, lookup_indices, min_anchor_deltas,
+                             min_anchor_delta_indices, positional_lookup_indices, positional_min_deltas,
+                             positional_min_delta_indices, x_grad=None):
+        """Sequence-concat backward (reference LUTLayer.py:901-1009)."""
+        assert x.device == self.device
+        assert self._concatenation_product
+        source_x_shape = x.shape
+        batch_size, sequence_length = x.shape[0], x.shape[1]
+        assert sequence_length == self._sequence_length
+        shp = (batch_size, sequence_length, self._n_detectors)
+        assert tuple(lookup_indices.shape) == shp and tuple(min_anchor_deltas.shape) == shp
+        assert tuple(min_anchor_delta_indices.shape) == shp
+        x = x.contiguous().view(-1)
+        lookup_indices = lookup_indices.reshape(-1)
+        min_anchor_deltas = min_anchor_deltas.reshape(-1)
+        min_anchor_delta_indices = min_anchor_delta_indices.reshape(-1)
+        if self._positional_dim > 0:
+            pshp = (sequence_length - 1, self._n_detectors)
+            assert tuple(positional_lookup_indices.shape) == pshp
+            positional_lookup_indices = positional_lookup_indices.reshape(-1)
+            positional_min_deltas = positional_min_deltas.reshape(-1)
+            positional_min_delta_indices = positional_min_delta_indices.reshape(-1)
+            positional_grad = torch.zeros([(sequence_length - 1) * self._n_detectors * self._positional_dim],
+                                          dtype=torch.float32, device=self.device)
+        else:
+            assert positional_lookup_indices is None
+            positional_grad = None
+        external_output = x_grad is not None
+        if not external_output:
+            x_grad = torch.zeros_like(x)
+        target_w_grad, overwrite = self._weight_grad_target()
+        assert tuple(grad_output.shape) == (batch_size, sequence_length) + tuple(self.output_shape())
+        grad_output = grad_output.contiguous().view(-1)
+        external_lr = self._external_lr()
+        self._lut_dm.backward_backprop_concat(
+            self._weights, batch_size, grad_output, self._detector_anchors, lookup_indices,
+            min_anchor_deltas, min_anchor_delta_indices, x_grad, external_lr, positional_lookup_indices,
+            positional_min_deltas, positional_min_delta_indices, positional_grad, target_w_grad, None,
+            overwrite_weights_gradients=overwrite)
+        if not external_output:
+            target_w_grad = self._process_gradients(target_w_grad, batch_size) \
+                if target_w_grad is not None else None
+        if self._positional_dim > 0 and self._weights_gradient_policy.normalized:
+            positional_grad /= positional_grad.abs().max().clip(1e-16)
+        result = () if external_output else (x_grad.view(source_x_shape),)
+        return result + (target_w_grad, positional_grad)
+
     def to(self, *args, **kwargs):
         super().to(*args, **kwargs)
         device = kwargs.get("device", None)

@@ -443,6 +443,115 @@ class _LUTDataManagerBase:
                 _ptr(w_input_gradients), float(external_lr), _ptr(w_weights_gradients),
                 int(bool(overwrite_weights_gradients)), ctypes.c_void_p(st)))
 
+    # ---------------------------------------------------------------- sequence-concat mode
+    def forward_step_concat(self, r_weights, batch_size, r_input, r_detector_anchors, w_output,
+                            w_lookup_indices, cmp_eps, r_positional_embeddings,
+                            w_positional_lookup_indices, w_min_anchor_deltas=None,
+                            w_min_anchor_delta_indices=None, w_positional_min_deltas=None,
+                            w_positional_min_delta_indices=None, r_stream_handles=None):
+        """lut.cu pybind 1556-1575 -> lut_runtime.cu:399-593.  Input [B][S][I];
+        lookup indices / min deltas [B][S][T]; positional ones [(S-1)][T]."""
+        if batch_size == 0:
+            raise ValueError("batch_size == 0")
+        dev = self._device
+        S = self._sequence_length
+        if S <= 1:
+            raise ValueError("forward_step_concat should only be called when sequence_length > 1")
+        check_tensor(r_weights, "r_weights", True, dev)
+        check_tensor(r_input, "r_input", True, dev)
+        check_tensor(r_detector_anchors, "r_detector_anchors", False, dev, 4)
+        check_tensor(w_output, "w_output", True, dev)
+        check_tensor(w_lookup_indices, "w_lookup_indices", False, dev, 4)
+        for t, nm, real in ((w_min_anchor_deltas, "w_min_anchor_deltas", True),
+                            (w_min_anchor_delta_indices, "w_min_anchor_delta_indices", False),
+                            (r_positional_embeddings, "r_positional_embeddings", True),
+                            (w_positional_lookup_indices, "w_positional_lookup_indices", False),
+                            (w_positional_min_deltas, "w_positional_min_deltas", True),
+                            (w_positional_min_delta_indices, "w_positional_min_delta_indices", False)):
+            if t is not None:
+                check_tensor(t, nm, real, dev)
+        self._require_device()
+        B, T, P = int(batch_size), self._n_detectors, self._positional_dim
+        _require_numel(r_weights, self.get_weights_dimension(), "r_weights")
+        _require_numel(r_input, B * S * self._n_inputs, "r_input")
+        _require_numel(r_detector_anchors, T * self._n_anchors * 2, "r_detector_anchors")
+        _require_numel(w_output, B * S * self._n_outputs, "w_output")
+        _require_numel(w_lookup_indices, B * S * T, "w_lookup_indices")
+        if P > 0:
+            if r_positional_embeddings is None or w_positional_lookup_indices is None:
+                raise ValueError("positional embeddings and positional lookup indices must be "
+                                 "provided when positional_dim > 0")
+            _require_numel(r_positional_embeddings, (S - 1) * T * P, "r_positional_embeddings")
+            _require_numel(w_positional_lookup_indices, (S - 1) * T, "w_positional_lookup_indices")
+        with torch.cuda.device(dev):
+            st = self._stream(r_stream_handles)
+            _native.check(_native.lib().spiky_lut_forward_step_concat(
+                self._h, _ptr(r_weights), B, _ptr(r_input), _ptr(r_detector_anchors), _ptr(w_output),
+                _ptr(w_lookup_indices), float(cmp_eps), _ptr(r_positional_embeddings if P > 0 else None),
+                _ptr(w_positional_lookup_indices if P > 0 else None), _ptr(w_min_anchor_deltas),
+                _ptr(w_min_anchor_delta_indices), _ptr(w_positional_min_deltas if P > 0 else None),
+                _ptr(w_positional_min_delta_indices if P > 0 else None), ctypes.c_void_p(st)))
+
+    def backward_backprop_concat(self, r_weights, batch_size, r_output_gradients, r_detector_anchors,
+                                 r_lookup_indices, r_min_anchor_deltas, r_min_anchor_delta_indices,
+                                 w_input_gradients, external_lr, r_positional_lookup_indices=None,
+                                 r_positional_min_deltas=None, r_positional_min_delta_indices=None,
+                                 w_positional_embeddings_gradients=None, w_weights_gradients=None,
+                                 r_stream_handles=None, overwrite_weights_gradients=False):
+        """lut.cu pybind 1620-1636 -> lut_runtime.cu:595-850."""
+        if batch_size == 0:
+            raise ValueError("batch_size == 0")
+        dev = self._device
+        S = self._sequence_length
+        if S <= 1:
+            raise ValueError("backward_backprop_concat should only be called when sequence_length > 1")
+        for t, nm, real in ((r_weights, "r_weights", True), (r_output_gradients, "r_output_gradients", True),
+                            (r_detector_anchors, "r_detector_anchors", False),
+                            (r_lookup_indices, "r_lookup_indices", False),
+                            (r_min_anchor_deltas, "r_min_anchor_deltas", True),
+                            (r_min_anchor_delta_indices, "r_min_anchor_delta_indices", False),
+                            (w_input_gradients, "w_input_gradients", True)):
+            check_tensor(t, nm, real, dev)
+        for t, nm, real in ((r_positional_lookup_indices, "r_positional_lookup_indices", False),
+                            (r_positional_min_deltas, "r_positional_min_deltas", True),
+                            (r_positional_min_delta_indices, "r_positional_min_delta_indices", False),
+                            (w_positional_embeddings_gradients, "w_positional_embeddings_gradients", True),
+                            (w_weights_gradients, "w_weights_gradients", True)):
+            if t is not None:
+                check_tensor(t, nm, real, dev)
+        self._require_device()
+        B, T, P = int(batch_size), self._n_detectors, self._positional_dim
+        _require_numel(r_weights, self.get_weights_dimension(), "r_weights")
+        _require_numel(r_output_gradients, B * S * self._n_outputs, "r_output_gradients")
+        _require_numel(w_input_gradients, B * S * self._n_inputs, "w_input_gradients")
+        for t, nm in ((r_lookup_indices, "r_lookup_indices"), (r_min_anchor_deltas, "r_min_anchor_deltas"),
+                      (r_min_anchor_delta_indices, "r_min_anchor_delta_indices")):
+            _require_numel(t, B * S * T, nm)
+        if P > 0:
+            for t, nm in ((r_positional_lookup_indices, "r_positional_lookup_indices"),
+                          (r_positional_min_deltas, "r_positional_min_deltas"),
+                          (r_positional_min_delta_indices, "r_positional_min_delta_indices")):
+                if t is None:
+                    raise ValueError(f"{nm} must be provided when positional_dim > 0")
+                _require_numel(t, (S - 1) * T, nm)
+            if w_positional_embeddings_gradients is None:
+                raise ValueError("w_positional_embeddings_gradients must be provided when positional_dim > 0")
+            _require_numel(w_positional_embeddings_gradients, (S - 1) * T * P,
+                           "w_positional_embeddings_gradients")
+        if w_weights_gradients is not None:
+            _require_numel(w_weights_gradients, self.get_weights_dimension(), "w_weights_gradients")
+        with torch.cuda.device(dev):
+            st = self._stream(r_stream_handles)
+            _native.check(_native.lib().spiky_lut_backward_backprop_concat(
+                self._h, _ptr(r_weights), B, _ptr(r_output_gradients), _ptr(r_detector_anchors),
+                _ptr(r_lookup_indices), _ptr(r_min_anchor_deltas), _ptr(r_min_anchor_delta_indices),
+                _ptr(w_input_gradients), float(external_lr),
+                _ptr(r_positional_lookup_indices if P > 0 else None),
+                _ptr(r_positional_min_deltas if P > 0 else None),
+                _ptr(r_positional_min_delta_indices if P > 0 else None),
+                _ptr(w_positional_embeddings_gradients if P > 0 else None), _ptr(w_weights_gradients),
+                int(bool(overwrite_weights_gradients)), ctypes.c_void_p(st)))
+
     # ---------------------------------------------------------------- export
     def count_synapses(self, neuron_indices_to_process):
         """Number of forward synapses of the given lookup neurons."""
