@@ -134,12 +134,87 @@ def cpu_baseline(x, anchors, W, go, B_full, I, T, Nc, O, sample_B):
     }
 
 
+TRANSFORMER = dict(vocab_size=256, embedding_dim=256, context_size=256, positional_dim=4, num_layers=4,
+                   num_heads=4, n_detectors=16, n_anchors_per_detector=8,
+                   n_anchors_per_detector_attention=6)
+TRANSFORMER_BATCH = 32
+
+
+def transformer_g_bytes(B, cfg):
+    """G-model bytes of one forward + backward of the config-5 transformer:
+    every causal pair reads one attention row forward and its main and flipped
+    rows backward (plus the row read-modify-write of the weight gradient);
+    feed-forward and unembedding layers as in g_model_bytes over B*S rows."""
+    S, E, V = cfg["context_size"], cfg["embedding_dim"], cfg["vocab_size"]
+    T_att = cfg["n_detectors"] * cfg["num_heads"]
+    pairs = S * (S - 1) // 2
+    att = B * pairs * T_att * E * 4 * (1 + 2 + 2)
+    fc = lambda O: sum(g_model_bytes(B * S, E, cfg["n_detectors"], cfg["n_anchors_per_detector"], O).values())
+    return cfg["num_layers"] * (att + fc(E)) + fc(V)
+
+
+def bench_transformer(args):
+    """LUTTransformer forward + cross-entropy + backward on
+    random byte tokens with next-token targets."""
+    import torch
+    import torch.nn.functional as F
+    from spiky_amd import LUTTransformer
+    dev = torch.device("cuda:0")
+    cfg = TRANSFORMER
+    B, S, V = TRANSFORMER_BATCH, cfg["context_size"], cfg["vocab_size"]
+    log(f"config 5: LUTTransformer {cfg}, batch {B}")
+    model = LUTTransformer(**cfg, device=dev, seed=1)
+    gen = torch.Generator(device=dev).manual_seed(2)
+    with torch.no_grad():
+        for layer in model._lut_layers():
+            layer._weights.normal_(0.0, 0.01, generator=gen)
+    gt = torch.Generator(device=dev).manual_seed(0)
+    stream = torch.randint(0, V, (B, S + 1), device=dev, generator=gt)
+    tokens, targets = stream[:, :S].contiguous(), stream[:, 1:].contiguous()
+    params = [l._weights for l in model._lut_layers()] + \
+             [b["attention_lut"]._positional_embeddings for b in model.layers]
+
+    def step():
+        for p in params:
+            p.grad = None
+        logits = model(tokens)
+        loss = F.cross_entropy(logits.reshape(-1, V), targets.reshape(-1))
+        loss.backward()
+
+    log("warmup")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} steps")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    g = transformer_g_bytes(B, cfg)
+    res = {
+        "metric": "LUTTransformer fwd+bwd samples/sec (BASELINE config 5)",
+        "value": round(B / (ms / 1e3), 2),
+        "unit": "samples/s",
+        "tokens_per_s": round(B * S / (ms / 1e3), 1),
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32 (fp64 partial sums)",
+        "data": "synthetic (uniform random byte tokens, next-token targets, N(0,0.01) tables)",
+        "config": {"workload": "BASELINE config 5: LUTTransformer block stack fwd+bwd", "batch": B, **cfg},
+        "roofline": {"bound": "hbm", "achieved": round(g / (ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(g / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                     "traffic": None, "algorithmic_bytes_per_step": g, "scope": "whole step, G model"},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(res), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS))
+    ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS) + [5])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="only run a plain copy of this many MiB (counter calibration) and exit")
@@ -151,6 +226,10 @@ def main():
         print("bench.py measures one GPU only: this build's LUT path runs on a single MI355X "
               "(the multi-GPU table-parallel design is described, not built).", file=sys.stderr)
         sys.exit(2)
+
+    if args.config == 5:
+        bench_transformer(args)
+        return
 
     import torch
     from spiky_amd import LUTLayer

@@ -2,6 +2,7 @@
 Spiky LUT API (LUTForwardFN, LUTLayer, ProjectionLUTLayer, LUTTransformer)."""
 from . import _native  # noqa: F401
 from .lut.lut_data_manager import LUTDataManagerF, LUTDataManagerI  # noqa: F401
+from .lut.LUTTransformer import LUTTransformer  # noqa: F401
 from .lut.LUTLayer import (  # noqa: F401
     GradientPolicy, GradientType, LUTLayer, LUTLayerBasic, LUTSharedContext, Conv2DLUTLayer,
     ProjectionLUTLayer, SynapseMeta,

@@ -27,10 +27,11 @@
 //                       with sequential block dots and integer payloads, so the
 //                       int32 accumulators are bit-identical.
 //   k_seq_xgrad         x_grad[b][s][anchor] +-= du(b, t, s) for every table.
-//   k_wgrad_seq_lds     one workgroup per (table, Q value, column slice): the
+//   k_wgrad_seq_sort    one workgroup per (table, Q value, column slice): the
 //                       gradient of that sub-table slice (2^(Nc+Npe) rows x C
-//                       columns, <= 128 KiB) is accumulated in LDS from every
-//                       (b, j) whose Q is that value and written to HBM once.
+//                       columns) is summed in registers from every (b, j) whose
+//                       Q is that value, after an LDS counting sort of the
+//                       (b, j, i) entries by target row, and written once.
 #include "lut_kernels.h"
 
 #include <algorithm>
@@ -508,25 +509,38 @@ __global__ __launch_bounds__(kBlock) void k_zero64(double *__restrict__ p, uint6
 
 // ---------------------------------------------------------------------------
 // gather_w_gradients_seq_fc (proto:3944-4304), one workgroup per (table t,
-// Q value q, column slice).  cv holds the commit values of every (b, s)
-// (k_wgrad_commit_values); samples / offsets are the (b, s) rows of each table
-// bucketed by their index (k_bucket_samples).
+// Q value q, column slice of C columns).  The sub-table's 2^(Nc+Npe) rows x C
+// gradient sums live in registers (32 per thread); the items (b, j) of the
+// bucket (t, q) are taken in batches: each batch's (item, earlier position i)
+// entries are bucketed by target row (LDS counting sort), then every thread
+// adds the commit values of its rows' entries from an LDS copy of the batch's
+// gradient rows.  No floating-point atomics; each weight-gradient element is
+// written once (the zero-fill of the caller's buffer is fused away).
 constexpr int kSeqWgThreads = 1024;
-constexpr int kSeqWgAccWords = 32768;  // 128 KiB accumulator
-constexpr int kSeqWgKeys = 8192;       // K indices of up to 8192 (b, s) rows at a time
+constexpr int kSeqWgOut = 32;            // outputs (row, column) per thread
+constexpr int kSeqWgRowsMax = 4096;      // sub-table rows 2^(Nc+Npe)
+constexpr int kSeqWgEntries = 16384;     // entries per batch
+constexpr int kSeqWgGvWords = 8192;      // batch gradient rows (items x C)
+constexpr int kSeqWgKeys = 8192;         // K indices of up to 8192 (b, s) rows at a time
 constexpr int kSeqWgPe = 1024;
 
 template <bool INT_MODE, bool OVERWRITE>
-__global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_lds(
+__global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
     const uint32_t *__restrict__ cv, const int32_t *__restrict__ offsets,
     const int32_t *__restrict__ samples, const uint2 *__restrict__ pack,
     const uint2 *__restrict__ ppack, float *__restrict__ target, uint32_t batch, uint32_t seq,
     uint32_t n_outputs, uint32_t n_detectors, uint32_t n_anchors, uint32_t pe_dim,
-    uint32_t cols, uint32_t n_slices, double int_rescaler) {
-    __shared__ uint32_t acc[kSeqWgAccWords];
+    uint32_t cols, uint32_t n_slices, uint32_t items_per_batch, double int_rescaler) {
+    __shared__ uint32_t cnt[kSeqWgRowsMax];
+    __shared__ uint32_t cur[kSeqWgRowsMax];
+    __shared__ uint16_t ent[kSeqWgEntries];
+    __shared__ uint32_t gv[kSeqWgGvWords];
     __shared__ uint16_t ktab[kSeqWgKeys];
     __shared__ uint16_t ptab[kSeqWgPe];
+    __shared__ uint32_t bitems[kSeqWgGvWords / 4];  // row ids of the batch's items
     const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & (kWave - 1);
+    const uint32_t wave = tid / kWave;
     const uint32_t slice = blockIdx.x % n_slices;
     const uint32_t tq = blockIdx.x / n_slices;
     const uint32_t n_q = 1u << n_anchors;
@@ -535,13 +549,16 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_lds(
     const uint32_t pmask = (1u << pe_dim) - 1;
     const uint32_t n_rows = batch * seq;
     const uint32_t col0 = slice * cols;
-    const uint32_t lanes_per_item = cols / 4;
-    const uint32_t items_per_pass = kSeqWgThreads / lanes_per_item;
-    const uint32_t my_item = tid / lanes_per_item;
-    const uint32_t my_q4 = tid % lanes_per_item;
-    const uint32_t c = col0 + my_q4 * 4;
-    const bool active = c < n_outputs;
-    for (uint32_t k = tid; k < sub_rows * cols; k += kSeqWgThreads) acc[k] = 0u;
+    // output k of this thread: row my_row0 + k, column my_col (cols divides
+    // the 1024 threads; a thread's rows are consecutive so their LDS count
+    // words sit at immediate offsets from one address)
+    const uint32_t my_col = tid % cols;
+    const uint32_t my_row0 = (tid / cols) * kSeqWgOut;
+
+    uint32_t acc[kSeqWgOut];
+#pragma unroll
+    for (int k = 0; k < kSeqWgOut; k++) acc[k] = 0u;
+
     for (uint32_t d = tid; d + 1 < seq; d += kSeqWgThreads)
         ptab[d] = (uint16_t)(rec_idx(ppack[(size_t)t * (seq - 1) + d]) & pmask);
     const int32_t *off_t = offsets + (size_t)t * (n_q + 1);
@@ -549,13 +566,12 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_lds(
     const int32_t *smp = samples + (size_t)t * n_rows;
     const uint2 *kp = pack + (size_t)t * n_rows;
     const uint32_t rows_per_chunk = (kSeqWgKeys / seq) * seq;
-    // the bucket is ascending in (b, s): walk it in chunks of whole samples
+
     int32_t k0 = beg;
     for (uint32_t r0 = 0; r0 < n_rows && k0 < end; r0 += rows_per_chunk) {
         const uint32_t r1 = min(r0 + rows_per_chunk, n_rows);
         __syncthreads();
         for (uint32_t r = r0 + tid; r < r1; r += kSeqWgThreads) ktab[r - r0] = (uint16_t)rec_idx(kp[r]);
-        __syncthreads();
         // first bucket position at or past row r1 (uniform binary search)
         int32_t lo = k0, hi = end;
         while (lo < hi) {
@@ -563,53 +579,98 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_lds(
             if ((uint32_t)smp[mid] < r1) lo = mid + 1; else hi = mid;
         }
         const int32_t k1 = lo;
-        for (int32_t kb = k0; kb < k1; kb += (int32_t)items_per_pass) {
-            const int32_t k = kb + (int32_t)my_item;
-            if (k >= k1 || !active) continue;
-            const uint32_t r = (uint32_t)smp[k];
-            const uint32_t bl = r / seq - r0 / seq, j = r % seq;
-            const uint4 v = *reinterpret_cast<const uint4 *>(cv + (size_t)r * n_outputs + c);
-            const uint16_t *kt = ktab + (size_t)bl * seq;
-            for (uint32_t i = 0; i < j; i++) {
-                const uint32_t row = ((uint32_t)kt[i] << pe_dim) | ptab[j - i - 1];
-                uint32_t *a = acc + (row & (sub_rows - 1)) * cols + my_q4 * 4;
-                if (INT_MODE) {
-                    atomicAdd(a + 0, v.x);
-                    atomicAdd(a + 1, v.y);
-                    atomicAdd(a + 2, v.z);
-                    atomicAdd(a + 3, v.w);
-                } else {
-                    atomicAdd(reinterpret_cast<float *>(a + 0), __uint_as_float(v.x));
-                    atomicAdd(reinterpret_cast<float *>(a + 1), __uint_as_float(v.y));
-                    atomicAdd(reinterpret_cast<float *>(a + 2), __uint_as_float(v.z));
-                    atomicAdd(reinterpret_cast<float *>(a + 3), __uint_as_float(v.w));
+        for (int32_t kb = k0; kb < k1; kb += (int32_t)items_per_batch) {
+            const uint32_t nb = (uint32_t)min((int32_t)items_per_batch, k1 - kb);
+            __syncthreads();
+            // stage the batch: item rows, their gradient columns, zero counts
+            for (uint32_t it = tid; it < nb; it += kSeqWgThreads) bitems[it] = (uint32_t)smp[kb + it];
+            for (uint32_t r = tid; r < sub_rows; r += kSeqWgThreads) cnt[r] = 0u;
+            __syncthreads();
+            for (uint32_t e = tid; e < nb * cols; e += kSeqWgThreads) {
+                const uint32_t it = e / cols, cc = col0 + e % cols;
+                gv[e] = cc < n_outputs ? cv[(size_t)bitems[it] * n_outputs + cc] : 0u;
+            }
+            // count: one wavefront per item, lanes over earlier positions i
+            for (uint32_t it = wave; it < nb; it += kSeqWgThreads / kWave) {
+                const uint32_t r = bitems[it];
+                const uint32_t j = r % seq;
+                const uint16_t *kt = ktab + (r / seq - r0 / seq) * seq;
+                for (uint32_t i = lane; i < j; i += kWave)
+                    atomicAdd(&cnt[(((uint32_t)kt[i] << pe_dim) | ptab[j - i - 1]) & (sub_rows - 1)], 1u);
+            }
+            __syncthreads();
+            // exclusive scan of the counts into cur (one pass per 1024 rows)
+            uint32_t carry = 0;
+            for (uint32_t base = 0; base < sub_rows; base += kSeqWgThreads) {
+                const uint32_t r = base + tid;
+                const uint32_t v = r < sub_rows ? cnt[r] : 0u;
+                uint32_t incl = v;
+#pragma unroll
+                for (int o = 1; o < kWave; o <<= 1) {
+                    const uint32_t y = __shfl_up(incl, o, kWave);
+                    if ((int)lane >= o) incl += y;
                 }
+                __shared__ uint32_t wsum[kSeqWgThreads / kWave];
+                if (lane == kWave - 1) wsum[wave] = incl;
+                __syncthreads();
+                uint32_t wprefix = 0;
+                for (uint32_t w = 0; w < wave; w++) wprefix += wsum[w];
+                uint32_t total = 0;
+                for (uint32_t w = 0; w < kSeqWgThreads / kWave; w++) total += wsum[w];
+                if (r < sub_rows) cur[r] = carry + wprefix + incl - v;
+                carry += total;
+                __syncthreads();
+            }
+            // scatter the entries' item numbers into their rows' buckets
+            for (uint32_t it = wave; it < nb; it += kSeqWgThreads / kWave) {
+                const uint32_t r = bitems[it];
+                const uint32_t j = r % seq;
+                const uint16_t *kt = ktab + (r / seq - r0 / seq) * seq;
+                for (uint32_t i = lane; i < j; i += kWave) {
+                    const uint32_t row = (((uint32_t)kt[i] << pe_dim) | ptab[j - i - 1]) & (sub_rows - 1);
+                    ent[atomicAdd(&cur[row], 1u)] = (uint16_t)it;
+                }
+            }
+            __syncthreads();
+            // cur[row] is now the end of the row's bucket, cur - cnt its start
+#pragma unroll
+            for (int k = 0; k < kSeqWgOut; k++) {
+                const uint32_t row = my_row0 + (uint32_t)k;
+                const uint32_t e1 = row < sub_rows ? cur[row] : 0u;
+                const uint32_t e0 = row < sub_rows ? e1 - cnt[row] : 0u;
+                uint32_t a = acc[k];
+                for (uint32_t e = e0; e < e1; e++) {
+                    const uint32_t v = gv[(uint32_t)ent[e] * cols + my_col];
+                    if (INT_MODE)
+                        a += v;
+                    else
+                        a = __float_as_uint(__uint_as_float(a) + __uint_as_float(v));
+                }
+                acc[k] = a;
+                // one output's bucket bounds live at a time (register budget)
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
         k0 = k1;
     }
-    __syncthreads();
-    // write the sub-table slice: rows q*sub_rows .. of table t
+    // write the sub-table slice (rows q * sub_rows .. of table t)
     float *dst = target + ((size_t)t * n_q + q) * sub_rows * n_outputs;
-    for (uint32_t k = tid; k < sub_rows * lanes_per_item; k += kSeqWgThreads) {
-        const uint32_t row = k / lanes_per_item, qq = k % lanes_per_item;
-        const uint32_t cc = col0 + qq * 4;
-        if (cc >= n_outputs) continue;
-        const uint32_t *a = acc + row * cols + qq * 4;
-        float *p = dst + (size_t)row * n_outputs + cc;
-        float o[4];
+    const uint32_t cc = col0 + my_col;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            if (INT_MODE) {
-                int32_t iv = (int32_t)a[e];
-                if (!OVERWRITE) iv = wrap_add(iv, __float_as_int(p[e]));
-                o[e] = (float)(((double)iv * kDenom32Reciproc) / int_rescaler);
-            } else {
-                o[e] = __uint_as_float(a[e]);
-                if (!OVERWRITE) o[e] = p[e] + o[e];
-            }
+    for (int k = 0; k < kSeqWgOut; k++) {
+        const uint32_t row = my_row0 + (uint32_t)k;
+        if (row >= sub_rows || cc >= n_outputs) continue;
+        float *p = dst + (size_t)row * n_outputs + cc;
+        float v;
+        if (INT_MODE) {
+            int32_t iv = (int32_t)acc[k];
+            if (!OVERWRITE) iv = wrap_add(iv, __float_as_int(*p));
+            v = (float)(((double)iv * kDenom32Reciproc) / int_rescaler);
+        } else {
+            v = __uint_as_float(acc[k]);
+            if (!OVERWRITE) v = *p + v;
         }
-        *reinterpret_cast<float4 *>(p) = make_float4(o[0], o[1], o[2], o[3]);
+        *p = v;
     }
 }
 
@@ -652,17 +713,26 @@ uint32_t seq_vec(uint32_t n_outputs) {
     return 1;
 }
 
-// Columns of a weight-gradient LDS slice (0: the LDS path does not apply).
+// Columns of a weight-gradient slice (0: the sort path does not apply): a
+// power of two with sub_rows * C <= 1024 threads x 32 outputs and the batch's
+// gradient rows (>= 1 item of C columns) in LDS.
 uint32_t seq_wg_cols(const SeqShape &s) {
     const uint64_t sub_rows = 1ull << (s.n_anchors + s.pe_dim);
-    if (s.n_outputs % 4 != 0 || s.seq > (uint32_t)kSeqWgKeys || s.seq - 1 > (uint32_t)kSeqWgPe ||
-        s.n_anchors > 12)
+    if (sub_rows > (uint64_t)kSeqWgRowsMax || s.seq > (uint32_t)kSeqWgKeys ||
+        s.seq - 1 > (uint32_t)kSeqWgPe || s.seq - 1 > (uint32_t)kSeqWgEntries)
         return 0;
-    uint32_t cols = 32;
-    while (cols >= 4 && sub_rows * cols > (uint64_t)kSeqWgAccWords) cols /= 2;
-    if (cols < 4) return 0;
-    while (cols > 4 && cols / 2 >= s.n_outputs) cols /= 2;
+    uint32_t cols = 64;
+    while (cols > 1 && sub_rows * cols > (uint64_t)kSeqWgThreads * kSeqWgOut) cols /= 2;
+    while (cols > 1 && cols / 2 >= s.n_outputs) cols /= 2;
     return cols;
+}
+
+// Items per batch: their entries (< seq each) and gradient rows must fit.
+uint32_t seq_wg_items(const SeqShape &s, uint32_t cols) {
+    uint32_t n = (uint32_t)kSeqWgEntries / std::max<uint32_t>(1, s.seq - 1);
+    n = std::min<uint32_t>(n, (uint32_t)kSeqWgGvWords / cols);
+    n = std::min<uint32_t>(n, (uint32_t)kSeqWgGvWords / 4);
+    return std::min<uint32_t>(n, 65535u);
 }
 
 }  // namespace
@@ -859,10 +929,11 @@ hipError_t launch_backward_seq(const SeqShape &s, float *w, const float *g, cons
         const uint32_t n_slices = (s.n_outputs + cols - 1) / cols;
         const uint64_t grid = (uint64_t)s.n_detectors * (1u << s.n_anchors) * n_slices;
         if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
-#define SPIKY_WSEQ(IM, OW)                                                                            \
-    hipLaunchKernelGGL((k_wgrad_seq_lds<IM, OW>), dim3((uint32_t)grid), dim3(kSeqWgThreads), 0, st, cv, \
-                       offsets, samples, pack, ppack, target, s.batch, s.seq, s.n_outputs,            \
-                       s.n_detectors, s.n_anchors, s.pe_dim, cols, n_slices, int_rescaler)
+        const uint32_t ipb = seq_wg_items(s, cols);
+#define SPIKY_WSEQ(IM, OW)                                                                             \
+    hipLaunchKernelGGL((k_wgrad_seq_sort<IM, OW>), dim3((uint32_t)grid), dim3(kSeqWgThreads), 0, st, cv, \
+                       offsets, samples, pack, ppack, target, s.batch, s.seq, s.n_outputs,             \
+                       s.n_detectors, s.n_anchors, s.pe_dim, cols, n_slices, ipb, int_rescaler)
         if (int_mode) {
             if (overwrite) SPIKY_WSEQ(true, true); else SPIKY_WSEQ(true, false);
         } else {

@@ -206,9 +206,12 @@ class _LUTDataManagerBase:
 
     def initialize_detectors(self, encoded_pairs_permutations, max_n_inputs_per_detector,
                              detector_anchors, compact_mode):
-        """prepare_detectors(_compact) (lut_compile_time_kernels_logic.proto:1-125)."""
-        check_tensor(encoded_pairs_permutations, "encoded_pairs_permutations", False, self._device, 4)
-        check_tensor(detector_anchors, "detector_anchors", False, self._device, 4)
+        """prepare_detectors(_compact) (lut_compile_time_kernels_logic.proto:1-125).
+        The decode runs on the host, so both tensors may live on the host or on
+        the manager's device."""
+        for t, nm in ((encoded_pairs_permutations, "encoded_pairs_permutations"),
+                      (detector_anchors, "detector_anchors")):
+            check_tensor(t, nm, False, -1 if t.device.type == "cpu" else self._device, 4)
         if self._detector_inputs is None:
             raise ValueError("detector_connections_manager not initialized")
         n = int(max_n_inputs_per_detector)
