@@ -71,6 +71,10 @@ hipError_t launch_fill_tm(const FcShape &s, const float *w, const int32_t *idx, 
                           bool int_mode, double int_rescaler, void *scratch, hipStream_t st);
 
 // fp32-summation min-margin input gradient through per-slice partial dots.
+// out[i] (+)= sum over k of part[k][i] in ascending k (fp32, or wrapping int32
+// then the int epilogue), i < n, n % 4 == 0.
+hipError_t launch_block_commit(const uint32_t *part, float *out, uint64_t n, uint32_t n_blocks,
+                               bool int_mode, double int_rescaler, hipStream_t st);
 bool tm_propagate_applies(const FcShape &s);
 size_t tm_propagate_scratch_bytes(const FcShape &s);
 hipError_t launch_propagate_tm(const FcShape &s, const float *w, const float *g,

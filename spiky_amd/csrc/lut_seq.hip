@@ -251,6 +251,203 @@ __global__ __launch_bounds__(kBlock) void k_fill_seq(
 }
 
 // ---------------------------------------------------------------------------
+// Sub-table-major forward: one 1024-thread workgroup per (table t, Q value q,
+// column slice of C columns).  The sub-table slice W[t][q][*][c0, c0 + C)
+// (2^(Nc+Npe) rows, at most 128 KiB) is staged in LDS once, so each table byte
+// crosses HBM once per forward.  The items (b, j) of the bucket (t, q) are
+// taken longest-first from an LDS-sorted list; C lanes own one item and sum
+// its pairs i < j in ascending i in fp64, reading rows from LDS.  The commit
+// value of table t, fp32(sum) (int mode: the int32 payload), goes to
+// part[t][b*S + j][o]; k_fill_commit adds the tables in ascending order, the
+// reference CPU path's order (proto:1807-1904), so the output is bit-identical.
+// Position 0 has no pairs: its value is -0.0f (0 in int mode), which leaves
+// every sum unchanged.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr int kSfThreads = 1024;
+constexpr int kSfTabFloats = 32768;   // 128 KiB sub-table slice
+constexpr int kSfItems = 2048;        // items sorted per chunk of a bucket
+constexpr int kSfPe = 2048;           // distances S - 1
+
+template <int C, bool INT_MODE>
+__global__ __launch_bounds__(kSfThreads) void k_fill_seq_lds(
+    const float *__restrict__ w, const uint2 *__restrict__ pack, const uint2 *__restrict__ ppack,
+    const int32_t *__restrict__ offsets, const int32_t *__restrict__ samples,
+    uint32_t *__restrict__ part, uint32_t batch, uint32_t seq, uint32_t n_outputs,
+    uint32_t n_anchors, uint32_t pe_dim, uint32_t n_slices, double int_rescaler) {
+    constexpr int kSlots = kWave / C;  // items per wavefront
+    __shared__ __attribute__((aligned(16))) float tab[kSfTabFloats + 64];  // + a zero row
+    __shared__ __attribute__((aligned(16))) uint32_t rowtab[kSfThreads];
+    __shared__ uint16_t ptab[kSfPe];
+    __shared__ uint32_t keys[kSfItems];
+    __shared__ uint32_t irow[kSfItems];
+    __shared__ uint32_t next_item;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & (kWave - 1);
+    const uint32_t wave = tid / kWave;
+    const uint32_t half = lane / C, cl = lane % C;
+    uint32_t *my_rows = rowtab + (wave * kSlots + half) * C;
+    const uint32_t slice = blockIdx.x % n_slices;
+    const uint32_t tq = blockIdx.x / n_slices;
+    const uint32_t n_q = 1u << n_anchors;
+    const uint32_t t = tq / n_q, q = tq % n_q;
+    const uint32_t sub_rows = 1u << (n_anchors + pe_dim);
+    const uint32_t pmask = (1u << pe_dim) - 1;
+    const uint32_t n_rows = batch * seq;
+    const uint32_t c0 = slice * C;
+    const int32_t beg = offsets[(size_t)t * (n_q + 1) + q];
+    const int32_t end = offsets[(size_t)t * (n_q + 1) + q + 1];
+    if (beg >= end) return;  // uniform over the workgroup
+
+    const int32_t *smp = samples + (size_t)t * n_rows;
+    const uint2 *kp = pack + (size_t)t * n_rows;
+    const uint32_t col = c0 + cl;
+    const float *sub = w + ((size_t)t * n_q + q) * sub_rows * n_outputs + c0;
+    const uint32_t n_e = sub_rows * (C / 4);
+    const uint32_t zero_off = sub_rows * C * 4;  // byte offset of the zero row
+    const uint8_t *tab_b = reinterpret_cast<const uint8_t *>(tab);
+
+    // the first chunk's item rows: loads in flight with the staging loads
+    uint32_t rr[kSfItems / kSfThreads];
+#pragma unroll
+    for (int u = 0; u < kSfItems / kSfThreads; u++) {
+        const uint32_t it = u * kSfThreads + tid;
+        rr[u] = (int32_t)it < end - beg ? (uint32_t)smp[beg + it] : 0u;
+    }
+    // stage the slice: C / 4 lanes per row, 16-byte loads (O % 4 == 0)
+    for (uint32_t e0 = 0; e0 < n_e; e0 += 8 * kSfThreads) {
+        f32x4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const uint32_t e = e0 + u * kSfThreads + tid;
+            const uint32_t r = e / (C / 4), c4 = (e % (C / 4)) * 4;
+            v[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (e < n_e && c0 + c4 < n_outputs)
+                v[u] = *reinterpret_cast<const f32x4 *>(sub + (size_t)r * n_outputs + c4);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const uint32_t e = e0 + u * kSfThreads + tid;
+            if (e < n_e) *reinterpret_cast<f32x4 *>(tab + (e / (C / 4)) * C + (e % (C / 4)) * 4) = v[u];
+        }
+    }
+    for (uint32_t d = tid; d + 1 < seq; d += kSfThreads)
+        ptab[d] = (uint16_t)(rec_idx(ppack[(size_t)t * (seq - 1) + d]) & pmask);
+    if (tid < (uint32_t)C) tab[sub_rows * C + tid] = 0.0f;
+
+    for (int32_t k0 = beg; k0 < end; k0 += kSfItems) {
+        const uint32_t n = (uint32_t)min((int32_t)kSfItems, end - k0);
+        uint32_t p2 = 1;
+        while (p2 < n) p2 <<= 1;
+        if (k0 != beg) {
+#pragma unroll
+            for (int u = 0; u < kSfItems / kSfThreads; u++) {
+                const uint32_t it = u * kSfThreads + tid;
+                rr[u] = it < n ? (uint32_t)smp[k0 + it] : 0u;
+            }
+        }
+        __syncthreads();  // staging done / the previous chunk is done with keys and irow
+        // key: (S - 1 - j) << 16 | item, so ascending order is longest-first
+#pragma unroll
+        for (int u = 0; u < kSfItems / kSfThreads; u++) {
+            const uint32_t it = u * kSfThreads + tid;
+            if (it < p2) {
+                irow[it] = rr[u];
+                keys[it] = it < n ? (((seq - 1 - rr[u] % seq) << 16) | it) : 0xFFFFFFFFu;
+            }
+        }
+        __syncthreads();
+        for (uint32_t k = 2; k <= p2; k <<= 1) {
+            for (uint32_t jj = k >> 1; jj > 0; jj >>= 1) {
+                for (uint32_t i = tid; i < p2; i += kSfThreads) {
+                    const uint32_t ixj = i ^ jj;
+                    if (ixj > i) {
+                        const uint32_t a = keys[i], c = keys[ixj];
+                        if (((i & k) == 0) == (a > c)) {
+                            keys[i] = c;
+                            keys[ixj] = a;
+                        }
+                    }
+                }
+                __syncthreads();
+            }
+        }
+        if (tid == 0) next_item = 0;
+        __syncthreads();
+        // items are taken kSlots at a time, longest first; the next group's rows
+        // and first key records are fetched while the current group runs
+        uint32_t base = 0;
+        if (lane == 0) base = atomicAdd(&next_item, (uint32_t)kSlots);
+        base = uniform(__shfl(base, 0, kWave));
+        uint32_t my = base + half;
+        bool have = my < n;
+        uint32_t row = have ? irow[keys[my] & 0xFFFFu] : 0u;
+        uint32_t j = have ? row % seq : 0u;
+        // key record words of positions i: loaded unconditionally (index clamped
+        // into the sample) one chunk ahead, and first read through an empty asm
+        // so the wait for them lands where they are used
+        const uint32_t *kw = reinterpret_cast<const uint32_t *>(kp) + 1;  // .y words
+        uint32_t rec = kw[2 * (row - j + min(cl, j > 0 ? j - 1 : 0u))];
+        while (base < n) {
+            uint32_t nbase = 0;
+            if (lane == 0) nbase = atomicAdd(&next_item, (uint32_t)kSlots);
+            nbase = uniform(__shfl(nbase, 0, kWave));
+            const uint32_t nmy = nbase + half;
+            const bool nhave = nmy < n;
+            const uint32_t nrow = nhave ? irow[keys[nmy] & 0xFFFFu] : 0u;
+            const uint32_t nj = nhave ? nrow % seq : 0u;
+            const uint32_t nrec = kw[2 * (nrow - nj + min(cl, nj > 0 ? nj - 1 : 0u))];
+
+            const uint32_t brow = row - j;  // b * S
+            // the wavefront walks to its longest item's j; shorter items read the
+            // zero row there (adding +0.0 leaves an fp64 sum that starts at +0.0
+            // unchanged: it can never be -0.0)
+            uint32_t jw = j;
+#pragma unroll
+            for (int o = C; o < kWave; o <<= 1) jw = max(jw, (uint32_t)__shfl_xor(jw, o, kWave));
+            jw = uniform(jw);
+            double acc = 0.0;
+            for (uint32_t i0 = 0; i0 < jw; i0 += C) {
+                // this chunk's C row offsets (bytes), one per lane
+                const uint32_t i = i0 + cl;
+                asm volatile("" : "+v"(rec));
+                my_rows[cl] = i < j ? (((((rec & 0xFFFFu) << pe_dim) | ptab[j - i - 1]) & (sub_rows - 1)) * C) * 4u
+                                    : zero_off;
+                rec = kw[2 * (brow + min(i + C, j > 0 ? j - 1 : 0u))];  // next chunk, in flight meanwhile
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+                for (int u = 0; u < C; u += 4) {
+                    const uint4 r4 = *reinterpret_cast<const uint4 *>(my_rows + u);
+                    const float v0 = *reinterpret_cast<const float *>(tab_b + r4.x + cl * 4);
+                    const float v1 = *reinterpret_cast<const float *>(tab_b + r4.y + cl * 4);
+                    const float v2 = *reinterpret_cast<const float *>(tab_b + r4.z + cl * 4);
+                    const float v3 = *reinterpret_cast<const float *>(tab_b + r4.w + cl * 4);
+                    acc += (double)v0;
+                    acc += (double)v1;
+                    acc += (double)v2;
+                    acc += (double)v3;
+                }
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            }
+            if (have && col < n_outputs) {
+                uint32_t v;
+                if (INT_MODE)
+                    v = (uint32_t)(j > 0 ? (int32_t)(acc * kDenom32 * int_rescaler) : 0);
+                else
+                    v = j > 0 ? __float_as_uint((float)acc) : 0x80000000u;
+                __builtin_nontemporal_store(v, part + ((size_t)t * n_rows + row) * n_outputs + col);
+            }
+            base = nbase;
+            have = nhave;
+            row = nrow;
+            j = nj;
+            rec = nrec;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // propagate_through_detectors_seq_fc_logic (proto:3629-3835), fp32 summation.
 constexpr int kDppHalfMirror = 0x141;
 constexpr int kDppXor1 = 0xB1;
@@ -272,21 +469,27 @@ __device__ __forceinline__ uint32_t rs_pair(uint32_t l) {
     return 4u * (l >= 4 ? 1u : 0u) + 2u * (l & 1u) + ((l >> 1) & 1u);
 }
 
+// Units (one wavefront each) are the (t, b*S + j) items in bucket order
+// (table, then Q value): each XCD takes a contiguous range of units (workgroup
+// i runs on XCD i % 8), so the 2^(Nc+Npe)-row sub-table (t, Q) the items of a
+// bucket read stays in that XCD's L2 while they run.
 template <int NJ>
 __global__ __launch_bounds__(kBlock) void k_propagate_seq(
     const float *__restrict__ w, const float *__restrict__ g, const uint2 *__restrict__ pack,
-    const uint2 *__restrict__ ppack, double *__restrict__ dq, double *__restrict__ dk,
-    double *__restrict__ dpe, uint32_t batch, uint32_t seq, uint32_t n_outputs,
-    uint32_t n_detectors, uint32_t n_anchors, uint32_t pe_dim) {
+    const uint2 *__restrict__ ppack, const int32_t *__restrict__ samples, double *__restrict__ dq,
+    double *__restrict__ dk, double *__restrict__ dpe, uint32_t batch, uint32_t seq,
+    uint32_t n_outputs, uint32_t n_detectors, uint32_t n_anchors, uint32_t pe_dim,
+    uint32_t wg_per_xcd) {
     const uint32_t lane = threadIdx.x & (kWave - 1);
     const uint32_t wave = uniform(threadIdx.x / kWave);
-    const uint32_t unit = blockIdx.x * kWPB + wave;
-    const uint32_t per_bt = seq - 1;
-    const uint32_t bt = unit / per_bt;
-    if (bt >= batch * n_detectors) return;
-    const uint32_t j = seq - 1 - unit % per_bt;  // long rows first
-    const uint32_t b = bt / n_detectors, t = bt % n_detectors;
     const uint32_t n_rows = batch * seq;
+    const uint32_t wg = (blockIdx.x % 8) * wg_per_xcd + blockIdx.x / 8;
+    const uint32_t unit = wg * kWPB + wave;
+    if (unit >= n_detectors * n_rows) return;
+    const uint32_t t = unit / n_rows;
+    const uint32_t row = (uint32_t)samples[unit];
+    const uint32_t j = row % seq, b = row / seq;
+    if (j == 0) return;
     const uint32_t kbits = n_anchors + pe_dim;
     const uint32_t pmask = (1u << pe_dim) - 1;
     const uint2 *kp = pack + (size_t)t * n_rows + (size_t)b * seq;
@@ -713,6 +916,21 @@ uint32_t seq_vec(uint32_t n_outputs) {
     return 1;
 }
 
+// Columns of a forward slice for k_fill_seq_lds (0: it does not apply): the
+// widest power of two <= 64 whose sub-table slice fits the LDS table.
+uint32_t seq_fill_cols(const SeqShape &s) {
+    const uint64_t sub_rows = 1ull << (s.n_anchors + s.pe_dim);
+    const uint64_t rows = (uint64_t)s.batch * s.seq;
+    if (s.n_outputs % 4 != 0 || s.seq - 1 > (uint32_t)kSfPe || rows > 0x7fffffffull ||
+        (uint64_t)s.n_detectors * rows * s.n_outputs * 4 > (8ull << 30))
+        return 0;
+    uint32_t cols = 64;
+    while (cols > 8 && sub_rows * cols > (uint64_t)kSfTabFloats) cols /= 2;
+    if (sub_rows * cols > (uint64_t)kSfTabFloats) return 0;
+    while (cols > 8 && cols / 2 >= s.n_outputs) cols /= 2;
+    return cols;
+}
+
 // Columns of a weight-gradient slice (0: the sort path does not apply): a
 // power of two with sub_rows * C <= 1024 threads x 32 outputs and the batch's
 // gradient rows (>= 1 item of C columns) in LDS.
@@ -741,10 +959,17 @@ uint32_t seq_wg_items(const SeqShape &s, uint32_t cols) {
 //          bucket offsets [T][2^Nc+1] | samples [T][B*S] | commit values [B*S][O]
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// forward scratch: pack | ppack | [bucket offsets | samples | partials [T][B*S][O]]
 size_t seq_scratch_bytes(const SeqShape &s, bool backward) {
     const size_t rows = (size_t)s.batch * s.seq;
     size_t n = align256(rows * s.n_detectors * 8) + align256((size_t)s.n_detectors * (s.seq - 1) * 8);
-    if (!backward) return n;
+    if (!backward) {
+        if (seq_fill_cols(s) == 0) return n;
+        n += align256((size_t)s.n_detectors * ((1u << s.n_anchors) + 1) * 4);
+        n += align256((size_t)s.n_detectors * rows * 4);
+        n += align256((size_t)s.n_detectors * rows * s.n_outputs * 4);
+        return n;
+    }
     n += 2 * align256(rows * s.n_detectors * 8);
     n += align256((size_t)(s.seq - 1) * s.n_detectors * std::max<uint32_t>(s.pe_dim, 1) * 8);
     n += align256((size_t)s.n_detectors * ((1u << s.n_anchors) + 1) * 4);
@@ -792,6 +1017,36 @@ hipError_t launch_forward_seq(const SeqShape &s, const float *w, const float *x,
                        (const int32_t *)nullptr, ppack, s.seq - 1, s.n_detectors);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
+    const uint32_t fcols = seq_fill_cols(s);
+    if (fcols > 0) {
+        size_t off = align256((size_t)rows * s.n_detectors * 8) + align256((size_t)s.n_detectors * (s.seq - 1) * 8);
+        int32_t *offsets = reinterpret_cast<int32_t *>(sp + off);
+        off += align256((size_t)s.n_detectors * ((1u << s.n_anchors) + 1) * 4);
+        int32_t *samples = reinterpret_cast<int32_t *>(sp + off);
+        off += align256((size_t)s.n_detectors * rows * 4);
+        uint32_t *part = reinterpret_cast<uint32_t *>(sp + off);
+        FcShape fs2 = fs;
+        e = launch_bucket_samples(fs2, idx, offsets, samples, st);
+        if (e != hipSuccess) return e;
+        const uint32_t n_slices = (s.n_outputs + fcols - 1) / fcols;
+        const uint64_t grid = (uint64_t)s.n_detectors * (1u << s.n_anchors) * n_slices;
+        if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
+#define SPIKY_FLDS(C, IM)                                                                          \
+    hipLaunchKernelGGL((k_fill_seq_lds<C, IM>), dim3((uint32_t)grid), dim3(kSfThreads), 0, st, w,    \
+                       pack, ppack, offsets, samples, part, s.batch, s.seq, s.n_outputs,            \
+                       s.n_anchors, s.pe_dim, n_slices, int_rescaler)
+        switch (fcols) {
+            case 64: if (int_mode) SPIKY_FLDS(64, true); else SPIKY_FLDS(64, false); break;
+            case 32: if (int_mode) SPIKY_FLDS(32, true); else SPIKY_FLDS(32, false); break;
+            case 16: if (int_mode) SPIKY_FLDS(16, true); else SPIKY_FLDS(16, false); break;
+            default: if (int_mode) SPIKY_FLDS(8, true); else SPIKY_FLDS(8, false); break;
+        }
+#undef SPIKY_FLDS
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        return launch_block_commit(part, out, (uint64_t)rows * s.n_outputs, s.n_detectors, int_mode,
+                                   int_rescaler, st);
+    }
     const uint32_t vec = seq_vec(s.n_outputs);
     const uint32_t n_slices = (s.n_outputs + kWave * vec - 1) / (kWave * vec);
     const uint64_t units = (uint64_t)s.batch * (s.seq - 1);
@@ -856,6 +1111,20 @@ hipError_t launch_backward_seq(const SeqShape &s, float *w, const float *g, cons
     if (e != hipSuccess) return e;
     const int2 *ap = reinterpret_cast<const int2 *>(anchors);
 
+    FcShape fs{};
+    fs.batch = rows;
+    fs.n_inputs = s.n_inputs;
+    fs.n_outputs = s.n_outputs;
+    fs.n_detectors = s.n_detectors;
+    fs.n_anchors = s.n_anchors;
+    fs.n_entries = 1u << s.n_anchors;
+    fs.dgs = s.dgs;
+    fs.ogs = s.ogs;
+    // (t, Q) buckets of the rows: the propagate's schedule and the weight
+    // gradient's sub-tables
+    e = launch_bucket_samples(fs, idx, offsets, samples, st);
+    if (e != hipSuccess) return e;
+
     // input and positional gradients
     const uint32_t nj = (s.n_outputs + 255) / 256;
     if (!int_mode && s.n_outputs % 4 == 0 && nj <= 4) {
@@ -863,13 +1132,15 @@ hipError_t launch_backward_seq(const SeqShape &s, float *w, const float *g, cons
         hipLaunchKernelGGL(k_zero64, dim3(blocks_for(n_acc)), dim3(kBlock), 0, st, dq, n_acc);
         hipLaunchKernelGGL(k_zero64, dim3(blocks_for(n_acc)), dim3(kBlock), 0, st, dk, n_acc);
         hipLaunchKernelGGL(k_zero64, dim3(blocks_for(n_dpe)), dim3(kBlock), 0, st, dpe, (uint64_t)n_dpe);
-        const uint64_t units = (uint64_t)s.batch * s.n_detectors * (s.seq - 1);
-        const uint64_t grid = (units + kWPB - 1) / kWPB;
-        if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
+        const uint64_t units = (uint64_t)rows * s.n_detectors;
+        const uint64_t n_wg = (units + kWPB - 1) / kWPB;
+        const uint64_t wg_per_xcd = (n_wg + 7) / 8;
+        const uint64_t grid = wg_per_xcd * 8;
+        if (grid > 0x7fffffffu || units > 0xffffffffull) return hipErrorInvalidConfiguration;
 #define SPIKY_PSEQ(NJ)                                                                            \
     hipLaunchKernelGGL(k_propagate_seq<NJ>, dim3((uint32_t)grid), dim3(kBlock), 0, st, w, g, pack, \
-                       ppack, dq, dk, dpe, s.batch, s.seq, s.n_outputs, s.n_detectors, s.n_anchors, \
-                       s.pe_dim)
+                       ppack, samples, dq, dk, dpe, s.batch, s.seq, s.n_outputs, s.n_detectors,     \
+                       s.n_anchors, s.pe_dim, (uint32_t)wg_per_xcd)
         switch (nj) {
             case 1: SPIKY_PSEQ(1); break;
             case 2: SPIKY_PSEQ(2); break;
@@ -911,21 +1182,10 @@ hipError_t launch_backward_seq(const SeqShape &s, float *w, const float *g, cons
     if (e != hipSuccess || target == nullptr) return e;
 
     // weight gradient (or the in-place update of the weights)
-    FcShape fs{};
-    fs.batch = rows;
-    fs.n_inputs = s.n_inputs;
-    fs.n_outputs = s.n_outputs;
-    fs.n_detectors = s.n_detectors;
-    fs.n_anchors = s.n_anchors;
-    fs.n_entries = 1u << s.n_anchors;
-    fs.dgs = s.dgs;
-    fs.ogs = s.ogs;
     e = launch_wgrad_commit_values(g, cv, (uint64_t)rows * s.n_outputs, lr, int_mode, int_rescaler, st);
     if (e != hipSuccess) return e;
     const uint32_t cols = seq_wg_cols(s);
     if (cols > 0) {
-        e = launch_bucket_samples(fs, idx, offsets, samples, st);
-        if (e != hipSuccess) return e;
         const uint32_t n_slices = (s.n_outputs + cols - 1) / cols;
         const uint64_t grid = (uint64_t)s.n_detectors * (1u << s.n_anchors) * n_slices;
         if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;

@@ -627,6 +627,21 @@ hipError_t launch_fill_tm(const FcShape &s, const float *w, const int32_t *idx, 
     return hipGetLastError();
 }
 
+hipError_t launch_block_commit(const uint32_t *part, float *out, uint64_t n, uint32_t n_blocks,
+                               bool int_mode, double int_rescaler, hipStream_t st) {
+    if (n % 4 != 0) return hipErrorInvalidValue;
+    const uint64_t n_quads = n / 4;
+    const uint64_t cgrid = (n_quads + 255) / 256;
+    if (cgrid > 0x7fffffffu) return hipErrorInvalidConfiguration;
+    if (int_mode)
+        hipLaunchKernelGGL(k_fill_commit<true>, dim3((uint32_t)cgrid), dim3(256), 0, st, part, out,
+                           n_quads, n_blocks, n, int_rescaler);
+    else
+        hipLaunchKernelGGL(k_fill_commit<false>, dim3((uint32_t)cgrid), dim3(256), 0, st, part, out,
+                           n_quads, n_blocks, n, int_rescaler);
+    return hipGetLastError();
+}
+
 bool tm_propagate_applies(const FcShape &s) {
     const uint64_t n_slices = (s.n_outputs + kTmCols - 1) / kTmCols;
     return s.batch >= 256 && s.n_entries <= (uint32_t)kTmMaxEntries && s.n_outputs % 4 == 0 &&
