@@ -27,11 +27,11 @@
 //                       with sequential block dots and integer payloads, so the
 //                       int32 accumulators are bit-identical.
 //   k_seq_xgrad         x_grad[b][s][anchor] +-= du(b, t, s) for every table.
-//   k_wgrad_seq_sort    one workgroup per (table, Q value, column slice): the
-//                       gradient of that sub-table slice (2^(Nc+Npe) rows x C
-//                       columns) is summed in registers from every (b, j) whose
-//                       Q is that value, after an LDS counting sort of the
-//                       (b, j, i) entries by target row, and written once.
+//   k_wgrad_seq_sort    one workgroup per (table, Q value): an LDS counting sort
+//                       of the (b, j, i) entries of every (b, j) whose Q is that
+//                       value by target row, then per column slice the
+//                       sub-table's gradient (2^(Nc+Npe) rows x C columns) is
+//                       summed in registers and written once.
 #include "lut_kernels.h"
 
 #include <algorithm>
@@ -462,6 +462,16 @@ __device__ __forceinline__ void rs16_step(double (&v)[16], int m, bool upper) {
     }
 }
 
+template <int CTRL, int NV>
+__device__ __forceinline__ void rs_any(double (&v)[NV], int m, bool upper) {
+#pragma unroll
+    for (int jj = 0; jj < m; jj++) {
+        const double send = upper ? v[jj] : v[m + jj];
+        const double keep = upper ? v[m + jj] : v[jj];
+        v[jj] = keep + dpp_f64<CTRL>(send);
+    }
+}
+
 // 16 items per lane, the 8 lanes of a group hold column pieces: afterwards lane
 // l holds the group sums of items 2u, 2u+1 with u = 4*(l>=4) + 2*(l&1) + ((l>>1)&1)
 // in v[0], v[1].
@@ -469,25 +479,53 @@ __device__ __forceinline__ uint32_t rs_pair(uint32_t l) {
     return 4u * (l >= 4 ? 1u : 0u) + 2u * (l & 1u) + ((l >> 1) & 1u);
 }
 
-// Units (one wavefront each) are the (t, b*S + j) items in bucket order
-// (table, then Q value): each XCD takes a contiguous range of units (workgroup
-// i runs on XCD i % 8), so the 2^(Nc+Npe)-row sub-table (t, Q) the items of a
-// bucket read stays in that XCD's L2 while they run.
-template <int NJ>
+// Two passes, each over (t, b*S + j) items in bucket order, one workgroup per
+// item (its wavefronts take the pairs i < j kPB at a time).  Workgroup i runs
+// on XCD i % 8 and each XCD takes a contiguous range of items, so the sub-table
+// a bucket's items read stays in that XCD's L2 while they run.
+//   ALT = false, items bucketed by Q: for each pair, the main row
+//     (Q, K_i, P) and, for a K flip, the flipped row (Q, K_i ^ bit, P) and, for
+//     a PE flip, (Q, K_i, P ^ bit): fp64 dots with g[b][j] (DPP
+//     reduce-scatter), du-scaled and added to dk[b][t][i] / dpe with fp64
+//     atomics.  The main rows of the Q-flip pairs are summed instead.
+//   ALT = true, items bucketed by Q' = Q ^ (1 << minIdx_j): the flipped rows
+//     (Q', K_i, P) of the Q-flip pairs are summed.
+// Each pass stores g[b][j] . (its row sum) into qsum[b][t][j]; the Q-flip
+// term of (b, t, j) is du(minDelta_j) * (main sum - flipped sum), formed in
+// k_seq_xgrad (the reference's per-pair main_grad_sum - alt_grad_sum,
+// proto:3740-3783, summed over the pairs first).
+// A batch's pair records are decoded by lanes 0..kPB-1 and broadcast with
+// readlane; all of its row loads are issued before any of them is used.
+constexpr uint32_t kPfMain = 1, kPfK = 2, kPfPe = 4, kPfQ = 8;
+
+template <int NV>
+__device__ __forceinline__ void rs_steps(double (&v)[NV], uint32_t l8) {
+    // reduce-scatter NV values over the 8 lanes of a group (bits of l8 from
+    // the top), then plain sums over the bits left
+    if (NV >= 2) rs_any<kDppHalfMirror, NV>(v, NV / 2, l8 >= 4);
+    if (NV >= 4) rs_any<kDppXor1, NV>(v, NV / 4, (l8 & 1) != 0);
+    if (NV >= 8) rs_any<kDppXor2, NV>(v, NV / 8, ((l8 >> 1) & 1) != 0);
+    if (NV < 4) v[0] += dpp_f64<kDppXor1>(v[0]);
+    if (NV < 8) v[0] += dpp_f64<kDppXor2>(v[0]);
+}
+
+template <int NJ, bool ALT>
 __global__ __launch_bounds__(kBlock) void k_propagate_seq(
     const float *__restrict__ w, const float *__restrict__ g, const uint2 *__restrict__ pack,
-    const uint2 *__restrict__ ppack, const int32_t *__restrict__ samples, double *__restrict__ dq,
+    const uint2 *__restrict__ ppack, const int32_t *__restrict__ samples, double *__restrict__ qsum,
     double *__restrict__ dk, double *__restrict__ dpe, uint32_t batch, uint32_t seq,
     uint32_t n_outputs, uint32_t n_detectors, uint32_t n_anchors, uint32_t pe_dim,
     uint32_t wg_per_xcd) {
+    constexpr int kPB = NJ == 1 ? 4 : (NJ == 2 ? 2 : 1);  // pairs per batch
+    constexpr int kNV = 2 * kPB;
+    __shared__ double wpart[kWPB];
     const uint32_t lane = threadIdx.x & (kWave - 1);
     const uint32_t wave = uniform(threadIdx.x / kWave);
     const uint32_t n_rows = batch * seq;
-    const uint32_t wg = (blockIdx.x % 8) * wg_per_xcd + blockIdx.x / 8;
-    const uint32_t unit = wg * kWPB + wave;
-    if (unit >= n_detectors * n_rows) return;
-    const uint32_t t = unit / n_rows;
-    const uint32_t row = (uint32_t)samples[unit];
+    const uint32_t item = (blockIdx.x % 8) * wg_per_xcd + blockIdx.x / 8;
+    if (item >= n_detectors * n_rows) return;
+    const uint32_t t = item / n_rows;
+    const uint32_t row = (uint32_t)samples[item];
     const uint32_t j = row % seq, b = row / seq;
     if (j == 0) return;
     const uint32_t kbits = n_anchors + pe_dim;
@@ -495,6 +533,12 @@ __global__ __launch_bounds__(kBlock) void k_propagate_seq(
     const uint2 *kp = pack + (size_t)t * n_rows + (size_t)b * seq;
     const uint2 *pp = ppack + (size_t)t * (seq - 1);
     const float *wt = w + (size_t)t * (1u << (n_anchors + kbits)) * n_outputs;
+    const uint2 qr = kp[j];
+    const int32_t qm = rec_mi(qr);
+    if (ALT && qm < 0) return;
+    const uint32_t Q = rec_idx(qr);
+    const float qd = rec_md(qr);
+    const uint32_t qsub = ALT ? (Q ^ (1u << qm)) : Q;  // the sub-table read
 
     float gv[NJ][4];
     bool act[NJ];
@@ -509,89 +553,300 @@ __global__ __launch_bounds__(kBlock) void k_propagate_seq(
         gv[jj][2] = q.z;
         gv[jj][3] = q.w;
     }
-    const uint2 qr = kp[j];
-    const uint32_t Q = rec_idx(qr);
-    const int32_t qm = rec_mi(qr);
-    const float qd = rec_md(qr);
     const uint32_t l8 = lane & 7;
-    const uint32_t my_u = rs_pair(l8);
-    double q_acc = 0.0;
-
-    for (uint32_t i0 = 0; i0 < j; i0 += 8) {
-        const uint32_t n = min(8u, j - i0);
-        double items[16];
+    double rsum[NJ][4];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const uint32_t i = i0 + min((uint32_t)u, n - 1);
+    for (int jj = 0; jj < NJ; jj++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) rsum[jj][v] = 0.0;
+
+    for (uint32_t i0 = wave * kPB; i0 < j; i0 += kPB * kWPB) {
+        const uint32_t n = min((uint32_t)kPB, j - i0);
+        // decode the batch's pairs, one per lane
+        uint32_t v_main = 0, v_alt = 0, v_pe = 0, v_flags = 0;
+        if (lane < n) {
+            const uint32_t i = i0 + lane;
+            const uint2 kr = kp[i];
+            const uint2 pr = pp[j - i - 1];
+            const uint32_t K = rec_idx(kr), P = rec_idx(pr) & pmask;
+            const float kd = rec_md(kr);
+            const bool qflip = fabsf(qd) < fabsf(kd);
+            v_main = (qsub << kbits) | (K << pe_dim) | P;
+            if (ALT) {
+                v_flags = qflip ? (kPfMain | kPfQ) : 0u;
+            } else {
+                const int32_t km = rec_mi(kr), pm = rec_mi(pr);
+                const float pdl = rec_md(pr);
+                const bool kflip = !qflip && km >= 0;
+                const bool peflip = pe_dim > 0 && pm >= 0 && fabsf(pdl) < fabsf(qd) && fabsf(pdl) < fabsf(kd);
+                const bool qs = qflip && qm >= 0;
+                v_alt = v_main ^ (kflip ? (1u << (km + pe_dim)) : 0u);
+                v_pe = v_main ^ (peflip ? (1u << pm) : 0u);
+                v_flags = (kflip ? kPfK : 0u) | (peflip ? kPfPe : 0u) | (qs ? kPfQ : 0u);
+                if (v_flags) v_flags |= kPfMain;
+            }
+        }
+        f32x4 m[kPB][NJ], a[kPB][NJ], e[kPB][NJ];
+        uint32_t fl[kPB];
+#pragma unroll
+        for (int u = 0; u < kPB; u++) {
+            fl[u] = (uint32_t)__builtin_amdgcn_readlane((int)v_flags, u);
+            const uint32_t mr = (uint32_t)__builtin_amdgcn_readlane((int)v_main, u);
+            const uint32_t ar = (uint32_t)__builtin_amdgcn_readlane((int)v_alt, u);
+            const uint32_t er = (uint32_t)__builtin_amdgcn_readlane((int)v_pe, u);
+#pragma unroll
+            for (int jj = 0; jj < NJ; jj++) {
+                const uint32_t c = (jj * kWave + lane) * 4;
+                m[u][jj] = f32x4{0.f, 0.f, 0.f, 0.f};
+                a[u][jj] = m[u][jj];
+                e[u][jj] = m[u][jj];
+                if (!act[jj]) continue;
+                if (fl[u] & kPfMain) m[u][jj] = *reinterpret_cast<const f32x4 *>(wt + (size_t)mr * n_outputs + c);
+                if (!ALT && (fl[u] & kPfK)) a[u][jj] = *reinterpret_cast<const f32x4 *>(wt + (size_t)ar * n_outputs + c);
+                if (!ALT && (fl[u] & kPfPe)) e[u][jj] = *reinterpret_cast<const f32x4 *>(wt + (size_t)er * n_outputs + c);
+            }
+        }
+        double items[kNV];
+#pragma unroll
+        for (int u = 0; u < kPB; u++) {
+            double d1 = 0.0, d2 = 0.0;
+#pragma unroll
+            for (int jj = 0; jj < NJ; jj++) {
+                if (fl[u] & kPfQ) {
+#pragma unroll
+                    for (int v = 0; v < 4; v++) rsum[jj][v] += (double)m[u][jj][v];
+                }
+                if (!ALT && (fl[u] & kPfK)) {
+#pragma unroll
+                    for (int v = 0; v < 4; v++) d1 += ((double)m[u][jj][v] - (double)a[u][jj][v]) * (double)gv[jj][v];
+                }
+                if (!ALT && (fl[u] & kPfPe)) {
+#pragma unroll
+                    for (int v = 0; v < 4; v++) d2 += ((double)m[u][jj][v] - (double)e[u][jj][v]) * (double)gv[jj][v];
+                }
+            }
+            items[2 * u] = d1;
+            items[2 * u + 1] = d2;
+        }
+        if (ALT) continue;
+        rs_steps<kNV>(items, l8);
+#pragma unroll
+        for (int s = 8; s < kWave; s <<= 1) items[0] += __shfl_xor(items[0], s, kWave);
+        // lanes 0..7: value vi of the batch (pair vi / 2; d1 if even, d2 if odd)
+        const uint32_t vi = kNV == 8 ? rs_pair(l8) : (kNV == 4 ? 2u * (l8 >= 4 ? 1u : 0u) + (l8 & 1u) : (l8 >= 4 ? 1u : 0u));
+        const uint32_t u = vi / 2;
+        if (lane < 8 && u < n && (kNV == 8 || (kNV == 4 ? ((l8 >> 1) & 1u) == 0 : (l8 & 3u) == 0))) {
+            const uint32_t i = i0 + u;
+            const uint2 kr = kp[i];
+            if ((vi & 1u) == 0) {
+                const float kd = rec_md(kr);
+                if (!(fabsf(qd) < fabsf(kd)) && rec_mi(kr) >= 0)
+                    atomicAdd(dk + ((size_t)b * n_detectors + t) * seq + i, du_of_margin(kd) * items[0]);
+            } else {
+                const uint2 pr = pp[j - i - 1];
+                const int32_t pm = rec_mi(pr);
+                const float kd = rec_md(kr), pdl = rec_md(pr);
+                if (pe_dim > 0 && pm >= 0 && fabsf(pdl) < fabsf(qd) && fabsf(pdl) < fabsf(kd))
+                    atomicAdd(dpe + ((size_t)(j - i - 1) * n_detectors + t) * pe_dim + pm,
+                              du_of_margin(pdl) * items[0]);
+            }
+        }
+    }
+    // g[b][j] . row sum, over the lanes and then the wavefronts
+    double s = 0.0;
+#pragma unroll
+    for (int jj = 0; jj < NJ; jj++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) s += rsum[jj][v] * (double)gv[jj][v];
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) s += __shfl_xor(s, o, kWave);
+    if (lane == 0) wpart[wave] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double tot = 0.0;
+        for (int k = 0; k < kWPB; k++) tot += wpart[k];
+        qsum[((size_t)b * n_detectors + t) * seq + j] = tot;
+    }
+}
+
+// Main pass, pair-parallel form (fp32 summation, O % 4 == 0, O <= kPairMaxO):
+// one 256-thread workgroup per (t, b*S + j) item in (t, Q) bucket order
+// (XCD-local as above).  g[b][j] is staged in LDS as fp64.  A wavefront takes
+// 8 pairs at a time, 8 lanes per pair; lane s of a pair owns the 4-column
+// pieces c = 4 * (s + 8k), so each 8-lane group reads 128 contiguous bytes of
+// a row per load.  Per pair the lanes form the fp64 dots of g with the main
+// row, the K-flipped row (K flips) and the PE-flipped row (PE flips) --
+// the reference's main / alt grad sums (proto:3740-3834) over all outputs --
+// and reduce them over the 8 lanes with DPP.  Results, without atomics:
+//   tk[b][t][j][i] = main - kalt for a K flip, else 0;
+//   tp[b][t][j][i] = main - pealt for a PE flip, else 0;
+//   qsum[b][t][j]  = sum of main over the Q-flip pairs.
+// The triangles are [j*(j-1)/2 + i] per (b, t); k_seq_tri_reduce sums them.
+constexpr int kPairMaxO = 2048;  // a multiple of 128 (groups of 4 chunks)
+
+__global__ __launch_bounds__(kBlock) void k_propagate_seq_pairs(
+    const float *__restrict__ w, const float *__restrict__ g, const uint2 *__restrict__ pack,
+    const uint2 *__restrict__ ppack, const int32_t *__restrict__ samples, double *__restrict__ qsum,
+    double *__restrict__ tk, double *__restrict__ tp, uint32_t batch, uint32_t seq,
+    uint32_t n_outputs, uint32_t n_detectors, uint32_t n_anchors, uint32_t pe_dim,
+    uint32_t wg_per_xcd) {
+    __shared__ __attribute__((aligned(16))) double gd[kPairMaxO];
+    __shared__ double wpart[kWPB];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & (kWave - 1);
+    const uint32_t wave = uniform(tid / kWave);
+    const uint32_t n_rows = batch * seq;
+    const uint32_t item = (blockIdx.x % 8) * wg_per_xcd + blockIdx.x / 8;
+    if (item >= n_detectors * n_rows) return;
+    const uint32_t t = item / n_rows;
+    const uint32_t row = (uint32_t)samples[item];
+    const uint32_t j = row % seq, b = row / seq;
+    if (j == 0) return;
+    const uint32_t kbits = n_anchors + pe_dim;
+    const uint32_t pmask = (1u << pe_dim) - 1;
+    const uint2 *kp = pack + (size_t)t * n_rows + (size_t)b * seq;
+    const uint2 *pp = ppack + (size_t)t * (seq - 1);
+    const float *wt = w + (size_t)t * (1u << (n_anchors + kbits)) * n_outputs;
+    const uint2 qr = kp[j];
+    const int32_t qm = rec_mi(qr);
+    const uint32_t Q = rec_idx(qr);
+    const float qd = rec_md(qr);
+    const uint32_t n_chunks = (n_outputs + 31) / 32;  // 32 columns per chunk (8 lanes x 4)
+    // g in fp64, zero past the last output up to whole groups of 4 chunks
+    // (the clamped loads there add 0)
+    for (uint32_t c = tid; c < ((n_chunks + 3) / 4) * 128; c += kBlock)
+        gd[c] = c < n_outputs ? (double)g[((size_t)b * seq + j) * n_outputs + c] : 0.0;
+    __syncthreads();
+
+    const uint32_t p = lane / 8, s = lane % 8;
+    const size_t tri = ((size_t)b * n_detectors + t) * ((size_t)seq * (seq - 1) / 2) + (size_t)j * (j - 1) / 2;
+    double qacc = 0.0;
+    for (uint32_t i0 = wave * 8; i0 < j; i0 += 8 * kWPB) {
+        const uint32_t i = i0 + p;
+        const bool live = i < j;
+        uint32_t mrow = 0, arow = 0, erow = 0;
+        bool kflip = false, peflip = false, qs = false;
+        if (live) {
             const uint2 kr = kp[i];
             const uint2 pr = pp[j - i - 1];
             const uint32_t K = rec_idx(kr), P = rec_idx(pr) & pmask;
             const int32_t km = rec_mi(kr), pm = rec_mi(pr);
             const float kd = rec_md(kr), pdl = rec_md(pr);
             const bool qflip = fabsf(qd) < fabsf(kd);
-            const int32_t fm = qflip ? qm : km;
-            const uint32_t main_row = (Q << kbits) | (K << pe_dim) | P;
-            uint32_t alt_row = main_row;
-            if (fm >= 0) alt_row = qflip ? (main_row ^ (1u << (fm + kbits))) : (main_row ^ (1u << (fm + pe_dim)));
-            const bool peflip = pe_dim > 0 && pm >= 0 && fabsf(pdl) < fabsf(qd) && fabsf(pdl) < fabsf(kd);
-            const uint32_t pe_row = peflip ? (main_row ^ (1u << pm)) : main_row;
-            double d1 = 0.0, d2 = 0.0;
-#pragma unroll
-            for (int jj = 0; jj < NJ; jj++) {
-                if (!act[jj]) continue;
-                const uint32_t c = (jj * kWave + lane) * 4;
-                const float4 m = *reinterpret_cast<const float4 *>(wt + (size_t)main_row * n_outputs + c);
-                const float4 a = *reinterpret_cast<const float4 *>(wt + (size_t)alt_row * n_outputs + c);
-                d1 += ((double)m.x - (double)a.x) * (double)gv[jj][0];
-                d1 += ((double)m.y - (double)a.y) * (double)gv[jj][1];
-                d1 += ((double)m.z - (double)a.z) * (double)gv[jj][2];
-                d1 += ((double)m.w - (double)a.w) * (double)gv[jj][3];
-                if (peflip) {
-                    const float4 e = *reinterpret_cast<const float4 *>(wt + (size_t)pe_row * n_outputs + c);
-                    d2 += ((double)m.x - (double)e.x) * (double)gv[jj][0];
-                    d2 += ((double)m.y - (double)e.y) * (double)gv[jj][1];
-                    d2 += ((double)m.z - (double)e.z) * (double)gv[jj][2];
-                    d2 += ((double)m.w - (double)e.w) * (double)gv[jj][3];
-                }
-            }
-            items[2 * u] = d1;
-            items[2 * u + 1] = d2;
+            kflip = !qflip && km >= 0;
+            peflip = pe_dim > 0 && pm >= 0 && fabsf(pdl) < fabsf(qd) && fabsf(pdl) < fabsf(kd);
+            qs = qflip && qm >= 0;
+            mrow = (Q << kbits) | (K << pe_dim) | P;
+            arow = kflip ? (mrow ^ (1u << (km + pe_dim))) : mrow;
+            erow = peflip ? (mrow ^ (1u << pm)) : mrow;
         }
-        // reduce-scatter inside each 8-lane group, then sum the 8 groups
-        rs16_step<kDppHalfMirror>(items, 8, l8 >= 4);
-        rs16_step<kDppXor1>(items, 4, (l8 & 1) != 0);
-        rs16_step<kDppXor2>(items, 2, ((l8 >> 1) & 1) != 0);
+        // every lane loads all three rows (a row that is not flipped is the main
+        // row again, whose dot then equals the main dot exactly): no divergent
+        // loads; columns past the last output re-read the last 4 and meet g = 0
+        double ms = 0.0, as = 0.0, es = 0.0;
+        const float *mp = wt + (size_t)mrow * n_outputs;
+        const float *ap = wt + (size_t)arow * n_outputs;
+        const float *ep = wt + (size_t)erow * n_outputs;
+        for (uint32_t k0 = 0; k0 < n_chunks; k0 += 4) {
+            f32x4 mv[4], av[4], ev[4];
 #pragma unroll
-        for (int s = 8; s < kWave; s <<= 1) {
-            items[0] += __shfl_xor(items[0], s, kWave);
-            items[1] += __shfl_xor(items[1], s, kWave);
-        }
-        // lanes 0..7 hold the totals of pair my_u
-        if (lane < 8 && my_u < n) {
-            const uint32_t i = i0 + my_u;
-            const uint2 kr = kp[i];
-            const uint2 pr = pp[j - i - 1];
-            const int32_t km = rec_mi(kr), pm = rec_mi(pr);
-            const float kd = rec_md(kr), pdl = rec_md(pr);
-            const bool qflip = fabsf(qd) < fabsf(kd);
-            const int32_t fm = qflip ? qm : km;
-            if (fm >= 0) {
-                const double du = du_of_margin(qflip ? qd : kd) * items[0];
-                if (qflip)
-                    q_acc += du;
-                else
-                    atomicAdd(dk + ((size_t)b * n_detectors + t) * seq + i, du);
+            for (int k = 0; k < 4; k++) {
+                const uint32_t c = min((k0 + k) * 32 + 4 * s, n_outputs - 4);
+                mv[k] = *reinterpret_cast<const f32x4 *>(mp + c);
+                av[k] = *reinterpret_cast<const f32x4 *>(ap + c);
+                ev[k] = *reinterpret_cast<const f32x4 *>(ep + c);
             }
-            if (pe_dim > 0 && pm >= 0 && fabsf(pdl) < fabsf(qd) && fabsf(pdl) < fabsf(kd))
-                atomicAdd(dpe + ((size_t)(j - i - 1) * n_detectors + t) * pe_dim + pm,
-                          du_of_margin(pdl) * items[1]);
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t c = (k0 + k) * 32 + 4 * s;
+                const double2 g01 = *reinterpret_cast<const double2 *>(gd + c);
+                const double2 g23 = *reinterpret_cast<const double2 *>(gd + c + 2);
+                ms += (double)mv[k][0] * g01.x;
+                ms += (double)mv[k][1] * g01.y;
+                ms += (double)mv[k][2] * g23.x;
+                ms += (double)mv[k][3] * g23.y;
+                as += (double)av[k][0] * g01.x;
+                as += (double)av[k][1] * g01.y;
+                as += (double)av[k][2] * g23.x;
+                as += (double)av[k][3] * g23.y;
+                es += (double)ev[k][0] * g01.x;
+                es += (double)ev[k][1] * g01.y;
+                es += (double)ev[k][2] * g23.x;
+                es += (double)ev[k][3] * g23.y;
+            }
+        }
+        // sums over the 8 lanes of the pair
+        ms += dpp_f64<kDppXor1>(ms);
+        as += dpp_f64<kDppXor1>(as);
+        es += dpp_f64<kDppXor1>(es);
+        ms += dpp_f64<kDppXor2>(ms);
+        as += dpp_f64<kDppXor2>(as);
+        es += dpp_f64<kDppXor2>(es);
+        ms += dpp_f64<kDppHalfMirror>(ms);
+        as += dpp_f64<kDppHalfMirror>(as);
+        es += dpp_f64<kDppHalfMirror>(es);
+        if (live && s == 0) {
+            tk[tri + i] = kflip ? ms - as : 0.0;
+            tp[tri + i] = peflip ? ms - es : 0.0;
+            if (qs) qacc += ms;
         }
     }
-    // the wave's Q-flip total for (b, t, j): lanes 0..7 hold the pieces
-    double s = lane < 8 ? q_acc : 0.0;
 #pragma unroll
-    for (int o = 1; o < 8; o <<= 1) s += __shfl_xor(s, o, kWave);
-    if (lane == 0) dq[((size_t)b * n_detectors + t) * seq + j] = s;
+    for (int o = 8; o < kWave; o <<= 1) qacc += __shfl_xor(qacc, o, kWave);
+    if (lane == 0) wpart[wave] = qacc;
+    __syncthreads();
+    if (tid == 0) {
+        double tot = 0.0;
+        for (int k = 0; k < kWPB; k++) tot += wpart[k];
+        qsum[((size_t)b * n_detectors + t) * seq + j] = tot;
+    }
+}
+
+// One workgroup per (b, t): column sums of tk (the K-flip terms of each
+// position i, over the later positions j) and diagonal sums of tp (the PE-flip
+// terms of each distance d = j - i - 1).  Position s gets du(minDelta_s) *
+// (qsum_main - qsum_alt + column sum); unless |du| <= EPS it goes to
+// x_grad[b][s] at the min anchor of (b, s, t) (+du at a1, -du at a2).  The
+// diagonal sums times du(pe minDelta) are added to dpe[d][t][pe minIdx].
+__global__ __launch_bounds__(kBlock) void k_seq_tri_reduce(
+    const double *__restrict__ tk, const double *__restrict__ tp, const double *__restrict__ qs_main,
+    const double *__restrict__ qs_alt, const uint2 *__restrict__ pack, const uint2 *__restrict__ ppack,
+    const int2 *__restrict__ anchors, float *__restrict__ x_grad, double *__restrict__ dpe,
+    uint32_t batch, uint32_t seq, uint32_t n_inputs, uint32_t n_detectors, uint32_t n_anchors,
+    uint32_t pe_dim) {
+    const uint32_t bt = blockIdx.x;
+    const uint32_t b = bt / n_detectors, t = bt % n_detectors;
+    const size_t base = (size_t)bt * ((size_t)seq * (seq - 1) / 2);
+    for (uint32_t s0 = 0; s0 < seq; s0 += kBlock) {
+        const uint32_t s = s0 + threadIdx.x;  // column i = s and diagonal d = s
+        double col = 0.0, diag = 0.0;
+        if (s < seq) {
+#pragma unroll 8
+            for (uint32_t jr = s + 1; jr < seq; jr++) {
+                const size_t ro = base + (size_t)jr * (jr - 1) / 2;
+                col += tk[ro + s];
+                diag += tp[ro + (jr - s - 1)];
+            }
+            const uint2 rec = pack[(size_t)t * batch * seq + (size_t)b * seq + s];
+            const size_t q = ((size_t)b * n_detectors + t) * seq + s;
+            const double du = du_of_margin(rec_md(rec)) * (qs_main[q] - qs_alt[q] + col);
+            const int32_t m = rec_mi(rec);
+            if (fabs(du) > kEps && m >= 0 && (uint32_t)m < n_anchors) {
+                const int2 a = anchors[(size_t)t * n_anchors + m];
+                if ((uint32_t)a.x < n_inputs && (uint32_t)a.y < n_inputs) {
+                    float *xg = x_grad + ((size_t)b * seq + s) * n_inputs;
+                    unsafeAtomicAdd(xg + a.x, (float)du);
+                    unsafeAtomicAdd(xg + a.y, (float)(-du));
+                }
+            }
+            if (pe_dim > 0 && s + 1 < seq && diag != 0.0) {
+                const uint2 pr = ppack[(size_t)t * (seq - 1) + s];
+                const int32_t pm = rec_mi(pr);
+                if (pm >= 0)
+                    atomicAdd(dpe + ((size_t)s * n_detectors + t) * pe_dim + pm, du_of_margin(rec_md(pr)) * diag);
+            }
+        }
+    }
 }
 
 // Exact decomposition: one thread per (b, t, pair, output block).
@@ -671,10 +926,24 @@ __global__ __launch_bounds__(kBlock) void k_propagate_seq_exact(
     }
 }
 
-// x_grad[b][s][a1] += du, [a2] -= du with du = dq + dk of (b, t, s) and the
-// min anchor of (b, s, t) (both the Q flips at s and the K flips at s flip
-// that anchor), dropped unless |du| > EPS.
-__global__ __launch_bounds__(kBlock) void k_seq_xgrad(const double *__restrict__ dq,
+// Bucket key of the Q-flip pass: Q ^ (1 << minIdx), or 2^Nc (a bin past every
+// sub-table) when no anchor can flip.
+__global__ __launch_bounds__(kBlock) void k_seq_alt_keys(const int32_t *__restrict__ idx,
+                                                         const int32_t *__restrict__ mi,
+                                                         int32_t *__restrict__ keys, uint64_t n,
+                                                         uint32_t n_anchors) {
+    const uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (i >= n) return;
+    const int32_t m = mi[i];
+    keys[i] = (m >= 0 && (uint32_t)m < n_anchors) ? (int32_t)(((uint32_t)idx[i] ^ (1u << m)) & ((1u << n_anchors) - 1))
+                                                   : (int32_t)(1u << n_anchors);
+}
+
+// x_grad[b][s][a1] += du, [a2] -= du with du = du(minDelta) * (qsum_main -
+// qsum_alt) + dk of (b, t, s) and the min anchor of (b, s, t) (both the Q flips
+// at s and the K flips at s flip that anchor), dropped unless |du| > EPS.
+__global__ __launch_bounds__(kBlock) void k_seq_xgrad(const double *__restrict__ qs_main,
+                                                      const double *__restrict__ qs_alt,
                                                       const double *__restrict__ dk,
                                                       const uint2 *__restrict__ pack,
                                                       const int2 *__restrict__ anchors,
@@ -687,9 +956,10 @@ __global__ __launch_bounds__(kBlock) void k_seq_xgrad(const double *__restrict__
     const uint32_t s = (uint32_t)(it % seq);
     const uint32_t t = (uint32_t)((it / seq) % n_detectors);
     const uint32_t b = (uint32_t)(it / ((uint64_t)seq * n_detectors));
-    const double du = dq[it] + dk[it];
+    const uint2 rec = pack[(size_t)t * batch * seq + (size_t)b * seq + s];
+    const double du = du_of_margin(rec_md(rec)) * (qs_main[it] - qs_alt[it]) + dk[it];
     if (!(fabs(du) > kEps)) return;
-    const int32_t m = rec_mi(pack[(size_t)t * batch * seq + (size_t)b * seq + s]);
+    const int32_t m = rec_mi(rec);
     if (m < 0 || (uint32_t)m >= n_anchors) return;
     const int2 a = anchors[(size_t)t * n_anchors + m];
     if ((uint32_t)a.x >= n_inputs || (uint32_t)a.y >= n_inputs) return;
@@ -712,20 +982,23 @@ __global__ __launch_bounds__(kBlock) void k_zero64(double *__restrict__ p, uint6
 
 // ---------------------------------------------------------------------------
 // gather_w_gradients_seq_fc (proto:3944-4304), one workgroup per (table t,
-// Q value q, column slice of C columns).  The sub-table's 2^(Nc+Npe) rows x C
-// gradient sums live in registers (32 per thread); the items (b, j) of the
-// bucket (t, q) are taken in batches: each batch's (item, earlier position i)
-// entries are bucketed by target row (LDS counting sort), then every thread
-// adds the commit values of its rows' entries from an LDS copy of the batch's
-// gradient rows.  No floating-point atomics; each weight-gradient element is
-// written once (the zero-fill of the caller's buffer is fused away).
+// Q value q).  The items (b, j) of the bucket (t, q) are taken in batches; a
+// batch's (item, earlier position i) entries are bucketed by their target row
+// (K_i, PE_{j-i-1}) once (LDS counting sort), then for each column slice of C
+// columns the batch's gradient rows are staged in LDS and every thread sums
+// the commit values of its 32 (row, column) outputs' entries in registers and
+// writes them (the first batch stores or adds as asked, later ones add).  No
+// floating-point atomics and, for a bucket of one batch, each weight-gradient
+// element is written once (the zero-fill of the caller's buffer is fused
+// away).  fp32 sums come in bucket order rather than the reference CPU path's
+// order; int32 payload sums are exact.
 constexpr int kSeqWgThreads = 1024;
-constexpr int kSeqWgOut = 32;            // outputs (row, column) per thread
 constexpr int kSeqWgRowsMax = 4096;      // sub-table rows 2^(Nc+Npe)
-constexpr int kSeqWgEntries = 16384;     // entries per batch
+constexpr int kSeqWgEntries = 32768;     // entries per batch
 constexpr int kSeqWgGvWords = 8192;      // batch gradient rows (items x C)
 constexpr int kSeqWgKeys = 8192;         // K indices of up to 8192 (b, s) rows at a time
 constexpr int kSeqWgPe = 1024;
+constexpr int kSeqWgItems = 256;
 
 template <bool INT_MODE, bool OVERWRITE>
 __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
@@ -740,27 +1013,17 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
     __shared__ uint32_t gv[kSeqWgGvWords];
     __shared__ uint16_t ktab[kSeqWgKeys];
     __shared__ uint16_t ptab[kSeqWgPe];
-    __shared__ uint32_t bitems[kSeqWgGvWords / 4];  // row ids of the batch's items
+    __shared__ uint32_t bitems[kSeqWgItems];  // row ids of the batch's items
+    __shared__ uint32_t wsum[kSeqWgThreads / kWave];
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & (kWave - 1);
     const uint32_t wave = tid / kWave;
-    const uint32_t slice = blockIdx.x % n_slices;
-    const uint32_t tq = blockIdx.x / n_slices;
     const uint32_t n_q = 1u << n_anchors;
-    const uint32_t t = tq / n_q, q = tq % n_q;
+    const uint32_t t = blockIdx.x / n_q, q = blockIdx.x % n_q;
     const uint32_t sub_rows = 1u << (n_anchors + pe_dim);
     const uint32_t pmask = (1u << pe_dim) - 1;
     const uint32_t n_rows = batch * seq;
-    const uint32_t col0 = slice * cols;
-    // output k of this thread: row my_row0 + k, column my_col (cols divides
-    // the 1024 threads; a thread's rows are consecutive so their LDS count
-    // words sit at immediate offsets from one address)
-    const uint32_t my_col = tid % cols;
-    const uint32_t my_row0 = (tid / cols) * kSeqWgOut;
-
-    uint32_t acc[kSeqWgOut];
-#pragma unroll
-    for (int k = 0; k < kSeqWgOut; k++) acc[k] = 0u;
+    const uint32_t my_col = tid % cols;  // cols divides the 1024 threads
 
     for (uint32_t d = tid; d + 1 < seq; d += kSeqWgThreads)
         ptab[d] = (uint16_t)(rec_idx(ppack[(size_t)t * (seq - 1) + d]) & pmask);
@@ -769,7 +1032,9 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
     const int32_t *smp = samples + (size_t)t * n_rows;
     const uint2 *kp = pack + (size_t)t * n_rows;
     const uint32_t rows_per_chunk = (kSeqWgKeys / seq) * seq;
+    float *dst = target + ((size_t)t * n_q + q) * sub_rows * n_outputs;
 
+    bool first = true;
     int32_t k0 = beg;
     for (uint32_t r0 = 0; r0 < n_rows && k0 < end; r0 += rows_per_chunk) {
         const uint32_t r1 = min(r0 + rows_per_chunk, n_rows);
@@ -785,14 +1050,10 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
         for (int32_t kb = k0; kb < k1; kb += (int32_t)items_per_batch) {
             const uint32_t nb = (uint32_t)min((int32_t)items_per_batch, k1 - kb);
             __syncthreads();
-            // stage the batch: item rows, their gradient columns, zero counts
+            // the batch's items; zero counts
             for (uint32_t it = tid; it < nb; it += kSeqWgThreads) bitems[it] = (uint32_t)smp[kb + it];
             for (uint32_t r = tid; r < sub_rows; r += kSeqWgThreads) cnt[r] = 0u;
             __syncthreads();
-            for (uint32_t e = tid; e < nb * cols; e += kSeqWgThreads) {
-                const uint32_t it = e / cols, cc = col0 + e % cols;
-                gv[e] = cc < n_outputs ? cv[(size_t)bitems[it] * n_outputs + cc] : 0u;
-            }
             // count: one wavefront per item, lanes over earlier positions i
             for (uint32_t it = wave; it < nb; it += kSeqWgThreads / kWave) {
                 const uint32_t r = bitems[it];
@@ -813,7 +1074,6 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
                     const uint32_t y = __shfl_up(incl, o, kWave);
                     if ((int)lane >= o) incl += y;
                 }
-                __shared__ uint32_t wsum[kSeqWgThreads / kWave];
                 if (lane == kWave - 1) wsum[wave] = incl;
                 __syncthreads();
                 uint32_t wprefix = 0;
@@ -834,46 +1094,94 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
                     ent[atomicAdd(&cur[row], 1u)] = (uint16_t)it;
                 }
             }
-            __syncthreads();
             // cur[row] is now the end of the row's bucket, cur - cnt its start
-#pragma unroll
-            for (int k = 0; k < kSeqWgOut; k++) {
-                const uint32_t row = my_row0 + (uint32_t)k;
-                const uint32_t e1 = row < sub_rows ? cur[row] : 0u;
-                const uint32_t e0 = row < sub_rows ? e1 - cnt[row] : 0u;
-                uint32_t a = acc[k];
-                for (uint32_t e = e0; e < e1; e++) {
-                    const uint32_t v = gv[(uint32_t)ent[e] * cols + my_col];
-                    if (INT_MODE)
-                        a += v;
-                    else
-                        a = __float_as_uint(__uint_as_float(a) + __uint_as_float(v));
+            for (uint32_t sl = 0; sl < n_slices; sl++) {
+                const uint32_t col0 = sl * cols;
+                __syncthreads();  // scatter done / the previous slice is done with gv
+                for (uint32_t e = tid; e < nb * cols; e += kSeqWgThreads) {
+                    const uint32_t it = e / cols, cc = col0 + e % cols;
+                    gv[e] = cc < n_outputs ? cv[(size_t)bitems[it] * n_outputs + cc] : 0u;
                 }
-                acc[k] = a;
-                // one output's bucket bounds live at a time (register budget)
-                __builtin_amdgcn_sched_barrier(0);
+                __syncthreads();
+                // lane group g (cols lanes) takes the rows whose entries start in
+                // [g E / G, (g + 1) E / G): about equal work whatever the row sizes
+                const uint32_t n_groups = kSeqWgThreads / cols, grp = tid / cols;
+                const uint32_t total = cur[sub_rows - 1];  // entries of the batch
+                auto first_row = [&](uint32_t gi) -> uint32_t {
+                    if (gi >= n_groups) return sub_rows;
+                    const uint32_t tgt = (uint32_t)(((uint64_t)total * gi + n_groups - 1) / n_groups);
+                    uint32_t lo = 0, hi = sub_rows;  // first row r with start(r) >= tgt
+                    while (lo < hi) {
+                        const uint32_t mid = (lo + hi) / 2;
+                        if (cur[mid] - cnt[mid] < tgt) lo = mid + 1; else hi = mid;
+                    }
+                    return gi == 0 ? 0u : lo;
+                };
+                const uint32_t rs = first_row(grp), re = first_row(grp + 1);
+                const uint32_t cc = col0 + my_col;
+                const bool store = first && OVERWRITE;
+                for (uint32_t row = rs; row < re; row++) {
+                    const uint32_t e1 = cur[row];
+                    uint32_t e = e1 - cnt[row];
+                    uint32_t a = 0u;
+                    // four entries at a time: their LDS reads overlap
+                    for (; e + 4 <= e1; e += 4) {
+                        const uint32_t v0 = gv[(uint32_t)ent[e] * cols + my_col];
+                        const uint32_t v1 = gv[(uint32_t)ent[e + 1] * cols + my_col];
+                        const uint32_t v2 = gv[(uint32_t)ent[e + 2] * cols + my_col];
+                        const uint32_t v3 = gv[(uint32_t)ent[e + 3] * cols + my_col];
+                        if (INT_MODE) {
+                            a += v0 + v1 + v2 + v3;
+                        } else {
+                            float f = __uint_as_float(a);
+                            f += __uint_as_float(v0);
+                            f += __uint_as_float(v1);
+                            f += __uint_as_float(v2);
+                            f += __uint_as_float(v3);
+                            a = __float_as_uint(f);
+                        }
+                    }
+                    for (; e < e1; e++) {
+                        const uint32_t v = gv[(uint32_t)ent[e] * cols + my_col];
+                        if (INT_MODE)
+                            a += v;
+                        else
+                            a = __float_as_uint(__uint_as_float(a) + __uint_as_float(v));
+                    }
+                    // this batch's sum of (row, cc): rows q * sub_rows .. of table t
+                    if (cc < n_outputs) {
+                        float *p = dst + (size_t)row * n_outputs + cc;
+                        float v;
+                        if (INT_MODE) {
+                            int32_t iv = (int32_t)a;
+                            if (!store) iv = wrap_add(iv, __float_as_int(*p));
+                            // the int epilogue runs after the last batch; until
+                            // then the sums stay int32 bits
+                            v = __int_as_float(iv);
+                        } else {
+                            v = __uint_as_float(a);
+                            if (!store) v = *p + v;
+                        }
+                        *p = v;
+                    }
+                }
             }
+            first = false;
         }
         k0 = k1;
     }
-    // write the sub-table slice (rows q * sub_rows .. of table t)
-    float *dst = target + ((size_t)t * n_q + q) * sub_rows * n_outputs;
-    const uint32_t cc = col0 + my_col;
-#pragma unroll
-    for (int k = 0; k < kSeqWgOut; k++) {
-        const uint32_t row = my_row0 + (uint32_t)k;
-        if (row >= sub_rows || cc >= n_outputs) continue;
-        float *p = dst + (size_t)row * n_outputs + cc;
-        float v;
-        if (INT_MODE) {
-            int32_t iv = (int32_t)acc[k];
-            if (!OVERWRITE) iv = wrap_add(iv, __float_as_int(*p));
-            v = (float)(((double)iv * kDenom32Reciproc) / int_rescaler);
-        } else {
-            v = __uint_as_float(acc[k]);
-            if (!OVERWRITE) v = *p + v;
+    if (INT_MODE) {
+        // int epilogue of the sub-table (every row; untouched ones hold the
+        // caller's int bits or, when overwriting, zero)
+        __syncthreads();
+        for (uint32_t e = tid; e < sub_rows * n_outputs; e += kSeqWgThreads) {
+            float *p = dst + e;
+            const int32_t iv = (first && OVERWRITE) ? 0 : __float_as_int(*p);
+            *p = (float)(((double)iv * kDenom32Reciproc) / int_rescaler);
         }
-        *p = v;
+    } else if (first && OVERWRITE) {
+        // an empty bucket: its sub-table gradient is zero
+        for (uint32_t e = tid; e < sub_rows * n_outputs; e += kSeqWgThreads) dst[e] = 0.0f;
     }
 }
 
@@ -916,6 +1224,16 @@ uint32_t seq_vec(uint32_t n_outputs) {
     return 1;
 }
 
+// Bytes of one pair triangle [B][T][S(S-1)/2] of fp64.
+uint64_t seq_tri_bytes(const SeqShape &s) {
+    return (uint64_t)s.batch * s.n_detectors * ((uint64_t)s.seq * (s.seq - 1) / 2) * 8;
+}
+
+// The pair-parallel main pass and its triangle reduction apply (fp32 sums).
+bool seq_pairs_applies(const SeqShape &s) {
+    return s.n_outputs % 4 == 0 && s.n_outputs <= (uint32_t)kPairMaxO && seq_tri_bytes(s) <= (16ull << 30);
+}
+
 // Columns of a forward slice for k_fill_seq_lds (0: it does not apply): the
 // widest power of two <= 64 whose sub-table slice fits the LDS table.
 uint32_t seq_fill_cols(const SeqShape &s) {
@@ -932,15 +1250,13 @@ uint32_t seq_fill_cols(const SeqShape &s) {
 }
 
 // Columns of a weight-gradient slice (0: the sort path does not apply): a
-// power of two with sub_rows * C <= 1024 threads x 32 outputs and the batch's
-// gradient rows (>= 1 item of C columns) in LDS.
+// power of two <= 64 (one lane per column of a lane group).
 uint32_t seq_wg_cols(const SeqShape &s) {
     const uint64_t sub_rows = 1ull << (s.n_anchors + s.pe_dim);
     if (sub_rows > (uint64_t)kSeqWgRowsMax || s.seq > (uint32_t)kSeqWgKeys ||
         s.seq - 1 > (uint32_t)kSeqWgPe || s.seq - 1 > (uint32_t)kSeqWgEntries)
         return 0;
     uint32_t cols = 64;
-    while (cols > 1 && sub_rows * cols > (uint64_t)kSeqWgThreads * kSeqWgOut) cols /= 2;
     while (cols > 1 && cols / 2 >= s.n_outputs) cols /= 2;
     return cols;
 }
@@ -949,8 +1265,7 @@ uint32_t seq_wg_cols(const SeqShape &s) {
 uint32_t seq_wg_items(const SeqShape &s, uint32_t cols) {
     uint32_t n = (uint32_t)kSeqWgEntries / std::max<uint32_t>(1, s.seq - 1);
     n = std::min<uint32_t>(n, (uint32_t)kSeqWgGvWords / cols);
-    n = std::min<uint32_t>(n, (uint32_t)kSeqWgGvWords / 4);
-    return std::min<uint32_t>(n, 65535u);
+    return std::min<uint32_t>(n, (uint32_t)kSeqWgItems);
 }
 
 }  // namespace
@@ -970,11 +1285,17 @@ size_t seq_scratch_bytes(const SeqShape &s, bool backward) {
         n += align256((size_t)s.n_detectors * rows * s.n_outputs * 4);
         return n;
     }
-    n += 2 * align256(rows * s.n_detectors * 8);
+    n += 3 * align256(rows * s.n_detectors * 8);
     n += align256((size_t)(s.seq - 1) * s.n_detectors * std::max<uint32_t>(s.pe_dim, 1) * 8);
     n += align256((size_t)s.n_detectors * ((1u << s.n_anchors) + 1) * 4);
     n += align256((size_t)s.n_detectors * rows * 4);
     n += align256(rows * s.n_outputs * 4);
+    // Q-flip pass: keys [B*S][T], offsets [T][2^(Nc+1)+1], samples [T][B*S]
+    n += align256(rows * s.n_detectors * 4);
+    n += align256((size_t)s.n_detectors * ((2u << s.n_anchors) + 1) * 4);
+    n += align256((size_t)s.n_detectors * rows * 4);
+    // pair triangles of the pair-parallel main pass
+    if (seq_pairs_applies(s)) n += 2 * align256(seq_tri_bytes(s));
     return n;
 }
 
@@ -1091,6 +1412,8 @@ hipError_t launch_backward_seq(const SeqShape &s, float *w, const float *g, cons
     off += align256((size_t)s.n_detectors * (s.seq - 1) * 8);
     double *dq = reinterpret_cast<double *>(sp + off);
     off += align256((size_t)rows * s.n_detectors * 8);
+    double *dq_alt = reinterpret_cast<double *>(sp + off);
+    off += align256((size_t)rows * s.n_detectors * 8);
     double *dk = reinterpret_cast<double *>(sp + off);
     off += align256((size_t)rows * s.n_detectors * 8);
     double *dpe = reinterpret_cast<double *>(sp + off);
@@ -1101,6 +1424,17 @@ hipError_t launch_backward_seq(const SeqShape &s, float *w, const float *g, cons
     int32_t *samples = reinterpret_cast<int32_t *>(sp + off);
     off += align256((size_t)s.n_detectors * rows * 4);
     uint32_t *cv = reinterpret_cast<uint32_t *>(sp + off);
+    off += align256((size_t)rows * s.n_outputs * 4);
+    int32_t *alt_keys = reinterpret_cast<int32_t *>(sp + off);
+    off += align256((size_t)rows * s.n_detectors * 4);
+    int32_t *offsets2 = reinterpret_cast<int32_t *>(sp + off);
+    off += align256((size_t)s.n_detectors * ((2u << s.n_anchors) + 1) * 4);
+    int32_t *samples2 = reinterpret_cast<int32_t *>(sp + off);
+    off += align256((size_t)s.n_detectors * rows * 4);
+    const bool pairs = seq_pairs_applies(s);
+    double *tk = pairs ? reinterpret_cast<double *>(sp + off) : nullptr;
+    if (pairs) off += align256(seq_tri_bytes(s));
+    double *tp = pairs ? reinterpret_cast<double *>(sp + off) : nullptr;
 
     hipLaunchKernelGGL(k_seq_pack, dim3((s.n_detectors + 63) / 64, (rows + 63) / 64), dim3(kBlock),
                        0, st, idx, md, mi, pack, rows, s.n_detectors);
@@ -1130,26 +1464,52 @@ hipError_t launch_backward_seq(const SeqShape &s, float *w, const float *g, cons
     if (!int_mode && s.n_outputs % 4 == 0 && nj <= 4) {
         const uint64_t n_acc = (uint64_t)rows * s.n_detectors;
         hipLaunchKernelGGL(k_zero64, dim3(blocks_for(n_acc)), dim3(kBlock), 0, st, dq, n_acc);
+        hipLaunchKernelGGL(k_zero64, dim3(blocks_for(n_acc)), dim3(kBlock), 0, st, dq_alt, n_acc);
         hipLaunchKernelGGL(k_zero64, dim3(blocks_for(n_acc)), dim3(kBlock), 0, st, dk, n_acc);
+        hipLaunchKernelGGL(k_seq_alt_keys, dim3(blocks_for(n_acc)), dim3(kBlock), 0, st, idx, mi,
+                           alt_keys, n_acc, s.n_anchors);
+        FcShape fs_alt = fs;
+        fs_alt.n_entries = 2u << s.n_anchors;
+        e = launch_bucket_samples(fs_alt, alt_keys, offsets2, samples2, st);
+        if (e != hipSuccess) return e;
         hipLaunchKernelGGL(k_zero64, dim3(blocks_for(n_dpe)), dim3(kBlock), 0, st, dpe, (uint64_t)n_dpe);
-        const uint64_t units = (uint64_t)rows * s.n_detectors;
-        const uint64_t n_wg = (units + kWPB - 1) / kWPB;
-        const uint64_t wg_per_xcd = (n_wg + 7) / 8;
+        const uint64_t units = (uint64_t)rows * s.n_detectors;  // one workgroup each
+        const uint64_t wg_per_xcd = (units + 7) / 8;
         const uint64_t grid = wg_per_xcd * 8;
-        if (grid > 0x7fffffffu || units > 0xffffffffull) return hipErrorInvalidConfiguration;
-#define SPIKY_PSEQ(NJ)                                                                            \
-    hipLaunchKernelGGL(k_propagate_seq<NJ>, dim3((uint32_t)grid), dim3(kBlock), 0, st, w, g, pack, \
-                       ppack, samples, dq, dk, dpe, s.batch, s.seq, s.n_outputs, s.n_detectors,     \
+        if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
+#define SPIKY_PSEQ(NJ, ALT, SMP, QS)                                                                 \
+    hipLaunchKernelGGL((k_propagate_seq<NJ, ALT>), dim3((uint32_t)grid), dim3(kBlock), 0, st, w, g, \
+                       pack, ppack, SMP, QS, dk, dpe, s.batch, s.seq, s.n_outputs, s.n_detectors,   \
                        s.n_anchors, s.pe_dim, (uint32_t)wg_per_xcd)
-        switch (nj) {
-            case 1: SPIKY_PSEQ(1); break;
-            case 2: SPIKY_PSEQ(2); break;
-            case 3: SPIKY_PSEQ(3); break;
-            default: SPIKY_PSEQ(4); break;
+#define SPIKY_PSEQ2(NJ)                                \
+    SPIKY_PSEQ(NJ, false, samples, dq);                \
+    SPIKY_PSEQ(NJ, true, samples2, dq_alt)
+        if (pairs) {
+            hipLaunchKernelGGL(k_propagate_seq_pairs, dim3((uint32_t)grid), dim3(kBlock), 0, st, w, g,
+                               pack, ppack, samples, dq, tk, tp, s.batch, s.seq, s.n_outputs,
+                               s.n_detectors, s.n_anchors, s.pe_dim, (uint32_t)wg_per_xcd);
+            switch (nj) {
+                case 1: SPIKY_PSEQ(1, true, samples2, dq_alt); break;
+                case 2: SPIKY_PSEQ(2, true, samples2, dq_alt); break;
+                case 3: SPIKY_PSEQ(3, true, samples2, dq_alt); break;
+                default: SPIKY_PSEQ(4, true, samples2, dq_alt); break;
+            }
+            hipLaunchKernelGGL(k_seq_tri_reduce, dim3(s.batch * s.n_detectors), dim3(kBlock), 0, st,
+                               tk, tp, dq, dq_alt, pack, ppack, ap, x_grad, dpe, s.batch, s.seq,
+                               s.n_inputs, s.n_detectors, s.n_anchors, s.pe_dim);
+        } else {
+            switch (nj) {
+                case 1: SPIKY_PSEQ2(1); break;
+                case 2: SPIKY_PSEQ2(2); break;
+                case 3: SPIKY_PSEQ2(3); break;
+                default: SPIKY_PSEQ2(4); break;
+            }
+            hipLaunchKernelGGL(k_seq_xgrad, dim3(blocks_for(n_acc)), dim3(kBlock), 0, st, dq, dq_alt,
+                               dk, pack, ap, x_grad, s.batch, s.seq, s.n_inputs, s.n_detectors,
+                               s.n_anchors);
         }
+#undef SPIKY_PSEQ2
 #undef SPIKY_PSEQ
-        hipLaunchKernelGGL(k_seq_xgrad, dim3(blocks_for(n_acc)), dim3(kBlock), 0, st, dq, dk, pack,
-                           ap, x_grad, s.batch, s.seq, s.n_inputs, s.n_detectors, s.n_anchors);
         if (s.pe_dim > 0)
             hipLaunchKernelGGL(k_seq_pe_commit, dim3(blocks_for(n_dpe)), dim3(kBlock), 0, st, dpe,
                                pe_grad, (uint32_t)n_dpe);
@@ -1187,7 +1547,7 @@ hipError_t launch_backward_seq(const SeqShape &s, float *w, const float *g, cons
     const uint32_t cols = seq_wg_cols(s);
     if (cols > 0) {
         const uint32_t n_slices = (s.n_outputs + cols - 1) / cols;
-        const uint64_t grid = (uint64_t)s.n_detectors * (1u << s.n_anchors) * n_slices;
+        const uint64_t grid = (uint64_t)s.n_detectors * (1u << s.n_anchors);
         if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
         const uint32_t ipb = seq_wg_items(s, cols);
 #define SPIKY_WSEQ(IM, OW)                                                                             \
