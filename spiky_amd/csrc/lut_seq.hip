@@ -1091,7 +1091,7 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
                 const uint16_t *kt = ktab + (r / seq - r0 / seq) * seq;
                 for (uint32_t i = lane; i < j; i += kWave) {
                     const uint32_t row = (((uint32_t)kt[i] << pe_dim) | ptab[j - i - 1]) & (sub_rows - 1);
-                    ent[atomicAdd(&cur[row], 1u)] = (uint16_t)it;
+                    ent[atomicAdd(&cur[row], 1u)] = (uint16_t)(it * cols);  // the item's gv row
                 }
             }
             // cur[row] is now the end of the row's bucket, cur - cnt its start
@@ -1124,29 +1124,26 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
                     const uint32_t e1 = cur[row];
                     uint32_t e = e1 - cnt[row];
                     uint32_t a = 0u;
-                    // four entries at a time: their LDS reads overlap
-                    for (; e + 4 <= e1; e += 4) {
-                        const uint32_t v0 = gv[(uint32_t)ent[e] * cols + my_col];
-                        const uint32_t v1 = gv[(uint32_t)ent[e + 1] * cols + my_col];
-                        const uint32_t v2 = gv[(uint32_t)ent[e + 2] * cols + my_col];
-                        const uint32_t v3 = gv[(uint32_t)ent[e + 3] * cols + my_col];
+                    // eight entries at a time, their LDS reads in flight together;
+                    // the last group re-reads the row's last entry and adds +0
+                    // past its end (the sum starts at +0 and is never -0, so
+                    // that changes nothing)
+                    for (; e < e1; e += 8) {
+                        uint32_t v[8];
+#pragma unroll
+                        for (int u = 0; u < 8; u++) {
+                            const uint32_t g = gv[(uint32_t)ent[min(e + u, e1 - 1)] + my_col];
+                            v[u] = e + u < e1 ? g : 0u;
+                        }
                         if (INT_MODE) {
-                            a += v0 + v1 + v2 + v3;
+#pragma unroll
+                            for (int u = 0; u < 8; u++) a += v[u];
                         } else {
                             float f = __uint_as_float(a);
-                            f += __uint_as_float(v0);
-                            f += __uint_as_float(v1);
-                            f += __uint_as_float(v2);
-                            f += __uint_as_float(v3);
+#pragma unroll
+                            for (int u = 0; u < 8; u++) f += __uint_as_float(v[u]);
                             a = __float_as_uint(f);
                         }
-                    }
-                    for (; e < e1; e++) {
-                        const uint32_t v = gv[(uint32_t)ent[e] * cols + my_col];
-                        if (INT_MODE)
-                            a += v;
-                        else
-                            a = __float_as_uint(__uint_as_float(a) + __uint_as_float(v));
                     }
                     // this batch's sum of (row, cc): rows q * sub_rows .. of table t
                     if (cc < n_outputs) {
