@@ -64,7 +64,7 @@ def lib():
                                               _i64, _int, _f64]
         L.oracle_propagate_seq.argtypes = [_f32p, _f32p, _i32p, _f32p, _i32p, _vp, _vp, _vp, _i32p,
                                            _f32p, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
-                                           _i64, _int, _f64]
+                                           _i64, _int, _f64, _vp, _vp]
         L.oracle_gather_wgrad_seq.argtypes = [_f32p, _i32p, _vp, _f32p, _i64, _i64, _i64, _i64, _i64,
                                               _i64, _i64, _f32, _f32, _int, _f64]
         _lib = L
@@ -203,19 +203,29 @@ def fill_outputs_seq(w, idx, pidx, batch, n_outputs, n_detectors, seq_len, n_anc
 
 def propagate_seq(w, g, idx, md, mi, pidx, pmd, pmi, anchors, batch, n_inputs, n_outputs,
                   n_detectors, seq_len, n_anchors, positional_dim, ogs=32, x_grad=None,
-                  pe_grad=None, int_mode=False, int_rescaler=1.0):
-    """Returns (x_grad [B*S*I], pe_grad [(S-1)*T*Npe] or None)."""
+                  pe_grad=None, int_mode=False, int_rescaler=1.0, acc64=False):
+    """Returns (x_grad [B*S*I], pe_grad [(S-1)*T*Npe] or None).  With acc64
+    (fp32 summation) the same terms are summed in fp64 and returned as float64
+    arrays: the reference's sums without the fp32 rounding of each partial."""
     if x_grad is None:
         x_grad = np.zeros(batch * seq_len * n_inputs, dtype=np.float32)
     if pe_grad is None and positional_dim > 0:
         pe_grad = np.zeros((seq_len - 1) * n_detectors * positional_dim, dtype=np.float32)
+    xg64 = pg64 = None
+    if acc64 and not int_mode:
+        xg64 = np.zeros(batch * seq_len * n_inputs, dtype=np.float64)
+        if positional_dim > 0:
+            pg64 = np.zeros((seq_len - 1) * n_detectors * positional_dim, dtype=np.float64)
     pidx, pmd, pmi = (None if a is None else _c(a, dt) for a, dt in
                       ((pidx, np.int32), (pmd, np.float32), (pmi, np.int32)))
     lib().oracle_propagate_seq(_c(w, np.float32), _c(g, np.float32), _c(idx, np.int32),
                                _c(md, np.float32), _c(mi, np.int32), _ptr(pidx), _ptr(pmd),
                                _ptr(pmi), _c(anchors, np.int32), x_grad, _ptr(pe_grad), batch,
                                n_inputs, n_outputs, n_detectors, seq_len, n_anchors,
-                               positional_dim, ogs, int(int_mode), float(int_rescaler))
+                               positional_dim, ogs, int(int_mode), float(int_rescaler),
+                               _ptr(xg64), _ptr(pg64))
+    if xg64 is not None:
+        return xg64, pg64
     return x_grad, pe_grad
 
 

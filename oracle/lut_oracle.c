@@ -489,12 +489,16 @@ static inline double block_dot(const float *w, int64_t row, const float *gj, int
 /* detector, output block): flip Q's min anchor if |dQ| < |dK| else K's; the */
 /* positional flip applies when |dPE| is strictly the smallest.  pe_grad may */
 /* be NULL when positional_dim == 0.                                         */
+/* x_grad64 / pe_grad64 (fp32 summation only, may be null): when given, the */
+/* same terms (same EPS cut) are accumulated there in fp64 instead of into   */
+/* the fp32 buffers -- the reference's sums without its fp32 rounding of     */
+/* every partial sum, to check a device path that rounds fewer times.        */
 void oracle_propagate_seq(
     const float *w, const float *g, const int32_t *idx, const float *md, const int32_t *mi,
     const int32_t *pidx, const float *pmd, const int32_t *pmi, const int32_t *anchors,
     float *x_grad, float *pe_grad, int64_t batch, int64_t n_inputs, int64_t n_outputs,
     int64_t n_detectors, int64_t seq_len, int64_t n_anchors, int64_t positional_dim, int64_t ogs,
-    int int_mode, double int_rescaler)
+    int int_mode, double int_rescaler, double *x_grad64, double *pe_grad64)
 {
     const int64_t nlpd = (int64_t)1 << (2 * n_anchors + positional_dim);
     const int64_t n_ob = (n_outputs + ogs - 1) / ogs;
@@ -534,14 +538,24 @@ void oracle_propagate_seq(
         du *= ms - as;
         if (flip >= 0) {
             const int32_t *ap = anchors + (t * n_anchors + flip) * 2;
-            push_input_grad(x_grad + (b * seq_len + src_pos) * n_inputs, ap[0], ap[1], du, int_mode,
-                            int_rescaler);
+            if (x_grad64 && !int_mode) {
+                double *xg = x_grad64 + (b * seq_len + src_pos) * n_inputs;
+                if (fabs(du) > OR_EPS) {
+                    xg[ap[0]] += du;
+                    xg[ap[1]] -= du;
+                }
+            } else {
+                push_input_grad(x_grad + (b * seq_len + src_pos) * n_inputs, ap[0], ap[1], du, int_mode,
+                                int_rescaler);
+            }
         }
         if (pd > 0 && fabsf(pdl) < fabsf(qd) && fabsf(pdl) < fabsf(kd) && pm >= 0) {
             int64_t pe_row = t * nlpd + seq_row(Q, K, P ^ (1 << pm), n_anchors, pd);
             double dpe = du_of_margin(pdl) * (ms - block_dot(w, pe_row, gj, n_outputs, o0, o1));
             float *dst = pe_grad + pe_off * pd + pm;
-            if (int_mode)
+            if (pe_grad64 && !int_mode)
+                pe_grad64[pe_off * pd + pm] += dpe;
+            else if (int_mode)
                 *as_i32(dst) = wrap_add(*as_i32(dst), (int32_t)(dpe * OR_DENOM32 * int_rescaler));
             else
                 *dst = (float)((double)*dst + dpe);

@@ -11,7 +11,9 @@ Bars:
     so it is bit-exact only when g is integer-valued (order-free sums), and
     otherwise within the fp32 summation bound n * 2^-24 * sum|terms|;
   * fp32 input and positional gradients: |gpu - cpu| <= 1e-5 * max|row| plus
-    the sub-EPS terms the reference drops per (pair, table, block).
+    the sub-EPS terms the reference drops per (pair, table, block), where cpu
+    is the oracle's terms summed in fp64 (its fp32 partial sums are the
+    reference's own rounding noise, pinned in test_oracle_seq_pins.py).
 """
 import numpy as np
 import pytest
@@ -56,10 +58,10 @@ def close_rows(gpu, cpu, rows, n_terms):
 
 
 def run_seq(oracle, B, S, I, T, Nc, Npe, O, fgs=32, bgs=32, seed=0, int_rescaler=None, lr=1.0,
-            int_grad=False, internal=False):
+            int_grad=False, internal=False, inputs=None):
     dev = torch.device("cuda:0")
     int_mode = int_rescaler is not None
-    x, anchors, W, pe, go = seq_inputs(seed, B, S, I, T, Nc, Npe, O, int_grad)
+    x, anchors, W, pe, go = inputs if inputs is not None else seq_inputs(seed, B, S, I, T, Nc, Npe, O, int_grad)
     dm = make_seq_dm(I, O, T, Nc, S, Npe, fgs, bgs, int_rescaler, lr)
     print(f"[seq] B={B} S={S} I={I} T={T} Nc={Nc} Npe={Npe} O={O} int={int_mode} internal={internal}",
           flush=True)
@@ -94,8 +96,11 @@ def run_seq(oracle, B, S, I, T, Nc, Npe, O, fgs=32, bgs=32, seed=0, int_rescaler
         rpli, rpmd, rpmi = oracle.check_pe(pe.numpy(), S, T, Npe)
     rout = oracle.fill_outputs_seq(Wn, ridx, rpli, B, O, T, S, Nc, Npe, int_mode=int_mode,
                                    int_rescaler=int_rescaler or 1.0)
+    # fp32 summation: the oracle's terms summed in fp64 (the reference CPU path
+    # rounds every partial sum to fp32, an error that grows with S * T terms)
     rxg, rpeg = oracle.propagate_seq(Wn, gn, ridx, rmd, rmi, rpli, rpmd, rpmi, an, B, I, O, T, S, Nc,
-                                     Npe, ogs=fgs, int_mode=int_mode, int_rescaler=int_rescaler or 1.0)
+                                     Npe, ogs=fgs, int_mode=int_mode, int_rescaler=int_rescaler or 1.0,
+                                     acc64=not int_mode)
     if int_mode:
         oracle.convert_int_to_float(rout, int_rescaler)
         oracle.convert_int_to_float(rxg, int_rescaler)
@@ -159,6 +164,34 @@ def test_seq_no_positional(oracle, cuda_device):
 def test_seq_two_tiles_wide_rows(oracle, cuda_device):
     # S > 32 (several pair tiles in the reference order), 256 outputs (4 per lane)
     run_seq(oracle, 2, 40, 24, 3, 3, 3, 256, seed=4)
+
+
+def test_seq_attention_layer_shape(oracle, cuda_device):
+    # the config-5 attention layer's per-table shape (S = 256, Nc = 6, Npe = 4,
+    # 2^10-row sub-tables, O = 256) at a batch and table count the oracle
+    # finishes in seconds: LDS-sliced forward, pair-parallel backward
+    run_seq(oracle, 2, 256, 64, 4, 6, 4, 256, seed=11)
+
+
+def test_seq_one_bucket_chunks(oracle, cuda_device):
+    # all-zero inputs put every (b, s) of a table in one Q bucket: more items
+    # than one sorted chunk of the forward (2048), many weight-gradient
+    # batches, and rows past one staged key chunk (8192)
+    B, S, I, T, Nc, Npe, O = 160, 64, 16, 2, 3, 2, 64
+    x, anchors, W, pe, go = seq_inputs(12, B, S, I, T, Nc, Npe, O)
+    x.zero_()
+    run_seq(oracle, B, S, I, T, Nc, Npe, O, seed=12, inputs=(x, anchors, W, pe, go))
+
+
+def test_seq_attention_layer_shape_int32(oracle, cuda_device):
+    run_seq(oracle, 2, 256, 64, 4, 6, 4, 256, seed=13, int_rescaler=0.25)
+
+
+def test_seq_one_bucket_chunks_int32(oracle, cuda_device):
+    B, S, I, T, Nc, Npe, O = 160, 64, 16, 2, 3, 2, 64
+    x, anchors, W, pe, go = seq_inputs(14, B, S, I, T, Nc, Npe, O)
+    x.zero_()
+    run_seq(oracle, B, S, I, T, Nc, Npe, O, seed=14, int_rescaler=0.5, inputs=(x, anchors, W, pe, go))
 
 
 def test_seq_odd_outputs_and_groups(oracle, cuda_device):

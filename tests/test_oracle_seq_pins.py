@@ -172,3 +172,31 @@ def test_check_pe_special_cases(oracle):
     pidx = oracle.check_pe(pe, 3, 1, 4, cmp_eps=0.3, train=False)
     # |v| < eps -> bit 0; |v| == eps is outside the band (misc.h:16)
     assert list(pidx) == [0b1000, 0b0010]
+
+
+def test_seq_backward_fp64_accumulation(oracle):
+    """acc64 sums the same terms as the fp32 restatement: equal after rounding
+    when every element gets one term (S = 2, one block), and within the fp32
+    summation bound n * 2^-24 * sum|partial| otherwise."""
+    rng = np.random.default_rng(21)
+    for B, S, I, T, Nc, Npe, O in ((3, 2, 40, 1, 3, 2, 16), (2, 24, 12, 5, 3, 2, 40)):
+        x = rng.standard_normal(B * S * I).astype(np.float32)
+        anchors = np.concatenate([rng.permutation(I)[:2] for _ in range(T * Nc)]).astype(np.int32)
+        W = (rng.standard_normal(T * (1 << (2 * Nc + Npe)) * O) * 0.01).astype(np.float32)
+        pe = rng.uniform(-1, 1, (S - 1) * T * Npe).astype(np.float32)
+        g = rng.standard_normal(B * S * O).astype(np.float32)
+        idx, md, mi = oracle.check_detectors(x, anchors, B * S, I, T, Nc)
+        pli, pmd, pmi = oracle.check_pe(pe, S, T, Npe)
+        args = (W, g, idx, md, mi, pli, pmd, pmi, anchors, B, I, O, T, S, Nc, Npe)
+        xg32, pg32 = oracle.propagate_seq(*args)
+        xg64, pg64 = oracle.propagate_seq(*args, acc64=True)
+        assert xg64.dtype == np.float64
+        if S == 2:
+            # anchors are distinct per table and T = 1: one term per element
+            assert np.array_equal(xg64.astype(np.float32), xg32)
+            assert np.array_equal(pg64.astype(np.float32), pg32)
+        else:
+            n = S * T * ((O + 31) // 32)
+            scale = np.abs(xg64).reshape(B * S, I).max(axis=1, keepdims=True) * 4 + 1e-30
+            err = np.abs(xg32.astype(np.float64) - xg64).reshape(B * S, I)
+            assert np.all(err <= n * 2.0 ** -24 * scale)
