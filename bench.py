@@ -28,7 +28,7 @@ PEAK_HBM_GBS = 8000.0  # MI355X HBM3E peak
 CONFIGS = {
     # name: (B, I, T, Nc, O, x_dist, cpu_sample_B)
     1: (64, 784, 256, 6, 10, "uniform", 64),
-    3: (1024, 4096, 8192, 8, 1024, "normal", 16),
+    3: (1024, 4096, 8192, 8, 1024, "normal", 256),
 }
 
 
@@ -107,7 +107,7 @@ def cpu_baseline(x, anchors, W, go, B_full, I, T, Nc, O, sample_B):
     wg = np.empty(T * E * O, np.float32)
     times = []
     zero_fill = []
-    for rep in range(4):
+    for rep in range(3):
         t0 = time.perf_counter()
         out = np.zeros(sample_B * O, np.float32)
         idx, md, mi = oracle.check_detectors(xn, an, sample_B, I, T, Nc)
@@ -129,9 +129,104 @@ def cpu_baseline(x, anchors, W, go, B_full, I, T, Nc, O, sample_B):
         "cores": 1,
         "kind": "port",
         "sample": (f"config workload at batch {sample_B} of {B_full} (same tables, anchors, inputs); "
-                   f"median of 3 timed steps after 1 warm-up; step {med:.3f} s of which w_grad "
+                   f"median of 2 timed steps after 1 warm-up; step {med:.3f} s of which w_grad "
                    f"zero-fill {float(np.median(zero_fill[1:])):.3f} s"),
     }
+
+
+INT8 = dict(B=4096, I=4096, T=8192, Nc=8, O=1024, int_rescaler=0.001, cpu_B=2048)
+
+
+def bench_int8(args):
+    """the config-3 layer with int8 tables (uniform in
+    [-127, 127]) and one fp32 scale per table (uniform [0.001, 0.01]),
+    int32 summation (LUTDataManagerI), inference forward at batch 4096:
+    indices plus the gather-sum of scale[t] * q rows."""
+    import torch
+    import numpy as np
+    from spiky_amd import LUTDataManagerI
+    c = INT8
+    B, I, T, Nc, O = c["B"], c["I"], c["T"], c["Nc"], c["O"]
+    E = 1 << Nc
+    dev = torch.device("cuda:0")
+    log(f"config 4: int8 tables, B={B} I={I} T={T} Nc={Nc} O={O}")
+    anchors = make_anchors(T, I, Nc, 1, dev)
+    gq = torch.Generator(device=dev).manual_seed(4)
+    q8 = torch.randint(-127, 128, (T * E * O,), device=dev, generator=gq, dtype=torch.int8)
+    scales = torch.rand(T, device=dev, generator=gq) * 0.009 + 0.001
+    gx = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(B * I, device=dev, generator=gx)
+    dm = LUTDataManagerI(I, O, T, Nc, 1, 0, 0, 32, 32, c["int_rescaler"])
+    dm.register_synapse_meta(1.0, -1.0, 1.0, 0.0, 0.0)
+    dm.initialize_neurons(True)
+    dm.to_device(0)
+    out = torch.empty(B * O, device=dev)
+    idx = torch.empty(B * T, dtype=torch.int32, device=dev)
+
+    def step():
+        out.zero_()  # the caller's zeroed output (LUTLayer.py:631)
+        dm.forward_step_i8(q8, scales, B, x, anchors, out, idx)
+
+    log("warmup")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    dm.get_kernel_times(reset=True)
+    dm.set_kernel_timing(True)
+    log(f"timing {args.steps} steps")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    dm.set_kernel_timing(False)
+    ktimes = dm.get_kernel_times(reset=True)
+    log(f"{ms:.3f} ms/step; kernels {ktimes}")
+    gb = {"check_detectors": B * I * 4 + T * Nc * 8 + B * T * 4,
+          "fill_outputs_fc_i8": B * T * O * 1 + T * 4 + B * O * 4}
+    dom = max(ktimes.items(), key=lambda kv: kv[1][1])[0]
+    dom_ms = ktimes[dom][1] / ktimes[dom][0]
+    achieved = gb[dom] / (dom_ms * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu_baseline:
+        import oracle
+        sb = c["cpu_B"]
+        log(f"cpu baseline: copying int8 tables to host ({q8.numel() / 1e9:.1f} GB)")
+        qn, scn = q8.cpu().numpy(), scales.cpu().numpy()
+        xn, an = x[:sb * I].cpu().numpy(), anchors.cpu().numpy()
+        times = []
+        for rep in range(3):
+            t1 = time.perf_counter()
+            o = np.zeros(sb * O, np.float32)
+            ridx = oracle.check_detectors(xn, an, sb, I, T, Nc, train=False)
+            oracle.fill_outputs_fc(None, ridx, sb, O, T, E, out=o, q8=qn, scales=scn, int_mode=True,
+                                   int_rescaler=c["int_rescaler"])
+            oracle.convert_int_to_float(o, c["int_rescaler"])
+            dt = time.perf_counter() - t1
+            log(f"cpu baseline rep {rep}: {dt:.2f} s")
+            if rep > 0:
+                times.append(dt)
+        med = float(np.median(times))
+        cpu = {"value": sb / med, "unit": "samples/s", "cores": 1, "kind": "port",
+               "sample": f"config-4 workload at batch {sb} of {B}; median of 2 after 1 warm-up; step {med:.3f} s"}
+    res = {
+        "metric": "int8 LUT forward samples/sec at 8192 tables (BASELINE config 4)",
+        "value": round(B / (ms / 1e3), 1),
+        "unit": "samples/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 tables, int32 accumulators",
+        "data": "synthetic (seeded N(0,1) inputs, int8 tables uniform [-127,127], scales uniform [0.001,0.01])",
+        "config": {"workload": "BASELINE config 4: int8 LUT layer inference forward", "batch": B,
+                   "n_inputs": I, "n_tables": T, "anchors_per_table": Nc, "n_outputs": O,
+                   "table_bytes": T * E * O, "int_rescaler": c["int_rescaler"], "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": gb[dom], "ms_per_launch": round(dom_ms, 4),
+                     "kernels": {k: round(v[1] / v[0], 4) for k, v in ktimes.items()}},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
 
 
 TRANSFORMER = dict(vocab_size=256, embedding_dim=256, context_size=256, positional_dim=4, num_layers=4,
@@ -214,7 +309,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS) + [5])
+    ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS) + [4, 5])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="only run a plain copy of this many MiB (counter calibration) and exit")
@@ -229,6 +324,9 @@ def main():
 
     if args.config == 5:
         bench_transformer(args)
+        return
+    if args.config == 4:
+        bench_int8(args)
         return
 
     import torch

@@ -449,8 +449,8 @@ int spiky_lut_forward_step(spiky_lut_manager *m, const float *weights, uint32_t 
                       "check_detectors");
         });
         if (m->fully_connected == 1) {
-            if (spiky::tm_fill_applies(s)) {
-                void *scr = m->scratch_fwd.ensure(spiky::tm_fill_scratch_bytes(s));
+            if (spiky::tm_fill_applies(s, m->int_mode)) {
+                void *scr = m->scratch_fwd.ensure(spiky::tm_fill_scratch_bytes(s, m->int_mode));
                 m->timed("fill_outputs_fc", st, [&] {
                     check_hip(spiky::launch_fill_tm(s, weights, lookup_indices, output, m->int_mode,
                                                     m->int_rescaler, scr, st),
@@ -511,11 +511,20 @@ int spiky_lut_forward_step_i8(spiky_lut_manager *m, const int8_t *q8, const floa
                                                     min_deltas, min_delta_indices, st),
                       "check_detectors");
         });
-        m->timed("fill_outputs_fc_i8", st, [&] {
-            check_hip(spiky::launch_fill_fc_i8(s, q8, scales, lookup_indices, output, m->int_mode,
-                                               m->int_rescaler, st),
-                      "fill_outputs_fc_i8");
-        });
+        if (spiky::tm_fill_applies(s, m->int_mode)) {
+            void *scr = m->scratch_fwd.ensure(spiky::tm_fill_scratch_bytes(s, m->int_mode));
+            m->timed("fill_outputs_fc_i8", st, [&] {
+                check_hip(spiky::launch_fill_tm_i8(s, q8, scales, lookup_indices, output, m->int_mode,
+                                                   m->int_rescaler, scr, st),
+                          "fill_outputs_fc_i8");
+            });
+        } else {
+            m->timed("fill_outputs_fc_i8", st, [&] {
+                check_hip(spiky::launch_fill_fc_i8(s, q8, scales, lookup_indices, output, m->int_mode,
+                                                   m->int_rescaler, st),
+                          "fill_outputs_fc_i8");
+            });
+        }
     });
 }
 

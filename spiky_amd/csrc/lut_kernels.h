@@ -65,10 +65,14 @@ hipError_t launch_bucket_samples(const FcShape &s, const int32_t *idx, int32_t *
 // ---- table-major fully connected path (lut_tm.hip) ------------------------
 // Forward gather-sum through per-block partials in scratch; bit-identical to
 // launch_fill_fc_f32.  Applies to fp32 tables with E <= 256 and O % 4 == 0.
-bool tm_fill_applies(const FcShape &s);
-size_t tm_fill_scratch_bytes(const FcShape &s);
+bool tm_fill_applies(const FcShape &s, bool int_mode);
+size_t tm_fill_scratch_bytes(const FcShape &s, bool int_mode);
 hipError_t launch_fill_tm(const FcShape &s, const float *w, const int32_t *idx, float *out,
                           bool int_mode, double int_rescaler, void *scratch, hipStream_t st);
+// The same with int8 tables and one fp32 scale per table (weight = scale * q).
+hipError_t launch_fill_tm_i8(const FcShape &s, const int8_t *q8, const float *scales,
+                             const int32_t *idx, float *out, bool int_mode, double int_rescaler,
+                             void *scratch, hipStream_t st);
 
 // fp32-summation min-margin input gradient through per-slice partial dots.
 // out[i] (+)= sum over k of part[k][i] in ascending k (fp32, or wrapping int32

@@ -29,6 +29,9 @@
 // before adding it to HBM once (no global atomics).
 #include "lut_kernels.h"
 
+#include <algorithm>
+#include <type_traits>
+
 namespace spiky {
 namespace {
 
@@ -125,25 +128,41 @@ struct KeyPieces {
     static constexpr int kCount = StageLayout<KEY, SPT>::kKeys / kPer;
 };
 
-template <typename KEY, int SPT>
+// Row chunk of 4 weights at (row, col): fp32 tables load them; int8 tables
+// load 4 bytes and stage scale[t] * (float)q, the int8 mapping's weight.
+template <typename WT>
+__device__ __forceinline__ f32x4 load_quad(const WT *p, float sc);
+template <>
+__device__ __forceinline__ f32x4 load_quad<float>(const float *p, float) {
+    return *reinterpret_cast<const f32x4 *>(p);
+}
+template <>
+__device__ __forceinline__ f32x4 load_quad<int8_t>(const int8_t *p, float sc) {
+    const uint32_t raw = *reinterpret_cast<const uint32_t *>(p);
+    return f32x4{sc * (float)(int8_t)(raw & 0xFFu), sc * (float)(int8_t)((raw >> 8) & 0xFFu),
+                 sc * (float)(int8_t)((raw >> 16) & 0xFFu), sc * (float)(int8_t)(raw >> 24)};
+}
+
+template <typename KEY, int SPT, typename WT = float>
 __device__ __forceinline__ void stage_load(f32x4 (&rows)[kTmPF][2], u32x4 (&keys)[kTmPF],
-                                           const float *__restrict__ w,
+                                           const WT *__restrict__ w,
                                            const KEY *__restrict__ keys_t, uint32_t tid,
                                            uint32_t t_first, uint32_t nt, uint32_t n_entries,
                                            uint32_t n_outputs, uint32_t col0, uint32_t batch,
-                                           uint32_t b_base) {
+                                           uint32_t b_base, const float *__restrict__ scales = nullptr) {
     constexpr int kPer = KeyPieces<KEY, SPT>::kPer;
 #pragma unroll
     for (int p = 0; p < kTmPF; p++) {
         const uint32_t t = t_first + min((uint32_t)p, nt - 1);
-        const float *wt = w + (size_t)t * n_entries * n_outputs;
+        const WT *wt = w + (size_t)t * n_entries * n_outputs;
+        const float sc = scales ? scales[t] : 1.0f;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const uint32_t c = tid + (uint32_t)h * kTmThreads;
             const uint32_t row = (c >> 3) & (n_entries - 1);
             uint32_t col = col0 + (c & 7) * 4;
             if (col >= n_outputs) col = 0;
-            rows[p][h] = *reinterpret_cast<const f32x4 *>(wt + (size_t)row * n_outputs + col);
+            rows[p][h] = load_quad<WT>(wt + (size_t)row * n_outputs + col, sc);
         }
         if ((int)tid < KeyPieces<KEY, SPT>::kCount) {
             // keys of samples b_base + tid*kPer .. +kPer-1 (zero past the batch)
@@ -184,11 +203,15 @@ __device__ __forceinline__ void stage_store(const f32x4 (&rows)[kTmPF][2],
 // ---------------------------------------------------------------------------
 // Forward partials.  part[k][b][o] = commit value of table block k for (b, o).
 // ---------------------------------------------------------------------------
-template <int SPT, bool INT_MODE>
+// A unit covers bpu consecutive blocks of dgs tables (bpu = 1 for fp32 sums;
+// int32 payloads, whose wrapping sum is associative, may fold several blocks
+// into one partial).  Each block's payload is formed from its own fp64 sum.
+template <int SPT, bool INT_MODE, typename WT = float>
 __global__ __launch_bounds__(kTmThreads) void k_fill_tm(
-    const float *__restrict__ w, const uint8_t *__restrict__ idx_t, uint32_t *__restrict__ part,
-    uint32_t batch, uint32_t n_outputs, uint32_t n_detectors, uint32_t n_entries, uint32_t dgs,
-    uint32_t n_slices, uint32_t n_chunks, double int_rescaler) {
+    const WT *__restrict__ w, const float *__restrict__ scales, const uint8_t *__restrict__ idx_t,
+    uint32_t *__restrict__ part, uint32_t batch, uint32_t n_outputs, uint32_t n_detectors,
+    uint32_t n_entries, uint32_t dgs, uint32_t bpu, uint32_t n_slices, uint32_t n_chunks,
+    double int_rescaler) {
     using L = StageLayout<uint8_t, SPT>;
     __shared__ __attribute__((aligned(16))) uint8_t smem[2 * L::kStageBytes];
     const uint32_t tid = threadIdx.x;
@@ -198,8 +221,8 @@ __global__ __launch_bounds__(kTmThreads) void k_fill_tm(
     const uint32_t rest = blockIdx.x / n_slices;
     const uint32_t chunk = rest % n_chunks;
     const uint32_t k = rest / n_chunks;
-    const uint32_t t0 = k * dgs;
-    const uint32_t t1 = min(t0 + dgs, n_detectors);
+    const uint32_t t0 = k * dgs * bpu;
+    const uint32_t t1 = min(t0 + dgs * bpu, n_detectors);
     const uint32_t b_base = chunk * (kTmPass * SPT);
     const uint32_t col0 = slice * kTmCols;
     const uint32_t q = lane & 7;
@@ -208,17 +231,21 @@ __global__ __launch_bounds__(kTmThreads) void k_fill_tm(
     const uint32_t s_loc0 = wave * 8 + (lane >> 3);
 
     double acc[SPT][4];
+    int32_t ipay[SPT][4];
 #pragma unroll
     for (int i = 0; i < SPT; i++)
 #pragma unroll
-        for (int c = 0; c < 4; c++) acc[i][c] = 0.0;
+        for (int c = 0; c < 4; c++) {
+            acc[i][c] = 0.0;
+            ipay[i][c] = 0;
+        }
 
     const uint32_t nt_all = t1 - t0;
     const uint32_t n_stages = (nt_all + kTmPF - 1) / kTmPF;
     f32x4 rows[kTmPF][2];
     u32x4 keys4[kTmPF];
-    stage_load<uint8_t, SPT>(rows, keys4, w, idx_t, tid, t0, min((uint32_t)kTmPF, nt_all), n_entries,
-                             n_outputs, col0, batch, b_base);
+    stage_load<uint8_t, SPT, WT>(rows, keys4, w, idx_t, tid, t0, min((uint32_t)kTmPF, nt_all), n_entries,
+                                 n_outputs, col0, batch, b_base, scales);
     for (uint32_t st = 0; st < n_stages; st++) {
         uint8_t *stage = smem + (st & 1) * L::kStageBytes;
         stage_store<uint8_t, SPT>(rows, keys4, stage, tid);
@@ -226,8 +253,8 @@ __global__ __launch_bounds__(kTmThreads) void k_fill_tm(
         const uint32_t nt = min((uint32_t)kTmPF, t1 - ts);
         if (st + 1 < n_stages) {
             const uint32_t tn = ts + kTmPF;
-            stage_load<uint8_t, SPT>(rows, keys4, w, idx_t, tid, tn, min((uint32_t)kTmPF, t1 - tn),
-                                     n_entries, n_outputs, col0, batch, b_base);
+            stage_load<uint8_t, SPT, WT>(rows, keys4, w, idx_t, tid, tn, min((uint32_t)kTmPF, t1 - tn),
+                                         n_entries, n_outputs, col0, batch, b_base, scales);
         }
         __syncthreads();
         for (uint32_t p = 0; p < nt; p++) {
@@ -242,6 +269,17 @@ __global__ __launch_bounds__(kTmThreads) void k_fill_tm(
                 acc[i][2] += (double)v.z;
                 acc[i][3] += (double)v.w;
             }
+            // end of a block of dgs tables: its int32 payload joins the unit's sum
+            const uint32_t tt = ts + p + 1;
+            if (INT_MODE && ((tt - t0) % dgs == 0 || tt == t1)) {
+#pragma unroll
+                for (int i = 0; i < SPT; i++)
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        ipay[i][c] = wrap_add(ipay[i][c], (int32_t)(acc[i][c] * kDenom32 * int_rescaler));
+                        acc[i][c] = 0.0;
+                    }
+            }
         }
     }
     if (col >= n_outputs) return;
@@ -251,10 +289,10 @@ __global__ __launch_bounds__(kTmThreads) void k_fill_tm(
         if (b >= batch) continue;
         uint4 o;
         if (INT_MODE) {
-            o.x = (uint32_t)(int32_t)(acc[i][0] * kDenom32 * int_rescaler);
-            o.y = (uint32_t)(int32_t)(acc[i][1] * kDenom32 * int_rescaler);
-            o.z = (uint32_t)(int32_t)(acc[i][2] * kDenom32 * int_rescaler);
-            o.w = (uint32_t)(int32_t)(acc[i][3] * kDenom32 * int_rescaler);
+            o.x = (uint32_t)ipay[i][0];
+            o.y = (uint32_t)ipay[i][1];
+            o.z = (uint32_t)ipay[i][2];
+            o.w = (uint32_t)ipay[i][3];
         } else {
             o.x = __float_as_uint((float)acc[i][0]);
             o.y = __float_as_uint((float)acc[i][1]);
@@ -262,6 +300,147 @@ __global__ __launch_bounds__(kTmThreads) void k_fill_tm(
             o.w = __float_as_uint((float)acc[i][3]);
         }
         // written once, read once by the commit kernel: non-temporal
+        __builtin_nontemporal_store(
+            u32x4{o.x, o.y, o.z, o.w},
+            reinterpret_cast<u32x4 *>(part + ((size_t)k * batch + b) * n_outputs + col));
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Forward partials, LDS-DMA form (fp32 tables with 256 entries): a ring of
+// kDmaRing one-table stages in LDS, filled by global_load_lds_dwordx4 three
+// tables ahead (no staging registers).  Lane l of a wave writes 16 bytes at
+// the wave's LDS base + 16 l, so chunk c of a stage (row c / 8, column quad
+// c % 8) lands at byte 16 c: the [row][128 B] image the compute reads.  The
+// stage's keys (SPT * 128 samples, u8) come from a transposed index padded to
+// whole chunks of samples, loaded by wave 0.  Each wave waits for its own
+// loads with an explicit vmcnt, then the workgroup barrier publishes the
+// stage.  Arithmetic and partials are those of k_fill_tm.
+// ---------------------------------------------------------------------------
+constexpr int kDmaRing = 4;
+constexpr int kDmaRows = kTmMaxEntries * 128;  // bytes of a stage's rows
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ void dma16(const void *g, void *lds_base) {
+    __builtin_amdgcn_global_load_lds(g, (lds_void *)lds_base, 16, 0, 0);
+}
+
+// wait until at most N of this wave's vector-memory loads are outstanding
+__device__ __forceinline__ void wait_vm(uint32_t n) {
+    switch (n) {
+        case 0: __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+        case 1: __asm__ volatile("s_waitcnt vmcnt(1)" ::: "memory"); break;
+        case 2: __asm__ volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
+        case 3: __asm__ volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
+        case 4: __asm__ volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+        case 5: __asm__ volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
+        default: __asm__ volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
+    }
+}
+
+template <int SPT, bool INT_MODE>
+__global__ __launch_bounds__(kTmThreads) void k_fill_tm_dma(
+    const float *__restrict__ w, const uint8_t *__restrict__ idx_t, uint32_t *__restrict__ part,
+    uint32_t batch, uint32_t pitch, uint32_t n_outputs, uint32_t n_detectors, uint32_t dgs,
+    uint32_t bpu, uint32_t n_slices, uint32_t n_chunks, double int_rescaler) {
+    constexpr int kKeyBytes = kTmPass * SPT;
+    constexpr int kStage = kDmaRows + kKeyBytes;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[kDmaRing * kStage];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & (kWave - 1);
+    const uint32_t wave = tid / kWave;
+    const uint32_t slice = blockIdx.x % n_slices;
+    const uint32_t rest = blockIdx.x / n_slices;
+    const uint32_t chunk = rest % n_chunks;
+    const uint32_t k = rest / n_chunks;
+    const uint32_t t0 = k * dgs * bpu;
+    const uint32_t t1 = min(t0 + dgs * bpu, n_detectors);
+    const uint32_t b_base = chunk * kKeyBytes;
+    const uint32_t col0 = slice * kTmCols;
+    const uint32_t q = lane & 7;
+    const uint32_t col = col0 + q * 4;
+    const uint32_t s_loc0 = wave * 8 + (lane >> 3);
+    // this thread's two row chunks of every stage
+    uint32_t goff[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const uint32_t c = tid + (uint32_t)h * kTmThreads;
+        uint32_t cc = col0 + (c & 7) * 4;
+        if (cc >= n_outputs) cc = 0;
+        goff[h] = (c >> 3) * n_outputs + cc;
+    }
+    const uint32_t n_loads = wave == 0 ? 3u : 2u;  // per stage, this wave
+    auto issue = [&](uint32_t si) {
+        const uint32_t t = t0 + si;
+        uint8_t *stage = smem + (si % kDmaRing) * kStage;
+        const float *wt = w + (size_t)t * kTmMaxEntries * n_outputs;
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+            dma16(wt + goff[h], stage + ((uint32_t)h * kTmThreads + wave * kWave) * 16);
+        if (wave == 0) {
+            // the stage's keys: kKeyBytes bytes, 16 per lane of the first lanes
+            if (lane * 16 < (uint32_t)kKeyBytes)
+                dma16(idx_t + (size_t)t * pitch + b_base + lane * 16, stage + kDmaRows);
+        }
+    };
+
+    double acc[SPT][4];
+    int32_t ipay[SPT][4];
+#pragma unroll
+    for (int i = 0; i < SPT; i++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            acc[i][c] = 0.0;
+            ipay[i][c] = 0;
+        }
+    const uint32_t nt = t1 - t0;
+    for (uint32_t si = 0; si < min((uint32_t)(kDmaRing - 1), nt); si++) issue(si);
+    for (uint32_t st = 0; st < nt; st++) {
+        // stages issued so far: 0 .. min(st + ring - 2, nt - 1); wait for st's
+        wait_vm(min((uint32_t)(kDmaRing - 2), nt - 1 - st) * n_loads);
+        // stage st visible to all waves; every wave is done with stage st - 1
+        // (its reads of it were consumed).  A bare s_barrier: __syncthreads'
+        // fence would also wait for the later stages' loads.
+        __asm__ volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        __asm__ volatile("" ::: "memory");
+        if (st + kDmaRing - 1 < nt) issue(st + kDmaRing - 1);
+        const uint8_t *tb = smem + (st % kDmaRing) * kStage;
+        const uint8_t *keys = tb + kDmaRows;
+#pragma unroll
+        for (int i = 0; i < SPT; i++) {
+            const uint32_t r = (uint32_t)keys[s_loc0 + kTmPass * i];
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(tb + r * 128 + q * 16);
+            acc[i][0] += (double)v.x;
+            acc[i][1] += (double)v.y;
+            acc[i][2] += (double)v.z;
+            acc[i][3] += (double)v.w;
+        }
+        const uint32_t tt = t0 + st + 1;
+        if (INT_MODE && ((tt - t0) % dgs == 0 || tt == t1)) {
+#pragma unroll
+            for (int i = 0; i < SPT; i++)
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    ipay[i][c] = wrap_add(ipay[i][c], (int32_t)(acc[i][c] * kDenom32 * int_rescaler));
+                    acc[i][c] = 0.0;
+                }
+        }
+    }
+    if (col >= n_outputs) return;
+#pragma unroll
+    for (int i = 0; i < SPT; i++) {
+        const uint32_t b = b_base + s_loc0 + kTmPass * i;
+        if (b >= batch) continue;
+        uint4 o;
+        if (INT_MODE) {
+            o = make_uint4((uint32_t)ipay[i][0], (uint32_t)ipay[i][1], (uint32_t)ipay[i][2],
+                           (uint32_t)ipay[i][3]);
+        } else {
+            o = make_uint4(__float_as_uint((float)acc[i][0]), __float_as_uint((float)acc[i][1]),
+                           __float_as_uint((float)acc[i][2]), __float_as_uint((float)acc[i][3]));
+        }
         __builtin_nontemporal_store(
             u32x4{o.x, o.y, o.z, o.w},
             reinterpret_cast<u32x4 *>(part + ((size_t)k * batch + b) * n_outputs + col));
@@ -517,9 +696,11 @@ __global__ __launch_bounds__(kScatterThreads) void k_propagate_scatter(
 }
 
 // keys_t[t][b] = idx[b][t] (u8), through a 64x64 LDS tile.
+// idx_t[t][b] (row pitch `pitch` >= batch; samples past the batch get 0).
 __global__ __launch_bounds__(256) void k_transpose_idx(const int32_t *__restrict__ idx,
                                                        uint8_t *__restrict__ idx_t,
-                                                       uint32_t batch, uint32_t n_detectors) {
+                                                       uint32_t batch, uint32_t n_detectors,
+                                                       uint32_t pitch) {
     __shared__ uint8_t tile[64][65];
     const uint32_t tb = blockIdx.x * 64;  // table tile
     const uint32_t bb = blockIdx.y * 64;  // sample tile
@@ -527,12 +708,12 @@ __global__ __launch_bounds__(256) void k_transpose_idx(const int32_t *__restrict
     const uint32_t ty = threadIdx.x >> 6;
     for (uint32_t r = ty; r < 64; r += 4) {
         const uint32_t b = bb + r, t = tb + tx;
-        if (b < batch && t < n_detectors) tile[r][tx] = (uint8_t)idx[(size_t)b * n_detectors + t];
+        tile[r][tx] = (b < batch && t < n_detectors) ? (uint8_t)idx[(size_t)b * n_detectors + t] : 0;
     }
     __syncthreads();
     for (uint32_t r = ty; r < 64; r += 4) {
         const uint32_t t = tb + r, b = bb + tx;
-        if (b < batch && t < n_detectors) idx_t[(size_t)t * batch + b] = tile[tx][r];
+        if (b < pitch && t < n_detectors) idx_t[(size_t)t * pitch + b] = tile[tx][r];
     }
 }
 
@@ -574,38 +755,83 @@ uint32_t tm_spt(uint32_t batch) {
 
 }  // namespace
 
-bool tm_fill_applies(const FcShape &s) {
+// Blocks of dgs tables per unit: 1 for fp32 sums (every block is a rounding
+// point committed in order); with int32 payloads, enough to leave about 2048
+// units.
+static uint32_t tm_fill_bpu(const FcShape &s, bool int_mode) {
+    if (!int_mode) return 1;
     const uint64_t n_blocks = (s.n_detectors + s.dgs - 1) / s.dgs;
+    const uint64_t spt = tm_spt(s.batch);
+    const uint64_t n_chunks = (s.batch + kTmPass * spt - 1) / (kTmPass * spt);
+    const uint64_t n_slices = (s.n_outputs + kTmCols - 1) / kTmCols;
+    const uint64_t units = n_blocks * n_chunks * n_slices;
+    return (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(n_blocks, units / 2048));
+}
+
+bool tm_fill_applies(const FcShape &s, bool int_mode) {
+    const uint64_t n_blocks = (s.n_detectors + s.dgs - 1) / s.dgs;
+    const uint64_t bpu = tm_fill_bpu(s, int_mode);
     return s.batch >= 256 && s.n_entries <= (uint32_t)kTmMaxEntries && s.n_outputs % 4 == 0 &&
            s.n_outputs >= 64 && s.dgs >= 8 &&
-           n_blocks * s.batch * s.n_outputs * 4 <= (4ull << 30);
+           ((n_blocks + bpu - 1) / bpu) * s.batch * s.n_outputs * 4 <= (4ull << 30);
 }
 
-size_t tm_fill_scratch_bytes(const FcShape &s) {
+// Row pitch of the transposed index: whole chunks of samples, so that every
+// stage's key row can be loaded in 16-byte pieces.
+static uint32_t tm_fill_pitch(const FcShape &s) {
+    const uint32_t spt = tm_spt(s.batch);
+    const uint32_t n_chunks = (s.batch + kTmPass * spt - 1) / (kTmPass * spt);
+    return n_chunks * kTmPass * spt;
+}
+
+size_t tm_fill_scratch_bytes(const FcShape &s, bool int_mode) {
     const uint64_t n_blocks = (s.n_detectors + s.dgs - 1) / s.dgs;
-    const size_t keys = ((size_t)s.n_detectors * s.batch + 255) & ~(size_t)255;
-    return keys + (size_t)n_blocks * s.batch * s.n_outputs * 4;
+    const uint64_t bpu = tm_fill_bpu(s, int_mode);
+    const size_t keys = ((size_t)s.n_detectors * tm_fill_pitch(s) + 255) & ~(size_t)255;
+    return keys + (size_t)((n_blocks + bpu - 1) / bpu) * s.batch * s.n_outputs * 4;
 }
 
-hipError_t launch_fill_tm(const FcShape &s, const float *w, const int32_t *idx, float *out,
-                          bool int_mode, double int_rescaler, void *scratch, hipStream_t st) {
+template <typename WT>
+static hipError_t launch_fill_tm_impl(const FcShape &s, const WT *w, const float *scales,
+                                      const int32_t *idx, float *out, bool int_mode,
+                                      double int_rescaler, void *scratch, hipStream_t st) {
     uint8_t *idx_t = reinterpret_cast<uint8_t *>(scratch);
-    const size_t keys = ((size_t)s.n_detectors * s.batch + 255) & ~(size_t)255;
+    const uint32_t pitch = tm_fill_pitch(s);
+    const size_t keys = ((size_t)s.n_detectors * pitch + 255) & ~(size_t)255;
     uint32_t *part = reinterpret_cast<uint32_t *>(reinterpret_cast<uint8_t *>(scratch) + keys);
-    hipLaunchKernelGGL(k_transpose_idx, dim3((s.n_detectors + 63) / 64, (s.batch + 63) / 64),
-                       dim3(256), 0, st, idx, idx_t, s.batch, s.n_detectors);
+    // the DMA form reads whole 16-byte key pieces: pad the rows with zeros
+    const bool dma = std::is_same<WT, float>::value && s.n_entries == (uint32_t)kTmMaxEntries;
+    const uint32_t ipitch = dma ? pitch : s.batch;
+    hipLaunchKernelGGL(k_transpose_idx, dim3((s.n_detectors + 63) / 64, (ipitch + 63) / 64),
+                       dim3(256), 0, st, idx, idx_t, s.batch, s.n_detectors, ipitch);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const uint32_t spt = tm_spt(s.batch);
     const uint32_t n_chunks = (s.batch + kTmPass * spt - 1) / (kTmPass * spt);
     const uint32_t n_slices = (s.n_outputs + kTmCols - 1) / kTmCols;
     const uint32_t n_blocks = (s.n_detectors + s.dgs - 1) / s.dgs;
-    const uint64_t grid = (uint64_t)n_blocks * n_chunks * n_slices;
+    const uint32_t bpu = tm_fill_bpu(s, int_mode);
+    const uint32_t n_parts = (n_blocks + bpu - 1) / bpu;
+    const uint64_t grid = (uint64_t)n_parts * n_chunks * n_slices;
     if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
-#define SPIKY_TM(SPT, IM)                                                                        \
-    hipLaunchKernelGGL((k_fill_tm<SPT, IM>), dim3((uint32_t)grid), dim3(kTmThreads), 0, st, w,  \
-                       idx_t, part, s.batch, s.n_outputs, s.n_detectors, s.n_entries, s.dgs,   \
+    if (dma) {
+        const float *wf = reinterpret_cast<const float *>(w);
+#define SPIKY_TMD(SPT, IM)                                                                          \
+    hipLaunchKernelGGL((k_fill_tm_dma<SPT, IM>), dim3((uint32_t)grid), dim3(kTmThreads), 0, st, wf, \
+                       idx_t, part, s.batch, ipitch, s.n_outputs, s.n_detectors, s.dgs, bpu,       \
                        n_slices, n_chunks, int_rescaler)
+        switch (spt) {
+            case 1: if (int_mode) SPIKY_TMD(1, true); else SPIKY_TMD(1, false); break;
+            case 2: if (int_mode) SPIKY_TMD(2, true); else SPIKY_TMD(2, false); break;
+            case 4: if (int_mode) SPIKY_TMD(4, true); else SPIKY_TMD(4, false); break;
+            default: if (int_mode) SPIKY_TMD(8, true); else SPIKY_TMD(8, false); break;
+        }
+#undef SPIKY_TMD
+    } else {
+#define SPIKY_TM(SPT, IM)                                                                            \
+    hipLaunchKernelGGL((k_fill_tm<SPT, IM, WT>), dim3((uint32_t)grid), dim3(kTmThreads), 0, st, w,  \
+                       scales, idx_t, part, s.batch, s.n_outputs, s.n_detectors, s.n_entries, s.dgs, \
+                       bpu, n_slices, n_chunks, int_rescaler)
     switch (spt) {
         case 1: if (int_mode) SPIKY_TM(1, true); else SPIKY_TM(1, false); break;
         case 2: if (int_mode) SPIKY_TM(2, true); else SPIKY_TM(2, false); break;
@@ -613,6 +839,7 @@ hipError_t launch_fill_tm(const FcShape &s, const float *w, const int32_t *idx, 
         default: if (int_mode) SPIKY_TM(8, true); else SPIKY_TM(8, false); break;
     }
 #undef SPIKY_TM
+    }
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     const uint64_t n_quads = (uint64_t)s.batch * s.n_outputs / 4;
@@ -620,11 +847,22 @@ hipError_t launch_fill_tm(const FcShape &s, const float *w, const int32_t *idx, 
     const uint32_t cgrid = (uint32_t)((n_quads + 255) / 256);
     if (int_mode)
         hipLaunchKernelGGL(k_fill_commit<true>, dim3(cgrid), dim3(256), 0, st, part, out, n_quads,
-                           n_blocks, stride, int_rescaler);
+                           n_parts, stride, int_rescaler);
     else
         hipLaunchKernelGGL(k_fill_commit<false>, dim3(cgrid), dim3(256), 0, st, part, out,
-                           n_quads, n_blocks, stride, int_rescaler);
+                           n_quads, n_parts, stride, int_rescaler);
     return hipGetLastError();
+}
+
+hipError_t launch_fill_tm(const FcShape &s, const float *w, const int32_t *idx, float *out,
+                          bool int_mode, double int_rescaler, void *scratch, hipStream_t st) {
+    return launch_fill_tm_impl<float>(s, w, nullptr, idx, out, int_mode, int_rescaler, scratch, st);
+}
+
+hipError_t launch_fill_tm_i8(const FcShape &s, const int8_t *q8, const float *scales,
+                             const int32_t *idx, float *out, bool int_mode, double int_rescaler,
+                             void *scratch, hipStream_t st) {
+    return launch_fill_tm_impl<int8_t>(s, q8, scales, idx, out, int_mode, int_rescaler, scratch, st);
 }
 
 hipError_t launch_block_commit(const uint32_t *part, float *out, uint64_t n, uint32_t n_blocks,

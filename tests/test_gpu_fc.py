@@ -245,6 +245,38 @@ def test_int8_tables(oracle, cuda_device, B, O):
         assert np.array_equal(out.cpu().numpy(), rout)
 
 
+@pytest.mark.parametrize("tables", ["int8", "fp32"])
+def test_table_major_folded_blocks(oracle, cuda_device, tables):
+    """int32 summation with many 8-table blocks: the table-major forward folds
+    several blocks' payloads into one partial (wrapping int32 sums are
+    associative); every accumulator must still be bit-exact."""
+    dev = cuda_device
+    B, I, T, Nc, O, dgs, resc = 300, 256, 16384, 6, 64, 8, 0.25
+    E = 1 << Nc
+    g = torch.Generator().manual_seed(31)
+    x = torch.randn(B * I, generator=g)
+    anchors = torch.stack([torch.randperm(I, generator=g)[:2] for _ in range(T * Nc)]).to(torch.int32).flatten()
+    dm = make_dm(I, O, T, Nc, 32, dgs, int_rescaler=resc)
+    out = torch.zeros(B * O, device=dev)
+    idx = torch.empty(B * T, dtype=torch.int32, device=dev)
+    if tables == "int8":
+        q = torch.randint(-127, 128, (T * E * O,), generator=g, dtype=torch.int8)
+        sc = torch.rand(T, generator=g) * 0.009 + 0.001
+        dm.forward_step_i8(q.to(dev), sc.to(dev), B, x.to(dev), anchors.to(dev), out, idx)
+        kw = dict(q8=q.numpy(), scales=sc.numpy())
+        W = None
+    else:
+        W = (torch.randn(T * E * O, generator=g) * 0.01)
+        dm.forward_step(W.to(dev), B, x.to(dev), anchors.to(dev), out, idx)
+        kw = {}
+        W = W.numpy()
+    ridx = oracle.check_detectors(x.numpy(), anchors.numpy(), B, I, T, Nc, train=False)
+    rout = oracle.fill_outputs_fc(W, ridx, B, O, T, E, dgs=dgs, int_mode=True, int_rescaler=resc, **kw)
+    oracle.convert_int_to_float(rout, resc)
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    assert np.array_equal(out.cpu().numpy(), rout)
+
+
 def test_errors_on_device(cuda_device):
     dev = cuda_device
     dm = make_dm(8, 4, 4, 2)
