@@ -573,11 +573,13 @@ __global__ __launch_bounds__(kTmThreads) void k_propagate_tm(
                 const uint32_t ra = (key >> 8) & emask;
                 const f32x4 a = *reinterpret_cast<const f32x4 *>(tb + rm * 128 + q * 16);
                 const f32x4 e = *reinterpret_cast<const f32x4 *>(tb + ra * 128 + q * 16);
-                double d = ((double)a.x - (double)e.x) * (double)gv[i].x;
-                d += ((double)a.y - (double)e.y) * (double)gv[i].y;
-                d += ((double)a.z - (double)e.z) * (double)gv[i].z;
-                d += ((double)a.w - (double)e.w) * (double)gv[i].w;
-                dv[i] = d;
+                // the lane's 4-column piece in fp32 (error ~1e-7 of its terms),
+                // the sums over lanes, slices and tables in fp64
+                float d = (a.x - e.x) * gv[i].x;
+                d = __builtin_fmaf(a.y - e.y, gv[i].y, d);
+                d = __builtin_fmaf(a.z - e.z, gv[i].z, d);
+                d = __builtin_fmaf(a.w - e.w, gv[i].w, d);
+                dv[i] = (double)d;
             }
             // the 8 lanes of a sample group each hold a 4-column piece of the
             // SPT dots; after the reduce-scatter lane q holds sample rs_item's sum
