@@ -134,6 +134,132 @@ def cpu_baseline(x, anchors, W, go, B_full, I, T, Nc, O, sample_B):
     }
 
 
+PROJ = dict(B=128, cpu_reps=121)
+
+
+def build_projection_stack(device, seed=1):
+    """BASELINE config 2 on this build's ProjectionLUTLayer: 28x28 input;
+    layer 1 a 12x12 grid (stride 2) of 5x5 receptive fields, 32 tables of 5
+    anchor pairs per group, each projecting onto a 4x4 patch (16 channels) of
+    a 48x48 map; layer 2 a 5x5 grid (stride 2 positions = 8 pixels) of 3x3-
+    position (12x12-pixel) windows of that map, 64 tables of 6 pairs per group,
+    each onto 4x8 = 32 channels of a 20x40 map; a dense head of 128 tables,
+    6 pairs, 10 outputs."""
+    from spiky_amd import LUTLayer, ProjectionLUTLayer
+    from spiky_amd.util.synapse_growth import PointSamplingPolicy, PointSamplingType
+    l1 = ProjectionLUTLayer((28, 28), (48, 48), 5, 144, 32, (5, 5), (4, 4),
+                            detectors_sampling_policy=PointSamplingPolicy(
+                                PointSamplingType.Grid, pad_h=2.0, pad_w=2.0, grid_h=12, grid_w=12,
+                                stride_h=2, stride_w=2),
+                            random_seed=seed, device=device)
+    l2 = ProjectionLUTLayer((48, 48), (20, 40), 6, 25, 64, (12, 12), (4, 8),
+                            detectors_sampling_policy=PointSamplingPolicy(
+                                PointSamplingType.Grid, pad_h=6.0, pad_w=6.0, grid_h=5, grid_w=5,
+                                stride_h=8, stride_w=8),
+                            random_seed=seed + 1, device=device)
+    head = LUTLayer(800, 6, 128, 10, random_seed=seed + 2, device=device)
+    return l1, l2, head
+
+
+def bench_projection(args):
+    """the sparse ProjectionLUTLayer stack forward and
+    backward at batch 128 on 80%-zero uniform images."""
+    import torch
+    import numpy as np
+    B = PROJ["B"]
+    dev = torch.device("cuda:0")
+    log("config 2: ProjectionLUTLayer stack")
+    l1, l2, head = build_projection_stack(dev)
+    gen = torch.Generator(device=dev).manual_seed(2)
+    with torch.no_grad():
+        for layer in (l1, l2, head):
+            layer._weights.normal_(0.0, 0.01, generator=gen)
+    gx = torch.Generator(device=dev).manual_seed(0)
+    x = torch.rand(B, 1, 28, 28, device=dev, generator=gx)
+    x = (x * (torch.rand(B, 1, 28, 28, device=dev, generator=gx) > 0.8)).requires_grad_(True)
+    g = torch.randn(B, 1, 10, device=dev, generator=gx)
+    params = [l1._weights, l2._weights, head._weights]
+
+    def step():
+        for p_ in params:
+            p_.grad = None
+        x.grad = None
+        y1 = l1(x)
+        y2 = l2(y1.reshape(B, 1, 48, 48))
+        out = head(y2.reshape(B, 1, 800))
+        out.backward(g)
+
+    log("warmup")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} steps")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    log(f"{ms:.3f} ms/step")
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_projection(l1, l2, head, x.detach(), g, B, PROJ["cpu_reps"])
+    res = {
+        "metric": "ProjectionLUTLayer stack fwd+bwd samples/sec (BASELINE config 2)",
+        "value": round(B / (ms / 1e3), 1),
+        "unit": "samples/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32 (fp64 partial sums)",
+        "data": "synthetic (uniform [0,1) 28x28 images with 80% of pixels zeroed, N(0,0.01) tables, N(0,1) grads)",
+        "config": {"workload": "BASELINE config 2: sparse ProjectionLUTLayer stack fwd+bwd", "batch": B,
+                   "layer1": "28x28 -> 48x48, 144 groups x 32 tables, 5 pairs, 5x5 fields, 16 targets",
+                   "layer2": "48x48 -> 20x40, 25 groups x 64 tables, 6 pairs, 12x12 fields, 32 targets",
+                   "head": "800 -> 10, 128 tables, 6 pairs", "parallelism": "single GPU"},
+        "roofline": None,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+
+
+def cpu_projection(l1, l2, head, x, g, B, reps):
+    """The C oracle over the same stack: forward through the three layers, then
+    backward (input and weight gradients of each)."""
+    import numpy as np
+    import oracle
+
+    def sparse_parts(layer):
+        offs, tg = layer._lut_dm.lookup_connectivity()
+        return (layer._weights.detach().cpu().numpy(), layer._detector_anchors.cpu().numpy(), offs, tg,
+                layer._lut_dm.get_max_forward_groups_per_neuron())
+
+    p1, p2 = sparse_parts(l1), sparse_parts(l2)
+    Wh, ah = head._weights.detach().cpu().numpy(), head._detector_anchors.cpu().numpy()
+    xn, gn = x.cpu().numpy().reshape(-1), g.cpu().numpy().reshape(-1)
+    times = []
+    for rep in range(reps):
+        t0 = time.perf_counter()
+        acts = [xn]
+        saved = []
+        for (W, an, offs, tg, _), (I, O, T, Nc) in ((p1, (784, 2304, 4608, 5)), (p2, (2304, 800, 1600, 6))):
+            idx, md, mi = oracle.check_detectors(acts[-1], an, B, I, T, Nc)
+            saved.append((idx, md, mi))
+            acts.append(oracle.fill_outputs_sparse(W, idx, offs, tg, B, O, T, 1 << Nc))
+        hidx, hmd, hmi = oracle.check_detectors(acts[-1], ah, B, 800, 128, 6)
+        oracle.fill_outputs_fc(Wh, hidx, B, 10, 128, 64)
+        grad = oracle.propagate_fc(Wh, gn, hidx, hmd, hmi, ah, B, 800, 10, 128, 6, 64)
+        oracle.gather_wgrad_fc(gn, hidx, np.zeros(Wh.size, np.float32), B, 10, 128, 64)
+        for (W, an, offs, tg, maxg), (idx, md, mi), (I, O, T, Nc) in (
+                (p2, saved[1], (2304, 800, 1600, 6)), (p1, saved[0], (784, 2304, 4608, 5))):
+            oracle.gather_wgrad_sparse(grad, idx, offs, tg, np.zeros(W.size, np.float32), B, O, T, 1 << Nc)
+            grad = oracle.propagate_sparse(W, grad, idx, md, mi, an, offs, tg, B, I, O, T, Nc, 1 << Nc, 32, maxg)
+        dt = time.perf_counter() - t0
+        if rep > 0:
+            times.append(dt)
+    med = float(np.median(times))
+    return {"value": B / med, "unit": "samples/s", "cores": 1, "kind": "port",
+            "sample": f"the whole config-2 step at batch {B}; median of {reps - 1} after 1 warm-up; step {med:.3f} s"}
+
+
 INT8 = dict(B=4096, I=4096, T=8192, Nc=8, O=1024, int_rescaler=0.001, cpu_B=2048)
 
 
@@ -309,7 +435,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS) + [4, 5])
+    ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS) + [2, 4, 5])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="only run a plain copy of this many MiB (counter calibration) and exit")
@@ -327,6 +453,9 @@ def main():
         return
     if args.config == 4:
         bench_int8(args)
+        return
+    if args.config == 2:
+        bench_projection(args)
         return
 
     import torch

@@ -182,8 +182,10 @@ class _LUTDataManagerBase:
                                  random_seed=None):
         """Detector input lists from a ChunkOfConnections buffer (lut.cu:332-430):
         sources are input neurons [0, n_inputs), targets detector neurons
-        [n_inputs, n_inputs + n_detectors) after ids_shift."""
-        check_tensor(connections_buffer, "connections_buffer", False, self._device, 4)
+        [n_inputs, n_inputs + n_detectors) after ids_shift.  The lists are built on
+        the host, so the buffer may live on the host or on the manager's device."""
+        check_tensor(connections_buffer, "connections_buffer", False,
+                     -1 if connections_buffer.device.type == "cpu" else self._device, 4)
         src, tgt = parse_connections(connections_buffer, single_input_group_size, ids_shift)
         det = tgt - self._n_inputs
         ok = (src >= 0) & (src < self._n_inputs) & (det >= 0) & (det < self._n_detectors)
@@ -250,12 +252,14 @@ class _LUTDataManagerBase:
                                random_seed=None):
         """Lookup neuron -> output synapses from a ChunkOfConnections buffer
         (lut.cu:560-578): sources are lookup neurons [0, n_lookup), targets
-        output neurons [n_lookup, n_lookup + n_outputs) after ids_shift."""
+        output neurons [n_lookup, n_lookup + n_outputs) after ids_shift.  Built on
+        the host: the buffer may live on the host or on the manager's device."""
         if self._fully_connected:
             raise ValueError("can't add lookup connections in fully connected mode")
         if self._fully_connected is None:
             raise ValueError("neurons are not initialized (call initialize_neurons first)")
-        check_tensor(connections_buffer, "connections_buffer", False, self._device, 4)
+        check_tensor(connections_buffer, "connections_buffer", False,
+                     -1 if connections_buffer.device.type == "cpu" else self._device, 4)
         src, tgt = parse_connections(connections_buffer, single_input_group_size, ids_shift)
         out = tgt - self._n_lookup
         ok = (src >= 0) & (src < self._n_lookup) & (out >= 0) & (out < self._n_outputs)

@@ -95,6 +95,23 @@ def test_projection_layer_sparse_parity(oracle, cuda_device):
     assert np.array_equal(layer._weights.grad.cpu().numpy(), rwg)
 
 
+def test_projection_layer_built_on_device(cuda_device):
+    """A ProjectionLUTLayer constructed with device=cuda grows its connectivity
+    on the host and gives the same layer as one built on the host and moved."""
+    dev = cuda_device
+    kw = dict(random_seed=7)
+    a = ProjectionLUTLayer((16, 16), (12, 12), 4, 9, 4, (5, 5), (4, 4), device=dev, **kw)
+    b = ProjectionLUTLayer((16, 16), (12, 12), 4, 9, 4, (5, 5), (4, 4), **kw).to(dev)
+    assert torch.equal(a._detector_anchors.cpu(), b._detector_anchors.cpu())
+    oa, ta = a._lut_dm.lookup_connectivity()
+    ob, tb = b._lut_dm.lookup_connectivity()
+    assert np.array_equal(np.asarray(oa), np.asarray(ob)) and np.array_equal(np.asarray(ta), np.asarray(tb))
+    with torch.no_grad():
+        b._weights.copy_(a._weights)
+    x = torch.rand(3, 1, 16, 16, device=dev)
+    assert torch.equal(a(x), b(x))
+
+
 @pytest.mark.parametrize("B", [1024])
 def test_config3_full_size(oracle, cuda_device, B):
     """BASELINE config 3 at its real size.  The oracle cannot hold the whole
