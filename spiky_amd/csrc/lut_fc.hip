@@ -8,7 +8,8 @@
 //   out      fp32 [B][O];  x_grad fp32 [B][I];  w_grad like W
 //
 // Kernels and their schedules:
-//   k_check_detectors   one thread per (b, t).
+//   k_check_detectors   one thread per table over the x rows of a few samples
+//                       staged in LDS (one thread per (b, t) for very wide x).
 //   k_fill_fc           one wavefront per (sample, column slice of 64*VEC);
 //                       slices are mapped to XCDs (workgroup id mod 8) so each
 //                       XCD's L2 serves one column slice of every table to all
@@ -99,6 +100,73 @@ __global__ __launch_bounds__(kBlock) void k_check_detectors(
     if (TRAIN) {
         md[o] = mind;
         mi[o] = mink;
+    }
+}
+
+// The same logic with the x rows of `spb` consecutive samples staged in LDS.
+// A thread owns one table: it loads the table's anchor pairs once and
+// evaluates them for every staged sample, so the anchor reads are shared by
+// spb samples and the 2 * n_anchors input reads per (sample, table) are LDS
+// reads instead of dependent global loads.
+constexpr int kCheckMaxAnchors = 16;
+constexpr uint32_t kCheckLdsBytes = 64 * 1024;
+
+template <bool TRAIN, int NA>
+__global__ __launch_bounds__(1024) void k_check_detectors_lds(
+    const float *__restrict__ x, const int2 *__restrict__ anchors, uint32_t batch,
+    uint32_t n_inputs, uint32_t n_detectors, uint32_t n_anchors, uint32_t spb, float cmp_eps,
+    int32_t *__restrict__ idx, float *__restrict__ md, int32_t *__restrict__ mi) {
+    extern __shared__ float xs[];
+    const uint32_t b0 = blockIdx.y * spb;
+    const uint32_t nb = min(spb, batch - b0);
+    const uint32_t n_el = nb * n_inputs;
+    const float *src = x + (size_t)b0 * n_inputs;
+    if ((n_el & 3u) == 0 && (reinterpret_cast<uintptr_t>(src) & 15u) == 0) {
+        const float4 *s4 = reinterpret_cast<const float4 *>(src);
+        float4 *d4 = reinterpret_cast<float4 *>(xs);
+        for (uint32_t i = threadIdx.x; i < n_el / 4; i += blockDim.x) d4[i] = s4[i];
+    } else {
+        for (uint32_t i = threadIdx.x; i < n_el; i += blockDim.x) xs[i] = src[i];
+    }
+    __syncthreads();
+    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n_detectors) return;
+    // the table's pairs in registers (fully unrolled, compile-time indices);
+    // pairs past n_anchors or with an input id outside [0, n_inputs) are
+    // skipped, marked by x = -1
+    int2 a[NA];
+    const int2 *ap = anchors + (size_t)t * n_anchors;
+#pragma unroll
+    for (int k = 0; k < NA; k++) {
+        int2 v = make_int2(-1, -1);
+        if ((uint32_t)k < n_anchors) v = ap[k];
+        if ((uint32_t)v.x >= n_inputs || (uint32_t)v.y >= n_inputs) v = make_int2(-1, -1);
+        a[k] = v;
+    }
+    for (uint32_t sl = 0; sl < nb; sl++) {
+        const float *xr = xs + sl * n_inputs;
+        int32_t li = 0;
+        float mind = 0.0f;
+        int32_t mink = -1;
+#pragma unroll
+        for (int k = 0; k < NA; k++) {
+            if (a[k].x >= 0) {
+                const float d = xr[a[k].x] - xr[a[k].y];
+                if (rounded_greater0(d, cmp_eps)) li |= (1 << k);
+                if (TRAIN) {
+                    if (mink == -1 || fabsf(d) < fabsf(mind)) {
+                        mind = d;
+                        mink = (int32_t)k;
+                    }
+                }
+            }
+        }
+        const size_t o = (size_t)(b0 + sl) * n_detectors + t;
+        idx[o] = li;
+        if (TRAIN) {
+            md[o] = mind;
+            mi[o] = mink;
+        }
     }
 }
 
@@ -489,18 +557,27 @@ __global__ __launch_bounds__(kBlock) void k_wgrad_fc_atomic(
 // offsets[t][e] .. offsets[t][e+1] delimit bucket e in samples[t][*], and the
 // samples of a bucket are in ascending order.
 // ---------------------------------------------------------------------------
+// The lookup indices come from idx [B][T] (a strided column per table) or, when
+// key_t is given, from the low byte of the transposed keys [T][key_pitch] that the
+// table-major propagate writes (main index | alternative << 8): one contiguous
+// row per table.
 __global__ __launch_bounds__(kWave) void k_bucket_samples(
-    const int32_t *__restrict__ idx, uint32_t batch, uint32_t n_detectors, uint32_t n_entries,
-    uint32_t n_bits, int32_t *__restrict__ offsets, int32_t *__restrict__ samples) {
+    const int32_t *__restrict__ idx, const uint16_t *__restrict__ key_t, uint32_t key_pitch,
+    uint32_t batch, uint32_t n_detectors, uint32_t n_entries, uint32_t n_bits,
+    int32_t *__restrict__ offsets, int32_t *__restrict__ samples) {
     extern __shared__ int32_t cnt[];
     const uint32_t t = blockIdx.x;
     const uint32_t lane = threadIdx.x;
     const uint32_t emask = n_entries - 1;
+    const uint16_t *kt = key_t ? key_t + (size_t)t * key_pitch : nullptr;
+    auto key_of = [&](uint32_t b) -> uint32_t {
+        return kt ? ((uint32_t)kt[b] & 0xFFu & emask) : ((uint32_t)idx[(size_t)b * n_detectors + t] & emask);
+    };
     for (uint32_t e = lane; e < n_entries; e += kWave) cnt[e] = 0;
     __syncthreads();
     for (uint32_t base = 0; base < batch; base += kWave) {
         const uint32_t b = base + lane;
-        if (b < batch) atomicAdd(&cnt[(uint32_t)idx[(size_t)b * n_detectors + t] & emask], 1);
+        if (b < batch) atomicAdd(&cnt[key_of(b)], 1);
     }
     __syncthreads();
     // exclusive scan of cnt[0..E) by one wavefront: each lane sums a contiguous run
@@ -530,7 +607,7 @@ __global__ __launch_bounds__(kWave) void k_bucket_samples(
     for (uint32_t base = 0; base < batch; base += kWave) {
         const uint32_t b = base + lane;
         const bool valid = b < batch;
-        const uint32_t key = valid ? ((uint32_t)idx[(size_t)b * n_detectors + t] & emask) : 0u;
+        const uint32_t key = valid ? key_of(b) : 0u;
         uint64_t peers = __ballot(valid);
         for (uint32_t bit = 0; bit < n_bits; bit++) {
             const bool kb = (key >> bit) & 1u;
@@ -776,10 +853,34 @@ bool rowsum_applies(const FcShape &s) {
 hipError_t launch_check_detectors(const FcShape &s, const float *x, const int32_t *anchors,
                                   float cmp_eps, int32_t *idx, float *min_deltas,
                                   int32_t *min_idx, hipStream_t st) {
+    if ((uint64_t)s.batch * s.n_detectors == 0) return hipSuccess;
+    const int2 *ap = reinterpret_cast<const int2 *>(anchors);
+    const uint32_t spb_lds = kCheckLdsBytes / 4 / std::max<uint32_t>(s.n_inputs, 1);
+    if (s.n_anchors <= (uint32_t)kCheckMaxAnchors && spb_lds >= 1 &&
+        (s.batch + std::min<uint32_t>(spb_lds, 16) - 1) / std::min<uint32_t>(spb_lds, 16) <= 65535u) {
+        // one thread per table, x rows of spb samples in LDS; spb is lowered so
+        // that the grid still holds ~512 workgroups where the batch allows it
+        const uint32_t threads = std::min<uint32_t>(1024, (s.n_detectors + 63) / 64 * 64);
+        const uint32_t gx = (s.n_detectors + threads - 1) / threads;
+        const uint64_t want = std::max<uint64_t>(1, (uint64_t)s.batch * gx / 512);
+        uint32_t spb = (uint32_t)std::min<uint64_t>({(uint64_t)spb_lds, want, 16});
+        while ((s.batch + spb - 1) / spb > 65535u) spb++;
+        const uint32_t gy = (s.batch + spb - 1) / spb;
+        const size_t lds = (size_t)spb * s.n_inputs * sizeof(float);
+#define SPIKY_CHK(TR, NA)                                                                       \
+    hipLaunchKernelGGL((k_check_detectors_lds<TR, NA>), dim3(gx, gy), dim3(threads), lds, st, x, ap, \
+                       s.batch, s.n_inputs, s.n_detectors, s.n_anchors, spb, cmp_eps, idx,       \
+                       min_deltas, min_idx)
+        if (min_deltas) {
+            if (s.n_anchors <= 8) SPIKY_CHK(true, 8); else SPIKY_CHK(true, 16);
+        } else {
+            if (s.n_anchors <= 8) SPIKY_CHK(false, 8); else SPIKY_CHK(false, 16);
+        }
+#undef SPIKY_CHK
+        return hipGetLastError();
+    }
     const uint32_t bpr = (s.n_detectors + kBlock - 1) / kBlock;
     const uint64_t grid = (uint64_t)bpr * s.batch;
-    if (grid == 0) return hipSuccess;
-    const int2 *ap = reinterpret_cast<const int2 *>(anchors);
     if (min_deltas)
         hipLaunchKernelGGL(k_check_detectors<true>, dim3((uint32_t)grid), dim3(kBlock), 0, st, x,
                            ap, s.n_inputs, s.n_detectors, s.n_anchors, bpr, cmp_eps, idx,
@@ -880,11 +981,13 @@ size_t wgrad_fc_scratch_bytes(const FcShape &s) {
 
 hipError_t launch_wgrad_fc(const FcShape &s, const float *g, const int32_t *idx, float *target,
                            double lr, bool int_mode, double int_rescaler, bool overwrite,
-                           void *scratch, hipStream_t st) {
+                           void *scratch, hipStream_t st, const uint16_t *key_t,
+                           uint32_t key_pitch) {
     if (rowsum_applies(s) && scratch != nullptr) {
         int32_t *offsets = reinterpret_cast<int32_t *>(scratch);
         int32_t *samples = offsets + (size_t)s.n_detectors * (s.n_entries + 1);
-        hipError_t e = launch_bucket_samples(s, idx, offsets, samples, st);
+        hipError_t e = launch_bucket_samples(s, idx, offsets, samples, st,
+                                             s.n_entries <= 256 ? key_t : nullptr, key_pitch);
         if (e != hipSuccess) return e;
         // 4 columns per lane once that still leaves 4 slices (two XCDs per slice)
         const uint32_t vec = (s.n_outputs % 4 == 0 && s.n_outputs >= 1024) ? 4 : pick_vec(s.n_outputs);
@@ -956,13 +1059,14 @@ hipError_t launch_wgrad_commit_values(const float *g, uint32_t *cv, uint64_t n, 
 }
 
 hipError_t launch_bucket_samples(const FcShape &s, const int32_t *idx, int32_t *offsets,
-                                 int32_t *samples, hipStream_t st) {
+                                 int32_t *samples, hipStream_t st, const uint16_t *key_t,
+                                 uint32_t key_pitch) {
     if (s.n_detectors == 0) return hipSuccess;
     uint32_t n_bits = 0;
     while ((1u << n_bits) < s.n_entries) n_bits++;
     hipLaunchKernelGGL(k_bucket_samples, dim3(s.n_detectors), dim3(kWave),
-                       s.n_entries * sizeof(int32_t), st, idx, s.batch, s.n_detectors,
-                       s.n_entries, n_bits, offsets, samples);
+                       s.n_entries * sizeof(int32_t), st, idx, key_t, key_pitch, s.batch,
+                       s.n_detectors, s.n_entries, n_bits, offsets, samples);
     return hipGetLastError();
 }
 

@@ -513,8 +513,8 @@ __global__ __launch_bounds__(256) void k_fill_commit(const uint32_t *__restrict_
 template <int SPT>
 __global__ __launch_bounds__(kTmThreads) void k_propagate_tm(
     const float *__restrict__ w, const float *__restrict__ g, const uint16_t *__restrict__ key_t,
-    float *__restrict__ dpart, uint32_t batch, uint32_t n_outputs, uint32_t n_detectors,
-    uint32_t n_entries, uint32_t tpu, uint32_t n_slices, uint32_t n_chunks) {
+    float *__restrict__ dpart, uint32_t batch, uint32_t pitch, uint32_t n_outputs,
+    uint32_t n_detectors, uint32_t n_entries, uint32_t tpu, uint32_t n_slices, uint32_t n_chunks) {
     using L = StageLayout<uint16_t, SPT>;
     __shared__ __attribute__((aligned(16))) uint8_t smem[2 * L::kStageBytes];
     const uint32_t tid = threadIdx.x;
@@ -546,8 +546,9 @@ __global__ __launch_bounds__(kTmThreads) void k_propagate_tm(
     const uint32_t n_stages = (nt_all + kTmPF - 1) / kTmPF;
     f32x4 rows[kTmPF][2];
     u32x4 keys4[kTmPF];
+    // keys rows have `pitch` (a whole number of chunks, zero past the batch)
     stage_load<uint16_t, SPT>(rows, keys4, w, key_t, tid, t0, min((uint32_t)kTmPF, nt_all), n_entries,
-                              n_outputs, col0, batch, b_base);
+                              n_outputs, col0, pitch, b_base);
     for (uint32_t st = 0; st < n_stages; st++) {
         uint8_t *stage = smem + (st & 1) * L::kStageBytes;
         stage_store<uint16_t, SPT>(rows, keys4, stage, tid);
@@ -556,7 +557,7 @@ __global__ __launch_bounds__(kTmThreads) void k_propagate_tm(
         if (st + 1 < n_stages) {
             const uint32_t tn = ts + kTmPF;
             stage_load<uint16_t, SPT>(rows, keys4, w, key_t, tid, tn, min((uint32_t)kTmPF, t1 - tn),
-                                      n_entries, n_outputs, col0, batch, b_base);
+                                      n_entries, n_outputs, col0, pitch, b_base);
         }
         __syncthreads();
         for (uint32_t p = 0; p < nt; p++) {
@@ -590,6 +591,100 @@ __global__ __launch_bounds__(kTmThreads) void k_propagate_tm(
                 // merges them into full lines before they reach HBM
                 dpart[((size_t)slice * n_detectors + t) * batch + b] = (float)dv[0];
         }
+    }
+}
+
+// Propagate partials, LDS-DMA form (fp32 tables with 256 entries): the ring of
+// k_fill_tm_dma, with the stage's u16 keys (main | alt << 8) loaded by the
+// first kKeyWaves waves from keys transposed to a row pitch that is a whole
+// number of sample chunks.  Arithmetic and partials are those of
+// k_propagate_tm.
+template <int SPT>
+__global__ __launch_bounds__(kTmThreads) void k_propagate_tm_dma(
+    const float *__restrict__ w, const float *__restrict__ g, const uint16_t *__restrict__ key_t,
+    float *__restrict__ dpart, uint32_t batch, uint32_t pitch, uint32_t n_outputs,
+    uint32_t n_detectors, uint32_t tpu, uint32_t n_slices, uint32_t n_chunks) {
+    constexpr int kKeyBytes = kTmPass * SPT * 2;
+    constexpr int kStage = kDmaRows + kKeyBytes;
+    constexpr uint32_t kKeyWaves = (kKeyBytes + kWave * 16 - 1) / (kWave * 16);
+    __shared__ __attribute__((aligned(16))) uint8_t smem[kDmaRing * kStage];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & (kWave - 1);
+    const uint32_t wave = tid / kWave;
+    const uint32_t slice = blockIdx.x % n_slices;
+    const uint32_t rest = blockIdx.x / n_slices;
+    const uint32_t chunk = rest % n_chunks;
+    const uint32_t k = rest / n_chunks;
+    const uint32_t t0 = k * tpu;
+    const uint32_t t1 = min(t0 + tpu, n_detectors);
+    const uint32_t b_base = chunk * (kTmPass * SPT);
+    const uint32_t col0 = slice * kTmCols;
+    const uint32_t q = lane & 7;
+    const uint32_t col = col0 + q * 4;
+    const bool active = col < n_outputs;
+    const uint32_t s_loc0 = wave * 8 + (lane >> 3);
+
+    f32x4 gv[SPT];
+#pragma unroll
+    for (int i = 0; i < SPT; i++) {
+        const uint32_t b = min(b_base + s_loc0 + kTmPass * i, batch - 1);
+        gv[i] = active ? *reinterpret_cast<const f32x4 *>(g + (size_t)b * n_outputs + col)
+                       : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    uint32_t goff[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const uint32_t c = tid + (uint32_t)h * kTmThreads;
+        uint32_t cc = col0 + (c & 7) * 4;
+        if (cc >= n_outputs) cc = 0;
+        goff[h] = (c >> 3) * n_outputs + cc;
+    }
+    const uint32_t n_loads = wave < kKeyWaves ? 3u : 2u;  // per stage, this wave
+    auto issue = [&](uint32_t si) {
+        const uint32_t t = t0 + si;
+        uint8_t *stage = smem + (si % kDmaRing) * kStage;
+        const float *wt = w + (size_t)t * kTmMaxEntries * n_outputs;
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+            dma16(wt + goff[h], stage + ((uint32_t)h * kTmThreads + wave * kWave) * 16);
+        if (wave < kKeyWaves) {
+            const uint32_t byte = wave * kWave * 16 + lane * 16;
+            if (byte < (uint32_t)kKeyBytes)
+                dma16(reinterpret_cast<const uint8_t *>(key_t + (size_t)t * pitch + b_base) + byte,
+                      stage + kDmaRows + wave * kWave * 16);
+        }
+    };
+
+    const uint32_t nt = t1 - t0;
+    for (uint32_t si = 0; si < min((uint32_t)(kDmaRing - 1), nt); si++) issue(si);
+    for (uint32_t st = 0; st < nt; st++) {
+        wait_vm(min((uint32_t)(kDmaRing - 2), nt - 1 - st) * n_loads);
+        __asm__ volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        __asm__ volatile("" ::: "memory");
+        if (st + kDmaRing - 1 < nt) issue(st + kDmaRing - 1);
+        const uint8_t *tb = smem + (st % kDmaRing) * kStage;
+        const uint16_t *keys = reinterpret_cast<const uint16_t *>(tb + kDmaRows);
+        const uint32_t t = t0 + st;
+        double dv[8];
+#pragma unroll
+        for (int i = 0; i < SPT; i++) {
+            if (i == 4) __builtin_amdgcn_sched_barrier(0);
+            const uint32_t key = keys[s_loc0 + kTmPass * i];
+            const uint32_t rm = key & 0xFFu;
+            const uint32_t ra = key >> 8;
+            const f32x4 a = *reinterpret_cast<const f32x4 *>(tb + rm * 128 + q * 16);
+            const f32x4 e = *reinterpret_cast<const f32x4 *>(tb + ra * 128 + q * 16);
+            float d = (a.x - e.x) * gv[i].x;
+            d = __builtin_fmaf(a.y - e.y, gv[i].y, d);
+            d = __builtin_fmaf(a.z - e.z, gv[i].z, d);
+            d = __builtin_fmaf(a.w - e.w, gv[i].w, d);
+            dv[i] = (double)d;
+        }
+        reduce_scatter8<SPT>(dv, q);
+        const uint32_t b = b_base + s_loc0 + kTmPass * rs_item<SPT>(q);
+        if (rs_writer<SPT>(q) && b < batch)
+            dpart[((size_t)slice * n_detectors + t) * batch + b] = (float)dv[0];
     }
 }
 
@@ -720,12 +815,14 @@ __global__ __launch_bounds__(256) void k_transpose_idx(const int32_t *__restrict
 }
 
 // keys_t[t][b] = main | alt << 8 with alt = main ^ (1 << min_idx) (main when
-// the min-margin index is unused), through a 64x64 LDS tile.
+// the min-margin index is unused), through a 64x64 LDS tile; row pitch `pitch`
+// >= batch, samples past the batch get 0.
 __global__ __launch_bounds__(256) void k_transpose_keys(const int32_t *__restrict__ idx,
                                                         const int32_t *__restrict__ mi,
                                                         uint16_t *__restrict__ key_t,
-                                                        uint32_t batch, uint32_t n_detectors,
-                                                        uint32_t n_anchors, uint32_t n_entries) {
+                                                        uint32_t batch, uint32_t pitch,
+                                                        uint32_t n_detectors, uint32_t n_anchors,
+                                                        uint32_t n_entries) {
     __shared__ uint16_t tile[64][65];
     const uint32_t tb = blockIdx.x * 64;
     const uint32_t bb = blockIdx.y * 64;
@@ -739,12 +836,14 @@ __global__ __launch_bounds__(256) void k_transpose_keys(const int32_t *__restric
             const int32_t m = mi[bt];
             const uint32_t ra = (m >= 0 && (uint32_t)m < n_anchors) ? (rm ^ (1u << m)) : rm;
             tile[r][tx] = (uint16_t)(rm | (ra << 8));
+        } else {
+            tile[r][tx] = 0;
         }
     }
     __syncthreads();
     for (uint32_t r = ty; r < 64; r += 4) {
         const uint32_t t = tb + r, b = bb + tx;
-        if (b < batch && t < n_detectors) key_t[(size_t)t * batch + b] = tile[tx][r];
+        if (b < pitch && t < n_detectors) key_t[(size_t)t * pitch + b] = tile[tx][r];
     }
 }
 
@@ -889,10 +988,15 @@ bool tm_propagate_applies(const FcShape &s) {
            n_slices * s.batch * s.n_detectors * 4 <= (4ull << 30);
 }
 
-// scratch: keys [T][B] u16 | partial dots [slices][T][B] f32 | du [B][T] f32
+uint32_t tm_key_pitch(uint32_t batch) {
+    const uint32_t chunk = kTmPass * tm_spt(batch);
+    return (batch + chunk - 1) / chunk * chunk;
+}
+
+// scratch: keys [T][pitch] u16 | partial dots [slices][T][B] f32 | du [B][T] f32
 size_t tm_propagate_scratch_bytes(const FcShape &s) {
     const uint64_t n_slices = (s.n_outputs + kTmCols - 1) / kTmCols;
-    const size_t keys = ((size_t)s.n_detectors * s.batch * 2 + 255) & ~(size_t)255;
+    const size_t keys = ((size_t)s.n_detectors * tm_key_pitch(s.batch) * 2 + 255) & ~(size_t)255;
     return keys + (size_t)(n_slices + 1) * s.batch * s.n_detectors * 4;
 }
 
@@ -901,10 +1005,11 @@ hipError_t launch_propagate_tm(const FcShape &s, const float *w, const float *g,
                                const int32_t *min_idx, const int32_t *anchors, float *x_grad,
                                void *scratch, hipStream_t st) {
     uint16_t *key_t = reinterpret_cast<uint16_t *>(scratch);
-    const size_t keys = ((size_t)s.n_detectors * s.batch * 2 + 255) & ~(size_t)255;
+    const uint32_t pitch = tm_key_pitch(s.batch);
+    const size_t keys = ((size_t)s.n_detectors * pitch * 2 + 255) & ~(size_t)255;
     float *dpart = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(scratch) + keys);
-    hipLaunchKernelGGL(k_transpose_keys, dim3((s.n_detectors + 63) / 64, (s.batch + 63) / 64),
-                       dim3(256), 0, st, idx, min_idx, key_t, s.batch, s.n_detectors,
+    hipLaunchKernelGGL(k_transpose_keys, dim3((s.n_detectors + 63) / 64, (pitch + 63) / 64),
+                       dim3(256), 0, st, idx, min_idx, key_t, s.batch, pitch, s.n_detectors,
                        s.n_anchors, s.n_entries);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -915,10 +1020,17 @@ hipError_t launch_propagate_tm(const FcShape &s, const float *w, const float *g,
     const uint32_t n_units = (s.n_detectors + tpu - 1) / tpu;
     const uint64_t grid = (uint64_t)n_units * n_chunks * n_slices;
     if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
-#define SPIKY_PTM(SPT)                                                                            \
-    hipLaunchKernelGGL((k_propagate_tm<SPT>), dim3((uint32_t)grid), dim3(kTmThreads), 0, st, w, g, \
-                       key_t, dpart, s.batch, s.n_outputs, s.n_detectors, s.n_entries, tpu,       \
-                       n_slices, n_chunks)
+    // the LDS-DMA ring needs whole 256-row tables
+    const bool dma = s.n_entries == (uint32_t)kTmMaxEntries;
+#define SPIKY_PTM(SPT)                                                                              \
+    if (dma)                                                                                        \
+        hipLaunchKernelGGL((k_propagate_tm_dma<SPT>), dim3((uint32_t)grid), dim3(kTmThreads), 0, st, \
+                           w, g, key_t, dpart, s.batch, pitch, s.n_outputs, s.n_detectors, tpu,   \
+                           n_slices, n_chunks);                                                    \
+    else                                                                                            \
+        hipLaunchKernelGGL((k_propagate_tm<SPT>), dim3((uint32_t)grid), dim3(kTmThreads), 0, st, w, \
+                           g, key_t, dpart, s.batch, pitch, s.n_outputs, s.n_detectors,            \
+                           s.n_entries, tpu, n_slices, n_chunks)
     switch (spt) {
         case 1: SPIKY_PTM(1); break;
         case 2: SPIKY_PTM(2); break;
