@@ -587,7 +587,7 @@ int spiky_lut_backward_backprop(spiky_lut_manager *m, float *weights, uint32_t b
                 void *scr = wg_bytes ? scr_all + prop_bytes : nullptr;
                 m->timed("gather_w_gradients_fc", st, [&] {
                     // the table-major propagate left the transposed keys at its scratch start
-                    const uint16_t *key_t = tm ? reinterpret_cast<const uint16_t *>(scr_all) : nullptr;
+                    const uint32_t *key_t = tm ? reinterpret_cast<const uint32_t *>(scr_all) : nullptr;
                     check_hip(spiky::launch_wgrad_fc(s, output_grad, lookup_indices, target, lr,
                                                      m->int_mode, m->int_rescaler, overwrite, scr, st,
                                                      key_t, spiky::tm_key_pitch(s.batch)),

@@ -558,20 +558,20 @@ __global__ __launch_bounds__(kBlock) void k_wgrad_fc_atomic(
 // samples of a bucket are in ascending order.
 // ---------------------------------------------------------------------------
 // The lookup indices come from idx [B][T] (a strided column per table) or, when
-// key_t is given, from the low byte of the transposed keys [T][key_pitch] that the
-// table-major propagate writes (main index | alternative << 8): one contiguous
-// row per table.
+// key_t is given, from the transposed keys [T][key_pitch] that the table-major
+// propagate writes (main * 128 | (alternative * 128) << 16): one contiguous row
+// per table.
 __global__ __launch_bounds__(kWave) void k_bucket_samples(
-    const int32_t *__restrict__ idx, const uint16_t *__restrict__ key_t, uint32_t key_pitch,
+    const int32_t *__restrict__ idx, const uint32_t *__restrict__ key_t, uint32_t key_pitch,
     uint32_t batch, uint32_t n_detectors, uint32_t n_entries, uint32_t n_bits,
     int32_t *__restrict__ offsets, int32_t *__restrict__ samples) {
     extern __shared__ int32_t cnt[];
     const uint32_t t = blockIdx.x;
     const uint32_t lane = threadIdx.x;
     const uint32_t emask = n_entries - 1;
-    const uint16_t *kt = key_t ? key_t + (size_t)t * key_pitch : nullptr;
+    const uint32_t *kt = key_t ? key_t + (size_t)t * key_pitch : nullptr;
     auto key_of = [&](uint32_t b) -> uint32_t {
-        return kt ? ((uint32_t)kt[b] & 0xFFu & emask) : ((uint32_t)idx[(size_t)b * n_detectors + t] & emask);
+        return kt ? ((kt[b] >> 7) & 0xFFu & emask) : ((uint32_t)idx[(size_t)b * n_detectors + t] & emask);
     };
     for (uint32_t e = lane; e < n_entries; e += kWave) cnt[e] = 0;
     __syncthreads();
@@ -981,7 +981,7 @@ size_t wgrad_fc_scratch_bytes(const FcShape &s) {
 
 hipError_t launch_wgrad_fc(const FcShape &s, const float *g, const int32_t *idx, float *target,
                            double lr, bool int_mode, double int_rescaler, bool overwrite,
-                           void *scratch, hipStream_t st, const uint16_t *key_t,
+                           void *scratch, hipStream_t st, const uint32_t *key_t,
                            uint32_t key_pitch) {
     if (rowsum_applies(s) && scratch != nullptr) {
         int32_t *offsets = reinterpret_cast<int32_t *>(scratch);
@@ -1059,7 +1059,7 @@ hipError_t launch_wgrad_commit_values(const float *g, uint32_t *cv, uint64_t n, 
 }
 
 hipError_t launch_bucket_samples(const FcShape &s, const int32_t *idx, int32_t *offsets,
-                                 int32_t *samples, hipStream_t st, const uint16_t *key_t,
+                                 int32_t *samples, hipStream_t st, const uint32_t *key_t,
                                  uint32_t key_pitch) {
     if (s.n_detectors == 0) return hipSuccess;
     uint32_t n_bits = 0;

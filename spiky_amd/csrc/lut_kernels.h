@@ -50,11 +50,11 @@ size_t wgrad_fc_scratch_bytes(const FcShape &s);
 
 // Table-row gradient: target[row, o] += lr * g[b, o] for every sample b hitting row.
 // scratch may be null when wgrad_fc_scratch_bytes() is 0.  key_t, when given,
-// holds the transposed keys [T][key_pitch] (lookup index in the low byte) that
+// holds the transposed keys [T][key_pitch] (lookup index * 128 in bits 0..14) that
 // launch_propagate_tm leaves at the start of its scratch.
 hipError_t launch_wgrad_fc(const FcShape &s, const float *g, const int32_t *idx, float *target,
                            double lr, bool int_mode, double int_rescaler, bool overwrite,
-                           void *scratch, hipStream_t st, const uint16_t *key_t = nullptr,
+                           void *scratch, hipStream_t st, const uint32_t *key_t = nullptr,
                            uint32_t key_pitch = 0);
 
 // int32 fixed point -> fp32, in place.
@@ -64,7 +64,7 @@ hipError_t launch_convert_i2f(float *buf, uint64_t n, double int_rescaler, hipSt
 // offsets [n_detectors][E+1], samples [n_detectors][batch].
 hipError_t launch_bucket_samples(const FcShape &s, const int32_t *idx, int32_t *offsets,
                                  int32_t *samples, hipStream_t st,
-                                 const uint16_t *key_t = nullptr, uint32_t key_pitch = 0);
+                                 const uint32_t *key_t = nullptr, uint32_t key_pitch = 0);
 
 // ---- table-major fully connected path (lut_tm.hip) ------------------------
 // Forward gather-sum through per-block partials in scratch; bit-identical to

@@ -109,6 +109,71 @@ __device__ __forceinline__ bool rs_writer(uint32_t l) {
     return (N >= 2 || !h) && (N >= 4 || !b0) && (N >= 8 || !b1);
 }
 
+// fp32 form of reduce_scatter8 for the propagate's 32-column dots: both
+// halves are summed with DPP-sourced adds (no separate lane moves) and each
+// lane keeps its half, so a step costs 3 VALU per kept item.  The 4-column
+// lane pieces are fp32 already; summing the 8 pieces in fp32 adds three
+// roundings (relative ~2e-7 of the sum of |pieces|).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+template <int CTRL, int N>
+__device__ __forceinline__ void rs_step_f32(float (&v)[8], bool upper) {
+    if (N == 1) {
+        v[0] += dpp_f32<CTRL>(v[0]);
+        return;
+    }
+    constexpr int M = N / 2;
+#pragma unroll
+    for (int j = 0; j < M; j++) {
+        const float lo = v[j] + dpp_f32<CTRL>(v[j]);
+        const float hi = v[M + j] + dpp_f32<CTRL>(v[M + j]);
+        v[j] = upper ? hi : lo;
+    }
+}
+template <int N>
+__device__ __forceinline__ void reduce_scatter8_f32(float (&v)[8], uint32_t l) {
+    const bool h = l >= 4, b0 = l & 1, b1 = (l >> 1) & 1;
+    rs_step_f32<kDppHalfMirror, N>(v, h);
+    rs_step_f32<kDppXor1, (N >= 2 ? N / 2 : 1)>(v, b0);
+    rs_step_f32<kDppXor2, (N >= 4 ? N / 4 : 1)>(v, b1);
+}
+
+// The lane's 4-column pieces of (W[main] - W[alt]) . g for its SPT samples of
+// one staged table.  keys[] hold the two rows' byte offsets; all keys are read
+// first, then the rows of 4 samples at a time, so that 8 row reads are in
+// flight per wave (32 VGPRs of rows).
+template <int SPT>
+__device__ __forceinline__ void propagate_pieces(const uint8_t *tq, const uint32_t *keys,
+                                                 uint32_t s_loc0, const f32x4 (&gv)[SPT],
+                                                 float (&dv)[8]) {
+    uint32_t kk[SPT];
+#pragma unroll
+    for (int i = 0; i < SPT; i++) kk[i] = keys[s_loc0 + kTmPass * i];
+    constexpr int G = SPT < 4 ? SPT : 4;
+#pragma unroll
+    for (int h = 0; h < SPT; h += G) {
+        f32x4 a[G], e[G];
+#pragma unroll
+        for (int j = 0; j < G; j++) {
+            a[j] = *reinterpret_cast<const f32x4 *>(tq + (kk[h + j] & 0xFFFFu));
+            e[j] = *reinterpret_cast<const f32x4 *>(tq + (kk[h + j] >> 16));
+        }
+#pragma unroll
+        for (int j = 0; j < G; j++) {
+            const f32x4 &g = gv[h + j];
+            // the lane's 4-column piece in fp32 (error ~1e-7 of its terms)
+            float d = (a[j].x - e[j].x) * g.x;
+            d = __builtin_fmaf(a[j].y - e[j].y, g.y, d);
+            d = __builtin_fmaf(a[j].z - e[j].z, g.z, d);
+            d = __builtin_fmaf(a[j].w - e[j].w, g.w, d);
+            dv[h + j] = d;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
 // LDS image of one table in a stage: E rows x 128 bytes, then one key per
 // sample of the chunk (u8 row index for the forward, u16 main|alt<<8 for the
 // propagate).
@@ -339,17 +404,18 @@ __device__ __forceinline__ void wait_vm(uint32_t n) {
     }
 }
 
-template <int SPT, bool INT_MODE>
+// RING stages, RING - 1 tables ahead.
+template <int SPT, bool INT_MODE, int RING>
 __global__ __launch_bounds__(kTmThreads) void k_fill_tm_dma(
     const float *__restrict__ w, const uint8_t *__restrict__ idx_t, uint32_t *__restrict__ part,
     uint32_t batch, uint32_t pitch, uint32_t n_outputs, uint32_t n_detectors, uint32_t dgs,
     uint32_t bpu, uint32_t n_slices, uint32_t n_chunks, double int_rescaler) {
     constexpr int kKeyBytes = kTmPass * SPT;
     constexpr int kStage = kDmaRows + kKeyBytes;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[kDmaRing * kStage];
+    __shared__ __attribute__((aligned(16))) uint8_t smem[RING * kStage];
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & (kWave - 1);
-    const uint32_t wave = tid / kWave;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const uint32_t slice = blockIdx.x % n_slices;
     const uint32_t rest = blockIdx.x / n_slices;
     const uint32_t chunk = rest % n_chunks;
@@ -373,7 +439,7 @@ __global__ __launch_bounds__(kTmThreads) void k_fill_tm_dma(
     const uint32_t n_loads = wave == 0 ? 3u : 2u;  // per stage, this wave
     auto issue = [&](uint32_t si) {
         const uint32_t t = t0 + si;
-        uint8_t *stage = smem + (si % kDmaRing) * kStage;
+        uint8_t *stage = smem + (si % RING) * kStage;
         const float *wt = w + (size_t)t * kTmMaxEntries * n_outputs;
 #pragma unroll
         for (int h = 0; h < 2; h++)
@@ -395,18 +461,18 @@ __global__ __launch_bounds__(kTmThreads) void k_fill_tm_dma(
             ipay[i][c] = 0;
         }
     const uint32_t nt = t1 - t0;
-    for (uint32_t si = 0; si < min((uint32_t)(kDmaRing - 1), nt); si++) issue(si);
+    for (uint32_t si = 0; si < min((uint32_t)(RING - 1), nt); si++) issue(si);
     for (uint32_t st = 0; st < nt; st++) {
         // stages issued so far: 0 .. min(st + ring - 2, nt - 1); wait for st's
-        wait_vm(min((uint32_t)(kDmaRing - 2), nt - 1 - st) * n_loads);
+        wait_vm(min((uint32_t)(RING - 2), nt - 1 - st) * n_loads);
         // stage st visible to all waves; every wave is done with stage st - 1
         // (its reads of it were consumed).  A bare s_barrier: __syncthreads'
         // fence would also wait for the later stages' loads.
         __asm__ volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         __asm__ volatile("" ::: "memory");
-        if (st + kDmaRing - 1 < nt) issue(st + kDmaRing - 1);
-        const uint8_t *tb = smem + (st % kDmaRing) * kStage;
+        if (st + RING - 1 < nt) issue(st + RING - 1);
+        const uint8_t *tb = smem + (st % RING) * kStage;
         const uint8_t *keys = tb + kDmaRows;
 #pragma unroll
         for (int i = 0; i < SPT; i++) {
@@ -508,14 +574,15 @@ __global__ __launch_bounds__(256) void k_fill_commit(const uint32_t *__restrict_
 
 // ---------------------------------------------------------------------------
 // Propagate partials.  dpart[s][t][b] = fp32(sum over slice s's columns of
-// (W[t][main] - W[t][alt]) * g[b]) in fp64.  Key = main | alt << 8.
+// (W[t][main] - W[t][alt]) * g[b]).  Key = main * 128 | (alt * 128) << 16: the
+// two rows' byte offsets in the stage.
 // ---------------------------------------------------------------------------
 template <int SPT>
 __global__ __launch_bounds__(kTmThreads) void k_propagate_tm(
-    const float *__restrict__ w, const float *__restrict__ g, const uint16_t *__restrict__ key_t,
+    const float *__restrict__ w, const float *__restrict__ g, const uint32_t *__restrict__ key_t,
     float *__restrict__ dpart, uint32_t batch, uint32_t pitch, uint32_t n_outputs,
     uint32_t n_detectors, uint32_t n_entries, uint32_t tpu, uint32_t n_slices, uint32_t n_chunks) {
-    using L = StageLayout<uint16_t, SPT>;
+    using L = StageLayout<uint32_t, SPT>;
     __shared__ __attribute__((aligned(16))) uint8_t smem[2 * L::kStageBytes];
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & (kWave - 1);
@@ -531,7 +598,6 @@ __global__ __launch_bounds__(kTmThreads) void k_propagate_tm(
     const uint32_t q = lane & 7;
     const uint32_t col = col0 + q * 4;
     const bool active = col < n_outputs;
-    const uint32_t emask = n_entries - 1;
     const uint32_t s_loc0 = wave * 8 + (lane >> 3);
 
     f32x4 gv[SPT];
@@ -547,70 +613,56 @@ __global__ __launch_bounds__(kTmThreads) void k_propagate_tm(
     f32x4 rows[kTmPF][2];
     u32x4 keys4[kTmPF];
     // keys rows have `pitch` (a whole number of chunks, zero past the batch)
-    stage_load<uint16_t, SPT>(rows, keys4, w, key_t, tid, t0, min((uint32_t)kTmPF, nt_all), n_entries,
+    stage_load<uint32_t, SPT>(rows, keys4, w, key_t, tid, t0, min((uint32_t)kTmPF, nt_all), n_entries,
                               n_outputs, col0, pitch, b_base);
     for (uint32_t st = 0; st < n_stages; st++) {
         uint8_t *stage = smem + (st & 1) * L::kStageBytes;
-        stage_store<uint16_t, SPT>(rows, keys4, stage, tid);
+        stage_store<uint32_t, SPT>(rows, keys4, stage, tid);
         const uint32_t ts = t0 + st * kTmPF;
         const uint32_t nt = min((uint32_t)kTmPF, t1 - ts);
         if (st + 1 < n_stages) {
             const uint32_t tn = ts + kTmPF;
-            stage_load<uint16_t, SPT>(rows, keys4, w, key_t, tid, tn, min((uint32_t)kTmPF, t1 - tn),
+            stage_load<uint32_t, SPT>(rows, keys4, w, key_t, tid, tn, min((uint32_t)kTmPF, t1 - tn),
                                       n_entries, n_outputs, col0, pitch, b_base);
         }
         __syncthreads();
         for (uint32_t p = 0; p < nt; p++) {
             const uint8_t *tb = stage + p * L::kTableBytes;
-            const uint16_t *keys = reinterpret_cast<const uint16_t *>(tb + kTmMaxEntries * 128);
+            const uint32_t *keys = reinterpret_cast<const uint32_t *>(tb + kTmMaxEntries * 128);
+            const uint8_t *tq = tb + q * 16;
             const uint32_t t = ts + p;
-            double dv[8];
-#pragma unroll
-            for (int i = 0; i < SPT; i++) {
-                // keep at most 4 samples' row reads in flight (128-VGPR budget)
-                if (i == 4) __builtin_amdgcn_sched_barrier(0);
-                const uint32_t key = keys[s_loc0 + kTmPass * i];
-                const uint32_t rm = key & emask;
-                const uint32_t ra = (key >> 8) & emask;
-                const f32x4 a = *reinterpret_cast<const f32x4 *>(tb + rm * 128 + q * 16);
-                const f32x4 e = *reinterpret_cast<const f32x4 *>(tb + ra * 128 + q * 16);
-                // the lane's 4-column piece in fp32 (error ~1e-7 of its terms),
-                // the sums over lanes, slices and tables in fp64
-                float d = (a.x - e.x) * gv[i].x;
-                d = __builtin_fmaf(a.y - e.y, gv[i].y, d);
-                d = __builtin_fmaf(a.z - e.z, gv[i].z, d);
-                d = __builtin_fmaf(a.w - e.w, gv[i].w, d);
-                dv[i] = (double)d;
-            }
+            float dv[8];
+            propagate_pieces<SPT>(tq, keys, s_loc0, gv, dv);
             // the 8 lanes of a sample group each hold a 4-column piece of the
             // SPT dots; after the reduce-scatter lane q holds sample rs_item's sum
-            reduce_scatter8<SPT>(dv, q);
+            reduce_scatter8_f32<SPT>(dv, q);
             const uint32_t b = b_base + s_loc0 + kTmPass * rs_item<SPT>(q);
             if (rs_writer<SPT>(q) && b < batch)
                 // 4-byte pieces of 4 KiB table rows: plain stores, so that L2
                 // merges them into full lines before they reach HBM
-                dpart[((size_t)slice * n_detectors + t) * batch + b] = (float)dv[0];
+                dpart[((size_t)slice * n_detectors + t) * batch + b] = dv[0];
         }
     }
 }
 
 // Propagate partials, LDS-DMA form (fp32 tables with 256 entries): the ring of
-// k_fill_tm_dma, with the stage's u16 keys (main | alt << 8) loaded by the
+// k_fill_tm_dma, with the stage's u32 keys (the two rows' byte offsets) loaded by the
 // first kKeyWaves waves from keys transposed to a row pitch that is a whole
 // number of sample chunks.  Arithmetic and partials are those of
 // k_propagate_tm.
-template <int SPT>
+template <int SPT, int RING>
 __global__ __launch_bounds__(kTmThreads) void k_propagate_tm_dma(
-    const float *__restrict__ w, const float *__restrict__ g, const uint16_t *__restrict__ key_t,
+    const float *__restrict__ w, const float *__restrict__ g, const uint32_t *__restrict__ key_t,
     float *__restrict__ dpart, uint32_t batch, uint32_t pitch, uint32_t n_outputs,
     uint32_t n_detectors, uint32_t tpu, uint32_t n_slices, uint32_t n_chunks) {
-    constexpr int kKeyBytes = kTmPass * SPT * 2;
+    constexpr int kKeyBytes = kTmPass * SPT * 4;
     constexpr int kStage = kDmaRows + kKeyBytes;
     constexpr uint32_t kKeyWaves = (kKeyBytes + kWave * 16 - 1) / (kWave * 16);
-    __shared__ __attribute__((aligned(16))) uint8_t smem[kDmaRing * kStage];
+    __shared__ __attribute__((aligned(16))) uint8_t smem[RING * kStage];
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & (kWave - 1);
-    const uint32_t wave = tid / kWave;
+    // wave-uniform: the per-wave load count and vmcnt wait stay scalar
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const uint32_t slice = blockIdx.x % n_slices;
     const uint32_t rest = blockIdx.x / n_slices;
     const uint32_t chunk = rest % n_chunks;
@@ -642,7 +694,7 @@ __global__ __launch_bounds__(kTmThreads) void k_propagate_tm_dma(
     const uint32_t n_loads = wave < kKeyWaves ? 3u : 2u;  // per stage, this wave
     auto issue = [&](uint32_t si) {
         const uint32_t t = t0 + si;
-        uint8_t *stage = smem + (si % kDmaRing) * kStage;
+        uint8_t *stage = smem + (si % RING) * kStage;
         const float *wt = w + (size_t)t * kTmMaxEntries * n_outputs;
 #pragma unroll
         for (int h = 0; h < 2; h++)
@@ -656,35 +708,23 @@ __global__ __launch_bounds__(kTmThreads) void k_propagate_tm_dma(
     };
 
     const uint32_t nt = t1 - t0;
-    for (uint32_t si = 0; si < min((uint32_t)(kDmaRing - 1), nt); si++) issue(si);
+    for (uint32_t si = 0; si < min((uint32_t)(RING - 1), nt); si++) issue(si);
     for (uint32_t st = 0; st < nt; st++) {
-        wait_vm(min((uint32_t)(kDmaRing - 2), nt - 1 - st) * n_loads);
+        wait_vm(min((uint32_t)(RING - 2), nt - 1 - st) * n_loads);
         __asm__ volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         __asm__ volatile("" ::: "memory");
-        if (st + kDmaRing - 1 < nt) issue(st + kDmaRing - 1);
-        const uint8_t *tb = smem + (st % kDmaRing) * kStage;
-        const uint16_t *keys = reinterpret_cast<const uint16_t *>(tb + kDmaRows);
+        if (st + RING - 1 < nt) issue(st + RING - 1);
+        const uint8_t *tb = smem + (st % RING) * kStage;
+        const uint32_t *keys = reinterpret_cast<const uint32_t *>(tb + kDmaRows);
+        const uint8_t *tq = tb + q * 16;
         const uint32_t t = t0 + st;
-        double dv[8];
-#pragma unroll
-        for (int i = 0; i < SPT; i++) {
-            if (i == 4) __builtin_amdgcn_sched_barrier(0);
-            const uint32_t key = keys[s_loc0 + kTmPass * i];
-            const uint32_t rm = key & 0xFFu;
-            const uint32_t ra = key >> 8;
-            const f32x4 a = *reinterpret_cast<const f32x4 *>(tb + rm * 128 + q * 16);
-            const f32x4 e = *reinterpret_cast<const f32x4 *>(tb + ra * 128 + q * 16);
-            float d = (a.x - e.x) * gv[i].x;
-            d = __builtin_fmaf(a.y - e.y, gv[i].y, d);
-            d = __builtin_fmaf(a.z - e.z, gv[i].z, d);
-            d = __builtin_fmaf(a.w - e.w, gv[i].w, d);
-            dv[i] = (double)d;
-        }
-        reduce_scatter8<SPT>(dv, q);
+        float dv[8];
+        propagate_pieces<SPT>(tq, keys, s_loc0, gv, dv);
+        reduce_scatter8_f32<SPT>(dv, q);
         const uint32_t b = b_base + s_loc0 + kTmPass * rs_item<SPT>(q);
         if (rs_writer<SPT>(q) && b < batch)
-            dpart[((size_t)slice * n_detectors + t) * batch + b] = (float)dv[0];
+            dpart[((size_t)slice * n_detectors + t) * batch + b] = dv[0];
     }
 }
 
@@ -814,16 +854,17 @@ __global__ __launch_bounds__(256) void k_transpose_idx(const int32_t *__restrict
     }
 }
 
-// keys_t[t][b] = main | alt << 8 with alt = main ^ (1 << min_idx) (main when
-// the min-margin index is unused), through a 64x64 LDS tile; row pitch `pitch`
-// >= batch, samples past the batch get 0.
+// keys_t[t][b] = main * 128 | (alt * 128) << 16 (the rows' byte offsets in a
+// 128-byte-row stage) with alt = main ^ (1 << min_idx) (main when the
+// min-margin index is unused), through a 64x64 LDS tile; row pitch `pitch` >=
+// batch, samples past the batch get 0.
 __global__ __launch_bounds__(256) void k_transpose_keys(const int32_t *__restrict__ idx,
                                                         const int32_t *__restrict__ mi,
-                                                        uint16_t *__restrict__ key_t,
+                                                        uint32_t *__restrict__ key_t,
                                                         uint32_t batch, uint32_t pitch,
                                                         uint32_t n_detectors, uint32_t n_anchors,
                                                         uint32_t n_entries) {
-    __shared__ uint16_t tile[64][65];
+    __shared__ uint32_t tile[64][65];
     const uint32_t tb = blockIdx.x * 64;
     const uint32_t bb = blockIdx.y * 64;
     const uint32_t tx = threadIdx.x & 63;
@@ -835,7 +876,7 @@ __global__ __launch_bounds__(256) void k_transpose_keys(const int32_t *__restric
             const uint32_t rm = (uint32_t)idx[bt] & (n_entries - 1);
             const int32_t m = mi[bt];
             const uint32_t ra = (m >= 0 && (uint32_t)m < n_anchors) ? (rm ^ (1u << m)) : rm;
-            tile[r][tx] = (uint16_t)(rm | (ra << 8));
+            tile[r][tx] = (rm << 7) | (ra << 23);
         } else {
             tile[r][tx] = 0;
         }
@@ -917,10 +958,12 @@ static hipError_t launch_fill_tm_impl(const FcShape &s, const WT *w, const float
     if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
     if (dma) {
         const float *wf = reinterpret_cast<const float *>(w);
-#define SPIKY_TMD(SPT, IM)                                                                          \
-    hipLaunchKernelGGL((k_fill_tm_dma<SPT, IM>), dim3((uint32_t)grid), dim3(kTmThreads), 0, st, wf, \
-                       idx_t, part, s.batch, ipitch, s.n_outputs, s.n_detectors, s.dgs, bpu,       \
-                       n_slices, n_chunks, int_rescaler)
+        // a 4-stage ring, one workgroup per CU.  (A 2-stage ring with chunks of
+        // 512 samples and two workgroups per CU measured 15% slower at config 3.)
+#define SPIKY_TMD(SPT, IM)                                                                         \
+    hipLaunchKernelGGL((k_fill_tm_dma<SPT, IM, kDmaRing>), dim3((uint32_t)grid),                   \
+                       dim3(kTmThreads), 0, st, wf, idx_t, part, s.batch, ipitch, s.n_outputs,     \
+                       s.n_detectors, s.dgs, bpu, n_slices, n_chunks, int_rescaler)
         switch (spt) {
             case 1: if (int_mode) SPIKY_TMD(1, true); else SPIKY_TMD(1, false); break;
             case 2: if (int_mode) SPIKY_TMD(2, true); else SPIKY_TMD(2, false); break;
@@ -993,10 +1036,10 @@ uint32_t tm_key_pitch(uint32_t batch) {
     return (batch + chunk - 1) / chunk * chunk;
 }
 
-// scratch: keys [T][pitch] u16 | partial dots [slices][T][B] f32 | du [B][T] f32
+// scratch: keys [T][pitch] u32 | partial dots [slices][T][B] f32 | du [B][T] f32
 size_t tm_propagate_scratch_bytes(const FcShape &s) {
     const uint64_t n_slices = (s.n_outputs + kTmCols - 1) / kTmCols;
-    const size_t keys = ((size_t)s.n_detectors * tm_key_pitch(s.batch) * 2 + 255) & ~(size_t)255;
+    const size_t keys = ((size_t)s.n_detectors * tm_key_pitch(s.batch) * 4 + 255) & ~(size_t)255;
     return keys + (size_t)(n_slices + 1) * s.batch * s.n_detectors * 4;
 }
 
@@ -1004,15 +1047,17 @@ hipError_t launch_propagate_tm(const FcShape &s, const float *w, const float *g,
                                const int32_t *idx, const float *min_deltas,
                                const int32_t *min_idx, const int32_t *anchors, float *x_grad,
                                void *scratch, hipStream_t st) {
-    uint16_t *key_t = reinterpret_cast<uint16_t *>(scratch);
+    uint32_t *key_t = reinterpret_cast<uint32_t *>(scratch);
     const uint32_t pitch = tm_key_pitch(s.batch);
-    const size_t keys = ((size_t)s.n_detectors * pitch * 2 + 255) & ~(size_t)255;
+    const size_t keys = ((size_t)s.n_detectors * pitch * 4 + 255) & ~(size_t)255;
     float *dpart = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(scratch) + keys);
     hipLaunchKernelGGL(k_transpose_keys, dim3((s.n_detectors + 63) / 64, (pitch + 63) / 64),
                        dim3(256), 0, st, idx, min_idx, key_t, s.batch, pitch, s.n_detectors,
                        s.n_anchors, s.n_entries);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    // the LDS-DMA ring needs whole 256-row tables
+    const bool dma = s.n_entries == (uint32_t)kTmMaxEntries;
     const uint32_t spt = tm_spt(s.batch);
     const uint32_t n_chunks = (s.batch + kTmPass * spt - 1) / (kTmPass * spt);
     const uint32_t n_slices = (s.n_outputs + kTmCols - 1) / kTmCols;
@@ -1020,11 +1065,10 @@ hipError_t launch_propagate_tm(const FcShape &s, const float *w, const float *g,
     const uint32_t n_units = (s.n_detectors + tpu - 1) / tpu;
     const uint64_t grid = (uint64_t)n_units * n_chunks * n_slices;
     if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
-    // the LDS-DMA ring needs whole 256-row tables
-    const bool dma = s.n_entries == (uint32_t)kTmMaxEntries;
 #define SPIKY_PTM(SPT)                                                                              \
     if (dma)                                                                                        \
-        hipLaunchKernelGGL((k_propagate_tm_dma<SPT>), dim3((uint32_t)grid), dim3(kTmThreads), 0, st, \
+        hipLaunchKernelGGL((k_propagate_tm_dma<SPT, kDmaRing>), dim3((uint32_t)grid),              \
+                           dim3(kTmThreads), 0, st,                                                 \
                            w, g, key_t, dpart, s.batch, pitch, s.n_outputs, s.n_detectors, tpu,   \
                            n_slices, n_chunks);                                                    \
     else                                                                                            \
