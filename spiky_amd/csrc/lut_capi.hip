@@ -590,7 +590,8 @@ int spiky_lut_backward_backprop(spiky_lut_manager *m, float *weights, uint32_t b
                     const uint32_t *key_t = tm ? reinterpret_cast<const uint32_t *>(scr_all) : nullptr;
                     check_hip(spiky::launch_wgrad_fc(s, output_grad, lookup_indices, target, lr,
                                                      m->int_mode, m->int_rescaler, overwrite, scr, st,
-                                                     key_t, spiky::tm_key_pitch(s.batch)),
+                                                     key_t, spiky::tm_key_pitch(s.batch),
+                                                     spiky::tm_key_row_shift(s)),
                               "gather_w_gradients_fc");
                 });
             }

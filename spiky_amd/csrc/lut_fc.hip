@@ -559,11 +559,11 @@ __global__ __launch_bounds__(kBlock) void k_wgrad_fc_atomic(
 // ---------------------------------------------------------------------------
 // The lookup indices come from idx [B][T] (a strided column per table) or, when
 // key_t is given, from the transposed keys [T][key_pitch] that the table-major
-// propagate writes (main * 128 | (alternative * 128) << 16): one contiguous row
-// per table.
+// propagate writes (main << key_shift | (alternative << key_shift) << 16): one
+// contiguous row per table.
 __global__ __launch_bounds__(kWave) void k_bucket_samples(
     const int32_t *__restrict__ idx, const uint32_t *__restrict__ key_t, uint32_t key_pitch,
-    uint32_t batch, uint32_t n_detectors, uint32_t n_entries, uint32_t n_bits,
+    uint32_t key_shift, uint32_t batch, uint32_t n_detectors, uint32_t n_entries, uint32_t n_bits,
     int32_t *__restrict__ offsets, int32_t *__restrict__ samples) {
     extern __shared__ int32_t cnt[];
     const uint32_t t = blockIdx.x;
@@ -571,7 +571,7 @@ __global__ __launch_bounds__(kWave) void k_bucket_samples(
     const uint32_t emask = n_entries - 1;
     const uint32_t *kt = key_t ? key_t + (size_t)t * key_pitch : nullptr;
     auto key_of = [&](uint32_t b) -> uint32_t {
-        return kt ? ((kt[b] >> 7) & 0xFFu & emask) : ((uint32_t)idx[(size_t)b * n_detectors + t] & emask);
+        return kt ? (((kt[b] & 0xFFFFu) >> key_shift) & emask) : ((uint32_t)idx[(size_t)b * n_detectors + t] & emask);
     };
     for (uint32_t e = lane; e < n_entries; e += kWave) cnt[e] = 0;
     __syncthreads();
@@ -982,12 +982,13 @@ size_t wgrad_fc_scratch_bytes(const FcShape &s) {
 hipError_t launch_wgrad_fc(const FcShape &s, const float *g, const int32_t *idx, float *target,
                            double lr, bool int_mode, double int_rescaler, bool overwrite,
                            void *scratch, hipStream_t st, const uint32_t *key_t,
-                           uint32_t key_pitch) {
+                           uint32_t key_pitch, uint32_t key_shift) {
     if (rowsum_applies(s) && scratch != nullptr) {
         int32_t *offsets = reinterpret_cast<int32_t *>(scratch);
         int32_t *samples = offsets + (size_t)s.n_detectors * (s.n_entries + 1);
         hipError_t e = launch_bucket_samples(s, idx, offsets, samples, st,
-                                             s.n_entries <= 256 ? key_t : nullptr, key_pitch);
+                                             s.n_entries <= 256 ? key_t : nullptr, key_pitch,
+                                             key_shift);
         if (e != hipSuccess) return e;
         // 4 columns per lane once that still leaves 4 slices (two XCDs per slice)
         const uint32_t vec = (s.n_outputs % 4 == 0 && s.n_outputs >= 1024) ? 4 : pick_vec(s.n_outputs);
@@ -1060,13 +1061,13 @@ hipError_t launch_wgrad_commit_values(const float *g, uint32_t *cv, uint64_t n, 
 
 hipError_t launch_bucket_samples(const FcShape &s, const int32_t *idx, int32_t *offsets,
                                  int32_t *samples, hipStream_t st, const uint32_t *key_t,
-                                 uint32_t key_pitch) {
+                                 uint32_t key_pitch, uint32_t key_shift) {
     if (s.n_detectors == 0) return hipSuccess;
     uint32_t n_bits = 0;
     while ((1u << n_bits) < s.n_entries) n_bits++;
     hipLaunchKernelGGL(k_bucket_samples, dim3(s.n_detectors), dim3(kWave),
-                       s.n_entries * sizeof(int32_t), st, idx, key_t, key_pitch, s.batch,
-                       s.n_detectors, s.n_entries, n_bits, offsets, samples);
+                       s.n_entries * sizeof(int32_t), st, idx, key_t, key_pitch, key_shift,
+                       s.batch, s.n_detectors, s.n_entries, n_bits, offsets, samples);
     return hipGetLastError();
 }
 

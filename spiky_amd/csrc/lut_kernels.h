@@ -50,12 +50,12 @@ size_t wgrad_fc_scratch_bytes(const FcShape &s);
 
 // Table-row gradient: target[row, o] += lr * g[b, o] for every sample b hitting row.
 // scratch may be null when wgrad_fc_scratch_bytes() is 0.  key_t, when given,
-// holds the transposed keys [T][key_pitch] (lookup index * 128 in bits 0..14) that
-// launch_propagate_tm leaves at the start of its scratch.
+// holds the transposed keys [T][key_pitch] (lookup index << key_shift in the low
+// 16 bits) that launch_propagate_tm leaves at the start of its scratch.
 hipError_t launch_wgrad_fc(const FcShape &s, const float *g, const int32_t *idx, float *target,
                            double lr, bool int_mode, double int_rescaler, bool overwrite,
                            void *scratch, hipStream_t st, const uint32_t *key_t = nullptr,
-                           uint32_t key_pitch = 0);
+                           uint32_t key_pitch = 0, uint32_t key_shift = 7);
 
 // int32 fixed point -> fp32, in place.
 hipError_t launch_convert_i2f(float *buf, uint64_t n, double int_rescaler, hipStream_t st);
@@ -64,7 +64,8 @@ hipError_t launch_convert_i2f(float *buf, uint64_t n, double int_rescaler, hipSt
 // offsets [n_detectors][E+1], samples [n_detectors][batch].
 hipError_t launch_bucket_samples(const FcShape &s, const int32_t *idx, int32_t *offsets,
                                  int32_t *samples, hipStream_t st,
-                                 const uint32_t *key_t = nullptr, uint32_t key_pitch = 0);
+                                 const uint32_t *key_t = nullptr, uint32_t key_pitch = 0,
+                                 uint32_t key_shift = 7);
 
 // ---- table-major fully connected path (lut_tm.hip) ------------------------
 // Forward gather-sum through per-block partials in scratch; bit-identical to
@@ -84,8 +85,10 @@ hipError_t launch_fill_tm_i8(const FcShape &s, const int8_t *q8, const float *sc
 hipError_t launch_block_commit(const uint32_t *part, float *out, uint64_t n, uint32_t n_blocks,
                                bool int_mode, double int_rescaler, hipStream_t st);
 bool tm_propagate_applies(const FcShape &s);
-// Row pitch (samples) of the transposed keys the table-major propagate writes.
+// Row pitch (samples) and row shift of the transposed keys the table-major
+// propagate writes.
 uint32_t tm_key_pitch(uint32_t batch);
+uint32_t tm_key_row_shift(const FcShape &s);
 size_t tm_propagate_scratch_bytes(const FcShape &s);
 hipError_t launch_propagate_tm(const FcShape &s, const float *w, const float *g,
                                const int32_t *idx, const float *min_deltas,

@@ -728,6 +728,118 @@ __global__ __launch_bounds__(kTmThreads) void k_propagate_tm_dma(
     }
 }
 
+// Propagate partials over 64-column slices (fp32 tables with 256 entries,
+// n_outputs % 64 == 0).  A stage holds a table's 256 rows x 256 bytes: 16
+// lanes read one row, which the gfx950 LDS serves without bank conflicts
+// (8 lanes on random 128-byte rows conflict about half the time), and the
+// table bytes cross HBM in 256-byte pieces.  Thread layout: wave w, lane l:
+// sample w*4 + l/16 (+64 i for i < SPT), column quad l % 16.  A ring of two
+// stages (one table ahead, 136 KiB).  Each 8-lane half of a sample group
+// reduces its 32 columns, so dpart keeps the 32-column slices of
+// k_propagate_tm: dpart[2 * slice + half][t][b].  Keys are the rows' byte
+// offsets in this stage: main * 256 | (alt * 256) << 16.
+constexpr int kTm64Pass = (kTmThreads / kWave) * 4;  // samples per pass
+constexpr int kTm64Rows = kTmMaxEntries * 256;       // bytes of a stage's rows
+
+template <int SPT>
+__global__ __launch_bounds__(kTmThreads) void k_propagate_tm64(
+    const float *__restrict__ w, const float *__restrict__ g, const uint32_t *__restrict__ key_t,
+    float *__restrict__ dpart, uint32_t batch, uint32_t pitch, uint32_t n_outputs,
+    uint32_t n_detectors, uint32_t tpu, uint32_t n_slices, uint32_t n_chunks) {
+    constexpr int kRing = 2;
+    constexpr int kKeyBytes = kTm64Pass * SPT * 4;
+    constexpr int kStage = kTm64Rows + kKeyBytes;
+    constexpr uint32_t kKeyWaves = (kKeyBytes + kWave * 16 - 1) / (kWave * 16);
+    constexpr int kRowLoads = kTm64Rows / (kTmThreads * 16);  // 16-byte DMA loads per thread
+    __shared__ __attribute__((aligned(16))) uint8_t smem[kRing * kStage];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & (kWave - 1);
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const uint32_t slice = blockIdx.x % n_slices;
+    const uint32_t rest = blockIdx.x / n_slices;
+    const uint32_t chunk = rest % n_chunks;
+    const uint32_t k = rest / n_chunks;
+    const uint32_t t0 = k * tpu;
+    const uint32_t t1 = min(t0 + tpu, n_detectors);
+    const uint32_t b_base = chunk * (kTm64Pass * SPT);
+    const uint32_t col0 = slice * 64;
+    const uint32_t q = lane & 15;
+    const uint32_t half = q >> 3;
+    const uint32_t s_loc0 = wave * 4 + (lane >> 4);
+
+    f32x4 gv[SPT];
+#pragma unroll
+    for (int i = 0; i < SPT; i++) {
+        const uint32_t b = min(b_base + s_loc0 + kTm64Pass * i, batch - 1);
+        gv[i] = *reinterpret_cast<const f32x4 *>(g + (size_t)b * n_outputs + col0 + q * 4);
+    }
+    auto issue = [&](uint32_t si) {
+        const uint32_t t = t0 + si;
+        uint8_t *stage = smem + (si % kRing) * kStage;
+        const float *wt = w + (size_t)t * kTmMaxEntries * n_outputs + col0;
+#pragma unroll
+        for (int h = 0; h < kRowLoads; h++) {
+            const uint32_t c = (uint32_t)h * kTmThreads + tid;  // 16-byte chunk: row c / 16, quad c % 16
+            dma16(wt + (c >> 4) * n_outputs + (c & 15) * 4,
+                  stage + ((uint32_t)h * kTmThreads + wave * kWave) * 16);
+        }
+        if (wave < kKeyWaves) {
+            const uint32_t byte = wave * kWave * 16 + lane * 16;
+            if (byte < (uint32_t)kKeyBytes)
+                dma16(reinterpret_cast<const uint8_t *>(key_t + (size_t)t * pitch + b_base) + byte,
+                      stage + kTm64Rows + wave * kWave * 16);
+        }
+    };
+
+    const uint32_t nt = t1 - t0;
+    issue(0);
+    for (uint32_t st = 0; st < nt; st++) {
+        // only stage st is outstanding here: wait for it, then publish it
+        wait_vm(0);
+        __asm__ volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        __asm__ volatile("" ::: "memory");
+        // every wave is done with stage st - 1: its slot takes stage st + 1
+        if (st + 1 < nt) issue(st + 1);
+        const uint8_t *tb = smem + (st % kRing) * kStage;
+        const uint32_t *keys = reinterpret_cast<const uint32_t *>(tb + kTm64Rows);
+        const uint8_t *tq = tb + q * 16;
+        const uint32_t t = t0 + st;
+        float *dp = dpart + ((size_t)(2 * slice + half) * n_detectors + t) * batch;
+#pragma unroll
+        for (int h8 = 0; h8 < SPT; h8 += 8) {
+            constexpr int N = SPT < 8 ? SPT : 8;
+            float dv[8];
+#pragma unroll
+            for (int h = 0; h < N; h += 2) {
+                const uint32_t k0 = keys[s_loc0 + kTm64Pass * (h8 + h)];
+                const uint32_t k1 = keys[s_loc0 + kTm64Pass * (h8 + h + 1)];
+                const f32x4 a0 = *reinterpret_cast<const f32x4 *>(tq + (k0 & 0xFFFFu));
+                const f32x4 e0 = *reinterpret_cast<const f32x4 *>(tq + (k0 >> 16));
+                const f32x4 a1 = *reinterpret_cast<const f32x4 *>(tq + (k1 & 0xFFFFu));
+                const f32x4 e1 = *reinterpret_cast<const f32x4 *>(tq + (k1 >> 16));
+                const f32x4 &g0 = gv[h8 + h];
+                const f32x4 &g1 = gv[h8 + h + 1];
+                float d0 = (a0.x - e0.x) * g0.x;
+                d0 = __builtin_fmaf(a0.y - e0.y, g0.y, d0);
+                d0 = __builtin_fmaf(a0.z - e0.z, g0.z, d0);
+                d0 = __builtin_fmaf(a0.w - e0.w, g0.w, d0);
+                float d1 = (a1.x - e1.x) * g1.x;
+                d1 = __builtin_fmaf(a1.y - e1.y, g1.y, d1);
+                d1 = __builtin_fmaf(a1.z - e1.z, g1.z, d1);
+                d1 = __builtin_fmaf(a1.w - e1.w, g1.w, d1);
+                dv[h] = d0;
+                dv[h + 1] = d1;
+            }
+            // the 8 lanes of each half hold 4-column pieces of N dots; after the
+            // reduce-scatter lane (q & 7) holds sample rs_item's 32-column sum
+            reduce_scatter8_f32<N>(dv, q & 7);
+            const uint32_t b = b_base + s_loc0 + kTm64Pass * (h8 + rs_item<N>(q & 7));
+            if (rs_writer<N>(q & 7) && b < batch) dp[b] = dv[0];
+        }
+    }
+}
+
 // du[b][t] = sum over slices s ascending of du(min margin of (b, t)) *
 // dpart[s][t][b] (fp64), or 0 when the min-margin index is unused.  One
 // workgroup per 64 tables x 64 samples tile; md / mi and du pass through LDS so
@@ -854,8 +966,8 @@ __global__ __launch_bounds__(256) void k_transpose_idx(const int32_t *__restrict
     }
 }
 
-// keys_t[t][b] = main * 128 | (alt * 128) << 16 (the rows' byte offsets in a
-// 128-byte-row stage) with alt = main ^ (1 << min_idx) (main when the
+// keys_t[t][b] = main << row_shift | (alt << row_shift) << 16 (the rows' byte
+// offsets in a stage of 128- or 256-byte rows) with alt = main ^ (1 << min_idx) (main when the
 // min-margin index is unused), through a 64x64 LDS tile; row pitch `pitch` >=
 // batch, samples past the batch get 0.
 __global__ __launch_bounds__(256) void k_transpose_keys(const int32_t *__restrict__ idx,
@@ -863,7 +975,7 @@ __global__ __launch_bounds__(256) void k_transpose_keys(const int32_t *__restric
                                                         uint32_t *__restrict__ key_t,
                                                         uint32_t batch, uint32_t pitch,
                                                         uint32_t n_detectors, uint32_t n_anchors,
-                                                        uint32_t n_entries) {
+                                                        uint32_t n_entries, uint32_t row_shift) {
     __shared__ uint32_t tile[64][65];
     const uint32_t tb = blockIdx.x * 64;
     const uint32_t bb = blockIdx.y * 64;
@@ -876,7 +988,7 @@ __global__ __launch_bounds__(256) void k_transpose_keys(const int32_t *__restric
             const uint32_t rm = (uint32_t)idx[bt] & (n_entries - 1);
             const int32_t m = mi[bt];
             const uint32_t ra = (m >= 0 && (uint32_t)m < n_anchors) ? (rm ^ (1u << m)) : rm;
-            tile[r][tx] = (rm << 7) | (ra << 23);
+            tile[r][tx] = (rm << row_shift) | (ra << (row_shift + 16));
         } else {
             tile[r][tx] = 0;
         }
@@ -1031,6 +1143,17 @@ bool tm_propagate_applies(const FcShape &s) {
            n_slices * s.batch * s.n_detectors * 4 <= (4ull << 30);
 }
 
+static hipError_t launch_propagate_finish(const FcShape &s, float *dpart, uint32_t n_slices,
+                                          const float *min_deltas, const int32_t *min_idx,
+                                          const int32_t *anchors, float *x_grad, hipStream_t st);
+
+// the 64-column propagate: whole 256-row fp32 tables, 64-column slices
+static bool tm_propagate_wide(const FcShape &s) {
+    return s.n_entries == (uint32_t)kTmMaxEntries && s.n_outputs % 64 == 0 && s.batch >= 256;
+}
+
+uint32_t tm_key_row_shift(const FcShape &s) { return tm_propagate_wide(s) ? 8u : 7u; }
+
 uint32_t tm_key_pitch(uint32_t batch) {
     const uint32_t chunk = kTmPass * tm_spt(batch);
     return (batch + chunk - 1) / chunk * chunk;
@@ -1051,18 +1174,40 @@ hipError_t launch_propagate_tm(const FcShape &s, const float *w, const float *g,
     const uint32_t pitch = tm_key_pitch(s.batch);
     const size_t keys = ((size_t)s.n_detectors * pitch * 4 + 255) & ~(size_t)255;
     float *dpart = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(scratch) + keys);
+    const bool wide = tm_propagate_wide(s);
     hipLaunchKernelGGL(k_transpose_keys, dim3((s.n_detectors + 63) / 64, (pitch + 63) / 64),
                        dim3(256), 0, st, idx, min_idx, key_t, s.batch, pitch, s.n_detectors,
-                       s.n_anchors, s.n_entries);
+                       s.n_anchors, s.n_entries, wide ? 8u : 7u);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    const uint32_t n_slices = (s.n_outputs + kTmCols - 1) / kTmCols;
+    const uint32_t tpu = 32;
+    const uint32_t n_units = (s.n_detectors + tpu - 1) / tpu;
+    if (wide) {
+        // 64-column slices; chunks of 1024 samples as the key pitch assumes
+        const uint32_t spt64 = s.batch <= 256 ? 4 : (s.batch <= 512 ? 8 : 16);
+        const uint32_t n_chunks = (s.batch + kTm64Pass * spt64 - 1) / (kTm64Pass * spt64);
+        const uint32_t n_slices64 = s.n_outputs / 64;
+        const uint64_t grid = (uint64_t)n_units * n_chunks * n_slices64;
+        if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
+#define SPIKY_P64(SPT)                                                                              \
+    hipLaunchKernelGGL((k_propagate_tm64<SPT>), dim3((uint32_t)grid), dim3(kTmThreads), 0, st, w, g, \
+                       key_t, dpart, s.batch, pitch, s.n_outputs, s.n_detectors, tpu, n_slices64,  \
+                       n_chunks)
+        switch (spt64) {
+            case 4: SPIKY_P64(4); break;
+            case 8: SPIKY_P64(8); break;
+            default: SPIKY_P64(16); break;
+        }
+#undef SPIKY_P64
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        return launch_propagate_finish(s, dpart, n_slices, min_deltas, min_idx, anchors, x_grad, st);
+    }
     // the LDS-DMA ring needs whole 256-row tables
     const bool dma = s.n_entries == (uint32_t)kTmMaxEntries;
     const uint32_t spt = tm_spt(s.batch);
     const uint32_t n_chunks = (s.batch + kTmPass * spt - 1) / (kTmPass * spt);
-    const uint32_t n_slices = (s.n_outputs + kTmCols - 1) / kTmCols;
-    const uint32_t tpu = 32;
-    const uint32_t n_units = (s.n_detectors + tpu - 1) / tpu;
     const uint64_t grid = (uint64_t)n_units * n_chunks * n_slices;
     if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
 #define SPIKY_PTM(SPT)                                                                              \
@@ -1084,6 +1229,14 @@ hipError_t launch_propagate_tm(const FcShape &s, const float *w, const float *g,
 #undef SPIKY_PTM
     e = hipGetLastError();
     if (e != hipSuccess) return e;
+    return launch_propagate_finish(s, dpart, n_slices, min_deltas, min_idx, anchors, x_grad, st);
+}
+
+// du from the slice partials, then the input-gradient scatter
+static hipError_t launch_propagate_finish(const FcShape &s, float *dpart, uint32_t n_slices,
+                                          const float *min_deltas, const int32_t *min_idx,
+                                          const int32_t *anchors, float *x_grad, hipStream_t st) {
+    hipError_t e;
     float *du = dpart + (size_t)n_slices * s.batch * s.n_detectors;
     hipLaunchKernelGGL(k_propagate_reduce, dim3((s.n_detectors + 63) / 64, (s.batch + 63) / 64),
                        dim3(256), 0, st, dpart, min_deltas, min_idx, du, s.batch, s.n_detectors,

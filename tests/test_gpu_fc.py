@@ -138,6 +138,14 @@ def test_table_major_two_sample_chunks(oracle, cuda_device):
     run_fc(oracle, 1030, 300, 40, 8, 100, seed=15)
 
 
+@pytest.mark.parametrize("B,O", [(256, 128), (300, 192), (1100, 64)])
+def test_table_major_wide_slices(oracle, cuda_device, B, O):
+    # 256-entry tables and O % 64 == 0: the propagate's 64-column slices (16
+    # lanes per 256-byte row) with 4, 8 and 16 samples per lane, and a second
+    # sample chunk of 76 samples
+    run_fc(oracle, B, 300, 40, 8, O, seed=16)
+
+
 def test_large_batch_int32_summation(oracle, cuda_device):
     run_fc(oracle, 530, 64, 20, 4, 512, seed=14, int_rescaler=0.5)
 
