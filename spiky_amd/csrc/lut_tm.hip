@@ -69,6 +69,7 @@ __device__ __forceinline__ double dpp_f64(double v) {
 constexpr int kDppHalfMirror = 0x141;  // lane l of 8 <-> 7 - l
 constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int kDppRowRor8 = 0x128;     // lane l of 16 <- lane (l + 8) % 16
 
 // One reduce-scatter step over a lane pairing: the pair sums its N items and
 // each lane keeps half of them (the lane with `upper` set keeps the upper
@@ -735,20 +736,25 @@ __global__ __launch_bounds__(kTmThreads) void k_propagate_tm_dma(
 // table bytes cross HBM in 256-byte pieces.  Thread layout: wave w, lane l:
 // sample w*4 + l/16 (+64 i for i < SPT), column quad l % 16.  A ring of two
 // stages (one table ahead, 136 KiB).  Each 8-lane half of a sample group
-// reduces its 32 columns, so dpart keeps the 32-column slices of
-// k_propagate_tm: dpart[2 * slice + half][t][b].  Keys are the rows' byte
-// offsets in this stage: main * 256 | (alt * 256) << 16.
+// reduces its 32 columns; the two 32-column dots become the reference's block
+// terms du * dot (fp64, each dropped unless |term| > EPS when the blocks are
+// 32 outputs wide, proto:833-863) and their sum goes to dpart[slice][t][b]
+// (fp32), so k_propagate_reduce_pre only sums slices.  Keys are the rows' byte
+// offsets in this stage, main * 256 | (alt * 256) << 16, and du_t[t][b] is
+// du(min margin) (0 when the sample's min-margin index is unused); both rows
+// have the key pitch.
 constexpr int kTm64Pass = (kTmThreads / kWave) * 4;  // samples per pass
 constexpr int kTm64Rows = kTmMaxEntries * 256;       // bytes of a stage's rows
 
 template <int SPT>
 __global__ __launch_bounds__(kTmThreads) void k_propagate_tm64(
     const float *__restrict__ w, const float *__restrict__ g, const uint32_t *__restrict__ key_t,
-    float *__restrict__ dpart, uint32_t batch, uint32_t pitch, uint32_t n_outputs,
-    uint32_t n_detectors, uint32_t tpu, uint32_t n_slices, uint32_t n_chunks) {
+    const float *__restrict__ du_t, float *__restrict__ dpart, uint32_t batch, uint32_t pitch,
+    uint32_t n_outputs, uint32_t n_detectors, uint32_t tpu, uint32_t n_slices, uint32_t n_chunks,
+    bool block_eps) {
     constexpr int kRing = 2;
-    constexpr int kKeyBytes = kTm64Pass * SPT * 4;
-    constexpr int kStage = kTm64Rows + kKeyBytes;
+    constexpr int kKeyBytes = kTm64Pass * SPT * 4;  // keys, then as many bytes of du
+    constexpr int kStage = kTm64Rows + 2 * kKeyBytes;
     constexpr uint32_t kKeyWaves = (kKeyBytes + kWave * 16 - 1) / (kWave * 16);
     constexpr int kRowLoads = kTm64Rows / (kTmThreads * 16);  // 16-byte DMA loads per thread
     __shared__ __attribute__((aligned(16))) uint8_t smem[kRing * kStage];
@@ -783,11 +789,15 @@ __global__ __launch_bounds__(kTmThreads) void k_propagate_tm64(
             dma16(wt + (c >> 4) * n_outputs + (c & 15) * 4,
                   stage + ((uint32_t)h * kTmThreads + wave * kWave) * 16);
         }
-        if (wave < kKeyWaves) {
-            const uint32_t byte = wave * kWave * 16 + lane * 16;
+        if (wave < 2 * kKeyWaves) {
+            // waves 0 .. kKeyWaves-1 load the keys, the next kKeyWaves the du values
+            const bool is_du = wave >= kKeyWaves;
+            const uint32_t wk = is_du ? wave - kKeyWaves : wave;
+            const uint32_t byte = wk * kWave * 16 + lane * 16;
+            const uint8_t *src = is_du ? reinterpret_cast<const uint8_t *>(du_t + (size_t)t * pitch + b_base)
+                                       : reinterpret_cast<const uint8_t *>(key_t + (size_t)t * pitch + b_base);
             if (byte < (uint32_t)kKeyBytes)
-                dma16(reinterpret_cast<const uint8_t *>(key_t + (size_t)t * pitch + b_base) + byte,
-                      stage + kTm64Rows + wave * kWave * 16);
+                dma16(src + byte, stage + kTm64Rows + (is_du ? kKeyBytes : 0) + wk * kWave * 16);
         }
     };
 
@@ -803,9 +813,10 @@ __global__ __launch_bounds__(kTmThreads) void k_propagate_tm64(
         if (st + 1 < nt) issue(st + 1);
         const uint8_t *tb = smem + (st % kRing) * kStage;
         const uint32_t *keys = reinterpret_cast<const uint32_t *>(tb + kTm64Rows);
+        const float *dus = reinterpret_cast<const float *>(tb + kTm64Rows + kKeyBytes);
         const uint8_t *tq = tb + q * 16;
         const uint32_t t = t0 + st;
-        float *dp = dpart + ((size_t)(2 * slice + half) * n_detectors + t) * batch;
+        float *dp = dpart + ((size_t)slice * n_detectors + t) * batch;
 #pragma unroll
         for (int h8 = 0; h8 < SPT; h8 += 8) {
             constexpr int N = SPT < 8 ? SPT : 8;
@@ -834,8 +845,13 @@ __global__ __launch_bounds__(kTmThreads) void k_propagate_tm64(
             // the 8 lanes of each half hold 4-column pieces of N dots; after the
             // reduce-scatter lane (q & 7) holds sample rs_item's 32-column sum
             reduce_scatter8_f32<N>(dv, q & 7);
-            const uint32_t b = b_base + s_loc0 + kTm64Pass * (h8 + rs_item<N>(q & 7));
-            if (rs_writer<N>(q & 7) && b < batch) dp[b] = dv[0];
+            const uint32_t sl = s_loc0 + kTm64Pass * (h8 + rs_item<N>(q & 7));
+            double term = (double)dus[sl] * (double)dv[0];
+            if (block_eps && !(fabs(term) > kEps)) term = 0.0;
+            // lanes q and q ^ 8 hold the two 32-column blocks of the same sample
+            const double other = dpp_f64<kDppRowRor8>(term);
+            const uint32_t b = b_base + sl;
+            if (half == 0 && rs_writer<N>(q & 7) && b < batch) dp[b] = (float)(term + other);
         }
     }
 }
@@ -908,6 +924,45 @@ __global__ __launch_bounds__(256) void k_propagate_reduce(const float *__restric
     }
 }
 
+// du[b][t] = fp32 of the fp64 sum over slices s ascending of dpart[s][t][b]
+// (terms du(margin) * dot already formed by k_propagate_tm64), or 0 unless
+// |sum| > EPS.  Same 64 x 64 tiling as k_propagate_reduce.
+__global__ __launch_bounds__(256) void k_propagate_reduce_pre(const float *__restrict__ dpart,
+                                                              float *__restrict__ du_out,
+                                                              uint32_t batch, uint32_t n_detectors,
+                                                              uint32_t n_slices) {
+    __shared__ float s_du[64][65];
+    const uint32_t tb = blockIdx.x * 64;
+    const uint32_t bb = blockIdx.y * 64;
+    const uint32_t tx = threadIdx.x & 63;
+    const uint32_t ty = threadIdx.x >> 6;
+    for (uint32_t r = ty; r < 64; r += 4) {
+        const uint32_t t = tb + r, b = bb + tx;
+        float du = 0.0f;
+        if (b < batch && t < n_detectors) {
+            const float *p = dpart + (size_t)t * batch + b;
+            const size_t stride = (size_t)n_detectors * batch;
+            double acc = 0.0;
+            uint32_t sI = 0;
+            for (; sI + 8 <= n_slices; sI += 8) {
+                float v[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) v[u] = p[(sI + u) * stride];
+#pragma unroll
+                for (int u = 0; u < 8; u++) acc += (double)v[u];
+            }
+            for (; sI < n_slices; sI++) acc += (double)p[sI * stride];
+            if (fabs(acc) > kEps) du = (float)acc;
+        }
+        s_du[tx][r] = du;
+    }
+    __syncthreads();
+    for (uint32_t r = ty; r < 64; r += 4) {
+        const uint32_t b = bb + r, t = tb + tx;
+        if (b < batch && t < n_detectors) du_out[(size_t)b * n_detectors + t] = s_du[r][tx];
+    }
+}
+
 // x_grad[b][a1] += du, x_grad[b][a2] -= du for every table with |du| > EPS
 // (propagate_through_detector, proto:821-867).  One workgroup per group of
 // samples; their input-gradient rows are accumulated in LDS and added to HBM
@@ -969,14 +1024,18 @@ __global__ __launch_bounds__(256) void k_transpose_idx(const int32_t *__restrict
 // keys_t[t][b] = main << row_shift | (alt << row_shift) << 16 (the rows' byte
 // offsets in a stage of 128- or 256-byte rows) with alt = main ^ (1 << min_idx) (main when the
 // min-margin index is unused), through a 64x64 LDS tile; row pitch `pitch` >=
-// batch, samples past the batch get 0.
+// batch, samples past the batch get 0.  With du_t, also du_t[t][b] = fp32 of
+// du(min margin), 0 when the min-margin index is unused.
 __global__ __launch_bounds__(256) void k_transpose_keys(const int32_t *__restrict__ idx,
                                                         const int32_t *__restrict__ mi,
+                                                        const float *__restrict__ md,
                                                         uint32_t *__restrict__ key_t,
+                                                        float *__restrict__ du_t,
                                                         uint32_t batch, uint32_t pitch,
                                                         uint32_t n_detectors, uint32_t n_anchors,
                                                         uint32_t n_entries, uint32_t row_shift) {
     __shared__ uint32_t tile[64][65];
+    __shared__ float dtile[64][65];
     const uint32_t tb = blockIdx.x * 64;
     const uint32_t bb = blockIdx.y * 64;
     const uint32_t tx = threadIdx.x & 63;
@@ -989,14 +1048,19 @@ __global__ __launch_bounds__(256) void k_transpose_keys(const int32_t *__restric
             const int32_t m = mi[bt];
             const uint32_t ra = (m >= 0 && (uint32_t)m < n_anchors) ? (rm ^ (1u << m)) : rm;
             tile[r][tx] = (rm << row_shift) | (ra << (row_shift + 16));
+            if (du_t) dtile[r][tx] = (m >= 0 && (uint32_t)m < n_anchors) ? (float)du_of_margin(md[bt]) : 0.0f;
         } else {
             tile[r][tx] = 0;
+            dtile[r][tx] = 0.0f;
         }
     }
     __syncthreads();
     for (uint32_t r = ty; r < 64; r += 4) {
         const uint32_t t = tb + r, b = bb + tx;
-        if (b < pitch && t < n_detectors) key_t[(size_t)t * pitch + b] = tile[tx][r];
+        if (b < pitch && t < n_detectors) {
+            key_t[(size_t)t * pitch + b] = tile[tx][r];
+            if (du_t) du_t[(size_t)t * pitch + b] = dtile[tx][r];
+        }
     }
 }
 
@@ -1146,6 +1210,8 @@ bool tm_propagate_applies(const FcShape &s) {
 static hipError_t launch_propagate_finish(const FcShape &s, float *dpart, uint32_t n_slices,
                                           const float *min_deltas, const int32_t *min_idx,
                                           const int32_t *anchors, float *x_grad, hipStream_t st);
+static hipError_t launch_propagate_scatter(const FcShape &s, const float *du, const int32_t *min_idx,
+                                           const int32_t *anchors, float *x_grad, hipStream_t st);
 
 // the 64-column propagate: whole 256-row fp32 tables, 64-column slices
 static bool tm_propagate_wide(const FcShape &s) {
@@ -1159,11 +1225,12 @@ uint32_t tm_key_pitch(uint32_t batch) {
     return (batch + chunk - 1) / chunk * chunk;
 }
 
-// scratch: keys [T][pitch] u32 | partial dots [slices][T][B] f32 | du [B][T] f32
+// scratch: keys [T][pitch] u32 | du_t [T][pitch] f32 | partial dots
+// [slices][T][B] f32 | du [B][T] f32
 size_t tm_propagate_scratch_bytes(const FcShape &s) {
     const uint64_t n_slices = (s.n_outputs + kTmCols - 1) / kTmCols;
     const size_t keys = ((size_t)s.n_detectors * tm_key_pitch(s.batch) * 4 + 255) & ~(size_t)255;
-    return keys + (size_t)(n_slices + 1) * s.batch * s.n_detectors * 4;
+    return 2 * keys + (size_t)(n_slices + 1) * s.batch * s.n_detectors * 4;
 }
 
 hipError_t launch_propagate_tm(const FcShape &s, const float *w, const float *g,
@@ -1173,11 +1240,12 @@ hipError_t launch_propagate_tm(const FcShape &s, const float *w, const float *g,
     uint32_t *key_t = reinterpret_cast<uint32_t *>(scratch);
     const uint32_t pitch = tm_key_pitch(s.batch);
     const size_t keys = ((size_t)s.n_detectors * pitch * 4 + 255) & ~(size_t)255;
-    float *dpart = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(scratch) + keys);
+    float *du_t = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(scratch) + keys);
+    float *dpart = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(scratch) + 2 * keys);
     const bool wide = tm_propagate_wide(s);
     hipLaunchKernelGGL(k_transpose_keys, dim3((s.n_detectors + 63) / 64, (pitch + 63) / 64),
-                       dim3(256), 0, st, idx, min_idx, key_t, s.batch, pitch, s.n_detectors,
-                       s.n_anchors, s.n_entries, wide ? 8u : 7u);
+                       dim3(256), 0, st, idx, min_idx, min_deltas, key_t, wide ? du_t : nullptr,
+                       s.batch, pitch, s.n_detectors, s.n_anchors, s.n_entries, wide ? 8u : 7u);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const uint32_t n_slices = (s.n_outputs + kTmCols - 1) / kTmCols;
@@ -1192,8 +1260,8 @@ hipError_t launch_propagate_tm(const FcShape &s, const float *w, const float *g,
         if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
 #define SPIKY_P64(SPT)                                                                              \
     hipLaunchKernelGGL((k_propagate_tm64<SPT>), dim3((uint32_t)grid), dim3(kTmThreads), 0, st, w, g, \
-                       key_t, dpart, s.batch, pitch, s.n_outputs, s.n_detectors, tpu, n_slices64,  \
-                       n_chunks)
+                       key_t, du_t, dpart, s.batch, pitch, s.n_outputs, s.n_detectors, tpu,        \
+                       n_slices64, n_chunks, s.ogs == (uint32_t)kTmCols)
         switch (spt64) {
             case 4: SPIKY_P64(4); break;
             case 8: SPIKY_P64(8); break;
@@ -1202,7 +1270,13 @@ hipError_t launch_propagate_tm(const FcShape &s, const float *w, const float *g,
 #undef SPIKY_P64
         e = hipGetLastError();
         if (e != hipSuccess) return e;
-        return launch_propagate_finish(s, dpart, n_slices, min_deltas, min_idx, anchors, x_grad, st);
+        // the partials already hold du * dot: sum the 64-column slices
+        float *du = dpart + (size_t)n_slices * s.batch * s.n_detectors;
+        hipLaunchKernelGGL(k_propagate_reduce_pre, dim3((s.n_detectors + 63) / 64, (s.batch + 63) / 64),
+                           dim3(256), 0, st, dpart, du, s.batch, s.n_detectors, n_slices64);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        return launch_propagate_scatter(s, du, min_idx, anchors, x_grad, st);
     }
     // the LDS-DMA ring needs whole 256-row tables
     const bool dma = s.n_entries == (uint32_t)kTmMaxEntries;
@@ -1243,6 +1317,12 @@ static hipError_t launch_propagate_finish(const FcShape &s, float *dpart, uint32
                        s.n_anchors, n_slices, s.ogs == (uint32_t)kTmCols);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
+    return launch_propagate_scatter(s, du, min_idx, anchors, x_grad, st);
+}
+
+// x_grad from du [B][T]
+static hipError_t launch_propagate_scatter(const FcShape &s, const float *du, const int32_t *min_idx,
+                                           const int32_t *anchors, float *x_grad, hipStream_t st) {
     const uint32_t spg = std::max<uint32_t>(1, std::min<uint32_t>(16, kScatterLds / 4 / s.n_inputs));
     const uint32_t groups = (s.batch + spg - 1) / spg;
     hipLaunchKernelGGL(k_propagate_scatter, dim3(groups), dim3(kScatterThreads), 0, st, du,
