@@ -430,6 +430,78 @@ def bench_transformer(args):
     print(json.dumps(res), flush=True)
 
 
+DENSIFY = dict(words=1 << 28, densities=(0.01, 0.1, 0.5), cpu_words=1 << 25)
+
+
+def bench_densify(args):
+    """The Sparse policy's dense -> sparse export (DenseToSparseConverter,
+    lut_densify.hip) on a 1 GiB fp32 gradient at three densities, with
+    erase_input=True as LUTLayer uses it.  HBM bytes per call: the source read
+    twice (count, then compaction), 12 bytes per kept word (int64 index + value)
+    and 16 per erased quad."""
+    import torch
+    from spiky_amd.util.torch_utils import DenseToSparseConverter
+    dev = torch.device("cuda:0")
+    n = DENSIFY["words"]
+    g = torch.Generator(device=dev).manual_seed(0)
+    conv = DenseToSparseConverter()
+    rows = []
+    for dens in DENSIFY["densities"]:
+        src0 = torch.randn(n, device=dev, generator=g)
+        src0[torch.rand(n, device=dev, generator=g) >= dens] = 0.0
+        nnz = int(torch.count_nonzero(src0))
+        quads = int(torch.count_nonzero(src0.view(-1, 4).abs().sum(1)))
+        bufs = (torch.empty(nnz, dtype=torch.int64, device=dev), torch.empty(nnz, device=dev))
+        src = torch.empty_like(src0)
+        times = []
+        for it in range(args.warmup + args.steps):
+            src.copy_(src0)
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            conv.dense_to_sparse_32(src, True, bufs, decouple=False)
+            b.record()
+            torch.cuda.synchronize()
+            if it >= args.warmup:
+                times.append(a.elapsed_time(b))
+        ms = float(sorted(times)[len(times) // 2])
+        traffic = 2 * 4 * n + 12 * nnz + 16 * quads
+        rows.append({"density": dens, "nnz": nnz, "ms": round(ms, 4),
+                     "gb_per_s": round(traffic / ms / 1e6, 1)})
+        log(f"densify density {dens}: {ms:.3f} ms, {traffic / ms / 1e6:.0f} GB/s")
+    main_row = rows[1]
+    cpu = None
+    if not args.no_cpu_baseline:
+        import numpy as np
+        import oracle
+        m = DENSIFY["cpu_words"]
+        rng = np.random.default_rng(0)
+        a = rng.standard_normal(m).astype(np.float32)
+        a[rng.random(m) >= DENSIFY["densities"][1]] = 0.0
+        t = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            oracle.dense_to_sparse_32(a)
+            t.append(time.perf_counter() - t0)
+        med = float(np.median(t[1:]))
+        cpu = {"value": round(m * 4 / med / 1e9, 2), "unit": "GB/s of source", "cores": 1, "kind": "port",
+               "sample": f"numpy restatement on {m} words at density 0.1; median of 4 after 1 warm-up; "
+                         f"{med:.3f} s per call"}
+    out = {
+        "metric": "dense_to_sparse_32 source GB/s (GradientType.Sparse export, density 0.1)",
+        "value": round(n * 4 / main_row["ms"] / 1e6, 1), "unit": "GB/s of source", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": main_row["ms"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u32",
+        "data": "synthetic (N(0,1) fp32 words, zeroed at random to the density)",
+        "config": {"workload": "dense -> sparse COO of a 1 GiB fp32 gradient, erase_input=True",
+                   "words": n, "densities": rows},
+        "roofline": {"bound": "hbm", "achieved": main_row["gb_per_s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(main_row["gb_per_s"] / PEAK_HBM_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -437,6 +509,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS) + [2, 4, 5])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--densify", action="store_true",
+                    help="time the dense -> sparse gradient converter instead of a LUT config")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="only run a plain copy of this many MiB (counter calibration) and exit")
     args = ap.parse_args()
@@ -448,6 +522,9 @@ def main():
               "(the multi-GPU table-parallel design is described, not built).", file=sys.stderr)
         sys.exit(2)
 
+    if args.densify:
+        bench_densify(args)
+        return
     if args.config == 5:
         bench_transformer(args)
         return

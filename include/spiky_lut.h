@@ -186,6 +186,34 @@ void spiky_lut_reset_profiler(spiky_lut_manager *m);
 int spiky_lut_set_kernel_timing(spiky_lut_manager *m, int enable);
 int spiky_lut_kernel_times(spiky_lut_manager *m, char *buf, uint64_t buf_len, int reset);
 
+/* ---- dense -> sparse converter --------------------------------------------
+ * Replaces DenseToSparseConverterNative (spiky_cuda/torch_utils/torch_utils.cu:
+ * 11-339; Python side spiky/util/torch_utils.py:7-125).  A 32-bit word of the
+ * source is kept when its bit pattern is non-zero (the reference's int4
+ * compare, torch_utils_kernels_logic.proto:20-35).  Unlike the reference,
+ * whose blocks claim output ranges with an atomic, the output is in ascending
+ * index order.  The workspace is caller memory of
+ * spiky_densify32_workspace_bytes(n) bytes on the source's device. */
+
+/* Bytes of workspace for a source of n words. */
+uint64_t spiky_densify32_workspace_bytes(uint64_t n);
+
+/* DenseToSparseConverterNative::count_nonzero: *counter (device int64) =
+ * number of non-zero words; n % 4 == 0 or SPIKY_VALUE_ERROR with the
+ * reference's text.  Leaves the per-tile offsets in the workspace. */
+int spiky_count_nonzero32(const void *source, uint64_t n, void *workspace,
+                          uint64_t workspace_bytes, int64_t *counter, void *stream);
+
+/* DenseToSparseConverterNative::dense_to_sparse_32: writes the indices (int64)
+ * and raw 32-bit values of the non-zero words, at most `capacity` of them;
+ * *counter = the number of non-zero words (which may exceed capacity: the
+ * caller checks).  erase_input != 0 zeroes the kept words of the source.
+ * counted != 0 reuses the workspace of an spiky_count_nonzero32 call on the
+ * same, unchanged source (skips one read of it). */
+int spiky_dense_to_sparse32(void *source, uint64_t n, int64_t *indices, void *values,
+                            uint64_t capacity, void *workspace, uint64_t workspace_bytes,
+                            int64_t *counter, int erase_input, int counted, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

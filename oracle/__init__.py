@@ -238,3 +238,18 @@ def gather_wgrad_seq(g, idx, pidx, target, batch, n_outputs, n_detectors, seq_le
                                   float(first_meta_lr), float(external_lr), int(int_mode),
                                   float(int_rescaler))
     return target
+
+
+def dense_to_sparse_32(source):
+    """Non-zero 32-bit words of a 1-D array: (int64 indices ascending, values
+    of the same dtype).  A word counts as non-zero when its bit pattern is
+    non-zero, as in the reference's int4 compare (densify_logic,
+    spiky_cuda/torch_utils/torch_utils_kernels_logic.proto:20-35), so a float
+    -0.0 is kept.  The reference orders its output only within a block; this
+    restatement (and the HIP path) orders it by index."""
+    src = np.ascontiguousarray(source)
+    if src.dtype.itemsize != 4:
+        raise ValueError("source must be 32-bit")
+    bits = src.view(np.uint32)
+    idx = np.flatnonzero(bits).astype(np.int64)
+    return idx, src[idx].copy()

@@ -48,6 +48,9 @@ _SIGNATURES = {
     "spiky_lut_kernel_times": ([_vp, ctypes.c_char_p, _u64, _i32], _i32),
     "spiky_grow_cuboid": ([_u32, _vp, _vp, _u32, _vp, _vp, _vp, _f32, _u64, _u32, _vp, _vp, _u64,
                            ctypes.POINTER(_u64)], _i32),
+    "spiky_densify32_workspace_bytes": ([_u64], _u64),
+    "spiky_count_nonzero32": ([_vp, _u64, _vp, _u64, _vp, _vp], _i32),
+    "spiky_dense_to_sparse32": ([_vp, _u64, _vp, _vp, _u64, _vp, _u64, _vp, _i32, _i32, _vp], _i32),
 }
 
 # Sequence-mode entry points are bound when the library exports them.

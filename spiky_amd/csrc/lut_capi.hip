@@ -766,6 +766,44 @@ int spiky_lut_decode_anchors_compact(const uint32_t *encoded_pairs, uint32_t n_d
     });
 }
 
+// ---- dense -> sparse converter (torch_utils.cu:11-339) ---------------------
+
+uint64_t spiky_densify32_workspace_bytes(uint64_t n) { return spiky::densify32_workspace_bytes(n); }
+
+int spiky_count_nonzero32(const void *source, uint64_t n, void *workspace,
+                          uint64_t workspace_bytes, int64_t *counter, void *stream) {
+    return guarded([&] {
+        // torch_utils.py:63-67 (the size rule; the dtype rule is the caller's)
+        if (n % 4 != 0) throw ValueError("source tensor size must be divisable by 4");
+        if (!counter || (n > 0 && !source)) throw ValueError("null pointer");
+        if (!workspace || workspace_bytes < spiky::densify32_workspace_bytes(n))
+            throw ValueError("densify workspace too small");
+        check_hip(spiky::launch_densify32_count(static_cast<const uint32_t *>(source), n, workspace,
+                                                counter, as_stream(stream)),
+                  "count_nonzero");
+    });
+}
+
+int spiky_dense_to_sparse32(void *source, uint64_t n, int64_t *indices, void *values,
+                            uint64_t capacity, void *workspace, uint64_t workspace_bytes,
+                            int64_t *counter, int erase_input, int counted, void *stream) {
+    return guarded([&] {
+        if (n % 4 != 0) throw ValueError("source tensor size must be divisable by 4");
+        if (!counter || (n > 0 && !source) || (capacity > 0 && (!indices || !values)))
+            throw ValueError("null pointer");
+        if (!workspace || workspace_bytes < spiky::densify32_workspace_bytes(n))
+            throw ValueError("densify workspace too small");
+        const hipStream_t st = as_stream(stream);
+        uint32_t *src = static_cast<uint32_t *>(source);
+        if (!counted)
+            check_hip(spiky::launch_densify32_count(src, n, workspace, counter, st), "dense_to_sparse_32");
+        check_hip(spiky::launch_densify32_write(src, n, workspace, indices,
+                                                static_cast<uint32_t *>(values), capacity,
+                                                erase_input != 0, st),
+                  "dense_to_sparse_32");
+    });
+}
+
 int spiky_lut_profiling_stats(const spiky_lut_manager *m, char *buf, uint64_t buf_len) {
     return guarded([&] {
         require_manager(m);

@@ -170,4 +170,17 @@ hipError_t launch_wgrad_sparse(const SparseShape &s, const float *g, const int32
                                float *target, double lr, bool int_mode, double int_rescaler,
                                void *scratch, uint64_t n_synapses, hipStream_t st);
 
+// ---- dense -> sparse compaction of 32-bit words (lut_densify.hip) ---------
+// Workspace (tile counts, then offsets) for a source of n words (n % 4 == 0).
+uint64_t densify32_workspace_bytes(uint64_t n);
+// Counts the non-zero words of src into the workspace and *total (device).
+hipError_t launch_densify32_count(const uint32_t *src, uint64_t n, void *workspace,
+                                  int64_t *total, hipStream_t st);
+// After launch_densify32_count on the same src: writes the non-zero words'
+// indices and values in ascending order (at most `capacity`), zeroing them in
+// src when erase is set.
+hipError_t launch_densify32_write(uint32_t *src, uint64_t n, const void *workspace,
+                                  int64_t *indices, uint32_t *values, uint64_t capacity, bool erase,
+                                  hipStream_t st);
+
 }  // namespace spiky

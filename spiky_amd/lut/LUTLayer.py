@@ -24,6 +24,7 @@ import torch.nn as nn
 
 from .lut_data_manager import LUTDataManagerF, LUTDataManagerI
 from ..util.chunk_of_connections import ChunkOfConnections, repeat_connections_incrementing_source
+from ..util.torch_utils import DenseToSparseConverter
 from ..util.synapse_growth import (Conv2DSynapseGrowthHelper, GivenRectanglesSynapseGrowthHelper,
                                    PointSamplingPolicy, PointSamplingType,
                                    RandomRectanglesSynapseGrowthHelper)
@@ -67,6 +68,9 @@ class LUTSharedContext(object):
 
     def __init__(self, do_asserts=False, _cmp_eps=0.0):
         self._weight_gradients_buffers = []
+        self._densify_indices_buffers = []
+        self._densify_values_buffers = []
+        self._dense_to_sparse_converters = []
         self._device = None
         self._do_asserts = do_asserts
         self._cmp_eps = _cmp_eps
@@ -85,6 +89,27 @@ class LUTSharedContext(object):
         if self._do_asserts:
             assert torch.count_nonzero(buf) == 0
         return buf[:numel]
+
+    def get_dense_to_sparse_converter(self, multi_id=0):
+        """Converter of the Sparse policy's gradients (reference LUTLayer.py:87-94)."""
+        while len(self._dense_to_sparse_converters) <= multi_id:
+            self._dense_to_sparse_converters.append(None)
+        if self._dense_to_sparse_converters[multi_id] is None:
+            self._dense_to_sparse_converters[multi_id] = DenseToSparseConverter()
+        return self._dense_to_sparse_converters[multi_id]
+
+    def get_densify_buffers(self, numel, device, multi_id=0):
+        """(indices int64, values fp32) buffers of at least numel entries
+        (reference LUTLayer.py:96-99)."""
+        if self._device is None:
+            raise RuntimeError('LUTSharedContext device is None, call to_device(...) first')
+        for bufs, dtype in ((self._densify_indices_buffers, torch.int64),
+                            (self._densify_values_buffers, torch.float32)):
+            while len(bufs) <= multi_id:
+                bufs.append(None)
+            if bufs[multi_id] is None or bufs[multi_id].numel() < numel or bufs[multi_id].device != device:
+                bufs[multi_id] = torch.empty([numel], dtype=dtype, device=device)
+        return self._densify_indices_buffers[multi_id], self._densify_values_buffers[multi_id]
 
     def get_cuda_streams(self, device, multi_id=0):
         if device.type != 'cuda':
@@ -105,6 +130,8 @@ class LUTSharedContext(object):
         self._device = dev
         self._weight_gradients_buffers = [None if b is None else b.to(dev)
                                           for b in self._weight_gradients_buffers]
+        self._densify_indices_buffers = [None if b is None else b.to(dev) for b in self._densify_indices_buffers]
+        self._densify_values_buffers = [None if b is None else b.to(dev) for b in self._densify_values_buffers]
         return self
 
 
@@ -362,17 +389,34 @@ class LUTLayerBasic(nn.Module):
         """Kernels are stream-ordered on torch's current stream; nothing to wait for."""
         return None
 
+    def _gradient_densify_buffer_size(self, batch_size):
+        """Densify buffer entries for a batch (reference LUTLayer.py:551-565):
+        the reference's bound, here capped at the gradient's own size, which no
+        count of non-zero words can exceed."""
+        if self._is_fully_connected:
+            per_neuron = self._n_outputs
+        else:
+            per_neuron = self._lut_dm.get_max_forward_groups_per_neuron() * self._forward_group_size
+        n = self._n_detectors * per_neuron * batch_size
+        if self._sequence_length != 1:
+            n *= self._sequence_length * (self._sequence_length - 1) // 2
+        return min(n, ((self._weights.numel() + 3) // 4) * 4)
+
     def _process_gradients(self, target_w_grad, batch_size):
         """Gradient policy post-processing (reference LUTLayer.py:567-609)."""
         if self._weights_gradient_policy.type == GradientType.Sparse:
-            idx = torch.nonzero(target_w_grad, as_tuple=False).flatten()
-            if idx.numel() == 0:
+            converter = self._shared_context.get_dense_to_sparse_converter(self._multi_id)
+            indices, values = converter.dense_to_sparse_32(
+                target_w_grad, erase_input=True,
+                densify_buffers=self._shared_context.get_densify_buffers(
+                    self._gradient_densify_buffer_size(batch_size), self.device, self._multi_id),
+                stream=None, decouple=True)
+            if indices is None:
                 return None
-            values = target_w_grad[idx].clone()
-            target_w_grad[idx] = 0.0
             if self._weights_gradient_policy.normalized:
                 values /= values.abs().max().clip(1e-16)
-            return torch.sparse_coo_tensor(indices=idx.unsqueeze(0), values=values,
+            # the converter's indices ascend, so the tensor is coalesced
+            return torch.sparse_coo_tensor(indices=indices.unsqueeze(0), values=values,
                                            size=self._weights.shape, device=self.device,
                                            check_invariants=False, is_coalesced=True,
                                            requires_grad=False)

@@ -182,3 +182,27 @@ def test_projection_builder_invariants():
         inside = [y * OW + x for y in range(OH) for x in range(OW)
                   if out_mask[y, x] and abs(x - cx) <= pw / 2 and abs(y - cy) <= ph / 2]
         assert set(inside) <= set(base.tolist())
+
+
+def test_densify_validation():
+    """Host-side checks of the dense -> sparse converter (reference
+    torch_utils.py:59-64): they fire before any device work."""
+    from spiky_amd import _native
+    L = _native.lib()
+    # u32 tile offsets (8-byte padded) + u64 chunk offsets (1024 tiles of
+    # 4096 words per chunk) + the total slot
+    assert L.spiky_densify32_workspace_bytes(0) == 8
+    assert L.spiky_densify32_workspace_bytes(4096) == 8 + 16
+    assert L.spiky_densify32_workspace_bytes(4096 * 1025) == 4104 + 24
+    with pytest.raises(ValueError, match="divisable by 4"):
+        _native.check(L.spiky_count_nonzero32(None, 6, None, 0, None, None))
+    with pytest.raises(ValueError, match="divisable by 4"):
+        _native.check(L.spiky_dense_to_sparse32(None, 10, None, None, 0, None, 0, None, 0, 0, None))
+    from spiky_amd.util.torch_utils import DenseToSparseConverter
+    conv = DenseToSparseConverter()
+    with pytest.raises(ValueError, match="element_size == 4"):
+        conv.dense_to_sparse_32(torch.zeros(8, dtype=torch.float64))
+    with pytest.raises(ValueError, match="divisable by 4"):
+        conv.dense_to_sparse_32(torch.zeros(6))
+    with pytest.raises(ValueError, match="GPU device"):
+        conv.dense_to_sparse_32(torch.zeros(8))

@@ -58,6 +58,15 @@ def test_lut_layer_sparse_and_normalized_policies(oracle, cuda_device):
         rwg = np.zeros(T * E * O, np.float32)
         oracle.gather_wgrad_fc(np.ones(B * O, np.float32), ridx, rwg, B, O, T, E)
         got = layer._weights.grad
+        if policy.type == GradientType.Sparse:
+            # the converter's COO output: ascending indices (autograd's
+            # accumulation into .grad does not keep the coalesced flag), and
+            # the shared dense buffer left zeroed for the next step
+            # (erase_input=True)
+            assert got.is_sparse
+            ind = got._indices()[0]
+            assert bool((ind[1:] > ind[:-1]).all())
+            assert torch.count_nonzero(layer._shared_context._weight_gradients_buffers[0]) == 0
         got = got.to_dense() if got.is_sparse else got
         if policy.normalized:
             rwg = rwg / max(np.abs(rwg).max(), 1e-16)

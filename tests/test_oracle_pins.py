@@ -314,3 +314,27 @@ def test_golden_fixtures(oracle):
     wg = np.zeros(T * E * O, np.float32)
     oracle.gather_wgrad_fc(z["g"], idx, wg, B, O, T, E, ogs=int(z["ogs"]))
     assert np.array_equal(wg, z["w_grad"])
+
+
+def test_dense_to_sparse_oracle_pins(oracle):
+    """The converter's selection rule, pinned by the reference docstring's
+    example (torch_utils.py:14-20), the bit-pattern rule of its int4 compare
+    (a float -0.0 is kept, torch_utils_kernels_logic.proto:20-35), int32
+    words, and a brute-force loop on a random array."""
+    idx, val = oracle.dense_to_sparse_32(np.array([1.0, 0.0, 2.0, 0.0, 3.0], np.float32))
+    assert idx.tolist() == [0, 2, 4] and val.tolist() == [1.0, 2.0, 3.0]
+    idx, val = oracle.dense_to_sparse_32(np.array([0.0, -0.0, 0.0, 5.0], np.float32))
+    assert idx.tolist() == [1, 3]
+    assert np.signbit(val[0]) and val[0] == 0.0
+    idx, val = oracle.dense_to_sparse_32(np.array([0, -7, 0, (1 << 31) - 1], np.int32))
+    assert idx.tolist() == [1, 3] and val.tolist() == [-7, (1 << 31) - 1]
+    rng = np.random.default_rng(5)
+    a = rng.random(1000).astype(np.float32)
+    a[a > 0.5] = 0.0
+    a[::37] = -0.0
+    want = [i for i in range(a.size) if a.view(np.uint32)[i] != 0]
+    idx, val = oracle.dense_to_sparse_32(a)
+    assert idx.tolist() == want
+    assert np.array_equal(val.view(np.uint32), a.view(np.uint32)[want])
+    with pytest.raises(ValueError):
+        oracle.dense_to_sparse_32(np.zeros(4, np.float64))
