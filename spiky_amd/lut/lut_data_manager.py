@@ -112,6 +112,37 @@ class _LUTDataManagerBase:
         self._n_synapses = 0
         self._compiled = False
 
+    # ---------------------------------------------------------------- pickling
+    def __getstate__(self):
+        """pickle_lut_neuron_manager (lut.cu:1409-1438): only a manager on the
+        CPU serialises.  The state is this object's build-time record (sizes,
+        synapse metas, connectivity); the native manager is rebuilt from it."""
+        if self._device != -1:
+            raise RuntimeError("net must be on CPU before serialization")
+        return {k: v for k, v in self.__dict__.items() if k != "_h"}
+
+    def __setstate__(self, state):
+        """unpickle_lut_neuron_manager (lut.cu:1440-1473)."""
+        self.__dict__.update(state)
+        L = _native.lib()
+        handle = ctypes.c_void_p()
+        _native.check(L.spiky_lut_create(
+            self._n_inputs, self._n_outputs, self._n_detectors, self._n_anchors,
+            self._sequence_length, self._positional_dim, int(self._args[6]),
+            self._forward_group_size, self._backward_group_size, int(self._int_mode),
+            self._int_rescaler, ctypes.byref(handle)))
+        self._h = handle
+        out = ctypes.c_uint32()
+        for meta in self._metas:
+            _native.check(L.spiky_lut_register_synapse_meta(self._h, *meta, ctypes.byref(out)))
+        if self._fully_connected is not None:
+            _native.check(L.spiky_lut_initialize_neurons(self._h, int(self._fully_connected)))
+        if self._compiled and not self._fully_connected:
+            offs, tg = self._csr
+            _native.check(L.spiky_lut_set_sparse_connectivity(
+                self._h, offs.ctypes.data_as(ctypes.c_void_p),
+                tg.ctypes.data_as(ctypes.c_void_p) if tg.size else None, int(tg.size)))
+
     def __del__(self):
         h = getattr(self, "_h", None)
         if h is not None and h.value:

@@ -36,6 +36,13 @@ class DenseToSparseConverter:
         self._workspace = None
         self._calls = 0
 
+    def __getstate__(self):
+        # the counter and workspace are device caches, rebuilt on first use
+        st = dict(self.__dict__)
+        st["_counter_buffer"] = None
+        st["_workspace"] = None
+        return st
+
     def _ensure(self, source):
         dev = source.device
         if self._counter_buffer is None or self._counter_buffer.device != dev:

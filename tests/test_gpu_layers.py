@@ -183,3 +183,30 @@ def test_config3_full_size(oracle, cuda_device, B):
         r = np.zeros(E * O, np.float32)
         oracle.gather_wgrad_fc(go.cpu().numpy(), idx.view(B, T)[:, t].cpu().numpy().copy(), r, B, O, 1, E)
         assert np.array_equal(wg.view(T, E * O)[t].cpu().numpy(), r)
+
+
+def test_pickle_checkpoint_roundtrip(cuda_device):
+    """A trained layer refuses to pickle on the device (lut.cu:1410-1412); moved
+    to the CPU it pickles, and restored on the device it gives the same
+    outputs and gradients bit for bit."""
+    import pickle
+    dev = cuda_device
+    B, I, T, Nc, O = 32, 96, 64, 5, 24
+    layer = LUTLayer(I, Nc, T, O, random_seed=9).to(dev)
+    with torch.no_grad():
+        layer._weights.normal_(0.0, 0.01)
+    with pytest.raises(RuntimeError, match="net must be on CPU before serialization"):
+        pickle.dumps(layer)
+    x = torch.randn(B, 1, I, device=dev, requires_grad=True)
+    g = torch.randn(B, 1, O, device=dev)
+    y1 = layer(x)
+    y1.backward(g)
+    wg1, xg1 = layer._weights.grad.clone(), x.grad.clone()
+    blob = pickle.dumps(layer.to("cpu"))
+    restored = pickle.loads(blob).to(dev)
+    x.grad = None
+    y2 = restored(x)
+    y2.backward(g)
+    assert torch.equal(y1, y2)
+    assert torch.equal(wg1, restored._weights.grad)
+    assert torch.equal(xg1, x.grad)
