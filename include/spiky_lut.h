@@ -140,6 +140,38 @@ int spiky_lut_backward_backprop_concat(spiky_lut_manager *m, float *weights, uin
                                        float *positional_grad, float *weight_grad,
                                        int overwrite_weight_grad, void *stream);
 
+/* Replaces forward_step_product (lut.cu:847-943 -> lut_runtime.cu:852-1049),
+ * fully connected managers.  The manager is built with sequence_length 1 and
+ * n_inputs = n_inputs_1 + n_inputs_2 + positional_dim; sequence_length is the
+ * real one.  Every pair i < j of a sequence looks up each table over the
+ * virtual row [input_1[i] | input_2[j] | pe[(j-i-1)*T + t]] (sliced_mode:
+ * interleaved, virtual id = 3 * k + source).  output [B*S*O] is summed into
+ * (int32 summation: the caller zeroes it; it is converted to float here).
+ * positional_embeddings [(S-1)*T*pd] when positional_dim > 0.  Anchor ids
+ * beyond the virtual row are skipped like unused (-1) ones. */
+int spiky_lut_forward_step_product(spiky_lut_manager *m, const float *weights, uint32_t batch_size,
+                                   uint32_t sequence_length, const float *input_1,
+                                   const float *input_2, const int32_t *anchors, float *output,
+                                   uint32_t n_inputs_1, uint32_t n_inputs_2, int sliced_mode,
+                                   float cmp_eps, const float *positional_embeddings, void *stream);
+
+/* Replaces backward_backprop_product (lut.cu:945-1039 -> lut_runtime.cu:
+ * 1051-1456).  input_grad_1/2 [B*S*n] may be the same buffer (the layer passes
+ * one x twice).  external_lr >= 0 (GradientType.Internal) updates the weights
+ * in place with lr * -external_lr and needs weight_grad == NULL; otherwise
+ * weight_grad [T*E*O] is summed into with lr.  positional_grad [(S-1)*T*pd]
+ * when positional_dim > 0.  int32 summation converts every buffer it summed
+ * into to float at the end (lut_runtime.cu:1405-1456). */
+int spiky_lut_backward_backprop_product(spiky_lut_manager *m, float *weights, uint32_t batch_size,
+                                        uint32_t sequence_length, const float *input_1,
+                                        const float *input_2, const int32_t *anchors,
+                                        const float *output_grad, float *input_grad_1,
+                                        float *input_grad_2, double external_lr,
+                                        uint32_t n_inputs_1, uint32_t n_inputs_2, int sliced_mode,
+                                        float cmp_eps, float *weight_grad,
+                                        const float *positional_embeddings, float *positional_grad,
+                                        void *stream);
+
 /* Replaces add_lookup_connections + compile for sparse managers
  * (lut.cu:560-627) with this build's CSR: lookup neuron n owns synapses
  * [syn_offsets[n], syn_offsets[n+1]) whose targets are output indices in

@@ -67,6 +67,16 @@ def lib():
                                            _i64, _int, _f64, _vp, _vp]
         L.oracle_gather_wgrad_seq.argtypes = [_f32p, _i32p, _vp, _f32p, _i64, _i64, _i64, _i64, _i64,
                                               _i64, _i64, _f32, _f32, _int, _f64]
+        L.oracle_fill_outputs_product.argtypes = [_f32p, _f32p, _vp, _i32p, _f32p, _i64, _i64, _i64, _i64,
+                                                  _i64, _i64, _i64, _i64, _int, _f32, _int, _f64, _f32p]
+        L.oracle_propagate_product.argtypes = [_f32p, _f32p, _vp, _i32p, _f32p, _f32p, _i64, _i64, _i64,
+                                               _i64, _i64, _i64, _i64, _i64, _int, _f32, _f64, _int, _f64,
+                                               _f32p, _f32p, _vp, _vp]
+        L.oracle_fill_outputs_product64.argtypes = [_f32p, _f32p, _vp, _i32p, _f32p, _i64, _i64, _i64,
+                                                    _i64, _i64, _i64, _i64, _i64, _int, _f32, _vp, _vp]
+        L.oracle_propagate_product64.argtypes = [_f32p, _f32p, _vp, _i32p, _f32p, _f32p, _i64, _i64,
+                                                 _i64, _i64, _i64, _i64, _i64, _i64, _int, _f32, _f64,
+                                                 _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
         _lib = L
     return _lib
 
@@ -253,3 +263,79 @@ def dense_to_sparse_32(source):
     bits = src.view(np.uint32)
     idx = np.flatnonzero(bits).astype(np.int64)
     return idx, src[idx].copy()
+
+
+def fill_outputs_product(x1, x2, pe, anchors, w, batch, seq_len, n1, n2, pd, n_detectors, n_anchors,
+                         n_outputs, sliced=False, cmp_eps=0.0, int_mode=False, int_rescaler=1.0,
+                         out=None):
+    """Product-mode forward (fill_outputs_product_cpu_logic, proto:2148-2264):
+    out [B*S*O] accumulated into; x1 [B*S*n1], x2 [B*S*n2], pe [(S-1)*T*pd] or
+    None, anchors int32 pairs [T*Nc*2] (-1 = unused) over the virtual row."""
+    if out is None:
+        out = np.zeros(batch * seq_len * n_outputs, dtype=np.float32)
+    pe = None if pe is None or pd == 0 else _c(pe, np.float32)
+    lib().oracle_fill_outputs_product(_c(x1, np.float32), _c(x2, np.float32), _ptr(pe),
+                                      _c(anchors, np.int32), _c(w, np.float32), batch, seq_len, n1,
+                                      n2, pd, n_detectors, n_anchors, n_outputs, int(sliced),
+                                      float(cmp_eps), int(int_mode), float(int_rescaler), out)
+    return out
+
+
+def propagate_product(x1, x2, pe, anchors, w, g, batch, seq_len, n1, n2, pd, n_detectors, n_anchors,
+                      n_outputs, sliced=False, cmp_eps=0.0, lr=1.0, int_mode=False,
+                      int_rescaler=1.0, x_grad=None, pe_grad=None, w_grad=None, same_x=True):
+    """Product-mode backward (propagate_backward_product_cpu_logic,
+    proto:2396-2628).  With same_x (the layer's call: x1 is x2) both roles
+    accumulate into one x_grad [B*S*n1]; returns (x_grad, pe_grad, w_grad)
+    (x2_grad appended when not same_x).  w_grad None skips the weight
+    gradient (Internal policy)."""
+    if x_grad is None:
+        x_grad = np.zeros(batch * seq_len * n1, dtype=np.float32)
+    x2_grad = x_grad if same_x else np.zeros(batch * seq_len * n2, dtype=np.float32)
+    if pe_grad is None and pd > 0:
+        pe_grad = np.zeros((seq_len - 1) * n_detectors * pd, dtype=np.float32)
+    pe = None if pe is None or pd == 0 else _c(pe, np.float32)
+    lib().oracle_propagate_product(_c(x1, np.float32), _c(x2, np.float32), _ptr(pe),
+                                   _c(anchors, np.int32), _c(w, np.float32), _c(g, np.float32), batch,
+                                   seq_len, n1, n2, pd, n_detectors, n_anchors, n_outputs, int(sliced),
+                                   float(cmp_eps), float(lr), int(int_mode), float(int_rescaler),
+                                   x_grad, x2_grad, _ptr(pe_grad), _ptr(w_grad))
+    if same_x:
+        return x_grad, pe_grad, w_grad
+    return x_grad, pe_grad, w_grad, x2_grad
+
+
+def fill_outputs_product64(x1, x2, pe, anchors, w, batch, seq_len, n1, n2, pd, n_detectors, n_anchors,
+                           n_outputs, sliced=False, cmp_eps=0.0):
+    """fp64 mode of fill_outputs_product: (sum, abs) of the reference's terms
+    per output, in float64.  Any fp32 summation order of n terms lies within
+    n * 2^-24 * abs of sum (the tolerance of an order-free GPU sum)."""
+    m = batch * seq_len * n_outputs
+    tot, mag = np.zeros(m), np.zeros(m)
+    pe = None if pe is None or pd == 0 else _c(pe, np.float32)
+    lib().oracle_fill_outputs_product64(_c(x1, np.float32), _c(x2, np.float32), _ptr(pe),
+                                        _c(anchors, np.int32), _c(w, np.float32), batch, seq_len, n1,
+                                        n2, pd, n_detectors, n_anchors, n_outputs, int(sliced),
+                                        float(cmp_eps), _ptr(tot), _ptr(mag))
+    return tot, mag
+
+
+def propagate_product64(x1, x2, pe, anchors, w, g, batch, seq_len, n1, n2, pd, n_detectors, n_anchors,
+                        n_outputs, sliced=False, cmp_eps=0.0, lr=1.0, weights=True):
+    """fp64 mode of propagate_product with x1 is x2 (the layer's call):
+    returns {"x", "pe", "w"} -> (sum, abs) of the terms ((float)du pushes,
+    (float)(g*lr) gradient terms); "w" is None when weights is False."""
+    nx = batch * seq_len * n1
+    x_s, x_a = np.zeros(nx), np.zeros(nx)
+    npe = (seq_len - 1) * n_detectors * pd
+    pe_s, pe_a = (np.zeros(npe), np.zeros(npe)) if pd > 0 else (None, None)
+    nw = (n_detectors << n_anchors) * n_outputs
+    w_s, w_a = (np.zeros(nw), np.zeros(nw)) if weights else (None, None)
+    pe = None if pe is None or pd == 0 else _c(pe, np.float32)
+    lib().oracle_propagate_product64(_c(x1, np.float32), _c(x2, np.float32), _ptr(pe),
+                                     _c(anchors, np.int32), _c(w, np.float32), _c(g, np.float32), batch,
+                                     seq_len, n1, n2, pd, n_detectors, n_anchors, n_outputs, int(sliced),
+                                     float(cmp_eps), float(lr), _ptr(x_s), _ptr(x_a), _ptr(x_s),
+                                     _ptr(x_a), _ptr(pe_s), _ptr(pe_a), _ptr(w_s), _ptr(w_a))
+    return {"x": (x_s, x_a), "pe": (pe_s, pe_a) if pd > 0 else None,
+            "w": (w_s, w_a) if weights else None}

@@ -594,3 +594,222 @@ void oracle_gather_wgrad_seq(
         }
     });
 }
+
+/* ------------------------------------------------------------------------ */
+/* Product mode (concatenation_product == False): every causal pair i < j   */
+/* of a sequence is one LUT lookup over the virtual input row               */
+/* [x1[i] (n1) | x2[j] (n2) | pe[j-i-1][t] (pd)] (or, in sliced mode, the   */
+/* interleaving x1[0] x2[0] pe[0] x1[1] ...), with per-detector positional  */
+/* slices pe[(j-i-1)*T + t][pd].  Restated from                             */
+/* calculate_product_lookup_index(_backprop), proto:32-181,                 */
+/* fill_outputs_product_cpu_logic proto:2148-2264,                          */
+/* propagate_backward_product_cpu_logic proto:2396-2628 with                */
+/* propagate_through_detector_product proto:869-1023, accumulate_grad_sum_fc */
+/* (CPU branch) proto:397-472 and gather_weight_gradients_fc proto:716-790, */
+/* in the serial order of misc.h:119-129 (b, then j*T + t, then i).          */
+/* ------------------------------------------------------------------------ */
+static inline float prod_value(const float *x1, const float *x2, const float *pe, int64_t n1,
+                               int64_t n2, int sliced, int32_t id, int *source, int64_t *index)
+{
+    if (sliced) {
+        const int c = id % 3;
+        const int64_t k = id / 3;
+        *source = c;
+        *index = k;
+        return c == 0 ? x1[k] : (c == 1 ? x2[k] : pe[k]);
+    }
+    if (id < n1) { *source = 0; *index = id; return x1[id]; }
+    if (id < n1 + n2) { *source = 1; *index = id - n1; return x2[id - n1]; }
+    *source = 2;
+    *index = id - n1 - n2;
+    return pe[id - n1 - n2];
+}
+
+typedef struct {
+    int32_t idx, alt;
+    float md;
+    int src1, src2;
+    int64_t k1, k2;
+} prod_pair;
+
+/* lookup index, and the min-margin anchor of calculate_product_lookup_index_backprop:
+ * strict |delta| < |min| from FLT_MAX (the first of equal margins wins) */
+static prod_pair prod_lookup(const float *x1, const float *x2, const float *pe,
+                             const int32_t *anc, int64_t n_anchors, int64_t n1, int64_t n2,
+                             int sliced, float cmp_eps)
+{
+    prod_pair p;
+    p.idx = 0; p.alt = 0; p.md = 3.402823466e+38f; p.src1 = -1; p.src2 = -1; p.k1 = 0; p.k2 = 0;
+    int32_t flip = -1;
+    for (int64_t k = 0; k < n_anchors; k++) {
+        const int32_t a1 = anc[2 * k], a2 = anc[2 * k + 1];
+        if (a1 < 0 || a2 < 0) continue; /* unused pair */
+        int s1, s2;
+        int64_t i1, i2;
+        const float v1 = prod_value(x1, x2, pe, n1, n2, sliced, a1, &s1, &i1);
+        const float v2 = prod_value(x1, x2, pe, n1, n2, sliced, a2, &s2, &i2);
+        const float d = v1 - v2;
+        if (rounded_greater0(d, cmp_eps)) p.idx |= (1 << k);
+        if (fabsf(d) < fabsf(p.md)) {
+            p.md = d; flip = (int32_t)k; p.src1 = s1; p.src2 = s2; p.k1 = i1; p.k2 = i2;
+        }
+    }
+    p.alt = flip >= 0 ? (p.idx ^ (1 << flip)) : p.idx;
+    return p;
+}
+
+/* The fp64 mode of the product oracle (a test tolerance aid, not a
+ * restatement): every term the reference adds -- the weight payload row[c],
+ * the pushes (float)du and -(float)du, the gradient term (float)(g*lr) -- is
+ * summed in fp64 into *_sum, and its magnitude into *_abs.  Any fp32 summation
+ * order of n such terms lies within n * 2^-24 * abs of sum.  NULL = off. */
+typedef struct {
+    double *x1_sum, *x1_abs, *x2_sum, *x2_abs, *pe_sum, *pe_abs, *w_sum, *w_abs;
+} prod_acc64;
+
+static inline void acc64_add(double *sum, double *abs_, int64_t i, double v)
+{
+    sum[i] += v;
+    abs_[i] += fabs(v);
+}
+
+static void fill_outputs_product_core(
+    const float *x1, const float *x2, const float *pe, const int32_t *anchors, const float *w,
+    int64_t batch, int64_t seq_len, int64_t n1, int64_t n2, int64_t pd, int64_t n_detectors,
+    int64_t n_anchors, int64_t n_outputs, int sliced, float cmp_eps, int int_mode,
+    double int_rescaler, float *out, double *out_sum, double *out_abs)
+{
+    const int64_t E = (int64_t)1 << n_anchors;
+    for (int64_t b = 0; b < batch; b++)
+        for (int64_t j = 0; j < seq_len; j++)
+            for (int64_t t = 0; t < n_detectors; t++)
+                for (int64_t i = 0; i < j; i++) {
+                    const float *pet = pd > 0 ? pe + ((j - i - 1) * n_detectors + t) * pd : NULL;
+                    const prod_pair p = prod_lookup(x1 + (b * seq_len + i) * n1, x2 + (b * seq_len + j) * n2,
+                                                    pet, anchors + t * n_anchors * 2, n_anchors, n1, n2,
+                                                    sliced, cmp_eps);
+                    const float *row = w + (t * E + p.idx) * n_outputs;
+                    const int64_t o0 = (b * seq_len + j) * n_outputs;
+                    for (int64_t c = 0; c < n_outputs; c++) {
+                        if (out_sum)
+                            acc64_add(out_sum, out_abs, o0 + c, (double)row[c]);
+                        else if (int_mode)
+                            as_i32(out + o0)[c] = wrap_add(as_i32(out + o0)[c],
+                                                           (int32_t)((double)row[c] * OR_DENOM32 * int_rescaler));
+                        else
+                            out[o0 + c] += row[c];
+                    }
+                }
+}
+
+void oracle_fill_outputs_product(
+    const float *x1, const float *x2, const float *pe, const int32_t *anchors, const float *w,
+    int64_t batch, int64_t seq_len, int64_t n1, int64_t n2, int64_t pd, int64_t n_detectors,
+    int64_t n_anchors, int64_t n_outputs, int sliced, float cmp_eps, int int_mode,
+    double int_rescaler, float *out)
+{
+    fill_outputs_product_core(x1, x2, pe, anchors, w, batch, seq_len, n1, n2, pd, n_detectors,
+                              n_anchors, n_outputs, sliced, cmp_eps, int_mode, int_rescaler, out,
+                              NULL, NULL);
+}
+
+void oracle_fill_outputs_product64(
+    const float *x1, const float *x2, const float *pe, const int32_t *anchors, const float *w,
+    int64_t batch, int64_t seq_len, int64_t n1, int64_t n2, int64_t pd, int64_t n_detectors,
+    int64_t n_anchors, int64_t n_outputs, int sliced, float cmp_eps, double *out_sum,
+    double *out_abs)
+{
+    fill_outputs_product_core(x1, x2, pe, anchors, w, batch, seq_len, n1, n2, pd, n_detectors,
+                              n_anchors, n_outputs, sliced, cmp_eps, 0, 1.0, NULL, out_sum, out_abs);
+}
+
+static inline void prod_push(float *dst, double du, int int_mode, double int_rescaler)
+{
+    if (int_mode)
+        *as_i32(dst) = wrap_add(*as_i32(dst), (int32_t)(du * OR_DENOM32 * int_rescaler));
+    else
+        *dst += (float)du;
+}
+
+static void propagate_product_core(
+    const float *x1, const float *x2, const float *pe, const int32_t *anchors, const float *w,
+    const float *g, int64_t batch, int64_t seq_len, int64_t n1, int64_t n2, int64_t pd,
+    int64_t n_detectors, int64_t n_anchors, int64_t n_outputs, int sliced, float cmp_eps,
+    double lr, int int_mode, double int_rescaler, float *x1_grad, float *x2_grad, float *pe_grad,
+    float *w_grad, const prod_acc64 *acc)
+{
+    const int64_t E = (int64_t)1 << n_anchors;
+    for (int64_t b = 0; b < batch; b++)
+        for (int64_t j = 0; j < seq_len; j++)
+            for (int64_t t = 0; t < n_detectors; t++)
+                for (int64_t i = 0; i < j; i++) {
+                    const int64_t pe_off = ((j - i - 1) * n_detectors + t) * pd;
+                    const prod_pair p = prod_lookup(x1 + (b * seq_len + i) * n1, x2 + (b * seq_len + j) * n2,
+                                                    pd > 0 ? pe + pe_off : NULL, anchors + t * n_anchors * 2,
+                                                    n_anchors, n1, n2, sliced, cmp_eps);
+                    const float *gj = g + (b * seq_len + j) * n_outputs;
+                    if (p.src1 >= 0) {
+                        double ms = 0.0, as = 0.0;
+                        const float *rm = w + (t * E + p.idx) * n_outputs;
+                        const float *ra = w + (t * E + p.alt) * n_outputs;
+                        for (int64_t c = 0; c < n_outputs; c++) ms += (double)rm[c] * (double)gj[c];
+                        for (int64_t c = 0; c < n_outputs; c++) as += (double)ra[c] * (double)gj[c];
+                        const double du = du_of_margin(p.md) * (ms - as);
+                        if (fabs(du) > OR_EPS) {
+                            const int64_t base[3] = {(b * seq_len + i) * n1, (b * seq_len + j) * n2, pe_off};
+                            if (acc) {
+                                double *sums[3] = {acc->x1_sum, acc->x2_sum, acc->pe_sum};
+                                double *abss[3] = {acc->x1_abs, acc->x2_abs, acc->pe_abs};
+                                if (sums[p.src1]) acc64_add(sums[p.src1], abss[p.src1], base[p.src1] + p.k1, (double)(float)du);
+                                if (sums[p.src2]) acc64_add(sums[p.src2], abss[p.src2], base[p.src2] + p.k2, (double)(float)-du);
+                            } else {
+                                float *dst[3] = {x1_grad, x2_grad, pe_grad};
+                                if (dst[p.src1]) prod_push(dst[p.src1] + base[p.src1] + p.k1, du, int_mode, int_rescaler);
+                                if (dst[p.src2]) prod_push(dst[p.src2] + base[p.src2] + p.k2, -du, int_mode, int_rescaler);
+                            }
+                        }
+                    }
+                    if (acc ? acc->w_sum != NULL : w_grad != NULL) {
+                        const int64_t r0 = (t * E + p.idx) * n_outputs;
+                        for (int64_t c = 0; c < n_outputs; c++) {
+                            const double gg = (double)gj[c];
+                            if (!(fabs(gg) > OR_EPS)) continue;
+                            if (acc)
+                                acc64_add(acc->w_sum, acc->w_abs, r0 + c, (double)(float)(gg * lr));
+                            else if (int_mode)
+                                as_i32(w_grad + r0)[c] = wrap_add(as_i32(w_grad + r0)[c], (int32_t)(gg * lr * OR_DENOM32 * int_rescaler));
+                            else
+                                w_grad[r0 + c] += (float)(gg * lr);
+                        }
+                    }
+                }
+}
+
+/* x1_grad / x2_grad may alias (the layer passes one x and one x_grad twice);
+ * w_grad may be NULL (Internal policy: no weight gradient in this pass). */
+void oracle_propagate_product(
+    const float *x1, const float *x2, const float *pe, const int32_t *anchors, const float *w,
+    const float *g, int64_t batch, int64_t seq_len, int64_t n1, int64_t n2, int64_t pd,
+    int64_t n_detectors, int64_t n_anchors, int64_t n_outputs, int sliced, float cmp_eps,
+    double lr, int int_mode, double int_rescaler, float *x1_grad, float *x2_grad, float *pe_grad,
+    float *w_grad)
+{
+    propagate_product_core(x1, x2, pe, anchors, w, g, batch, seq_len, n1, n2, pd, n_detectors,
+                           n_anchors, n_outputs, sliced, cmp_eps, lr, int_mode, int_rescaler,
+                           x1_grad, x2_grad, pe_grad, w_grad, NULL);
+}
+
+/* fp64 mode of oracle_propagate_product (see prod_acc64); any pair of
+ * sum/abs pointers may be NULL, and x1_* / x2_* may alias. */
+void oracle_propagate_product64(
+    const float *x1, const float *x2, const float *pe, const int32_t *anchors, const float *w,
+    const float *g, int64_t batch, int64_t seq_len, int64_t n1, int64_t n2, int64_t pd,
+    int64_t n_detectors, int64_t n_anchors, int64_t n_outputs, int sliced, float cmp_eps,
+    double lr, double *x1_sum, double *x1_abs, double *x2_sum, double *x2_abs, double *pe_sum,
+    double *pe_abs, double *w_sum, double *w_abs)
+{
+    const prod_acc64 acc = {x1_sum, x1_abs, x2_sum, x2_abs, pe_sum, pe_abs, w_sum, w_abs};
+    propagate_product_core(x1, x2, pe, anchors, w, g, batch, seq_len, n1, n2, pd, n_detectors,
+                           n_anchors, n_outputs, sliced, cmp_eps, lr, 0, 1.0, NULL, NULL, NULL, NULL,
+                           &acc);
+}

@@ -59,6 +59,11 @@ _OPTIONAL_SIGNATURES = {
         [_vp, _vp, _u32, _vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i32),
     "spiky_lut_backward_backprop_concat": (
         [_vp, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _vp, _f64, _vp, _vp, _vp, _vp, _vp, _i32, _vp], _i32),
+    "spiky_lut_forward_step_product": (
+        [_vp, _vp, _u32, _u32, _vp, _vp, _vp, _vp, _u32, _u32, _i32, _f32, _vp, _vp], _i32),
+    "spiky_lut_backward_backprop_product": (
+        [_vp, _vp, _u32, _u32, _vp, _vp, _vp, _vp, _vp, _vp, _f64, _u32, _u32, _i32, _f32, _vp, _vp,
+         _vp, _vp], _i32),
 }
 
 

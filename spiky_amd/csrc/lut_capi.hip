@@ -735,6 +735,132 @@ int spiky_lut_backward_backprop_concat(spiky_lut_manager *m, float *weights, uin
     });
 }
 
+// Product mode: the manager is built with sequence_length 1 and n_inputs
+// 2 * n + pd; the real sequence length comes with each call (lut.cu:880-887).
+static spiky::ProductShape product_shape(const spiky_lut_manager *m, uint32_t batch_size,
+                                         uint32_t sequence_length, uint32_t n_inputs_1,
+                                         uint32_t n_inputs_2, int sliced_mode, float cmp_eps,
+                                         const char *what) {
+    if (batch_size == 0) throw ValueError("batch_size == 0");
+    if (m->sequence_length != 1)
+        throw ValueError(std::string(what) +
+                         ": this is an experimental method, this->sequence_length should be equal to "
+                         "1, real length of the sequence is passed as the method parameter");
+    if (sequence_length == 0) throw ValueError("sequence_length == 0");
+    require_initialized(m);
+    if (m->fully_connected != 1)
+        throw ValueError("product mode is built for fully connected managers only");
+    spiky::ProductShape s;
+    s.batch = batch_size;
+    s.seq_len = sequence_length;
+    s.n1 = n_inputs_1;
+    s.n2 = n_inputs_2;
+    s.pd = m->positional_dim;
+    s.n_detectors = m->n_detectors;
+    s.n_anchors = m->n_anchors;
+    s.n_outputs = m->n_outputs;
+    s.sliced = sliced_mode != 0;
+    s.cmp_eps = cmp_eps;
+    if (!spiky::product_applies(s))
+        throw ValueError("product mode shape out of range (n_detectors * 2^n_anchors must be <= 16384, "
+                         "batch_size * sequence_length <= 4194240)");
+    return s;
+}
+
+int spiky_lut_forward_step_product(spiky_lut_manager *m, const float *weights, uint32_t batch_size,
+                                   uint32_t sequence_length, const float *input_1,
+                                   const float *input_2, const int32_t *anchors, float *output,
+                                   uint32_t n_inputs_1, uint32_t n_inputs_2, int sliced_mode,
+                                   float cmp_eps, const float *positional_embeddings,
+                                   void *stream) {
+    return guarded([&] {
+        require_manager(m);
+        const spiky::ProductShape s = product_shape(m, batch_size, sequence_length, n_inputs_1,
+                                                    n_inputs_2, sliced_mode, cmp_eps,
+                                                    "forward_step_product");
+        if (!weights || !input_1 || !input_2 || !anchors || !output)
+            throw ValueError("null tensor pointer");
+        if (s.pd > 0 && !positional_embeddings)
+            throw ValueError("r_positional_embeddings must be provided when positional_dim > 0");
+        ScopedTimer timer(m->stats, "lut::runtime::forward_product");
+        m->context_active = true;
+        const hipStream_t st = as_stream(stream);
+        void *scr = m->scratch_fwd.ensure(spiky::product_scratch_bytes(s, false));
+        m->timed("fill_outputs_product", st, [&] {
+            check_hip(spiky::launch_forward_product(s, weights, input_1, input_2,
+                                                    positional_embeddings, anchors, output,
+                                                    m->int_mode, m->int_rescaler, scr, st),
+                      "forward_step_product");
+        });
+        if (m->int_mode)
+            check_hip(spiky::launch_convert_i2f(output, (uint64_t)s.batch * s.seq_len * s.n_outputs,
+                                                m->int_rescaler, st),
+                      "convert_integers_to_floats");
+    });
+}
+
+int spiky_lut_backward_backprop_product(spiky_lut_manager *m, float *weights, uint32_t batch_size,
+                                        uint32_t sequence_length, const float *input_1,
+                                        const float *input_2, const int32_t *anchors,
+                                        const float *output_grad, float *input_grad_1,
+                                        float *input_grad_2, double external_lr,
+                                        uint32_t n_inputs_1, uint32_t n_inputs_2, int sliced_mode,
+                                        float cmp_eps, float *weight_grad,
+                                        const float *positional_embeddings, float *positional_grad,
+                                        void *stream) {
+    return guarded([&] {
+        require_manager(m);
+        if (batch_size == 0) throw ValueError("batch_size == 0");
+        if (!m->context_active) throw ValueError("no active context");
+        const spiky::ProductShape s = product_shape(m, batch_size, sequence_length, n_inputs_1,
+                                                    n_inputs_2, sliced_mode, cmp_eps,
+                                                    "backward_backprop_product");
+        // lut_runtime.cu:1075-1077
+        if (external_lr >= 0.0 && weight_grad != nullptr)
+            throw ValueError("in internal weight gradients mode w_weights_gradients should be nullptr");
+        if (external_lr >= 0.0 && m->int_mode)
+            throw ValueError("summation dtype torch.int32 can't be combined with GradientType.Internal");
+        if (!weights || !input_1 || !input_2 || !anchors || !output_grad || !input_grad_1 ||
+            !input_grad_2)
+            throw ValueError("null tensor pointer");
+        if (s.pd > 0 && (!positional_embeddings || !positional_grad))
+            throw ValueError("positional embeddings and their gradients must be provided when positional_dim > 0");
+        ScopedTimer timer(m->stats, "lut::runtime::backward_product");
+        const hipStream_t st = as_stream(stream);
+        double lr = (double)m->metas[0][0];
+        if (external_lr >= 0.0) lr *= -external_lr;
+        float *target = (external_lr >= 0.0) ? weights : weight_grad;
+        void *scr = m->scratch.ensure(spiky::product_scratch_bytes(s, true));
+        m->timed("backward_product", st, [&] {
+            check_hip(spiky::launch_backward_product(s, weights, input_1, input_2,
+                                                     positional_embeddings, anchors, output_grad,
+                                                     input_grad_1, input_grad_2, positional_grad,
+                                                     target, lr, m->int_mode, m->int_rescaler, scr,
+                                                     st),
+                      "backward_backprop_product");
+        });
+        if (m->int_mode) {
+            // lut_runtime.cu:1405-1456: every buffer this call summed into
+            const uint64_t bs = (uint64_t)s.batch * s.seq_len;
+            check_hip(spiky::launch_convert_i2f(input_grad_1, bs * s.n1, m->int_rescaler, st),
+                      "convert_integers_to_floats");
+            if (input_grad_2 != input_grad_1)
+                check_hip(spiky::launch_convert_i2f(input_grad_2, bs * s.n2, m->int_rescaler, st),
+                          "convert_integers_to_floats");
+            if (weight_grad)
+                check_hip(spiky::launch_convert_i2f(weight_grad,
+                                                    (uint64_t)m->n_lookup * m->n_outputs,
+                                                    m->int_rescaler, st),
+                          "convert_integers_to_floats");
+            if (s.pd > 0)
+                check_hip(spiky::launch_convert_i2f(
+                              positional_grad, (uint64_t)s.pd * s.n_detectors * (s.seq_len - 1),
+                              m->int_rescaler, st),
+                          "convert_integers_to_floats");
+        }
+    });
+}
+
 int spiky_lut_decode_anchors_compact(const uint32_t *encoded_pairs, uint32_t n_detectors,
                                      uint32_t max_pairs_per_detector, uint32_t n_anchors,
                                      const int64_t *in_offsets, const int32_t *in_ids,

@@ -170,6 +170,29 @@ hipError_t launch_wgrad_sparse(const SparseShape &s, const float *g, const int32
                                float *target, double lr, bool int_mode, double int_rescaler,
                                void *scratch, uint64_t n_synapses, hipStream_t st);
 
+// ---- product mode (concatenation_product == False, lut_product.hip) ---------
+struct ProductShape {
+    uint32_t batch, seq_len, n1, n2, pd, n_detectors, n_anchors, n_outputs;
+    bool sliced;
+    float cmp_eps;
+};
+bool product_applies(const ProductShape &s);
+size_t product_scratch_bytes(const ProductShape &s, bool backward);
+// out (+)= sum over pairs i < j and tables of W[t][lookup]; int32 payloads
+// when int_mode (the caller converts).
+hipError_t launch_forward_product(const ProductShape &s, const float *w, const float *x1,
+                                  const float *x2, const float *pe, const int32_t *anchors,
+                                  float *out, bool int_mode, double int_rescaler, void *scratch,
+                                  hipStream_t st);
+// Input, positional and (target != null) weight gradients; x1_grad may alias
+// x2_grad.  target gets lr * g terms (weight gradient, or the weights
+// themselves with lr = meta lr * -external lr for the Internal policy).
+hipError_t launch_backward_product(const ProductShape &s, const float *w, const float *x1,
+                                   const float *x2, const float *pe, const int32_t *anchors,
+                                   const float *g, float *x1_grad, float *x2_grad, float *pe_grad,
+                                   float *target, double lr, bool int_mode, double int_rescaler,
+                                   void *scratch, hipStream_t st);
+
 // ---- dense -> sparse compaction of 32-bit words (lut_densify.hip) ---------
 // Workspace (tile counts, then offsets) for a source of n words (n % 4 == 0).
 uint64_t densify32_workspace_bytes(uint64_t n);

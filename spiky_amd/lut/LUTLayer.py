@@ -12,7 +12,9 @@ Changed, on purpose:
     LUTLayer.py:539-549);
   * the Dense weight gradient is written, not accumulated, so it needs no
     zeros_like pass (LUTLayer.py:864) -- same values;
-  * the detector anchors are a registered buffer (they travel with state_dict).
+  * the detector anchors are a registered buffer (they travel with state_dict);
+  * in product mode lut_shape() counts the 2^n_anchors rows each table has
+    (the reference's Conv2DLUTLayer counts 4^n_anchors there, LUTLayer.py:1299).
 """
 from dataclasses import dataclass
 from enum import Enum
@@ -189,10 +191,15 @@ class LUTLayerBasic(nn.Module):
         self._multi_id = 0
         if self._sequence_length == 1 and not concatenation_product:
             raise ValueError("concatenation_product == False doesn't make sense with sequence_length == 1")
-        if not concatenation_product:
-            raise NotImplementedError("product mode (concatenation_product=False) is not part of this build")
         self._concatenation_product = concatenation_product
         self._sliced_product_mode = sliced_product_mode
+        if self._sliced_product_mode and concatenation_product:
+            raise ValueError("sliced_product_mode == True doesn't make sense in concatenation product mode")
+        if self._sliced_product_mode and n_inputs != positional_dim:
+            raise ValueError("if sliced_product_mode == True then n_inputs and positional_dim should be equal")
+        if not concatenation_product and not is_fully_connected:
+            raise NotImplementedError("product mode (concatenation_product=False) is built for fully "
+                                      "connected lookup tables only")
         self._unified_positional_embeddings = unified_pe
         if shared_context is None:
             self._own_shared_context = True
@@ -214,7 +221,11 @@ class LUTLayerBasic(nn.Module):
         if _initial_synapse_capacity is None:
             _initial_synapse_capacity = LUTLayerBasic.n_lut_channels(
                 n_anchors_per_detector, sequence_length, concatenation_product) * n_detectors * n_outputs
-        args = (n_inputs, n_outputs, n_detectors, n_anchors_per_detector, sequence_length,
+        # product mode: the manager sees one virtual row [x_i | x_j | pe] per
+        # pair and a sequence length of 1 (reference LUTLayer.py:306-324)
+        n_virtual = n_inputs if concatenation_product else 2 * n_inputs + (positional_dim or 0)
+        args = (n_virtual, n_outputs, n_detectors, n_anchors_per_detector,
+                sequence_length if concatenation_product else 1,
                 positional_dim if positional_dim is not None else 0, _initial_synapse_capacity,
                 _forward_group_size, _backward_group_size)
         if summation_dtype == torch.float32:
@@ -230,8 +241,8 @@ class LUTLayerBasic(nn.Module):
                 initial_weight=sm.initial_weight)
             assert m_id == i
         self._lut_dm.initialize_neurons(is_fully_connected)
-        self._input_neuron_ids = torch.arange(0, self._n_inputs, dtype=torch.int32)
-        self._detector_neuron_ids = torch.arange(self._n_inputs, self._n_inputs + self._n_detectors,
+        self._input_neuron_ids = torch.arange(0, n_virtual, dtype=torch.int32)
+        self._detector_neuron_ids = torch.arange(n_virtual, n_virtual + self._n_detectors,
                                                  dtype=torch.int32)
         self._lookup_neuron_ids = torch.arange(0, self._n_lookup_neurons, dtype=torch.int32)
         self._output_neuron_ids = torch.arange(self._n_lookup_neurons,
@@ -251,7 +262,8 @@ class LUTLayerBasic(nn.Module):
         """Every detector reads every input: the FC receptive field, set directly
         (the growth engine would produce exactly these ascending lists)."""
         dm = self._lut_dm
-        dm._detector_inputs = [list(range(self._n_inputs)) for _ in range(self._n_detectors)]
+        n = self._input_neuron_ids.numel()
+        dm._detector_inputs = [list(range(n)) for _ in range(self._n_detectors)]
 
     def initialize_detectors(self, compact_mode=True, seed=None):
         """Anchors from torch-generated pair codes (reference LUTLayer.py:373-407)."""
@@ -602,6 +614,72 @@ class LUTLayerBasic(nn.Module):
         result = () if external_output else (x_grad.view(source_x_shape),)
         return result + (target_w_grad, positional_grad)
 
+    def forward_step_product(self, x, pos_embeddings, output=None):
+        """Product-mode forward (reference LUTLayer.py:779-821): every pair
+        i < j of a sequence is one lookup per table over [x_i | x_j | pe]."""
+        if not (len(x.shape) == len(self.input_shape()) + 2 and tuple(x.shape[2:]) == tuple(self.input_shape())):
+            raise ValueError(f"Input x has invalid shape {x.shape}; expected "
+                             f"{(x.shape[0], 'S', *self.input_shape())} input_shape={self.input_shape()}")
+        assert not self._concatenation_product
+        assert x.device == self.device
+        batch_size, sequence_length = x.shape[0], x.shape[1]
+        assert sequence_length == self._sequence_length, \
+            f"Input sequence_length {sequence_length} does not match constructor sequence_length {self._sequence_length}"
+        x = x.contiguous().view(-1)
+        external_output = output is not None
+        if not external_output:
+            output = torch.zeros([batch_size * sequence_length * self._n_outputs], dtype=torch.float32,
+                                 device=self.device)
+        if pos_embeddings is not None:
+            pos_embeddings = pos_embeddings.contiguous()
+        self._lut_dm.forward_step_product(
+            self._weights, batch_size, self._sequence_length, x, x, self._detector_anchors, output,
+            self._n_inputs, self._n_inputs, self._sliced_product_mode, self._shared_context._cmp_eps,
+            pos_embeddings)
+        return None if external_output else \
+            output.view((batch_size, sequence_length) + tuple(self.output_shape()))
+
+    def backward_step_product(self, x, pos_embeddings, grad_output, x_grad=None):
+        """Product-mode backward (reference LUTLayer.py:1011-1089): input,
+        positional and weight gradients from the same pair lookups."""
+        assert x.device == self.device
+        assert not self._concatenation_product
+        source_x_shape = x.shape
+        batch_size, sequence_length = x.shape[0], x.shape[1]
+        assert sequence_length == self._sequence_length
+        expected_shape = (batch_size, sequence_length) + tuple(self.input_shape())
+        assert tuple(x.shape) == expected_shape, f"Expected input shape {expected_shape}, got {x.shape}"
+        x = x.contiguous().view(-1)
+        external_output = x_grad is not None
+        if not external_output:
+            x_grad = torch.zeros_like(x)
+        if self._weights_gradient_policy.type == GradientType.Internal:
+            target_w_grad = None
+        elif self._weights_gradient_policy.type == GradientType.Sparse:
+            numel = ((self._weights.numel() + 3) // 4) * 4
+            target_w_grad = self._shared_context.get_weight_gradients_buffer(numel, self.device,
+                                                                             self._multi_id)
+        else:
+            target_w_grad = torch.zeros_like(self._weights, requires_grad=False)
+        positional_grad = None
+        if self._positional_dim > 0:
+            pos_embeddings = pos_embeddings.contiguous()
+            positional_grad = torch.zeros_like(pos_embeddings, requires_grad=False)
+        assert grad_output.device == self.device
+        assert tuple(grad_output.shape) == (batch_size, sequence_length) + tuple(self.output_shape())
+        grad_output = grad_output.contiguous().view(-1)
+        external_lr = self._external_lr()
+        self._lut_dm.backward_backprop_product(
+            self._weights, batch_size, self._sequence_length, x, x, self._detector_anchors, grad_output,
+            x_grad, x_grad, external_lr, self._n_inputs, self._n_inputs, self._sliced_product_mode,
+            self._shared_context._cmp_eps, target_w_grad, pos_embeddings, positional_grad)
+        if not external_output and target_w_grad is not None:
+            target_w_grad = self._process_gradients(target_w_grad, batch_size)
+        if self._positional_dim > 0 and self._weights_gradient_policy.normalized:
+            positional_grad /= positional_grad.abs().max().clip(1e-16)
+        result = () if external_output else (x_grad.view(source_x_shape),)
+        return result + (target_w_grad, positional_grad)
+
     def to(self, *args, **kwargs):
         super().to(*args, **kwargs)
         device = kwargs.get("device", None)
@@ -627,13 +705,18 @@ class LUTLayerBasic(nn.Module):
                 if lut_layer._sequence_length == 1:
                     output, li, md, mi = lut_layer.forward_step(x)
                     ctx.save_for_backward(x, li, md, mi)
-                else:
+                elif lut_layer._concatenation_product:
                     (output, li, md, mi, pli, pmd, pmi) = lut_layer.forward_step_concat(x, pos_embeddings)
                     ctx.save_for_backward(x, li, md, mi, pli, pmd, pmi)
+                else:
+                    output = lut_layer.forward_step_product(x, pos_embeddings)
+                    ctx.save_for_backward(x, pos_embeddings)
                 return output
             if lut_layer._sequence_length == 1:
                 return lut_layer.forward_step(x)
-            return lut_layer.forward_step_concat(x, pos_embeddings)
+            if lut_layer._concatenation_product:
+                return lut_layer.forward_step_concat(x, pos_embeddings)
+            return lut_layer.forward_step_product(x, pos_embeddings)
 
         @staticmethod
         def backward(ctx, *grad_outputs):
@@ -642,6 +725,11 @@ class LUTLayerBasic(nn.Module):
                 (x, li, md, mi) = ctx.saved_tensors
                 x_grad, w_grad = ctx.lut_layer.backward_step(x, grad_output, li, md, mi)
                 return x_grad, w_grad, None, None
+            if not ctx.lut_layer._concatenation_product:
+                (x, pos_embeddings) = ctx.saved_tensors
+                x_grad, w_grad, pe_grad = ctx.lut_layer.backward_step_product(x, pos_embeddings,
+                                                                              grad_output)
+                return x_grad, w_grad, pe_grad, None
             (x, li, md, mi, pli, pmd, pmi) = ctx.saved_tensors
             x_grad, w_grad, pe_grad = ctx.lut_layer.backward_step_concat(x, grad_output, li, md, mi,
                                                                          pli, pmd, pmi)
@@ -695,17 +783,29 @@ class Conv2DLUTLayer(LUTLayerBasic):
                  _explicit_anchors=None, _int_rescaler=0.001, _forward_group_size=32,
                  _backward_group_size=32, _max_groups_in_growth_buffer=2 ** 20, random_seed=None,
                  device=None):
-        if not concatenation_product:
-            raise NotImplementedError("product mode (concatenation_product=False) is not part of this build")
+        # detectors see the virtual row of product mode: [x_i | x_j | pe], or
+        # sliced, x_i x_j pe interleaved (reference LUTLayer.py:1273-1292)
+        if concatenation_product:
+            input_shape_ex = tuple(input_shape)
+        elif sliced_product_mode:
+            input_shape_ex = (input_shape[0], input_shape[1] * 3)
+        else:
+            input_shape_ex = (input_shape[0], input_shape[1] * 2 + (positional_dim or 0))
         if receptive_field_shape is None:
             assert receptive_field_stride_shape is None
-            rf, rs = input_shape, input_shape
-        else:
+            rf, rs = input_shape_ex, input_shape_ex
+        elif concatenation_product:
             rf, rs = receptive_field_shape, receptive_field_stride_shape
-        c_helper_1 = Conv2DSynapseGrowthHelper(input_shape[0], input_shape[1], rf[0], rf[1], rs[0], rs[1],
-                                               detectors_shape[0], detectors_shape[1])
+        elif sliced_product_mode:
+            rf = (receptive_field_shape[0], receptive_field_shape[1] * 3)
+            rs = (receptive_field_stride_shape[0], receptive_field_stride_shape[1] * 3)
+        else:
+            raise ValueError("a receptive field in product mode needs sliced_product_mode == True")
+        c_helper_1 = Conv2DSynapseGrowthHelper(input_shape_ex[0], input_shape_ex[1], rf[0], rf[1],
+                                               rs[0], rs[1], detectors_shape[0], detectors_shape[1])
         lut_shape = c_helper_1.out_h, c_helper_1.out_w
-        n_lut_channels = LUTLayerBasic.n_lut_channels(n_anchors_per_detector, sequence_length)
+        n_lut_channels = LUTLayerBasic.n_lut_channels(n_anchors_per_detector, sequence_length,
+                                                      concatenation_product)
         n_inputs = input_shape[0] * input_shape[1]
         n_detectors = lut_shape[0] * lut_shape[1]
         if lut_receptive_field_shape is not None:
@@ -746,7 +846,7 @@ class Conv2DLUTLayer(LUTLayerBasic):
                 self._set_full_detector_connectivity()
             else:
                 connections = c_helper_1.grow_synapses(
-                    input_ids=self.get_input_neuron_ids().view(input_shape) + 1,
+                    input_ids=self.get_input_neuron_ids().view(input_shape_ex) + 1,
                     output_ids=self.get_detector_neuron_ids().view(lut_shape[0], lut_shape[1]) + 1,
                     seed=random_seed)
                 self.add_detector_connections(chunk_of_connections=connections, ids_shift=-1,

@@ -590,6 +590,103 @@ class _LUTDataManagerBase:
                 _ptr(w_positional_embeddings_gradients if P > 0 else None), _ptr(w_weights_gradients),
                 int(bool(overwrite_weights_gradients)), ctypes.c_void_p(st)))
 
+    def _product_sizes(self, batch_size, sequence_length, n_inputs_1, n_inputs_2, what):
+        if batch_size == 0:
+            raise ValueError("batch_size == 0")
+        if self._sequence_length != 1:
+            raise ValueError(f"{what}: this is an experimental method, this->sequence_length should be "
+                             "equal to 1, real length of the sequence is passed as the method parameter")
+        if sequence_length == 0:
+            raise ValueError("sequence_length == 0")
+        return int(batch_size), int(sequence_length), int(n_inputs_1), int(n_inputs_2)
+
+    def forward_step_product(self, r_weights, batch_size, sequence_length, r_input_1, r_input_2,
+                             r_detector_anchors, w_output, n_inputs_1, n_inputs_2, sliced_mode=False,
+                             cmp_eps=0.0, r_positional_embeddings=None, r_stream_handles=None):
+        """lut.cu:847-943 -> lut_runtime.cu:852-1049.  The manager has
+        sequence_length 1; the real one is the argument.  r_input_1 [B][S][n1],
+        r_input_2 [B][S][n2], w_output [B][S][O] summed into, positional
+        embeddings [(S-1)][T][pd]."""
+        dev = self._device
+        B, S, n1, n2 = self._product_sizes(batch_size, sequence_length, n_inputs_1, n_inputs_2,
+                                           "forward_step_product")
+        check_tensor(r_weights, "r_weights", True, dev)
+        check_tensor(r_input_1, "r_input_1", True, dev)
+        check_tensor(r_input_2, "r_input_2", True, dev)
+        check_tensor(r_detector_anchors, "r_detector_anchors", False, dev, 4)
+        check_tensor(w_output, "w_output", True, dev)
+        if r_positional_embeddings is not None:
+            check_tensor(r_positional_embeddings, "r_positional_embeddings", True, dev)
+        self._require_device()
+        T, P = self._n_detectors, self._positional_dim
+        _require_numel(r_weights, self.get_weights_dimension(), "r_weights")
+        _require_numel(r_input_1, B * S * n1, "r_input_1")
+        _require_numel(r_input_2, B * S * n2, "r_input_2")
+        _require_numel(r_detector_anchors, T * self._n_anchors * 2, "r_detector_anchors")
+        _require_numel(w_output, B * S * self._n_outputs, "w_output")
+        if P > 0:
+            if r_positional_embeddings is None:
+                raise ValueError("r_positional_embeddings must be provided when positional_dim > 0")
+            _require_numel(r_positional_embeddings, (S - 1) * T * P, "r_positional_embeddings")
+        with torch.cuda.device(dev):
+            st = self._stream(r_stream_handles)
+            _native.check(_native.lib().spiky_lut_forward_step_product(
+                self._h, _ptr(r_weights), B, S, _ptr(r_input_1), _ptr(r_input_2),
+                _ptr(r_detector_anchors), _ptr(w_output), n1, n2, int(bool(sliced_mode)),
+                float(cmp_eps), _ptr(r_positional_embeddings if P > 0 else None),
+                ctypes.c_void_p(st)))
+
+    def backward_backprop_product(self, r_weights, batch_size, sequence_length, r_input_1, r_input_2,
+                                  r_detector_anchors, r_output_gradients, w_input_gradients_1,
+                                  w_input_gradients_2, external_lr, n_inputs_1, n_inputs_2,
+                                  sliced_mode=False, cmp_eps=0.0, w_weights_gradients=None,
+                                  r_positional_embeddings=None, w_positional_embeddings_gradients=None,
+                                  r_stream_handles=None):
+        """lut.cu:945-1039 -> lut_runtime.cu:1051-1456.  The two input
+        gradients may be one tensor (the layer's call)."""
+        dev = self._device
+        B, S, n1, n2 = self._product_sizes(batch_size, sequence_length, n_inputs_1, n_inputs_2,
+                                           "backward_backprop_product")
+        for t, nm, real in ((r_weights, "r_weights", True), (r_input_1, "r_input_1", True),
+                            (r_input_2, "r_input_2", True),
+                            (r_detector_anchors, "r_detector_anchors", False),
+                            (r_output_gradients, "r_output_gradients", True),
+                            (w_input_gradients_1, "w_input_gradients_1", True),
+                            (w_input_gradients_2, "w_input_gradients_2", True)):
+            check_tensor(t, nm, real, dev)
+        for t, nm in ((w_weights_gradients, "w_weights_gradients"),
+                      (r_positional_embeddings, "r_positional_embeddings"),
+                      (w_positional_embeddings_gradients, "w_positional_embeddings_gradients")):
+            if t is not None:
+                check_tensor(t, nm, True, dev)
+        self._require_device()
+        T, P = self._n_detectors, self._positional_dim
+        _require_numel(r_weights, self.get_weights_dimension(), "r_weights")
+        _require_numel(r_input_1, B * S * n1, "r_input_1")
+        _require_numel(r_input_2, B * S * n2, "r_input_2")
+        _require_numel(r_detector_anchors, T * self._n_anchors * 2, "r_detector_anchors")
+        _require_numel(r_output_gradients, B * S * self._n_outputs, "r_output_gradients")
+        _require_numel(w_input_gradients_1, B * S * n1, "w_input_gradients_1")
+        _require_numel(w_input_gradients_2, B * S * n2, "w_input_gradients_2")
+        if w_weights_gradients is not None:
+            _require_numel(w_weights_gradients, self.get_weights_dimension(), "w_weights_gradients")
+        if P > 0:
+            if r_positional_embeddings is None or w_positional_embeddings_gradients is None:
+                raise ValueError("positional embeddings and their gradients must be provided when "
+                                 "positional_dim > 0")
+            _require_numel(r_positional_embeddings, (S - 1) * T * P, "r_positional_embeddings")
+            _require_numel(w_positional_embeddings_gradients, (S - 1) * T * P,
+                           "w_positional_embeddings_gradients")
+        with torch.cuda.device(dev):
+            st = self._stream(r_stream_handles)
+            _native.check(_native.lib().spiky_lut_backward_backprop_product(
+                self._h, _ptr(r_weights), B, S, _ptr(r_input_1), _ptr(r_input_2),
+                _ptr(r_detector_anchors), _ptr(r_output_gradients), _ptr(w_input_gradients_1),
+                _ptr(w_input_gradients_2), float(external_lr), n1, n2, int(bool(sliced_mode)),
+                float(cmp_eps), _ptr(w_weights_gradients),
+                _ptr(r_positional_embeddings if P > 0 else None),
+                _ptr(w_positional_embeddings_gradients if P > 0 else None), ctypes.c_void_p(st)))
+
     # ---------------------------------------------------------------- export
     def count_synapses(self, neuron_indices_to_process):
         """Number of forward synapses of the given lookup neurons."""

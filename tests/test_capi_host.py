@@ -206,3 +206,71 @@ def test_densify_validation():
         conv.dense_to_sparse_32(torch.zeros(6))
     with pytest.raises(ValueError, match="GPU device"):
         conv.dense_to_sparse_32(torch.zeros(8))
+
+
+def test_product_validation():
+    """Product-mode host checks (lut.cu:880-891, 986-997; lut_runtime.cu:
+    1075-1077) raise before any device access."""
+    from spiky_amd import _native
+    L = _native.lib()
+    d = ctypes.c_void_p(16)
+
+    def make(seq_len, fc=1):
+        h = ctypes.c_void_p()
+        _native.check(L.spiky_lut_create(8, 4, 4, 2, seq_len, 0, 0, 32, 32, 0, 0.0, ctypes.byref(h)))
+        _native.check(L.spiky_lut_register_synapse_meta(h, 1.0, 0.0, 1.0, 0.0, 0.0, None))
+        _native.check(L.spiky_lut_initialize_neurons(h, fc))
+        return h
+
+    h = make(4)
+    try:
+        with pytest.raises(ValueError, match="sequence_length should be equal to 1"):
+            _native.check(L.spiky_lut_forward_step_product(h, d, 2, 5, d, d, d, d, 4, 4, 0, 0.0, None,
+                                                           None))
+    finally:
+        L.spiky_lut_destroy(h)
+    h = make(1)
+    try:
+        with pytest.raises(ValueError, match="batch_size == 0"):
+            _native.check(L.spiky_lut_forward_step_product(h, d, 0, 5, d, d, d, d, 4, 4, 0, 0.0, None,
+                                                           None))
+        with pytest.raises(ValueError, match="sequence_length == 0"):
+            _native.check(L.spiky_lut_forward_step_product(h, d, 2, 0, d, d, d, d, 4, 4, 0, 0.0, None,
+                                                           None))
+        with pytest.raises(ValueError, match="no active context"):
+            _native.check(L.spiky_lut_backward_backprop_product(h, d, 2, 5, d, d, d, d, d, d, -1.0, 4, 4,
+                                                                0, 0.0, d, None, None, None))
+    finally:
+        L.spiky_lut_destroy(h)
+    h = make(1, fc=0)
+    try:
+        with pytest.raises(ValueError, match="sparse connectivity is not compiled"):
+            _native.check(L.spiky_lut_forward_step_product(h, d, 2, 5, d, d, d, d, 4, 4, 0, 0.0, None,
+                                                           None))
+    finally:
+        L.spiky_lut_destroy(h)
+
+
+def test_product_layer_construction():
+    """Product-mode layers build on the host: the manager sees the virtual
+    row (2n + pd inputs, or 3n sliced) and a sequence length of 1, and the
+    reference's argument checks hold (LUTLayer.py:264-274)."""
+    from spiky_amd import LUTLayer
+    layer = LUTLayer(16, 4, 8, 32, sequence_length=6, concatenation_product=False, positional_dim=4,
+                     random_seed=1)
+    assert layer._lut_dm.get_number_of_inputs() == 36
+    assert layer._weights.numel() == 8 * 16 * 32
+    assert layer.lut_shape() == (8, 16)
+    a = layer._detector_anchors
+    assert a.min() >= 0 and a.max() < 36
+    assert layer._positional_embeddings.numel() == 5 * 8 * 4
+    sl = LUTLayer(16, 4, 8, 32, sequence_length=6, concatenation_product=False,
+                  sliced_product_mode=True, positional_dim=16, random_seed=1)
+    assert sl._lut_dm.get_number_of_inputs() == 48
+    with pytest.raises(ValueError, match="doesn't make sense with sequence_length == 1"):
+        LUTLayer(16, 4, 8, 32, sequence_length=1, concatenation_product=False)
+    with pytest.raises(ValueError, match="n_inputs and positional_dim should be equal"):
+        LUTLayer(16, 4, 8, 32, sequence_length=6, concatenation_product=False,
+                 sliced_product_mode=True, positional_dim=4)
+    with pytest.raises(ValueError, match="doesn't make sense in concatenation product mode"):
+        LUTLayer(16, 4, 8, 32, sequence_length=6, sliced_product_mode=True, positional_dim=16)
