@@ -24,6 +24,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E peak
+PEAK_FP64_TFLOPS = 78.6  # MI355X fp64 (vector and matrix)
 
 CONFIGS = {
     # name: (B, I, T, Nc, O, x_dist, cpu_sample_B)
@@ -430,6 +431,88 @@ def bench_transformer(args):
     print(json.dumps(res), flush=True)
 
 
+PRODUCT = dict(batch=32, seq_len=256, n_inputs=256, n_detectors=64, n_anchors=6, n_outputs=256,
+               positional_dim=4, cpu_batch=2)
+
+
+def product_flops(B, S, T, Nc, O):
+    """fp64 FMA flops of the three count products of one product-mode fwd+bwd
+    (out += Cnt.W, P = G.W^T, W_grad += Cnt^T.G), each B*S x T*2^Nc x O."""
+    return 3 * 2 * B * S * (T << Nc) * O
+
+
+def bench_product(args):
+    """Product-mode LUT layer (concatenation_product=False) forward + backward
+    at the attention shape of BASELINE config 5: 32 sequences of 256 tokens,
+    d_model 256, 16 detectors x 4 heads, 6 anchors (64-row tables) over the
+    virtual row [x_i | x_j | pe] with positional_dim 4, Dense weight gradient."""
+    import torch
+    from spiky_amd import LUTLayer
+    dev = torch.device("cuda:0")
+    c = PRODUCT
+    B, S, n, T, Nc, O, pd = (c[k] for k in ("batch", "seq_len", "n_inputs", "n_detectors", "n_anchors",
+                                             "n_outputs", "positional_dim"))
+    log(f"product: B={B} S={S} n={n} T={T} Nc={Nc} O={O} pd={pd}")
+    layer = LUTLayer(n, Nc, T, O, sequence_length=S, concatenation_product=False, positional_dim=pd,
+                     random_seed=1, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(2)
+    with torch.no_grad():
+        layer._weights.normal_(0.0, 0.01, generator=gen)
+    x = torch.randn(B, S, n, device=dev, generator=gen).requires_grad_(True)
+    go = torch.randn(B, S, O, device=dev, generator=gen)
+
+    def step():
+        x.grad = None
+        layer._weights.grad = None
+        layer._positional_embeddings.grad = None
+        layer(x).backward(go)
+
+    log("warmup")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} steps")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    fl = product_flops(B, S, T, Nc, O)
+    lookups = 2 * B * (S * (S - 1) // 2) * T
+    cpu = None
+    if not args.no_cpu_baseline:
+        import numpy as np
+        import oracle
+        cb = c["cpu_batch"]
+        xs = x.detach()[:cb].cpu().numpy().reshape(-1)
+        W = layer._weights.detach().cpu().numpy()
+        anc = layer._detector_anchors.cpu().numpy()
+        pe = layer._prepare_positional_embeddings().detach().cpu().numpy()
+        g = go[:cb].cpu().numpy().reshape(-1)
+        geo = (cb, S, n, n, pd, T, Nc, O)
+        t0 = time.perf_counter()
+        oracle.fill_outputs_product(xs, xs, pe, anc, W, *geo)
+        oracle.propagate_product(xs, xs, pe, anc, W, g, *geo, w_grad=np.zeros(W.size, np.float32))
+        sec = time.perf_counter() - t0
+        cpu = {"value": round(cb / sec, 4), "unit": "samples/s", "cores": 1, "kind": "port",
+               "sample": f"C restatement of the reference's CPU product path (serial, 1 thread) on {cb} of "
+                         f"the {B} sequences, forward + backward: {sec:.2f} s"}
+    res = {
+        "metric": "product-mode LUT layer fwd+bwd samples/sec (config-5 attention shape)",
+        "value": round(B / (ms / 1e3), 2), "unit": "samples/s",
+        "pair_lookups_per_s": round(lookups / (ms / 1e3), 1),
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f64 (fp32 I/O)",
+        "data": "synthetic (N(0,1) inputs and upstream grads, N(0,0.01) tables)",
+        "config": {"workload": "product-mode LUT layer fwd+bwd, config-5 attention shape", **c},
+        "roofline": {"bound": "mfma", "achieved": round(fl / (ms * 1e-3) / 1e12, 2), "peak": PEAK_FP64_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(fl / (ms * 1e-3) / 1e12 / PEAK_FP64_TFLOPS, 4),
+                     "traffic": None, "flops_per_step": fl, "scope": "whole step, fp64 count products"},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+
+
 DENSIFY = dict(words=1 << 28, densities=(0.01, 0.1, 0.5), cpu_words=1 << 25)
 
 
@@ -509,6 +592,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS) + [2, 4, 5])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--product", action="store_true",
+                    help="time the product-mode LUT layer (concatenation_product=False) instead")
     ap.add_argument("--densify", action="store_true",
                     help="time the dense -> sparse gradient converter instead of a LUT config")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
@@ -522,6 +607,8 @@ def main():
               "(the multi-GPU table-parallel design is described, not built).", file=sys.stderr)
         sys.exit(2)
 
+    if args.product:
+        return bench_product(args)
     if args.densify:
         bench_densify(args)
         return

@@ -27,6 +27,7 @@
 // in a serial order: equal within the fp32 rounding of that order.
 #include "lut_kernels.h"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace spiky {
@@ -170,6 +171,160 @@ __global__ __launch_bounds__(kPrThreads) void k_prod_pairs(
     for (uint32_t k = threadIdx.x; k < TE; k += kPrThreads) crow[k] = (float)hist[k];
 }
 
+// The same pass with the lookups served from LDS.  Per workgroup (b, j):
+//   anc  [T*Nc]      uint2  each anchor pair decoded to (source << 30 | index),
+//                           kNoSlot when unused or beyond the virtual row
+//   hist [T*E]       u32    row counts
+//   x2   [n2]        f32    x2[b, j]
+//   x2g  [n2]        f32    (BWD) the pushes into x2_grad[b, j], flushed once
+//   x1c  [C*n1]      f32    x1 rows i0 .. i0+C-1 of the chunk being looked up
+//   pec  [C*T*pd]    f32    the positional slices those rows use (distances
+//                           j-i-1 for the chunk's i, contiguous in pe)
+// Threads take the chunk's pairs table-fastest, so a wave reads one x1 row
+// and neighbouring positional slices.  Pushes into x1 rows (other workgroups'
+// x2 rows) and into pe stay global atomics.
+constexpr uint32_t kNoSlot = 0xFFFFFFFFu;
+constexpr uint32_t kPrLdsBudget = 48 * 1024;
+
+struct PairsLayout {
+    uint32_t chunk;  // x1 rows per chunk; 0 = does not fit
+    uint32_t bytes;
+};
+
+PairsLayout pairs_layout(const ProductShape &s, bool bwd) {
+    const uint64_t TE = (uint64_t)s.n_detectors << s.n_anchors;
+    const uint64_t fixed = (uint64_t)s.n_detectors * s.n_anchors * 8 + TE * 4 +
+                           (uint64_t)s.n2 * 4 * (bwd ? 2 : 1);
+    const uint64_t per_row = ((uint64_t)s.n1 + (uint64_t)s.n_detectors * s.pd) * 4;
+    if (fixed + per_row > kPrLdsBudget) return {0, 0};
+    uint64_t c = (kPrLdsBudget - fixed) / per_row;
+    c = c < s.seq_len ? c : s.seq_len;
+    return {(uint32_t)c, (uint32_t)(fixed + c * per_row)};
+}
+
+__device__ __forceinline__ uint32_t anchor_code(int32_t id, uint32_t n1, uint32_t n2, uint32_t pd,
+                                                bool sliced) {
+    if (id < 0) return kNoSlot;
+    int32_t src;
+    uint32_t k;
+    if (!prod_locate(n1, n2, pd, sliced, (uint32_t)id, src, k)) return kNoSlot;
+    return ((uint32_t)src << 30) | k;
+}
+
+template <bool BWD, bool INT_MODE>
+__global__ __launch_bounds__(kPrThreads) void k_prod_pairs_lds(
+    const float *__restrict__ x1, const float *__restrict__ x2, const float *__restrict__ pe,
+    const int2 *__restrict__ anchors, const double *__restrict__ P, float *__restrict__ cnt,
+    float *__restrict__ x1_grad, float *__restrict__ x2_grad, float *__restrict__ pe_grad,
+    uint32_t S, uint32_t n1, uint32_t n2, uint32_t pd, uint32_t T, uint32_t n_anchors, bool sliced,
+    float cmp_eps, double int_rescaler, uint32_t C) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const uint32_t E = 1u << n_anchors;
+    const uint32_t TE = T * E;
+    const uint32_t TN = T * n_anchors;
+    uint2 *anc = reinterpret_cast<uint2 *>(smem);
+    uint32_t *hist = reinterpret_cast<uint32_t *>(anc + TN);
+    float *xs = reinterpret_cast<float *>(hist + TE);  // x2 | (x2g) | x1c | pec
+    float *x2g = xs + n2;
+    float *x1c = BWD ? x2g + n2 : xs + n2;
+    float *pec = x1c + (size_t)C * n1;
+    const uint32_t bj = blockIdx.x;
+    const uint32_t b = bj / S, j = bj % S;
+    const uint32_t tid = threadIdx.x;
+    for (uint32_t k = tid; k < TN; k += kPrThreads) {
+        const int2 ap = anchors[k];
+        uint2 c = make_uint2(anchor_code(ap.x, n1, n2, pd, sliced), anchor_code(ap.y, n1, n2, pd, sliced));
+        if (c.y == kNoSlot) c.x = kNoSlot;
+        anc[k] = c;
+    }
+    for (uint32_t k = tid; k < TE; k += kPrThreads) hist[k] = 0;
+    const float *x2j = x2 + (size_t)bj * n2;
+    for (uint32_t k = tid; k < n2; k += kPrThreads) {
+        xs[k] = x2j[k];
+        if (BWD) x2g[k] = 0.0f;
+    }
+    const double *Pbj = BWD ? P + (size_t)bj * TE : nullptr;
+    for (uint32_t i0 = 0; i0 < j; i0 += C) {
+        const uint32_t i1 = min(i0 + C, j);
+        const uint32_t rows = i1 - i0;
+        const uint32_t dlo = j - i1;  // distances j-i-1 of the chunk: dlo .. dlo+rows-1
+        __syncthreads();
+        {
+            const float *src = x1 + ((size_t)b * S + i0) * n1;
+            for (uint32_t k = tid; k < rows * n1; k += kPrThreads) x1c[k] = src[k];
+            const float *ps = pe + (size_t)dlo * T * pd;
+            for (uint32_t k = tid; k < rows * T * pd; k += kPrThreads) pec[k] = ps[k];
+        }
+        __syncthreads();
+        const uint32_t n_pairs = rows * T;
+        for (uint32_t p = tid; p < n_pairs; p += kPrThreads) {
+            const uint32_t r = p / T, t = p - r * T;
+            const uint32_t i = i0 + r;
+            const uint32_t d = j - i - 1;
+            // offsets of the three sources in the row space x1c[...]
+            const int32_t base0 = (int32_t)(r * n1);
+            const int32_t base1 = (int32_t)(xs - x1c);  // negative: x2 precedes x1c
+            const int32_t base2 = (int32_t)(C * n1 + ((d - dlo) * T + t) * pd);
+            int32_t idx = 0, flip = -1;
+            float md = 3.402823466e+38f;
+            uint32_t c1 = kNoSlot, c2 = kNoSlot;
+            for (uint32_t a = 0; a < n_anchors; a++) {
+                const uint2 c = anc[t * n_anchors + a];
+                if (c.x == kNoSlot) continue;
+                const uint32_t s1 = c.x >> 30, s2 = c.y >> 30;
+                const int32_t o1 = (s1 == 0 ? base0 : (s1 == 1 ? base1 : base2)) + (int32_t)(c.x & 0x3FFFFFFFu);
+                const int32_t o2 = (s2 == 0 ? base0 : (s2 == 1 ? base1 : base2)) + (int32_t)(c.y & 0x3FFFFFFFu);
+                const float dv = x1c[o1] - x1c[o2];
+                if (rgreater0(dv, cmp_eps)) idx |= (1 << a);
+                if (fabsf(dv) < fabsf(md)) {
+                    md = dv;
+                    flip = (int32_t)a;
+                    c1 = c.x;
+                    c2 = c.y;
+                }
+            }
+            atomicAdd(&hist[t * E + (uint32_t)idx], 1u);
+            if (BWD && flip >= 0) {
+                const int32_t alt = idx ^ (1 << flip);
+                const double du = du_of_margin(md) * (Pbj[t * E + idx] - Pbj[t * E + alt]);
+                if (fabs(du) > kEps) {
+#pragma unroll
+                    for (int h = 0; h < 2; h++) {
+                        const uint32_t c = h == 0 ? c1 : c2;
+                        const uint32_t src = c >> 30, k = c & 0x3FFFFFFFu;
+                        const double v = h == 0 ? du : -du;
+                        const int32_t pay = INT_MODE ? (int32_t)(v * kDenom32 * int_rescaler) : 0;
+                        const float fv = (float)v;
+                        if (src == 1) {
+                            if (INT_MODE) atomicAdd(reinterpret_cast<int32_t *>(x2g + k), pay);
+                            else atomicAdd(x2g + k, fv);
+                        } else {
+                            float *dst = src == 0 ? x1_grad + ((size_t)b * S + i) * n1 + k
+                                                  : pe_grad + ((size_t)d * T + t) * pd + k;
+                            if (INT_MODE) atomicAdd(reinterpret_cast<int32_t *>(dst), pay);
+                            else atomicAdd(dst, fv);
+                        }
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+    float *crow = cnt + (size_t)bj * TE;
+    for (uint32_t k = tid; k < TE; k += kPrThreads) crow[k] = (float)hist[k];
+    if (BWD) {
+        float *dst = x2_grad + (size_t)bj * n2;
+        for (uint32_t k = tid; k < n2; k += kPrThreads) {
+            if (INT_MODE) {
+                const int32_t v = reinterpret_cast<const int32_t *>(x2g)[k];
+                if (v != 0) atomicAdd(reinterpret_cast<int32_t *>(dst + k), v);
+            } else if (x2g[k] != 0.0f) {
+                atomicAdd(dst + k, x2g[k]);
+            }
+        }
+    }
+}
+
 // C[M][N] (+)= A[M][K] . B[K][N] on the VALU: 64 x 64 tiles, 256 threads of 4 x 4
 // outputs, K in steps of 16 through LDS.  A(m, k) = TA ? A[k*lda + m] : A[m*lda + k],
 // B likewise with TB.  BMODE: 0 plain; 1 weight payload (int32 forward); 2 weight-
@@ -273,6 +428,143 @@ hipError_t gemm(const float *A, uint32_t lda, const float *B, uint32_t ldb, void
     return hipGetLastError();
 }
 
+// The fp64 products on the matrix cores (v_mfma_f64_16x16x4f64): 64 x 64
+// workgroup tiles, four waves of 32 x 32 (2 x 2 MFMA tiles), K in steps of 16
+// through LDS as fp64 (operands converted and, for BMODE 2, cut and scaled on
+// the way in, exactly as the VALU kernel does).  Lane layout of the
+// instruction (measured on gfx950): A[i][k] in lane i + 16k, B[k][j] in lane
+// j + 16k, D[q + 4r][j] in register r of lane j + 16q -- not the fp32
+// instruction's D[4q + r][j].  gridDim.z splits K; with a split the
+// workgroup stores its fp64 partial tile to part[z] and k_prod_splitk_reduce
+// adds the partials in z order (deterministic) into C.
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+constexpr int kMfK = 16;
+
+template <bool TA, bool TB, int BMODE, int OUT>
+__global__ __launch_bounds__(256) void k_prod_gemm_mfma(const float *__restrict__ A, uint32_t lda,
+                                                        const float *__restrict__ B, uint32_t ldb,
+                                                        void *__restrict__ C, double *__restrict__ part,
+                                                        uint32_t M, uint32_t N, uint32_t K,
+                                                        uint32_t k_chunk, double lr) {
+    __shared__ double As[kMfK][kGmTile + 1];
+    __shared__ double Bs[kMfK][kGmTile + 1];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63, wave = tid >> 6;
+    const uint32_t wm = (wave & 1) * 32, wn = (wave >> 1) * 32;
+    const uint32_t li = lane & 15, lq = lane >> 4;
+    const uint32_t m0 = blockIdx.y * kGmTile, n0 = blockIdx.x * kGmTile;
+    const uint32_t kb = blockIdx.z * k_chunk;
+    const uint32_t ke = min(K, kb + k_chunk);
+    f64x4 acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < 2; b++) acc[a][b] = f64x4{0.0, 0.0, 0.0, 0.0};
+    for (uint32_t k0 = kb; k0 < ke; k0 += kMfK) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const uint32_t e = tid + 256u * u;
+            uint32_t kk, mm;
+            if (TA) { mm = e & 63; kk = e >> 6; } else { kk = e & 15; mm = e >> 4; }
+            const uint32_t m = m0 + mm, k = k0 + kk;
+            float a = 0.0f;
+            if (m < M && k < ke) a = TA ? A[(size_t)k * lda + m] : A[(size_t)m * lda + k];
+            As[kk][mm] = (double)a;
+            uint32_t kb2, nn;
+            if (TB) { kb2 = e & 15; nn = e >> 4; } else { nn = e & 63; kb2 = e >> 6; }
+            const uint32_t n = n0 + nn, k2 = k0 + kb2;
+            float bv = 0.0f;
+            if (n < N && k2 < ke) bv = TB ? B[(size_t)n * ldb + k2] : B[(size_t)k2 * ldb + n];
+            double bt = (double)bv;
+            if (BMODE == 2) bt = (fabs(bt) > kEps) ? bt * lr : 0.0;
+            Bs[kb2][nn] = bt;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int ks = 0; ks < kMfK / 4; ks++) {
+            const uint32_t kr = ks * 4 + lq;
+            const double a0 = As[kr][wm + li], a1 = As[kr][wm + 16 + li];
+            const double b0 = Bs[kr][wn + li], b1 = Bs[kr][wn + 16 + li];
+            acc[0][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b0, acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b1, acc[0][1], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b0, acc[1][0], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b1, acc[1][1], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+    double *pz = part ? part + (size_t)blockIdx.z * M * N : nullptr;
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < 2; b++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const uint32_t m = m0 + wm + a * 16 + lq + 4 * r;
+                const uint32_t n = n0 + wn + b * 16 + li;
+                if (m >= M || n >= N) continue;
+                const size_t o = (size_t)m * N + n;
+                const double v = acc[a][b][r];
+                if (pz) {
+                    pz[o] = v;
+                } else if (OUT == 0) {
+                    float *Cf = reinterpret_cast<float *>(C);
+                    Cf[o] = (float)((double)Cf[o] + v);
+                } else {
+                    reinterpret_cast<double *>(C)[o] = v;
+                }
+            }
+}
+
+template <int OUT>
+__global__ __launch_bounds__(256) void k_prod_splitk_reduce(const double *__restrict__ part,
+                                                            void *__restrict__ C, uint64_t MN,
+                                                            uint32_t splits) {
+    for (uint64_t o = (uint64_t)blockIdx.x * 256 + threadIdx.x; o < MN; o += (uint64_t)gridDim.x * 256) {
+        double v = 0.0;
+        for (uint32_t z = 0; z < splits; z++) v += part[(size_t)z * MN + o];
+        if (OUT == 0) {
+            float *Cf = reinterpret_cast<float *>(C);
+            Cf[o] = (float)((double)Cf[o] + v);
+        } else {
+            reinterpret_cast<double *>(C)[o] = v;
+        }
+    }
+}
+
+// K splits: enough workgroups to cover the chip four times over, each split
+// at least 256 deep.
+uint32_t splitk_for(uint32_t M, uint32_t N, uint32_t K) {
+    const uint64_t tiles = (uint64_t)((M + kGmTile - 1) / kGmTile) * ((N + kGmTile - 1) / kGmTile);
+    uint64_t split = (1024 + tiles - 1) / tiles;
+    const uint64_t max_split = K / 256 > 0 ? K / 256 : 1;
+    if (split > max_split) split = max_split;
+    if (split > 16) split = 16;
+    return (uint32_t)(split < 1 ? 1 : split);
+}
+
+size_t splitk_bytes(uint32_t M, uint32_t N, uint32_t K) {
+    const uint32_t z = splitk_for(M, N, K);
+    return z > 1 ? (size_t)z * M * N * 8 : 0;
+}
+
+template <bool TA, bool TB, int BMODE, int OUT>
+hipError_t gemm_mfma(const float *A, uint32_t lda, const float *B, uint32_t ldb, void *C, uint32_t M,
+                     uint32_t N, uint32_t K, double lr, double *part, hipStream_t st) {
+    if (M == 0 || N == 0) return hipSuccess;
+    const uint32_t z = part ? splitk_for(M, N, K) : 1;  // no partial buffer: no split
+    const uint32_t k_chunk = ((K + z - 1) / z + kMfK - 1) / kMfK * kMfK;
+    const dim3 grid((N + kGmTile - 1) / kGmTile, (M + kGmTile - 1) / kGmTile, z);
+    if (grid.y > 65535u) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL((k_prod_gemm_mfma<TA, TB, BMODE, OUT>), grid, dim3(256), 0, st, A, lda, B, ldb,
+                       C, z > 1 ? part : nullptr, M, N, K, k_chunk, lr);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || z == 1) return e;
+    const uint64_t MN = (uint64_t)M * N;
+    const uint32_t blocks = (uint32_t)std::min<uint64_t>((MN + 255) / 256, 4096);
+    hipLaunchKernelGGL((k_prod_splitk_reduce<OUT>), dim3(blocks), dim3(256), 0, st, part, C, MN, z);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 bool product_applies(const ProductShape &s) {
@@ -281,12 +573,24 @@ bool product_applies(const ProductShape &s) {
            (uint64_t)s.batch * s.seq_len <= 65535ull * kGmTile;
 }
 
-// scratch: Cnt [B*S][T*E] f32 | P [B*S][T*E] f64 (backward)
-size_t product_scratch_bytes(const ProductShape &s, bool backward) {
+// scratch: Cnt [B*S][T*E] f32 | P [B*S][T*E] f64 (backward) | split-K partials
+// of the product that sums over the longest dimension (forward: Cnt . W over
+// T*E; backward: Cnt^T . g' over B*S)
+static size_t cnt_bytes(const ProductShape &s) {
     const uint64_t TE = (uint64_t)s.n_detectors << s.n_anchors;
-    const uint64_t BS = (uint64_t)s.batch * s.seq_len;
-    const size_t cnt = (BS * TE * 4 + 255) & ~(size_t)255;
-    return cnt + (backward ? BS * TE * 8 : 0);
+    return ((uint64_t)s.batch * s.seq_len * TE * 4 + 255) & ~(size_t)255;
+}
+
+static size_t p_bytes(const ProductShape &s) {
+    const uint64_t TE = (uint64_t)s.n_detectors << s.n_anchors;
+    return ((uint64_t)s.batch * s.seq_len * TE * 8 + 255) & ~(size_t)255;
+}
+
+size_t product_scratch_bytes(const ProductShape &s, bool backward) {
+    const uint32_t TE = s.n_detectors << s.n_anchors;
+    const uint32_t BS = s.batch * s.seq_len;
+    if (!backward) return cnt_bytes(s) + splitk_bytes(BS, s.n_outputs, TE);
+    return cnt_bytes(s) + p_bytes(s) + splitk_bytes(TE, s.n_outputs, BS);
 }
 
 hipError_t launch_forward_product(const ProductShape &s, const float *w, const float *x1,
@@ -299,12 +603,20 @@ hipError_t launch_forward_product(const ProductShape &s, const float *w, const f
     if (BS == 0) return hipSuccess;
     float *cnt = reinterpret_cast<float *>(scratch);
     const int2 *anc = reinterpret_cast<const int2 *>(anchors);
+    const PairsLayout lay = pairs_layout(s, false);
 #define SPIKY_PP(IM)                                                                              \
-    hipLaunchKernelGGL((k_prod_pairs<false, IM>), dim3(BS), dim3(kPrThreads), TE * 4, st, x1, x2, \
-                       pe, anc, (const double *)nullptr, cnt, (float *)nullptr, (float *)nullptr, \
-                       (float *)nullptr, s.seq_len, s.n1, s.n2, s.pd, s.n_detectors, s.n_anchors, \
-                       s.sliced, s.cmp_eps, int_rescaler)
-    if (int_mode) SPIKY_PP(true); else SPIKY_PP(false);
+    if (lay.chunk)                                                                                \
+        hipLaunchKernelGGL((k_prod_pairs_lds<false, IM>), dim3(BS), dim3(kPrThreads), lay.bytes,  \
+                           st, x1, x2, pe, anc, (const double *)nullptr, cnt, (float *)nullptr,   \
+                           (float *)nullptr, (float *)nullptr, s.seq_len, s.n1, s.n2, s.pd,       \
+                           s.n_detectors, s.n_anchors, s.sliced, s.cmp_eps, int_rescaler,         \
+                           lay.chunk);                                                            \
+    else                                                                                          \
+        hipLaunchKernelGGL((k_prod_pairs<false, IM>), dim3(BS), dim3(kPrThreads), TE * 4, st, x1, \
+                           x2, pe, anc, (const double *)nullptr, cnt, (float *)nullptr,           \
+                           (float *)nullptr, (float *)nullptr, s.seq_len, s.n1, s.n2, s.pd,       \
+                           s.n_detectors, s.n_anchors, s.sliced, s.cmp_eps, int_rescaler)
+    if (int_mode) { SPIKY_PP(true); } else { SPIKY_PP(false); }
 #undef SPIKY_PP
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -312,8 +624,9 @@ hipError_t launch_forward_product(const ProductShape &s, const float *w, const f
     if (int_mode)
         return gemm<false, false, 1, 1>(cnt, TE, w, s.n_outputs, out, BS, s.n_outputs, TE, 0.0,
                                         int_rescaler, st);
-    return gemm<false, false, 0, 0>(cnt, TE, w, s.n_outputs, out, BS, s.n_outputs, TE, 0.0,
-                                    int_rescaler, st);
+    double *part = reinterpret_cast<double *>(reinterpret_cast<uint8_t *>(scratch) + cnt_bytes(s));
+    return gemm_mfma<false, false, 0, 0>(cnt, TE, w, s.n_outputs, out, BS, s.n_outputs, TE, 0.0, part,
+                                         st);
 }
 
 hipError_t launch_backward_product(const ProductShape &s, const float *w, const float *x1,
@@ -326,18 +639,26 @@ hipError_t launch_backward_product(const ProductShape &s, const float *w, const 
     const uint32_t BS = s.batch * s.seq_len;
     if (BS == 0) return hipSuccess;
     float *cnt = reinterpret_cast<float *>(scratch);
-    double *P = reinterpret_cast<double *>(reinterpret_cast<uint8_t *>(scratch) +
-                                           (((size_t)BS * TE * 4 + 255) & ~(size_t)255));
-    // P[bj][k] = sum_o g[bj][o] * W[k][o]  (fp64)
-    hipError_t e = gemm<false, true, 0, 2>(g, s.n_outputs, w, s.n_outputs, P, BS, TE, s.n_outputs,
-                                           0.0, int_rescaler, st);
+    double *P = reinterpret_cast<double *>(reinterpret_cast<uint8_t *>(scratch) + cnt_bytes(s));
+    double *part = reinterpret_cast<double *>(reinterpret_cast<uint8_t *>(scratch) + cnt_bytes(s) +
+                                              p_bytes(s));
+    // P[bj][k] = sum_o g[bj][o] * W[k][o]  (fp64; no split: B*S x T*E tiles fill the chip)
+    hipError_t e = gemm_mfma<false, true, 0, 2>(g, s.n_outputs, w, s.n_outputs, P, BS, TE,
+                                                s.n_outputs, 0.0, nullptr, st);
     if (e != hipSuccess) return e;
     const int2 *anc = reinterpret_cast<const int2 *>(anchors);
+    const PairsLayout lay = pairs_layout(s, true);
 #define SPIKY_PB(IM)                                                                              \
-    hipLaunchKernelGGL((k_prod_pairs<true, IM>), dim3(BS), dim3(kPrThreads), TE * 4, st, x1, x2,   \
-                       pe, anc, P, cnt, x1_grad, x2_grad, pe_grad, s.seq_len, s.n1, s.n2, s.pd,  \
-                       s.n_detectors, s.n_anchors, s.sliced, s.cmp_eps, int_rescaler)
-    if (int_mode) SPIKY_PB(true); else SPIKY_PB(false);
+    if (lay.chunk)                                                                                \
+        hipLaunchKernelGGL((k_prod_pairs_lds<true, IM>), dim3(BS), dim3(kPrThreads), lay.bytes,   \
+                           st, x1, x2, pe, anc, P, cnt, x1_grad, x2_grad, pe_grad, s.seq_len,     \
+                           s.n1, s.n2, s.pd, s.n_detectors, s.n_anchors, s.sliced, s.cmp_eps,     \
+                           int_rescaler, lay.chunk);                                              \
+    else                                                                                          \
+        hipLaunchKernelGGL((k_prod_pairs<true, IM>), dim3(BS), dim3(kPrThreads), TE * 4, st, x1,  \
+                           x2, pe, anc, P, cnt, x1_grad, x2_grad, pe_grad, s.seq_len, s.n1, s.n2, \
+                           s.pd, s.n_detectors, s.n_anchors, s.sliced, s.cmp_eps, int_rescaler)
+    if (int_mode) { SPIKY_PB(true); } else { SPIKY_PB(false); }
 #undef SPIKY_PB
     e = hipGetLastError();
     if (e != hipSuccess || target == nullptr) return e;
@@ -345,8 +666,8 @@ hipError_t launch_backward_product(const ProductShape &s, const float *w, const 
     if (int_mode)
         return gemm<true, false, 2, 1>(cnt, TE, g, s.n_outputs, target, TE, s.n_outputs, BS, lr,
                                        int_rescaler, st);
-    return gemm<true, false, 2, 0>(cnt, TE, g, s.n_outputs, target, TE, s.n_outputs, BS, lr,
-                                   int_rescaler, st);
+    return gemm_mfma<true, false, 2, 0>(cnt, TE, g, s.n_outputs, target, TE, s.n_outputs, BS, lr,
+                                        part, st);
 }
 
 }  // namespace spiky
