@@ -171,156 +171,166 @@ __global__ __launch_bounds__(kPrThreads) void k_prod_pairs(
     for (uint32_t k = threadIdx.x; k < TE; k += kPrThreads) crow[k] = (float)hist[k];
 }
 
-// The same pass with the lookups served from LDS.  Per workgroup (b, j):
-//   anc  [T*Nc]      uint2  each anchor pair decoded to (source << 30 | index),
-//                           kNoSlot when unused or beyond the virtual row
-//   hist [T*E]       u32    row counts
-//   x2   [n2]        f32    x2[b, j]
-//   x2g  [n2]        f32    (BWD) the pushes into x2_grad[b, j], flushed once
-//   x1c  [C*n1]      f32    x1 rows i0 .. i0+C-1 of the chunk being looked up
-//   pec  [C*T*pd]    f32    the positional slices those rows use (distances
-//                           j-i-1 for the chunk's i, contiguous in pe)
-// Threads take the chunk's pairs table-fastest, so a wave reads one x1 row
-// and neighbouring positional slices.  Pushes into x1 rows (other workgroups'
-// x2 rows) and into pe stay global atomics.
-constexpr uint32_t kNoSlot = 0xFFFFFFFFu;
-constexpr uint32_t kPrLdsBudget = 48 * 1024;
+// Table-major pass: one workgroup of 1024 threads per (b, table t, block of
+// JB positions j).  Every lane looks up the same table, so the only inputs it
+// reads are the 2*Nc anchor inputs of t, staged once per row:
+//   code [Nc]      int2   the two operands of each anchor: source (x1[b, i],
+//                          x2[b, j] or pe[j-i-1]) << 28 | slot; -1 = unused
+//   hist [JB*E/2]  u32    counts of (j, row e), two 16-bit counters a word
+//                          (a count is at most S - 1 < 65536)
+//   xs   [R][2Nc]  f32    value of slot s in row r (R = last j of the block + 1)
+//   acc  [R][2Nc]  f32    (BWD) pushes into slot s of row r, flushed once
+// P is read from L2: the lanes of a wave share j, so each read touches a few
+// lines of one 8*E-byte row segment.  Pushes reach HBM as one atomic per
+// (row, slot) per workgroup instead of one per lookup.
+constexpr uint32_t kTbThreads = 1024;
+constexpr uint32_t kPtBudget = 64 * 1024;
 
-struct PairsLayout {
-    uint32_t chunk;  // x1 rows per chunk; 0 = does not fit
+struct TableLayout {
+    uint32_t jb;  // positions per workgroup; 0 = does not fit
     uint32_t bytes;
 };
 
-PairsLayout pairs_layout(const ProductShape &s, bool bwd) {
-    const uint64_t TE = (uint64_t)s.n_detectors << s.n_anchors;
-    const uint64_t fixed = (uint64_t)s.n_detectors * s.n_anchors * 8 + TE * 4 +
-                           (uint64_t)s.n2 * 4 * (bwd ? 2 : 1);
-    const uint64_t per_row = ((uint64_t)s.n1 + (uint64_t)s.n_detectors * s.pd) * 4;
-    if (fixed + per_row > kPrLdsBudget) return {0, 0};
-    uint64_t c = (kPrLdsBudget - fixed) / per_row;
-    c = c < s.seq_len ? c : s.seq_len;
-    return {(uint32_t)c, (uint32_t)(fixed + c * per_row)};
+TableLayout table_layout(const ProductShape &s, bool bwd) {
+    const uint64_t E = 1ull << s.n_anchors;
+    const uint64_t NS = 2ull * s.n_anchors;
+    const uint64_t fixed = (uint64_t)s.n_anchors * 8 + 4 + (uint64_t)s.seq_len * NS * 4 * (bwd ? 2 : 1);
+    const uint64_t per_j = E * 2;
+    if (fixed + per_j > kPtBudget) return {0, 0};
+    uint64_t jb = (kPtBudget - fixed) / per_j;
+    if (jb > s.seq_len) jb = s.seq_len;
+    return {(uint32_t)jb, (uint32_t)(fixed + ((jb * E + 1) / 2) * 4)};
 }
 
-__device__ __forceinline__ uint32_t anchor_code(int32_t id, uint32_t n1, uint32_t n2, uint32_t pd,
-                                                bool sliced) {
-    if (id < 0) return kNoSlot;
-    int32_t src;
-    uint32_t k;
-    if (!prod_locate(n1, n2, pd, sliced, (uint32_t)id, src, k)) return kNoSlot;
-    return ((uint32_t)src << 30) | k;
+// The grid is one dimension of B * T * ceil(S / JB) workgroups.
+TableLayout table_grid_ok(const ProductShape &s, TableLayout lay) {
+    if (!lay.jb) return lay;
+    const uint64_t n = (uint64_t)s.batch * s.n_detectors * ((s.seq_len + lay.jb - 1) / lay.jb);
+    return n <= 0x7fffffffull ? lay : TableLayout{0, 0};
 }
 
 template <bool BWD, bool INT_MODE>
-__global__ __launch_bounds__(kPrThreads) void k_prod_pairs_lds(
+__global__ __launch_bounds__(kTbThreads) void k_prod_pairs_tbl(
     const float *__restrict__ x1, const float *__restrict__ x2, const float *__restrict__ pe,
     const int2 *__restrict__ anchors, const double *__restrict__ P, float *__restrict__ cnt,
     float *__restrict__ x1_grad, float *__restrict__ x2_grad, float *__restrict__ pe_grad,
     uint32_t S, uint32_t n1, uint32_t n2, uint32_t pd, uint32_t T, uint32_t n_anchors, bool sliced,
-    float cmp_eps, double int_rescaler, uint32_t C) {
+    float cmp_eps, double int_rescaler, uint32_t JB, uint32_t n_jblocks) {
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t E = 1u << n_anchors;
-    const uint32_t TE = T * E;
-    const uint32_t TN = T * n_anchors;
-    uint2 *anc = reinterpret_cast<uint2 *>(smem);
-    uint32_t *hist = reinterpret_cast<uint32_t *>(anc + TN);
-    float *xs = reinterpret_cast<float *>(hist + TE);  // x2 | (x2g) | x1c | pec
-    float *x2g = xs + n2;
-    float *x1c = BWD ? x2g + n2 : xs + n2;
-    float *pec = x1c + (size_t)C * n1;
-    const uint32_t bj = blockIdx.x;
-    const uint32_t b = bj / S, j = bj % S;
+    const uint32_t NS = 2 * n_anchors;
+    int2 *code = reinterpret_cast<int2 *>(smem);
+    uint32_t *hist = reinterpret_cast<uint32_t *>(code + n_anchors);
+    const uint32_t hist_words = (JB * E + 1) / 2;
+    float *xs = reinterpret_cast<float *>(hist + hist_words);
     const uint32_t tid = threadIdx.x;
-    for (uint32_t k = tid; k < TN; k += kPrThreads) {
-        const int2 ap = anchors[k];
-        uint2 c = make_uint2(anchor_code(ap.x, n1, n2, pd, sliced), anchor_code(ap.y, n1, n2, pd, sliced));
-        if (c.y == kNoSlot) c.x = kNoSlot;
-        anc[k] = c;
+    const uint32_t jblk = blockIdx.x % n_jblocks;
+    const uint32_t bt = blockIdx.x / n_jblocks;
+    const uint32_t t = bt % T, b = bt / T;
+    const uint32_t j0 = jblk * JB;
+    const uint32_t j_end = min(S, j0 + JB);
+    const uint32_t R = j_end;  // rows 0 .. j_end-1 (i, j and distances all below j_end)
+    float *acc = xs + (size_t)R * NS;  // BWD only
+    if (tid < n_anchors) {
+        const int2 ap = anchors[(size_t)t * n_anchors + tid];
+        int2 c = make_int2(-1, -1);
+        int32_t s1, s2;
+        uint32_t k1, k2;
+        if (ap.x >= 0 && ap.y >= 0 && prod_locate(n1, n2, pd, sliced, (uint32_t)ap.x, s1, k1) &&
+            prod_locate(n1, n2, pd, sliced, (uint32_t)ap.y, s2, k2))
+            c = make_int2((s1 << 28) | (int32_t)(2 * tid), (s2 << 28) | (int32_t)(2 * tid + 1));
+        code[tid] = c;
     }
-    for (uint32_t k = tid; k < TE; k += kPrThreads) hist[k] = 0;
-    const float *x2j = x2 + (size_t)bj * n2;
-    for (uint32_t k = tid; k < n2; k += kPrThreads) {
-        xs[k] = x2j[k];
-        if (BWD) x2g[k] = 0.0f;
-    }
-    const double *Pbj = BWD ? P + (size_t)bj * TE : nullptr;
-    for (uint32_t i0 = 0; i0 < j; i0 += C) {
-        const uint32_t i1 = min(i0 + C, j);
-        const uint32_t rows = i1 - i0;
-        const uint32_t dlo = j - i1;  // distances j-i-1 of the chunk: dlo .. dlo+rows-1
-        __syncthreads();
-        {
-            const float *src = x1 + ((size_t)b * S + i0) * n1;
-            for (uint32_t k = tid; k < rows * n1; k += kPrThreads) x1c[k] = src[k];
-            const float *ps = pe + (size_t)dlo * T * pd;
-            for (uint32_t k = tid; k < rows * T * pd; k += kPrThreads) pec[k] = ps[k];
+    for (uint32_t e = tid; e < hist_words; e += kTbThreads) hist[e] = 0;
+    __syncthreads();
+    // stage the slot values of rows 0 .. R-1 (positional slots: distance r, valid r < S-1)
+    for (uint32_t e = tid; e < R * NS; e += kTbThreads) {
+        const uint32_t r = e / NS, sidx = e - r * NS;
+        const int2 ap = anchors[(size_t)t * n_anchors + sidx / 2];
+        const int2 c = code[sidx / 2];
+        float v = 0.0f;
+        if (c.x != -1) {
+            int32_t src;
+            uint32_t k;
+            prod_locate(n1, n2, pd, sliced, (uint32_t)((sidx & 1) ? ap.y : ap.x), src, k);
+            if (src == 0) v = x1[((size_t)b * S + r) * n1 + k];
+            else if (src == 1) v = x2[((size_t)b * S + r) * n2 + k];
+            else if (r + 1 < S) v = pe[((size_t)r * T + t) * pd + k];
         }
-        __syncthreads();
-        const uint32_t n_pairs = rows * T;
-        for (uint32_t p = tid; p < n_pairs; p += kPrThreads) {
-            const uint32_t r = p / T, t = p - r * T;
-            const uint32_t i = i0 + r;
-            const uint32_t d = j - i - 1;
-            // offsets of the three sources in the row space x1c[...]
-            const int32_t base0 = (int32_t)(r * n1);
-            const int32_t base1 = (int32_t)(xs - x1c);  // negative: x2 precedes x1c
-            const int32_t base2 = (int32_t)(C * n1 + ((d - dlo) * T + t) * pd);
-            int32_t idx = 0, flip = -1;
-            float md = 3.402823466e+38f;
-            uint32_t c1 = kNoSlot, c2 = kNoSlot;
-            for (uint32_t a = 0; a < n_anchors; a++) {
-                const uint2 c = anc[t * n_anchors + a];
-                if (c.x == kNoSlot) continue;
-                const uint32_t s1 = c.x >> 30, s2 = c.y >> 30;
-                const int32_t o1 = (s1 == 0 ? base0 : (s1 == 1 ? base1 : base2)) + (int32_t)(c.x & 0x3FFFFFFFu);
-                const int32_t o2 = (s2 == 0 ? base0 : (s2 == 1 ? base1 : base2)) + (int32_t)(c.y & 0x3FFFFFFFu);
-                const float dv = x1c[o1] - x1c[o2];
-                if (rgreater0(dv, cmp_eps)) idx |= (1 << a);
-                if (fabsf(dv) < fabsf(md)) {
-                    md = dv;
-                    flip = (int32_t)a;
-                    c1 = c.x;
-                    c2 = c.y;
-                }
+        xs[e] = v;
+        if (BWD) acc[e] = 0.0f;
+    }
+    __syncthreads();
+    const double *Pt = BWD ? P + (size_t)t * E : nullptr;
+    const size_t TE = (size_t)T * E;
+    // pairs (i < j, j in the block), j-major, kTbThreads apart per thread
+    uint32_t j = j0, i = tid;
+    while (j < j_end && i >= j) {
+        i -= j;
+        j++;
+    }
+    while (j < j_end) {
+        const int32_t B0 = (int32_t)(i * NS), B1 = (int32_t)(j * NS), B2 = B1 - B0 - (int32_t)NS;
+        int32_t idx = 0, flip = -1;
+        float md = 3.402823466e+38f;
+        for (uint32_t a = 0; a < n_anchors; a++) {
+            const int2 c = code[a];
+            if (c.x == -1) continue;
+            const int32_t s1 = c.x >> 28, s2 = c.y >> 28;
+            const float v1 = xs[(s1 == 0 ? B0 : (s1 == 1 ? B1 : B2)) + (c.x & 0xFFFFFFF)];
+            const float v2 = xs[(s2 == 0 ? B0 : (s2 == 1 ? B1 : B2)) + (c.y & 0xFFFFFFF)];
+            const float dv = v1 - v2;
+            if (rgreater0(dv, cmp_eps)) idx |= (1 << a);
+            if (fabsf(dv) < fabsf(md)) {
+                md = dv;
+                flip = (int32_t)a;
             }
-            atomicAdd(&hist[t * E + (uint32_t)idx], 1u);
-            if (BWD && flip >= 0) {
-                const int32_t alt = idx ^ (1 << flip);
-                const double du = du_of_margin(md) * (Pbj[t * E + idx] - Pbj[t * E + alt]);
-                if (fabs(du) > kEps) {
+        }
+        const uint32_t h = (j - j0) * E + (uint32_t)idx;
+        atomicAdd(&hist[h >> 1], 1u << (16 * (h & 1)));
+        if (BWD && flip >= 0) {
+            const double *Pbj = Pt + ((size_t)b * S + j) * TE;
+            const double du = du_of_margin(md) * (Pbj[idx] - Pbj[idx ^ (1 << flip)]);
+            if (fabs(du) > kEps) {
+                const int2 c = code[flip];
 #pragma unroll
-                    for (int h = 0; h < 2; h++) {
-                        const uint32_t c = h == 0 ? c1 : c2;
-                        const uint32_t src = c >> 30, k = c & 0x3FFFFFFFu;
-                        const double v = h == 0 ? du : -du;
-                        const int32_t pay = INT_MODE ? (int32_t)(v * kDenom32 * int_rescaler) : 0;
-                        const float fv = (float)v;
-                        if (src == 1) {
-                            if (INT_MODE) atomicAdd(reinterpret_cast<int32_t *>(x2g + k), pay);
-                            else atomicAdd(x2g + k, fv);
-                        } else {
-                            float *dst = src == 0 ? x1_grad + ((size_t)b * S + i) * n1 + k
-                                                  : pe_grad + ((size_t)d * T + t) * pd + k;
-                            if (INT_MODE) atomicAdd(reinterpret_cast<int32_t *>(dst), pay);
-                            else atomicAdd(dst, fv);
-                        }
-                    }
+                for (int hh = 0; hh < 2; hh++) {
+                    const int32_t cc = hh == 0 ? c.x : c.y;
+                    const int32_t sr = cc >> 28;
+                    const int32_t pos = (sr == 0 ? B0 : (sr == 1 ? B1 : B2)) + (cc & 0xFFFFFFF);
+                    const double v = hh == 0 ? du : -du;
+                    if (INT_MODE)
+                        atomicAdd(reinterpret_cast<int32_t *>(acc + pos), (int32_t)(v * kDenom32 * int_rescaler));
+                    else
+                        atomicAdd(acc + pos, (float)v);
                 }
             }
+        }
+        i += kTbThreads;
+        while (j < j_end && i >= j) {
+            i -= j;
+            j++;
         }
     }
     __syncthreads();
-    float *crow = cnt + (size_t)bj * TE;
-    for (uint32_t k = tid; k < TE; k += kPrThreads) crow[k] = (float)hist[k];
+    for (uint32_t e = tid; e < (j_end - j0) * E; e += kTbThreads) {
+        const uint32_t jj = e / E, ee = e - jj * E;
+        cnt[((size_t)b * S + j0 + jj) * TE + (size_t)t * E + ee] = (float)((hist[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+    }
     if (BWD) {
-        float *dst = x2_grad + (size_t)bj * n2;
-        for (uint32_t k = tid; k < n2; k += kPrThreads) {
-            if (INT_MODE) {
-                const int32_t v = reinterpret_cast<const int32_t *>(x2g)[k];
-                if (v != 0) atomicAdd(reinterpret_cast<int32_t *>(dst + k), v);
-            } else if (x2g[k] != 0.0f) {
-                atomicAdd(dst + k, x2g[k]);
-            }
+        for (uint32_t e = tid; e < R * NS; e += kTbThreads) {
+            const uint32_t r = e / NS, sidx = e - r * NS;
+            const int32_t iv = reinterpret_cast<const int32_t *>(acc)[e];
+            if (iv == 0) continue;  // +0.0f, or a zero int32 sum (a -0.0f sum adds nothing either)
+            const int2 ap = anchors[(size_t)t * n_anchors + sidx / 2];
+            int32_t src;
+            uint32_t k;
+            prod_locate(n1, n2, pd, sliced, (uint32_t)((sidx & 1) ? ap.y : ap.x), src, k);
+            float *dst = src == 0 ? x1_grad + ((size_t)b * S + r) * n1 + k
+                                  : (src == 1 ? x2_grad + ((size_t)b * S + r) * n2 + k
+                                              : pe_grad + ((size_t)r * T + t) * pd + k);
+            if (INT_MODE) atomicAdd(reinterpret_cast<int32_t *>(dst), iv);
+            else atomicAdd(dst, acc[e]);
         }
     }
 }
@@ -603,14 +613,15 @@ hipError_t launch_forward_product(const ProductShape &s, const float *w, const f
     if (BS == 0) return hipSuccess;
     float *cnt = reinterpret_cast<float *>(scratch);
     const int2 *anc = reinterpret_cast<const int2 *>(anchors);
-    const PairsLayout lay = pairs_layout(s, false);
+    const TableLayout lay = table_grid_ok(s, table_layout(s, false));
+    const uint32_t njb = lay.jb ? (s.seq_len + lay.jb - 1) / lay.jb : 0;
 #define SPIKY_PP(IM)                                                                              \
-    if (lay.chunk)                                                                                \
-        hipLaunchKernelGGL((k_prod_pairs_lds<false, IM>), dim3(BS), dim3(kPrThreads), lay.bytes,  \
-                           st, x1, x2, pe, anc, (const double *)nullptr, cnt, (float *)nullptr,   \
-                           (float *)nullptr, (float *)nullptr, s.seq_len, s.n1, s.n2, s.pd,       \
-                           s.n_detectors, s.n_anchors, s.sliced, s.cmp_eps, int_rescaler,         \
-                           lay.chunk);                                                            \
+    if (lay.jb)                                                                                   \
+        hipLaunchKernelGGL((k_prod_pairs_tbl<false, IM>), dim3(s.batch * s.n_detectors * njb),    \
+                           dim3(kTbThreads), lay.bytes, st, x1, x2, pe, anc,                      \
+                           (const double *)nullptr, cnt, (float *)nullptr, (float *)nullptr,      \
+                           (float *)nullptr, s.seq_len, s.n1, s.n2, s.pd, s.n_detectors,          \
+                           s.n_anchors, s.sliced, s.cmp_eps, int_rescaler, lay.jb, njb);          \
     else                                                                                          \
         hipLaunchKernelGGL((k_prod_pairs<false, IM>), dim3(BS), dim3(kPrThreads), TE * 4, st, x1, \
                            x2, pe, anc, (const double *)nullptr, cnt, (float *)nullptr,           \
@@ -647,13 +658,14 @@ hipError_t launch_backward_product(const ProductShape &s, const float *w, const 
                                                 s.n_outputs, 0.0, nullptr, st);
     if (e != hipSuccess) return e;
     const int2 *anc = reinterpret_cast<const int2 *>(anchors);
-    const PairsLayout lay = pairs_layout(s, true);
+    const TableLayout lay = table_grid_ok(s, table_layout(s, true));
+    const uint32_t njb = lay.jb ? (s.seq_len + lay.jb - 1) / lay.jb : 0;
 #define SPIKY_PB(IM)                                                                              \
-    if (lay.chunk)                                                                                \
-        hipLaunchKernelGGL((k_prod_pairs_lds<true, IM>), dim3(BS), dim3(kPrThreads), lay.bytes,   \
-                           st, x1, x2, pe, anc, P, cnt, x1_grad, x2_grad, pe_grad, s.seq_len,     \
-                           s.n1, s.n2, s.pd, s.n_detectors, s.n_anchors, s.sliced, s.cmp_eps,     \
-                           int_rescaler, lay.chunk);                                              \
+    if (lay.jb)                                                                                   \
+        hipLaunchKernelGGL((k_prod_pairs_tbl<true, IM>), dim3(s.batch * s.n_detectors * njb),     \
+                           dim3(kTbThreads), lay.bytes, st, x1, x2, pe, anc, P, cnt, x1_grad,     \
+                           x2_grad, pe_grad, s.seq_len, s.n1, s.n2, s.pd, s.n_detectors,          \
+                           s.n_anchors, s.sliced, s.cmp_eps, int_rescaler, lay.jb, njb);          \
     else                                                                                          \
         hipLaunchKernelGGL((k_prod_pairs<true, IM>), dim3(BS), dim3(kPrThreads), TE * 4, st, x1,  \
                            x2, pe, anc, P, cnt, x1_grad, x2_grad, pe_grad, s.seq_len, s.n1, s.n2, \

@@ -156,11 +156,17 @@ def test_product_largest_histogram_int32(oracle, cuda_device):
     run_product(oracle, B=1, S=5, n=12, T=64, Nc=8, O=8, pd=0, int_rescaler=0.01, seed=7)
 
 
-def test_product_wide_rows_global_path(oracle, cuda_device):
-    """Rows too wide for the LDS-staged lookups (2 * n * 4 bytes beyond the
-    48 KB budget) take the pass that reads them from global memory."""
+def test_product_long_sequence_global_path(oracle, cuda_device):
+    """A sequence too long for the table-major pass (its 2*Nc anchor inputs of
+    every position, S * 12 * 4 bytes, beyond the 64 KB LDS budget) takes the
+    pass that reads the rows from global memory."""
+    run_product(oracle, B=1, S=1400, n=8, T=3, Nc=6, O=8, pd=2, seed=10)
+    run_product(oracle, B=1, S=1400, n=8, T=3, Nc=6, O=8, pd=2, int_rescaler=0.001, seed=10)
+
+
+def test_product_wide_rows(oracle, cuda_device):
+    """Rows of 6200 inputs: only the anchor inputs are staged."""
     run_product(oracle, B=1, S=4, n=6200, T=3, Nc=3, O=8, pd=2, seed=10)
-    run_product(oracle, B=1, S=4, n=6200, T=3, Nc=3, O=8, pd=2, int_rescaler=0.001, seed=10)
 
 
 def test_product_shortest_sequence(oracle, cuda_device):
