@@ -438,75 +438,107 @@ hipError_t gemm(const float *A, uint32_t lda, const float *B, uint32_t ldb, void
     return hipGetLastError();
 }
 
-// The fp64 products on the matrix cores (v_mfma_f64_16x16x4f64): 64 x 64
-// workgroup tiles, four waves of 32 x 32 (2 x 2 MFMA tiles), K in steps of 16
-// through LDS as fp64 (operands converted and, for BMODE 2, cut and scaled on
-// the way in, exactly as the VALU kernel does).  Lane layout of the
+// The fp64 products on the matrix cores (v_mfma_f64_16x16x4f64).  A
+// workgroup of WM x WN waves owns a (WM*WTM*16) x (WN*WTN*16) tile, each wave
+// WTM x WTN MFMA tiles of 16 x 16; K runs in steps of 16 through a double
+// buffer in LDS, fp64 (operands converted and, for BMODE 2, cut and scaled on
+// the way in, exactly as the VALU kernel does), with the next step's global
+// loads in flight while the current one multiplies.  Lane layout of the
 // instruction (measured on gfx950): A[i][k] in lane i + 16k, B[k][j] in lane
 // j + 16k, D[q + 4r][j] in register r of lane j + 16q -- not the fp32
-// instruction's D[4q + r][j].  gridDim.z splits K; with a split the
-// workgroup stores its fp64 partial tile to part[z] and k_prod_splitk_reduce
-// adds the partials in z order (deterministic) into C.
+// instruction's D[4q + r][j].  gridDim.z splits K; with a split the workgroup
+// stores its fp64 partial tile to part[z] and k_prod_splitk_reduce adds the
+// partials in z order (deterministic) into C.
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 constexpr int kMfK = 16;
 
-template <bool TA, bool TB, int BMODE, int OUT>
-__global__ __launch_bounds__(256) void k_prod_gemm_mfma(const float *__restrict__ A, uint32_t lda,
-                                                        const float *__restrict__ B, uint32_t ldb,
-                                                        void *__restrict__ C, double *__restrict__ part,
-                                                        uint32_t M, uint32_t N, uint32_t K,
-                                                        uint32_t k_chunk, double lr) {
-    __shared__ double As[kMfK][kGmTile + 1];
-    __shared__ double Bs[kMfK][kGmTile + 1];
-    const uint32_t tid = threadIdx.x;
-    const uint32_t lane = tid & 63, wave = tid >> 6;
-    const uint32_t wm = (wave & 1) * 32, wn = (wave >> 1) * 32;
+template <int WTM, int WTN, int WM, int WN, bool TA, bool TB, int BMODE, int OUT>
+__global__ __launch_bounds__(64 * WM * WN) void k_prod_gemm_mfma(
+    const float *__restrict__ A, uint32_t lda, const float *__restrict__ B, uint32_t ldb,
+    void *__restrict__ C, double *__restrict__ part, uint32_t M, uint32_t N, uint32_t K,
+    uint32_t k_chunk, double lr) {
+    constexpr int TM = WM * WTM * 16, TN = WN * WTN * 16, NT = 64 * WM * WN;
+    constexpr int LA = TM * kMfK / NT, LB = kMfK * TN / NT;
+    static_assert(LA * NT == TM * kMfK && LB * NT == kMfK * TN, "tile does not split over threads");
+    __shared__ double As[2][kMfK][TM + 1];
+    __shared__ double Bs[2][kMfK][TN + 1];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t wm = (wave % WM) * WTM * 16, wn = (wave / WM) * WTN * 16;
     const uint32_t li = lane & 15, lq = lane >> 4;
-    const uint32_t m0 = blockIdx.y * kGmTile, n0 = blockIdx.x * kGmTile;
-    const uint32_t kb = blockIdx.z * k_chunk;
-    const uint32_t ke = min(K, kb + k_chunk);
-    f64x4 acc[2][2];
+    const uint32_t m0 = blockIdx.y * TM, n0 = blockIdx.x * TN;
+    const uint32_t kb = blockIdx.z * k_chunk, ke = min(K, kb + k_chunk);
+    f64x4 acc[WTM][WTN];
 #pragma unroll
-    for (int a = 0; a < 2; a++)
+    for (int a = 0; a < WTM; a++)
 #pragma unroll
-        for (int b = 0; b < 2; b++) acc[a][b] = f64x4{0.0, 0.0, 0.0, 0.0};
-    for (uint32_t k0 = kb; k0 < ke; k0 += kMfK) {
+        for (int b = 0; b < WTN; b++) acc[a][b] = f64x4{0.0, 0.0, 0.0, 0.0};
+    float ra[LA], rb[LB];
+    // element e of a tile: the index order follows the source's contiguous
+    // dimension, for coalescing
+    auto gload = [&](uint32_t k0) {
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const uint32_t e = tid + 256u * u;
-            uint32_t kk, mm;
-            if (TA) { mm = e & 63; kk = e >> 6; } else { kk = e & 15; mm = e >> 4; }
+        for (int u = 0; u < LA; u++) {
+            const uint32_t e = tid + NT * u;
+            const uint32_t mm = TA ? e % TM : e / kMfK, kk = TA ? e / TM : e % kMfK;
             const uint32_t m = m0 + mm, k = k0 + kk;
-            float a = 0.0f;
-            if (m < M && k < ke) a = TA ? A[(size_t)k * lda + m] : A[(size_t)m * lda + k];
-            As[kk][mm] = (double)a;
-            uint32_t kb2, nn;
-            if (TB) { kb2 = e & 15; nn = e >> 4; } else { nn = e & 63; kb2 = e >> 6; }
-            const uint32_t n = n0 + nn, k2 = k0 + kb2;
-            float bv = 0.0f;
-            if (n < N && k2 < ke) bv = TB ? B[(size_t)n * ldb + k2] : B[(size_t)k2 * ldb + n];
-            double bt = (double)bv;
-            if (BMODE == 2) bt = (fabs(bt) > kEps) ? bt * lr : 0.0;
-            Bs[kb2][nn] = bt;
+            ra[u] = (m < M && k < ke) ? (TA ? A[(size_t)k * lda + m] : A[(size_t)m * lda + k]) : 0.0f;
         }
-        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < LB; u++) {
+            const uint32_t e = tid + NT * u;
+            const uint32_t nn = TB ? e / kMfK : e % TN, kk = TB ? e % kMfK : e / TN;
+            const uint32_t n = n0 + nn, k = k0 + kk;
+            rb[u] = (n < N && k < ke) ? (TB ? B[(size_t)n * ldb + k] : B[(size_t)k * ldb + n]) : 0.0f;
+        }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < LA; u++) {
+            const uint32_t e = tid + NT * u;
+            const uint32_t mm = TA ? e % TM : e / kMfK, kk = TA ? e / TM : e % kMfK;
+            As[buf][kk][mm] = (double)ra[u];
+        }
+#pragma unroll
+        for (int u = 0; u < LB; u++) {
+            const uint32_t e = tid + NT * u;
+            const uint32_t nn = TB ? e / kMfK : e % TN, kk = TB ? e % kMfK : e / TN;
+            double bt = (double)rb[u];
+            if (BMODE == 2) bt = (fabs(bt) > kEps) ? bt * lr : 0.0;
+            Bs[buf][kk][nn] = bt;
+        }
+    };
+    int buf = 0;
+    if (kb < ke) {
+        gload(kb);
+        lstore(0);
+    }
+    __syncthreads();
+    for (uint32_t k0 = kb; k0 < ke; k0 += kMfK) {
+        const bool more = k0 + kMfK < ke;
+        if (more) gload(k0 + kMfK);
 #pragma unroll
         for (int ks = 0; ks < kMfK / 4; ks++) {
             const uint32_t kr = ks * 4 + lq;
-            const double a0 = As[kr][wm + li], a1 = As[kr][wm + 16 + li];
-            const double b0 = Bs[kr][wn + li], b1 = Bs[kr][wn + 16 + li];
-            acc[0][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b0, acc[0][0], 0, 0, 0);
-            acc[0][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b1, acc[0][1], 0, 0, 0);
-            acc[1][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b0, acc[1][0], 0, 0, 0);
-            acc[1][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b1, acc[1][1], 0, 0, 0);
+            double av[WTM], bv[WTN];
+#pragma unroll
+            for (int a = 0; a < WTM; a++) av[a] = As[buf][kr][wm + a * 16 + li];
+#pragma unroll
+            for (int b = 0; b < WTN; b++) bv[b] = Bs[buf][kr][wn + b * 16 + li];
+#pragma unroll
+            for (int a = 0; a < WTM; a++)
+#pragma unroll
+                for (int b = 0; b < WTN; b++)
+                    acc[a][b] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[a], bv[b], acc[a][b], 0, 0, 0);
         }
+        if (more) lstore(buf ^ 1);
         __syncthreads();
+        buf ^= 1;
     }
     double *pz = part ? part + (size_t)blockIdx.z * M * N : nullptr;
 #pragma unroll
-    for (int a = 0; a < 2; a++)
+    for (int a = 0; a < WTM; a++)
 #pragma unroll
-        for (int b = 0; b < 2; b++)
+        for (int b = 0; b < WTN; b++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const uint32_t m = m0 + wm + a * 16 + lq + 4 * r;
@@ -541,11 +573,11 @@ __global__ __launch_bounds__(256) void k_prod_splitk_reduce(const double *__rest
     }
 }
 
-// K splits: enough workgroups to cover the chip four times over, each split
-// at least 256 deep.
+// K splits of the 64 x 64-tile products: about 2048 workgroups (eight per
+// CU), each split at least 256 deep.
 uint32_t splitk_for(uint32_t M, uint32_t N, uint32_t K) {
-    const uint64_t tiles = (uint64_t)((M + kGmTile - 1) / kGmTile) * ((N + kGmTile - 1) / kGmTile);
-    uint64_t split = (1024 + tiles - 1) / tiles;
+    const uint64_t tiles = (uint64_t)((M + 63) / 64) * ((N + 63) / 64);
+    uint64_t split = (2048 + tiles - 1) / tiles;
     const uint64_t max_split = K / 256 > 0 ? K / 256 : 1;
     if (split > max_split) split = max_split;
     if (split > 16) split = 16;
@@ -557,16 +589,25 @@ size_t splitk_bytes(uint32_t M, uint32_t N, uint32_t K) {
     return z > 1 ? (size_t)z * M * N * 8 : 0;
 }
 
+// part == nullptr: one pass over K on the 128 x 64 tile (the product whose
+// output tiles already fill the chip); else the 64 x 64 tile split over K.
 template <bool TA, bool TB, int BMODE, int OUT>
 hipError_t gemm_mfma(const float *A, uint32_t lda, const float *B, uint32_t ldb, void *C, uint32_t M,
                      uint32_t N, uint32_t K, double lr, double *part, hipStream_t st) {
     if (M == 0 || N == 0) return hipSuccess;
-    const uint32_t z = part ? splitk_for(M, N, K) : 1;  // no partial buffer: no split
+    if (!part) {
+        const dim3 grid((N + 63) / 64, (M + 127) / 128, 1);
+        if (grid.y > 65535u) return hipErrorInvalidConfiguration;
+        hipLaunchKernelGGL((k_prod_gemm_mfma<4, 2, 2, 2, TA, TB, BMODE, OUT>), grid, dim3(256), 0, st,
+                           A, lda, B, ldb, C, (double *)nullptr, M, N, K, K, lr);
+        return hipGetLastError();
+    }
+    const uint32_t z = splitk_for(M, N, K);
     const uint32_t k_chunk = ((K + z - 1) / z + kMfK - 1) / kMfK * kMfK;
-    const dim3 grid((N + kGmTile - 1) / kGmTile, (M + kGmTile - 1) / kGmTile, z);
+    const dim3 grid((N + 63) / 64, (M + 63) / 64, z);
     if (grid.y > 65535u) return hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL((k_prod_gemm_mfma<TA, TB, BMODE, OUT>), grid, dim3(256), 0, st, A, lda, B, ldb,
-                       C, z > 1 ? part : nullptr, M, N, K, k_chunk, lr);
+    hipLaunchKernelGGL((k_prod_gemm_mfma<2, 2, 2, 2, TA, TB, BMODE, OUT>), grid, dim3(256), 0, st, A,
+                       lda, B, ldb, C, z > 1 ? part : nullptr, M, N, K, k_chunk, lr);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || z == 1) return e;
     const uint64_t MN = (uint64_t)M * N;
