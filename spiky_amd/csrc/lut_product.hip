@@ -173,16 +173,20 @@ __global__ __launch_bounds__(kPrThreads) void k_prod_pairs(
 
 // Table-major pass: one workgroup of 1024 threads per (b, table t, block of
 // JB positions j).  Every lane looks up the same table, so the only inputs it
-// reads are the 2*Nc anchor inputs of t, staged once per row:
+// reads are the 2*Nc anchor inputs of t, staged once per row, slot-major:
 //   code [Nc]      int2   the two operands of each anchor: source (x1[b, i],
-//                          x2[b, j] or pe[j-i-1]) << 28 | slot; -1 = unused
+//                          x2[b, j] or pe[j-i-1]) << 28 | slot * R; -1 = unused
 //   hist [JB*E/2]  u32    counts of (j, row e), two 16-bit counters a word
 //                          (a count is at most S - 1 < 65536)
-//   xs   [R][2Nc]  f32    value of slot s in row r (R = last j of the block + 1)
-//   acc  [R][2Nc]  f32    (BWD) pushes into slot s of row r, flushed once
-// P is read from L2: the lanes of a wave share j, so each read touches a few
-// lines of one 8*E-byte row segment.  Pushes reach HBM as one atomic per
-// (row, slot) per workgroup instead of one per lookup.
+//   xs   [2Nc][R]  f32    value of slot s in row r (R = last j of the block + 1)
+//   acc  [2Nc][R]  f32    (BWD) pushes into slot s of row r, flushed once
+// Pairs go j-major over the lanes, so a wave reads consecutive rows i of a
+// slot (conflict-free) and one row j (a broadcast).  P is read from L2: the
+// lanes of a wave share j, so each read touches a few lines of one 8*E-byte
+// row segment.  Pushes into rows i and distances j-i-1 are LDS atomics on
+// consecutive words; pushes into the shared row j are summed over the wave
+// first (one atomic per slot), since up to 64 lanes would hit one word.
+// Pushes reach HBM as one atomic per (row, slot) per workgroup.
 constexpr uint32_t kTbThreads = 1024;
 constexpr uint32_t kPtBudget = 64 * 1024;
 
@@ -196,7 +200,7 @@ TableLayout table_layout(const ProductShape &s, bool bwd) {
     const uint64_t NS = 2ull * s.n_anchors;
     const uint64_t fixed = (uint64_t)s.n_anchors * 8 + 4 + (uint64_t)s.seq_len * NS * 4 * (bwd ? 2 : 1);
     const uint64_t per_j = E * 2;
-    if (fixed + per_j > kPtBudget) return {0, 0};
+    if (fixed + per_j > kPtBudget || NS * s.seq_len >= (1ull << 28)) return {0, 0};
     uint64_t jb = (kPtBudget - fixed) / per_j;
     if (jb > s.seq_len) jb = s.seq_len;
     return {(uint32_t)jb, (uint32_t)(fixed + ((jb * E + 1) / 2) * 4)};
@@ -209,13 +213,45 @@ TableLayout table_grid_ok(const ProductShape &s, TableLayout lay) {
     return n <= 0x7fffffffull ? lay : TableLayout{0, 0};
 }
 
-template <bool BWD, bool INT_MODE>
-__global__ __launch_bounds__(kTbThreads) void k_prod_pairs_tbl(
+// Sum over the 64 lanes of a wave (every lane active): rotations within rows
+// of 16, then the four row sums.
+template <typename V>
+__device__ __forceinline__ V wave_sum64(V v) {
+    auto rot = [](V x, auto ctrl) {
+        int xi;
+        __builtin_memcpy(&xi, &x, 4);
+        xi = __builtin_amdgcn_mov_dpp(xi, decltype(ctrl)::value, 0xF, 0xF, false);
+        V r;
+        __builtin_memcpy(&r, &xi, 4);
+        return r;
+    };
+    v += rot(v, std::integral_constant<int, 0x128>{});  // row_ror:8
+    v += rot(v, std::integral_constant<int, 0x124>{});  // row_ror:4
+    v += rot(v, std::integral_constant<int, 0x122>{});  // row_ror:2
+    v += rot(v, std::integral_constant<int, 0x121>{});  // row_ror:1
+    int vi;
+    __builtin_memcpy(&vi, &v, 4);
+    V r0, r1, r2, r3;
+    int t0 = __builtin_amdgcn_readlane(vi, 0), t1 = __builtin_amdgcn_readlane(vi, 16);
+    int t2 = __builtin_amdgcn_readlane(vi, 32), t3 = __builtin_amdgcn_readlane(vi, 48);
+    __builtin_memcpy(&r0, &t0, 4);
+    __builtin_memcpy(&r1, &t1, 4);
+    __builtin_memcpy(&r2, &t2, 4);
+    __builtin_memcpy(&r3, &t3, 4);
+    return (r0 + r1) + (r2 + r3);
+}
+
+// Two workgroups (eight waves a SIMD) must fit: that caps the scalar
+// registers the unrolled anchor loop may hoist.
+template <bool BWD, bool INT_MODE, int NCMAX>
+__global__ __launch_bounds__(kTbThreads) __attribute__((amdgpu_waves_per_eu(8))) void k_prod_pairs_tbl(
     const float *__restrict__ x1, const float *__restrict__ x2, const float *__restrict__ pe,
     const int2 *__restrict__ anchors, const double *__restrict__ P, float *__restrict__ cnt,
     float *__restrict__ x1_grad, float *__restrict__ x2_grad, float *__restrict__ pe_grad,
     uint32_t S, uint32_t n1, uint32_t n2, uint32_t pd, uint32_t T, uint32_t n_anchors, bool sliced,
     float cmp_eps, double int_rescaler, uint32_t JB, uint32_t n_jblocks) {
+    // int32 payloads are summed as uint32 (wrapping, as the reference's int sums)
+    typedef typename std::conditional<INT_MODE, uint32_t, float>::type push_t;
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t E = 1u << n_anchors;
     const uint32_t NS = 2 * n_anchors;
@@ -230,7 +266,7 @@ __global__ __launch_bounds__(kTbThreads) void k_prod_pairs_tbl(
     const uint32_t j0 = jblk * JB;
     const uint32_t j_end = min(S, j0 + JB);
     const uint32_t R = j_end;  // rows 0 .. j_end-1 (i, j and distances all below j_end)
-    float *acc = xs + (size_t)R * NS;  // BWD only
+    push_t *acc = reinterpret_cast<push_t *>(xs + (size_t)R * NS);  // BWD only
     if (tid < n_anchors) {
         const int2 ap = anchors[(size_t)t * n_anchors + tid];
         int2 c = make_int2(-1, -1);
@@ -238,18 +274,18 @@ __global__ __launch_bounds__(kTbThreads) void k_prod_pairs_tbl(
         uint32_t k1, k2;
         if (ap.x >= 0 && ap.y >= 0 && prod_locate(n1, n2, pd, sliced, (uint32_t)ap.x, s1, k1) &&
             prod_locate(n1, n2, pd, sliced, (uint32_t)ap.y, s2, k2))
-            c = make_int2((s1 << 28) | (int32_t)(2 * tid), (s2 << 28) | (int32_t)(2 * tid + 1));
+            c = make_int2((s1 << 28) | (int32_t)(2 * tid * R), (s2 << 28) | (int32_t)((2 * tid + 1) * R));
         code[tid] = c;
     }
     for (uint32_t e = tid; e < hist_words; e += kTbThreads) hist[e] = 0;
     __syncthreads();
     // stage the slot values of rows 0 .. R-1 (positional slots: distance r, valid r < S-1)
     for (uint32_t e = tid; e < R * NS; e += kTbThreads) {
-        const uint32_t r = e / NS, sidx = e - r * NS;
-        const int2 ap = anchors[(size_t)t * n_anchors + sidx / 2];
+        const uint32_t sidx = e / R, r = e - sidx * R;
         const int2 c = code[sidx / 2];
         float v = 0.0f;
         if (c.x != -1) {
+            const int2 ap = anchors[(size_t)t * n_anchors + sidx / 2];
             int32_t src;
             uint32_t k;
             prod_locate(n1, n2, pd, sliced, (uint32_t)((sidx & 1) ? ap.y : ap.x), src, k);
@@ -258,58 +294,114 @@ __global__ __launch_bounds__(kTbThreads) void k_prod_pairs_tbl(
             else if (r + 1 < S) v = pe[((size_t)r * T + t) * pd + k];
         }
         xs[e] = v;
-        if (BWD) acc[e] = 0.0f;
+        if (BWD) acc[e] = 0;
     }
     __syncthreads();
     const double *Pt = BWD ? P + (size_t)t * E : nullptr;
     const size_t TE = (size_t)T * E;
+    const uint32_t lane = tid & 63;
+    // the anchor codes are the same for every lane: scalar registers
+    int32_t ca[NCMAX], cb[NCMAX];
+#pragma unroll
+    for (int a = 0; a < NCMAX; a++) {
+        const int2 c = (uint32_t)a < n_anchors ? code[a] : make_int2(-1, -1);
+        ca[a] = __builtin_amdgcn_readfirstlane(c.x);
+        cb[a] = __builtin_amdgcn_readfirstlane(c.y);
+    }
+    const bool eps0 = cmp_eps == 0.0f;
     // pairs (i < j, j in the block), j-major, kTbThreads apart per thread
     uint32_t j = j0, i = tid;
     while (j < j_end && i >= j) {
         i -= j;
         j++;
     }
-    while (j < j_end) {
-        const int32_t B0 = (int32_t)(i * NS), B1 = (int32_t)(j * NS), B2 = B1 - B0 - (int32_t)NS;
-        int32_t idx = 0, flip = -1;
-        float md = 3.402823466e+38f;
-        for (uint32_t a = 0; a < n_anchors; a++) {
-            const int2 c = code[a];
-            if (c.x == -1) continue;
-            const int32_t s1 = c.x >> 28, s2 = c.y >> 28;
-            const float v1 = xs[(s1 == 0 ? B0 : (s1 == 1 ? B1 : B2)) + (c.x & 0xFFFFFFF)];
-            const float v2 = xs[(s2 == 0 ? B0 : (s2 == 1 ? B1 : B2)) + (c.y & 0xFFFFFFF)];
-            const float dv = v1 - v2;
-            if (rgreater0(dv, cmp_eps)) idx |= (1 << a);
-            if (fabsf(dv) < fabsf(md)) {
-                md = dv;
-                flip = (int32_t)a;
-            }
-        }
-        const uint32_t h = (j - j0) * E + (uint32_t)idx;
-        atomicAdd(&hist[h >> 1], 1u << (16 * (h & 1)));
-        if (BWD && flip >= 0) {
-            const double *Pbj = Pt + ((size_t)b * S + j) * TE;
-            const double du = du_of_margin(md) * (Pbj[idx] - Pbj[idx ^ (1 << flip)]);
-            if (fabs(du) > kEps) {
-                const int2 c = code[flip];
+    while (true) {
+        const bool active = j < j_end;
+        const uint64_t act = __ballot(active);
+        if (act == 0) break;  // wave-uniform: every lane of the wave leaves together
+        // pushes into the shared row j, summed over the wave below
+        int32_t ps0 = -1, ps1 = -1;
+        push_t pv0 = 0, pv1 = 0;
+        if (active) {
+            const int32_t B0 = (int32_t)i, B1 = (int32_t)j, B2 = (int32_t)(j - i - 1);
+            // every operand read is issued before the first compare
+            float v1[NCMAX], v2[NCMAX];
 #pragma unroll
-                for (int hh = 0; hh < 2; hh++) {
-                    const int32_t cc = hh == 0 ? c.x : c.y;
-                    const int32_t sr = cc >> 28;
-                    const int32_t pos = (sr == 0 ? B0 : (sr == 1 ? B1 : B2)) + (cc & 0xFFFFFFF);
-                    const double v = hh == 0 ? du : -du;
-                    if (INT_MODE)
-                        atomicAdd(reinterpret_cast<int32_t *>(acc + pos), (int32_t)(v * kDenom32 * int_rescaler));
-                    else
-                        atomicAdd(acc + pos, (float)v);
+            for (int a = 0; a < NCMAX; a++) {
+                if (ca[a] == -1) continue;  // uniform
+                const int32_t s1 = ca[a] >> 28, s2 = cb[a] >> 28;
+                v1[a] = xs[(s1 == 0 ? B0 : (s1 == 1 ? B1 : B2)) + (ca[a] & 0xFFFFFFF)];
+                v2[a] = xs[(s2 == 0 ? B0 : (s2 == 1 ? B1 : B2)) + (cb[a] & 0xFFFFFFF)];
+            }
+            int32_t idx = 0, flip = -1;
+            float md = 3.402823466e+38f;
+#pragma unroll
+            for (int a = 0; a < NCMAX; a++) {
+                if (ca[a] == -1) continue;
+                const float dv = v1[a] - v2[a];
+                // ROUNDED_COMPARISON_GREATER(dv, 0, cmp_eps), misc.h:16
+                const bool gt = (dv > 0.0f) & (eps0 | !(fabsf(dv) < cmp_eps));
+                idx |= gt ? (1 << a) : 0;
+                if (fabsf(dv) < fabsf(md)) {
+                    md = dv;
+                    flip = a;
+                }
+            }
+            const uint32_t h = (j - j0) * E + (uint32_t)idx;
+            atomicAdd(&hist[h >> 1], 1u << (16 * (h & 1)));
+            if (BWD && flip >= 0) {
+                const double *Pbj = Pt + ((size_t)b * S + j) * TE;
+                const double du = du_of_margin(md) * (Pbj[idx] - Pbj[idx ^ (1 << flip)]);
+                if (fabs(du) > kEps) {
+                    const int2 c = code[flip];
+#pragma unroll
+                    for (int hh = 0; hh < 2; hh++) {
+                        const int32_t cc = hh == 0 ? c.x : c.y;
+                        const int32_t sr = cc >> 28;
+                        const double v = hh == 0 ? du : -du;
+                        push_t pv;
+                        if (INT_MODE) pv = (push_t)(uint32_t)(int32_t)(v * kDenom32 * int_rescaler);
+                        else pv = (push_t)(float)v;
+                        if (sr == 1) {
+                            if (hh == 0) { ps0 = cc & 0xFFFFFFF; pv0 = pv; }
+                            else { ps1 = cc & 0xFFFFFFF; pv1 = pv; }
+                        } else {
+                            atomicAdd(acc + (sr == 0 ? B0 : B2) + (cc & 0xFFFFFFF), pv);
+                        }
+                    }
                 }
             }
         }
-        i += kTbThreads;
-        while (j < j_end && i >= j) {
-            i -= j;
-            j++;
+        if (BWD) {
+            // every lane of the wave is here; the row j of the first active lane
+            const uint32_t first = (uint32_t)__builtin_ctzll(act);
+            const uint32_t jw = (uint32_t)__builtin_amdgcn_readlane((int)j, (int)first);
+            const bool uniform = __ballot(active && j != jw) == 0;
+            if (!uniform) {
+                if (ps0 >= 0) atomicAdd(acc + ps0 + j, pv0);
+                if (ps1 >= 0) atomicAdd(acc + ps1 + j, pv1);
+            } else if (__ballot(ps0 >= 0 || ps1 >= 0) != 0) {
+#pragma unroll
+                for (int a = 0; a < NCMAX; a++) {
+#pragma unroll
+                    for (int hh = 0; hh < 2; hh++) {
+                        const int32_t cc = hh == 0 ? ca[a] : cb[a];
+                        if (cc == -1 || (cc >> 28) != 1) continue;  // uniform
+                        const int32_t sb = cc & 0xFFFFFFF;
+                        const push_t mine = (ps0 == sb ? pv0 : (push_t)0) + (ps1 == sb ? pv1 : (push_t)0);
+                        if (__ballot(mine != (push_t)0) == 0) continue;
+                        const push_t tot = wave_sum64(mine);
+                        if (lane == first) atomicAdd(acc + sb + jw, tot);
+                    }
+                }
+            }
+        }
+        if (active) {
+            i += kTbThreads;
+            while (j < j_end && i >= j) {
+                i -= j;
+                j++;
+            }
         }
     }
     __syncthreads();
@@ -319,7 +411,7 @@ __global__ __launch_bounds__(kTbThreads) void k_prod_pairs_tbl(
     }
     if (BWD) {
         for (uint32_t e = tid; e < R * NS; e += kTbThreads) {
-            const uint32_t r = e / NS, sidx = e - r * NS;
+            const uint32_t sidx = e / R, r = e - sidx * R;
             const int32_t iv = reinterpret_cast<const int32_t *>(acc)[e];
             if (iv == 0) continue;  // +0.0f, or a zero int32 sum (a -0.0f sum adds nothing either)
             const int2 ap = anchors[(size_t)t * n_anchors + sidx / 2];
@@ -330,7 +422,7 @@ __global__ __launch_bounds__(kTbThreads) void k_prod_pairs_tbl(
                                   : (src == 1 ? x2_grad + ((size_t)b * S + r) * n2 + k
                                               : pe_grad + ((size_t)r * T + t) * pd + k);
             if (INT_MODE) atomicAdd(reinterpret_cast<int32_t *>(dst), iv);
-            else atomicAdd(dst, acc[e]);
+            else atomicAdd(dst, reinterpret_cast<const float *>(acc)[e]);
         }
     }
 }
@@ -656,20 +748,25 @@ hipError_t launch_forward_product(const ProductShape &s, const float *w, const f
     const int2 *anc = reinterpret_cast<const int2 *>(anchors);
     const TableLayout lay = table_grid_ok(s, table_layout(s, false));
     const uint32_t njb = lay.jb ? (s.seq_len + lay.jb - 1) / lay.jb : 0;
+#define SPIKY_PT(IM, NCM)                                                                         \
+    hipLaunchKernelGGL((k_prod_pairs_tbl<false, IM, NCM>), dim3(s.batch * s.n_detectors * njb),   \
+                       dim3(kTbThreads), lay.bytes, st, x1, x2, pe, anc, (const double *)nullptr, \
+                       cnt, (float *)nullptr, (float *)nullptr, (float *)nullptr, s.seq_len,      \
+                       s.n1, s.n2, s.pd, s.n_detectors, s.n_anchors, s.sliced, s.cmp_eps,         \
+                       int_rescaler, lay.jb, njb)
 #define SPIKY_PP(IM)                                                                              \
-    if (lay.jb)                                                                                   \
-        hipLaunchKernelGGL((k_prod_pairs_tbl<false, IM>), dim3(s.batch * s.n_detectors * njb),    \
-                           dim3(kTbThreads), lay.bytes, st, x1, x2, pe, anc,                      \
-                           (const double *)nullptr, cnt, (float *)nullptr, (float *)nullptr,      \
-                           (float *)nullptr, s.seq_len, s.n1, s.n2, s.pd, s.n_detectors,          \
-                           s.n_anchors, s.sliced, s.cmp_eps, int_rescaler, lay.jb, njb);          \
-    else                                                                                          \
+    if (lay.jb) {                                                                                 \
+        if (s.n_anchors <= 4) SPIKY_PT(IM, 4);                                                    \
+        else if (s.n_anchors <= 8) SPIKY_PT(IM, 8);                                               \
+        else SPIKY_PT(IM, 16);                                                                    \
+    } else                                                                                        \
         hipLaunchKernelGGL((k_prod_pairs<false, IM>), dim3(BS), dim3(kPrThreads), TE * 4, st, x1, \
                            x2, pe, anc, (const double *)nullptr, cnt, (float *)nullptr,           \
                            (float *)nullptr, (float *)nullptr, s.seq_len, s.n1, s.n2, s.pd,       \
                            s.n_detectors, s.n_anchors, s.sliced, s.cmp_eps, int_rescaler)
     if (int_mode) { SPIKY_PP(true); } else { SPIKY_PP(false); }
 #undef SPIKY_PP
+#undef SPIKY_PT
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     // out[bj][o] (+)= sum_k cnt[bj][k] * W[k][o]
@@ -701,18 +798,23 @@ hipError_t launch_backward_product(const ProductShape &s, const float *w, const 
     const int2 *anc = reinterpret_cast<const int2 *>(anchors);
     const TableLayout lay = table_grid_ok(s, table_layout(s, true));
     const uint32_t njb = lay.jb ? (s.seq_len + lay.jb - 1) / lay.jb : 0;
+#define SPIKY_BT(IM, NCM)                                                                         \
+    hipLaunchKernelGGL((k_prod_pairs_tbl<true, IM, NCM>), dim3(s.batch * s.n_detectors * njb),    \
+                       dim3(kTbThreads), lay.bytes, st, x1, x2, pe, anc, P, cnt, x1_grad,         \
+                       x2_grad, pe_grad, s.seq_len, s.n1, s.n2, s.pd, s.n_detectors, s.n_anchors, \
+                       s.sliced, s.cmp_eps, int_rescaler, lay.jb, njb)
 #define SPIKY_PB(IM)                                                                              \
-    if (lay.jb)                                                                                   \
-        hipLaunchKernelGGL((k_prod_pairs_tbl<true, IM>), dim3(s.batch * s.n_detectors * njb),     \
-                           dim3(kTbThreads), lay.bytes, st, x1, x2, pe, anc, P, cnt, x1_grad,     \
-                           x2_grad, pe_grad, s.seq_len, s.n1, s.n2, s.pd, s.n_detectors,          \
-                           s.n_anchors, s.sliced, s.cmp_eps, int_rescaler, lay.jb, njb);          \
-    else                                                                                          \
+    if (lay.jb) {                                                                                 \
+        if (s.n_anchors <= 4) SPIKY_BT(IM, 4);                                                    \
+        else if (s.n_anchors <= 8) SPIKY_BT(IM, 8);                                               \
+        else SPIKY_BT(IM, 16);                                                                    \
+    } else                                                                                        \
         hipLaunchKernelGGL((k_prod_pairs<true, IM>), dim3(BS), dim3(kPrThreads), TE * 4, st, x1,  \
                            x2, pe, anc, P, cnt, x1_grad, x2_grad, pe_grad, s.seq_len, s.n1, s.n2, \
                            s.pd, s.n_detectors, s.n_anchors, s.sliced, s.cmp_eps, int_rescaler)
     if (int_mode) { SPIKY_PB(true); } else { SPIKY_PB(false); }
 #undef SPIKY_PB
+#undef SPIKY_BT
     e = hipGetLastError();
     if (e != hipSuccess || target == nullptr) return e;
     // target[k][o] (+)= sum_bj cnt[bj][k] * g'[bj][o]

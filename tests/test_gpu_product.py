@@ -169,6 +169,12 @@ def test_product_wide_rows(oracle, cuda_device):
     run_product(oracle, B=1, S=4, n=6200, T=3, Nc=3, O=8, pd=2, seed=10)
 
 
+@pytest.mark.parametrize("int_rescaler", [None, 0.001])
+def test_product_many_anchors(oracle, cuda_device, int_rescaler):
+    """10 anchors (1024-row tables): the widest anchor bucket of the pass."""
+    run_product(oracle, B=2, S=7, n=12, T=2, Nc=10, O=8, pd=3, int_rescaler=int_rescaler, seed=12)
+
+
 def test_product_shortest_sequence(oracle, cuda_device):
     """S = 2: one pair per sequence; position 0 receives nothing."""
     got = run_product(oracle, B=4, S=2, n=6, T=3, Nc=3, O=10, pd=2, seed=8)
