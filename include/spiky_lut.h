@@ -114,8 +114,9 @@ int spiky_lut_backward_backprop(spiky_lut_manager *m, float *weights, uint32_t b
  * (unused when positional_dim == 0), then fill_outputs_fully_connected_seq into
  * output [B][S][O].  Lookup indices / min deltas / min indices are [B][S][T];
  * positional ones [(S-1)][T].  min_deltas == NULL selects eval mode, and then
- * the three min-delta arguments must all be NULL.  Fully connected managers with
- * sequence_length > 1 only. */
+ * the three min-delta arguments must all be NULL.  Managers with
+ * sequence_length > 1; a sparse manager runs fill_outputs_sparse_seq
+ * (proto:1906-2015) over its compiled connectivity, weights per synapse. */
 int spiky_lut_forward_step_concat(spiky_lut_manager *m, const float *weights, uint32_t batch_size,
                                   const float *input, const int32_t *anchors, float *output,
                                   int32_t *lookup_indices, float cmp_eps,
@@ -129,7 +130,9 @@ int spiky_lut_forward_step_concat(spiky_lut_manager *m, const float *weights, ui
  * [B][S][I] and positional_grad [(S-1)][T][Npe], and gather_w_gradients_seq_fc
  * into weight_grad (external_lr < 0) or, for the Internal policy
  * (external_lr >= 0, weight_grad NULL), the in-place update of weights.
- * overwrite_weight_grad as for spiky_lut_backward_backprop. */
+ * overwrite_weight_grad as for spiky_lut_backward_backprop.  A sparse manager
+ * runs propagate_through_detectors_seq_sparse and gather_w_gradients_seq_sparse
+ * (proto:3371-3627, 3837-3942); its weight gradient is per synapse. */
 int spiky_lut_backward_backprop_concat(spiky_lut_manager *m, float *weights, uint32_t batch_size,
                                        const float *output_grad, const int32_t *anchors,
                                        const int32_t *lookup_indices, const float *min_deltas,

@@ -72,6 +72,14 @@ def lib():
         L.oracle_propagate_product.argtypes = [_f32p, _f32p, _vp, _i32p, _f32p, _f32p, _i64, _i64, _i64,
                                                _i64, _i64, _i64, _i64, _i64, _int, _f32, _f64, _int, _f64,
                                                _f32p, _f32p, _vp, _vp]
+        L.oracle_fill_outputs_seq_sparse.argtypes = [_f32p, _i32p, _vp, _i64p, _i32p, _f32p, _i64, _i64,
+                                                     _i64, _i64, _i64, _i64, _i64, _i64, _int, _f64]
+        L.oracle_propagate_seq_sparse.argtypes = [_f32p, _f32p, _i32p, _f32p, _i32p, _vp, _vp, _vp, _i32p,
+                                                  _i64p, _i32p, _f32p, _vp, _i64, _i64, _i64, _i64, _i64,
+                                                  _i64, _i64, _i64, _i64, _int, _f64, _vp, _vp, _vp, _vp]
+        L.oracle_gather_wgrad_seq_sparse.argtypes = [_f32p, _i32p, _vp, _i64p, _i32p, _f32p, _i64, _i64,
+                                                     _i64, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _int,
+                                                     _f64]
         L.oracle_fill_outputs_product64.argtypes = [_f32p, _f32p, _vp, _i32p, _f32p, _i64, _i64, _i64,
                                                     _i64, _i64, _i64, _i64, _i64, _int, _f32, _vp, _vp]
         L.oracle_propagate_product64.argtypes = [_f32p, _f32p, _vp, _i32p, _f32p, _f32p, _i64, _i64,
@@ -339,3 +347,62 @@ def propagate_product64(x1, x2, pe, anchors, w, g, batch, seq_len, n1, n2, pd, n
                                      _ptr(x_a), _ptr(pe_s), _ptr(pe_a), _ptr(w_s), _ptr(w_a))
     return {"x": (x_s, x_a), "pe": (pe_s, pe_a) if pd > 0 else None,
             "w": (w_s, w_a) if weights else None}
+
+
+# ---------------------------------------------------------------- sequence-concat, sparse
+def fill_outputs_seq_sparse(w, idx, pidx, syn_offsets, syn_targets, batch, seq_len, n_outputs, n_detectors,
+                            n_anchors, positional_dim, fgs, max_groups, int_mode=False, int_rescaler=1.0,
+                            out=None):
+    """Sequence-concat forward over sparse connectivity (proto:1906-2015):
+    out [B*S*O] accumulated into; idx [B*S*T]; pidx [(S-1)*T] or None."""
+    if out is None:
+        out = np.zeros(batch * seq_len * n_outputs, dtype=np.float32)
+    pidx = None if pidx is None or positional_dim == 0 else _c(pidx, np.int32)
+    lib().oracle_fill_outputs_seq_sparse(_c(w, np.float32), _c(idx, np.int32), _ptr(pidx),
+                                         _c(syn_offsets, np.int64), _c(syn_targets, np.int32), out, batch,
+                                         seq_len, n_outputs, n_detectors, n_anchors, positional_dim, fgs,
+                                         max_groups, int(int_mode), float(int_rescaler))
+    return out
+
+
+def propagate_seq_sparse(w, g, idx, md, mi, pidx, pmd, pmi, anchors, syn_offsets, syn_targets, batch,
+                         n_inputs, n_outputs, n_detectors, seq_len, n_anchors, positional_dim, fgs,
+                         max_groups, int_mode=False, int_rescaler=1.0, bounds=False):
+    """Sequence-concat backward into x / pe over sparse connectivity
+    (proto:3371-3627).  Returns (x_grad, pe_grad) and, with bounds, also
+    ((x_sum, x_abs), (pe_sum, pe_abs)): the pushes in fp64 and their magnitudes."""
+    x_grad = np.zeros(batch * seq_len * n_inputs, dtype=np.float32)
+    npe = (seq_len - 1) * n_detectors * positional_dim
+    pe_grad = np.zeros(npe, dtype=np.float32) if positional_dim > 0 else None
+    xs = xa = ps = pa = None
+    if bounds:
+        xs, xa = np.zeros(x_grad.size), np.zeros(x_grad.size)
+        if positional_dim > 0:
+            ps, pa = np.zeros(npe), np.zeros(npe)
+    pd = positional_dim > 0
+    lib().oracle_propagate_seq_sparse(
+        _c(w, np.float32), _c(g, np.float32), _c(idx, np.int32), _c(md, np.float32), _c(mi, np.int32),
+        _ptr(_c(pidx, np.int32) if pd else None), _ptr(_c(pmd, np.float32) if pd else None),
+        _ptr(_c(pmi, np.int32) if pd else None), _c(anchors, np.int32), _c(syn_offsets, np.int64),
+        _c(syn_targets, np.int32), x_grad, _ptr(pe_grad), batch, n_inputs, n_outputs, n_detectors,
+        seq_len, n_anchors, positional_dim, fgs, max_groups, int(int_mode), float(int_rescaler),
+        _ptr(xs), _ptr(xa), _ptr(ps), _ptr(pa))
+    if bounds:
+        return x_grad, pe_grad, (xs, xa), ((ps, pa) if pd else None)
+    return x_grad, pe_grad
+
+
+def gather_wgrad_seq_sparse(g, idx, pidx, syn_offsets, syn_targets, batch, seq_len, n_outputs,
+                            n_detectors, n_anchors, positional_dim, fgs, max_groups, lr=1.0,
+                            external_lr=-1.0, int_mode=False, int_rescaler=1.0, target=None):
+    """Sequence-concat weight gradient over sparse connectivity
+    (proto:3837-3942) into target [n_synapses]."""
+    if target is None:
+        target = np.zeros(int(np.asarray(syn_offsets)[-1]), dtype=np.float32)
+    pidx = None if pidx is None or positional_dim == 0 else _c(pidx, np.int32)
+    lib().oracle_gather_wgrad_seq_sparse(_c(g, np.float32), _c(idx, np.int32), _ptr(pidx),
+                                         _c(syn_offsets, np.int64), _c(syn_targets, np.int32), target,
+                                         batch, seq_len, n_outputs, n_detectors, n_anchors,
+                                         positional_dim, fgs, max_groups, float(lr), float(external_lr),
+                                         int(int_mode), float(int_rescaler))
+    return target

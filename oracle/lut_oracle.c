@@ -596,6 +596,189 @@ void oracle_gather_wgrad_seq(
 }
 
 /* ------------------------------------------------------------------------ */
+/* Sequence-concat over sparse lookup connectivity (this build's CSR: lookup */
+/* neuron n owns synapses [syn_offsets[n], syn_offsets[n+1]), forward group  */
+/* g = its synapses g*fgs .. g*fgs+fgs-1 in list order; W is per synapse).   */
+/* fill_outputs_sparse_seq_logic (proto:1906-2015),                          */
+/* propagate_through_detectors_seq_sparse_logic (proto:3371-3627) and        */
+/* gather_w_gradients_seq_sparse_logic (proto:3837-3942) in the serial order */
+/* of the reference CPU path: (b, group) -> (32x32 tile, detector) -> tile   */
+/* thread, whose pair is i = ti*32 + tid/32, j = tj*32 + tid%32 (these       */
+/* kernels index the tile the other way round from the FC ones).             */
+/* ------------------------------------------------------------------------ */
+#define FOR_SEQ_PAIRS_SPARSE(B, S, NOB, T, ...)                                        \
+    do {                                                                               \
+        int64_t tgw_ = ((S) + OR_TILE - 1) / OR_TILE;                                  \
+        for (int64_t b = 0; b < (B); b++)                                              \
+            for (int64_t ob = 0; ob < (NOB); ob++)                                     \
+                for (int64_t tile_ = 0; tile_ < tgw_ * tgw_; tile_++) {                \
+                    int64_t ti_ = tile_ / tgw_, tj_ = tile_ % tgw_;                    \
+                    if (ti_ > tj_) continue;                                           \
+                    for (int64_t t = 0; t < (T); t++)                                  \
+                        for (int64_t tid_ = 0; tid_ < OR_TILE * OR_TILE; tid_++) {     \
+                            int64_t i = ti_ * OR_TILE + tid_ / OR_TILE;                \
+                            int64_t j = tj_ * OR_TILE + tid_ % OR_TILE;                \
+                            if (i >= j || j >= (S)) continue;                          \
+                            __VA_ARGS__                                                \
+                        }                                                              \
+                }                                                                      \
+    } while (0)
+
+/* synapses of forward group ob of neuron n: [*s0, *s1), empty if absent */
+static inline void group_range(const int64_t *syn_offsets, int64_t n, int64_t ob, int64_t fgs,
+                               int64_t *s0, int64_t *s1)
+{
+    *s0 = syn_offsets[n] + ob * fgs;
+    *s1 = *s0 + fgs < syn_offsets[n + 1] ? *s0 + fgs : syn_offsets[n + 1];
+    if (*s0 > *s1) *s0 = *s1;
+}
+
+static inline double group_dot(const float *w, const int64_t *syn_offsets, const int32_t *syn_targets,
+                               int64_t n, int64_t ob, int64_t fgs, const float *gj)
+{
+    int64_t s0, s1;
+    double acc = 0.0;
+    group_range(syn_offsets, n, ob, fgs, &s0, &s1);
+    for (int64_t s = s0; s < s1; s++) acc += (double)w[s] * (double)gj[syn_targets[s]];
+    return acc;
+}
+
+/* out [B][S][O]: each synapse of the pair's group commits (float)(double)w  */
+/* (fire_single_synapse_group, proto:215-313), or its int32 payload.          */
+void oracle_fill_outputs_seq_sparse(
+    const float *w, const int32_t *idx, const int32_t *pidx, const int64_t *syn_offsets,
+    const int32_t *syn_targets, float *out, int64_t batch, int64_t seq_len, int64_t n_outputs,
+    int64_t n_detectors, int64_t n_anchors, int64_t positional_dim, int64_t fgs, int64_t max_groups,
+    int int_mode, double int_rescaler)
+{
+    const int64_t nlpd = (int64_t)1 << (2 * n_anchors + positional_dim);
+    FOR_SEQ_PAIRS_SPARSE(batch, seq_len, max_groups, n_detectors, {
+        int32_t K = idx[(b * seq_len + i) * n_detectors + t];
+        int32_t Q = idx[(b * seq_len + j) * n_detectors + t];
+        int32_t P = positional_dim > 0 ? pidx[(j - i - 1) * n_detectors + t] : 0;
+        int64_t n = t * nlpd + seq_row(Q, K, P, n_anchors, positional_dim);
+        int64_t s0, s1;
+        group_range(syn_offsets, n, ob, fgs, &s0, &s1);
+        float *oj = out + (b * seq_len + j) * n_outputs;
+        for (int64_t s = s0; s < s1; s++) {
+            int32_t tg = syn_targets[s];
+            double wt = (double)w[s];
+            if (int_mode)
+                as_i32(oj)[tg] = wrap_add(as_i32(oj)[tg], (int32_t)(wt * OR_DENOM32 * int_rescaler));
+            else
+                oj[tg] += (float)wt;
+        }
+    });
+}
+
+/* As oracle_propagate_seq over the pair's group ob of the main, flipped and */
+/* PE-flipped neurons.  x_sum / x_abs / pe_sum / pe_abs (fp32 summation,     */
+/* may be null): when given, the pushes are also accumulated there in fp64   */
+/* with their magnitudes -- the bound for a device path that adds the same   */
+/* terms in another order.                                                   */
+void oracle_propagate_seq_sparse(
+    const float *w, const float *g, const int32_t *idx, const float *md, const int32_t *mi,
+    const int32_t *pidx, const float *pmd, const int32_t *pmi, const int32_t *anchors,
+    const int64_t *syn_offsets, const int32_t *syn_targets, float *x_grad, float *pe_grad,
+    int64_t batch, int64_t n_inputs, int64_t n_outputs, int64_t n_detectors, int64_t seq_len,
+    int64_t n_anchors, int64_t positional_dim, int64_t fgs, int64_t max_groups, int int_mode,
+    double int_rescaler, double *x_sum, double *x_abs, double *pe_sum, double *pe_abs)
+{
+    const int64_t nlpd = (int64_t)1 << (2 * n_anchors + positional_dim);
+    const int64_t pd = positional_dim;
+    FOR_SEQ_PAIRS_SPARSE(batch, seq_len, max_groups, n_detectors, {
+        int64_t ko = (b * seq_len + i) * n_detectors + t, qo = (b * seq_len + j) * n_detectors + t;
+        int32_t K = idx[ko], Q = idx[qo];
+        int32_t km = mi[ko], qm = mi[qo];
+        float kd = md[ko], qd = md[qo];
+        int32_t P = 0, pm = -1;
+        float pdl = 0.0f;
+        int64_t pe_off = (j - i - 1) * n_detectors + t;
+        if (pd > 0) {
+            P = pidx[pe_off];
+            pm = pmi[pe_off];
+            pdl = pmd[pe_off];
+        }
+        const float *gj = g + (b * seq_len + j) * n_outputs;
+        int64_t main_n = t * nlpd + seq_row(Q, K, P, n_anchors, pd);
+        int64_t alt_n, src_pos;
+        int32_t flip;
+        double du;
+        if (fabsf(qd) < fabsf(kd)) {
+            alt_n = t * nlpd + seq_row(qm >= 0 ? Q ^ (1 << qm) : Q, K, P, n_anchors, pd);
+            du = du_of_margin(qd);
+            flip = qm;
+            src_pos = j;
+        } else {
+            alt_n = t * nlpd + seq_row(Q, km >= 0 ? K ^ (1 << km) : K, P, n_anchors, pd);
+            du = du_of_margin(kd);
+            flip = km;
+            src_pos = i;
+        }
+        double ms = group_dot(w, syn_offsets, syn_targets, main_n, ob, fgs, gj);
+        double as = group_dot(w, syn_offsets, syn_targets, alt_n, ob, fgs, gj);
+        du *= ms - as;
+        if (flip >= 0) {
+            const int32_t *ap = anchors + (t * n_anchors + flip) * 2;
+            int64_t row = (b * seq_len + src_pos) * n_inputs;
+            push_input_grad(x_grad + row, ap[0], ap[1], du, int_mode, int_rescaler);
+            if (x_sum && fabs(du) > OR_EPS) {
+                double f = (double)(float)du;
+                x_sum[row + ap[0]] += f;
+                x_abs[row + ap[0]] += fabs(f);
+                x_sum[row + ap[1]] -= f;
+                x_abs[row + ap[1]] += fabs(f);
+            }
+        }
+        if (pd > 0 && fabsf(pdl) < fabsf(qd) && fabsf(pdl) < fabsf(kd) && pm >= 0) {
+            int64_t pe_n = t * nlpd + seq_row(Q, K, P ^ (1 << pm), n_anchors, pd);
+            double dpe = du_of_margin(pdl) * (ms - group_dot(w, syn_offsets, syn_targets, pe_n, ob, fgs, gj));
+            float *dst = pe_grad + pe_off * pd + pm;
+            if (int_mode)
+                *as_i32(dst) = wrap_add(*as_i32(dst), (int32_t)(dpe * OR_DENOM32 * int_rescaler));
+            else
+                *dst = (float)((double)*dst + dpe);
+            if (pe_sum) {
+                double f = (double)(float)dpe;
+                pe_sum[pe_off * pd + pm] += f;
+                pe_abs[pe_off * pd + pm] += fabs(f);
+            }
+        }
+    });
+}
+
+/* target [n_synapses]: every synapse of the pair's group adds                */
+/* (float)(g[b][j][target] * lr) where |g| > EPS (gather_weight_gradients_sparse, */
+/* proto:584-714).                                                            */
+void oracle_gather_wgrad_seq_sparse(
+    const float *g, const int32_t *idx, const int32_t *pidx, const int64_t *syn_offsets,
+    const int32_t *syn_targets, float *target, int64_t batch, int64_t seq_len, int64_t n_outputs,
+    int64_t n_detectors, int64_t n_anchors, int64_t positional_dim, int64_t fgs, int64_t max_groups,
+    float first_meta_lr, float external_lr, int int_mode, double int_rescaler)
+{
+    const int64_t nlpd = (int64_t)1 << (2 * n_anchors + positional_dim);
+    double lr = (double)first_meta_lr;
+    if (external_lr >= 0) lr *= -(double)external_lr;
+    FOR_SEQ_PAIRS_SPARSE(batch, seq_len, max_groups, n_detectors, {
+        int32_t K = idx[(b * seq_len + i) * n_detectors + t];
+        int32_t Q = idx[(b * seq_len + j) * n_detectors + t];
+        int32_t P = positional_dim > 0 ? pidx[(j - i - 1) * n_detectors + t] : 0;
+        int64_t n = t * nlpd + seq_row(Q, K, P, n_anchors, positional_dim);
+        int64_t s0, s1;
+        group_range(syn_offsets, n, ob, fgs, &s0, &s1);
+        const float *gj = g + (b * seq_len + j) * n_outputs;
+        for (int64_t s = s0; s < s1; s++) {
+            double gg = (double)gj[syn_targets[s]];
+            if (!(fabs(gg) > OR_EPS)) continue;
+            if (int_mode)
+                as_i32(target)[s] = wrap_add(as_i32(target)[s], (int32_t)(gg * lr * OR_DENOM32 * int_rescaler));
+            else
+                target[s] += (float)(gg * lr);
+        }
+    });
+}
+
+/* ------------------------------------------------------------------------ */
 /* Product mode (concatenation_product == False): every causal pair i < j   */
 /* of a sequence is one LUT lookup over the virtual input row               */
 /* [x1[i] (n1) | x2[j] (n2) | pe[j-i-1][t] (pd)] (or, in sliced mode, the   */

@@ -10,7 +10,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libspiky_lut.so")
-SOURCES = ["lut_fc.hip", "lut_tm.hip", "lut_seq.hip", "lut_sparse.hip", "lut_densify.hip", "lut_product.hip",
+SOURCES = ["lut_fc.hip", "lut_tm.hip", "lut_seq.hip", "lut_sparse.hip", "lut_densify.hip", "lut_product.hip", "lut_seq_sparse.hip",
            "lut_builder.hip", "lut_capi.hip"]
 ARCH = os.environ.get("SPIKY_OFFLOAD_ARCH", "gfx950")
 

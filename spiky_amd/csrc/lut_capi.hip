@@ -365,7 +365,6 @@ int spiky_lut_set_sparse_connectivity(spiky_lut_manager *m, const int64_t *syn_o
     return guarded([&] {
         require_manager(m);
         if (m->fully_connected != 0) throw ValueError("can't add lookup connections in fully connected mode");
-        if (m->sequence_length != 1) throw ValueError("sparse connectivity needs sequence_length == 1");
         if (!syn_offsets || (n_synapses && !syn_targets)) throw ValueError("null connectivity arrays");
         const uint64_t nl = m->n_lookup;
         if (syn_offsets[0] != 0 || (uint64_t)syn_offsets[nl] != n_synapses)
@@ -384,7 +383,7 @@ int spiky_lut_set_sparse_connectivity(spiky_lut_manager *m, const int64_t *syn_o
         m->syn_targets.assign(syn_targets, syn_targets + n_synapses);
         m->max_groups = max_groups;
         // uniform topology: all lookup neurons of a detector share one ordered target list
-        const uint32_t E = m->n_entries();
+        const uint32_t E = (uint32_t)(m->n_lookup / m->n_detectors);  // rows of a table
         bool uniform = true;
         for (uint32_t t = 0; t < m->n_detectors && uniform; t++) {
             const uint64_t n0 = (uint64_t)t * E;
@@ -644,8 +643,6 @@ static void require_seq(const spiky_lut_manager *m, uint32_t batch_size, const c
     if (m->sequence_length <= 1)
         throw ValueError(std::string(what) + " should only be called when sequence_length > 1");
     require_initialized(m);
-    if (m->fully_connected != 1)
-        throw ValueError("sequence mode is built for fully connected managers only");
     if (2 * m->n_anchors + m->positional_dim > 24)
         throw ValueError("2 * n_anchors_per_detector + positional_dim > 24 is not supported");
     if ((uint64_t)batch_size * m->sequence_length > 0x7fffffffull)
@@ -678,6 +675,29 @@ int spiky_lut_forward_step_concat(spiky_lut_manager *m, const float *weights, ui
         m->context_active = true;
         const hipStream_t st = as_stream(stream);
         const spiky::SeqShape s = seq_shape(m, batch_size);
+        if (m->fully_connected != 1) {
+            // sparse lookup connectivity (lut_runtime.cu:518-545)
+            m->sync_connectivity();
+            if (!spiky::seq_sparse_applies(s, m->max_groups))
+                throw ValueError("sequence shape too large for the sparse sequence path");
+            m->timed("check_detectors_seq", st, [&] {
+                check_hip(spiky::launch_seq_indices(s, input, anchors, positional_embeddings,
+                                                    lookup_indices, positional_lookup_indices,
+                                                    min_deltas, min_delta_indices,
+                                                    positional_min_deltas,
+                                                    positional_min_delta_indices, cmp_eps, st),
+                          "check_detectors_seq");
+            });
+            m->timed("fill_outputs_sparse_seq", st, [&] {
+                check_hip(spiky::launch_fill_seq_sparse(s, m->max_groups, weights, lookup_indices,
+                                                        positional_lookup_indices,
+                                                        (const int64_t *)m->d_syn_offsets.ptr,
+                                                        (const int32_t *)m->d_syn_targets.ptr, output,
+                                                        m->int_mode, m->int_rescaler, st),
+                          "forward_step_concat");
+            });
+            return;
+        }
         void *scr = m->scratch_fwd.ensure(spiky::seq_scratch_bytes(s, false));
         m->timed("fill_outputs_seq", st, [&] {
             check_hip(spiky::launch_forward_seq(s, weights, input, anchors, positional_embeddings,
@@ -722,6 +742,24 @@ int spiky_lut_backward_backprop_concat(spiky_lut_manager *m, float *weights, uin
         if (ext >= 0.0f) lr *= -(double)ext;
         float *target = (ext >= 0.0f) ? weights : weight_grad;
         const bool overwrite = overwrite_weight_grad != 0 && target == weight_grad;
+        if (m->fully_connected != 1) {
+            // sparse lookup connectivity (lut_runtime.cu:639-740)
+            m->sync_connectivity();
+            if (!spiky::seq_sparse_applies(s, m->max_groups))
+                throw ValueError("sequence shape too large for the sparse sequence path");
+            m->timed("backward_seq_sparse", st, [&] {
+                check_hip(spiky::launch_backward_seq_sparse(
+                              s, m->max_groups, weights, output_grad, anchors, lookup_indices,
+                              min_deltas, min_delta_indices, positional_lookup_indices,
+                              positional_min_deltas, positional_min_delta_indices,
+                              (const int64_t *)m->d_syn_offsets.ptr,
+                              (const int32_t *)m->d_syn_targets.ptr, m->syn_targets.size(),
+                              input_grad, positional_grad, target, lr, overwrite, m->int_mode,
+                              m->int_rescaler, st),
+                          "backward_backprop_concat");
+            });
+            return;
+        }
         void *scr = m->scratch.ensure(spiky::seq_scratch_bytes(s, true));
         m->timed("backward_seq", st, [&] {
             check_hip(spiky::launch_backward_seq(s, weights, output_grad, anchors, lookup_indices,

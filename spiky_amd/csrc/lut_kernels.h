@@ -171,6 +171,30 @@ hipError_t launch_wgrad_sparse(const SparseShape &s, const float *g, const int32
                                void *scratch, uint64_t n_synapses, hipStream_t st);
 
 // ---- product mode (concatenation_product == False, lut_product.hip) ---------
+// Sequence-concat over sparse connectivity (lut_seq_sparse.hip).  The lookup
+// indices of the B*S rows and of the distances (check_detectors_seq,
+// check_positional_embeddings) come from launch_seq_indices.
+hipError_t launch_seq_indices(const SeqShape &s, const float *x, const int32_t *anchors,
+                              const float *pe, int32_t *idx, int32_t *pidx, float *md, int32_t *mi,
+                              float *pmd, int32_t *pmi, float cmp_eps, hipStream_t st);
+bool seq_sparse_applies(const SeqShape &s, uint32_t max_groups);
+// out (+)= the pairs' synapse weights; int32 payloads converted at the end.
+hipError_t launch_fill_seq_sparse(const SeqShape &s, uint32_t max_groups, const float *w,
+                                  const int32_t *idx, const int32_t *pidx, const int64_t *syn_offsets,
+                                  const int32_t *syn_targets, float *out, bool int_mode,
+                                  double int_rescaler, hipStream_t st);
+// Input and positional gradients, and (target != null) the synapse weight
+// gradient with lr (target == w: the Internal policy, applied after the
+// input gradient read the weights).
+hipError_t launch_backward_seq_sparse(const SeqShape &s, uint32_t max_groups, const float *w,
+                                      const float *g, const int32_t *anchors, const int32_t *idx,
+                                      const float *md, const int32_t *mi, const int32_t *pidx,
+                                      const float *pmd, const int32_t *pmi,
+                                      const int64_t *syn_offsets, const int32_t *syn_targets,
+                                      uint64_t n_synapses, float *x_grad, float *pe_grad,
+                                      float *target, double lr, bool overwrite, bool int_mode,
+                                      double int_rescaler, hipStream_t st);
+
 struct ProductShape {
     uint32_t batch, seq_len, n1, n2, pd, n_detectors, n_anchors, n_outputs;
     bool sliced;

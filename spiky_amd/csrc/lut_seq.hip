@@ -1296,6 +1296,33 @@ size_t seq_scratch_bytes(const SeqShape &s, bool backward) {
     return n;
 }
 
+hipError_t launch_seq_indices(const SeqShape &s, const float *x, const int32_t *anchors,
+                              const float *pe, int32_t *idx, int32_t *pidx, float *md, int32_t *mi,
+                              float *pmd, int32_t *pmi, float cmp_eps, hipStream_t st) {
+    FcShape fs{};
+    fs.batch = s.batch * s.seq;
+    fs.n_inputs = s.n_inputs;
+    fs.n_outputs = s.n_outputs;
+    fs.n_detectors = s.n_detectors;
+    fs.n_anchors = s.n_anchors;
+    fs.n_entries = 1u << s.n_anchors;
+    fs.dgs = s.dgs;
+    fs.ogs = s.ogs;
+    hipError_t e = launch_check_detectors(fs, x, anchors, cmp_eps, idx, md, mi, st);
+    if (e != hipSuccess) return e;
+    const uint32_t n_pe = (s.seq - 1) * s.n_detectors;
+    if (s.pe_dim > 0 && n_pe > 0) {
+        if (md)
+            hipLaunchKernelGGL(k_check_pe<true>, dim3(blocks_for(n_pe)), dim3(kBlock), 0, st, pe,
+                               n_pe, s.pe_dim, cmp_eps, pidx, pmd, pmi);
+        else
+            hipLaunchKernelGGL(k_check_pe<false>, dim3(blocks_for(n_pe)), dim3(kBlock), 0, st, pe,
+                               n_pe, s.pe_dim, cmp_eps, pidx, (float *)nullptr, (int32_t *)nullptr);
+        e = hipGetLastError();
+    }
+    return e;
+}
+
 hipError_t launch_forward_seq(const SeqShape &s, const float *w, const float *x,
                               const int32_t *anchors, const float *pe, float *out, int32_t *idx,
                               int32_t *pidx, float *md, int32_t *mi, float *pmd, int32_t *pmi,
@@ -1311,19 +1338,9 @@ hipError_t launch_forward_seq(const SeqShape &s, const float *w, const float *x,
     fs.n_entries = 1u << s.n_anchors;
     fs.dgs = s.dgs;
     fs.ogs = s.ogs;
-    hipError_t e = launch_check_detectors(fs, x, anchors, cmp_eps, idx, md, mi, st);
+    hipError_t e = launch_seq_indices(s, x, anchors, pe, idx, pidx, md, mi, pmd, pmi, cmp_eps, st);
     if (e != hipSuccess) return e;
     const uint32_t n_pe = (s.seq - 1) * s.n_detectors;
-    if (s.pe_dim > 0) {
-        if (md)
-            hipLaunchKernelGGL(k_check_pe<true>, dim3(blocks_for(n_pe)), dim3(kBlock), 0, st, pe,
-                               n_pe, s.pe_dim, cmp_eps, pidx, pmd, pmi);
-        else
-            hipLaunchKernelGGL(k_check_pe<false>, dim3(blocks_for(n_pe)), dim3(kBlock), 0, st, pe,
-                               n_pe, s.pe_dim, cmp_eps, pidx, (float *)nullptr, (int32_t *)nullptr);
-        e = hipGetLastError();
-        if (e != hipSuccess) return e;
-    }
     uint8_t *sp = reinterpret_cast<uint8_t *>(scratch);
     uint2 *pack = reinterpret_cast<uint2 *>(sp);
     uint2 *ppack = reinterpret_cast<uint2 *>(sp + align256((size_t)rows * s.n_detectors * 8));

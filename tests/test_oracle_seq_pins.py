@@ -200,3 +200,75 @@ def test_seq_backward_fp64_accumulation(oracle):
             scale = np.abs(xg64).reshape(B * S, I).max(axis=1, keepdims=True) * 4 + 1e-30
             err = np.abs(xg32.astype(np.float64) - xg64).reshape(B * S, I)
             assert np.all(err <= n * 2.0 ** -24 * scale)
+
+
+# ---------------------------------------------------------------- sparse connectivity
+def full_csr(T, E, O):
+    """Every lookup neuron targets every output in order: the sparse layout of
+    an FC table (synapse n*O + o is W[n][o])."""
+    n = T * E
+    return (np.arange(n + 1, dtype=np.int64) * O, np.tile(np.arange(O, dtype=np.int32), n))
+
+
+@pytest.mark.parametrize("Npe", [0, 2])
+def test_seq_sparse_full_connectivity_is_the_fc_path(oracle, Npe):
+    """With a CSR that lists every output of every neuron in order and groups
+    of ogs synapses, the sparse sequence functions see exactly the FC terms:
+    forward and weight gradient equal the FC oracle (integer values, exact);
+    int32 input / positional gradients equal bit for bit; fp32 ones hold the
+    same terms (both within their fp32 bound of the fp64 sum)."""
+    rng = np.random.default_rng(21)
+    B, S, I, T, Nc, O, ogs = 2, 7, 9, 3, 2, 10, 4
+    E = 1 << (2 * Nc + Npe)
+    idx, md, mi, pidx, pmd, pmi, W, anchors = rand_case(rng, B, S, I, T, Nc, Npe, O, int_weights=True)
+    off, tg = full_csr(T, E, O)
+    n_grp = (O + ogs - 1) // ogs
+    f_fc = oracle.fill_outputs_seq(W, idx.reshape(-1), pidx, B, O, T, S, Nc, Npe)
+    f_sp = oracle.fill_outputs_seq_sparse(W, idx.reshape(-1), pidx, off, tg, B, S, O, T, Nc, Npe, ogs, n_grp)
+    assert np.array_equal(f_fc, f_sp)
+    gi = rng.integers(-3, 4, size=B * S * O).astype(np.float32)
+    w_fc = np.zeros(W.size, np.float32)
+    oracle.gather_wgrad_seq(gi, idx.reshape(-1), pidx, w_fc, B, O, T, S, Nc, Npe, ogs=ogs, first_meta_lr=0.5)
+    w_sp = oracle.gather_wgrad_seq_sparse(gi, idx.reshape(-1), pidx, off, tg, B, S, O, T, Nc, Npe, ogs, n_grp,
+                                          lr=0.5)
+    assert np.array_equal(w_fc, w_sp)
+    g = rng.standard_normal(B * S * O).astype(np.float32)
+    args = (W, g, idx.reshape(-1), md.reshape(-1), mi.reshape(-1), pidx, pmd, pmi, anchors)
+    xi_fc, pi_fc = oracle.propagate_seq(*args, B, I, O, T, S, Nc, Npe, ogs=ogs, int_mode=True, int_rescaler=0.01)
+    xi_sp, pi_sp = oracle.propagate_seq_sparse(*args, off, tg, B, I, O, T, S, Nc, Npe, ogs, n_grp,
+                                               int_mode=True, int_rescaler=0.01)
+    assert np.array_equal(xi_fc.view(np.int32), xi_sp.view(np.int32))
+    if Npe:
+        assert np.array_equal(pi_fc.view(np.int32), pi_sp.view(np.int32))
+    xf, pf, (xs, xa), pb = oracle.propagate_seq_sparse(*args, off, tg, B, I, O, T, S, Nc, Npe, ogs, n_grp,
+                                                       bounds=True)
+    x64, _ = oracle.propagate_seq(*args, B, I, O, T, S, Nc, Npe, ogs=ogs, acc64=True)
+    n = 2 * T * S * n_grp
+    assert np.all(np.abs(x64 - xs) <= n * 2.0 ** -24 * xa + 1e-30)  # same terms
+    assert np.all(np.abs(xf - xs) <= n * 2.0 ** -24 * xa)
+    assert xa.max() > 0
+
+
+def test_seq_sparse_forward_brute_force(oracle):
+    """A random sparse topology (ragged neurons, empty ones, repeated targets)
+    against a direct loop over pairs and synapses, integer weights (exact)."""
+    rng = np.random.default_rng(22)
+    B, S, T, Nc, Npe, O, fgs = 2, 6, 2, 2, 1, 7, 3
+    E = 1 << (2 * Nc + Npe)
+    counts = rng.integers(0, 8, size=T * E)
+    off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    tg = rng.integers(0, O, size=off[-1]).astype(np.int32)
+    W = rng.integers(-5, 6, size=off[-1]).astype(np.float32)
+    idx = rng.integers(0, 1 << Nc, size=(B, S, T)).astype(np.int32)
+    pidx = rng.integers(0, 1 << Npe, size=(S - 1, T)).astype(np.int32)
+    max_groups = int((counts.max() + fgs - 1) // fgs)
+    got = oracle.fill_outputs_seq_sparse(W, idx.reshape(-1), pidx, off, tg, B, S, O, T, Nc, Npe, fgs, max_groups)
+    want = np.zeros((B, S, O), np.float64)
+    for b in range(B):
+        for j in range(S):
+            for i in range(j):
+                for t in range(T):
+                    n = t * E + np_row(idx[b, j, t], idx[b, i, t], pidx[j - i - 1, t], Nc, Npe)
+                    for s_ in range(off[n], off[n + 1]):
+                        want[b, j, tg[s_]] += W[s_]
+    assert np.array_equal(got, want.reshape(-1).astype(np.float32))
