@@ -143,15 +143,15 @@ int spiky_lut_backward_backprop_concat(spiky_lut_manager *m, float *weights, uin
                                        float *positional_grad, float *weight_grad,
                                        int overwrite_weight_grad, void *stream);
 
-/* Replaces forward_step_product (lut.cu:847-943 -> lut_runtime.cu:852-1049),
- * fully connected managers.  The manager is built with sequence_length 1 and
+/* Replaces forward_step_product (lut.cu:847-943 -> lut_runtime.cu:852-1049).  The manager is built with sequence_length 1 and
  * n_inputs = n_inputs_1 + n_inputs_2 + positional_dim; sequence_length is the
  * real one.  Every pair i < j of a sequence looks up each table over the
  * virtual row [input_1[i] | input_2[j] | pe[(j-i-1)*T + t]] (sliced_mode:
  * interleaved, virtual id = 3 * k + source).  output [B*S*O] is summed into
  * (int32 summation: the caller zeroes it; it is converted to float here).
  * positional_embeddings [(S-1)*T*pd] when positional_dim > 0.  Anchor ids
- * beyond the virtual row are skipped like unused (-1) ones. */
+ * beyond the virtual row are skipped like unused (-1) ones.  A sparse manager
+ * runs fill_outputs_product_sparse (proto:2266-2394) over its connectivity. */
 int spiky_lut_forward_step_product(spiky_lut_manager *m, const float *weights, uint32_t batch_size,
                                    uint32_t sequence_length, const float *input_1,
                                    const float *input_2, const int32_t *anchors, float *output,

@@ -80,6 +80,16 @@ def lib():
         L.oracle_gather_wgrad_seq_sparse.argtypes = [_f32p, _i32p, _vp, _i64p, _i32p, _f32p, _i64, _i64,
                                                      _i64, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _int,
                                                      _f64]
+        L.oracle_fill_outputs_product_sparse.argtypes = [_f32p, _f32p, _vp, _i32p, _f32p, _i64p, _i32p,
+                                                         _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                                         _int, _f32, _int, _f64, _vp, _vp, _vp]
+        L.oracle_propagate_product_sparse.argtypes = [_f32p, _f32p, _vp, _i32p, _f32p, _i64p, _i32p, _f32p,
+                                                      _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int,
+                                                      _f32, _f64, _int, _f64, _f32p, _f32p, _vp, _vp]
+        L.oracle_propagate_product_sparse64.argtypes = [_f32p, _f32p, _vp, _i32p, _f32p, _i64p, _i32p,
+                                                        _f32p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                                        _i64, _int, _f32, _f64, _vp, _vp, _vp, _vp, _vp,
+                                                        _vp, _vp, _vp]
         L.oracle_fill_outputs_product64.argtypes = [_f32p, _f32p, _vp, _i32p, _f32p, _i64, _i64, _i64,
                                                     _i64, _i64, _i64, _i64, _i64, _int, _f32, _vp, _vp]
         L.oracle_propagate_product64.argtypes = [_f32p, _f32p, _vp, _i32p, _f32p, _f32p, _i64, _i64,
@@ -406,3 +416,52 @@ def gather_wgrad_seq_sparse(g, idx, pidx, syn_offsets, syn_targets, batch, seq_l
                                          positional_dim, fgs, max_groups, float(lr), float(external_lr),
                                          int(int_mode), float(int_rescaler))
     return target
+
+
+# ---------------------------------------------------------------- product mode, sparse
+def fill_outputs_product_sparse(x1, x2, pe, anchors, w, syn_offsets, syn_targets, batch, seq_len, n1, n2,
+                                pd, n_detectors, n_anchors, n_outputs, sliced=False, cmp_eps=0.0,
+                                int_mode=False, int_rescaler=1.0, bounds=False):
+    """Product-mode forward over sparse connectivity (w per synapse).  Returns
+    out [B*S*O] (fp32 / int32 payloads), or with bounds the fp64 (sum, abs)
+    of the terms."""
+    m = batch * seq_len * n_outputs
+    out = np.zeros(m, dtype=np.float32)
+    tot = mag = None
+    if bounds:
+        tot, mag = np.zeros(m), np.zeros(m)
+    pe = None if pe is None or pd == 0 else _c(pe, np.float32)
+    lib().oracle_fill_outputs_product_sparse(
+        _c(x1, np.float32), _c(x2, np.float32), _ptr(pe), _c(anchors, np.int32), _c(w, np.float32),
+        _c(syn_offsets, np.int64), _c(syn_targets, np.int32), batch, seq_len, n1, n2, pd, n_detectors,
+        n_anchors, n_outputs, int(sliced), float(cmp_eps), int(int_mode), float(int_rescaler),
+        None if bounds else _ptr(out), _ptr(tot), _ptr(mag))
+    return (tot, mag) if bounds else out
+
+
+def propagate_product_sparse(x1, x2, pe, anchors, w, syn_offsets, syn_targets, g, batch, seq_len, n1, n2,
+                             pd, n_detectors, n_anchors, n_outputs, sliced=False, cmp_eps=0.0, lr=1.0,
+                             int_mode=False, int_rescaler=1.0, weights=True, bounds=False):
+    """Product-mode backward over sparse connectivity with x1 is x2.  Returns
+    (x_grad, pe_grad, w_grad [n_synapses] or None) or, with bounds,
+    {"x", "pe", "w"} -> fp64 (sum, abs) of the terms."""
+    nx = batch * seq_len * n1
+    npe = (seq_len - 1) * n_detectors * pd
+    nsyn = int(np.asarray(syn_offsets)[-1])
+    pe = None if pe is None or pd == 0 else _c(pe, np.float32)
+    common = (_c(x1, np.float32), _c(x2, np.float32), _ptr(pe), _c(anchors, np.int32), _c(w, np.float32),
+              _c(syn_offsets, np.int64), _c(syn_targets, np.int32), _c(g, np.float32), batch, seq_len, n1,
+              n2, pd, n_detectors, n_anchors, n_outputs, int(sliced), float(cmp_eps), float(lr))
+    if bounds:
+        xs, xa = np.zeros(nx), np.zeros(nx)
+        ps, pa = (np.zeros(npe), np.zeros(npe)) if pd > 0 else (None, None)
+        ws, wa = (np.zeros(nsyn), np.zeros(nsyn)) if weights else (None, None)
+        lib().oracle_propagate_product_sparse64(*common, _ptr(xs), _ptr(xa), _ptr(xs), _ptr(xa), _ptr(ps),
+                                                _ptr(pa), _ptr(ws), _ptr(wa))
+        return {"x": (xs, xa), "pe": (ps, pa) if pd > 0 else None, "w": (ws, wa) if weights else None}
+    x_grad = np.zeros(nx, dtype=np.float32)
+    pe_grad = np.zeros(npe, dtype=np.float32) if pd > 0 else None
+    w_grad = np.zeros(nsyn, dtype=np.float32) if weights else None
+    lib().oracle_propagate_product_sparse(*common, int(int_mode), float(int_rescaler), x_grad, x_grad,
+                                          _ptr(pe_grad), _ptr(w_grad))
+    return x_grad, pe_grad, w_grad

@@ -856,8 +856,11 @@ static inline void acc64_add(double *sum, double *abs_, int64_t i, double v)
     abs_[i] += fabs(v);
 }
 
+/* syn_offsets / syn_targets: sparse lookup connectivity (CSR of synapses per
+ * lookup neuron, weights per synapse), or NULL for fully connected tables. */
 static void fill_outputs_product_core(
     const float *x1, const float *x2, const float *pe, const int32_t *anchors, const float *w,
+    const int64_t *syn_offsets, const int32_t *syn_targets,
     int64_t batch, int64_t seq_len, int64_t n1, int64_t n2, int64_t pd, int64_t n_detectors,
     int64_t n_anchors, int64_t n_outputs, int sliced, float cmp_eps, int int_mode,
     double int_rescaler, float *out, double *out_sum, double *out_abs)
@@ -871,16 +874,21 @@ static void fill_outputs_product_core(
                     const prod_pair p = prod_lookup(x1 + (b * seq_len + i) * n1, x2 + (b * seq_len + j) * n2,
                                                     pet, anchors + t * n_anchors * 2, n_anchors, n1, n2,
                                                     sliced, cmp_eps);
-                    const float *row = w + (t * E + p.idx) * n_outputs;
+                    const int64_t n = t * E + p.idx;
                     const int64_t o0 = (b * seq_len + j) * n_outputs;
-                    for (int64_t c = 0; c < n_outputs; c++) {
+                    const int64_t c0 = syn_offsets ? syn_offsets[n] : 0;
+                    const int64_t c1 = syn_offsets ? syn_offsets[n + 1] : n_outputs;
+                    for (int64_t c = c0; c < c1; c++) {
+                        /* synapse c of the neuron, or output c of the table row */
+                        const int64_t o = syn_targets ? syn_targets[c] : c;
+                        const float wv = syn_offsets ? w[c] : w[n * n_outputs + c];
                         if (out_sum)
-                            acc64_add(out_sum, out_abs, o0 + c, (double)row[c]);
+                            acc64_add(out_sum, out_abs, o0 + o, (double)wv);
                         else if (int_mode)
-                            as_i32(out + o0)[c] = wrap_add(as_i32(out + o0)[c],
-                                                           (int32_t)((double)row[c] * OR_DENOM32 * int_rescaler));
+                            as_i32(out + o0)[o] = wrap_add(as_i32(out + o0)[o],
+                                                           (int32_t)((double)wv * OR_DENOM32 * int_rescaler));
                         else
-                            out[o0 + c] += row[c];
+                            out[o0 + o] += wv;
                     }
                 }
 }
@@ -891,9 +899,24 @@ void oracle_fill_outputs_product(
     int64_t n_anchors, int64_t n_outputs, int sliced, float cmp_eps, int int_mode,
     double int_rescaler, float *out)
 {
-    fill_outputs_product_core(x1, x2, pe, anchors, w, batch, seq_len, n1, n2, pd, n_detectors,
-                              n_anchors, n_outputs, sliced, cmp_eps, int_mode, int_rescaler, out,
-                              NULL, NULL);
+    fill_outputs_product_core(x1, x2, pe, anchors, w, NULL, NULL, batch, seq_len, n1, n2, pd,
+                              n_detectors, n_anchors, n_outputs, sliced, cmp_eps, int_mode,
+                              int_rescaler, out, NULL, NULL);
+}
+
+/* fill_outputs_product over sparse connectivity (fill_outputs_product_sparse_logic,
+ * proto:2266-2394; CPU branch fill_outputs_product_cpu_logic proto:2148-2264):
+ * every synapse of the pair's neuron commits its weight to its target. */
+void oracle_fill_outputs_product_sparse(
+    const float *x1, const float *x2, const float *pe, const int32_t *anchors, const float *w,
+    const int64_t *syn_offsets, const int32_t *syn_targets, int64_t batch, int64_t seq_len,
+    int64_t n1, int64_t n2, int64_t pd, int64_t n_detectors, int64_t n_anchors, int64_t n_outputs,
+    int sliced, float cmp_eps, int int_mode, double int_rescaler, float *out, double *out_sum,
+    double *out_abs)
+{
+    fill_outputs_product_core(x1, x2, pe, anchors, w, syn_offsets, syn_targets, batch, seq_len, n1,
+                              n2, pd, n_detectors, n_anchors, n_outputs, sliced, cmp_eps, int_mode,
+                              int_rescaler, out, out_sum, out_abs);
 }
 
 void oracle_fill_outputs_product64(
@@ -902,8 +925,9 @@ void oracle_fill_outputs_product64(
     int64_t n_anchors, int64_t n_outputs, int sliced, float cmp_eps, double *out_sum,
     double *out_abs)
 {
-    fill_outputs_product_core(x1, x2, pe, anchors, w, batch, seq_len, n1, n2, pd, n_detectors,
-                              n_anchors, n_outputs, sliced, cmp_eps, 0, 1.0, NULL, out_sum, out_abs);
+    fill_outputs_product_core(x1, x2, pe, anchors, w, NULL, NULL, batch, seq_len, n1, n2, pd,
+                              n_detectors, n_anchors, n_outputs, sliced, cmp_eps, 0, 1.0, NULL,
+                              out_sum, out_abs);
 }
 
 static inline void prod_push(float *dst, double du, int int_mode, double int_rescaler)
@@ -916,7 +940,7 @@ static inline void prod_push(float *dst, double du, int int_mode, double int_res
 
 static void propagate_product_core(
     const float *x1, const float *x2, const float *pe, const int32_t *anchors, const float *w,
-    const float *g, int64_t batch, int64_t seq_len, int64_t n1, int64_t n2, int64_t pd,
+    const int64_t *syn_offsets, const int32_t *syn_targets, const float *g, int64_t batch, int64_t seq_len, int64_t n1, int64_t n2, int64_t pd,
     int64_t n_detectors, int64_t n_anchors, int64_t n_outputs, int sliced, float cmp_eps,
     double lr, int int_mode, double int_rescaler, float *x1_grad, float *x2_grad, float *pe_grad,
     float *w_grad, const prod_acc64 *acc)
@@ -931,12 +955,21 @@ static void propagate_product_core(
                                                     pd > 0 ? pe + pe_off : NULL, anchors + t * n_anchors * 2,
                                                     n_anchors, n1, n2, sliced, cmp_eps);
                     const float *gj = g + (b * seq_len + j) * n_outputs;
+                    const int64_t nm = t * E + p.idx, na = t * E + p.alt;
                     if (p.src1 >= 0) {
                         double ms = 0.0, as = 0.0;
-                        const float *rm = w + (t * E + p.idx) * n_outputs;
-                        const float *ra = w + (t * E + p.alt) * n_outputs;
-                        for (int64_t c = 0; c < n_outputs; c++) ms += (double)rm[c] * (double)gj[c];
-                        for (int64_t c = 0; c < n_outputs; c++) as += (double)ra[c] * (double)gj[c];
+                        if (syn_offsets) {
+                            /* every synapse of the neuron, in list order (proto:2452-2489) */
+                            for (int64_t c = syn_offsets[nm]; c < syn_offsets[nm + 1]; c++)
+                                ms += (double)w[c] * (double)gj[syn_targets[c]];
+                            for (int64_t c = syn_offsets[na]; c < syn_offsets[na + 1]; c++)
+                                as += (double)w[c] * (double)gj[syn_targets[c]];
+                        } else {
+                            const float *rm = w + nm * n_outputs;
+                            const float *ra = w + na * n_outputs;
+                            for (int64_t c = 0; c < n_outputs; c++) ms += (double)rm[c] * (double)gj[c];
+                            for (int64_t c = 0; c < n_outputs; c++) as += (double)ra[c] * (double)gj[c];
+                        }
                         const double du = du_of_margin(p.md) * (ms - as);
                         if (fabs(du) > OR_EPS) {
                             const int64_t base[3] = {(b * seq_len + i) * n1, (b * seq_len + j) * n2, pe_off};
@@ -953,16 +986,18 @@ static void propagate_product_core(
                         }
                     }
                     if (acc ? acc->w_sum != NULL : w_grad != NULL) {
-                        const int64_t r0 = (t * E + p.idx) * n_outputs;
-                        for (int64_t c = 0; c < n_outputs; c++) {
-                            const double gg = (double)gj[c];
+                        /* row nm's outputs; sparse: every synapse of neuron nm */
+                        const int64_t c0 = syn_offsets ? syn_offsets[nm] : nm * n_outputs;
+                        const int64_t c1 = syn_offsets ? syn_offsets[nm + 1] : (nm + 1) * n_outputs;
+                        for (int64_t c = c0; c < c1; c++) {
+                            const double gg = (double)gj[syn_targets ? syn_targets[c] : c - c0];
                             if (!(fabs(gg) > OR_EPS)) continue;
                             if (acc)
-                                acc64_add(acc->w_sum, acc->w_abs, r0 + c, (double)(float)(gg * lr));
+                                acc64_add(acc->w_sum, acc->w_abs, c, (double)(float)(gg * lr));
                             else if (int_mode)
-                                as_i32(w_grad + r0)[c] = wrap_add(as_i32(w_grad + r0)[c], (int32_t)(gg * lr * OR_DENOM32 * int_rescaler));
+                                as_i32(w_grad)[c] = wrap_add(as_i32(w_grad)[c], (int32_t)(gg * lr * OR_DENOM32 * int_rescaler));
                             else
-                                w_grad[r0 + c] += (float)(gg * lr);
+                                w_grad[c] += (float)(gg * lr);
                         }
                     }
                 }
@@ -977,9 +1012,40 @@ void oracle_propagate_product(
     double lr, int int_mode, double int_rescaler, float *x1_grad, float *x2_grad, float *pe_grad,
     float *w_grad)
 {
-    propagate_product_core(x1, x2, pe, anchors, w, g, batch, seq_len, n1, n2, pd, n_detectors,
-                           n_anchors, n_outputs, sliced, cmp_eps, lr, int_mode, int_rescaler,
-                           x1_grad, x2_grad, pe_grad, w_grad, NULL);
+    propagate_product_core(x1, x2, pe, anchors, w, NULL, NULL, g, batch, seq_len, n1, n2, pd,
+                           n_detectors, n_anchors, n_outputs, sliced, cmp_eps, lr, int_mode,
+                           int_rescaler, x1_grad, x2_grad, pe_grad, w_grad, NULL);
+}
+
+/* oracle_propagate_product over sparse connectivity (propagate_backward_product_cpu_logic,
+ * proto:2396-2628): the main and flipped sums run over every synapse of the
+ * two neurons, one du per pair.  The weight gradient adds to every synapse of
+ * the pair's neuron (as the GPU kernel gather_w_gradients_product_sparse,
+ * proto:2946-3073, over all forward groups; the CPU branch passes output block
+ * 0 and so reaches only a neuron's first group, proto:2580-2596). */
+void oracle_propagate_product_sparse(
+    const float *x1, const float *x2, const float *pe, const int32_t *anchors, const float *w,
+    const int64_t *syn_offsets, const int32_t *syn_targets, const float *g, int64_t batch,
+    int64_t seq_len, int64_t n1, int64_t n2, int64_t pd, int64_t n_detectors, int64_t n_anchors,
+    int64_t n_outputs, int sliced, float cmp_eps, double lr, int int_mode, double int_rescaler,
+    float *x1_grad, float *x2_grad, float *pe_grad, float *w_grad)
+{
+    propagate_product_core(x1, x2, pe, anchors, w, syn_offsets, syn_targets, g, batch, seq_len, n1,
+                           n2, pd, n_detectors, n_anchors, n_outputs, sliced, cmp_eps, lr, int_mode,
+                           int_rescaler, x1_grad, x2_grad, pe_grad, w_grad, NULL);
+}
+
+void oracle_propagate_product_sparse64(
+    const float *x1, const float *x2, const float *pe, const int32_t *anchors, const float *w,
+    const int64_t *syn_offsets, const int32_t *syn_targets, const float *g, int64_t batch,
+    int64_t seq_len, int64_t n1, int64_t n2, int64_t pd, int64_t n_detectors, int64_t n_anchors,
+    int64_t n_outputs, int sliced, float cmp_eps, double lr, double *x1_sum, double *x1_abs,
+    double *x2_sum, double *x2_abs, double *pe_sum, double *pe_abs, double *w_sum, double *w_abs)
+{
+    const prod_acc64 acc = {x1_sum, x1_abs, x2_sum, x2_abs, pe_sum, pe_abs, w_sum, w_abs};
+    propagate_product_core(x1, x2, pe, anchors, w, syn_offsets, syn_targets, g, batch, seq_len, n1,
+                           n2, pd, n_detectors, n_anchors, n_outputs, sliced, cmp_eps, lr, 0, 1.0,
+                           NULL, NULL, NULL, NULL, &acc);
 }
 
 /* fp64 mode of oracle_propagate_product (see prod_acc64); any pair of
@@ -992,7 +1058,7 @@ void oracle_propagate_product64(
     double *pe_abs, double *w_sum, double *w_abs)
 {
     const prod_acc64 acc = {x1_sum, x1_abs, x2_sum, x2_abs, pe_sum, pe_abs, w_sum, w_abs};
-    propagate_product_core(x1, x2, pe, anchors, w, g, batch, seq_len, n1, n2, pd, n_detectors,
-                           n_anchors, n_outputs, sliced, cmp_eps, lr, 0, 1.0, NULL, NULL, NULL, NULL,
-                           &acc);
+    propagate_product_core(x1, x2, pe, anchors, w, NULL, NULL, g, batch, seq_len, n1, n2, pd,
+                           n_detectors, n_anchors, n_outputs, sliced, cmp_eps, lr, 0, 1.0, NULL,
+                           NULL, NULL, NULL, &acc);
 }

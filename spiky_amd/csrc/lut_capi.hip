@@ -786,8 +786,6 @@ static spiky::ProductShape product_shape(const spiky_lut_manager *m, uint32_t ba
                          "1, real length of the sequence is passed as the method parameter");
     if (sequence_length == 0) throw ValueError("sequence_length == 0");
     require_initialized(m);
-    if (m->fully_connected != 1)
-        throw ValueError("product mode is built for fully connected managers only");
     spiky::ProductShape s;
     s.batch = batch_size;
     s.seq_len = sequence_length;
@@ -799,9 +797,11 @@ static spiky::ProductShape product_shape(const spiky_lut_manager *m, uint32_t ba
     s.n_outputs = m->n_outputs;
     s.sliced = sliced_mode != 0;
     s.cmp_eps = cmp_eps;
-    if (!spiky::product_applies(s))
+    if (m->fully_connected == 1 && !spiky::product_applies(s))
         throw ValueError("product mode shape out of range (n_detectors * 2^n_anchors must be <= 16384, "
                          "batch_size * sequence_length <= 4194240)");
+    if (m->fully_connected != 1 && !spiky::product_sparse_applies(s))
+        throw ValueError("product mode shape out of range for sparse connectivity");
     return s;
 }
 
@@ -823,13 +823,25 @@ int spiky_lut_forward_step_product(spiky_lut_manager *m, const float *weights, u
         ScopedTimer timer(m->stats, "lut::runtime::forward_product");
         m->context_active = true;
         const hipStream_t st = as_stream(stream);
-        void *scr = m->scratch_fwd.ensure(spiky::product_scratch_bytes(s, false));
-        m->timed("fill_outputs_product", st, [&] {
-            check_hip(spiky::launch_forward_product(s, weights, input_1, input_2,
-                                                    positional_embeddings, anchors, output,
-                                                    m->int_mode, m->int_rescaler, scr, st),
-                      "forward_step_product");
-        });
+        if (m->fully_connected == 1) {
+            void *scr = m->scratch_fwd.ensure(spiky::product_scratch_bytes(s, false));
+            m->timed("fill_outputs_product", st, [&] {
+                check_hip(spiky::launch_forward_product(s, weights, input_1, input_2,
+                                                        positional_embeddings, anchors, output,
+                                                        m->int_mode, m->int_rescaler, scr, st),
+                          "forward_step_product");
+            });
+        } else {
+            m->sync_connectivity();
+            m->timed("fill_outputs_product_sparse", st, [&] {
+                check_hip(spiky::launch_forward_product_sparse(
+                              s, weights, input_1, input_2, positional_embeddings, anchors,
+                              (const int64_t *)m->d_syn_offsets.ptr,
+                              (const int32_t *)m->d_syn_targets.ptr, output, m->int_mode,
+                              m->int_rescaler, st),
+                          "forward_step_product");
+            });
+        }
         if (m->int_mode)
             check_hip(spiky::launch_convert_i2f(output, (uint64_t)s.batch * s.seq_len * s.n_outputs,
                                                 m->int_rescaler, st),
@@ -868,15 +880,28 @@ int spiky_lut_backward_backprop_product(spiky_lut_manager *m, float *weights, ui
         double lr = (double)m->metas[0][0];
         if (external_lr >= 0.0) lr *= -external_lr;
         float *target = (external_lr >= 0.0) ? weights : weight_grad;
-        void *scr = m->scratch.ensure(spiky::product_scratch_bytes(s, true));
-        m->timed("backward_product", st, [&] {
-            check_hip(spiky::launch_backward_product(s, weights, input_1, input_2,
-                                                     positional_embeddings, anchors, output_grad,
-                                                     input_grad_1, input_grad_2, positional_grad,
-                                                     target, lr, m->int_mode, m->int_rescaler, scr,
-                                                     st),
-                      "backward_backprop_product");
-        });
+        if (m->fully_connected == 1) {
+            void *scr = m->scratch.ensure(spiky::product_scratch_bytes(s, true));
+            m->timed("backward_product", st, [&] {
+                check_hip(spiky::launch_backward_product(s, weights, input_1, input_2,
+                                                         positional_embeddings, anchors, output_grad,
+                                                         input_grad_1, input_grad_2, positional_grad,
+                                                         target, lr, m->int_mode, m->int_rescaler, scr,
+                                                         st),
+                          "backward_backprop_product");
+            });
+        } else {
+            m->sync_connectivity();
+            m->timed("backward_product_sparse", st, [&] {
+                check_hip(spiky::launch_backward_product_sparse(
+                              s, weights, input_1, input_2, positional_embeddings, anchors,
+                              (const int64_t *)m->d_syn_offsets.ptr,
+                              (const int32_t *)m->d_syn_targets.ptr, output_grad, input_grad_1,
+                              input_grad_2, positional_grad, target, lr, m->int_mode,
+                              m->int_rescaler, st),
+                          "backward_backprop_product");
+            });
+        }
         if (m->int_mode) {
             // lut_runtime.cu:1405-1456: every buffer this call summed into
             const uint64_t bs = (uint64_t)s.batch * s.seq_len;
@@ -886,8 +911,7 @@ int spiky_lut_backward_backprop_product(spiky_lut_manager *m, float *weights, ui
                 check_hip(spiky::launch_convert_i2f(input_grad_2, bs * s.n2, m->int_rescaler, st),
                           "convert_integers_to_floats");
             if (weight_grad)
-                check_hip(spiky::launch_convert_i2f(weight_grad,
-                                                    (uint64_t)m->n_lookup * m->n_outputs,
+                check_hip(spiky::launch_convert_i2f(weight_grad, spiky_lut_weights_dimension(m),
                                                     m->int_rescaler, st),
                           "convert_integers_to_floats");
             if (s.pd > 0)

@@ -211,6 +211,19 @@ hipError_t launch_forward_product(const ProductShape &s, const float *w, const f
 // Input, positional and (target != null) weight gradients; x1_grad may alias
 // x2_grad.  target gets lr * g terms (weight gradient, or the weights
 // themselves with lr = meta lr * -external lr for the Internal policy).
+// Sparse lookup connectivity (weights per synapse of the CSR).
+bool product_sparse_applies(const ProductShape &s);
+hipError_t launch_forward_product_sparse(const ProductShape &s, const float *w, const float *x1,
+                                         const float *x2, const float *pe, const int32_t *anchors,
+                                         const int64_t *syn_offsets, const int32_t *syn_targets,
+                                         float *out, bool int_mode, double int_rescaler,
+                                         hipStream_t st);
+hipError_t launch_backward_product_sparse(const ProductShape &s, const float *w, const float *x1,
+                                          const float *x2, const float *pe, const int32_t *anchors,
+                                          const int64_t *syn_offsets, const int32_t *syn_targets,
+                                          const float *g, float *x1_grad, float *x2_grad,
+                                          float *pe_grad, float *target, double lr, bool int_mode,
+                                          double int_rescaler, hipStream_t st);
 hipError_t launch_backward_product(const ProductShape &s, const float *w, const float *x1,
                                    const float *x2, const float *pe, const int32_t *anchors,
                                    const float *g, float *x1_grad, float *x2_grad, float *pe_grad,

@@ -708,6 +708,106 @@ hipError_t gemm_mfma(const float *A, uint32_t lda, const float *B, uint32_t ldb,
     return hipGetLastError();
 }
 
+// Product mode over sparse lookup connectivity (this build's CSR, weights per
+// synapse): one thread per (b, table, pair), the reference's own
+// decomposition with fp32 / int32 atomics (fill_outputs_product_sparse_logic,
+// proto:2266-2394; propagate_backward_product_cpu_logic, proto:2396-2628: the
+// main and flipped sums over every synapse of the two neurons, one du per
+// pair; gather_w_gradients_product_sparse, proto:2946-3073: every synapse of
+// the pair's neuron).  MODE 0: forward; 1: input / positional gradients, and
+// the weight gradient when target is given; 2: the weight gradient alone (the
+// Internal policy, after mode 1 read the weights).
+template <int MODE, bool INT_MODE>
+__global__ __launch_bounds__(256) void k_prod_sparse(
+    const float *__restrict__ x1, const float *__restrict__ x2, const float *__restrict__ pe,
+    const int2 *__restrict__ anchors, const float *__restrict__ w, const int64_t *__restrict__ off,
+    const int32_t *__restrict__ tgt, const float *__restrict__ g, float *__restrict__ out,
+    float *__restrict__ x1_grad, float *__restrict__ x2_grad, float *__restrict__ pe_grad,
+    float *__restrict__ target, uint32_t S, uint32_t n1, uint32_t n2, uint32_t pd, uint32_t T,
+    uint32_t n_anchors, uint32_t O, bool sliced, float cmp_eps, double lr, double int_rescaler,
+    uint64_t n_pairs, uint64_t n_items) {
+    const uint64_t item = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (item >= n_items) return;
+    const uint64_t p = item % n_pairs;
+    const uint64_t bt = item / n_pairs;
+    const uint32_t t = (uint32_t)(bt % T), b = (uint32_t)(bt / T);
+    uint64_t jj = (uint64_t)((1.0 + sqrt(1.0 + 8.0 * (double)p)) * 0.5);
+    while (jj * (jj - 1) / 2 > p) jj--;
+    while ((jj + 1) * jj / 2 <= p) jj++;
+    const uint32_t j = (uint32_t)jj, i = (uint32_t)(p - jj * (jj - 1) / 2);
+    const size_t pe_off = ((size_t)(j - i - 1) * T + t) * pd;
+    const PairLookup lk = prod_lookup(x1 + ((size_t)b * S + i) * n1, x2 + ((size_t)b * S + j) * n2,
+                                      pd ? pe + pe_off : nullptr, anchors + (size_t)t * n_anchors,
+                                      n_anchors, n1, n2, pd, sliced, cmp_eps);
+    const uint32_t n = t * (1u << n_anchors) + (uint32_t)lk.idx;
+    const size_t orow = ((size_t)b * S + j) * O;
+    if (MODE == 0) {
+        for (int64_t sy = off[n]; sy < off[n + 1]; sy++) {
+            const uint32_t o = (uint32_t)tgt[sy];
+            if (o >= O) continue;
+            if (INT_MODE) atomicAdd(reinterpret_cast<int32_t *>(out + orow + o), (int32_t)((double)w[sy] * kDenom32 * int_rescaler));
+            else unsafeAtomicAdd(out + orow + o, w[sy]);
+        }
+        return;
+    }
+    const float *gj = g + orow;
+    if (MODE == 1 && lk.src1 >= 0) {
+        const uint32_t na = t * (1u << n_anchors) + (uint32_t)lk.alt;
+        double ms = 0.0, as = 0.0;
+        for (int64_t sy = off[n]; sy < off[n + 1]; sy++) {
+            const uint32_t o = (uint32_t)tgt[sy];
+            if (o < O) ms += (double)w[sy] * (double)gj[o];
+        }
+        for (int64_t sy = off[na]; sy < off[na + 1]; sy++) {
+            const uint32_t o = (uint32_t)tgt[sy];
+            if (o < O) as += (double)w[sy] * (double)gj[o];
+        }
+        const double du = du_of_margin(lk.md) * (ms - as);
+        if (fabs(du) > kEps) {
+            float *dst[3] = {x1_grad + ((size_t)b * S + i) * n1, x2_grad + ((size_t)b * S + j) * n2,
+                             pd ? pe_grad + pe_off : nullptr};
+            const int32_t srcs[2] = {lk.src1, lk.src2};
+            const uint32_t ks[2] = {lk.k1, lk.k2};
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                float *d = dst[srcs[h]];
+                if (!d) continue;
+                const double v = h == 0 ? du : -du;
+                if (INT_MODE) atomicAdd(reinterpret_cast<int32_t *>(d + ks[h]), (int32_t)(v * kDenom32 * int_rescaler));
+                else unsafeAtomicAdd(d + ks[h], (float)v);
+            }
+        }
+    }
+    if (target) {
+        for (int64_t sy = off[n]; sy < off[n + 1]; sy++) {
+            const uint32_t o = (uint32_t)tgt[sy];
+            if (o >= O) continue;
+            const double gg = (double)gj[o];
+            if (!(fabs(gg) > kEps)) continue;
+            if (INT_MODE) atomicAdd(reinterpret_cast<int32_t *>(target + sy), (int32_t)(gg * lr * kDenom32 * int_rescaler));
+            else unsafeAtomicAdd(target + sy, (float)(gg * lr));
+        }
+    }
+}
+
+template <int MODE, bool IM>
+hipError_t launch_prod_sparse(const ProductShape &s, const float *x1, const float *x2, const float *pe,
+                              const int32_t *anchors, const float *w, const int64_t *off,
+                              const int32_t *tgt, const float *g, float *out, float *x1_grad,
+                              float *x2_grad, float *pe_grad, float *target, double lr,
+                              double int_rescaler, hipStream_t st) {
+    const uint64_t n_pairs = (uint64_t)s.seq_len * (s.seq_len - 1) / 2;
+    const uint64_t n_items = (uint64_t)s.batch * s.n_detectors * n_pairs;
+    if (n_items == 0) return hipSuccess;
+    const uint64_t blocks = (n_items + 255) / 256;
+    if (blocks > 0x7fffffffull) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL((k_prod_sparse<MODE, IM>), dim3((uint32_t)blocks), dim3(256), 0, st, x1, x2, pe,
+                       reinterpret_cast<const int2 *>(anchors), w, off, tgt, g, out, x1_grad, x2_grad,
+                       pe_grad, target, s.seq_len, s.n1, s.n2, s.pd, s.n_detectors, s.n_anchors,
+                       s.n_outputs, s.sliced, s.cmp_eps, lr, int_rescaler, n_pairs, n_items);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 bool product_applies(const ProductShape &s) {
@@ -823,6 +923,50 @@ hipError_t launch_backward_product(const ProductShape &s, const float *w, const 
                                        int_rescaler, st);
     return gemm_mfma<true, false, 2, 0>(cnt, TE, g, s.n_outputs, target, TE, s.n_outputs, BS, lr,
                                         part, st);
+}
+
+}  // namespace spiky
+
+namespace spiky {
+
+bool product_sparse_applies(const ProductShape &s) {
+    const uint64_t n_items = (uint64_t)s.batch * s.n_detectors * ((uint64_t)s.seq_len * (s.seq_len - 1) / 2);
+    return s.n_anchors <= 24 && (n_items + 255) / 256 <= 0x7fffffffull;
+}
+
+hipError_t launch_forward_product_sparse(const ProductShape &s, const float *w, const float *x1,
+                                         const float *x2, const float *pe, const int32_t *anchors,
+                                         const int64_t *syn_offsets, const int32_t *syn_targets,
+                                         float *out, bool int_mode, double int_rescaler,
+                                         hipStream_t st) {
+    if (int_mode)
+        return launch_prod_sparse<0, true>(s, x1, x2, pe, anchors, w, syn_offsets, syn_targets, nullptr,
+                                           out, nullptr, nullptr, nullptr, nullptr, 0.0, int_rescaler, st);
+    return launch_prod_sparse<0, false>(s, x1, x2, pe, anchors, w, syn_offsets, syn_targets, nullptr, out,
+                                        nullptr, nullptr, nullptr, nullptr, 0.0, int_rescaler, st);
+}
+
+hipError_t launch_backward_product_sparse(const ProductShape &s, const float *w, const float *x1,
+                                          const float *x2, const float *pe, const int32_t *anchors,
+                                          const int64_t *syn_offsets, const int32_t *syn_targets,
+                                          const float *g, float *x1_grad, float *x2_grad,
+                                          float *pe_grad, float *target, double lr, bool int_mode,
+                                          double int_rescaler, hipStream_t st) {
+    // the Internal policy updates the weights: after the input gradient read them
+    const bool internal = target == w;
+    float *t1 = internal ? nullptr : target;
+    hipError_t e = int_mode
+        ? launch_prod_sparse<1, true>(s, x1, x2, pe, anchors, w, syn_offsets, syn_targets, g, nullptr,
+                                      x1_grad, x2_grad, pe_grad, t1, lr, int_rescaler, st)
+        : launch_prod_sparse<1, false>(s, x1, x2, pe, anchors, w, syn_offsets, syn_targets, g, nullptr,
+                                       x1_grad, x2_grad, pe_grad, t1, lr, int_rescaler, st);
+    if (e != hipSuccess || !internal) return e;
+    return int_mode ? launch_prod_sparse<2, true>(s, x1, x2, pe, anchors, w, syn_offsets, syn_targets, g,
+                                                  nullptr, nullptr, nullptr, nullptr, target, lr,
+                                                  int_rescaler, st)
+                    : launch_prod_sparse<2, false>(s, x1, x2, pe, anchors, w, syn_offsets, syn_targets, g,
+                                                   nullptr, nullptr, nullptr, nullptr, target, lr,
+                                                   int_rescaler, st);
 }
 
 }  // namespace spiky

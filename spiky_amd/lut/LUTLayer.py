@@ -197,9 +197,6 @@ class LUTLayerBasic(nn.Module):
             raise ValueError("sliced_product_mode == True doesn't make sense in concatenation product mode")
         if self._sliced_product_mode and n_inputs != positional_dim:
             raise ValueError("if sliced_product_mode == True then n_inputs and positional_dim should be equal")
-        if not concatenation_product and not is_fully_connected:
-            raise NotImplementedError("product mode (concatenation_product=False) is built for fully "
-                                      "connected lookup tables only")
         self._unified_positional_embeddings = unified_pe
         if shared_context is None:
             self._own_shared_context = True

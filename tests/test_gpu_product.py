@@ -361,3 +361,125 @@ def test_transformer_product_attention(oracle, cuda_device):
     for block in model.layers:
         pg = block["attention_lut"]._positional_embeddings.grad
         assert pg is not None and torch.isfinite(pg).all()
+
+
+# ---------------------------------------------------------------- sparse connectivity
+def run_product_sparse(oracle, B, S, n, T, Nc, O, pd, sliced=False, int_rescaler=None, internal=False,
+                       seed=0, lr=1.0, ext_lr=0.2):
+    """Product mode over a random ragged CSR (empty neurons, repeated targets)
+    against the oracle: int32 bit-exact; fp32 within the bounds above."""
+    dev = torch.device("cuda:0")
+    if sliced:
+        pd = n
+    int_mode = int_rescaler is not None
+    print(f"[product sparse] B={B} S={S} n={n} T={T} Nc={Nc} O={O} pd={pd} sliced={sliced} "
+          f"int={int_mode} internal={internal}", flush=True)
+    x, pe, anc, _, g = product_inputs(seed, B, S, n, T, Nc, O, pd, sliced)
+    rng = np.random.default_rng(seed + 100)
+    E = 1 << Nc
+    counts = rng.integers(0, 9, size=T * E)
+    off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    tg = rng.integers(0, O, size=int(off[-1])).astype(np.int32)
+    W = (rng.standard_normal(tg.size) * 0.1).astype(np.float32)
+    args = (2 * n + pd, O, T, Nc, 1, pd, 0, 4, 32)
+    dm = LUTDataManagerF(*args) if int_rescaler is None else LUTDataManagerI(*args, int_rescaler)
+    dm.register_synapse_meta(lr, -10.0, 10.0, 0.0, 0.0)
+    dm.initialize_neurons(False)
+    dm.set_lookup_connectivity(off, tg)
+    dm.compile(True, torch.zeros(tg.size))
+    dm.to_device(0)
+    xd, ad, Wd, gd = (torch.from_numpy(v).to(dev) for v in (x, anc, W, g))
+    ped = torch.from_numpy(pe).to(dev) if pd else None
+    out = torch.zeros(B * S * O, device=dev)
+    dm.forward_step_product(Wd, B, S, xd, xd, ad, out, n, n, sliced, 0.0, ped)
+    xg = torch.zeros(B * S * n, device=dev)
+    peg = torch.zeros((S - 1) * T * pd, device=dev) if pd else None
+    W_before = W.copy()
+    wg = None
+    if internal:
+        dm.backward_backprop_product(Wd, B, S, xd, xd, ad, gd, xg, xg, ext_lr, n, n, sliced, 0.0, None, ped, peg)
+    else:
+        wg = torch.zeros_like(Wd)
+        dm.backward_backprop_product(Wd, B, S, xd, xd, ad, gd, xg, xg, -1.0, n, n, sliced, 0.0, wg, ped, peg)
+    torch.cuda.synchronize()
+    geo = (B, S, n, n, pd, T, Nc, O)
+    eff_lr = lr * (-ext_lr if internal else 1.0)
+    if int_mode:
+        rout = oracle.fill_outputs_product_sparse(x, x, pe, anc, W, off, tg, *geo, sliced=sliced, int_mode=True,
+                                                  int_rescaler=int_rescaler)
+        rx, rp, rw = oracle.propagate_product_sparse(x, x, pe, anc, W, off, tg, g, *geo, sliced=sliced, lr=eff_lr,
+                                                     int_mode=True, int_rescaler=int_rescaler)
+        for buf in (rout, rx, rp, rw):
+            if buf is not None:
+                oracle.convert_int_to_float(buf, int_rescaler)
+        assert np.array_equal(out.cpu().numpy(), rout)
+        assert np.array_equal(xg.cpu().numpy(), rx)
+        if pd:
+            assert np.array_equal(peg.cpu().numpy(), rp)
+        assert np.array_equal(wg.cpu().numpy(), rw)
+        return
+    s, a = oracle.fill_outputs_product_sparse(x, x, pe, anc, W, off, tg, *geo, sliced=sliced, bounds=True)
+    n_fwd = T * S * int(counts.max())
+    within(out.cpu().numpy(), s, a, n_fwd, "forward")
+    r = oracle.propagate_product_sparse(x, x, pe, anc, W, off, tg, g, *geo, sliced=sliced, lr=eff_lr, bounds=True)
+    within(xg.cpu().numpy(), *r["x"], 2 * T * S, "x_grad")
+    if pd:
+        within(peg.cpu().numpy(), *r["pe"], 2 * B * S, "pe_grad")
+    n_w = B * S * (S - 1) // 2
+    if internal:
+        within(Wd.cpu().numpy(), W_before.astype(np.float64) + r["w"][0], r["w"][1] + np.abs(W_before), n_w,
+               "weights (Internal)")
+    else:
+        within(wg.cpu().numpy(), *r["w"], n_w, "w_grad")
+    assert np.abs(xg.cpu().numpy()).max() > 0
+
+
+@pytest.mark.parametrize("sliced,pd", [(False, 0), (False, 3), (True, 0)])
+def test_product_sparse_fp32(oracle, cuda_device, sliced, pd):
+    run_product_sparse(oracle, B=2, S=10, n=8, T=4, Nc=4, O=12, pd=pd, sliced=sliced, seed=13)
+
+
+@pytest.mark.parametrize("sliced", [False, True])
+def test_product_sparse_int32_bit_exact(oracle, cuda_device, sliced):
+    run_product_sparse(oracle, B=2, S=9, n=8, T=3, Nc=4, O=10, pd=2, sliced=sliced, int_rescaler=0.001, seed=14)
+
+
+def test_product_sparse_internal_policy(oracle, cuda_device):
+    run_product_sparse(oracle, B=2, S=8, n=6, T=3, Nc=3, O=9, pd=2, internal=True, lr=0.5, seed=15)
+
+
+def test_product_sparse_conv2d_layer_autograd(oracle, cuda_device):
+    """A sliced product-mode Conv2DLUTLayer with a lookup receptive field (sparse
+    connectivity) through autograd."""
+    from spiky_amd.lut.LUTLayer import Conv2DLUTLayer, SynapseMeta
+    dev = cuda_device
+    S = 5
+    layer = Conv2DLUTLayer(input_shape=(4, 4), n_anchors_per_detector=3, detectors_shape=(2, 2),
+                           output_kernel_shape=(2, 2), sequence_length=S, receptive_field_shape=(2, 2),
+                           receptive_field_stride_shape=(1, 1), lut_receptive_field_shape=(4, 4),
+                           lut_receptive_field_stride_shape=(2, 2), concatenation_product=False,
+                           sliced_product_mode=True, positional_dim=16,
+                           synapse_meta=SynapseMeta(initial_noise_level=1.0), _forward_group_size=3,
+                           random_seed=3, device=dev)
+    off, tg = layer._lut_dm.lookup_connectivity()
+    T, Nc, O, n = layer.n_detectors(), layer.n_anchors_per_detector(), layer.n_outputs(), 16
+    g = torch.Generator().manual_seed(6)
+    B = 2
+    x = torch.randn(B, S, 4, 4, generator=g).to(dev).requires_grad_(True)
+    y = layer(x)
+    go = torch.randn(B, S, 4, 4, generator=g).to(dev)
+    y.backward(go)
+    torch.cuda.synchronize()
+    xn = x.detach().cpu().numpy().reshape(-1)
+    anc = layer._detector_anchors.cpu().numpy()
+    W = layer._weights.detach().cpu().numpy()
+    pe = _full_pe(layer)
+    geo = (B, S, n, n, 16, T, Nc, O)
+    s, a = oracle.fill_outputs_product_sparse(xn, xn, pe, anc, W, off, tg, *geo, sliced=True, bounds=True)
+    within(y.detach().cpu().numpy().reshape(-1), s, a, T * S * int(np.diff(off).max()), "forward")
+    r = oracle.propagate_product_sparse(xn, xn, pe, anc, W, off, tg, go.cpu().numpy().reshape(-1), *geo,
+                                        sliced=True, bounds=True)
+    within(x.grad.cpu().numpy().reshape(-1), *r["x"], 2 * T * S, "x.grad")
+    within(layer._weights.grad.cpu().numpy(), *r["w"], B * S * (S - 1) // 2, "weights.grad")
+    within(layer._positional_embeddings.grad.cpu().numpy(), *r["pe"], 2 * B * S, "pe.grad")
+    assert np.abs(r["w"][0]).max() > 0

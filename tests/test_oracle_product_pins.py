@@ -121,3 +121,59 @@ def test_product_fp64_mode_walks_the_same_terms(oracle, sliced, pd):
     if pd:
         assert np.all(np.abs(peg - r["pe"][0]) <= n_terms * 2.0 ** -24 * r["pe"][1])
     assert r["x"][1].max() > 0
+
+
+def _full_csr(T, E, O):
+    n = T * E
+    return np.arange(n + 1, dtype=np.int64) * O, np.tile(np.arange(O, dtype=np.int32), n)
+
+
+@pytest.mark.parametrize("sliced,pd", [(False, 2), (True, 0)])
+def test_product_sparse_full_connectivity_is_the_fc_path(oracle, sliced, pd):
+    """A CSR that lists every output of every neuron in order turns the sparse
+    product functions into the FC ones: equal outputs, input, positional and
+    weight gradients (int32 payloads bit for bit; integer fp32 values exactly)."""
+    B, S, n, T, Nc, O, pd, x, pe, anc, w = _case(31, sliced, pd)
+    a = anc.reshape(-1)
+    off, tg = _full_csr(T, 1 << Nc, O)
+    geo = (B, S, n, n, pd, T, Nc, O)
+    assert np.array_equal(oracle.fill_outputs_product(x, x, pe, a, w, *geo, sliced=sliced),
+                          oracle.fill_outputs_product_sparse(x, x, pe, a, w, off, tg, *geo, sliced=sliced))
+    rng = np.random.default_rng(6)
+    g = rng.standard_normal(B * S * O).astype(np.float32)
+    fc = oracle.propagate_product(x, x, pe, a, w, g, *geo, sliced=sliced, lr=0.5, int_mode=True,
+                                  int_rescaler=0.01, w_grad=np.zeros(w.size, np.float32))
+    sp = oracle.propagate_product_sparse(x, x, pe, a, w, off, tg, g, *geo, sliced=sliced, lr=0.5,
+                                         int_mode=True, int_rescaler=0.01)
+    for u, v in zip(fc, sp):
+        if u is not None:
+            assert np.array_equal(u.view(np.int32), v.view(np.int32))
+    f64 = oracle.propagate_product64(x, x, pe, a, w, g, *geo, sliced=sliced, lr=0.5)
+    s64 = oracle.propagate_product_sparse(x, x, pe, a, w, off, tg, g, *geo, sliced=sliced, lr=0.5, bounds=True)
+    for k in ("x", "pe", "w"):
+        if f64[k] is not None:
+            assert np.array_equal(f64[k][0], s64[k][0]) and np.array_equal(f64[k][1], s64[k][1])
+
+
+def test_product_sparse_brute_force(oracle):
+    """A random ragged topology (empty neurons, repeated targets) against a
+    direct loop over pairs and synapses, integer weights (exact)."""
+    B, S, n, T, Nc, O, pd, x, pe, anc, _ = _case(32, False, 2)
+    rng = np.random.default_rng(7)
+    E = 1 << Nc
+    counts = rng.integers(0, 6, size=T * E)
+    off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    tg = rng.integers(0, O, size=off[-1]).astype(np.int32)
+    w = rng.integers(-4, 5, size=off[-1]).astype(np.float32)
+    got = oracle.fill_outputs_product_sparse(x, x, pe, anc.reshape(-1), w, off, tg, B, S, n, n, pd, T, Nc, O)
+    want = np.zeros((B, S, O))
+    for b in range(B):
+        for j in range(S):
+            for t in range(T):
+                for i in range(j):
+                    pe_t = pe[((j - i - 1) * T + t) * pd:((j - i - 1) * T + t + 1) * pd]
+                    idx, _, _, _ = _lookup(_triple(x, b, i, j, pe_t, S, n, False), anc[t], 0.0)
+                    m = t * E + idx
+                    for s_ in range(off[m], off[m + 1]):
+                        want[b, j, tg[s_]] += w[s_]
+    assert np.array_equal(got, want.reshape(-1).astype(np.float32))
