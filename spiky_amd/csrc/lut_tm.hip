@@ -269,6 +269,24 @@ __device__ __forceinline__ void stage_store(const f32x4 (&rows)[kTmPF][2],
 // ---------------------------------------------------------------------------
 // Forward partials.  part[k][b][o] = commit value of table block k for (b, o).
 // ---------------------------------------------------------------------------
+// Workgroups are dealt to the 8 XCDs round robin (workgroup i runs on XCD
+// i % 8).  The forward maps the n_slices column slices of one unit of tables
+// to consecutive workgroups of the same XCD, so that the slices of a table row
+// are fetched together, from one XCD, while they run side by side: whole 4 KiB
+// rows reach HBM at once instead of 128-byte pieces spread over all XCDs
+// (config 3: 2.04 -> 1.80 ms).  Grids that are not a whole number of
+// 8 * n_slices workgroups keep the plain order.
+__device__ __forceinline__ void xcd_slice_unit(uint32_t n_slices, uint32_t &slice, uint32_t &rest) {
+    if (gridDim.x % (8u * n_slices) == 0) {
+        const uint32_t local = blockIdx.x / 8u;
+        slice = local % n_slices;
+        rest = (local / n_slices) * 8u + blockIdx.x % 8u;
+    } else {
+        slice = blockIdx.x % n_slices;
+        rest = blockIdx.x / n_slices;
+    }
+}
+
 // A unit covers bpu consecutive blocks of dgs tables (bpu = 1 for fp32 sums;
 // int32 payloads, whose wrapping sum is associative, may fold several blocks
 // into one partial).  Each block's payload is formed from its own fp64 sum.
@@ -283,8 +301,8 @@ __global__ __launch_bounds__(kTmThreads) void k_fill_tm(
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & (kWave - 1);
     const uint32_t wave = tid / kWave;
-    const uint32_t slice = blockIdx.x % n_slices;
-    const uint32_t rest = blockIdx.x / n_slices;
+    uint32_t slice, rest;
+    xcd_slice_unit(n_slices, slice, rest);
     const uint32_t chunk = rest % n_chunks;
     const uint32_t k = rest / n_chunks;
     const uint32_t t0 = k * dgs * bpu;
@@ -417,8 +435,8 @@ __global__ __launch_bounds__(kTmThreads) void k_fill_tm_dma(
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & (kWave - 1);
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-    const uint32_t slice = blockIdx.x % n_slices;
-    const uint32_t rest = blockIdx.x / n_slices;
+    uint32_t slice, rest;
+    xcd_slice_unit(n_slices, slice, rest);
     const uint32_t chunk = rest % n_chunks;
     const uint32_t k = rest / n_chunks;
     const uint32_t t0 = k * dgs * bpu;
