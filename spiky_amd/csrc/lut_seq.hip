@@ -994,11 +994,16 @@ __global__ __launch_bounds__(kBlock) void k_zero64(double *__restrict__ p, uint6
 // order; int32 payload sums are exact.
 constexpr int kSeqWgThreads = 1024;
 constexpr int kSeqWgRowsMax = 4096;      // sub-table rows 2^(Nc+Npe)
-constexpr int kSeqWgEntries = 32768;     // entries per batch
-constexpr int kSeqWgGvWords = 8192;      // batch gradient rows (items x C)
+// LDS: 32 KiB of row counts and cursors, 48 KiB of u8 entries, 60 KiB of
+// gradient rows, 19 KiB of index tables: 192 items of 255 earlier positions
+// and 64 columns fit one batch, so a (table, Q) bucket of up to 192 items --
+// every bucket of 2^6 Q values over 8192 (b, s) rows in practice -- is summed
+// and written in one pass.
+constexpr int kSeqWgEntries = 49152;     // entries per batch (u8 item numbers)
+constexpr int kSeqWgGvWords = 15360;     // batch gradient rows (items x C)
 constexpr int kSeqWgKeys = 8192;         // K indices of up to 8192 (b, s) rows at a time
 constexpr int kSeqWgPe = 1024;
-constexpr int kSeqWgItems = 256;
+constexpr int kSeqWgItems = 256;         // u8 entries: at most 256 items a batch
 
 template <bool INT_MODE, bool OVERWRITE>
 __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
@@ -1009,7 +1014,7 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
     uint32_t cols, uint32_t n_slices, uint32_t items_per_batch, double int_rescaler) {
     __shared__ uint32_t cnt[kSeqWgRowsMax];
     __shared__ uint32_t cur[kSeqWgRowsMax];
-    __shared__ uint16_t ent[kSeqWgEntries];
+    __shared__ uint8_t ent[kSeqWgEntries];
     __shared__ uint32_t gv[kSeqWgGvWords];
     __shared__ uint16_t ktab[kSeqWgKeys];
     __shared__ uint16_t ptab[kSeqWgPe];
@@ -1091,7 +1096,7 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
                 const uint16_t *kt = ktab + (r / seq - r0 / seq) * seq;
                 for (uint32_t i = lane; i < j; i += kWave) {
                     const uint32_t row = (((uint32_t)kt[i] << pe_dim) | ptab[j - i - 1]) & (sub_rows - 1);
-                    ent[atomicAdd(&cur[row], 1u)] = (uint16_t)(it * cols);  // the item's gv row
+                    ent[atomicAdd(&cur[row], 1u)] = (uint8_t)it;  // the item's gv row is it * cols
                 }
             }
             // cur[row] is now the end of the row's bucket, cur - cnt its start
@@ -1123,6 +1128,9 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
                 for (uint32_t row = rs; row < re; row++) {
                     const uint32_t e1 = cur[row];
                     uint32_t e = e1 - cnt[row];
+                    // a row without entries in this batch keeps what it holds
+                    // (it is only written when this pass stores)
+                    if (!store && e == e1) continue;
                     uint32_t a = 0u;
                     // eight entries at a time, their LDS reads in flight together;
                     // the last group re-reads the row's last entry and adds +0
@@ -1132,7 +1140,7 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
                         uint32_t v[8];
 #pragma unroll
                         for (int u = 0; u < 8; u++) {
-                            const uint32_t g = gv[(uint32_t)ent[min(e + u, e1 - 1)] + my_col];
+                            const uint32_t g = gv[(uint32_t)ent[min(e + u, e1 - 1)] * cols + my_col];
                             v[u] = e + u < e1 ? g : 0u;
                         }
                         if (INT_MODE) {
