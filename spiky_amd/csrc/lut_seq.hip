@@ -263,6 +263,7 @@ __global__ __launch_bounds__(kBlock) void k_fill_seq(
 // Position 0 has no pairs: its value is -0.0f (0 in int mode), which leaves
 // every sum unchanged.
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kSfThreads = 1024;
 constexpr int kSfTabFloats = 32768;   // 128 KiB sub-table slice
 constexpr int kSfItems = 2048;        // items sorted per chunk of a bucket
@@ -1011,7 +1012,7 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
     const int32_t *__restrict__ samples, const uint2 *__restrict__ pack,
     const uint2 *__restrict__ ppack, float *__restrict__ target, uint32_t batch, uint32_t seq,
     uint32_t n_outputs, uint32_t n_detectors, uint32_t n_anchors, uint32_t pe_dim,
-    uint32_t cols, uint32_t n_slices, uint32_t items_per_batch, double int_rescaler) {
+    uint32_t cols, uint32_t n_slices, uint32_t items_per_batch, double int_rescaler, bool quad) {
     __shared__ uint32_t cnt[kSeqWgRowsMax];
     __shared__ uint32_t cur[kSeqWgRowsMax];
     __shared__ uint8_t ent[kSeqWgEntries];
@@ -1103,14 +1104,18 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
             for (uint32_t sl = 0; sl < n_slices; sl++) {
                 const uint32_t col0 = sl * cols;
                 __syncthreads();  // scatter done / the previous slice is done with gv
-                for (uint32_t e = tid; e < nb * cols; e += kSeqWgThreads) {
+                // the batch's gradient rows, then a zero row (item nb) that the
+                // quad path reads for entries past a row's end
+                for (uint32_t e = tid; e < (nb + 1) * cols; e += kSeqWgThreads) {
                     const uint32_t it = e / cols, cc = col0 + e % cols;
-                    gv[e] = cc < n_outputs ? cv[(size_t)bitems[it] * n_outputs + cc] : 0u;
+                    gv[e] = (it < nb && cc < n_outputs) ? cv[(size_t)bitems[it] * n_outputs + cc] : 0u;
                 }
                 __syncthreads();
-                // lane group g (cols lanes) takes the rows whose entries start in
-                // [g E / G, (g + 1) E / G): about equal work whatever the row sizes
-                const uint32_t n_groups = kSeqWgThreads / cols, grp = tid / cols;
+                // lane group g (cols lanes, or 16 lanes of 4 columns on the quad
+                // path) takes the rows whose entries start in [g E / G, (g + 1) E / G):
+                // about equal work whatever the row sizes
+                const uint32_t lanes = quad ? 16u : cols;
+                const uint32_t n_groups = kSeqWgThreads / lanes, grp = tid / lanes;
                 const uint32_t total = cur[sub_rows - 1];  // entries of the batch
                 auto first_row = [&](uint32_t gi) -> uint32_t {
                     if (gi >= n_groups) return sub_rows;
@@ -1123,8 +1128,71 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
                     return gi == 0 ? 0u : lo;
                 };
                 const uint32_t rs = first_row(grp), re = first_row(grp + 1);
-                const uint32_t cc = col0 + my_col;
                 const bool store = first && OVERWRITE;
+                if (quad) {
+                    // 64-column slices, lane k of a group holding columns 4k .. 4k+3:
+                    // one 16-byte LDS read per entry.  The group walks its rows in
+                    // one loop: each turn adds four entries of the current row
+                    // (entries past its end read the zero row, adding +0, which
+                    // leaves a sum that starts at +0 unchanged) or, at the row's
+                    // end, writes the row and moves on.
+                    const uint32_t c4 = (tid & 15u) * 4u;
+                    const uint32_t cq = col0 + c4;
+                    uint32_t row = rs, e = 0, e1 = 0;
+                    if (row < re) {
+                        e1 = cur[row];
+                        e = e1 - cnt[row];
+                    }
+                    bool touched = e < e1;
+                    float af[4] = {0.f, 0.f, 0.f, 0.f};
+                    uint32_t ai[4] = {0u, 0u, 0u, 0u};
+                    while (row < re) {
+                        if (e < e1) {
+                            u32x4 g[4];
+#pragma unroll
+                            for (int u = 0; u < 4; u++) {
+                                const uint32_t it = e + u < e1 ? (uint32_t)ent[e + u] : nb;
+                                g[u] = *reinterpret_cast<const u32x4 *>(gv + it * 64u + c4);
+                            }
+#pragma unroll
+                            for (int u = 0; u < 4; u++)
+#pragma unroll
+                                for (int c = 0; c < 4; c++) {
+                                    if (INT_MODE) ai[c] += g[u][c];
+                                    else af[c] += __uint_as_float(g[u][c]);
+                                }
+                            e += 4;
+                        } else {
+                            if ((store || touched) && cq < n_outputs) {
+                                u32x4 *p = reinterpret_cast<u32x4 *>(dst + (size_t)row * n_outputs + cq);
+                                u32x4 o;
+                                if (store) {
+#pragma unroll
+                                    for (int c = 0; c < 4; c++) o[c] = INT_MODE ? ai[c] : __float_as_uint(af[c]);
+                                } else {
+                                    const u32x4 old = *p;
+#pragma unroll
+                                    for (int c = 0; c < 4; c++)
+                                        o[c] = INT_MODE ? (uint32_t)wrap_add((int32_t)ai[c], (int32_t)old[c])
+                                                        : __float_as_uint(__uint_as_float(old[c]) + af[c]);
+                                }
+                                *p = o;
+                            }
+#pragma unroll
+                            for (int c = 0; c < 4; c++) {
+                                af[c] = 0.f;
+                                ai[c] = 0u;
+                            }
+                            if (++row < re) {
+                                e1 = cur[row];
+                                e = e1 - cnt[row];
+                                touched = e < e1;
+                            }
+                        }
+                    }
+                    continue;
+                }
+                const uint32_t cc = col0 + my_col;
                 for (uint32_t row = rs; row < re; row++) {
                     const uint32_t e1 = cur[row];
                     uint32_t e = e1 - cnt[row];
@@ -1269,7 +1337,7 @@ uint32_t seq_wg_cols(const SeqShape &s) {
 // Items per batch: their entries (< seq each) and gradient rows must fit.
 uint32_t seq_wg_items(const SeqShape &s, uint32_t cols) {
     uint32_t n = (uint32_t)kSeqWgEntries / std::max<uint32_t>(1, s.seq - 1);
-    n = std::min<uint32_t>(n, (uint32_t)kSeqWgGvWords / cols);
+    n = std::min<uint32_t>(n, (uint32_t)kSeqWgGvWords / cols - 1);  // and the zero row
     return std::min<uint32_t>(n, (uint32_t)kSeqWgItems);
 }
 
@@ -1572,10 +1640,12 @@ hipError_t launch_backward_seq(const SeqShape &s, float *w, const float *g, cons
         const uint64_t grid = (uint64_t)s.n_detectors * (1u << s.n_anchors);
         if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
         const uint32_t ipb = seq_wg_items(s, cols);
+        // 16-byte row pieces: 64-column slices of whole quads, 16-byte aligned rows
+        const bool quad = cols == 64 && s.n_outputs % 4 == 0 && ((uintptr_t)target & 15) == 0;
 #define SPIKY_WSEQ(IM, OW)                                                                             \
     hipLaunchKernelGGL((k_wgrad_seq_sort<IM, OW>), dim3((uint32_t)grid), dim3(kSeqWgThreads), 0, st, cv, \
                        offsets, samples, pack, ppack, target, s.batch, s.seq, s.n_outputs,             \
-                       s.n_detectors, s.n_anchors, s.pe_dim, cols, n_slices, ipb, int_rescaler)
+                       s.n_detectors, s.n_anchors, s.pe_dim, cols, n_slices, ipb, int_rescaler, quad)
         if (int_mode) {
             if (overwrite) SPIKY_WSEQ(true, true); else SPIKY_WSEQ(true, false);
         } else {
