@@ -741,9 +741,9 @@ __global__ __launch_bounds__(kBlock) void k_propagate_seq_pairs(
             arow = kflip ? (mrow ^ (1u << (km + pe_dim))) : mrow;
             erow = peflip ? (mrow ^ (1u << pm)) : mrow;
         }
-        // every lane loads all three rows (a row that is not flipped is the main
-        // row again, whose dot then equals the main dot exactly): no divergent
-        // loads; columns past the last output re-read the last 4 and meet g = 0
+        // the flipped rows are loaded only by the pairs that use them (their
+        // 8 lanes share the flag, so a skipped row issues no requests); columns
+        // past the last output re-read the last 4 and meet g = 0
         double ms = 0.0, as = 0.0, es = 0.0;
         const float *mp = wt + (size_t)mrow * n_outputs;
         const float *ap = wt + (size_t)arow * n_outputs;
@@ -754,8 +754,8 @@ __global__ __launch_bounds__(kBlock) void k_propagate_seq_pairs(
             for (int k = 0; k < 4; k++) {
                 const uint32_t c = min((k0 + k) * 32 + 4 * s, n_outputs - 4);
                 mv[k] = *reinterpret_cast<const f32x4 *>(mp + c);
-                av[k] = *reinterpret_cast<const f32x4 *>(ap + c);
-                ev[k] = *reinterpret_cast<const f32x4 *>(ep + c);
+                av[k] = kflip ? *reinterpret_cast<const f32x4 *>(ap + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+                ev[k] = peflip ? *reinterpret_cast<const f32x4 *>(ep + c) : f32x4{0.f, 0.f, 0.f, 0.f};
             }
 #pragma unroll
             for (int k = 0; k < 4; k++) {
