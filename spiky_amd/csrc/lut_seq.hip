@@ -266,18 +266,23 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kSfThreads = 1024;
 constexpr int kSfTabFloats = 32768;   // 128 KiB sub-table slice
-constexpr int kSfItems = 2048;        // items sorted per chunk of a bucket
+constexpr int kSfItems = 1024;        // items sorted per chunk of a bucket
 constexpr int kSfPe = 2048;           // distances S - 1
 
+// C / 4 lanes own an item, lane l of it holding columns 4l .. 4l+3 of the slice:
+// one 16-byte LDS read per pair and four independent fp64 sums, each taking
+// the pairs in ascending i.
 template <int C, bool INT_MODE>
 __global__ __launch_bounds__(kSfThreads) void k_fill_seq_lds(
     const float *__restrict__ w, const uint2 *__restrict__ pack, const uint2 *__restrict__ ppack,
     const int32_t *__restrict__ offsets, const int32_t *__restrict__ samples,
     uint32_t *__restrict__ part, uint32_t batch, uint32_t seq, uint32_t n_outputs,
     uint32_t n_anchors, uint32_t pe_dim, uint32_t n_slices, double int_rescaler) {
-    constexpr int kSlots = kWave / C;  // items per wavefront
+    constexpr int L = C / 4;           // lanes per item
+    constexpr int kSlots = kWave / L;  // items per wavefront
+    constexpr int kPer = C / L;        // row offsets each lane forms per chunk of C pairs (4)
     __shared__ __attribute__((aligned(16))) float tab[kSfTabFloats + 64];  // + a zero row
-    __shared__ __attribute__((aligned(16))) uint32_t rowtab[kSfThreads];
+    __shared__ __attribute__((aligned(16))) uint32_t rowtab[(kSfThreads / kWave) * kSlots * C];
     __shared__ uint16_t ptab[kSfPe];
     __shared__ uint32_t keys[kSfItems];
     __shared__ uint32_t irow[kSfItems];
@@ -285,7 +290,7 @@ __global__ __launch_bounds__(kSfThreads) void k_fill_seq_lds(
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & (kWave - 1);
     const uint32_t wave = tid / kWave;
-    const uint32_t half = lane / C, cl = lane % C;
+    const uint32_t half = lane / L, cl = lane % L;
     uint32_t *my_rows = rowtab + (wave * kSlots + half) * C;
     const uint32_t slice = blockIdx.x % n_slices;
     const uint32_t tq = blockIdx.x / n_slices;
@@ -301,11 +306,11 @@ __global__ __launch_bounds__(kSfThreads) void k_fill_seq_lds(
 
     const int32_t *smp = samples + (size_t)t * n_rows;
     const uint2 *kp = pack + (size_t)t * n_rows;
-    const uint32_t col = c0 + cl;
+    const uint32_t col = c0 + cl * 4;
     const float *sub = w + ((size_t)t * n_q + q) * sub_rows * n_outputs + c0;
     const uint32_t n_e = sub_rows * (C / 4);
     const uint32_t zero_off = sub_rows * C * 4;  // byte offset of the zero row
-    const uint8_t *tab_b = reinterpret_cast<const uint8_t *>(tab);
+    const uint8_t *tab_b = reinterpret_cast<const uint8_t *>(tab) + cl * 16;
 
     // the first chunk's item rows: loads in flight with the staging loads
     uint32_t rr[kSfItems / kSfThreads];
@@ -335,6 +340,8 @@ __global__ __launch_bounds__(kSfThreads) void k_fill_seq_lds(
         ptab[d] = (uint16_t)(rec_idx(ppack[(size_t)t * (seq - 1) + d]) & pmask);
     if (tid < (uint32_t)C) tab[sub_rows * C + tid] = 0.0f;
 
+    // key record words of positions i (.y words)
+    const uint32_t *kw = reinterpret_cast<const uint32_t *>(kp) + 1;
     for (int32_t k0 = beg; k0 < end; k0 += kSfItems) {
         const uint32_t n = (uint32_t)min((int32_t)kSfItems, end - k0);
         uint32_t p2 = 1;
@@ -383,11 +390,13 @@ __global__ __launch_bounds__(kSfThreads) void k_fill_seq_lds(
         bool have = my < n;
         uint32_t row = have ? irow[keys[my] & 0xFFFFu] : 0u;
         uint32_t j = have ? row % seq : 0u;
-        // key record words of positions i: loaded unconditionally (index clamped
-        // into the sample) one chunk ahead, and first read through an empty asm
-        // so the wait for them lands where they are used
-        const uint32_t *kw = reinterpret_cast<const uint32_t *>(kp) + 1;  // .y words
-        uint32_t rec = kw[2 * (row - j + min(cl, j > 0 ? j - 1 : 0u))];
+        // key records of this lane's pairs of a chunk (i = i0 + cl + L k),
+        // loaded unconditionally (index clamped into the sample) one chunk
+        // ahead, and first read through an empty asm so the wait for them lands
+        // where they are used
+        uint32_t rec[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; k++) rec[k] = kw[2 * (row - j + min(cl + L * k, j > 0 ? j - 1 : 0u))];
         while (base < n) {
             uint32_t nbase = 0;
             if (lane == 0) nbase = atomicAdd(&next_item, (uint32_t)kSlots);
@@ -396,7 +405,9 @@ __global__ __launch_bounds__(kSfThreads) void k_fill_seq_lds(
             const bool nhave = nmy < n;
             const uint32_t nrow = nhave ? irow[keys[nmy] & 0xFFFFu] : 0u;
             const uint32_t nj = nhave ? nrow % seq : 0u;
-            const uint32_t nrec = kw[2 * (nrow - nj + min(cl, nj > 0 ? nj - 1 : 0u))];
+            uint32_t nrec[kPer];
+#pragma unroll
+            for (int k = 0; k < kPer; k++) nrec[k] = kw[2 * (nrow - nj + min(cl + L * k, nj > 0 ? nj - 1 : 0u))];
 
             const uint32_t brow = row - j;  // b * S
             // the wavefront walks to its longest item's j; shorter items read the
@@ -404,46 +415,57 @@ __global__ __launch_bounds__(kSfThreads) void k_fill_seq_lds(
             // unchanged: it can never be -0.0)
             uint32_t jw = j;
 #pragma unroll
-            for (int o = C; o < kWave; o <<= 1) jw = max(jw, (uint32_t)__shfl_xor(jw, o, kWave));
+            for (int o = L; o < kWave; o <<= 1) jw = max(jw, (uint32_t)__shfl_xor(jw, o, kWave));
             jw = uniform(jw);
-            double acc = 0.0;
+            double acc[4] = {0.0, 0.0, 0.0, 0.0};
             for (uint32_t i0 = 0; i0 < jw; i0 += C) {
-                // this chunk's C row offsets (bytes), one per lane
-                const uint32_t i = i0 + cl;
-                asm volatile("" : "+v"(rec));
-                my_rows[cl] = i < j ? (((((rec & 0xFFFFu) << pe_dim) | ptab[j - i - 1]) & (sub_rows - 1)) * C) * 4u
-                                    : zero_off;
-                rec = kw[2 * (brow + min(i + C, j > 0 ? j - 1 : 0u))];  // next chunk, in flight meanwhile
+                // this chunk's C row offsets (bytes), kPer per lane
+#pragma unroll
+                for (int k = 0; k < kPer; k++) {
+                    const uint32_t i = i0 + cl + L * k;
+                    asm volatile("" : "+v"(rec[k]));
+                    const uint32_t d = i < j ? j - i - 1 : 0u;
+                    my_rows[cl + L * k] =
+                        i < j ? (((((rec[k] & 0xFFFFu) << pe_dim) | ptab[d]) & (sub_rows - 1)) * C) * 4u : zero_off;
+                    rec[k] = kw[2 * (brow + min(i + C, j > 0 ? j - 1 : 0u))];  // next chunk, in flight meanwhile
+                }
                 __builtin_amdgcn_wave_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
 #pragma unroll
                 for (int u = 0; u < C; u += 4) {
                     const uint4 r4 = *reinterpret_cast<const uint4 *>(my_rows + u);
-                    const float v0 = *reinterpret_cast<const float *>(tab_b + r4.x + cl * 4);
-                    const float v1 = *reinterpret_cast<const float *>(tab_b + r4.y + cl * 4);
-                    const float v2 = *reinterpret_cast<const float *>(tab_b + r4.z + cl * 4);
-                    const float v3 = *reinterpret_cast<const float *>(tab_b + r4.w + cl * 4);
-                    acc += (double)v0;
-                    acc += (double)v1;
-                    acc += (double)v2;
-                    acc += (double)v3;
+                    const f32x4 v0 = *reinterpret_cast<const f32x4 *>(tab_b + r4.x);
+                    const f32x4 v1 = *reinterpret_cast<const f32x4 *>(tab_b + r4.y);
+                    const f32x4 v2 = *reinterpret_cast<const f32x4 *>(tab_b + r4.z);
+                    const f32x4 v3 = *reinterpret_cast<const f32x4 *>(tab_b + r4.w);
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        acc[c] += (double)v0[c];
+                        acc[c] += (double)v1[c];
+                        acc[c] += (double)v2[c];
+                        acc[c] += (double)v3[c];
+                    }
                 }
                 __builtin_amdgcn_wave_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
             }
             if (have && col < n_outputs) {
-                uint32_t v;
-                if (INT_MODE)
-                    v = (uint32_t)(j > 0 ? (int32_t)(acc * kDenom32 * int_rescaler) : 0);
-                else
-                    v = j > 0 ? __float_as_uint((float)acc) : 0x80000000u;
-                __builtin_nontemporal_store(v, part + ((size_t)t * n_rows + row) * n_outputs + col);
+                u32x4 v;
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    if (INT_MODE)
+                        v[c] = (uint32_t)(j > 0 ? (int32_t)(acc[c] * kDenom32 * int_rescaler) : 0);
+                    else
+                        v[c] = j > 0 ? __float_as_uint((float)acc[c]) : 0x80000000u;
+                }
+                __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(part + ((size_t)t * n_rows + row) * n_outputs + col));
             }
             base = nbase;
             have = nhave;
             row = nrow;
             j = nj;
-            rec = nrec;
+#pragma unroll
+            for (int k = 0; k < kPer; k++) rec[k] = nrec[k];
         }
     }
 }
