@@ -5,12 +5,15 @@ unembedding (reference src/spiky/lut/LUTTransformer.py:15-480).
 Every LUT layer runs on this build's HIP kernels: the attention layers are
 `LUTLayer`s with `sequence_length = context_size` (causal pairs i < j, rows
 Q_j | K_i | PE_(j-i-1)); the feed-forward and unembedding layers are
-`LUTLayer`s applied to the [B*S, 1, E] reshape of the activations.
+`LUTLayer`s applied to the [B*S, 1, E] reshape of the activations.  A 2-D
+`embedding_dim` (h, w) makes each attention layer a `Conv2DLUTLayer` over the
+[h, w] grid with one receptive field covering it (sparse lookup connectivity,
+LUTTransformer.py:43-67); everything else sees E = h * w features.
 """
 import torch
 import torch.nn as nn
 
-from .LUTLayer import GradientPolicy, LUTLayer, LUTSharedContext, SynapseMeta
+from .LUTLayer import Conv2DLUTLayer, GradientPolicy, LUTLayer, LUTSharedContext, SynapseMeta
 
 
 class LUTTransformer(nn.Module):
@@ -28,9 +31,13 @@ class LUTTransformer(nn.Module):
                  summation_dtype=torch.float32, _int_rescaler=0.001, _forward_group_size=32,
                  _backward_group_size=32, dropout=0.0, use_batch_norm=False):
         super().__init__()
-        if not isinstance(embedding_dim, int):
-            raise NotImplementedError("2-D embedding shapes (a Conv2DLUTLayer attention) are not part of "
-                                      "this build; pass an int embedding_dim")
+        if isinstance(embedding_dim, int):
+            n_embeddings = embedding_dim
+        else:
+            # LUTTransformer.py:111-115
+            embedding_dim = tuple(embedding_dim)
+            assert len(embedding_dim) == 2
+            n_embeddings = embedding_dim[0] * embedding_dim[1]
         self.vocab_size = vocab_size
         self.embedding_dim = embedding_dim
         self.context_size = context_size
@@ -55,7 +62,7 @@ class LUTTransformer(nn.Module):
             lut_shared_context.to_device(self.device)
         self.lut_shared_context = lut_shared_context
 
-        E = embedding_dim
+        E = n_embeddings
         self.token_embedder = nn.Embedding(vocab_size, E, device=self.device)
         self.token_embedder.weight.requires_grad_(False)
         with torch.no_grad():
@@ -74,12 +81,23 @@ class LUTTransformer(nn.Module):
         self.layers = nn.ModuleList()
         for li in range(num_layers):
             block = nn.ModuleDict()
-            block["attention_lut"] = LUTLayer(
-                n_inputs=E, n_anchors_per_detector=self.n_anchors_per_detector_attention,
-                n_detectors=n_detectors * num_heads, n_outputs=E, sequence_length=context_size,
-                concatenation_product=concatenation_product, sliced_product_mode=sliced_product_mode,
-                positional_dim=positional_dim, unified_pe=unified_pe,
-                random_seed=None if seed is None else seed + li * num_heads, **common)
+            attention_seed = None if seed is None else seed + li * num_heads
+            if isinstance(embedding_dim, int):
+                block["attention_lut"] = LUTLayer(
+                    n_inputs=E, n_anchors_per_detector=self.n_anchors_per_detector_attention,
+                    n_detectors=n_detectors * num_heads, n_outputs=E, sequence_length=context_size,
+                    concatenation_product=concatenation_product, sliced_product_mode=sliced_product_mode,
+                    positional_dim=positional_dim, unified_pe=unified_pe, random_seed=attention_seed,
+                    **common)
+            else:
+                # LUTTransformer.py:43-67
+                block["attention_lut"] = Conv2DLUTLayer(
+                    input_shape=embedding_dim, n_anchors_per_detector=self.n_anchors_per_detector_attention,
+                    detectors_shape=(1, n_detectors * num_heads), output_kernel_shape=embedding_dim,
+                    sequence_length=context_size, concatenation_product=concatenation_product,
+                    sliced_product_mode=sliced_product_mode, positional_dim=positional_dim,
+                    unified_pe=unified_pe, receptive_field_shape=embedding_dim,
+                    receptive_field_stride_shape=embedding_dim, random_seed=attention_seed, **common)
             block["attention_dropout"] = nn.Dropout(dropout)
             block["attention_bn"] = nn.BatchNorm1d(E, device=self.device) if use_batch_norm else None
             if not no_ffn:
@@ -118,11 +136,14 @@ class LUTTransformer(nn.Module):
     def forward(self, tokens):
         """tokens [B, S] -> logits [B, S, vocab_size] (LUTTransformer.py:209-271)."""
         B, S = tokens.shape[0], self.context_size
-        E = self.embedding_dim
+        grid = not isinstance(self.embedding_dim, int)
+        E = self.embedding_dim[0] * self.embedding_dim[1] if grid else self.embedding_dim
         z = self.token_embedder(tokens)
         if self._debug_last_forward is not None:
             self._debug_last_forward = [tokens.to(torch.float32), z.detach().clone()]
         for block in self.layers:
+            if grid:
+                z = z.reshape((B, S) + self.embedding_dim)
             a = block["attention_lut"](z)
             if self._debug_last_forward is not None:
                 self._debug_last_forward.append(a.detach().clone())
@@ -130,6 +151,8 @@ class LUTTransformer(nn.Module):
             if self.use_batch_norm:
                 a = self._bn(block["attention_bn"], a)
             z = z + a
+            if grid:
+                z = z.reshape(B, S, E)
             if not self.no_ffn:
                 f = block["ffn"](z.reshape(B * S, 1, E)).reshape(B, S, E)
                 if self._debug_last_forward is not None:

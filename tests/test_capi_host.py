@@ -274,3 +274,26 @@ def test_product_layer_construction():
                  sliced_product_mode=True, positional_dim=4)
     with pytest.raises(ValueError, match="doesn't make sense in concatenation product mode"):
         LUTLayer(16, 4, 8, 32, sequence_length=6, sliced_product_mode=True, positional_dim=16)
+
+
+def test_transformer_2d_embedding_construction():
+    """A 2-D embedding_dim builds Conv2DLUTLayer attention layers over the grid
+    whose one receptive field covers it (LUTTransformer.py:43-67, 111-115):
+    fully connected lookups, anchors among the h * w inputs, E = h * w
+    features for the embedding, feed-forward and unembedding layers."""
+    from spiky_amd import LUTTransformer
+    from spiky_amd.lut.LUTLayer import Conv2DLUTLayer, LUTLayer
+    m = LUTTransformer(vocab_size=16, embedding_dim=(4, 2), context_size=5, positional_dim=2, num_layers=2,
+                       num_heads=2, n_detectors=3, n_anchors_per_detector=4, n_anchors_per_detector_attention=3,
+                       seed=11)
+    assert m.token_embedder.weight.shape == (16, 8)
+    for block in m.layers:
+        att = block["attention_lut"]
+        assert type(att) is Conv2DLUTLayer and att._is_fully_connected
+        assert att.input_shape() == (4, 2) and att.output_shape() == (4, 2)
+        assert att._n_detectors == 6 and att._n_outputs == 8
+        assert att._weights.numel() == 6 * (1 << (2 * 3 + 2)) * 8
+        a = att._detector_anchors
+        assert a.min() >= 0 and a.max() < 8
+        assert isinstance(block["ffn"], LUTLayer) and block["ffn"]._n_outputs == 8
+    assert m.unembedder._lut_dm.get_number_of_inputs() == 8

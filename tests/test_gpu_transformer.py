@@ -17,9 +17,14 @@ def _anchors(layer):
     return layer._detector_anchors.detach().cpu().numpy()
 
 
+def _n_embeddings(model):
+    e = model.embedding_dim
+    return e if isinstance(e, int) else e[0] * e[1]
+
+
 def oracle_forward(oracle, model, tokens):
     B, S = tokens.shape
-    E, V = model.embedding_dim, model.vocab_size
+    E, V = _n_embeddings(model), model.vocab_size
     z = model.token_embedder.weight.detach().cpu().numpy()[tokens.cpu().numpy()].astype(np.float32)
     saved = []
     for block in model.layers:
@@ -47,13 +52,24 @@ def oracle_forward(oracle, model, tokens):
     return logits.reshape(B, S, V), saved
 
 
-def test_transformer_forward_backward(oracle, cuda_device):
+@pytest.mark.parametrize("embedding_dim", [16, (4, 4)])
+def test_transformer_forward_backward(oracle, cuda_device, embedding_dim):
+    """With a 2-D embedding_dim (h, w) each attention layer is a Conv2DLUTLayer
+    over the [h, w] grid whose receptive field covers it
+    (LUTTransformer.py:43-67, 226-252): its anchors come from the grid's
+    h * w inputs in row-major order and its lookups reach every output, so
+    the same oracle chain over E = h * w features applies."""
     from spiky_amd import LUTTransformer
+    from spiky_amd.lut.LUTLayer import Conv2DLUTLayer, LUTLayer
     dev = cuda_device
-    B, S, V, E = 3, 9, 16, 16
-    model = LUTTransformer(vocab_size=V, embedding_dim=E, context_size=S, positional_dim=2, num_layers=2,
-                           num_heads=2, n_detectors=3, n_anchors_per_detector=4,
+    B, S, V = 3, 9, 16
+    model = LUTTransformer(vocab_size=V, embedding_dim=embedding_dim, context_size=S, positional_dim=2,
+                           num_layers=2, num_heads=2, n_detectors=3, n_anchors_per_detector=4,
                            n_anchors_per_detector_attention=3, device=dev, seed=11)
+    E = _n_embeddings(model)
+    # LUTLayer is the one-window Conv2DLUTLayer: compare the exact classes
+    kind = LUTLayer if isinstance(embedding_dim, int) else Conv2DLUTLayer
+    assert all(type(b["attention_lut"]) is kind for b in model.layers)
     g = torch.Generator().manual_seed(5)
     with torch.no_grad():
         for p in (l._weights for l in model._lut_layers()):
@@ -99,3 +115,4 @@ def test_transformer_forward_backward(oracle, cuda_device):
             grad_in = (grad_in + xg).astype(np.float32)
         else:
             grad_in = xg
+
