@@ -475,6 +475,7 @@ __global__ __launch_bounds__(kSfThreads) void k_fill_seq_lds(
 constexpr int kDppHalfMirror = 0x141;
 constexpr int kDppXor1 = 0xB1;
 constexpr int kDppXor2 = 0x4E;
+constexpr int kRecStage = 512;  // key / positional records an item stages in LDS (j <= 512)
 
 template <int CTRL>
 __device__ __forceinline__ void rs16_step(double (&v)[16], int m, bool upper) {
@@ -542,6 +543,7 @@ __global__ __launch_bounds__(kBlock) void k_propagate_seq(
     constexpr int kPB = NJ == 1 ? 4 : (NJ == 2 ? 2 : 1);  // pairs per batch
     constexpr int kNV = 2 * kPB;
     __shared__ double wpart[kWPB];
+    __shared__ uint2 srec[kRecStage], sprec[kRecStage];
     const uint32_t lane = threadIdx.x & (kWave - 1);
     const uint32_t wave = uniform(threadIdx.x / kWave);
     const uint32_t n_rows = batch * seq;
@@ -562,6 +564,15 @@ __global__ __launch_bounds__(kBlock) void k_propagate_seq(
     const uint32_t Q = rec_idx(qr);
     const float qd = rec_md(qr);
     const uint32_t qsub = ALT ? (Q ^ (1u << qm)) : Q;  // the sub-table read
+    // the item's key records of positions i < j and positional records of
+    // distances d < j, staged once so a batch waits for one L2 trip (its rows)
+    const bool staged = j <= (uint32_t)kRecStage;
+    if (staged)
+        for (uint32_t i = threadIdx.x; i < j; i += kBlock) {
+            srec[i] = kp[i];
+            sprec[i] = pp[i];
+        }
+    __syncthreads();
 
     float gv[NJ][4];
     bool act[NJ];
@@ -589,8 +600,8 @@ __global__ __launch_bounds__(kBlock) void k_propagate_seq(
         uint32_t v_main = 0, v_alt = 0, v_pe = 0, v_flags = 0;
         if (lane < n) {
             const uint32_t i = i0 + lane;
-            const uint2 kr = kp[i];
-            const uint2 pr = pp[j - i - 1];
+            const uint2 kr = staged ? srec[i] : kp[i];
+            const uint2 pr = staged ? sprec[j - i - 1] : pp[j - i - 1];
             const uint32_t K = rec_idx(kr), P = rec_idx(pr) & pmask;
             const float kd = rec_md(kr);
             const bool qflip = fabsf(qd) < fabsf(kd);
@@ -660,13 +671,13 @@ __global__ __launch_bounds__(kBlock) void k_propagate_seq(
         const uint32_t u = vi / 2;
         if (lane < 8 && u < n && (kNV == 8 || (kNV == 4 ? ((l8 >> 1) & 1u) == 0 : (l8 & 3u) == 0))) {
             const uint32_t i = i0 + u;
-            const uint2 kr = kp[i];
+            const uint2 kr = staged ? srec[i] : kp[i];
             if ((vi & 1u) == 0) {
                 const float kd = rec_md(kr);
                 if (!(fabsf(qd) < fabsf(kd)) && rec_mi(kr) >= 0)
                     atomicAdd(dk + ((size_t)b * n_detectors + t) * seq + i, du_of_margin(kd) * items[0]);
             } else {
-                const uint2 pr = pp[j - i - 1];
+                const uint2 pr = staged ? sprec[j - i - 1] : pp[j - i - 1];
                 const int32_t pm = rec_mi(pr);
                 const float kd = rec_md(kr), pdl = rec_md(pr);
                 if (pe_dim > 0 && pm >= 0 && fabsf(pdl) < fabsf(qd) && fabsf(pdl) < fabsf(kd))
@@ -715,6 +726,7 @@ __global__ __launch_bounds__(kBlock) void k_propagate_seq_pairs(
     uint32_t wg_per_xcd) {
     __shared__ __attribute__((aligned(16))) double gd[kPairMaxO];
     __shared__ double wpart[kWPB];
+    __shared__ uint2 srec[kRecStage], sprec[kRecStage];
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & (kWave - 1);
     const uint32_t wave = uniform(tid / kWave);
@@ -739,6 +751,14 @@ __global__ __launch_bounds__(kBlock) void k_propagate_seq_pairs(
     // (the clamped loads there add 0)
     for (uint32_t c = tid; c < ((n_chunks + 3) / 4) * 128; c += kBlock)
         gd[c] = c < n_outputs ? (double)g[((size_t)b * seq + j) * n_outputs + c] : 0.0;
+    // the item's key and positional records, staged once (one L2 trip per pair
+    // batch instead of two)
+    const bool staged = j <= (uint32_t)kRecStage;
+    if (staged)
+        for (uint32_t i = tid; i < j; i += kBlock) {
+            srec[i] = kp[i];
+            sprec[i] = pp[i];
+        }
     __syncthreads();
 
     const uint32_t p = lane / 8, s = lane % 8;
@@ -750,8 +770,8 @@ __global__ __launch_bounds__(kBlock) void k_propagate_seq_pairs(
         uint32_t mrow = 0, arow = 0, erow = 0;
         bool kflip = false, peflip = false, qs = false;
         if (live) {
-            const uint2 kr = kp[i];
-            const uint2 pr = pp[j - i - 1];
+            const uint2 kr = staged ? srec[i] : kp[i];
+            const uint2 pr = staged ? sprec[j - i - 1] : pp[j - i - 1];
             const uint32_t K = rec_idx(kr), P = rec_idx(pr) & pmask;
             const int32_t km = rec_mi(kr), pm = rec_mi(pr);
             const float kd = rec_md(kr), pdl = rec_md(pr);
