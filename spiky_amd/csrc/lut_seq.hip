@@ -269,18 +269,35 @@ constexpr int kSfTabFloats = 32768;   // 128 KiB sub-table slice
 constexpr int kSfItems = 1024;        // items sorted per chunk of a bucket
 constexpr int kSfPe = 2048;           // distances S - 1
 
-// C / 4 lanes own an item, lane l of it holding columns 4l .. 4l+3 of the slice:
-// one 16-byte LDS read per pair and four independent fp64 sums, each taking
-// the pairs in ascending i.
+// VW consecutive columns of one LDS row (VW = 1, 2 or 4 floats).
+template <int VW>
+__device__ __forceinline__ void lds_cols(const uint8_t *p, float (&v)[VW]) {
+    if constexpr (VW == 4) {
+        const f32x4 q = *reinterpret_cast<const f32x4 *>(p);
+        v[0] = q[0]; v[1] = q[1]; v[2] = q[2]; v[3] = q[3];
+    } else if constexpr (VW == 2) {
+        const float2 q = *reinterpret_cast<const float2 *>(p);
+        v[0] = q.x; v[1] = q.y;
+    } else {
+        v[0] = *reinterpret_cast<const float *>(p);
+    }
+}
+
+// C / VW lanes own an item, lane l of it holding columns VW l .. VW l + VW-1 of
+// the slice (VW = 4 at 64-column slices, 2 at 32, 1 below): 16 lanes an item,
+// so a bucket of ~128 items makes ~32 item groups for the 16 wavefronts and
+// the longest-first queue balances them; one VW-float LDS read per pair and
+// VW independent fp64 sums, each taking the pairs in ascending i.
 template <int C, bool INT_MODE>
 __global__ __launch_bounds__(kSfThreads) void k_fill_seq_lds(
     const float *__restrict__ w, const uint2 *__restrict__ pack, const uint2 *__restrict__ ppack,
     const int32_t *__restrict__ offsets, const int32_t *__restrict__ samples,
     uint32_t *__restrict__ part, uint32_t batch, uint32_t seq, uint32_t n_outputs,
     uint32_t n_anchors, uint32_t pe_dim, uint32_t n_slices, double int_rescaler) {
-    constexpr int L = C / 4;           // lanes per item
+    constexpr int VW = C >= 64 ? 4 : (C >= 32 ? 2 : 1);  // columns per lane
+    constexpr int L = C / VW;          // lanes per item
     constexpr int kSlots = kWave / L;  // items per wavefront
-    constexpr int kPer = C / L;        // row offsets each lane forms per chunk of C pairs (4)
+    constexpr int kPer = C / L;        // row offsets each lane forms per chunk of C pairs (VW)
     __shared__ __attribute__((aligned(16))) float tab[kSfTabFloats + 64];  // + a zero row
     __shared__ __attribute__((aligned(16))) uint32_t rowtab[(kSfThreads / kWave) * kSlots * C];
     __shared__ uint16_t ptab[kSfPe];
@@ -306,11 +323,11 @@ __global__ __launch_bounds__(kSfThreads) void k_fill_seq_lds(
 
     const int32_t *smp = samples + (size_t)t * n_rows;
     const uint2 *kp = pack + (size_t)t * n_rows;
-    const uint32_t col = c0 + cl * 4;
+    const uint32_t col = c0 + cl * VW;
     const float *sub = w + ((size_t)t * n_q + q) * sub_rows * n_outputs + c0;
     const uint32_t n_e = sub_rows * (C / 4);
     const uint32_t zero_off = sub_rows * C * 4;  // byte offset of the zero row
-    const uint8_t *tab_b = reinterpret_cast<const uint8_t *>(tab) + cl * 16;
+    const uint8_t *tab_b = reinterpret_cast<const uint8_t *>(tab) + cl * VW * 4;
 
     // the first chunk's item rows: loads in flight with the staging loads
     uint32_t rr[kSfItems / kSfThreads];
@@ -417,7 +434,9 @@ __global__ __launch_bounds__(kSfThreads) void k_fill_seq_lds(
 #pragma unroll
             for (int o = L; o < kWave; o <<= 1) jw = max(jw, (uint32_t)__shfl_xor(jw, o, kWave));
             jw = uniform(jw);
-            double acc[4] = {0.0, 0.0, 0.0, 0.0};
+            double acc[VW];
+#pragma unroll
+            for (int c = 0; c < VW; c++) acc[c] = 0.0;
             for (uint32_t i0 = 0; i0 < jw; i0 += C) {
                 // this chunk's C row offsets (bytes), kPer per lane
 #pragma unroll
@@ -434,12 +453,13 @@ __global__ __launch_bounds__(kSfThreads) void k_fill_seq_lds(
 #pragma unroll
                 for (int u = 0; u < C; u += 4) {
                     const uint4 r4 = *reinterpret_cast<const uint4 *>(my_rows + u);
-                    const f32x4 v0 = *reinterpret_cast<const f32x4 *>(tab_b + r4.x);
-                    const f32x4 v1 = *reinterpret_cast<const f32x4 *>(tab_b + r4.y);
-                    const f32x4 v2 = *reinterpret_cast<const f32x4 *>(tab_b + r4.z);
-                    const f32x4 v3 = *reinterpret_cast<const f32x4 *>(tab_b + r4.w);
+                    float v0[VW], v1[VW], v2[VW], v3[VW];
+                    lds_cols<VW>(tab_b + r4.x, v0);
+                    lds_cols<VW>(tab_b + r4.y, v1);
+                    lds_cols<VW>(tab_b + r4.z, v2);
+                    lds_cols<VW>(tab_b + r4.w, v3);
 #pragma unroll
-                    for (int c = 0; c < 4; c++) {
+                    for (int c = 0; c < VW; c++) {
                         acc[c] += (double)v0[c];
                         acc[c] += (double)v1[c];
                         acc[c] += (double)v2[c];
@@ -450,15 +470,14 @@ __global__ __launch_bounds__(kSfThreads) void k_fill_seq_lds(
                 __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
             }
             if (have && col < n_outputs) {
-                u32x4 v;
+                uint32_t *dst = part + ((size_t)t * n_rows + row) * n_outputs + col;
 #pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    if (INT_MODE)
-                        v[c] = (uint32_t)(j > 0 ? (int32_t)(acc[c] * kDenom32 * int_rescaler) : 0);
-                    else
-                        v[c] = j > 0 ? __float_as_uint((float)acc[c]) : 0x80000000u;
+                for (int c = 0; c < VW; c++) {
+                    const uint32_t v = INT_MODE
+                        ? (uint32_t)(j > 0 ? (int32_t)(acc[c] * kDenom32 * int_rescaler) : 0)
+                        : (j > 0 ? __float_as_uint((float)acc[c]) : 0x80000000u);
+                    __builtin_nontemporal_store(v, dst + c);
                 }
-                __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(part + ((size_t)t * n_rows + row) * n_outputs + col));
             }
             base = nbase;
             have = nhave;
