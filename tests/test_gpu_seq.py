@@ -58,7 +58,7 @@ def close_rows(gpu, cpu, rows, n_terms):
 
 
 def run_seq(oracle, B, S, I, T, Nc, Npe, O, fgs=32, bgs=32, seed=0, int_rescaler=None, lr=1.0,
-            int_grad=False, internal=False, inputs=None):
+            int_grad=False, internal=False, inputs=None, accumulate=False):
     dev = torch.device("cuda:0")
     int_mode = int_rescaler is not None
     x, anchors, W, pe, go = inputs if inputs is not None else seq_inputs(seed, B, S, I, T, Nc, Npe, O, int_grad)
@@ -83,6 +83,15 @@ def run_seq(oracle, B, S, I, T, Nc, Npe, O, fgs=32, bgs=32, seed=0, int_rescaler
         W_before = Wd.clone()
         dm.backward_backprop_concat(Wd, B, ged, ad, idx, md, mi, xg, 0.1, pli, pmd, pmi, peg, None)
         wg = None
+    elif accumulate:
+        # the caller's gradient buffer already holds values (every 7th one -0.0):
+        # the kernels add to it, and rows no pair reaches keep their bits
+        gp = torch.Generator().manual_seed(seed + 100)
+        prefill = torch.randn(Wd.numel(), generator=gp) * 0.01
+        prefill[::7] = -0.0
+        wg = prefill.to(dev)
+        dm.backward_backprop_concat(Wd, B, ged, ad, idx, md, mi, xg, -1.0, pli, pmd, pmi, peg, wg,
+                                    overwrite_weights_gradients=False)
     else:
         wg = torch.empty_like(Wd)
         dm.backward_backprop_concat(Wd, B, ged, ad, idx, md, mi, xg, -1.0, pli, pmd, pmi, peg, wg,
@@ -131,6 +140,17 @@ def run_seq(oracle, B, S, I, T, Nc, Npe, O, fgs=32, bgs=32, seed=0, int_rescaler
         oracle.gather_wgrad_seq(gn, ridx, rpli, rW, B, O, T, S, Nc, Npe, ogs=fgs, first_meta_lr=lr,
                                 external_lr=np.float32(ext))
         got, ref, base = Wd.cpu().numpy(), rW, W_before.cpu().numpy()
+    elif accumulate:
+        base = prefill.numpy()
+        rwg = base.copy()
+        oracle.gather_wgrad_seq(gn, ridx, rpli, rwg, B, O, T, S, Nc, Npe, ogs=fgs, first_meta_lr=lr)
+        got, ref = wg.cpu().numpy(), rwg
+        reach = np.zeros(Wn.size, np.float32)
+        oracle.gather_wgrad_seq(np.ones_like(gn), ridx, rpli, reach, B, O, T, S, Nc, Npe, ogs=fgs,
+                                first_meta_lr=1.0)
+        untouched = reach == 0
+        assert untouched.any() and (~untouched).any()
+        assert np.array_equal(got[untouched].view(np.uint32), base[untouched].view(np.uint32))
     else:
         rwg = np.zeros(Wn.size, np.float32)
         oracle.gather_wgrad_seq(gn, ridx, rpli, rwg, B, O, T, S, Nc, Npe, ogs=fgs, first_meta_lr=lr,
@@ -205,6 +225,16 @@ def test_seq_int32_summation(oracle, cuda_device):
 
 def test_seq_internal_policy(oracle, cuda_device):
     run_seq(oracle, 2, 9, 16, 3, 3, 2, 32, seed=7, lr=0.5, internal=True)
+
+
+def test_seq_internal_policy_wide_rows(oracle, cuda_device):
+    # 64-column weight-gradient slices (16-byte row pieces) adding into the weights
+    run_seq(oracle, 2, 40, 16, 3, 3, 2, 64, seed=15, lr=0.5, internal=True)
+
+
+def test_seq_accumulate_into_gradient(oracle, cuda_device):
+    # the attention layer's per-table shape, adding into a filled gradient buffer
+    run_seq(oracle, 2, 256, 64, 2, 6, 4, 256, seed=16, accumulate=True)
 
 
 def test_seq_eval_mode(oracle, cuda_device):
