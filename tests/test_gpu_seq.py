@@ -195,7 +195,7 @@ def test_seq_attention_layer_shape(oracle, cuda_device):
 
 def test_seq_one_bucket_chunks(oracle, cuda_device):
     # all-zero inputs put every (b, s) of a table in one Q bucket: more items
-    # than one sorted chunk of the forward (2048), many weight-gradient
+    # than one sorted chunk of the forward (1024), many weight-gradient
     # batches, and rows past one staged key chunk (8192)
     B, S, I, T, Nc, Npe, O = 160, 64, 16, 2, 3, 2, 64
     x, anchors, W, pe, go = seq_inputs(12, B, S, I, T, Nc, Npe, O)
