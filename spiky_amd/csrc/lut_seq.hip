@@ -1196,8 +1196,9 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
                     // one 16-byte LDS read per entry.  The group walks its rows in
                     // one loop: each turn adds kQuadStep entries of the current row
                     // (entries past its end read the zero row, adding +0, which
-                    // leaves a sum that starts at +0 unchanged) or, at the row's
-                    // end, writes the row and moves on.
+                    // leaves a sum that starts at +0 unchanged), and the row's last
+                    // turn -- the only turn of a row without entries -- also writes
+                    // it and moves on.
                     const uint32_t c4 = (tid & 15u) * 4u;
                     const uint32_t cq = col0 + c4;
                     uint32_t row = rs, e = 0, e1 = 0;
@@ -1209,22 +1210,22 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
                     float af[4] = {0.f, 0.f, 0.f, 0.f};
                     uint32_t ai[4] = {0u, 0u, 0u, 0u};
                     while (row < re) {
-                        if (e < e1) {
-                            u32x4 g[kQuadStep];
+                        u32x4 g[kQuadStep];
 #pragma unroll
-                            for (int u = 0; u < kQuadStep; u++) {
-                                const uint32_t it = e + u < e1 ? (uint32_t)ent[e + u] : nb;
-                                g[u] = *reinterpret_cast<const u32x4 *>(gv + it * 64u + c4);
+                        for (int u = 0; u < kQuadStep; u++) {
+                            const uint32_t it = e + u < e1 ? (uint32_t)ent[e + u] : nb;
+                            g[u] = *reinterpret_cast<const u32x4 *>(gv + it * 64u + c4);
+                        }
+#pragma unroll
+                        for (int u = 0; u < kQuadStep; u++)
+#pragma unroll
+                            for (int c = 0; c < 4; c++) {
+                                if (INT_MODE) ai[c] += g[u][c];
+                                else af[c] += __uint_as_float(g[u][c]);
                             }
-#pragma unroll
-                            for (int u = 0; u < kQuadStep; u++)
-#pragma unroll
-                                for (int c = 0; c < 4; c++) {
-                                    if (INT_MODE) ai[c] += g[u][c];
-                                    else af[c] += __uint_as_float(g[u][c]);
-                                }
-                            e += kQuadStep;
-                        } else {
+                        e += kQuadStep;
+                        if (e >= e1) {
+                            // the row's last turn: write it and move on
                             if ((store || touched) && cq < n_outputs) {
                                 u32x4 *p = reinterpret_cast<u32x4 *>(dst + (size_t)row * n_outputs + cq);
                                 u32x4 o;
