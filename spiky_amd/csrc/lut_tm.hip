@@ -46,6 +46,7 @@ constexpr int kTmPF = 2;  // tables per pipeline stage
 // HIP's struct-based float4 is demoted to scratch memory
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ double du_of_margin(float md) {
     double du = (double)md;
@@ -187,30 +188,44 @@ struct StageLayout {
 
 // Each thread's share of one stage: row chunks c = tid and tid + 1024 (E <= 256
 // rows x 8 chunks of 16 bytes), and for the first kKeyPieces threads one
-// 16-byte piece of the stage's key row.
+// 8-byte piece of the stage's key row (8-byte pieces keep the staging
+// registers every thread carries to two per table).
 template <typename KEY, int SPT>
 struct KeyPieces {
-    static constexpr int kPer = 16 / (int)sizeof(KEY);
+    static constexpr int kPer = 8 / (int)sizeof(KEY);
     static constexpr int kCount = StageLayout<KEY, SPT>::kKeys / kPer;
 };
 
-// Row chunk of 4 weights at (row, col): fp32 tables load them; int8 tables
-// load 4 bytes and stage scale[t] * (float)q, the int8 mapping's weight.
+// What a thread holds of a stage between its loads and its LDS writes: fp32
+// quads, or for int8 tables the raw 4-byte words and the tables' scales,
+// converted when written (4x fewer staging registers).
 template <typename WT>
-__device__ __forceinline__ f32x4 load_quad(const WT *p, float sc);
+struct StageRaw {
+    typedef f32x4 type;
+};
 template <>
-__device__ __forceinline__ f32x4 load_quad<float>(const float *p, float) {
+struct StageRaw<int8_t> {
+    typedef uint32_t type;
+};
+template <typename WT>
+__device__ __forceinline__ typename StageRaw<WT>::type load_raw(const WT *p);
+template <>
+__device__ __forceinline__ f32x4 load_raw<float>(const float *p) {
     return *reinterpret_cast<const f32x4 *>(p);
 }
 template <>
-__device__ __forceinline__ f32x4 load_quad<int8_t>(const int8_t *p, float sc) {
-    const uint32_t raw = *reinterpret_cast<const uint32_t *>(p);
+__device__ __forceinline__ uint32_t load_raw<int8_t>(const int8_t *p) {
+    return *reinterpret_cast<const uint32_t *>(p);
+}
+__device__ __forceinline__ f32x4 raw_quad(const f32x4 &v, float) { return v; }
+__device__ __forceinline__ f32x4 raw_quad(uint32_t raw, float sc) {
     return f32x4{sc * (float)(int8_t)(raw & 0xFFu), sc * (float)(int8_t)((raw >> 8) & 0xFFu),
                  sc * (float)(int8_t)((raw >> 16) & 0xFFu), sc * (float)(int8_t)(raw >> 24)};
 }
 
 template <typename KEY, int SPT, typename WT = float>
-__device__ __forceinline__ void stage_load(f32x4 (&rows)[kTmPF][2], u32x4 (&keys)[kTmPF],
+__device__ __forceinline__ void stage_load(typename StageRaw<WT>::type (&rows)[kTmPF][2],
+                                           float (&scs)[kTmPF], u32x2 (&keys)[kTmPF],
                                            const WT *__restrict__ w,
                                            const KEY *__restrict__ keys_t, uint32_t tid,
                                            uint32_t t_first, uint32_t nt, uint32_t n_entries,
@@ -221,37 +236,37 @@ __device__ __forceinline__ void stage_load(f32x4 (&rows)[kTmPF][2], u32x4 (&keys
     for (int p = 0; p < kTmPF; p++) {
         const uint32_t t = t_first + min((uint32_t)p, nt - 1);
         const WT *wt = w + (size_t)t * n_entries * n_outputs;
-        const float sc = scales ? scales[t] : 1.0f;
+        scs[p] = scales ? scales[t] : 1.0f;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const uint32_t c = tid + (uint32_t)h * kTmThreads;
             const uint32_t row = (c >> 3) & (n_entries - 1);
             uint32_t col = col0 + (c & 7) * 4;
             if (col >= n_outputs) col = 0;
-            rows[p][h] = load_quad<WT>(wt + (size_t)row * n_outputs + col, sc);
+            rows[p][h] = load_raw<WT>(wt + (size_t)row * n_outputs + col);
         }
         if ((int)tid < KeyPieces<KEY, SPT>::kCount) {
             // keys of samples b_base + tid*kPer .. +kPer-1 (zero past the batch)
             const uint32_t b = b_base + tid * kPer;
             const KEY *src = keys_t + (size_t)t * batch + b;
             if (b + kPer <= batch && batch % kPer == 0) {
-                keys[p] = *reinterpret_cast<const u32x4 *>(src);
+                keys[p] = *reinterpret_cast<const u32x2 *>(src);
             } else {
-                uint32_t wd[4] = {0u, 0u, 0u, 0u};
+                uint32_t wd[2] = {0u, 0u};
 #pragma unroll
                 for (int q = 0; q < kPer; q++) {
                     const uint32_t v = (b + q < batch) ? (uint32_t)src[q] : 0u;
                     wd[q / (4 / (int)sizeof(KEY))] |= v << (8 * sizeof(KEY) * (q % (4 / (int)sizeof(KEY))));
                 }
-                keys[p] = u32x4{wd[0], wd[1], wd[2], wd[3]};
+                keys[p] = u32x2{wd[0], wd[1]};
             }
         }
     }
 }
 
-template <typename KEY, int SPT>
-__device__ __forceinline__ void stage_store(const f32x4 (&rows)[kTmPF][2],
-                                            const u32x4 (&keys)[kTmPF], uint8_t *stage,
+template <typename KEY, int SPT, typename RT>
+__device__ __forceinline__ void stage_store(const RT (&rows)[kTmPF][2], const float (&scs)[kTmPF],
+                                            const u32x2 (&keys)[kTmPF], uint8_t *stage,
                                             uint32_t tid) {
 #pragma unroll
     for (int p = 0; p < kTmPF; p++) {
@@ -259,10 +274,10 @@ __device__ __forceinline__ void stage_store(const f32x4 (&rows)[kTmPF][2],
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const uint32_t c = tid + (uint32_t)h * kTmThreads;
-            *reinterpret_cast<f32x4 *>(tb + c * 16) = rows[p][h];
+            *reinterpret_cast<f32x4 *>(tb + c * 16) = raw_quad(rows[p][h], scs[p]);
         }
         if ((int)tid < KeyPieces<KEY, SPT>::kCount)
-            *reinterpret_cast<u32x4 *>(tb + kTmMaxEntries * 128 + tid * 16) = keys[p];
+            *reinterpret_cast<u32x2 *>(tb + kTmMaxEntries * 128 + tid * 8) = keys[p];
     }
 }
 
@@ -326,18 +341,19 @@ __global__ __launch_bounds__(kTmThreads) void k_fill_tm(
 
     const uint32_t nt_all = t1 - t0;
     const uint32_t n_stages = (nt_all + kTmPF - 1) / kTmPF;
-    f32x4 rows[kTmPF][2];
-    u32x4 keys4[kTmPF];
-    stage_load<uint8_t, SPT, WT>(rows, keys4, w, idx_t, tid, t0, min((uint32_t)kTmPF, nt_all), n_entries,
+    typename StageRaw<WT>::type rows[kTmPF][2];
+    float scs[kTmPF];
+    u32x2 keys4[kTmPF];
+    stage_load<uint8_t, SPT, WT>(rows, scs, keys4, w, idx_t, tid, t0, min((uint32_t)kTmPF, nt_all), n_entries,
                                  n_outputs, col0, batch, b_base, scales);
     for (uint32_t st = 0; st < n_stages; st++) {
         uint8_t *stage = smem + (st & 1) * L::kStageBytes;
-        stage_store<uint8_t, SPT>(rows, keys4, stage, tid);
+        stage_store<uint8_t, SPT>(rows, scs, keys4, stage, tid);
         const uint32_t ts = t0 + st * kTmPF;
         const uint32_t nt = min((uint32_t)kTmPF, t1 - ts);
         if (st + 1 < n_stages) {
             const uint32_t tn = ts + kTmPF;
-            stage_load<uint8_t, SPT, WT>(rows, keys4, w, idx_t, tid, tn, min((uint32_t)kTmPF, t1 - tn),
+            stage_load<uint8_t, SPT, WT>(rows, scs, keys4, w, idx_t, tid, tn, min((uint32_t)kTmPF, t1 - tn),
                                          n_entries, n_outputs, col0, batch, b_base, scales);
         }
         __syncthreads();
@@ -630,18 +646,19 @@ __global__ __launch_bounds__(kTmThreads) void k_propagate_tm(
     const uint32_t nt_all = t1 - t0;
     const uint32_t n_stages = (nt_all + kTmPF - 1) / kTmPF;
     f32x4 rows[kTmPF][2];
-    u32x4 keys4[kTmPF];
+    float scs[kTmPF];
+    u32x2 keys4[kTmPF];
     // keys rows have `pitch` (a whole number of chunks, zero past the batch)
-    stage_load<uint32_t, SPT>(rows, keys4, w, key_t, tid, t0, min((uint32_t)kTmPF, nt_all), n_entries,
+    stage_load<uint32_t, SPT>(rows, scs, keys4, w, key_t, tid, t0, min((uint32_t)kTmPF, nt_all), n_entries,
                               n_outputs, col0, pitch, b_base);
     for (uint32_t st = 0; st < n_stages; st++) {
         uint8_t *stage = smem + (st & 1) * L::kStageBytes;
-        stage_store<uint32_t, SPT>(rows, keys4, stage, tid);
+        stage_store<uint32_t, SPT>(rows, scs, keys4, stage, tid);
         const uint32_t ts = t0 + st * kTmPF;
         const uint32_t nt = min((uint32_t)kTmPF, t1 - ts);
         if (st + 1 < n_stages) {
             const uint32_t tn = ts + kTmPF;
-            stage_load<uint32_t, SPT>(rows, keys4, w, key_t, tid, tn, min((uint32_t)kTmPF, t1 - tn),
+            stage_load<uint32_t, SPT>(rows, scs, keys4, w, key_t, tid, tn, min((uint32_t)kTmPF, t1 - tn),
                                       n_entries, n_outputs, col0, pitch, b_base);
         }
         __syncthreads();
