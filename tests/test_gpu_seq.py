@@ -214,6 +214,14 @@ def test_seq_one_bucket_chunks_int32(oracle, cuda_device):
     run_seq(oracle, B, S, I, T, Nc, Npe, O, seed=14, int_rescaler=0.5, inputs=(x, anchors, W, pe, go))
 
 
+@pytest.mark.parametrize("shape", [(2, 20, 16, 3, 3, 2, 16), (2, 24, 16, 2, 6, 6, 32)])
+def test_seq_narrow_forward_slices(oracle, cuda_device, shape):
+    # 16-column forward slices (O = 16) and 8-column slices (2^12-row
+    # sub-tables): one column a lane in the LDS-staged forward
+    B, S, I, T, Nc, Npe, O = shape
+    run_seq(oracle, B, S, I, T, Nc, Npe, O, seed=17 + Nc)
+
+
 def test_seq_odd_outputs_and_groups(oracle, cuda_device):
     # O not a multiple of 4: exact decomposition path; odd group sizes
     run_seq(oracle, 2, 10, 12, 3, 2, 2, 37, fgs=8, bgs=5, seed=5)
