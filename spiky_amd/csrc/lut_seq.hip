@@ -736,6 +736,10 @@ __global__ __launch_bounds__(kBlock) void k_propagate_seq(
 //   qsum[b][t][j]  = sum of main over the Q-flip pairs.
 // The triangles are [j*(j-1)/2 + i] per (b, t); k_seq_tri_reduce sums them.
 constexpr int kPairMaxO = 2048;  // a multiple of 128 (groups of 4 chunks)
+constexpr int kPairChunks = 2;   // 32-column chunks whose rows are loaded together (divides 4)
+
+// fp64 words of g the pair kernel stages: whole groups of 4 chunks of 32 columns
+inline uint32_t pair_g_doubles(uint32_t n_outputs) { return ((n_outputs + 31) / 32 + 3) / 4 * 128; }
 
 __global__ __launch_bounds__(kBlock) void k_propagate_seq_pairs(
     const float *__restrict__ w, const float *__restrict__ g, const uint2 *__restrict__ pack,
@@ -743,7 +747,8 @@ __global__ __launch_bounds__(kBlock) void k_propagate_seq_pairs(
     double *__restrict__ tk, double *__restrict__ tp, uint32_t batch, uint32_t seq,
     uint32_t n_outputs, uint32_t n_detectors, uint32_t n_anchors, uint32_t pe_dim,
     uint32_t wg_per_xcd) {
-    __shared__ __attribute__((aligned(16))) double gd[kPairMaxO];
+    // g in fp64, sized at launch: whole groups of 4 chunks (pair_g_doubles)
+    extern __shared__ __attribute__((aligned(16))) double gd[];
     __shared__ double wpart[kWPB];
     __shared__ uint2 srec[kRecStage], sprec[kRecStage];
     const uint32_t tid = threadIdx.x;
@@ -809,17 +814,17 @@ __global__ __launch_bounds__(kBlock) void k_propagate_seq_pairs(
         const float *mp = wt + (size_t)mrow * n_outputs;
         const float *ap = wt + (size_t)arow * n_outputs;
         const float *ep = wt + (size_t)erow * n_outputs;
-        for (uint32_t k0 = 0; k0 < n_chunks; k0 += 4) {
-            f32x4 mv[4], av[4], ev[4];
+        for (uint32_t k0 = 0; k0 < n_chunks; k0 += kPairChunks) {
+            f32x4 mv[kPairChunks], av[kPairChunks], ev[kPairChunks];
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
+            for (int k = 0; k < kPairChunks; k++) {
                 const uint32_t c = min((k0 + k) * 32 + 4 * s, n_outputs - 4);
                 mv[k] = *reinterpret_cast<const f32x4 *>(mp + c);
                 av[k] = kflip ? *reinterpret_cast<const f32x4 *>(ap + c) : f32x4{0.f, 0.f, 0.f, 0.f};
                 ev[k] = peflip ? *reinterpret_cast<const f32x4 *>(ep + c) : f32x4{0.f, 0.f, 0.f, 0.f};
             }
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
+            for (int k = 0; k < kPairChunks; k++) {
                 const uint32_t c = (k0 + k) * 32 + 4 * s;
                 const double2 g01 = *reinterpret_cast<const double2 *>(gd + c);
                 const double2 g23 = *reinterpret_cast<const double2 *>(gd + c + 2);
@@ -1638,7 +1643,8 @@ hipError_t launch_backward_seq(const SeqShape &s, float *w, const float *g, cons
     SPIKY_PSEQ(NJ, false, samples, dq);                \
     SPIKY_PSEQ(NJ, true, samples2, dq_alt)
         if (pairs) {
-            hipLaunchKernelGGL(k_propagate_seq_pairs, dim3((uint32_t)grid), dim3(kBlock), 0, st, w, g,
+            hipLaunchKernelGGL(k_propagate_seq_pairs, dim3((uint32_t)grid), dim3(kBlock),
+                               pair_g_doubles(s.n_outputs) * sizeof(double), st, w, g,
                                pack, ppack, samples, dq, tk, tp, s.batch, s.seq, s.n_outputs,
                                s.n_detectors, s.n_anchors, s.pe_dim, (uint32_t)wg_per_xcd);
             switch (nj) {
