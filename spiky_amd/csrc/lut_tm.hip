@@ -563,7 +563,7 @@ __global__ __launch_bounds__(256) void k_fill_commit(const uint32_t *__restrict_
     int32_t ir[4] = {__float_as_int(run.x), __float_as_int(run.y), __float_as_int(run.z),
                      __float_as_int(run.w)};
     uint32_t k = 0;
-    constexpr int kU = 8;
+    constexpr int kU = 16;  // loads in flight a thread (config 3: 0.219 ms; 0.225 ms with 8)
     for (; k + kU <= n_blocks; k += kU) {
         uint4 v[kU];
 #pragma unroll
