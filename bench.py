@@ -38,8 +38,9 @@ def log(msg):
 
 
 def g_model_bytes(B, I, T, Nc, O, w=4):
-    """Algorithmic bytes per kernel family, gather model: every logical row
-    access counts once per use."""
+    """Algorithmic bytes per kernel family, gather model (the embedding-bag
+    convention): every logical row access counts once per use, with no credit
+    for cache or LDS reuse."""
     return {
         "check_detectors": B * I * 4 + T * Nc * 8 + B * T * 12,
         "fill_outputs_fc": B * T * O * w + B * O * 4,
