@@ -42,6 +42,8 @@ def check_tensor(t, name, real_or_int, device, sizeof_int=4):
             raise RuntimeError(
                 f"tensor {name} must have real data type (float or double depending on build)")
     else:
+        if sizeof_int == 1 and t.dtype != torch.int8:
+            raise RuntimeError(f"tensor {name} must have dtype int8")
         if sizeof_int == 4 and t.dtype != torch.int32:
             raise RuntimeError(f"tensor {name} must have dtype int32")
         if sizeof_int == 8 and t.dtype != torch.int64:
@@ -361,18 +363,35 @@ class _LUTDataManagerBase:
         self._device = int(device)
 
     # ---------------------------------------------------------------- runtime
-    def _stream(self, r_stream_handles):
+    def _launch(self, r_stream_handles, call):
+        """Runs call(stream) on the manager's device and checks its status.
+
+        Without handles the kernels go on torch's current stream.  With
+        handles they go on r_stream_handles[0], which first waits for the
+        current stream; afterwards the current stream waits for it, so a
+        caller that reads the outputs (or frees the inputs) on the current
+        stream is ordered after the kernels, and calls on different handles
+        never overlap on the manager's scratch memory.  The reference makes
+        the same guarantee by synchronising the device
+        (lut_runtime.cu:99,244,423)."""
+        self._require_device()
+        if r_stream_handles is not None:
+            check_tensor(r_stream_handles, "r_stream_handles", False, -1, 8)
+            if r_stream_handles.numel() < 3:
+                raise ValueError("r_stream_handles must have at least 3 elements")
         dev = torch.device("cuda", self._device)
-        cur = torch.cuda.current_stream(dev)
-        if r_stream_handles is None:
-            return cur.cuda_stream
-        check_tensor(r_stream_handles, "r_stream_handles", False, -1, 8)
-        if r_stream_handles.numel() < 3:
-            raise ValueError("r_stream_handles must have at least 3 elements")
-        h = int(r_stream_handles[0].item())
-        ext = torch.cuda.ExternalStream(h, device=dev)
-        ext.wait_stream(cur)
-        return h
+        with torch.cuda.device(dev):
+            cur = torch.cuda.current_stream(dev)
+            if r_stream_handles is None:
+                _native.check(call(ctypes.c_void_p(cur.cuda_stream)))
+                return
+            h = int(r_stream_handles[0].item())
+            ext = torch.cuda.ExternalStream(h, device=dev)
+            ext.wait_stream(cur)
+            try:
+                _native.check(call(ctypes.c_void_p(h)))
+            finally:
+                cur.wait_stream(ext)
 
     def _require_device(self):
         if self._device < 0:
@@ -395,7 +414,6 @@ class _LUTDataManagerBase:
             check_tensor(w_min_anchor_delta_indices, "w_min_anchor_delta_indices", False, dev, 4)
         if batch_size == 0:
             raise ValueError("batch_size == 0")
-        self._require_device()
         B = int(batch_size)
         _require_numel(r_weights, self.get_weights_dimension(), "r_weights")
         _require_numel(r_input, B * self._n_inputs, "r_input")
@@ -406,12 +424,10 @@ class _LUTDataManagerBase:
             _require_numel(w_min_anchor_deltas, B * self._n_detectors, "w_min_anchor_deltas")
         if w_min_anchor_delta_indices is not None:
             _require_numel(w_min_anchor_delta_indices, B * self._n_detectors, "w_min_anchor_delta_indices")
-        with torch.cuda.device(dev):
-            st = self._stream(r_stream_handles)
-            _native.check(_native.lib().spiky_lut_forward_step(
-                self._h, _ptr(r_weights), B, _ptr(r_input), _ptr(r_detector_anchors),
-                _ptr(w_output), _ptr(w_lookup_indices), float(cmp_eps), _ptr(w_min_anchor_deltas),
-                _ptr(w_min_anchor_delta_indices), ctypes.c_void_p(st)))
+        self._launch(r_stream_handles, lambda st: _native.lib().spiky_lut_forward_step(
+            self._h, _ptr(r_weights), B, _ptr(r_input), _ptr(r_detector_anchors),
+            _ptr(w_output), _ptr(w_lookup_indices), float(cmp_eps), _ptr(w_min_anchor_deltas),
+            _ptr(w_min_anchor_delta_indices), st))
 
     def forward_step_i8(self, r_weights_q8, r_scales, batch_size, r_input, r_detector_anchors,
                         w_output, w_lookup_indices, cmp_eps=0.0, r_stream_handles=None,
@@ -419,30 +435,33 @@ class _LUTDataManagerBase:
         """forward_step over int8 tables with one fp32 scale per detector
         (weight = scale[t] * q); fully connected managers only."""
         dev = self._device
-        if not isinstance(r_weights_q8, torch.Tensor) or r_weights_q8.dtype != torch.int8:
-            raise RuntimeError("tensor r_weights_q8 must have dtype int8")
-        if r_weights_q8.dim() != 1 or not r_weights_q8.is_contiguous():
-            raise RuntimeError("tensor r_weights_q8 must be flat and has stride = 1")
+        check_tensor(r_weights_q8, "r_weights_q8", False, dev, 1)
         check_tensor(r_scales, "r_scales", True, dev)
         check_tensor(r_input, "r_input", True, dev)
         check_tensor(r_detector_anchors, "r_detector_anchors", False, dev, 4)
         check_tensor(w_output, "w_output", True, dev)
         check_tensor(w_lookup_indices, "w_lookup_indices", False, dev, 4)
+        if w_min_anchor_deltas is not None:
+            check_tensor(w_min_anchor_deltas, "w_min_anchor_deltas", True, dev)
+        if w_min_anchor_delta_indices is not None:
+            check_tensor(w_min_anchor_delta_indices, "w_min_anchor_delta_indices", False, dev, 4)
         if batch_size == 0:
             raise ValueError("batch_size == 0")
-        self._require_device()
         B = int(batch_size)
         _require_numel(r_weights_q8, self._n_lookup * self._n_outputs, "r_weights_q8")
         _require_numel(r_scales, self._n_detectors, "r_scales")
         _require_numel(r_input, B * self._n_inputs, "r_input")
+        _require_numel(r_detector_anchors, self._n_detectors * self._n_anchors * 2, "r_detector_anchors")
         _require_numel(w_output, B * self._n_outputs, "w_output")
         _require_numel(w_lookup_indices, B * self._n_detectors, "w_lookup_indices")
-        with torch.cuda.device(dev):
-            st = self._stream(r_stream_handles)
-            _native.check(_native.lib().spiky_lut_forward_step_i8(
-                self._h, _ptr(r_weights_q8), _ptr(r_scales), B, _ptr(r_input),
-                _ptr(r_detector_anchors), _ptr(w_output), _ptr(w_lookup_indices), float(cmp_eps),
-                _ptr(w_min_anchor_deltas), _ptr(w_min_anchor_delta_indices), ctypes.c_void_p(st)))
+        if w_min_anchor_deltas is not None:
+            _require_numel(w_min_anchor_deltas, B * self._n_detectors, "w_min_anchor_deltas")
+        if w_min_anchor_delta_indices is not None:
+            _require_numel(w_min_anchor_delta_indices, B * self._n_detectors, "w_min_anchor_delta_indices")
+        self._launch(r_stream_handles, lambda st: _native.lib().spiky_lut_forward_step_i8(
+            self._h, _ptr(r_weights_q8), _ptr(r_scales), B, _ptr(r_input),
+            _ptr(r_detector_anchors), _ptr(w_output), _ptr(w_lookup_indices), float(cmp_eps),
+            _ptr(w_min_anchor_deltas), _ptr(w_min_anchor_delta_indices), st))
 
     def backward_backprop(self, r_weights, batch_size, r_output_gradients, r_detector_anchors,
                           r_lookup_indices, r_min_anchor_deltas, r_min_anchor_delta_indices,
@@ -463,23 +482,21 @@ class _LUTDataManagerBase:
         check_tensor(r_min_anchor_delta_indices, "r_min_anchor_delta_indices", False, dev, 4)
         if w_weights_gradients is not None:
             check_tensor(w_weights_gradients, "w_weights_gradients", True, dev)
-        self._require_device()
         B = int(batch_size)
         _require_numel(r_weights, self.get_weights_dimension(), "r_weights")
         _require_numel(r_output_gradients, B * self._n_outputs, "r_output_gradients")
+        _require_numel(r_detector_anchors, self._n_detectors * self._n_anchors * 2, "r_detector_anchors")
         _require_numel(w_input_gradients, B * self._n_inputs, "w_input_gradients")
         for t, nm in ((r_lookup_indices, "r_lookup_indices"), (r_min_anchor_deltas, "r_min_anchor_deltas"),
                       (r_min_anchor_delta_indices, "r_min_anchor_delta_indices")):
             _require_numel(t, B * self._n_detectors, nm)
         if w_weights_gradients is not None:
             _require_numel(w_weights_gradients, self.get_weights_dimension(), "w_weights_gradients")
-        with torch.cuda.device(dev):
-            st = self._stream(r_stream_handles)
-            _native.check(_native.lib().spiky_lut_backward_backprop(
-                self._h, _ptr(r_weights), B, _ptr(r_output_gradients), _ptr(r_detector_anchors),
-                _ptr(r_lookup_indices), _ptr(r_min_anchor_deltas), _ptr(r_min_anchor_delta_indices),
-                _ptr(w_input_gradients), float(external_lr), _ptr(w_weights_gradients),
-                int(bool(overwrite_weights_gradients)), ctypes.c_void_p(st)))
+        self._launch(r_stream_handles, lambda st: _native.lib().spiky_lut_backward_backprop(
+            self._h, _ptr(r_weights), B, _ptr(r_output_gradients), _ptr(r_detector_anchors),
+            _ptr(r_lookup_indices), _ptr(r_min_anchor_deltas), _ptr(r_min_anchor_delta_indices),
+            _ptr(w_input_gradients), float(external_lr), _ptr(w_weights_gradients),
+            int(bool(overwrite_weights_gradients)), st))
 
     # ---------------------------------------------------------------- sequence-concat mode
     def forward_step_concat(self, r_weights, batch_size, r_input, r_detector_anchors, w_output,
@@ -508,27 +525,32 @@ class _LUTDataManagerBase:
                             (w_positional_min_delta_indices, "w_positional_min_delta_indices", False)):
             if t is not None:
                 check_tensor(t, nm, real, dev)
-        self._require_device()
         B, T, P = int(batch_size), self._n_detectors, self._positional_dim
         _require_numel(r_weights, self.get_weights_dimension(), "r_weights")
         _require_numel(r_input, B * S * self._n_inputs, "r_input")
         _require_numel(r_detector_anchors, T * self._n_anchors * 2, "r_detector_anchors")
         _require_numel(w_output, B * S * self._n_outputs, "w_output")
         _require_numel(w_lookup_indices, B * S * T, "w_lookup_indices")
+        for t, nm in ((w_min_anchor_deltas, "w_min_anchor_deltas"),
+                      (w_min_anchor_delta_indices, "w_min_anchor_delta_indices")):
+            if t is not None:
+                _require_numel(t, B * S * T, nm)
         if P > 0:
+            for t, nm in ((w_positional_min_deltas, "w_positional_min_deltas"),
+                          (w_positional_min_delta_indices, "w_positional_min_delta_indices")):
+                if t is not None:
+                    _require_numel(t, (S - 1) * T, nm)
             if r_positional_embeddings is None or w_positional_lookup_indices is None:
                 raise ValueError("positional embeddings and positional lookup indices must be "
                                  "provided when positional_dim > 0")
             _require_numel(r_positional_embeddings, (S - 1) * T * P, "r_positional_embeddings")
             _require_numel(w_positional_lookup_indices, (S - 1) * T, "w_positional_lookup_indices")
-        with torch.cuda.device(dev):
-            st = self._stream(r_stream_handles)
-            _native.check(_native.lib().spiky_lut_forward_step_concat(
-                self._h, _ptr(r_weights), B, _ptr(r_input), _ptr(r_detector_anchors), _ptr(w_output),
-                _ptr(w_lookup_indices), float(cmp_eps), _ptr(r_positional_embeddings if P > 0 else None),
-                _ptr(w_positional_lookup_indices if P > 0 else None), _ptr(w_min_anchor_deltas),
-                _ptr(w_min_anchor_delta_indices), _ptr(w_positional_min_deltas if P > 0 else None),
-                _ptr(w_positional_min_delta_indices if P > 0 else None), ctypes.c_void_p(st)))
+        self._launch(r_stream_handles, lambda st: _native.lib().spiky_lut_forward_step_concat(
+            self._h, _ptr(r_weights), B, _ptr(r_input), _ptr(r_detector_anchors), _ptr(w_output),
+            _ptr(w_lookup_indices), float(cmp_eps), _ptr(r_positional_embeddings if P > 0 else None),
+            _ptr(w_positional_lookup_indices if P > 0 else None), _ptr(w_min_anchor_deltas),
+            _ptr(w_min_anchor_delta_indices), _ptr(w_positional_min_deltas if P > 0 else None),
+            _ptr(w_positional_min_delta_indices if P > 0 else None), st))
 
     def backward_backprop_concat(self, r_weights, batch_size, r_output_gradients, r_detector_anchors,
                                  r_lookup_indices, r_min_anchor_deltas, r_min_anchor_delta_indices,
@@ -557,10 +579,10 @@ class _LUTDataManagerBase:
                             (w_weights_gradients, "w_weights_gradients", True)):
             if t is not None:
                 check_tensor(t, nm, real, dev)
-        self._require_device()
         B, T, P = int(batch_size), self._n_detectors, self._positional_dim
         _require_numel(r_weights, self.get_weights_dimension(), "r_weights")
         _require_numel(r_output_gradients, B * S * self._n_outputs, "r_output_gradients")
+        _require_numel(r_detector_anchors, T * self._n_anchors * 2, "r_detector_anchors")
         _require_numel(w_input_gradients, B * S * self._n_inputs, "w_input_gradients")
         for t, nm in ((r_lookup_indices, "r_lookup_indices"), (r_min_anchor_deltas, "r_min_anchor_deltas"),
                       (r_min_anchor_delta_indices, "r_min_anchor_delta_indices")):
@@ -578,17 +600,15 @@ class _LUTDataManagerBase:
                            "w_positional_embeddings_gradients")
         if w_weights_gradients is not None:
             _require_numel(w_weights_gradients, self.get_weights_dimension(), "w_weights_gradients")
-        with torch.cuda.device(dev):
-            st = self._stream(r_stream_handles)
-            _native.check(_native.lib().spiky_lut_backward_backprop_concat(
-                self._h, _ptr(r_weights), B, _ptr(r_output_gradients), _ptr(r_detector_anchors),
-                _ptr(r_lookup_indices), _ptr(r_min_anchor_deltas), _ptr(r_min_anchor_delta_indices),
-                _ptr(w_input_gradients), float(external_lr),
-                _ptr(r_positional_lookup_indices if P > 0 else None),
-                _ptr(r_positional_min_deltas if P > 0 else None),
-                _ptr(r_positional_min_delta_indices if P > 0 else None),
-                _ptr(w_positional_embeddings_gradients if P > 0 else None), _ptr(w_weights_gradients),
-                int(bool(overwrite_weights_gradients)), ctypes.c_void_p(st)))
+        self._launch(r_stream_handles, lambda st: _native.lib().spiky_lut_backward_backprop_concat(
+            self._h, _ptr(r_weights), B, _ptr(r_output_gradients), _ptr(r_detector_anchors),
+            _ptr(r_lookup_indices), _ptr(r_min_anchor_deltas), _ptr(r_min_anchor_delta_indices),
+            _ptr(w_input_gradients), float(external_lr),
+            _ptr(r_positional_lookup_indices if P > 0 else None),
+            _ptr(r_positional_min_deltas if P > 0 else None),
+            _ptr(r_positional_min_delta_indices if P > 0 else None),
+            _ptr(w_positional_embeddings_gradients if P > 0 else None), _ptr(w_weights_gradients),
+            int(bool(overwrite_weights_gradients)), st))
 
     def _product_sizes(self, batch_size, sequence_length, n_inputs_1, n_inputs_2, what):
         if batch_size == 0:
@@ -617,7 +637,6 @@ class _LUTDataManagerBase:
         check_tensor(w_output, "w_output", True, dev)
         if r_positional_embeddings is not None:
             check_tensor(r_positional_embeddings, "r_positional_embeddings", True, dev)
-        self._require_device()
         T, P = self._n_detectors, self._positional_dim
         _require_numel(r_weights, self.get_weights_dimension(), "r_weights")
         _require_numel(r_input_1, B * S * n1, "r_input_1")
@@ -628,13 +647,11 @@ class _LUTDataManagerBase:
             if r_positional_embeddings is None:
                 raise ValueError("r_positional_embeddings must be provided when positional_dim > 0")
             _require_numel(r_positional_embeddings, (S - 1) * T * P, "r_positional_embeddings")
-        with torch.cuda.device(dev):
-            st = self._stream(r_stream_handles)
-            _native.check(_native.lib().spiky_lut_forward_step_product(
-                self._h, _ptr(r_weights), B, S, _ptr(r_input_1), _ptr(r_input_2),
-                _ptr(r_detector_anchors), _ptr(w_output), n1, n2, int(bool(sliced_mode)),
-                float(cmp_eps), _ptr(r_positional_embeddings if P > 0 else None),
-                ctypes.c_void_p(st)))
+        self._launch(r_stream_handles, lambda st: _native.lib().spiky_lut_forward_step_product(
+            self._h, _ptr(r_weights), B, S, _ptr(r_input_1), _ptr(r_input_2),
+            _ptr(r_detector_anchors), _ptr(w_output), n1, n2, int(bool(sliced_mode)),
+            float(cmp_eps), _ptr(r_positional_embeddings if P > 0 else None),
+            st))
 
     def backward_backprop_product(self, r_weights, batch_size, sequence_length, r_input_1, r_input_2,
                                   r_detector_anchors, r_output_gradients, w_input_gradients_1,
@@ -659,7 +676,6 @@ class _LUTDataManagerBase:
                       (w_positional_embeddings_gradients, "w_positional_embeddings_gradients")):
             if t is not None:
                 check_tensor(t, nm, True, dev)
-        self._require_device()
         T, P = self._n_detectors, self._positional_dim
         _require_numel(r_weights, self.get_weights_dimension(), "r_weights")
         _require_numel(r_input_1, B * S * n1, "r_input_1")
@@ -677,15 +693,13 @@ class _LUTDataManagerBase:
             _require_numel(r_positional_embeddings, (S - 1) * T * P, "r_positional_embeddings")
             _require_numel(w_positional_embeddings_gradients, (S - 1) * T * P,
                            "w_positional_embeddings_gradients")
-        with torch.cuda.device(dev):
-            st = self._stream(r_stream_handles)
-            _native.check(_native.lib().spiky_lut_backward_backprop_product(
-                self._h, _ptr(r_weights), B, S, _ptr(r_input_1), _ptr(r_input_2),
-                _ptr(r_detector_anchors), _ptr(r_output_gradients), _ptr(w_input_gradients_1),
-                _ptr(w_input_gradients_2), float(external_lr), n1, n2, int(bool(sliced_mode)),
-                float(cmp_eps), _ptr(w_weights_gradients),
-                _ptr(r_positional_embeddings if P > 0 else None),
-                _ptr(w_positional_embeddings_gradients if P > 0 else None), ctypes.c_void_p(st)))
+        self._launch(r_stream_handles, lambda st: _native.lib().spiky_lut_backward_backprop_product(
+            self._h, _ptr(r_weights), B, S, _ptr(r_input_1), _ptr(r_input_2),
+            _ptr(r_detector_anchors), _ptr(r_output_gradients), _ptr(w_input_gradients_1),
+            _ptr(w_input_gradients_2), float(external_lr), n1, n2, int(bool(sliced_mode)),
+            float(cmp_eps), _ptr(w_weights_gradients),
+            _ptr(r_positional_embeddings if P > 0 else None),
+            _ptr(w_positional_embeddings_gradients if P > 0 else None), st))
 
     # ---------------------------------------------------------------- export
     def count_synapses(self, neuron_indices_to_process):

@@ -94,6 +94,91 @@ def test_tensor_checks():
         check_tensor(torch.zeros(4)[::2], "t", True, -1)
 
 
+def _fc_manager(int_mode=False, seq=1, pd=0):
+    from spiky_amd import LUTDataManagerF, LUTDataManagerI
+    B_, I, O, T, Nc = 4, 16, 8, 3, 2
+    if int_mode:
+        dm = LUTDataManagerI(I, O, T, Nc, seq, pd, 0, 32, 32, 0.001)
+    else:
+        dm = LUTDataManagerF(I, O, T, Nc, seq, pd, 0, 32, 32)
+    dm.register_synapse_meta(1.0, -1.0, 1.0, 0.0, 0.0)
+    dm.initialize_neurons(True)
+    return dm, (B_, I, O, T, Nc)
+
+
+def test_int8_forward_validation():
+    """forward_step_i8 checks the int8 tables, the optional min-delta outputs and
+    the anchors like every other tensor, before any launch."""
+    dm, (B, I, O, T, Nc) = _fc_manager(int_mode=True)
+    E = 1 << Nc
+    f = lambda n: torch.zeros(n)
+    i = lambda n: torch.zeros(n, dtype=torch.int32)
+    q8 = torch.zeros(T * E * O, dtype=torch.int8)
+    args = dict(r_weights_q8=q8, r_scales=f(T), batch_size=B, r_input=f(B * I),
+                r_detector_anchors=i(T * Nc * 2), w_output=f(B * O), w_lookup_indices=i(B * T))
+    with pytest.raises(RuntimeError, match="r_weights_q8 must have dtype int8"):
+        dm.forward_step_i8(**{**args, "r_weights_q8": torch.zeros(T * E * O, dtype=torch.int32)})
+    with pytest.raises(RuntimeError, match="r_weights_q8 must be flat"):
+        dm.forward_step_i8(**{**args, "r_weights_q8": q8.view(T, -1)})
+    with pytest.raises(ValueError, match="r_weights_q8 has"):
+        dm.forward_step_i8(**{**args, "r_weights_q8": q8[:-1]})
+    with pytest.raises(ValueError, match="r_detector_anchors has"):
+        dm.forward_step_i8(**{**args, "r_detector_anchors": i(T * Nc * 2 - 1)})
+    with pytest.raises(RuntimeError, match="w_min_anchor_deltas must have real"):
+        dm.forward_step_i8(**args, w_min_anchor_deltas=i(B * T), w_min_anchor_delta_indices=i(B * T))
+    with pytest.raises(ValueError, match="w_min_anchor_delta_indices has"):
+        dm.forward_step_i8(**args, w_min_anchor_deltas=f(B * T), w_min_anchor_delta_indices=i(B * T - 1))
+    # every check passed: only the device requirement is left
+    with pytest.raises(RuntimeError, match="HIP devices only"):
+        dm.forward_step_i8(**args, w_min_anchor_deltas=f(B * T), w_min_anchor_delta_indices=i(B * T))
+    # a manager on a GPU refuses host tensors before it reaches a kernel
+    dm.to_device(0)
+    with pytest.raises(RuntimeError, match="r_weights_q8 must be on CUDA"):
+        dm.forward_step_i8(**args)
+
+
+def test_backward_and_concat_size_validation():
+    dm, (B, I, O, T, Nc) = _fc_manager()
+    f = lambda n: torch.zeros(n)
+    i = lambda n: torch.zeros(n, dtype=torch.int32)
+    W = f(dm.get_weights_dimension())
+    with pytest.raises(ValueError, match="r_detector_anchors has"):
+        dm.backward_backprop(W, B, f(B * O), i(T * Nc * 2 - 2), i(B * T), f(B * T), i(B * T),
+                             f(B * I), -1.0, f(W.numel()))
+    S, P = 5, 2
+    dms, _ = _fc_manager(seq=S, pd=P)
+    Ws = f(dms.get_weights_dimension())
+    base = dict(r_weights=Ws, batch_size=B, r_input=f(B * S * I), r_detector_anchors=i(T * Nc * 2),
+                w_output=f(B * S * O), w_lookup_indices=i(B * S * T), cmp_eps=0.0,
+                r_positional_embeddings=f((S - 1) * T * P), w_positional_lookup_indices=i((S - 1) * T))
+    with pytest.raises(ValueError, match="w_min_anchor_deltas has"):
+        dms.forward_step_concat(**base, w_min_anchor_deltas=f(B * S * T - 1),
+                                w_min_anchor_delta_indices=i(B * S * T))
+    with pytest.raises(ValueError, match="w_positional_min_delta_indices has"):
+        dms.forward_step_concat(**base, w_min_anchor_deltas=f(B * S * T),
+                                w_min_anchor_delta_indices=i(B * S * T),
+                                w_positional_min_deltas=f((S - 1) * T),
+                                w_positional_min_delta_indices=i((S - 1) * T - 1))
+    with pytest.raises(ValueError, match="r_detector_anchors has"):
+        dms.backward_backprop_concat(Ws, B, f(B * S * O), i(1), i(B * S * T), f(B * S * T),
+                                     i(B * S * T), f(B * S * I), -1.0, i((S - 1) * T), f((S - 1) * T),
+                                     i((S - 1) * T), f((S - 1) * T * P), f(Ws.numel()))
+
+
+def test_stream_handles_are_validated_before_launch():
+    dm, (B, I, O, T, Nc) = _fc_manager()
+    f = lambda n: torch.zeros(n)
+    i = lambda n: torch.zeros(n, dtype=torch.int32)
+    W = f(dm.get_weights_dimension())
+    dm.to_device(0)
+    call = lambda h: dm._launch(h, lambda st: 0)
+    with pytest.raises(RuntimeError, match="r_stream_handles must have dtype int64"):
+        call(torch.zeros(3, dtype=torch.int32))
+    with pytest.raises(ValueError, match="at least 3 elements"):
+        call(torch.zeros(2, dtype=torch.int64))
+    del W
+
+
 def test_anchor_decode_matches_oracle(oracle):
     """The library's host decode equals the oracle's on random lists."""
     from spiky_amd import _native
