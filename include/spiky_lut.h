@@ -83,6 +83,23 @@ int spiky_lut_forward_step(spiky_lut_manager *m, const float *weights, uint32_t 
                            int32_t *lookup_indices, float cmp_eps, float *min_deltas,
                            int32_t *min_delta_indices, void *stream);
 
+/* Allocation-free forward.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments,
+ * semantics and results as spiky_lut_forward_step, on fully connected
+ * managers only; it calls no hipMalloc / hipFree.  Where the table-major
+ * forward needs scratch (transposed indices and block partials), that
+ * scratch is a library-owned static device array of
+ * SPIKY_NOALLOC_SCRATCH_BYTES, one copy per device, held until the process
+ * ends; shapes that need more return SPIKY_VALUE_ERROR without launching.
+ * Every call on one device shares that device's array, so calls that
+ * overlap on one device (different streams, threads or managers) race. */
+#define SPIKY_NOALLOC_SCRATCH_BYTES (64ull << 20)
+int spiky_lut_forward_step_noalloc(spiky_lut_manager *m, const float *weights,
+                                   uint32_t batch_size, const float *input, const int32_t *anchors,
+                                   float *output, int32_t *lookup_indices, float cmp_eps,
+                                   float *min_deltas, int32_t *min_delta_indices, void *stream);
+
 /* int8 tables with a per-detector fp32 scale, forward (eval or train).
  * Weight of row entry = scales[t] * (float)q8[...] in fp32.  Fully connected
  * managers only.  The int8 form has no counterpart in the reference (its

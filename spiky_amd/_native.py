@@ -38,6 +38,7 @@ _SIGNATURES = {
     "spiky_lut_max_forward_groups_per_neuron": ([_vp], _u32),
     "spiky_lut_n_synapses": ([_vp], _u64),
     "spiky_lut_forward_step": ([_vp, _vp, _u32, _vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp], _i32),
+    "spiky_lut_forward_step_noalloc": ([_vp, _vp, _u32, _vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp], _i32),
     "spiky_lut_forward_step_i8": ([_vp, _vp, _vp, _u32, _vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp], _i32),
     "spiky_lut_backward_backprop": ([_vp, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _vp, _f64, _vp, _i32, _vp], _i32),
     "spiky_lut_set_sparse_connectivity": ([_vp, _vp, _vp, _u64], _i32),

@@ -10,6 +10,7 @@
 #include <cstdio>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -223,6 +224,30 @@ struct spiky_lut_manager {
 };
 
 namespace {
+
+// Scratch of the allocation-free forward: one copy of this array per device,
+// allocated with the code object and held until the process ends.  Host code
+// never uses the array's name as a device address: noalloc_scratch() resolves
+// each device's own copy once, with that device current, and kernels receive
+// that pointer.
+static __device__ __align__(256) uint8_t scratch[SPIKY_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mutex;
+void *g_noalloc_ptr[kMaxDevices] = {};
+
+void *noalloc_scratch() {
+    int dev = 0;
+    check_hip(hipGetDevice(&dev), "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) throw std::runtime_error("device id out of range");
+    std::lock_guard<std::mutex> lock(g_noalloc_mutex);
+    if (!g_noalloc_ptr[dev]) {
+        void *p = nullptr;
+        check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        g_noalloc_ptr[dev] = p;
+    }
+    return g_noalloc_ptr[dev];
+}
 
 void require_manager(const spiky_lut_manager *m) {
     if (!m) throw ValueError("null manager");
@@ -483,6 +508,47 @@ int spiky_lut_forward_step(spiky_lut_manager *m, const float *weights, uint32_t 
                 });
             }
         }
+    });
+}
+
+int spiky_lut_forward_step_noalloc(spiky_lut_manager *m, const float *weights,
+                                   uint32_t batch_size, const float *input, const int32_t *anchors,
+                                   float *output, int32_t *lookup_indices, float cmp_eps,
+                                   float *min_deltas, int32_t *min_delta_indices, void *stream) {
+    return guarded([&] {
+        require_manager(m);
+        if (batch_size == 0) throw ValueError("batch_size == 0");
+        if (m->sequence_length != 1)
+            throw ValueError("forward_step should only be called when sequence_length == 1");
+        require_initialized(m);
+        if (m->fully_connected != 1)
+            throw ValueError("forward_step_noalloc needs a fully connected manager");
+        if (!weights || !input || !anchors || !output || !lookup_indices)
+            throw ValueError("null tensor pointer");
+        if ((min_deltas == nullptr) != (min_delta_indices == nullptr))
+            throw ValueError("w_min_anchor_deltas and w_min_anchor_delta_indices must be given together");
+        const spiky::FcShape s = m->shape(batch_size);
+        const bool tm = spiky::tm_fill_applies(s, m->int_mode);
+        const size_t need = tm ? spiky::tm_fill_scratch_bytes(s, m->int_mode) : 0;
+        if (need > SPIKY_NOALLOC_SCRATCH_BYTES)
+            throw ValueError("forward_step_noalloc: this shape needs " + std::to_string(need) +
+                             " bytes of scratch, more than the " +
+                             std::to_string(SPIKY_NOALLOC_SCRATCH_BYTES) +
+                             " the allocation-free path holds; use forward_step");
+        void *scr = tm ? noalloc_scratch() : nullptr;
+        m->context_active = true;
+        const hipStream_t st = as_stream(stream);
+        check_hip(spiky::launch_check_detectors(s, input, anchors, cmp_eps, lookup_indices, min_deltas,
+                                                min_delta_indices, st),
+                  "check_detectors");
+        if (tm)
+            check_hip(spiky::launch_fill_tm(s, weights, lookup_indices, output, m->int_mode,
+                                            m->int_rescaler, scr, st),
+                      "fill_outputs_fc");
+        else
+            check_hip(spiky::launch_fill_fc_f32(s, weights, lookup_indices, output, m->int_mode,
+                                                m->int_rescaler, st),
+                      "fill_outputs_fc");
     });
 }
 
