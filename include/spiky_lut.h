@@ -55,6 +55,17 @@ int spiky_lut_create(uint32_t n_inputs, uint32_t n_outputs, uint32_t n_detectors
                      uint32_t forward_group_size, uint32_t backward_group_size,
                      int summation_int32, double int_rescaler, spiky_lut_manager **out);
 
+/* fp32 summation order of the fully connected forward (no reference
+ * counterpart; default 0).  ordered != 0: one fp32 commit per block of
+ * backward_group_size tables, added in ascending block order -- the reference
+ * CPU path's arithmetic (lut_runtime_kernels_logic.proto:1214-1299 run serially),
+ * bit for bit.  ordered == 0: at large batches the table-major forward sums
+ * several blocks in fp64 before one fp32 commit, which is at least as close to
+ * the exact sum and within the reference GPU path's own order-dependent fp32
+ * tolerance (it commits blocks with atomics in any order).  int32 summation is
+ * bit-exact either way. */
+int spiky_lut_set_ordered_sums(spiky_lut_manager *m, int ordered);
+
 /* Replaces the pybind destructor (lut.cu ~LUTDataManager). */
 void spiky_lut_destroy(spiky_lut_manager *m);
 

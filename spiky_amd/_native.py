@@ -31,6 +31,7 @@ _SIGNATURES = {
     "spiky_lut_version": ([], ctypes.c_char_p),
     "spiky_lut_create": ([_u32, _u32, _u32, _u32, _u32, _u32, _u64, _u32, _u32, _i32, _f64, _pp], _i32),
     "spiky_lut_destroy": ([_vp], None),
+    "spiky_lut_set_ordered_sums": ([_vp, _i32], _i32),
     "spiky_lut_register_synapse_meta": ([_vp, _f32, _f32, _f32, _f32, _f32, ctypes.POINTER(_u32)], _i32),
     "spiky_lut_initialize_neurons": ([_vp, _i32], _i32),
     "spiky_lut_n_lookup_neurons": ([_vp], _u64),

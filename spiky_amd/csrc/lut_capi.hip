@@ -118,6 +118,7 @@ struct spiky_lut_manager {
     uint32_t forward_group_size, backward_group_size;
     bool int_mode;
     double int_rescaler;
+    bool ordered_sums = false;  // spiky_lut_set_ordered_sums
     uint64_t n_lookup;
     std::vector<std::vector<float>> metas;  // lr, min, max, noise, init
     int fully_connected = -1;               // -1: neurons not initialised
@@ -209,6 +210,7 @@ struct spiky_lut_manager {
         s.n_entries = n_entries();
         s.dgs = backward_group_size;
         s.ogs = forward_group_size;
+        s.ordered_sums = ordered_sums;
         return s;
     }
 
@@ -306,6 +308,13 @@ int spiky_lut_create(uint32_t n_inputs, uint32_t n_outputs, uint32_t n_detectors
         m->int_rescaler = summation_int32 ? int_rescaler : 0.0;
         m->n_lookup = (uint64_t)n_detectors << bits;  // lut.cu:42
         *out = m;
+    });
+}
+
+int spiky_lut_set_ordered_sums(spiky_lut_manager *m, int ordered) {
+    return guarded([&] {
+        require_manager(m);
+        m->ordered_sums = ordered != 0;
     });
 }
 

@@ -23,6 +23,10 @@ struct FcShape {
     uint32_t n_entries;  // 2^n_anchors
     uint32_t dgs;        // detectors per fp64 partial sum (backward_group_size)
     uint32_t ogs;        // outputs per gradient dot block (forward_group_size)
+    // fp32 summation: true keeps one fp32 commit per block of dgs tables in
+    // ascending block order (bit-identical to the reference CPU path); false lets
+    // the table-major forward sum several blocks in fp64 before one commit
+    bool ordered_sums = false;
 };
 
 // check_detectors(_eval): lookup index, and in train mode the min-margin anchor.
@@ -68,8 +72,11 @@ hipError_t launch_bucket_samples(const FcShape &s, const int32_t *idx, int32_t *
                                  uint32_t key_shift = 7);
 
 // ---- table-major fully connected path (lut_tm.hip) ------------------------
-// Forward gather-sum through per-block partials in scratch; bit-identical to
-// launch_fill_fc_f32.  Applies to fp32 tables with E <= 256 and O % 4 == 0.
+// Forward gather-sum through per-unit partials in scratch.  With
+// s.ordered_sums (and always for int32 summation) it is bit-identical to
+// launch_fill_fc_f32; otherwise each partial is the fp64 sum of several
+// blocks, committed in ascending order.  Applies to fp32 tables with E <= 256
+// and O % 4 == 0.
 bool tm_fill_applies(const FcShape &s, bool int_mode);
 size_t tm_fill_scratch_bytes(const FcShape &s, bool int_mode);
 hipError_t launch_fill_tm(const FcShape &s, const float *w, const int32_t *idx, float *out,

@@ -422,8 +422,12 @@ constexpr int kDmaRows = kTmMaxEntries * 128;  // bytes of a stage's rows
 
 typedef __attribute__((address_space(3))) void lds_void;
 
+// AUX is the load's cache policy: 0 default, kNonTemporal for table bytes that
+// are streamed once (measured 11% faster for a pure table stream on gfx950)
+constexpr int kNonTemporal = 2;
+template <int AUX = 0>
 __device__ __forceinline__ void dma16(const void *g, void *lds_base) {
-    __builtin_amdgcn_global_load_lds(g, (lds_void *)lds_base, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(g, (lds_void *)lds_base, 16, 0, AUX);
 }
 
 // wait until at most N of this wave's vector-memory loads are outstanding
@@ -478,7 +482,7 @@ __global__ __launch_bounds__(kTmThreads) void k_fill_tm_dma(
         const float *wt = w + (size_t)t * kTmMaxEntries * n_outputs;
 #pragma unroll
         for (int h = 0; h < 2; h++)
-            dma16(wt + goff[h], stage + ((uint32_t)h * kTmThreads + wave * kWave) * 16);
+            dma16<kNonTemporal>(wt + goff[h], stage + ((uint32_t)h * kTmThreads + wave * kWave) * 16);
         if (wave == 0) {
             // the stage's keys: kKeyBytes bytes, 16 per lane of the first lanes
             if (lane * 16 < (uint32_t)kKeyBytes)
@@ -764,65 +768,76 @@ __global__ __launch_bounds__(kTmThreads) void k_propagate_tm_dma(
     }
 }
 
-// Propagate partials over 64-column slices (fp32 tables with 256 entries,
-// n_outputs % 64 == 0).  A stage holds a table's 256 rows x 256 bytes: 16
-// lanes read one row, which the gfx950 LDS serves without bank conflicts
-// (8 lanes on random 128-byte rows conflict about half the time), and the
-// table bytes cross HBM in 256-byte pieces.  Thread layout: wave w, lane l:
-// sample w*4 + l/16 (+64 i for i < SPT), column quad l % 16.  A ring of two
-// stages (one table ahead, 136 KiB).  Each 8-lane half of a sample group
-// reduces its 32 columns; the two 32-column dots become the reference's block
-// terms du * dot (fp64, each dropped unless |term| > EPS when the blocks are
-// 32 outputs wide, proto:833-863) and their sum goes to dpart[slice][t][b]
-// (fp32), so k_propagate_reduce_pre only sums slices.  Keys are the rows' byte
-// offsets in this stage, main * 256 | (alt * 256) << 16, and du_t[t][b] is
-// du(min margin) (0 when the sample's min-margin index is unused); both rows
-// have the key pitch.
-constexpr int kTm64Pass = (kTmThreads / kWave) * 4;  // samples per pass
+// Propagate over whole tables (fp32 tables with 256 entries, n_outputs % 64 ==
+// 0).  A unit is TPU tables x every 64-column slice x one chunk of SPT * 128
+// samples.  The slice loop is outside the table loop: the slice's g columns
+// sit in registers (64 VGPRs at SPT = 8) while its TPU table stages stream
+// through a two-stage LDS-DMA ring (256 rows x 256 bytes each, the rows'
+// 256-byte HBM pieces loaded non-temporally), and every lane keeps one fp32
+// accumulator per table for one sample: the reference's per-(table, 32-output
+// block) terms du * (main - alt) of all the slices (proto:1421-1499, each
+// dropped unless |term| > EPS, proto:833-863).  du[b][t] is written once per
+// unit, so no per-slice partial crosses HBM (gfx950 pays about ten times a
+// read for a write mixed into a saturated read stream: config 3's 537 MB of
+// per-slice partials cost about 0.4 ms).
+//
+// Thread layout: wave w, lane l; sample group grp = l / 8 of the wave owns
+// sample w * 8 + grp (+128 i, i < SPT) and lane q = l % 8 the columns 8q ..
+// 8q + 7 of the slice, read as two 16-byte LDS pieces in swapped order on odd
+// groups (the two groups of a 16-lane LDS service group then read disjoint
+// bank halves of their rows).  Keys are the rows' byte offsets in a stage,
+// main * 256 | (alt * 256) << 16, and du_t[t][b] is du(min margin) (0 when
+// the sample's min-margin index is unused), both with the key pitch.
+constexpr int kUnitPass = (kTmThreads / kWave) * 8;  // samples per pass: 128
 constexpr int kTm64Rows = kTmMaxEntries * 256;       // bytes of a stage's rows
 
-template <int SPT>
-__global__ __launch_bounds__(kTmThreads) void k_propagate_tm64(
+template <int SPT, int TPU>
+__global__ __launch_bounds__(kTmThreads) void k_propagate_units(
     const float *__restrict__ w, const float *__restrict__ g, const uint32_t *__restrict__ key_t,
-    const float *__restrict__ du_t, float *__restrict__ dpart, uint32_t batch, uint32_t pitch,
-    uint32_t n_outputs, uint32_t n_detectors, uint32_t tpu, uint32_t n_slices, uint32_t n_chunks,
-    bool block_eps) {
-    constexpr int kRing = 2;
-    constexpr int kKeyBytes = kTm64Pass * SPT * 4;  // keys, then as many bytes of du
+    const float *__restrict__ du_t, float *__restrict__ du_out, uint32_t batch, uint32_t pitch,
+    uint32_t n_outputs, uint32_t n_detectors, uint32_t n_chunks, bool block_eps) {
+    static_assert(SPT == 4 || SPT == 8, "one or two groups of four samples a lane");
+    constexpr int kKeyBytes = kUnitPass * SPT * 4;    // keys, then as many bytes of du
     constexpr int kStage = kTm64Rows + 2 * kKeyBytes;
     constexpr uint32_t kKeyWaves = (kKeyBytes + kWave * 16 - 1) / (kWave * 16);
-    constexpr int kRowLoads = kTm64Rows / (kTmThreads * 16);  // 16-byte DMA loads per thread
-    __shared__ __attribute__((aligned(16))) uint8_t smem[kRing * kStage];
+    constexpr int kRowLoads = kTm64Rows / (kTmThreads * 16);
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kStage];
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & (kWave - 1);
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-    const uint32_t slice = blockIdx.x % n_slices;
-    const uint32_t rest = blockIdx.x / n_slices;
-    const uint32_t chunk = rest % n_chunks;
-    const uint32_t k = rest / n_chunks;
-    const uint32_t t0 = k * tpu;
-    const uint32_t t1 = min(t0 + tpu, n_detectors);
-    const uint32_t b_base = chunk * (kTm64Pass * SPT);
-    const uint32_t col0 = slice * 64;
-    const uint32_t q = lane & 15;
-    const uint32_t half = q >> 3;
-    const uint32_t s_loc0 = wave * 4 + (lane >> 4);
+    const uint32_t chunk = blockIdx.x % n_chunks;
+    const uint32_t t0 = (blockIdx.x / n_chunks) * TPU;
+    const uint32_t ntab = min((uint32_t)TPU, n_detectors - t0);
+    const uint32_t n_slices = n_outputs / 64;
+    const uint32_t b_base = chunk * (kUnitPass * SPT);
+    const uint32_t q = lane & 7;
+    const uint32_t grp = lane >> 3;
+    const uint32_t sw = (grp & 1) * 16;
+    const uint32_t s_loc0 = wave * 8 + grp;
+    // lanes q < 4 sum the slice's first 32-column block, lanes q >= 4 its
+    // second; lane q and lane 7 - q hold the same samples after each quad
+    // reduction, so one half-mirror exchange joins a sample's two blocks
+    const bool hi = q >= 4;
+    const uint32_t qm = hi ? 7 - q : q;
+    const bool c1 = (qm >> 1) & 1, c0 = qm & 1;
+    const uint32_t my_item = (hi && SPT == 8 ? 4u : 0u) + 2 * c1 + c0;
+    const bool writer = SPT == 8 || !hi;
+    const uint32_t my_b = b_base + s_loc0 + kUnitPass * my_item;
 
-    f32x4 gv[SPT];
+    float acc[TPU];
 #pragma unroll
-    for (int i = 0; i < SPT; i++) {
-        const uint32_t b = min(b_base + s_loc0 + kTm64Pass * i, batch - 1);
-        gv[i] = *reinterpret_cast<const f32x4 *>(g + (size_t)b * n_outputs + col0 + q * 4);
-    }
+    for (int j = 0; j < TPU; j++) acc[j] = 0.0f;
+    f32x4 g0[SPT], g1[SPT];
+    const uint32_t n_st = ntab * n_slices;
     auto issue = [&](uint32_t si) {
-        const uint32_t t = t0 + si;
-        uint8_t *stage = smem + (si % kRing) * kStage;
-        const float *wt = w + (size_t)t * kTmMaxEntries * n_outputs + col0;
+        const uint32_t sl = si / ntab, t = t0 + si % ntab;
+        uint8_t *stage = smem + (si & 1) * kStage;
+        const float *wt = w + (size_t)t * kTmMaxEntries * n_outputs + sl * 64;
 #pragma unroll
         for (int h = 0; h < kRowLoads; h++) {
-            const uint32_t c = (uint32_t)h * kTmThreads + tid;  // 16-byte chunk: row c / 16, quad c % 16
-            dma16(wt + (c >> 4) * n_outputs + (c & 15) * 4,
-                  stage + ((uint32_t)h * kTmThreads + wave * kWave) * 16);
+            const uint32_t c = (uint32_t)h * kTmThreads + tid;  // row c / 16, quad c % 16
+            dma16<kNonTemporal>(wt + (c >> 4) * n_outputs + (c & 15) * 4,
+                                stage + ((uint32_t)h * kTmThreads + wave * kWave) * 16);
         }
         if (wave < 2 * kKeyWaves) {
             // waves 0 .. kKeyWaves-1 load the keys, the next kKeyWaves the du values
@@ -836,58 +851,84 @@ __global__ __launch_bounds__(kTmThreads) void k_propagate_tm64(
         }
     };
 
-    const uint32_t nt = t1 - t0;
     issue(0);
-    for (uint32_t st = 0; st < nt; st++) {
-        // only stage st is outstanding here: wait for it, then publish it
+    for (uint32_t si = 0; si < n_st; si++) {
+        const uint32_t sl = si / ntab, tl = si % ntab;
+        if (tl == 0) {
+            // this slice's g columns, in the lane's read order
+#pragma unroll
+            for (int i = 0; i < SPT; i++) {
+                const uint32_t b = min(b_base + s_loc0 + kUnitPass * i, batch - 1);
+                const float *gp = g + (size_t)b * n_outputs + sl * 64 + q * 8;
+                g0[i] = *reinterpret_cast<const f32x4 *>(gp + (sw >> 2));
+                g1[i] = *reinterpret_cast<const f32x4 *>(gp + 4 - (sw >> 2));
+            }
+        }
+        // stage si (and the g columns) have landed; every wave is done with
+        // stage si - 1, whose slot takes stage si + 1
         wait_vm(0);
-        __asm__ volatile("" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        __asm__ volatile("" ::: "memory");
-        // every wave is done with stage st - 1: its slot takes stage st + 1
-        if (st + 1 < nt) issue(st + 1);
-        const uint8_t *tb = smem + (st % kRing) * kStage;
+        __syncthreads();
+        if (si + 1 < n_st) issue(si + 1);
+        const uint8_t *tb = smem + (si & 1) * kStage;
         const uint32_t *keys = reinterpret_cast<const uint32_t *>(tb + kTm64Rows);
         const float *dus = reinterpret_cast<const float *>(tb + kTm64Rows + kKeyBytes);
-        const uint8_t *tq = tb + q * 16;
-        const uint32_t t = t0 + st;
-        float *dp = dpart + ((size_t)slice * n_detectors + t) * batch;
+        const uint8_t *tq = tb + q * 32 + sw;
+        float tot[SPT / 4];
 #pragma unroll
-        for (int h8 = 0; h8 < SPT; h8 += 8) {
-            constexpr int N = SPT < 8 ? SPT : 8;
-            float dv[8];
+        for (int h = 0; h < SPT / 4; h++) {
+            // four samples at a time: the lane's 8-column pieces in fp32
+            float pc[4];
 #pragma unroll
-            for (int h = 0; h < N; h += 2) {
-                const uint32_t k0 = keys[s_loc0 + kTm64Pass * (h8 + h)];
-                const uint32_t k1 = keys[s_loc0 + kTm64Pass * (h8 + h + 1)];
-                const f32x4 a0 = *reinterpret_cast<const f32x4 *>(tq + (k0 & 0xFFFFu));
-                const f32x4 e0 = *reinterpret_cast<const f32x4 *>(tq + (k0 >> 16));
-                const f32x4 a1 = *reinterpret_cast<const f32x4 *>(tq + (k1 & 0xFFFFu));
-                const f32x4 e1 = *reinterpret_cast<const f32x4 *>(tq + (k1 >> 16));
-                const f32x4 &g0 = gv[h8 + h];
-                const f32x4 &g1 = gv[h8 + h + 1];
-                float d0 = (a0.x - e0.x) * g0.x;
-                d0 = __builtin_fmaf(a0.y - e0.y, g0.y, d0);
-                d0 = __builtin_fmaf(a0.z - e0.z, g0.z, d0);
-                d0 = __builtin_fmaf(a0.w - e0.w, g0.w, d0);
-                float d1 = (a1.x - e1.x) * g1.x;
-                d1 = __builtin_fmaf(a1.y - e1.y, g1.y, d1);
-                d1 = __builtin_fmaf(a1.z - e1.z, g1.z, d1);
-                d1 = __builtin_fmaf(a1.w - e1.w, g1.w, d1);
-                dv[h] = d0;
-                dv[h + 1] = d1;
+            for (int i = 0; i < 4; i++) {
+                const int ii = 4 * h + i;
+                const uint32_t kk = keys[s_loc0 + kUnitPass * ii];
+                const uint8_t *pm = tq + (kk & 0xFFFFu);
+                const uint8_t *pa = tq + (kk >> 16);
+                const f32x4 a0 = *reinterpret_cast<const f32x4 *>(pm);
+                const f32x4 a1 = *reinterpret_cast<const f32x4 *>(pm + 16 - 2 * sw);
+                const f32x4 e0 = *reinterpret_cast<const f32x4 *>(pa);
+                const f32x4 e1 = *reinterpret_cast<const f32x4 *>(pa + 16 - 2 * sw);
+                float d = (a0.x - e0.x) * g0[ii].x;
+                d = __builtin_fmaf(a0.y - e0.y, g0[ii].y, d);
+                d = __builtin_fmaf(a0.z - e0.z, g0[ii].z, d);
+                d = __builtin_fmaf(a0.w - e0.w, g0[ii].w, d);
+                d = __builtin_fmaf(a1.x - e1.x, g1[ii].x, d);
+                d = __builtin_fmaf(a1.y - e1.y, g1[ii].y, d);
+                d = __builtin_fmaf(a1.z - e1.z, g1[ii].z, d);
+                d = __builtin_fmaf(a1.w - e1.w, g1[ii].w, d);
+                pc[i] = d;
+                // at most two samples' rows in flight (32 VGPRs): the 64 VGPRs
+                // of g leave no room for more without spilling
+                if (i & 1) __builtin_amdgcn_sched_barrier(0);
             }
-            // the 8 lanes of each half hold 4-column pieces of N dots; after the
-            // reduce-scatter lane (q & 7) holds sample rs_item's 32-column sum
-            reduce_scatter8_f32<N>(dv, q & 7);
-            const uint32_t sl = s_loc0 + kTm64Pass * (h8 + rs_item<N>(q & 7));
-            double term = (double)dus[sl] * (double)dv[0];
-            if (block_eps && !(fabs(term) > kEps)) term = 0.0;
-            // lanes q and q ^ 8 hold the two 32-column blocks of the same sample
-            const double other = dpp_f64<kDppRowRor8>(term);
-            const uint32_t b = b_base + sl;
-            if (half == 0 && rs_writer<N>(q & 7) && b < batch) dp[b] = (float)(term + other);
+            // quad reduce-scatter (lanes q, q ^ 2, then q, q ^ 1): lane q is
+            // left with the 32-column block sum of sample 4h + 2 c1 + c0
+            float r2[2];
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const float lo = pc[j] + dpp_f32<kDppXor2>(pc[j]);
+                const float up = pc[2 + j] + dpp_f32<kDppXor2>(pc[2 + j]);
+                r2[j] = c1 ? up : lo;
+            }
+            const float lo = r2[0] + dpp_f32<kDppXor1>(r2[0]);
+            const float up = r2[1] + dpp_f32<kDppXor1>(r2[1]);
+            const float r1 = c0 ? up : lo;
+            // the reference's block term du * (main - alt), dropped unless
+            // |term| > EPS (proto:833-863), then the sample's two blocks joined
+            float term = dus[s_loc0 + kUnitPass * (4 * h + 2 * c1 + c0)] * r1;
+            if (block_eps && !(fabsf(term) > (float)kEps)) term = 0.0f;
+            tot[h] = term + dpp_f32<kDppHalfMirror>(term);
         }
+        const float add = (SPT == 8 && hi) ? tot[SPT / 4 - 1] : tot[0];
+#pragma unroll
+        for (int j = 0; j < TPU; j++)
+            if (j == (int)tl) acc[j] += add;
+    }
+    if (writer && my_b < batch) {
+        float *dst = du_out + (size_t)my_b * n_detectors + t0;
+#pragma unroll
+        for (int j = 0; j < TPU; j++)
+            if (j < (int)ntab) dst[j] = fabs((double)acc[j]) > kEps ? acc[j] : 0.0f;
     }
 }
 
@@ -949,45 +990,6 @@ __global__ __launch_bounds__(256) void k_propagate_reduce(const float *__restric
                 }
                 if (fabs(acc) > kEps) du = (float)acc;
             }
-        }
-        s_du[tx][r] = du;
-    }
-    __syncthreads();
-    for (uint32_t r = ty; r < 64; r += 4) {
-        const uint32_t b = bb + r, t = tb + tx;
-        if (b < batch && t < n_detectors) du_out[(size_t)b * n_detectors + t] = s_du[r][tx];
-    }
-}
-
-// du[b][t] = fp32 of the fp64 sum over slices s ascending of dpart[s][t][b]
-// (terms du(margin) * dot already formed by k_propagate_tm64), or 0 unless
-// |sum| > EPS.  Same 64 x 64 tiling as k_propagate_reduce.
-__global__ __launch_bounds__(256) void k_propagate_reduce_pre(const float *__restrict__ dpart,
-                                                              float *__restrict__ du_out,
-                                                              uint32_t batch, uint32_t n_detectors,
-                                                              uint32_t n_slices) {
-    __shared__ float s_du[64][65];
-    const uint32_t tb = blockIdx.x * 64;
-    const uint32_t bb = blockIdx.y * 64;
-    const uint32_t tx = threadIdx.x & 63;
-    const uint32_t ty = threadIdx.x >> 6;
-    for (uint32_t r = ty; r < 64; r += 4) {
-        const uint32_t t = tb + r, b = bb + tx;
-        float du = 0.0f;
-        if (b < batch && t < n_detectors) {
-            const float *p = dpart + (size_t)t * batch + b;
-            const size_t stride = (size_t)n_detectors * batch;
-            double acc = 0.0;
-            uint32_t sI = 0;
-            for (; sI + 8 <= n_slices; sI += 8) {
-                float v[8];
-#pragma unroll
-                for (int u = 0; u < 8; u++) v[u] = p[(sI + u) * stride];
-#pragma unroll
-                for (int u = 0; u < 8; u++) acc += (double)v[u];
-            }
-            for (; sI < n_slices; sI++) acc += (double)p[sI * stride];
-            if (fabs(acc) > kEps) du = (float)acc;
         }
         s_du[tx][r] = du;
     }
@@ -1099,6 +1101,8 @@ __global__ __launch_bounds__(256) void k_transpose_keys(const int32_t *__restric
     }
 }
 
+constexpr uint64_t kFoldUnits = 1024;
+
 uint32_t tm_spt(uint32_t batch) {
     if (batch <= (uint32_t)kTmPass) return 1;
     if (batch <= 2u * kTmPass) return 2;
@@ -1108,17 +1112,22 @@ uint32_t tm_spt(uint32_t batch) {
 
 }  // namespace
 
-// Blocks of dgs tables per unit: 1 for fp32 sums (every block is a rounding
-// point committed in order); with int32 payloads, enough to leave about 2048
-// units.
+// Blocks of dgs tables per unit.  Ordered fp32 sums: 1 (every block is a
+// rounding point committed in order).  int32 payloads (whose wrapping sum is
+// associative): enough to leave about 2048 units.  Folded fp32 sums: enough to
+// leave about 1024 units, each partial the fp64 sum of its blocks' tables --
+// the partials are written while the table stream is running, and on gfx950
+// a write mixed into a saturated read stream costs about ten times a read
+// (config 3: 1.07 GB of per-block partials, 134 MB folded eight blocks a unit).
 static uint32_t tm_fill_bpu(const FcShape &s, bool int_mode) {
-    if (!int_mode) return 1;
+    if (!int_mode && s.ordered_sums) return 1;
     const uint64_t n_blocks = (s.n_detectors + s.dgs - 1) / s.dgs;
     const uint64_t spt = tm_spt(s.batch);
     const uint64_t n_chunks = (s.batch + kTmPass * spt - 1) / (kTmPass * spt);
     const uint64_t n_slices = (s.n_outputs + kTmCols - 1) / kTmCols;
     const uint64_t units = n_blocks * n_chunks * n_slices;
-    return (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(n_blocks, units / 2048));
+    const uint64_t target = int_mode ? 2048 : kFoldUnits;
+    return (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(n_blocks, units / target));
 }
 
 bool tm_fill_applies(const FcShape &s, bool int_mode) {
@@ -1255,16 +1264,25 @@ static bool tm_propagate_wide(const FcShape &s) {
 
 uint32_t tm_key_row_shift(const FcShape &s) { return tm_propagate_wide(s) ? 8u : 7u; }
 
+// Samples of a chunk of the whole-table propagate (k_propagate_units): 512 up
+// to a batch of 512, else 1024.
+static uint32_t tm_units_spt(uint32_t batch) { return batch <= 4u * kUnitPass ? 4u : 8u; }
+
+// Row pitch of the transposed keys: whole chunks of samples of every
+// table-major propagate (at least 512 samples, the whole-table kernel's
+// smallest chunk), zero past the batch.
 uint32_t tm_key_pitch(uint32_t batch) {
-    const uint32_t chunk = kTmPass * tm_spt(batch);
+    const uint32_t chunk = kTmPass * std::max<uint32_t>(tm_spt(batch), 4u);
     return (batch + chunk - 1) / chunk * chunk;
 }
 
-// scratch: keys [T][pitch] u32 | du_t [T][pitch] f32 | partial dots
+// scratch: keys [T][pitch] u32 | du_t [T][pitch] f32 | then, for the
+// whole-table propagate, du [B][T] f32; for the slice propagate, partial dots
 // [slices][T][B] f32 | du [B][T] f32
 size_t tm_propagate_scratch_bytes(const FcShape &s) {
     const uint64_t n_slices = (s.n_outputs + kTmCols - 1) / kTmCols;
     const size_t keys = ((size_t)s.n_detectors * tm_key_pitch(s.batch) * 4 + 255) & ~(size_t)255;
+    if (tm_propagate_wide(s)) return 2 * keys + (size_t)s.batch * s.n_detectors * 4;
     return 2 * keys + (size_t)(n_slices + 1) * s.batch * s.n_detectors * 4;
 }
 
@@ -1287,28 +1305,21 @@ hipError_t launch_propagate_tm(const FcShape &s, const float *w, const float *g,
     const uint32_t tpu = 32;
     const uint32_t n_units = (s.n_detectors + tpu - 1) / tpu;
     if (wide) {
-        // 64-column slices; chunks of 1024 samples as the key pitch assumes
-        const uint32_t spt64 = s.batch <= 256 ? 4 : (s.batch <= 512 ? 8 : 16);
-        const uint32_t n_chunks = (s.batch + kTm64Pass * spt64 - 1) / (kTm64Pass * spt64);
-        const uint32_t n_slices64 = s.n_outputs / 64;
-        const uint64_t grid = (uint64_t)n_units * n_chunks * n_slices64;
+        // whole tables, every 64-column slice in one unit: du[b][t] directly
+        constexpr uint32_t kTpu = 8;
+        const uint32_t spt = tm_units_spt(s.batch);
+        const uint32_t n_chunks = (s.batch + kUnitPass * spt - 1) / (kUnitPass * spt);
+        const uint64_t grid = (uint64_t)((s.n_detectors + kTpu - 1) / kTpu) * n_chunks;
         if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
-#define SPIKY_P64(SPT)                                                                              \
-    hipLaunchKernelGGL((k_propagate_tm64<SPT>), dim3((uint32_t)grid), dim3(kTmThreads), 0, st, w, g, \
-                       key_t, du_t, dpart, s.batch, pitch, s.n_outputs, s.n_detectors, tpu,        \
-                       n_slices64, n_chunks, s.ogs == (uint32_t)kTmCols)
-        switch (spt64) {
-            case 4: SPIKY_P64(4); break;
-            case 8: SPIKY_P64(8); break;
-            default: SPIKY_P64(16); break;
-        }
-#undef SPIKY_P64
-        e = hipGetLastError();
-        if (e != hipSuccess) return e;
-        // the partials already hold du * dot: sum the 64-column slices
-        float *du = dpart + (size_t)n_slices * s.batch * s.n_detectors;
-        hipLaunchKernelGGL(k_propagate_reduce_pre, dim3((s.n_detectors + 63) / 64, (s.batch + 63) / 64),
-                           dim3(256), 0, st, dpart, du, s.batch, s.n_detectors, n_slices64);
+        float *du = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(scratch) + 2 * keys);
+        if (spt == 4)
+            hipLaunchKernelGGL((k_propagate_units<4, kTpu>), dim3((uint32_t)grid), dim3(kTmThreads), 0, st,
+                               w, g, key_t, du_t, du, s.batch, pitch, s.n_outputs, s.n_detectors, n_chunks,
+                               s.ogs == (uint32_t)kTmCols);
+        else
+            hipLaunchKernelGGL((k_propagate_units<8, kTpu>), dim3((uint32_t)grid), dim3(kTmThreads), 0, st,
+                               w, g, key_t, du_t, du, s.batch, pitch, s.n_outputs, s.n_detectors, n_chunks,
+                               s.ogs == (uint32_t)kTmCols);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
         return launch_propagate_scatter(s, du, min_idx, anchors, x_grad, st);

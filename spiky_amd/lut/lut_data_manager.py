@@ -139,6 +139,8 @@ class _LUTDataManagerBase:
             _native.check(L.spiky_lut_register_synapse_meta(self._h, *meta, ctypes.byref(out)))
         if self._fully_connected is not None:
             _native.check(L.spiky_lut_initialize_neurons(self._h, int(self._fully_connected)))
+        if getattr(self, "_ordered_sums", False):
+            _native.check(L.spiky_lut_set_ordered_sums(self._h, 1))
         if self._compiled and not self._fully_connected:
             offs, tg = self._csr
             _native.check(L.spiky_lut_set_sparse_connectivity(
@@ -358,6 +360,16 @@ class _LUTDataManagerBase:
     def lookup_connectivity(self):
         """(syn_offsets int64 [n_lookup+1], syn_targets int32) of a compiled sparse manager."""
         return getattr(self, "_csr", None)
+
+    def set_ordered_sums(self, ordered):
+        """True: the fp32 forward commits one fp32 value per block of
+        backward_group_size tables in ascending block order, bit-identical to
+        the reference CPU path (lut_runtime_kernels_logic.proto:1214-1299).
+        False (default): large batches sum several blocks in fp64 before one
+        commit, within the fp32 tolerance of the reference GPU path's
+        unordered atomics.  No effect on int32 summation."""
+        self._ordered_sums = bool(ordered)
+        _native.check(_native.lib().spiky_lut_set_ordered_sums(self._h, int(self._ordered_sums)))
 
     def to_device(self, device):
         self._device = int(device)

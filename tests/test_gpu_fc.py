@@ -285,6 +285,35 @@ def test_table_major_folded_blocks(oracle, cuda_device, tables):
     assert np.array_equal(out.cpu().numpy(), rout)
 
 
+@pytest.mark.parametrize("ordered", [False, True])
+def test_forward_fold_modes(oracle, cuda_device, ordered):
+    """Table-major fp32 forward with two 1024-sample chunks and 128 blocks of
+    32 tables (2048 units): ordered sums give the reference CPU path's output
+    bit for bit; the default folds two blocks into one fp64 sum, which is the
+    oracle's arithmetic with 64-table blocks, bit for bit, and within 1e-5 of
+    each row's largest output of the ordered result."""
+    from test_gpu_layers import fold_blocks
+    dev = cuda_device
+    B, I, T, Nc, O = 2048, 300, 4096, 8, 256
+    E = 1 << Nc
+    x, anchors, W, _ = make_inputs(21, B, I, T, Nc, O, x_normal=True)
+    dm = make_dm(I, O, T, Nc)
+    dm.set_ordered_sums(ordered)
+    fold = 1 if ordered else fold_blocks(B, T, O)
+    assert ordered or fold == 2
+    out = torch.zeros(B * O, device=dev)
+    idx = torch.empty(B * T, dtype=torch.int32, device=dev)
+    print(f"[fold] ordered={ordered} fold={fold}", flush=True)
+    dm.forward_step(W.to(dev), B, x.to(dev), anchors.to(dev), out, idx)
+    torch.cuda.synchronize()
+    ridx = oracle.check_detectors(x.numpy(), anchors.numpy(), B, I, T, Nc, train=False)
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    got = out.cpu().numpy()
+    assert np.array_equal(got, oracle.fill_outputs_fc(W.numpy(), ridx, B, O, T, E, dgs=32 * fold))
+    r32 = oracle.fill_outputs_fc(W.numpy(), ridx, B, O, T, E, dgs=32).reshape(B, O)
+    assert np.all(np.abs(got.reshape(B, O) - r32) <= 1e-5 * np.abs(r32).max(axis=1, keepdims=True))
+
+
 def test_errors_on_device(cuda_device):
     dev = cuda_device
     dm = make_dm(8, 4, 4, 2)

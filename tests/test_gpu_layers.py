@@ -121,21 +121,38 @@ def test_projection_layer_built_on_device(cuda_device):
     assert torch.equal(a(x), b(x))
 
 
-@pytest.mark.parametrize("B", [1024])
-def test_config3_full_size(oracle, cuda_device, B):
+def fold_blocks(B, T, O, dgs=32):
+    """Blocks of dgs tables the table-major fp32 forward sums in fp64 before one
+    commit when ordered sums are off: enough to leave about 1024 work units of
+    (block group, 32-column slice, 1024-sample chunk) -- the library's rule,
+    restated so a change of it shows here."""
+    n_blocks = -(-T // dgs)
+    spt = 1 if B <= 128 else 2 if B <= 256 else 4 if B <= 512 else 8
+    units = n_blocks * -(-B // (128 * spt)) * -(-O // 32)
+    return max(1, min(n_blocks, units // 1024))
+
+
+@pytest.mark.parametrize("ordered", [False, True])
+def test_config3_full_size(oracle, cuda_device, ordered):
     """BASELINE config 3 at its real size.  The oracle cannot hold the whole
     problem in seconds, so parity is checked on slices the arithmetic allows:
     every sample's forward output depends only on its own rows (gathered
     host-side into an E=1 table), every table's weight gradient only on that
-    table, every sample's input gradient only on its main and flipped rows."""
+    table, every sample's input gradient only on its main and flipped rows.
+    With ordered sums the output is the reference CPU path's, bit for bit;
+    by default (eight blocks folded into one fp64 sum) it is the oracle's with
+    256-table blocks bit for bit, and within 1e-5 of the ordered result."""
     dev = cuda_device
-    I, T, Nc, O = 4096, 8192, 8, 1024
+    B, I, T, Nc, O = 1024, 4096, 8192, 8, 1024
     E = 1 << Nc
     from spiky_amd import LUTDataManagerF
     dm = LUTDataManagerF(I, O, T, Nc, 1, 0, 0, 32, 32)
     dm.register_synapse_meta(1.0, -1.0, 1.0, 0.0, 0.0)
     dm.initialize_neurons(True)
     dm.to_device(0)
+    dm.set_ordered_sums(ordered)
+    fold = 1 if ordered else fold_blocks(B, T, O)
+    assert ordered or fold == 8
     gen = torch.Generator(device=dev).manual_seed(3)
     x = torch.randn(B * I, device=dev, generator=gen)
     W = torch.randn(T * E * O, device=dev, generator=gen) * 0.01
@@ -169,8 +186,11 @@ def test_config3_full_size(oracle, cuda_device, B):
     tt = torch.arange(T, device=dev)
     for s in samples:
         rows = Wv[tt, idx.view(B, T)[s].long()].cpu().numpy().reshape(-1)       # [T][O], E=1
-        r = oracle.fill_outputs_fc(rows, np.zeros((1, T), np.int32), 1, O, T, 1, dgs=32)
-        assert np.array_equal(out.view(B, O)[s].cpu().numpy(), r)
+        r = oracle.fill_outputs_fc(rows, np.zeros((1, T), np.int32), 1, O, T, 1, dgs=32 * fold)
+        got = out.view(B, O)[s].cpu().numpy()
+        assert np.array_equal(got, r)
+        r32 = oracle.fill_outputs_fc(rows, np.zeros((1, T), np.int32), 1, O, T, 1, dgs=32)
+        assert np.abs(got - r32).max() <= 1e-5 * np.abs(r32).max()
         li = idx.view(B, T)[s].long()
         alt = li ^ (1 << mi.view(B, T)[s].long())
         pair = torch.stack([Wv[tt, li], Wv[tt, alt]], 1).cpu().numpy().reshape(-1)  # [T][2][O]
