@@ -49,11 +49,69 @@ def g_model_bytes(B, I, T, Nc, O, w=4):
     }
 
 
+def unique_bytes(B, I, T, Nc, O, w=4):
+    """Unique bytes per kernel family: what one launch must move across HBM at
+    least, each tensor once.  Per unit: the detector check reads 4 B per input
+    element and 8 B per anchor pair and writes 12 B per (sample, table); the
+    forward reads every table byte and 4 B of index per (sample, table) and
+    updates 4 B per output; the propagate reads every table byte, 4 B of output
+    gradient per output and 12 B per (sample, table), and updates 4 B per input
+    gradient element; the weight gradient writes every gradient byte and reads
+    the output gradient and the indices."""
+    E = 1 << Nc
+    tables = T * E * O * w
+    return {
+        "check_detectors": B * I * 4 + T * Nc * 8 + B * T * 12,
+        "fill_outputs_fc": tables + B * T * 4 + 2 * B * O * 4,
+        "propagate_fc": tables + B * O * 4 + B * T * 12 + T * Nc * 8 + 2 * B * I * 4,
+        "gather_w_gradients_fc": T * E * O * 4 + B * O * 4 + B * T * 4,
+    }
+
+
 def compulsory_bytes(B, I, T, Nc, O):
     """Unique bytes a step must move at least: the tables read in forward and
     backward, and the weight gradient written once."""
     E = 1 << Nc
     return 3 * T * E * O * 4 + 2 * B * I * 4 + 2 * B * O * 4 + B * T * 12
+
+
+def source_digest():
+    """sha256 (first 16 hex digits) of the HIP sources the library is built
+    from; counter summaries record the digest they were taken at."""
+    import hashlib
+    h = hashlib.sha256()
+    csrc = os.path.join(ROOT, "spiky_amd", "csrc")
+    for name in sorted(os.listdir(csrc)):
+        if name.endswith((".hip", ".h")):
+            with open(os.path.join(csrc, name), "rb") as f:
+                h.update(name.encode() + b"\0" + f.read())
+    return h.hexdigest()[:16]
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+class pinned_core:
+    """Runs the enclosed CPU baseline on one host core (the reference CPU path
+    is single-threaded), restoring the affinity afterwards."""
+
+    def __enter__(self):
+        self.saved = os.sched_getaffinity(0)
+        self.core = min(self.saved)
+        os.sched_setaffinity(0, {self.core})
+        return self
+
+    def __exit__(self, *exc):
+        os.sched_setaffinity(0, self.saved)
+        return False
 
 
 def make_anchors(T, I, Nc, seed, device):
@@ -66,18 +124,23 @@ def make_anchors(T, I, Nc, seed, device):
 
 
 def load_traffic(kernel, config):
-    """HBM bytes per launch of `kernel`, from the committed rocprofv3 counter
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter
     summary (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the copy-kernel
-    calibration factor).  Lines read "<kernel> <bytes>"; None when absent."""
+    calibration factor), with the source digest the summary was taken at.
+    Lines read "<kernel> <bytes>" and "# sources <digest>".  Returns
+    (bytes or None, digest or None)."""
     path = os.path.join(ROOT, "profiles", f"hbm_traffic_config{config}.txt")
     if not os.path.exists(path):
-        return None
+        return None, None
+    value = digest = None
     with open(path) as f:
         for line in f:
             parts = line.split()
-            if len(parts) == 2 and parts[0] == kernel and not line.startswith("#"):
-                return float(parts[1])
-    return None
+            if line.startswith("# sources") and len(parts) == 3:
+                digest = parts[2]
+            elif len(parts) == 2 and parts[0] == kernel and not line.startswith("#"):
+                value = float(parts[1])
+    return value, digest
 
 
 def calibrate_copy(mib):
@@ -109,27 +172,30 @@ def cpu_baseline(x, anchors, W, go, B_full, I, T, Nc, O, sample_B):
     wg = np.empty(T * E * O, np.float32)
     times = []
     zero_fill = []
-    for rep in range(3):
-        t0 = time.perf_counter()
-        out = np.zeros(sample_B * O, np.float32)
-        idx, md, mi = oracle.check_detectors(xn, an, sample_B, I, T, Nc)
-        oracle.fill_outputs_fc(Wn, idx, sample_B, O, T, E, out=out)
-        xg = np.zeros(sample_B * I, np.float32)
-        tz = time.perf_counter()
-        wg.fill(0.0)
-        zero_fill.append(time.perf_counter() - tz)
-        oracle.propagate_fc(Wn, gn, idx, md, mi, an, sample_B, I, O, T, Nc, E, x_grad=xg)
-        oracle.gather_wgrad_fc(gn, idx, wg, sample_B, O, T, E)
-        dt = time.perf_counter() - t0
-        log(f"cpu baseline rep {rep}: {dt:.2f} s")
-        if rep > 0:
-            times.append(dt)
+    with pinned_core() as pin:
+        core = pin.core
+        for rep in range(3):
+            t0 = time.perf_counter()
+            out = np.zeros(sample_B * O, np.float32)
+            idx, md, mi = oracle.check_detectors(xn, an, sample_B, I, T, Nc)
+            oracle.fill_outputs_fc(Wn, idx, sample_B, O, T, E, out=out)
+            xg = np.zeros(sample_B * I, np.float32)
+            tz = time.perf_counter()
+            wg.fill(0.0)
+            zero_fill.append(time.perf_counter() - tz)
+            oracle.propagate_fc(Wn, gn, idx, md, mi, an, sample_B, I, O, T, Nc, E, x_grad=xg)
+            oracle.gather_wgrad_fc(gn, idx, wg, sample_B, O, T, E)
+            dt = time.perf_counter() - t0
+            log(f"cpu baseline rep {rep}: {dt:.2f} s")
+            if rep > 0:
+                times.append(dt)
     med = float(np.median(times))
     return {
         "value": sample_B / med,
         "unit": "samples/s",
         "cores": 1,
         "kind": "port",
+        "cpu": f"{cpu_model()} (pinned to core {core})",
         "sample": (f"config workload at batch {sample_B} of {B_full} (same tables, anchors, inputs); "
                    f"median of 2 timed steps after 1 warm-up; step {med:.3f} s of which w_grad "
                    f"zero-fill {float(np.median(zero_fill[1:])):.3f} s"),
@@ -195,13 +261,23 @@ def bench_projection(args):
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    dms = [l1._lut_dm, l2._lut_dm, head._lut_dm]
+    for d in dms:
+        d.get_kernel_times(reset=True)
+        d.set_kernel_timing(True)
     log(f"timing {args.steps} steps")
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    log(f"{ms:.3f} ms/step")
+    ktimes = {}
+    for name, d in zip(("layer1", "layer2", "head"), dms):
+        d.set_kernel_timing(False)
+        for k, (cnt, tot) in d.get_kernel_times(reset=True).items():
+            ktimes[f"{name}.{k}"] = tot / max(cnt, 1)
+    log(f"{ms:.3f} ms/step; kernels {ktimes}")
+    roofline = projection_roofline(l1, l2, head, x.detach(), B, ktimes)
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_projection(l1, l2, head, x.detach(), g, B, PROJ["cpu_reps"])
@@ -217,10 +293,51 @@ def bench_projection(args):
                    "layer1": "28x28 -> 48x48, 144 groups x 32 tables, 5 pairs, 5x5 fields, 16 targets",
                    "layer2": "48x48 -> 20x40, 25 groups x 64 tables, 6 pairs, 12x12 fields, 32 targets",
                    "head": "800 -> 10, 128 tables, 6 pairs", "parallelism": "single GPU"},
-        "roofline": None,
+        "roofline": roofline,
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)
+
+
+def projection_roofline(l1, l2, head, x, B, ktimes):
+    """Roofline of config 2's dominant kernel family, with bytes from the built
+    CSR.  Each (sample, table) lookup of a sparse layer reaches the synapses
+    of one lookup neuron: G model = 4 bytes x those synapses x 5 (forward
+    read, main and flipped reads in the propagate, read-modify-write of the
+    weight gradient) plus 12 bytes of index and margins; unique bytes = every
+    synapse weight (forward and propagate families) or weight-gradient word
+    (weight-gradient family) once, plus the activations."""
+    import numpy as np
+    import oracle
+    layers = {"layer1": (l1, 784, 2304, 5), "layer2": (l2, 2304, 800, 6)}
+    acts = {"layer1": x.cpu().numpy().reshape(-1)}
+    import torch
+    with torch.no_grad():
+        acts["layer2"] = l1(x).cpu().numpy().reshape(-1)
+    fams = {}
+    for name, (layer, I, O, Nc) in layers.items():
+        offs, tg = layer._lut_dm.lookup_connectivity()
+        T = layer.n_detectors()
+        idx = oracle.check_detectors(acts[name], layer._detector_anchors.cpu().numpy(), B, I, T, Nc,
+                                     train=False)
+        neuron = (np.arange(T)[None, :] * (1 << Nc) + idx.reshape(B, T)).reshape(-1)
+        hits = int(np.sum(offs[neuron + 1] - offs[neuron]))
+        n_syn = int(tg.size)
+        side = B * I * 4 + B * O * 4 + B * T * 12
+        fams[f"{name}.fill_outputs_sparse"] = (n_syn * 4 + side, hits * 4 + side)
+        fams[f"{name}.propagate_sparse"] = (n_syn * 4 + side + B * I * 4, 2 * hits * 4 + side)
+        fams[f"{name}.gather_w_gradients_sparse"] = (n_syn * 4 + B * O * 4 + B * T * 4, 2 * hits * 4)
+    known = {k: v for k, v in ktimes.items() if k in fams}
+    if not known:
+        return None
+    dom = max(known, key=known.get)
+    ms = known[dom]
+    ub, gb = fams[dom]
+    return {"bound": "hbm", "kernel": dom, "achieved": round(ub / (ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS,
+            "unit": "GB/s", "frac": round(ub / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "traffic": None,
+            "algorithmic_bytes_per_launch": ub, "ms_per_launch": round(ms, 4),
+            "g_model": {"bytes_per_launch": gb, "frac": round(gb / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
+            "kernels": {k: round(v, 4) for k, v in ktimes.items()}}
 
 
 def cpu_projection(l1, l2, head, x, g, B, reps):
@@ -238,6 +355,8 @@ def cpu_projection(l1, l2, head, x, g, B, reps):
     Wh, ah = head._weights.detach().cpu().numpy(), head._detector_anchors.cpu().numpy()
     xn, gn = x.cpu().numpy().reshape(-1), g.cpu().numpy().reshape(-1)
     times = []
+    pin = pinned_core()
+    pin.__enter__()
     for rep in range(reps):
         t0 = time.perf_counter()
         acts = [xn]
@@ -257,8 +376,10 @@ def cpu_projection(l1, l2, head, x, g, B, reps):
         dt = time.perf_counter() - t0
         if rep > 0:
             times.append(dt)
+    pin.__exit__(None, None, None)
     med = float(np.median(times))
     return {"value": B / med, "unit": "samples/s", "cores": 1, "kind": "port",
+            "cpu": f"{cpu_model()} (pinned to core {pin.core})",
             "sample": f"the whole config-2 step at batch {B}; median of {reps - 1} after 1 warm-up; step {med:.3f} s"}
 
 
@@ -312,9 +433,12 @@ def bench_int8(args):
     log(f"{ms:.3f} ms/step; kernels {ktimes}")
     gb = {"check_detectors": B * I * 4 + T * Nc * 8 + B * T * 4,
           "fill_outputs_fc_i8": B * T * O * 1 + T * 4 + B * O * 4}
+    # unique bytes: the int8 tables and scales once, the indices, the output once
+    ub = {"check_detectors": B * I * 4 + T * Nc * 8 + B * T * 4,
+          "fill_outputs_fc_i8": T * E * O + T * 4 + B * T * 4 + 2 * B * O * 4}
     dom = max(ktimes.items(), key=lambda kv: kv[1][1])[0]
     dom_ms = ktimes[dom][1] / ktimes[dom][0]
-    achieved = gb[dom] / (dom_ms * 1e-3) / 1e9
+    achieved = ub[dom] / (dom_ms * 1e-3) / 1e9
     cpu = None
     if not args.no_cpu_baseline:
         import oracle
@@ -323,19 +447,21 @@ def bench_int8(args):
         qn, scn = q8.cpu().numpy(), scales.cpu().numpy()
         xn, an = x[:sb * I].cpu().numpy(), anchors.cpu().numpy()
         times = []
-        for rep in range(3):
-            t1 = time.perf_counter()
-            o = np.zeros(sb * O, np.float32)
-            ridx = oracle.check_detectors(xn, an, sb, I, T, Nc, train=False)
-            oracle.fill_outputs_fc(None, ridx, sb, O, T, E, out=o, q8=qn, scales=scn, int_mode=True,
-                                   int_rescaler=c["int_rescaler"])
-            oracle.convert_int_to_float(o, c["int_rescaler"])
-            dt = time.perf_counter() - t1
-            log(f"cpu baseline rep {rep}: {dt:.2f} s")
-            if rep > 0:
-                times.append(dt)
+        with pinned_core() as pin:
+            for rep in range(3):
+                t1 = time.perf_counter()
+                o = np.zeros(sb * O, np.float32)
+                ridx = oracle.check_detectors(xn, an, sb, I, T, Nc, train=False)
+                oracle.fill_outputs_fc(None, ridx, sb, O, T, E, out=o, q8=qn, scales=scn, int_mode=True,
+                                       int_rescaler=c["int_rescaler"])
+                oracle.convert_int_to_float(o, c["int_rescaler"])
+                dt = time.perf_counter() - t1
+                log(f"cpu baseline rep {rep}: {dt:.2f} s")
+                if rep > 0:
+                    times.append(dt)
         med = float(np.median(times))
         cpu = {"value": sb / med, "unit": "samples/s", "cores": 1, "kind": "port",
+               "cpu": f"{cpu_model()} (pinned to core {pin.core})",
                "sample": f"config-4 workload at batch {sb} of {B}; median of 2 after 1 warm-up; step {med:.3f} s"}
     res = {
         "metric": "int8 LUT forward samples/sec at 8192 tables (BASELINE config 4)",
@@ -350,7 +476,9 @@ def bench_int8(args):
                    "table_bytes": T * E * O, "int_rescaler": c["int_rescaler"], "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
-                     "algorithmic_bytes_per_launch": gb[dom], "ms_per_launch": round(dom_ms, 4),
+                     "algorithmic_bytes_per_launch": ub[dom], "ms_per_launch": round(dom_ms, 4),
+                     "g_model": {"bytes_per_launch": gb[dom],
+                                 "frac": round(gb[dom] / (dom_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
                      "kernels": {k: round(v[1] / v[0], 4) for k, v in ktimes.items()}},
         "cpu_baseline": cpu,
     }
@@ -374,6 +502,96 @@ def transformer_g_bytes(B, cfg):
     att = B * pairs * T_att * E * 4 * (1 + 2 + 2)
     fc = lambda O: sum(g_model_bytes(B * S, E, cfg["n_detectors"], cfg["n_anchors_per_detector"], O).values())
     return cfg["num_layers"] * (att + fc(E)) + fc(V)
+
+
+def transformer_unique_bytes(B, model):
+    """Unique bytes of one config-5 step: every LUT table read in the forward
+    and in the backward and its weight gradient written once, plus each LUT
+    layer's input and output activations and their gradients once."""
+    S, E = model.context_size, model.embedding_dim if isinstance(model.embedding_dim, int) else \
+        model.embedding_dim[0] * model.embedding_dim[1]
+    total = 0
+    for layer in model._lut_layers():
+        total += 3 * layer._weights.numel() * 4
+        total += 2 * B * S * (layer._n_inputs + layer._n_outputs) * 4
+    return total
+
+
+def cpu_transformer(model, tokens, targets):
+    """The C oracle chained as the model runs (one sequence): embedding, per
+    block the sequence-concat attention LUT plus residual and the feed-forward
+    LUT plus residual, the unembedding LUT, the cross-entropy gradient, then
+    the backward through the same layers (input and weight gradients of every
+    LUT, positional-embedding gradients).  One host core, median of 2 after a
+    warm-up."""
+    import numpy as np
+    import oracle
+    B, S = tokens.shape
+    V = model.vocab_size
+    E = model.embedding_dim
+    blocks = []
+    for b in model.layers:
+        att, ffn = b["attention_lut"], b["ffn"]
+        blocks.append((att, ffn, att._weights.detach().cpu().numpy(), att._detector_anchors.cpu().numpy(),
+                       att._positional_embeddings.detach().cpu().numpy(), ffn._weights.detach().cpu().numpy(),
+                       ffn._detector_anchors.cpu().numpy()))
+    un = model.unembedder
+    Wu, au = un._weights.detach().cpu().numpy(), un._detector_anchors.cpu().numpy()
+    emb = model.token_embedder.weight.detach().cpu().numpy()
+    tk, tg = tokens.cpu().numpy(), targets.cpu().numpy().reshape(-1)
+
+    def one_step():
+        z = emb[tk].astype(np.float32).reshape(-1)
+        saved = []
+        for att, ffn, Wa, aa, pe, Wf, af in blocks:
+            T, Nc, Npe = att._n_detectors, att._n_anchors_per_detector, att._positional_dim
+            idx, md, mi = oracle.check_detectors(z, aa, B * S, E, T, Nc)
+            pidx, pmd, pmi = oracle.check_pe(pe, S, T, Npe)
+            a = oracle.fill_outputs_seq(Wa, idx, pidx, B, E, T, S, Nc, Npe)
+            saved.append(("att", att, Wa, aa, (idx, md, mi, pidx, pmd, pmi)))
+            z = z + a
+            Tf, Ncf = ffn._n_detectors, ffn._n_anchors_per_detector
+            fi, fmd, fmi = oracle.check_detectors(z, af, B * S, E, Tf, Ncf)
+            z = z + oracle.fill_outputs_fc(Wf, fi, B * S, E, Tf, 1 << Ncf)
+            saved.append(("ffn", ffn, Wf, af, (fi, fmd, fmi)))
+        Tu, Ncu = un._n_detectors, un._n_anchors_per_detector
+        ui, umd, umi = oracle.check_detectors(z, au, B * S, E, Tu, Ncu)
+        logits = oracle.fill_outputs_fc(Wu, ui, B * S, V, Tu, 1 << Ncu).reshape(B * S, V).astype(np.float64)
+        p = np.exp(logits - logits.max(axis=1, keepdims=True))
+        p /= p.sum(axis=1, keepdims=True)
+        p[np.arange(B * S), tg] -= 1.0
+        grad = (p / (B * S)).astype(np.float32).reshape(-1)
+        wg = np.zeros(Wu.size, np.float32)
+        oracle.gather_wgrad_fc(grad, ui, wg, B * S, V, Tu, 1 << Ncu)
+        grad = oracle.propagate_fc(Wu, grad, ui, umd, umi, au, B * S, E, V, Tu, Ncu, 1 << Ncu)
+        for kind, layer, W, an, keys in reversed(saved):
+            T, Nc = layer._n_detectors, layer._n_anchors_per_detector
+            wg = np.zeros(W.size, np.float32)
+            if kind == "ffn":
+                fi, fmd, fmi = keys
+                oracle.gather_wgrad_fc(grad, fi, wg, B * S, E, T, 1 << Nc)
+                xg = oracle.propagate_fc(W, grad, fi, fmd, fmi, an, B * S, E, E, T, Nc, 1 << Nc)
+            else:
+                idx, md, mi, pidx, pmd, pmi = keys
+                Npe = layer._positional_dim
+                oracle.gather_wgrad_seq(grad, idx, pidx, wg, B, E, T, S, Nc, Npe)
+                xg, _ = oracle.propagate_seq(W, grad, idx, md, mi, pidx, pmd, pmi, an, B, E, E, T, S, Nc, Npe)
+            grad = (grad + xg).astype(np.float32)
+
+    times = []
+    with pinned_core() as pin:
+        for rep in range(3):
+            t0 = time.perf_counter()
+            one_step()
+            dt = time.perf_counter() - t0
+            log(f"cpu baseline rep {rep}: {dt:.2f} s")
+            if rep > 0:
+                times.append(dt)
+    med = float(np.median(times))
+    return {"value": B / med, "unit": "samples/s", "cores": 1, "kind": "port",
+            "cpu": f"{cpu_model()} (pinned to core {pin.core})",
+            "sample": f"one sequence of the config-5 step (forward, cross-entropy gradient, backward) "
+                      f"through the C oracle; median of 2 after 1 warm-up; step {med:.2f} s"}
 
 
 def bench_transformer(args):
@@ -415,6 +633,10 @@ def bench_transformer(args):
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
     g = transformer_g_bytes(B, cfg)
+    u = transformer_unique_bytes(B, model)
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_transformer(model, tokens[:1], targets[:1])
     res = {
         "metric": "LUTTransformer fwd+bwd samples/sec (BASELINE config 5)",
         "value": round(B / (ms / 1e3), 2),
@@ -424,10 +646,13 @@ def bench_transformer(args):
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32 (fp64 partial sums)",
         "data": "synthetic (uniform random byte tokens, next-token targets, N(0,0.01) tables)",
         "config": {"workload": "BASELINE config 5: LUTTransformer block stack fwd+bwd", "batch": B, **cfg},
-        "roofline": {"bound": "hbm", "achieved": round(g / (ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(g / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                     "traffic": None, "algorithmic_bytes_per_step": g, "scope": "whole step, G model"},
-        "cpu_baseline": None,
+        "roofline": {"bound": "hbm", "achieved": round(u / (ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(u / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                     "traffic": None, "algorithmic_bytes_per_step": u,
+                     "scope": "whole step, unique bytes (every table read forward and backward, every "
+                              "weight gradient written once, activations)",
+                     "g_model": {"bytes_per_step": g, "frac": round(g / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}},
+        "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)
 
@@ -669,31 +894,44 @@ def main():
     log(f"{ms_per_step:.3f} ms/step, {value:.1f} samples/s; kernels {ktimes}")
 
     gbytes = g_model_bytes(B, I, T, Nc, O)
+    ubytes = unique_bytes(B, I, T, Nc, O)
     per_kernel = {}
     for name, (cnt, tot) in ktimes.items():
         ms = tot / max(cnt, 1)
-        b = gbytes.get(name)
         per_kernel[name] = {"ms_per_launch": round(ms, 4),
-                            "gbs_g_model": round(b / (ms * 1e-3) / 1e9, 1) if b else None}
+                            "unique_gbs": round(ubytes[name] / (ms * 1e-3) / 1e9, 1) if name in ubytes else None,
+                            "g_model_gbs": round(gbytes[name] / (ms * 1e-3) / 1e9, 1) if name in gbytes else None}
     dom = max(ktimes.items(), key=lambda kv: kv[1][1])[0]
     dom_ms = ktimes[dom][1] / ktimes[dom][0]
-    achieved = gbytes[dom] / (dom_ms * 1e-3) / 1e9
-    traffic = load_traffic(dom, args.config)
+    achieved = ubytes[dom] / (dom_ms * 1e-3) / 1e9
+    traffic, digest = load_traffic(dom, args.config)
+    stale = traffic is not None and digest != source_digest()
+    if stale:
+        traffic = None
     step_g = sum(gbytes.values())
     roofline = {
         "bound": "hbm",
         "kernel": dom,
+        # unique bytes of one launch (each tensor once) over its mean launch time
         "achieved": round(achieved, 1),
         "peak": PEAK_HBM_GBS,
         "unit": "GB/s",
         "frac": round(achieved / PEAK_HBM_GBS, 4),
+        "algorithmic_bytes_per_launch": ubytes[dom],
+        "ms_per_launch": round(dom_ms, 4),
+        # measured HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE,
+        # profiles/hbm_traffic_config3.txt), null when that summary predates
+        # the current kernel sources
         "traffic": traffic,
-        # measured HBM bytes (rocprofv3 counters, profiles/) over the same launch time
+        "traffic_source_digest": digest,
+        "traffic_stale": stale,
         "traffic_gbs": round(traffic / (dom_ms * 1e-3) / 1e9, 1) if traffic else None,
         "traffic_frac": round(traffic / (dom_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4) if traffic else None,
-        "algorithmic_bytes_per_launch": gbytes[dom],
-        "ms_per_launch": round(dom_ms, 4),
-        "step_g_model_frac": round(step_g / (ms_per_step * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+        # the gather model (every sample's row access counted, no reuse credit):
+        # above 1 wherever the table-major kernels serve rows from LDS
+        "g_model": {"bytes_per_launch": gbytes[dom],
+                    "frac": round(gbytes[dom] / (dom_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                    "step_frac": round(step_g / (ms_per_step * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
         "step_compulsory_frac": round(compulsory_bytes(B, I, T, Nc, O) / (ms_per_step * 1e-3) / 1e9
                                       / PEAK_HBM_GBS, 4),
         "kernels": per_kernel,
