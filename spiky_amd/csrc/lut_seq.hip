@@ -35,6 +35,7 @@
 #include "lut_kernels.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace spiky {
 namespace {
@@ -916,6 +917,347 @@ __global__ __launch_bounds__(kBlock) void k_seq_tri_reduce(
     }
 }
 
+// ---------------------------------------------------------------------------
+// Input and positional gradients, LDS-grouped form (fp32 summation, O of 64,
+// 128 or 256, Nc <= 10, S <= kGrpMaxDist + 1).
+//
+// Every (pair i < j, table) term of the reference (proto:3740-3834) is a dot
+// of g[b][j] with one to three rows of the (t, Q_j) sub-table: the main row
+// (Q_j, K_i, P_d), d = j - i - 1, the K-flipped row (Q_j, K_i ^ bit, P_d) of a
+// K flip, the PE-flipped row (Q_j, K_i, P_d ^ bit) of a PE flip; and a Q flip
+// dots g[b][j] with the Q-flipped row (Q_j ^ bit, K_i, P_d).  All of those rows
+// share their Q with a row of one sub-table, and every flip but the K flip of a
+// high bit stays inside a group of 2^gb K values.  So one 1024-thread
+// workgroup per (t, Q, K group) stages that group's rows -- 2^(gb + Npe) rows,
+// at most 128 KiB -- in LDS once, and computes the dots that read them:
+//   main role, the items (b, j) with Q_j = Q (bucket order): for each earlier
+//     position i whose K is in the group, the main row (-> qsum of j for a Q
+//     flip, -> position i for a K flip, -> distance d for a PE flip), a
+//     K-flipped row of a low bit (-> i, negated), a PE-flipped row (-> d,
+//     negated); for each earlier i whose K flips to the group by a high bit,
+//     the K-flipped row (-> i, negated);
+//   Q-flip role, the items with Q_j ^ bit = Q: for each earlier i in the group
+//     with a Q flip, the Q-flipped row (-> j, negated).
+// Positions come from per-(t, b) lists sorted by group (k_seq_group_lists).
+// A wavefront takes one item at a time with g[b][j] in registers (fp64),
+// turns 32 candidate positions a turn into row dots (a ballot compaction into
+// a per-wave LDS queue) and computes 8 dots at a time, 8 lanes a dot: lane s
+// of dot slot p reads 16 bytes of each 128-byte chunk, chunks taken in the
+// order (k + p) mod NCH so two slots that share a 16-lane LDS cycle read
+// opposite bank halves.  Dots are fp64 sums of exact fp32 products; the
+// contributions to j are summed in registers over the item, those to i go to
+// M[b][t][i] with fp64 atomics and those to d to an LDS sum per distance,
+// flushed (times du of the distance's positional margin) into dpe once.
+// Position s then takes du(minDelta_s) * M[b][t][s] (k_seq_xgrad), the same
+// total the pair triangles gave: qsum_main - qsum_alt + the K-flip column sum.
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int kGrpThreads = 1024;
+constexpr int kGrpWaves = kGrpThreads / kWave;
+constexpr int kGrpTabBytes = 128 * 1024;
+constexpr int kGrpMaxDist = 512;   // S - 1
+constexpr int kGrpQueue = 256;     // row-dot entries a wave holds (power of two)
+
+// Lists of one (t, b): positions of the sequence whose K is in group G
+// (list A) and positions whose K flips into group G by a bit >= gb (list B),
+// each ascending in i.  Entry: x = the position's minDelta bits,
+// y = i | (K & 0x3FF) << 16 | minIdx (0xF: none) << 26.
+__global__ __launch_bounds__(kWave) void k_seq_group_lists(
+    const uint2 *__restrict__ pack, uint2 *__restrict__ list_a, uint32_t *__restrict__ off_a,
+    uint2 *__restrict__ list_b, uint32_t *__restrict__ off_b, uint32_t batch, uint32_t seq,
+    uint32_t n_anchors, uint32_t gb) {
+    const uint32_t lane = threadIdx.x;
+    const uint32_t t = blockIdx.x / batch, b = blockIdx.x % batch;
+    const uint32_t ng = 1u << (n_anchors - gb);
+    const uint2 *kp = pack + (size_t)t * batch * seq + (size_t)b * seq;
+    const size_t lb = (size_t)t * batch + b;
+    uint2 *la = list_a + lb * seq, *lbp = list_b + lb * seq;
+    uint32_t *oa = off_a + lb * (ng + 1), *ob = off_b + lb * (ng + 1);
+    uint32_t na = 0, nb = 0;
+    const uint64_t below = (1ull << lane) - 1;
+    for (uint32_t G = 0; G < ng; G++) {
+        if (lane == 0) {
+            oa[G] = na;
+            ob[G] = nb;
+        }
+        for (uint32_t c0 = 0; c0 < seq; c0 += kWave) {
+            const uint32_t i = c0 + lane;
+            const bool valid = i < seq;
+            const uint2 r = valid ? kp[i] : make_uint2(0u, 0u);
+            const uint32_t K = rec_idx(r);
+            const int32_t km = rec_mi(r);
+            const bool in_a = valid && (K >> gb) == G;
+            const bool in_b = valid && km >= (int32_t)gb && (uint32_t)km < n_anchors &&
+                              ((K ^ (1u << km)) >> gb) == G;
+            const uint2 e = make_uint2(r.x, i | ((K & 0x3FFu) << 16) |
+                                                ((km < 0 ? 0xFu : (uint32_t)km & 0xFu) << 26));
+            const uint64_t ba = __ballot(in_a), bb = __ballot(in_b);
+            if (in_a) la[na + __popcll(ba & below)] = e;
+            if (in_b) lbp[nb + __popcll(bb & below)] = e;
+            na += __popcll(ba);
+            nb += __popcll(bb);
+        }
+    }
+    if (lane == 0) {
+        oa[ng] = na;
+        ob[ng] = nb;
+    }
+}
+
+// Queue entry (4 bytes): LDS row (9 bits) | cj << 9 | ci << 11 | cd << 13 |
+// i << 15, where cj, ci, cd are signed 2-bit coefficients (01 = +1, 11 = -1)
+// of the dot's share in position j, position i and distance d = j - i - 1.
+constexpr uint32_t kCoPlus = 1, kCoMinus = 3;
+constexpr int kCoJ = 9, kCoI = 11, kCoD = 13, kEntI = 15;
+
+__device__ __forceinline__ int32_t grp_code(uint32_t e, int at) {
+    return __builtin_amdgcn_sbfe((int32_t)e, at, 2);
+}
+
+// fp32 8-lane sum (xor 1, xor 2, half-row mirror), every lane of the group gets it
+__device__ __forceinline__ float grp_sum8f(float v) {
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), kDppXor1, 0xF, 0xF, true));
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), kDppXor2, 0xF, 0xF, true));
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), kDppHalfMirror, 0xF, 0xF, true));
+    return v;
+}
+
+template <int NCH>
+__global__ __launch_bounds__(kGrpThreads) void k_propagate_seq_grp(
+    const float *__restrict__ w, const float *__restrict__ g, const uint2 *__restrict__ pack,
+    const uint2 *__restrict__ ppack, const int32_t *__restrict__ offsets,
+    const int32_t *__restrict__ samples, const int32_t *__restrict__ offsets2,
+    const int32_t *__restrict__ samples2, const uint2 *__restrict__ list_a,
+    const uint32_t *__restrict__ off_a, const uint2 *__restrict__ list_b,
+    const uint32_t *__restrict__ off_b, double *__restrict__ macc, double *__restrict__ dpe,
+    uint32_t batch, uint32_t seq, uint32_t n_detectors, uint32_t n_anchors, uint32_t pe_dim,
+    uint32_t gb, uint32_t per_xcd) {
+    constexpr uint32_t O = NCH * 32;
+    constexpr uint32_t kRowBytes = O * 4;
+    __shared__ __attribute__((aligned(16))) uint8_t tab[kGrpTabBytes];
+    __shared__ double dsum[kGrpMaxDist];
+    __shared__ uint2 prec[kGrpMaxDist];
+    __shared__ uint32_t queue[kGrpWaves][kGrpQueue];
+    __shared__ uint32_t next_item;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & (kWave - 1);
+    const uint32_t wave = uniform(tid / kWave);
+    const uint32_t nq = 1u << n_anchors;
+    const uint32_t ng = 1u << (n_anchors - gb);
+    const uint32_t wid = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (wid >= n_detectors * nq * ng) return;
+    const uint32_t G = wid % ng, Q = (wid / ng) % nq, t = wid / (ng * nq);
+    const uint32_t n_rows = batch * seq;
+    const int32_t m0 = offsets[(size_t)t * (nq + 1) + Q];
+    const int32_t m1 = offsets[(size_t)t * (nq + 1) + Q + 1];
+    const int32_t a0 = offsets2[(size_t)t * (2 * nq + 1) + Q];
+    const int32_t a1 = offsets2[(size_t)t * (2 * nq + 1) + Q + 1];
+    const uint32_t n_main = (uint32_t)(m1 - m0);
+    const uint32_t n_items = n_main + (uint32_t)(a1 - a0);
+    if (n_items == 0) return;  // uniform over the workgroup
+    const uint32_t kbits = n_anchors + pe_dim;
+    const uint32_t n_dist = seq - 1;
+
+    // stage the group's rows (one contiguous block of the table)
+    {
+        const uint32_t bytes = (1u << (gb + pe_dim)) * kRowBytes;
+        const uint8_t *src = reinterpret_cast<const uint8_t *>(
+            w + ((((size_t)t << n_anchors | Q) << kbits) | ((size_t)G << (gb + pe_dim))) * O);
+        for (uint32_t off = wave * kWave * 16; off < bytes; off += kGrpThreads * 16)
+            if (off + lane * 16 < bytes)  // groups below 1 KiB: no lane reads past the block
+                __builtin_amdgcn_global_load_lds(src + off + lane * 16, (lds_void *)(tab + off), 16, 0, 2);
+    }
+    for (uint32_t d = tid; d < n_dist; d += kGrpThreads) {
+        prec[d] = ppack[(size_t)t * n_dist + d];
+        dsum[d] = 0.0;
+    }
+    if (tid == 0) next_item = 0;
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+
+    const uint32_t p = lane >> 3, s8 = lane & 7;
+    const uint32_t podd = p & 1;
+    const uint32_t pmask = (1u << pe_dim) - 1, gmask = (1u << gb) - 1;
+    const uint64_t below = (1ull << lane) - 1;
+    uint32_t *q = queue[wave];
+    // Slot p reads chunk k ^ (p & 1) at turn k, so slots p and p ^ 1 (one
+    // 16-lane LDS cycle) read opposite bank halves: even turns from base0 + 128 k,
+    // odd turns from base1 + 128 (k - 1) (immediate offsets).
+    const uint32_t c0l = podd * 128 + 16 * s8;
+    const uint32_t c1l = (1 - podd) * 128 + 16 * s8;
+    const int32_t *smp = samples + (size_t)t * n_rows + m0;
+    const int32_t *smp2 = samples2 + (size_t)t * n_rows + a0;
+    const uint2 *kp = pack + (size_t)t * n_rows;
+
+    for (;;) {
+        uint32_t it = 0;
+        if (lane == 0) it = atomicAdd(&next_item, 1u);
+        it = uniform(__shfl(it, 0, kWave));
+        if (it >= n_items) break;
+        const bool main_role = it < n_main;
+        const uint32_t row = (uint32_t)(main_role ? smp[it] : smp2[it - n_main]);
+        const uint32_t b = row / seq, j = row % seq;
+        if (j == 0) continue;
+        const uint2 qr = kp[row];
+        const int32_t qm = rec_mi(qr);
+        const float qd = rec_md(qr);
+        float gf[NCH][4];
+        {
+            const float *g0 = g + (size_t)row * O + c0l / 4;  // chunk k ^ (p & 1) as the LDS reads
+            const float *g1 = g + (size_t)row * O + c1l / 4;
+#pragma unroll
+            for (int k = 0; k < NCH; k++) {
+                const f32x4 v = (k & 1) ? *reinterpret_cast<const f32x4 *>(g1 + (k - 1) * 32)
+                                        : *reinterpret_cast<const f32x4 *>(g0 + k * 32);
+#pragma unroll
+                for (int c = 0; c < 4; c++) gf[k][c] = v[c];
+            }
+        }
+        // wait for g here, once an item: a first read inside the step loop would
+        // make every step wait for the vector-memory counter, global atomics of
+        // the earlier steps included
+#pragma unroll
+        for (int k = 0; k < NCH; k++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) __asm__ volatile("" : "+v"(gf[k][c]));
+        double *mrow = macc + ((size_t)b * n_detectors + t) * seq;
+        double jacc = 0.0;
+        uint32_t qh = 0, qt = 0;
+
+        // 8 row dots from the queue (n of them live): exact fp32 products (FMA)
+        // in four fp32 chains of NCH terms per lane, the chains and the slot's
+        // 8 lanes summed in fp32 (a tree of depth 5), the dot then in fp64
+        auto step = [&](uint32_t n) {
+            const uint32_t e = q[(qh + p) & (kGrpQueue - 1)];
+            const bool on = p < n;
+            const uint32_t rb = on ? (e & 0x1FFu) * kRowBytes : 0u;  // slots past n: row 0
+            const uint8_t *t0 = tab + rb + c0l;
+            const uint8_t *t1 = tab + rb + c1l;
+            float f0 = 0.f, f1 = 0.f, f2 = 0.f, f3 = 0.f;
+#pragma unroll
+            for (int k = 0; k < NCH; k++) {
+                const f32x4 v = (k & 1) ? *reinterpret_cast<const f32x4 *>(t1 + (k - 1) * 128)
+                                        : *reinterpret_cast<const f32x4 *>(t0 + k * 128);
+                f0 = fmaf(v[0], gf[k][0], f0);
+                f1 = fmaf(v[1], gf[k][1], f1);
+                f2 = fmaf(v[2], gf[k][2], f2);
+                f3 = fmaf(v[3], gf[k][3], f3);
+            }
+            const float part = on ? (f0 + f1) + (f2 + f3) : 0.f;
+            const double tot = (double)grp_sum8f(part);
+            jacc += (double)grp_code(e, kCoJ) * tot;  // the same in the group's 8 lanes
+            const bool pushes = on && ((e >> kCoI) & 0xFu) != 0;
+            if (__ballot(pushes)) {
+                if (pushes && s8 == 0) {
+                    const int32_t ci = grp_code(e, kCoI), cd = grp_code(e, kCoD);
+                    const uint32_t i = (e >> kEntI) & 0x3FFu;
+                    if (ci) unsafeAtomicAdd(mrow + i, (double)ci * tot);
+                    if (cd) atomicAdd(&dsum[j - i - 1], (double)cd * tot);
+                }
+            }
+            qh += n;
+        };
+
+        const size_t lb = (size_t)t * batch + b;
+        const uint32_t *oa = off_a + lb * (ng + 1);
+        const uint32_t *ob = off_b + lb * (ng + 1);
+        const uint2 *la = list_a + lb * seq;
+        const uint2 *lbl = list_b + lb * seq;
+        // main role: lanes 0-31 take list A, lanes 32-63 list B, 32 a turn;
+        // Q-flip role: all lanes list A, 64 a turn
+        auto run_lists = [&](auto main_tag) {
+            constexpr bool kMain = decltype(main_tag)::value;
+            const bool use_b = kMain && lane >= 32;
+            constexpr uint32_t span = kMain ? 32u : 64u;
+            uint32_t cur = (use_b ? ob[G] : oa[G]) + (kMain ? (lane & 31) : lane);
+            const uint32_t end = use_b ? ob[G + 1] : oa[G + 1];
+            const uint2 *lst = use_b ? lbl : la;
+            for (;;) {
+                const bool in = cur < end;
+                const uint2 r = in ? lst[cur] : make_uint2(0u, 0xFFFFu);
+                const uint32_t i = r.y & 0xFFFFu;
+                const bool valid = in && i < j;
+                if (__ballot(valid) == 0) break;  // ascending i: the rest are >= j
+                uint32_t n_rd = 0, e_a = 0, e_b = 0, e_c = 0;
+                if (valid) {
+                    const uint32_t K = (r.y >> 16) & 0x3FFu;
+                    const float kd = __uint_as_float(r.x);
+                    const uint2 pr = prec[j - i - 1];
+                    const uint32_t P = rec_idx(pr) & pmask;
+                    const bool qflip = fabsf(qd) < fabsf(kd);
+                    const uint32_t iw = i << kEntI;
+                    const uint32_t lrow = ((K & gmask) << pe_dim) | P;
+                    if constexpr (!kMain) {  // Q-flip role (qm >= 0 for these items)
+                        e_a = lrow | (kCoMinus << kCoJ) | iw;
+                        n_rd = qflip ? 1u : 0u;
+                    } else {
+                        const uint32_t kmc = r.y >> 26;
+                        const int32_t km = kmc == 0xFu ? -1 : (int32_t)kmc;
+                        if (use_b) {  // a K flip of a bit >= gb into this group
+                            e_a = ((((K ^ (1u << (km & 31))) & gmask) << pe_dim) | P) | (kCoMinus << kCoI) | iw;
+                            n_rd = qflip ? 0u : 1u;
+                        } else {
+                            const int32_t pm = rec_mi(pr);
+                            const float pdl = rec_md(pr);
+                            const bool kflip = !qflip && km >= 0;
+                            const bool peflip = pe_dim > 0 && pm >= 0 && fabsf(pdl) < fabsf(qd) &&
+                                                fabsf(pdl) < fabsf(kd);
+                            const bool qs = qflip && qm >= 0;
+                            const bool low_k = kflip && (uint32_t)km < gb;
+                            e_a = lrow | ((qs ? kCoPlus : 0u) << kCoJ) | ((kflip ? kCoPlus : 0u) << kCoI) |
+                                  ((peflip ? kCoPlus : 0u) << kCoD) | iw;
+                            const uint32_t e_k = (lrow ^ (1u << ((km + pe_dim) & 31))) | (kCoMinus << kCoI) | iw;
+                            const uint32_t e_p = (lrow ^ (1u << (pm & 31))) | (kCoMinus << kCoD) | iw;
+                            e_b = low_k ? e_k : e_p;
+                            e_c = e_p;
+                            n_rd = (qs || kflip || peflip) ? 1u + (low_k ? 1u : 0u) + (peflip ? 1u : 0u) : 0u;
+                        }
+                    }
+                }
+                const uint64_t b1 = __ballot(n_rd >= 1);
+                const uint64_t b2 = kMain ? __ballot(n_rd >= 2) : 0ull;
+                const uint64_t b3 = kMain ? __ballot(n_rd >= 3) : 0ull;
+                const uint32_t pos = qt + __popcll(b1 & below) + __popcll(b2 & below) + __popcll(b3 & below);
+                if (n_rd >= 1) q[pos & (kGrpQueue - 1)] = e_a;
+                if (kMain && n_rd >= 2) q[(pos + 1) & (kGrpQueue - 1)] = e_b;
+                if (kMain && n_rd >= 3) q[(pos + 2) & (kGrpQueue - 1)] = e_c;
+                qt += __popcll(b1) + __popcll(b2) + __popcll(b3);
+                cur += span;
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                while (qt - qh >= 8) step(8);
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            }
+        };
+        if (main_role)
+            run_lists(std::integral_constant<bool, true>());
+        else
+            run_lists(std::integral_constant<bool, false>());
+        if (qt != qh) step(qt - qh);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // the item's own total: one value per slot group, over the wavefront
+#pragma unroll
+        for (int o = 8; o < kWave; o <<= 1) jacc += __shfl_xor(jacc, o, kWave);
+        if (lane == 0 && jacc != 0.0) unsafeAtomicAdd(mrow + j, jacc);
+    }
+    __syncthreads();
+    // distance sums, scaled by du of the distance's positional margin
+    for (uint32_t d = tid; d < n_dist; d += kGrpThreads) {
+        const double v = dsum[d];
+        if (v != 0.0) {
+            const uint2 pr = prec[d];
+            const int32_t pm = rec_mi(pr);
+            if (pm >= 0)
+                unsafeAtomicAdd(dpe + ((size_t)d * n_detectors + t) * pe_dim + pm, du_of_margin(rec_md(pr)) * v);
+        }
+    }
+}
+
 // Exact decomposition: one thread per (b, t, pair, output block).
 template <bool INT_MODE>
 __global__ __launch_bounds__(kBlock) void k_propagate_seq_exact(
@@ -1009,6 +1351,7 @@ __global__ __launch_bounds__(kBlock) void k_seq_alt_keys(const int32_t *__restri
 // x_grad[b][s][a1] += du, [a2] -= du with du = du(minDelta) * (qsum_main -
 // qsum_alt) + dk of (b, t, s) and the min anchor of (b, s, t) (both the Q flips
 // at s and the K flips at s flip that anchor), dropped unless |du| > EPS.
+// qsum_alt and dk may be null (the grouped pass leaves one total in qsum_main).
 __global__ __launch_bounds__(kBlock) void k_seq_xgrad(const double *__restrict__ qs_main,
                                                       const double *__restrict__ qs_alt,
                                                       const double *__restrict__ dk,
@@ -1024,7 +1367,8 @@ __global__ __launch_bounds__(kBlock) void k_seq_xgrad(const double *__restrict__
     const uint32_t t = (uint32_t)((it / seq) % n_detectors);
     const uint32_t b = (uint32_t)(it / ((uint64_t)seq * n_detectors));
     const uint2 rec = pack[(size_t)t * batch * seq + (size_t)b * seq + s];
-    const double du = du_of_margin(rec_md(rec)) * (qs_main[it] - qs_alt[it]) + dk[it];
+    const double du = du_of_margin(rec_md(rec)) * (qs_main[it] - (qs_alt ? qs_alt[it] : 0.0)) +
+                      (dk ? dk[it] : 0.0);
     if (!(fabs(du) > kEps)) return;
     const int32_t m = rec_mi(rec);
     if (m < 0 || (uint32_t)m >= n_anchors) return;
@@ -1359,6 +1703,8 @@ __global__ __launch_bounds__(kBlock) void k_wgrad_seq_atomic(
 
 uint32_t blocks_for(uint64_t n) { return (uint32_t)((n + kBlock - 1) / kBlock); }
 
+uint64_t align256_u64(uint64_t x) { return (x + 255) & ~(uint64_t)255; }
+
 uint32_t seq_vec(uint32_t n_outputs) {
     if (n_outputs % 4 == 0 && n_outputs >= 64u * 4u * 4u) return 4;
     if (n_outputs % 2 == 0 && n_outputs >= 64u * 2u * 4u) return 2;
@@ -1373,6 +1719,26 @@ uint64_t seq_tri_bytes(const SeqShape &s) {
 // The pair-parallel main pass and its triangle reduction apply (fp32 sums).
 bool seq_pairs_applies(const SeqShape &s) {
     return s.n_outputs % 4 == 0 && s.n_outputs <= (uint32_t)kPairMaxO && seq_tri_bytes(s) <= (16ull << 30);
+}
+
+// K-group bits of the grouped input-gradient pass (-1: it does not apply):
+// the widest group whose 2^(gb + Npe) rows fit the 128 KiB LDS table.
+int seq_grp_bits(const SeqShape &s) {
+    if (s.n_outputs != 64 && s.n_outputs != 128 && s.n_outputs != 256) return -1;
+    if (s.n_anchors > 10 || s.seq < 2 || s.seq - 1 > (uint32_t)kGrpMaxDist) return -1;
+    if ((uint64_t)s.batch * s.seq > 0x7fffffffull) return -1;
+    uint32_t lr = 0;
+    while ((kGrpTabBytes >> (lr + 1)) >= (int)(s.n_outputs * 4)) lr++;
+    if (s.pe_dim > lr) return -1;
+    return (int)std::min<uint32_t>(s.n_anchors, lr - s.pe_dim);
+}
+
+// Bytes of the grouped pass's position lists: two [T][B][S] entry arrays and
+// two [T][B][groups + 1] offset arrays.
+uint64_t seq_grp_list_bytes(const SeqShape &s, int gb) {
+    const uint64_t tb = (uint64_t)s.n_detectors * s.batch;
+    const uint64_t ng = 1ull << (s.n_anchors - gb);
+    return 2 * align256_u64(tb * s.seq * 8) + 2 * align256_u64(tb * (ng + 1) * 4);
 }
 
 // Columns of a forward slice for k_fill_seq_lds (0: it does not apply): the
@@ -1435,8 +1801,13 @@ size_t seq_scratch_bytes(const SeqShape &s, bool backward) {
     n += align256(rows * s.n_detectors * 4);
     n += align256((size_t)s.n_detectors * ((2u << s.n_anchors) + 1) * 4);
     n += align256((size_t)s.n_detectors * rows * 4);
-    // pair triangles of the pair-parallel main pass
-    if (seq_pairs_applies(s)) n += 2 * align256(seq_tri_bytes(s));
+    // position lists of the grouped pass, else the pair triangles of the
+    // pair-parallel main pass
+    const int gb = seq_grp_bits(s);
+    if (gb >= 0)
+        n += seq_grp_list_bytes(s, gb);
+    else if (seq_pairs_applies(s))
+        n += 2 * align256(seq_tri_bytes(s));
     return n;
 }
 
@@ -1589,10 +1960,24 @@ hipError_t launch_backward_seq(const SeqShape &s, float *w, const float *g, cons
     off += align256((size_t)s.n_detectors * ((2u << s.n_anchors) + 1) * 4);
     int32_t *samples2 = reinterpret_cast<int32_t *>(sp + off);
     off += align256((size_t)s.n_detectors * rows * 4);
-    const bool pairs = seq_pairs_applies(s);
+    const int gb = int_mode ? -1 : seq_grp_bits(s);
+    const bool pairs = gb < 0 && seq_pairs_applies(s);
     double *tk = pairs ? reinterpret_cast<double *>(sp + off) : nullptr;
     if (pairs) off += align256(seq_tri_bytes(s));
     double *tp = pairs ? reinterpret_cast<double *>(sp + off) : nullptr;
+    uint2 *list_a = nullptr, *list_b = nullptr;
+    uint32_t *off_a = nullptr, *off_b = nullptr;
+    if (gb >= 0) {
+        const uint64_t tb = (uint64_t)s.n_detectors * s.batch;
+        const uint64_t ng = 1ull << (s.n_anchors - gb);
+        list_a = reinterpret_cast<uint2 *>(sp + off);
+        off += align256_u64(tb * s.seq * 8);
+        list_b = reinterpret_cast<uint2 *>(sp + off);
+        off += align256_u64(tb * s.seq * 8);
+        off_a = reinterpret_cast<uint32_t *>(sp + off);
+        off += align256_u64(tb * (ng + 1) * 4);
+        off_b = reinterpret_cast<uint32_t *>(sp + off);
+    }
 
     hipLaunchKernelGGL(k_seq_pack, dim3((s.n_detectors + 63) / 64, (rows + 63) / 64), dim3(kBlock),
                        0, st, idx, md, mi, pack, rows, s.n_detectors);
@@ -1642,7 +2027,29 @@ hipError_t launch_backward_seq(const SeqShape &s, float *w, const float *g, cons
 #define SPIKY_PSEQ2(NJ)                                \
     SPIKY_PSEQ(NJ, false, samples, dq);                \
     SPIKY_PSEQ(NJ, true, samples2, dq_alt)
-        if (pairs) {
+        if (gb >= 0) {
+            const uint32_t ng = 1u << (s.n_anchors - gb);
+            hipLaunchKernelGGL(k_seq_group_lists, dim3(s.n_detectors * s.batch), dim3(kWave), 0, st,
+                               pack, list_a, off_a, list_b, off_b, s.batch, s.seq, s.n_anchors,
+                               (uint32_t)gb);
+            const uint64_t n_wg = (uint64_t)s.n_detectors * (1u << s.n_anchors) * ng;
+            const uint64_t per_xcd = (n_wg + 7) / 8;
+            if (per_xcd * 8 > 0x7fffffffu) return hipErrorInvalidConfiguration;
+#define SPIKY_PGRP(NCH)                                                                             \
+    hipLaunchKernelGGL(k_propagate_seq_grp<NCH>, dim3((uint32_t)(per_xcd * 8)), dim3(kGrpThreads), \
+                       0, st, w, g, pack, ppack, offsets, samples, offsets2, samples2, list_a,      \
+                       off_a, list_b, off_b, dq, dpe, s.batch, s.seq, s.n_detectors, s.n_anchors,   \
+                       s.pe_dim, (uint32_t)gb, (uint32_t)per_xcd)
+            switch (s.n_outputs) {
+                case 64: SPIKY_PGRP(2); break;
+                case 128: SPIKY_PGRP(4); break;
+                default: SPIKY_PGRP(8); break;
+            }
+#undef SPIKY_PGRP
+            hipLaunchKernelGGL(k_seq_xgrad, dim3(blocks_for(n_acc)), dim3(kBlock), 0, st, dq,
+                               (const double *)nullptr, (const double *)nullptr, pack, ap, x_grad,
+                               s.batch, s.seq, s.n_inputs, s.n_detectors, s.n_anchors);
+        } else if (pairs) {
             hipLaunchKernelGGL(k_propagate_seq_pairs, dim3((uint32_t)grid), dim3(kBlock),
                                pair_g_doubles(s.n_outputs) * sizeof(double), st, w, g,
                                pack, ppack, samples, dq, tk, tp, s.batch, s.seq, s.n_outputs,

@@ -203,6 +203,17 @@ def test_seq_one_bucket_chunks(oracle, cuda_device):
     run_seq(oracle, B, S, I, T, Nc, Npe, O, seed=12, inputs=(x, anchors, W, pe, go))
 
 
+@pytest.mark.parametrize("shape", [(3, 100, 48, 3, 5, 5, 128), (2, 513, 32, 2, 5, 6, 64),
+                                   (2, 30, 16, 3, 1, 0, 64)])
+def test_seq_grouped_input_gradient(oracle, cuda_device, shape):
+    # the LDS-grouped input-gradient pass at shapes besides the attention
+    # layer's: four K groups of 128-output rows (K flips of the high bits cross
+    # groups), the longest sequence it takes (512 distances, 6 positional
+    # bits, four groups of 64-output rows), and a sub-table below one KiB
+    B, S, I, T, Nc, Npe, O = shape
+    run_seq(oracle, B, S, I, T, Nc, Npe, O, seed=30 + Nc)
+
+
 def test_seq_attention_layer_shape_int32(oracle, cuda_device):
     run_seq(oracle, 2, 256, 64, 4, 6, 4, 256, seed=13, int_rescaler=0.25)
 
