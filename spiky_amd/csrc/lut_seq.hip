@@ -956,7 +956,8 @@ constexpr int kGrpThreads = 1024;
 constexpr int kGrpWaves = kGrpThreads / kWave;
 constexpr int kGrpTabBytes = 128 * 1024;
 constexpr int kGrpMaxDist = 512;   // S - 1
-constexpr int kGrpQueue = 256;     // row-dot entries a wave holds (power of two)
+constexpr int kGrpQueue = 128;     // row-dot entries a wave holds (power of two)
+constexpr int kGrpMeta = 640;      // items whose metadata a workgroup stages at a time
 
 // Lists of one (t, b): positions of the sequence whose K is in group G
 // (list A) and positions whose K flips into group G by a bit >= gb (list B),
@@ -1014,6 +1015,9 @@ __device__ __forceinline__ int32_t grp_code(uint32_t e, int at) {
     return __builtin_amdgcn_sbfe((int32_t)e, at, 2);
 }
 
+// a list slot past the end: i = 0xFFFF is >= every j
+__device__ __forceinline__ uint2 grp_none() { return make_uint2(0u, 0xFFFFu); }
+
 // fp32 8-lane sum (xor 1, xor 2, half-row mirror), every lane of the group gets it
 __device__ __forceinline__ float grp_sum8f(float v) {
     v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), kDppXor1, 0xF, 0xF, true));
@@ -1038,6 +1042,8 @@ __global__ __launch_bounds__(kGrpThreads) void k_propagate_seq_grp(
     __shared__ double dsum[kGrpMaxDist];
     __shared__ uint2 prec[kGrpMaxDist];
     __shared__ uint32_t queue[kGrpWaves][kGrpQueue];
+    __shared__ uint4 meta[kGrpMeta];
+    __shared__ double jtot[kGrpMeta];  // the staged items' own totals
     __shared__ uint32_t next_item;
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & (kWave - 1);
@@ -1071,9 +1077,6 @@ __global__ __launch_bounds__(kGrpThreads) void k_propagate_seq_grp(
         prec[d] = ppack[(size_t)t * n_dist + d];
         dsum[d] = 0.0;
     }
-    if (tid == 0) next_item = 0;
-    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
 
     const uint32_t p = lane >> 3, s8 = lane & 7;
     const uint32_t podd = p & 1;
@@ -1082,168 +1085,233 @@ __global__ __launch_bounds__(kGrpThreads) void k_propagate_seq_grp(
     uint32_t *q = queue[wave];
     // Slot p reads chunk k ^ (p & 1) at turn k, so slots p and p ^ 1 (one
     // 16-lane LDS cycle) read opposite bank halves: even turns from base0 + 128 k,
-    // odd turns from base1 + 128 (k - 1) (immediate offsets).
+    // odd turns from base1 + 128 (k - 1) (immediate offsets).  g is held the same way.
     const uint32_t c0l = podd * 128 + 16 * s8;
     const uint32_t c1l = (1 - podd) * 128 + 16 * s8;
     const int32_t *smp = samples + (size_t)t * n_rows + m0;
     const int32_t *smp2 = samples2 + (size_t)t * n_rows + a0;
     const uint2 *kp = pack + (size_t)t * n_rows;
 
-    for (;;) {
-        uint32_t it = 0;
-        if (lane == 0) it = atomicAdd(&next_item, 1u);
-        it = uniform(__shfl(it, 0, kWave));
-        if (it >= n_items) break;
-        const bool main_role = it < n_main;
-        const uint32_t row = (uint32_t)(main_role ? smp[it] : smp2[it - n_main]);
-        const uint32_t b = row / seq, j = row % seq;
-        if (j == 0) continue;
-        const uint2 qr = kp[row];
-        const int32_t qm = rec_mi(qr);
-        const float qd = rec_md(qr);
-        float gf[NCH][4];
-        {
-            const float *g0 = g + (size_t)row * O + c0l / 4;  // chunk k ^ (p & 1) as the LDS reads
+    for (uint32_t c0 = 0; c0 < n_items; c0 += kGrpMeta) {
+        const uint32_t cn = min((uint32_t)kGrpMeta, n_items - c0);
+        if (c0 > 0) __syncthreads();  // the previous chunk's items are done with meta
+        // item metadata: x = row | (qm + 1) << 27, y = qd bits, z = list A range,
+        // w = list B range (begin | end << 16, the (t, b) lists of group G)
+        for (uint32_t k = tid; k < cn; k += kGrpThreads) {
+            const uint32_t it = c0 + k;
+            const uint32_t row = (uint32_t)(it < n_main ? smp[it] : smp2[it - n_main]);
+            const uint2 qr = kp[row];
+            const size_t lb = (size_t)t * batch + row / seq;
+            const uint32_t *oa = off_a + lb * (ng + 1);
+            const uint32_t *ob = off_b + lb * (ng + 1);
+            meta[k] = make_uint4(row | ((uint32_t)(rec_mi(qr) + 1) << 27), qr.x, oa[G] | (oa[G + 1] << 16),
+                                 ob[G] | (ob[G + 1] << 16));
+            jtot[k] = 0.0;
+        }
+        if (tid == 0) next_item = 0;
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the table block too
+        __syncthreads();
+
+        auto fetch = [&]() -> uint32_t {
+            uint32_t v = 0;
+            if (lane == 0) v = atomicAdd(&next_item, 1u);
+            return uniform(__shfl(v, 0, kWave));
+        };
+        // an item's loads: g[b][j] in this lane's chunk order and the first
+        // candidate of its lists (main role: lanes 0-31 list A, 32-47 list B;
+        // Q-flip role: every lane list A)
+        auto issue = [&](uint32_t k, uint4 &mm, float (&gg)[NCH][4]) -> uint2 {
+            mm = meta[k];
+            const uint32_t row = mm.x & 0x7FFFFFFu;
+            const bool main_r = c0 + k < n_main;
+            const float *g0 = g + (size_t)row * O + c0l / 4;
             const float *g1 = g + (size_t)row * O + c1l / 4;
 #pragma unroll
-            for (int k = 0; k < NCH; k++) {
-                const f32x4 v = (k & 1) ? *reinterpret_cast<const f32x4 *>(g1 + (k - 1) * 32)
-                                        : *reinterpret_cast<const f32x4 *>(g0 + k * 32);
+            for (int kk = 0; kk < NCH; kk++) {
+                const f32x4 v = (kk & 1) ? *reinterpret_cast<const f32x4 *>(g1 + (kk - 1) * 32)
+                                         : *reinterpret_cast<const f32x4 *>(g0 + kk * 32);
 #pragma unroll
-                for (int c = 0; c < 4; c++) gf[k][c] = v[c];
+                for (int c = 0; c < 4; c++) gg[kk][c] = v[c];
             }
-        }
-        // wait for g here, once an item: a first read inside the step loop would
-        // make every step wait for the vector-memory counter, global atomics of
-        // the earlier steps included
-#pragma unroll
-        for (int k = 0; k < NCH; k++)
-#pragma unroll
-            for (int c = 0; c < 4; c++) __asm__ volatile("" : "+v"(gf[k][c]));
-        double *mrow = macc + ((size_t)b * n_detectors + t) * seq;
-        double jacc = 0.0;
-        uint32_t qh = 0, qt = 0;
-
-        // 8 row dots from the queue (n of them live): exact fp32 products (FMA)
-        // in four fp32 chains of NCH terms per lane, the chains and the slot's
-        // 8 lanes summed in fp32 (a tree of depth 5), the dot then in fp64
-        auto step = [&](uint32_t n) {
-            const uint32_t e = q[(qh + p) & (kGrpQueue - 1)];
-            const bool on = p < n;
-            const uint32_t rb = on ? (e & 0x1FFu) * kRowBytes : 0u;  // slots past n: row 0
-            const uint8_t *t0 = tab + rb + c0l;
-            const uint8_t *t1 = tab + rb + c1l;
-            float f0 = 0.f, f1 = 0.f, f2 = 0.f, f3 = 0.f;
-#pragma unroll
-            for (int k = 0; k < NCH; k++) {
-                const f32x4 v = (k & 1) ? *reinterpret_cast<const f32x4 *>(t1 + (k - 1) * 128)
-                                        : *reinterpret_cast<const f32x4 *>(t0 + k * 128);
-                f0 = fmaf(v[0], gf[k][0], f0);
-                f1 = fmaf(v[1], gf[k][1], f1);
-                f2 = fmaf(v[2], gf[k][2], f2);
-                f3 = fmaf(v[3], gf[k][3], f3);
-            }
-            const float part = on ? (f0 + f1) + (f2 + f3) : 0.f;
-            const double tot = (double)grp_sum8f(part);
-            jacc += (double)grp_code(e, kCoJ) * tot;  // the same in the group's 8 lanes
-            const bool pushes = on && ((e >> kCoI) & 0xFu) != 0;
-            if (__ballot(pushes)) {
-                if (pushes && s8 == 0) {
-                    const int32_t ci = grp_code(e, kCoI), cd = grp_code(e, kCoD);
-                    const uint32_t i = (e >> kEntI) & 0x3FFu;
-                    if (ci) unsafeAtomicAdd(mrow + i, (double)ci * tot);
-                    if (cd) atomicAdd(&dsum[j - i - 1], (double)cd * tot);
-                }
-            }
-            qh += n;
+            const bool use_b = main_r && lane >= 32;
+            const uint32_t rng = use_b ? mm.w : mm.z;
+            const uint32_t cur = (rng & 0xFFFFu) + (use_b ? lane - 32 : lane);
+            const bool in = (!main_r || lane < 48) && cur < (rng >> 16);
+            const size_t lb = (size_t)t * batch + row / seq;
+            return in ? (use_b ? list_b : list_a)[lb * seq + cur] : grp_none();
         };
 
-        const size_t lb = (size_t)t * batch + b;
-        const uint32_t *oa = off_a + lb * (ng + 1);
-        const uint32_t *ob = off_b + lb * (ng + 1);
-        const uint2 *la = list_a + lb * seq;
-        const uint2 *lbl = list_b + lb * seq;
-        // main role: lanes 0-31 take list A, lanes 32-63 list B, 32 a turn;
-        // Q-flip role: all lanes list A, 64 a turn
-        auto run_lists = [&](auto main_tag) {
-            constexpr bool kMain = decltype(main_tag)::value;
-            const bool use_b = kMain && lane >= 32;
-            constexpr uint32_t span = kMain ? 32u : 64u;
-            uint32_t cur = (use_b ? ob[G] : oa[G]) + (kMain ? (lane & 31) : lane);
-            const uint32_t end = use_b ? ob[G + 1] : oa[G + 1];
-            const uint2 *lst = use_b ? lbl : la;
-            for (;;) {
-                const bool in = cur < end;
-                const uint2 r = in ? lst[cur] : make_uint2(0u, 0xFFFFu);
-                const uint32_t i = r.y & 0xFFFFu;
-                const bool valid = in && i < j;
-                if (__ballot(valid) == 0) break;  // ascending i: the rest are >= j
-                uint32_t n_rd = 0, e_a = 0, e_b = 0, e_c = 0;
-                if (valid) {
-                    const uint32_t K = (r.y >> 16) & 0x3FFu;
-                    const float kd = __uint_as_float(r.x);
-                    const uint2 pr = prec[j - i - 1];
-                    const uint32_t P = rec_idx(pr) & pmask;
-                    const bool qflip = fabsf(qd) < fabsf(kd);
-                    const uint32_t iw = i << kEntI;
-                    const uint32_t lrow = ((K & gmask) << pe_dim) | P;
-                    if constexpr (!kMain) {  // Q-flip role (qm >= 0 for these items)
-                        e_a = lrow | (kCoMinus << kCoJ) | iw;
-                        n_rd = qflip ? 1u : 0u;
-                    } else {
-                        const uint32_t kmc = r.y >> 26;
-                        const int32_t km = kmc == 0xFu ? -1 : (int32_t)kmc;
-                        if (use_b) {  // a K flip of a bit >= gb into this group
-                            e_a = ((((K ^ (1u << (km & 31))) & gmask) << pe_dim) | P) | (kCoMinus << kCoI) | iw;
-                            n_rd = qflip ? 0u : 1u;
-                        } else {
-                            const int32_t pm = rec_mi(pr);
-                            const float pdl = rec_md(pr);
-                            const bool kflip = !qflip && km >= 0;
-                            const bool peflip = pe_dim > 0 && pm >= 0 && fabsf(pdl) < fabsf(qd) &&
-                                                fabsf(pdl) < fabsf(kd);
-                            const bool qs = qflip && qm >= 0;
-                            const bool low_k = kflip && (uint32_t)km < gb;
-                            e_a = lrow | ((qs ? kCoPlus : 0u) << kCoJ) | ((kflip ? kCoPlus : 0u) << kCoI) |
-                                  ((peflip ? kCoPlus : 0u) << kCoD) | iw;
-                            const uint32_t e_k = (lrow ^ (1u << ((km + pe_dim) & 31))) | (kCoMinus << kCoI) | iw;
-                            const uint32_t e_p = (lrow ^ (1u << (pm & 31))) | (kCoMinus << kCoD) | iw;
-                            e_b = low_k ? e_k : e_p;
-                            e_c = e_p;
-                            n_rd = (qs || kflip || peflip) ? 1u + (low_k ? 1u : 0u) + (peflip ? 1u : 0u) : 0u;
+        uint32_t it = fetch();
+        uint4 m = make_uint4(0u, 0u, 0u, 0u);
+        float gf[NCH][4];
+        uint2 ent = grp_none();
+        if (it < cn) ent = issue(it, m, gf);
+        while (it < cn) {
+            // wait for this item's loads before the next item's are issued: the
+            // counter then covers them alone
+#pragma unroll
+            for (int k = 0; k < NCH; k++)
+#pragma unroll
+                for (int c = 0; c < 4; c++) __asm__ volatile("" : "+v"(gf[k][c]));
+            uint32_t ex = ent.x, ey = ent.y;
+            __asm__ volatile("" : "+v"(ex), "+v"(ey));
+            ent = make_uint2(ex, ey);
+            const uint32_t nit = fetch();
+            uint4 nm = make_uint4(0u, 0u, 0u, 0u);
+            float ng_[NCH][4];
+            uint2 nent = grp_none();
+            if (nit < cn) nent = issue(nit, nm, ng_);
+
+            const bool main_role = c0 + it < n_main;
+            const uint32_t row = m.x & 0x7FFFFFFu;
+            const uint32_t b = row / seq, j = row % seq;
+            const int32_t qm = (int32_t)(m.x >> 27) - 1;
+            const float qd = __uint_as_float(m.y);
+            if (j > 0) {
+                double *mrow = macc + ((size_t)b * n_detectors + t) * seq;
+                double jacc = 0.0;
+                uint32_t qh = 0, qt = 0;
+
+                // 8 row dots from the queue (n of them live): exact fp32 products
+                // (FMA) in four fp32 chains of NCH terms per lane, the chains and
+                // the slot's 8 lanes summed in fp32 (a tree of depth 5), the dot
+                // then in fp64
+                auto step = [&](uint32_t n) {
+                    const uint32_t e = q[(qh + p) & (kGrpQueue - 1)];
+                    const bool on = p < n;
+                    const uint32_t rb = on ? (e & 0x1FFu) * kRowBytes : 0u;  // slots past n: row 0
+                    const uint8_t *t0 = tab + rb + c0l;
+                    const uint8_t *t1 = tab + rb + c1l;
+                    float f0 = 0.f, f1 = 0.f, f2 = 0.f, f3 = 0.f;
+#pragma unroll
+                    for (int k = 0; k < NCH; k++) {
+                        const f32x4 v = (k & 1) ? *reinterpret_cast<const f32x4 *>(t1 + (k - 1) * 128)
+                                                : *reinterpret_cast<const f32x4 *>(t0 + k * 128);
+                        f0 = fmaf(v[0], gf[k][0], f0);
+                        f1 = fmaf(v[1], gf[k][1], f1);
+                        f2 = fmaf(v[2], gf[k][2], f2);
+                        f3 = fmaf(v[3], gf[k][3], f3);
+                    }
+                    const float part = on ? (f0 + f1) + (f2 + f3) : 0.f;
+                    const double tot = (double)grp_sum8f(part);
+                    jacc += (double)grp_code(e, kCoJ) * tot;  // the same in the group's 8 lanes
+                    const bool pushes = on && ((e >> kCoI) & 0xFu) != 0;
+                    if (__ballot(pushes)) {
+                        if (pushes && s8 == 0) {
+                            const int32_t ci = grp_code(e, kCoI), cd = grp_code(e, kCoD);
+                            const uint32_t i = (e >> kEntI) & 0x3FFu;
+                            if (ci) unsafeAtomicAdd(mrow + i, (double)ci * tot);
+                            if (cd) atomicAdd(&dsum[j - i - 1], (double)cd * tot);
                         }
                     }
-                }
-                const uint64_t b1 = __ballot(n_rd >= 1);
-                const uint64_t b2 = kMain ? __ballot(n_rd >= 2) : 0ull;
-                const uint64_t b3 = kMain ? __ballot(n_rd >= 3) : 0ull;
-                const uint32_t pos = qt + __popcll(b1 & below) + __popcll(b2 & below) + __popcll(b3 & below);
-                if (n_rd >= 1) q[pos & (kGrpQueue - 1)] = e_a;
-                if (kMain && n_rd >= 2) q[(pos + 1) & (kGrpQueue - 1)] = e_b;
-                if (kMain && n_rd >= 3) q[(pos + 2) & (kGrpQueue - 1)] = e_c;
-                qt += __popcll(b1) + __popcll(b2) + __popcll(b3);
-                cur += span;
+                    qh += n;
+                };
+
+                const size_t lb = (size_t)t * batch + b;
+                auto run_lists = [&](auto main_tag) {
+                    constexpr bool kMain = decltype(main_tag)::value;
+                    const bool use_b = kMain && lane >= 32;
+                    const bool lane_on = !kMain || lane < 48;
+                    const uint32_t span = kMain ? (use_b ? 16u : 32u) : 64u;
+                    const uint32_t rng = use_b ? m.w : m.z;
+                    uint32_t cur = (rng & 0xFFFFu) + (use_b ? lane - 32 : lane);
+                    const uint32_t end = rng >> 16;
+                    const uint2 *lst = (use_b ? list_b : list_a) + lb * seq;
+                    uint2 r = ent;  // the first candidate, loaded with the item
+                    for (;;) {
+                        const uint32_t i = r.y & 0xFFFFu;
+                        const bool valid = i < j;  // slots past a list's end carry i = 0xFFFF
+                        if (__ballot(valid) == 0) break;  // ascending i: the rest are >= j
+                        uint32_t n_rd = 0, e_a = 0, e_b = 0, e_c = 0;
+                        if (valid) {
+                            const uint32_t K = (r.y >> 16) & 0x3FFu;
+                            const float kd = __uint_as_float(r.x);
+                            const uint2 pr = prec[j - i - 1];
+                            const uint32_t P = rec_idx(pr) & pmask;
+                            const bool qflip = fabsf(qd) < fabsf(kd);
+                            const uint32_t iw = i << kEntI;
+                            const uint32_t lrow = ((K & gmask) << pe_dim) | P;
+                            if constexpr (!kMain) {  // Q-flip role (qm >= 0 for these items)
+                                e_a = lrow | (kCoMinus << kCoJ) | iw;
+                                n_rd = qflip ? 1u : 0u;
+                            } else {
+                                const uint32_t kmc = r.y >> 26;
+                                const int32_t km = kmc == 0xFu ? -1 : (int32_t)kmc;
+                                if (use_b) {  // a K flip of a bit >= gb into this group
+                                    e_a = ((((K ^ (1u << (km & 31))) & gmask) << pe_dim) | P) | (kCoMinus << kCoI) | iw;
+                                    n_rd = qflip ? 0u : 1u;
+                                } else {
+                                    const int32_t pm = rec_mi(pr);
+                                    const float pdl = rec_md(pr);
+                                    const bool kflip = !qflip && km >= 0;
+                                    const bool peflip = pe_dim > 0 && pm >= 0 && fabsf(pdl) < fabsf(qd) &&
+                                                        fabsf(pdl) < fabsf(kd);
+                                    const bool qs = qflip && qm >= 0;
+                                    const bool low_k = kflip && (uint32_t)km < gb;
+                                    e_a = lrow | ((qs ? kCoPlus : 0u) << kCoJ) | ((kflip ? kCoPlus : 0u) << kCoI) |
+                                          ((peflip ? kCoPlus : 0u) << kCoD) | iw;
+                                    const uint32_t e_k = (lrow ^ (1u << ((km + pe_dim) & 31))) | (kCoMinus << kCoI) | iw;
+                                    const uint32_t e_p = (lrow ^ (1u << (pm & 31))) | (kCoMinus << kCoD) | iw;
+                                    e_b = low_k ? e_k : e_p;
+                                    e_c = e_p;
+                                    n_rd = (qs || kflip || peflip) ? 1u + (low_k ? 1u : 0u) + (peflip ? 1u : 0u) : 0u;
+                                }
+                            }
+                        }
+                        const uint64_t b1 = __ballot(n_rd >= 1);
+                        const uint64_t b2 = kMain ? __ballot(n_rd >= 2) : 0ull;
+                        const uint64_t b3 = kMain ? __ballot(n_rd >= 3) : 0ull;
+                        const uint32_t pos = qt + __popcll(b1 & below) + __popcll(b2 & below) + __popcll(b3 & below);
+                        if (n_rd >= 1) q[pos & (kGrpQueue - 1)] = e_a;
+                        if (kMain && n_rd >= 2) q[(pos + 1) & (kGrpQueue - 1)] = e_b;
+                        if (kMain && n_rd >= 3) q[(pos + 2) & (kGrpQueue - 1)] = e_c;
+                        qt += __popcll(b1) + __popcll(b2) + __popcll(b3);
+                        cur += span;
+                        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                        __builtin_amdgcn_wave_barrier();
+                        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                        while (qt - qh >= 8) step(8);
+                        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                        __builtin_amdgcn_wave_barrier();
+                        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                        // lists longer than a turn: wait for the reload here, so the loop
+                        // head holds no wait that would cover the next item's loads
+                        r = (lane_on && cur < end) ? lst[cur] : grp_none();
+                        uint32_t rx = r.x, ry = r.y;
+                        __asm__ volatile("" : "+v"(rx), "+v"(ry));
+                        r = make_uint2(rx, ry);
+                    }
+                };
+                if (main_role)
+                    run_lists(std::integral_constant<bool, true>());
+                else
+                    run_lists(std::integral_constant<bool, false>());
+                if (qt != qh) step(qt - qh);
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_wave_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-                while (qt - qh >= 8) step(8);
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            }
-        };
-        if (main_role)
-            run_lists(std::integral_constant<bool, true>());
-        else
-            run_lists(std::integral_constant<bool, false>());
-        if (qt != qh) step(qt - qh);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // the item's own total: one value per slot group, over the wavefront
+                // the item's own total: one value per slot group, over the wavefront
 #pragma unroll
-        for (int o = 8; o < kWave; o <<= 1) jacc += __shfl_xor(jacc, o, kWave);
-        if (lane == 0 && jacc != 0.0) unsafeAtomicAdd(mrow + j, jacc);
+                for (int o = 8; o < kWave; o <<= 1) jacc += __shfl_xor(jacc, o, kWave);
+                if (lane == 0) jtot[it] = jacc;  // flushed with the chunk: no atomic before the next item's wait
+            }
+            it = nit;
+            m = nm;
+            ent = nent;
+#pragma unroll
+            for (int k = 0; k < NCH; k++)
+#pragma unroll
+                for (int c = 0; c < 4; c++) gf[k][c] = ng_[k][c];
+        }
+        __syncthreads();
+        // the chunk's item totals
+        for (uint32_t k = tid; k < cn; k += kGrpThreads) {
+            const double v = jtot[k];
+            if (v != 0.0) {
+                const uint32_t row = meta[k].x & 0x7FFFFFFu;
+                unsafeAtomicAdd(macc + ((size_t)(row / seq) * n_detectors + t) * seq + row % seq, v);
+            }
+        }
     }
     __syncthreads();
     // distance sums, scaled by du of the distance's positional margin
