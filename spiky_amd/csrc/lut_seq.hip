@@ -1484,6 +1484,7 @@ constexpr int kSeqWgKeys = 8192;         // K indices of up to 8192 (b, s) rows 
 constexpr int kSeqWgPe = 1024;
 constexpr int kSeqWgItems = 256;         // u8 entries: at most 256 items a batch
 constexpr int kQuadStep = 4;             // entries a turn of the 16-byte row loop (2: +6%, 8: +9%)
+constexpr int kSeqWgClasses = 64;        // row length classes (turns of kQuadStep entries, the last open)
 
 template <bool INT_MODE, bool OVERWRITE>
 __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
@@ -1500,6 +1501,7 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
     __shared__ uint16_t ptab[kSeqWgPe];
     __shared__ uint32_t bitems[kSeqWgItems];  // row ids of the batch's items
     __shared__ uint32_t wsum[kSeqWgThreads / kWave];
+    __shared__ uint32_t lhist[kSeqWgClasses];  // rows per length class (quad path)
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & (kWave - 1);
     const uint32_t wave = tid / kWave;
@@ -1579,7 +1581,46 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
                     ent[atomicAdd(&cur[row], 1u)] = (uint8_t)it;  // the item's gv row is it * cols
                 }
             }
-            // cur[row] is now the end of the row's bucket, cur - cnt its start
+            // cur[row] is now the end of the row's bucket, cur - cnt its start.
+            // The quad path walks rows four to a wavefront, one to each 16-lane
+            // group; rows of equal length (in turns) go together, so the groups
+            // of a wavefront reach their rows' ends on the same turn.  The order
+            // (longest class first) goes into the high half of cnt: cnt[k] >> 16
+            // is the k-th row of the walk, cnt[k] & 0xFFFF row k's count.
+            if (quad) {
+                __syncthreads();
+                for (uint32_t c = tid; c < (uint32_t)kSeqWgClasses; c += kSeqWgThreads) lhist[c] = 0u;
+                __syncthreads();
+                auto row_class = [&](uint32_t r) -> uint32_t {
+                    const uint32_t turns = (cnt[r] + kQuadStep - 1) / kQuadStep;
+                    return (uint32_t)kSeqWgClasses - 1u - min(turns, (uint32_t)kSeqWgClasses - 1u);
+                };
+                for (uint32_t r = tid; r < sub_rows; r += kSeqWgThreads) atomicAdd(&lhist[row_class(r)], 1u);
+                __syncthreads();
+                if (wave == 0) {
+                    const uint32_t v = lane < (uint32_t)kSeqWgClasses ? lhist[lane] : 0u;
+                    uint32_t incl = v;
+#pragma unroll
+                    for (int o = 1; o < kWave; o <<= 1) {
+                        const uint32_t y = __shfl_up(incl, o, kWave);
+                        if ((int)lane >= o) incl += y;
+                    }
+                    if (lane < (uint32_t)kSeqWgClasses) lhist[lane] = incl - v;
+                }
+                __syncthreads();
+                uint32_t rowc[kSeqWgRowsMax / kSeqWgThreads];
+#pragma unroll
+                for (int u = 0; u < kSeqWgRowsMax / kSeqWgThreads; u++) {
+                    const uint32_t r = u * kSeqWgThreads + tid;
+                    rowc[u] = r < sub_rows ? atomicAdd(&lhist[row_class(r)], 1u) : 0u;
+                }
+                __syncthreads();  // every class read before the high halves are written
+#pragma unroll
+                for (int u = 0; u < kSeqWgRowsMax / kSeqWgThreads; u++) {
+                    const uint32_t r = u * kSeqWgThreads + tid;
+                    if (r < sub_rows) atomicOr(&cnt[rowc[u]], r << 16);
+                }
+            }
             for (uint32_t sl = 0; sl < n_slices; sl++) {
                 const uint32_t col0 = sl * cols;
                 __syncthreads();  // scatter done / the previous slice is done with gv
@@ -1602,7 +1643,7 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
                     uint32_t lo = 0, hi = sub_rows;  // first row r with start(r) >= tgt
                     while (lo < hi) {
                         const uint32_t mid = (lo + hi) / 2;
-                        if (cur[mid] - cnt[mid] < tgt) lo = mid + 1; else hi = mid;
+                        if (cur[mid] - (cnt[mid] & 0xFFFFu) < tgt) lo = mid + 1; else hi = mid;
                     }
                     return gi == 0 ? 0u : lo;
                 };
@@ -1610,64 +1651,51 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
                 const bool store = first && OVERWRITE;
                 if (quad) {
                     // 64-column slices, lane k of a group holding columns 4k .. 4k+3:
-                    // one 16-byte LDS read per entry.  The group walks its rows in
-                    // one loop: each turn adds kQuadStep entries of the current row
-                    // (entries past its end read the zero row, adding +0, which
-                    // leaves a sum that starts at +0 unchanged), and the row's last
-                    // turn -- the only turn of a row without entries -- also writes
-                    // it and moves on.
+                    // one 16-byte LDS read per entry.  Wavefront w takes the rows at
+                    // walk positions 4 (w + 16 m) .. + 3, one per group, and adds
+                    // kQuadStep entries a turn (entries past a row's end read the
+                    // zero row, adding +0, which leaves a sum that starts at +0
+                    // unchanged); the group then writes its row.
                     const uint32_t c4 = (tid & 15u) * 4u;
                     const uint32_t cq = col0 + c4;
-                    uint32_t row = rs, e = 0, e1 = 0;
-                    if (row < re) {
-                        e1 = cur[row];
-                        e = e1 - cnt[row];
-                    }
-                    bool touched = e < e1;
-                    float af[4] = {0.f, 0.f, 0.f, 0.f};
-                    uint32_t ai[4] = {0u, 0u, 0u, 0u};
-                    while (row < re) {
-                        u32x4 g[kQuadStep];
+                    const uint32_t gw = (tid >> 4) & 3u;
+                    for (uint32_t k4 = wave * 4u; k4 < sub_rows; k4 += kSeqWgThreads / 16u) {
+                        const uint32_t pos = k4 + gw;
+                        const bool have = pos < sub_rows;
+                        const uint32_t row = have ? cnt[pos] >> 16 : 0u;
+                        const uint32_t n = have ? cnt[row] & 0xFFFFu : 0u;
+                        const uint32_t e1 = have ? cur[row] : 0u;
+                        float af[4] = {0.f, 0.f, 0.f, 0.f};
+                        uint32_t ai[4] = {0u, 0u, 0u, 0u};
+                        for (uint32_t e = e1 - n; e < e1; e += kQuadStep) {
+                            u32x4 g[kQuadStep];
 #pragma unroll
-                        for (int u = 0; u < kQuadStep; u++) {
-                            const uint32_t it = e + u < e1 ? (uint32_t)ent[e + u] : nb;
-                            g[u] = *reinterpret_cast<const u32x4 *>(gv + it * 64u + c4);
-                        }
-#pragma unroll
-                        for (int u = 0; u < kQuadStep; u++)
-#pragma unroll
-                            for (int c = 0; c < 4; c++) {
-                                if (INT_MODE) ai[c] += g[u][c];
-                                else af[c] += __uint_as_float(g[u][c]);
+                            for (int u = 0; u < kQuadStep; u++) {
+                                const uint32_t it = e + u < e1 ? (uint32_t)ent[e + u] : nb;
+                                g[u] = *reinterpret_cast<const u32x4 *>(gv + it * 64u + c4);
                             }
-                        e += kQuadStep;
-                        if (e >= e1) {
-                            // the row's last turn: write it and move on
-                            if ((store || touched) && cq < n_outputs) {
-                                u32x4 *p = reinterpret_cast<u32x4 *>(dst + (size_t)row * n_outputs + cq);
-                                u32x4 o;
-                                if (store) {
 #pragma unroll
-                                    for (int c = 0; c < 4; c++) o[c] = INT_MODE ? ai[c] : __float_as_uint(af[c]);
-                                } else {
-                                    const u32x4 old = *p;
+                            for (int u = 0; u < kQuadStep; u++)
 #pragma unroll
-                                    for (int c = 0; c < 4; c++)
-                                        o[c] = INT_MODE ? (uint32_t)wrap_add((int32_t)ai[c], (int32_t)old[c])
-                                                        : __float_as_uint(__uint_as_float(old[c]) + af[c]);
+                                for (int c = 0; c < 4; c++) {
+                                    if (INT_MODE) ai[c] += g[u][c];
+                                    else af[c] += __uint_as_float(g[u][c]);
                                 }
-                                *p = o;
-                            }
+                        }
+                        if (have && (store || n > 0) && cq < n_outputs) {
+                            u32x4 *p = reinterpret_cast<u32x4 *>(dst + (size_t)row * n_outputs + cq);
+                            u32x4 o;
+                            if (store) {
 #pragma unroll
-                            for (int c = 0; c < 4; c++) {
-                                af[c] = 0.f;
-                                ai[c] = 0u;
+                                for (int c = 0; c < 4; c++) o[c] = INT_MODE ? ai[c] : __float_as_uint(af[c]);
+                            } else {
+                                const u32x4 old = *p;
+#pragma unroll
+                                for (int c = 0; c < 4; c++)
+                                    o[c] = INT_MODE ? (uint32_t)wrap_add((int32_t)ai[c], (int32_t)old[c])
+                                                    : __float_as_uint(__uint_as_float(old[c]) + af[c]);
                             }
-                            if (++row < re) {
-                                e1 = cur[row];
-                                e = e1 - cnt[row];
-                                touched = e < e1;
-                            }
+                            *p = o;
                         }
                     }
                     continue;
