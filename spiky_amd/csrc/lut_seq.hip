@@ -1483,7 +1483,7 @@ constexpr int kSeqWgGvWords = 15360;     // batch gradient rows (items x C)
 constexpr int kSeqWgKeys = 8192;         // K indices of up to 8192 (b, s) rows at a time
 constexpr int kSeqWgPe = 1024;
 constexpr int kSeqWgItems = 256;         // u8 entries: at most 256 items a batch
-constexpr int kQuadStep = 4;             // entries a turn of the 16-byte row loop (2: +6%, 8: +9%)
+constexpr int kQuadStep = 2;             // entries a turn of the 16-byte row loop (4: +5%, 8: +7%)
 constexpr int kSeqWgClasses = 64;        // row length classes (turns of kQuadStep entries, the last open)
 
 template <bool INT_MODE, bool OVERWRITE>
