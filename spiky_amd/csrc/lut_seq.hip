@@ -45,6 +45,13 @@ constexpr int kBlock = 256;
 constexpr int kWPB = kBlock / kWave;
 
 __device__ __forceinline__ uint32_t uniform(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+// lane l's value of v (a scalar read, the same in every lane)
+__device__ __forceinline__ double readlane_f64(double v, int l) {
+    const uint64_t u = (uint64_t)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l);
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
 
 __device__ __forceinline__ int32_t wrap_add(int32_t a, int32_t b) {
     return (int32_t)((uint32_t)a + (uint32_t)b);
@@ -1026,6 +1033,14 @@ __device__ __forceinline__ float grp_sum8f(float v) {
     return v;
 }
 
+// A wavefront's item in the grouped pass: its number in the chunk, its metadata and the
+// first candidate of its lists.
+struct GrpItem {
+    uint32_t it;
+    uint4 m;
+    uint2 ent;
+};
+
 template <int NCH>
 __global__ __launch_bounds__(kGrpThreads) void k_propagate_seq_grp(
     const float *__restrict__ w, const float *__restrict__ g, const uint2 *__restrict__ pack,
@@ -1115,7 +1130,7 @@ __global__ __launch_bounds__(kGrpThreads) void k_propagate_seq_grp(
         auto fetch = [&]() -> uint32_t {
             uint32_t v = 0;
             if (lane == 0) v = atomicAdd(&next_item, 1u);
-            return uniform(__shfl(v, 0, kWave));
+            return uniform(v);  // lane 0 is the first active lane here
         };
         // an item's loads: g[b][j] in this lane's chunk order and the first
         // candidate of its lists (main role: lanes 0-31 list A, 32-47 list B;
@@ -1141,26 +1156,25 @@ __global__ __launch_bounds__(kGrpThreads) void k_propagate_seq_grp(
             return in ? (use_b ? list_b : list_a)[lb * seq + cur] : grp_none();
         };
 
-        uint32_t it = fetch();
-        uint4 m = make_uint4(0u, 0u, 0u, 0u);
-        float gf[NCH][4];
-        uint2 ent = grp_none();
-        if (it < cn) ent = issue(it, m, gf);
-        while (it < cn) {
+        // One visit: item cur with its g in gf; the next item's loads go to gn.  The
+        // loop alternates the two register sets, so no copy moves g between them.
+        auto visit = [&](const GrpItem cur, float (&gf)[NCH][4], float (&gn)[NCH][4]) -> GrpItem {
+            const uint32_t it = cur.it;
+            const uint4 m = cur.m;
             // wait for this item's loads before the next item's are issued: the
             // counter then covers them alone
 #pragma unroll
             for (int k = 0; k < NCH; k++)
 #pragma unroll
                 for (int c = 0; c < 4; c++) __asm__ volatile("" : "+v"(gf[k][c]));
-            uint32_t ex = ent.x, ey = ent.y;
+            uint32_t ex = cur.ent.x, ey = cur.ent.y;
             __asm__ volatile("" : "+v"(ex), "+v"(ey));
-            ent = make_uint2(ex, ey);
-            const uint32_t nit = fetch();
-            uint4 nm = make_uint4(0u, 0u, 0u, 0u);
-            float ng_[NCH][4];
-            uint2 nent = grp_none();
-            if (nit < cn) nent = issue(nit, nm, ng_);
+            const uint2 ent = make_uint2(ex, ey);
+            GrpItem nx;
+            nx.it = fetch();
+            nx.m = make_uint4(0u, 0u, 0u, 0u);
+            nx.ent = grp_none();
+            if (nx.it < cn) nx.ent = issue(nx.it, nx.m, gn);
 
             const bool main_role = c0 + it < n_main;
             const uint32_t row = m.x & 0x7FFFFFFu;
@@ -1290,18 +1304,26 @@ __global__ __launch_bounds__(kGrpThreads) void k_propagate_seq_grp(
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_wave_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-                // the item's own total: one value per slot group, over the wavefront
-#pragma unroll
-                for (int o = 8; o < kWave; o <<= 1) jacc += __shfl_xor(jacc, o, kWave);
-                if (lane == 0) jtot[it] = jacc;  // flushed with the chunk: no atomic before the next item's wait
+                // the item's own total: one value per slot group (its 8 lanes agree), summed
+                // over the groups by a row rotation and four lane reads (no LDS round trip)
+                const double pair = jacc + dpp_f64<0x128>(jacc);  // row_ror:8, the row's other group
+                const double jsum = (readlane_f64(pair, 0) + readlane_f64(pair, 16)) +
+                                    (readlane_f64(pair, 32) + readlane_f64(pair, 48));
+                if (lane == 0) jtot[it] = jsum;  // flushed with the chunk: no atomic before the next item's wait
             }
-            it = nit;
-            m = nm;
-            ent = nent;
-#pragma unroll
-            for (int k = 0; k < NCH; k++)
-#pragma unroll
-                for (int c = 0; c < 4; c++) gf[k][c] = ng_[k][c];
+            return nx;
+        };
+
+        float gr0[NCH][4], gr1[NCH][4];
+        GrpItem cur;
+        cur.it = fetch();
+        cur.m = make_uint4(0u, 0u, 0u, 0u);
+        cur.ent = grp_none();
+        if (cur.it < cn) cur.ent = issue(cur.it, cur.m, gr0);
+        while (cur.it < cn) {
+            cur = visit(cur, gr0, gr1);
+            if (cur.it >= cn) break;
+            cur = visit(cur, gr1, gr0);
         }
         __syncthreads();
         // the chunk's item totals
