@@ -946,15 +946,18 @@ __global__ __launch_bounds__(kBlock) void k_seq_tri_reduce(
 //   Q-flip role, the items with Q_j ^ bit = Q: for each earlier i in the group
 //     with a Q flip, the Q-flipped row (-> j, negated).
 // Positions come from per-(t, b) lists sorted by group (k_seq_group_lists).
-// A wavefront takes one item at a time with g[b][j] in registers (fp64),
-// turns 32 candidate positions a turn into row dots (a ballot compaction into
-// a per-wave LDS queue) and computes 8 dots at a time, 8 lanes a dot: lane s
-// of dot slot p reads 16 bytes of each 128-byte chunk, chunks taken in the
-// order (k + p) mod NCH so two slots that share a 16-lane LDS cycle read
-// opposite bank halves.  Dots are fp64 sums of exact fp32 products; the
-// contributions to j are summed in registers over the item, those to i go to
-// M[b][t][i] with fp64 atomics and those to d to an LDS sum per distance,
-// flushed (times du of the distance's positional margin) into dpe once.
+// A wavefront takes one item at a time with g[b][j] in registers (fp32, the
+// next item's prefetched into a second set), turns 32 + 16 candidate positions
+// a turn (main role; 64 in the Q-flip role) into row dots (a ballot compaction
+// into a per-wave LDS queue) and computes 8 dots at a time, 8 lanes a dot: lane
+// s of dot slot p reads 16 bytes of each 128-byte chunk, chunks taken in the
+// order k ^ (p & 1) so two slots that share a 16-lane LDS cycle read opposite
+// bank halves.  Dots are exact fp32 products in fp32 chains and an fp32 tree,
+// then fp64; the contributions to j are summed in registers over the item,
+// those to i in LDS per candidate (then one fp64 atomic into M[b][t][i] per
+// candidate, issued after the next item's loads) and those to d in an LDS sum
+// per distance, flushed (times du of the distance's positional margin) into dpe
+// once.
 // Position s then takes du(minDelta_s) * M[b][t][s] (k_seq_xgrad), the same
 // total the pair triangles gave: qsum_main - qsum_alt + the K-flip column sum.
 typedef __attribute__((address_space(3))) void lds_void;
@@ -964,7 +967,7 @@ constexpr int kGrpWaves = kGrpThreads / kWave;
 constexpr int kGrpTabBytes = 128 * 1024;
 constexpr int kGrpMaxDist = 512;   // S - 1
 constexpr int kGrpQueue = 128;     // row-dot entries a wave holds (power of two)
-constexpr int kGrpMeta = 640;      // items whose metadata a workgroup stages at a time
+constexpr int kGrpMeta = 320;      // items whose metadata a workgroup stages at a time
 
 // Lists of one (t, b): positions of the sequence whose K is in group G
 // (list A) and positions whose K flips into group G by a bit >= gb (list B),
@@ -1012,11 +1015,16 @@ __global__ __launch_bounds__(kWave) void k_seq_group_lists(
     }
 }
 
-// Queue entry (4 bytes): LDS row (9 bits) | cj << 9 | ci << 11 | cd << 13 |
-// i << 15, where cj, ci, cd are signed 2-bit coefficients (01 = +1, 11 = -1)
-// of the dot's share in position j, position i and distance d = j - i - 1.
+// Queue entry (4 bytes): cj | ci << 2 | cd << 4 | (l & 3) << 6 | the row's LDS
+// byte offset (bits 8-16: rows of 256 bytes or more in 128 KiB) | d << 17 |
+// (l >> 2) << 27, where cj, ci, cd are signed 2-bit coefficients (01 = +1,
+// 11 = -1) of the dot's share in position j, position i and distance
+// d = j - i - 1, and l is the lane that holds candidate i in its turn.
 constexpr uint32_t kCoPlus = 1, kCoMinus = 3;
-constexpr int kCoJ = 9, kCoI = 11, kCoD = 13, kEntI = 15;
+constexpr int kCoJ = 0, kCoI = 2, kCoD = 4, kEntD = 17;
+constexpr uint32_t kEntRow = 0x1FF00u;
+__device__ __forceinline__ uint32_t grp_lane_bits(uint32_t l) { return ((l & 3u) << 6) | ((l >> 2) << 27); }
+__device__ __forceinline__ uint32_t grp_lane(uint32_t e) { return ((e >> 6) & 3u) | ((e >> 25) & 0x3Cu); }
 
 __device__ __forceinline__ int32_t grp_code(uint32_t e, int at) {
     return __builtin_amdgcn_sbfe((int32_t)e, at, 2);
@@ -1059,6 +1067,7 @@ __global__ __launch_bounds__(kGrpThreads) void k_propagate_seq_grp(
     __shared__ uint32_t queue[kGrpWaves][kGrpQueue];
     __shared__ uint4 meta[kGrpMeta];
     __shared__ double jtot[kGrpMeta];  // the staged items' own totals
+    __shared__ double cacc[kGrpWaves][kWave];  // a turn's position-i sums, one per candidate lane
     __shared__ uint32_t next_item;
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & (kWave - 1);
@@ -1098,6 +1107,24 @@ __global__ __launch_bounds__(kGrpThreads) void k_propagate_seq_grp(
     const uint32_t pmask = (1u << pe_dim) - 1, gmask = (1u << gb) - 1;
     const uint64_t below = (1ull << lane) - 1;
     uint32_t *q = queue[wave];
+    for (uint32_t k = lane; k < kGrpQueue; k += kWave) q[k] = 0;  // a slot past n reads a valid row
+    // Position-i shares are summed in LDS per candidate lane (cacc) while a turn
+    // runs, then go to M[b][t][i] with one fp64 atomic per lane.  The last turn's
+    // sums of an item are flushed at the next item, after its loads are issued:
+    // the next wait for loads then finds these atomics long done (the counter it
+    // waits on covers atomics too).
+    double *const ca = cacc[wave];
+    ca[lane] = 0.0;
+    size_t fl_base = 0;    // M[b][t][0] of the sums in cacc
+    uint32_t fl_i = 0;     // this lane's candidate position of those sums
+    bool fl_pend = false;  // cacc holds an item's last turn, not yet flushed
+    auto flush = [&]() {
+        const double v = ca[lane];
+        if (v != 0.0) {
+            unsafeAtomicAdd(macc + fl_base + fl_i, v);
+            ca[lane] = 0.0;
+        }
+    };
     // Slot p reads chunk k ^ (p & 1) at turn k, so slots p and p ^ 1 (one
     // 16-lane LDS cycle) read opposite bank halves: even turns from base0 + 128 k,
     // odd turns from base1 + 128 (k - 1) (immediate offsets).  g is held the same way.
@@ -1175,6 +1202,10 @@ __global__ __launch_bounds__(kGrpThreads) void k_propagate_seq_grp(
             nx.m = make_uint4(0u, 0u, 0u, 0u);
             nx.ent = grp_none();
             if (nx.it < cn) nx.ent = issue(nx.it, nx.m, gn);
+            if (fl_pend) {  // the previous item's last turn
+                flush();
+                fl_pend = false;
+            }
 
             const bool main_role = c0 + it < n_main;
             const uint32_t row = m.x & 0x7FFFFFFu;
@@ -1182,20 +1213,21 @@ __global__ __launch_bounds__(kGrpThreads) void k_propagate_seq_grp(
             const int32_t qm = (int32_t)(m.x >> 27) - 1;
             const float qd = __uint_as_float(m.y);
             if (j > 0) {
-                double *mrow = macc + ((size_t)b * n_detectors + t) * seq;
+                const size_t mbase = ((size_t)b * n_detectors + t) * seq;
                 double jacc = 0.0;
                 uint32_t qh = 0, qt = 0;
 
                 // 8 row dots from the queue (n of them live): exact fp32 products
                 // (FMA) in four fp32 chains of NCH terms per lane, the chains and
                 // the slot's 8 lanes summed in fp32 (a tree of depth 5), the dot
-                // then in fp64
-                auto step = [&](uint32_t n) {
+                // then in fp64.  Slots past n read a stale entry's row (the ring
+                // starts zeroed) and add nothing.
+                auto step = [&](uint32_t n, auto main_tag) {
+                    constexpr bool kMain = decltype(main_tag)::value;
                     const uint32_t e = q[(qh + p) & (kGrpQueue - 1)];
                     const bool on = p < n;
-                    const uint32_t rb = on ? (e & 0x1FFu) * kRowBytes : 0u;  // slots past n: row 0
-                    const uint8_t *t0 = tab + rb + c0l;
-                    const uint8_t *t1 = tab + rb + c1l;
+                    const uint8_t *t0 = tab + ((e & kEntRow) | c0l);
+                    const uint8_t *t1 = tab + ((e & kEntRow) | c1l);
                     float f0 = 0.f, f1 = 0.f, f2 = 0.f, f3 = 0.f;
 #pragma unroll
                     for (int k = 0; k < NCH; k++) {
@@ -1208,14 +1240,17 @@ __global__ __launch_bounds__(kGrpThreads) void k_propagate_seq_grp(
                     }
                     const float part = on ? (f0 + f1) + (f2 + f3) : 0.f;
                     const double tot = (double)grp_sum8f(part);
-                    jacc += (double)grp_code(e, kCoJ) * tot;  // the same in the group's 8 lanes
-                    const bool pushes = on && ((e >> kCoI) & 0xFu) != 0;
-                    if (__ballot(pushes)) {
-                        if (pushes && s8 == 0) {
-                            const int32_t ci = grp_code(e, kCoI), cd = grp_code(e, kCoD);
-                            const uint32_t i = (e >> kEntI) & 0x3FFu;
-                            if (ci) unsafeAtomicAdd(mrow + i, (double)ci * tot);
-                            if (cd) atomicAdd(&dsum[j - i - 1], (double)cd * tot);
+                    if constexpr (!kMain) {
+                        jacc -= tot;  // Q-flip entries: cj = -1, no other share
+                    } else {
+                        jacc += (double)grp_code(e, kCoJ) * tot;  // the same in the group's 8 lanes
+                        const bool pushes = on && (e & (0xFu << kCoI)) != 0;
+                        if (__builtin_amdgcn_ballot_w64(pushes)) {
+                            if (pushes && s8 == 0) {
+                                const int32_t ci = grp_code(e, kCoI), cd = grp_code(e, kCoD);
+                                if (ci) atomicAdd(&ca[grp_lane(e)], (double)ci * tot);
+                                if (cd) atomicAdd(&dsum[(e >> kEntD) & 0x3FFu], (double)cd * tot);
+                            }
                         }
                     }
                     qh += n;
@@ -1243,8 +1278,8 @@ __global__ __launch_bounds__(kGrpThreads) void k_propagate_seq_grp(
                             const uint2 pr = prec[j - i - 1];
                             const uint32_t P = rec_idx(pr) & pmask;
                             const bool qflip = fabsf(qd) < fabsf(kd);
-                            const uint32_t iw = i << kEntI;
-                            const uint32_t lrow = ((K & gmask) << pe_dim) | P;
+                            const uint32_t iw = ((j - i - 1) << kEntD) | grp_lane_bits(lane);
+                            const uint32_t lrow = (((K & gmask) << pe_dim) | P) * kRowBytes;
                             if constexpr (!kMain) {  // Q-flip role (qm >= 0 for these items)
                                 e_a = lrow | (kCoMinus << kCoJ) | iw;
                                 n_rd = qflip ? 1u : 0u;
@@ -1252,7 +1287,7 @@ __global__ __launch_bounds__(kGrpThreads) void k_propagate_seq_grp(
                                 const uint32_t kmc = r.y >> 26;
                                 const int32_t km = kmc == 0xFu ? -1 : (int32_t)kmc;
                                 if (use_b) {  // a K flip of a bit >= gb into this group
-                                    e_a = ((((K ^ (1u << (km & 31))) & gmask) << pe_dim) | P) | (kCoMinus << kCoI) | iw;
+                                    e_a = (((((K ^ (1u << (km & 31))) & gmask) << pe_dim) | P) * kRowBytes) | (kCoMinus << kCoI) | iw;
                                     n_rd = qflip ? 0u : 1u;
                                 } else {
                                     const int32_t pm = rec_mi(pr);
@@ -1264,8 +1299,8 @@ __global__ __launch_bounds__(kGrpThreads) void k_propagate_seq_grp(
                                     const bool low_k = kflip && (uint32_t)km < gb;
                                     e_a = lrow | ((qs ? kCoPlus : 0u) << kCoJ) | ((kflip ? kCoPlus : 0u) << kCoI) |
                                           ((peflip ? kCoPlus : 0u) << kCoD) | iw;
-                                    const uint32_t e_k = (lrow ^ (1u << ((km + pe_dim) & 31))) | (kCoMinus << kCoI) | iw;
-                                    const uint32_t e_p = (lrow ^ (1u << (pm & 31))) | (kCoMinus << kCoD) | iw;
+                                    const uint32_t e_k = (lrow ^ (kRowBytes << ((km + pe_dim) & 31))) | (kCoMinus << kCoI) | iw;
+                                    const uint32_t e_p = (lrow ^ (kRowBytes << (pm & 31))) | (kCoMinus << kCoD) | iw;
                                     e_b = low_k ? e_k : e_p;
                                     e_c = e_p;
                                     n_rd = (qs || kflip || peflip) ? 1u + (low_k ? 1u : 0u) + (peflip ? 1u : 0u) : 0u;
@@ -1284,10 +1319,22 @@ __global__ __launch_bounds__(kGrpThreads) void k_propagate_seq_grp(
                         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                         __builtin_amdgcn_wave_barrier();
                         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-                        while (qt - qh >= 8) step(8);
+                        while (qt - qh >= 8) step(8, main_tag);
                         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                         __builtin_amdgcn_wave_barrier();
                         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                        if constexpr (kMain) {
+                            fl_i = i;  // cacc[lane] sums this turn's candidate
+                            if (__builtin_amdgcn_ballot_w64(lane_on && cur < end)) {
+                                // another turn follows: finish this one and flush its sums
+                                while (qt != qh) step(min(8u, qt - qh), main_tag);
+                                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                                __builtin_amdgcn_wave_barrier();
+                                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                                fl_base = mbase;
+                                flush();
+                            }
+                        }
                         // lists longer than a turn: wait for the reload here, so the loop
                         // head holds no wait that would cover the next item's loads
                         r = (lane_on && cur < end) ? lst[cur] : grp_none();
@@ -1295,12 +1342,16 @@ __global__ __launch_bounds__(kGrpThreads) void k_propagate_seq_grp(
                         __asm__ volatile("" : "+v"(rx), "+v"(ry));
                         r = make_uint2(rx, ry);
                     }
+                    if (qt != qh) step(qt - qh, main_tag);
+                    if constexpr (kMain) {
+                        fl_base = mbase;
+                        fl_pend = true;
+                    }
                 };
                 if (main_role)
                     run_lists(std::integral_constant<bool, true>());
                 else
                     run_lists(std::integral_constant<bool, false>());
-                if (qt != qh) step(qt - qh);
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_wave_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -1324,6 +1375,13 @@ __global__ __launch_bounds__(kGrpThreads) void k_propagate_seq_grp(
             cur = visit(cur, gr0, gr1);
             if (cur.it >= cn) break;
             cur = visit(cur, gr1, gr0);
+        }
+        if (fl_pend) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            flush();
+            fl_pend = false;
         }
         __syncthreads();
         // the chunk's item totals
