@@ -628,6 +628,100 @@ __global__ __launch_bounds__(kWave) void k_bucket_samples(
     }
 }
 
+// The same sort with a 1024-thread workgroup per table, for few tables over
+// many samples (the sequence layers: 16-64 tables of 8192 (b, s) rows).  Wave w
+// takes a contiguous run of the samples; per-wave bucket counts (LDS) are
+// scanned in (bucket, wave) order, so every wave knows where its run of each
+// bucket starts, and the waves scatter their runs in sample order: the result
+// equals the one-wavefront sort's.
+constexpr int kBsThreads = 1024;
+constexpr int kBsWaves = kBsThreads / kWave;
+constexpr uint32_t kBsMaxEntries = 1024;
+
+__global__ __launch_bounds__(kBsThreads) void k_bucket_samples_wg(
+    const int32_t *__restrict__ idx, const uint32_t *__restrict__ key_t, uint32_t key_pitch,
+    uint32_t key_shift, uint32_t batch, uint32_t n_detectors, uint32_t n_entries, uint32_t n_bits,
+    int32_t *__restrict__ offsets, int32_t *__restrict__ samples) {
+    extern __shared__ int32_t hist[];  // [kBsWaves][n_entries]
+    __shared__ int32_t wsum[kBsWaves];
+    const uint32_t t = blockIdx.x;
+    const uint32_t tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const uint32_t emask = n_entries - 1;
+    const uint32_t *kt = key_t ? key_t + (size_t)t * key_pitch : nullptr;
+    auto key_of = [&](uint32_t b) -> uint32_t {
+        return kt ? (((kt[b] & 0xFFFFu) >> key_shift) & emask) : ((uint32_t)idx[(size_t)b * n_detectors + t] & emask);
+    };
+    // this wave's run of samples: whole 64-sample groups
+    const uint32_t groups = (batch + kWave - 1) / kWave;
+    const uint32_t per = (groups + kBsWaves - 1) / kBsWaves;
+    const uint32_t r0 = min(wave * per * kWave, batch), r1 = min(r0 + per * kWave, batch);
+    int32_t *h = hist + wave * n_entries;
+    for (uint32_t e = lane; e < n_entries; e += kWave) h[e] = 0;
+    const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
+    // lanes with the same key in a group of 64 samples, and this lane's rank among them
+    auto peers_of = [&](uint32_t key, bool valid) -> uint64_t {
+        uint64_t peers = __ballot(valid);
+        for (uint32_t bit = 0; bit < n_bits; bit++) {
+            const bool kb = (key >> bit) & 1u;
+            const uint64_t bm = __ballot(kb);
+            peers &= kb ? bm : ~bm;
+        }
+        return peers;
+    };
+    for (uint32_t base = r0; base < r1; base += kWave) {
+        const uint32_t b = base + lane;
+        const bool valid = b < r1;
+        const uint32_t key = valid ? key_of(b) : 0u;
+        const uint64_t peers = peers_of(key, valid);
+        if (valid && lane == 63u - (uint32_t)__clzll(peers)) h[key] += __popcll(peers);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    __syncthreads();
+    // bucket e's runs: exclusive prefix over the waves, then over the buckets
+    int32_t tot = 0;
+    if (tid < n_entries) {
+        for (uint32_t w = 0; w < (uint32_t)kBsWaves; w++) {
+            const int32_t c = hist[w * n_entries + tid];
+            hist[w * n_entries + tid] = tot;
+            tot += c;
+        }
+    }
+    int32_t incl = tot;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const int32_t y = __shfl_up(incl, off, kWave);
+        if ((int)lane >= off) incl += y;
+    }
+    if (lane == kWave - 1) wsum[wave] = incl;
+    __syncthreads();
+    int32_t before = 0;
+    for (uint32_t w = 0; w < wave; w++) before += wsum[w];
+    int32_t *off_t = offsets + (size_t)t * (n_entries + 1);
+    if (tid < n_entries) {
+        const int32_t start = before + incl - tot;
+        off_t[tid] = start;
+        for (uint32_t w = 0; w < (uint32_t)kBsWaves; w++) hist[w * n_entries + tid] += start;
+    }
+    if (tid == 0) off_t[n_entries] = (int32_t)batch;
+    __syncthreads();
+    int32_t *smp_t = samples + (size_t)t * batch;
+    for (uint32_t base = r0; base < r1; base += kWave) {
+        const uint32_t b = base + lane;
+        const bool valid = b < r1;
+        const uint32_t key = valid ? key_of(b) : 0u;
+        const uint64_t peers = peers_of(key, valid);
+        if (valid) {
+            smp_t[h[key] + __popcll(peers & lt)] = (int32_t)b;
+            if (lane == 63u - (uint32_t)__clzll(peers)) h[key] += __popcll(peers);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+}
+
 // Commit values of the weight gradient, one per (sample, output): what the
 // reference adds to a table row for that sample (gather_weight_gradients_fc,
 // proto:731-790): (float)((double)g * lr) if |(double)g| > EPS, or the int32
@@ -1065,6 +1159,13 @@ hipError_t launch_bucket_samples(const FcShape &s, const int32_t *idx, int32_t *
     if (s.n_detectors == 0) return hipSuccess;
     uint32_t n_bits = 0;
     while ((1u << n_bits) < s.n_entries) n_bits++;
+    if (s.n_detectors < 1024 && s.batch >= 2048 && s.n_entries <= kBsMaxEntries) {
+        // few tables over many samples: a workgroup per table
+        hipLaunchKernelGGL(k_bucket_samples_wg, dim3(s.n_detectors), dim3(kBsThreads),
+                           (size_t)kBsWaves * s.n_entries * sizeof(int32_t), st, idx, key_t, key_pitch,
+                           key_shift, s.batch, s.n_detectors, s.n_entries, n_bits, offsets, samples);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(k_bucket_samples, dim3(s.n_detectors), dim3(kWave),
                        s.n_entries * sizeof(int32_t), st, idx, key_t, key_pitch, key_shift,
                        s.batch, s.n_detectors, s.n_entries, n_bits, offsets, samples);

@@ -146,6 +146,12 @@ def test_table_major_wide_slices(oracle, cuda_device, B, O):
     run_fc(oracle, B, 300, 40, 8, O, seed=16)
 
 
+def test_many_samples_few_tables(oracle, cuda_device):
+    # 4100 samples over 6 tables: the weight gradient's bucket sort runs a
+    # workgroup per table, with a ragged last 64-sample group
+    run_fc(oracle, 4100, 64, 6, 4, 64, seed=19)
+
+
 def test_large_batch_int32_summation(oracle, cuda_device):
     run_fc(oracle, 530, 64, 20, 4, 512, seed=14, int_rescaler=0.5)
 

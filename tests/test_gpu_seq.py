@@ -203,6 +203,12 @@ def test_seq_one_bucket_chunks(oracle, cuda_device):
     run_seq(oracle, B, S, I, T, Nc, Npe, O, seed=12, inputs=(x, anchors, W, pe, go))
 
 
+def test_seq_many_rows_few_tables(oracle, cuda_device):
+    # B*S >= 2048 rows over a few tables: the bucket sorts run a workgroup per
+    # table (per-wave runs of the rows, scanned in (bucket, wave) order)
+    run_seq(oracle, 16, 160, 32, 3, 4, 3, 64, seed=18)
+
+
 @pytest.mark.parametrize("shape", [(3, 100, 48, 3, 5, 5, 128), (2, 513, 32, 2, 5, 6, 64),
                                    (2, 30, 16, 3, 1, 0, 64)])
 def test_seq_grouped_input_gradient(oracle, cuda_device, shape):
