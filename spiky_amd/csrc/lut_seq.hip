@@ -263,7 +263,7 @@ __global__ __launch_bounds__(kBlock) void k_fill_seq(
 // column slice of C columns).  The sub-table slice W[t][q][*][c0, c0 + C)
 // (2^(Nc+Npe) rows, at most 128 KiB) is staged in LDS once, so each table byte
 // crosses HBM once per forward.  The items (b, j) of the bucket (t, q) are
-// taken longest-first from an LDS-sorted list; C lanes own one item and sum
+// taken longest-first (an LDS counting sort on length classes); C lanes own one item and sum
 // its pairs i < j in ascending i in fp64, reading rows from LDS.  The commit
 // value of table t, fp32(sum) (int mode: the int32 payload), goes to
 // part[t][b*S + j][o]; k_fill_commit adds the tables in ascending order, the
@@ -276,6 +276,7 @@ constexpr int kSfThreads = 1024;
 constexpr int kSfTabFloats = 32768;   // 128 KiB sub-table slice
 constexpr int kSfItems = 1024;        // items sorted per chunk of a bucket
 constexpr int kSfPe = 2048;           // distances S - 1
+constexpr int kSfLenClasses = 256;    // item length classes of the longest-first order
 
 // VW consecutive columns of one LDS row (VW = 1, 2 or 4 floats).
 template <int VW>
@@ -311,10 +312,13 @@ __global__ __launch_bounds__(kSfThreads) void k_fill_seq_lds(
     __shared__ uint16_t ptab[kSfPe];
     __shared__ uint32_t keys[kSfItems];
     __shared__ uint32_t irow[kSfItems];
+    __shared__ uint32_t jhist[kSfLenClasses];
     __shared__ uint32_t next_item;
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & (kWave - 1);
     const uint32_t wave = tid / kWave;
+    uint32_t jsh = 0;  // length classes: (S - 1 - j) >> jsh < kSfLenClasses
+    while (((seq - 1) >> jsh) >= (uint32_t)kSfLenClasses) jsh++;
     const uint32_t half = lane / L, cl = lane % L;
     uint32_t *my_rows = rowtab + (wave * kSlots + half) * C;
     const uint32_t slice = blockIdx.x % n_slices;
@@ -369,8 +373,6 @@ __global__ __launch_bounds__(kSfThreads) void k_fill_seq_lds(
     const uint32_t *kw = reinterpret_cast<const uint32_t *>(kp) + 1;
     for (int32_t k0 = beg; k0 < end; k0 += kSfItems) {
         const uint32_t n = (uint32_t)min((int32_t)kSfItems, end - k0);
-        uint32_t p2 = 1;
-        while (p2 < n) p2 <<= 1;
         if (k0 != beg) {
 #pragma unroll
             for (int u = 0; u < kSfItems / kSfThreads; u++) {
@@ -379,30 +381,48 @@ __global__ __launch_bounds__(kSfThreads) void k_fill_seq_lds(
             }
         }
         __syncthreads();  // staging done / the previous chunk is done with keys and irow
-        // key: (S - 1 - j) << 16 | item, so ascending order is longest-first
+        // Longest first: a counting sort of the items on (S - 1 - j) >> jsh (at most
+        // kSfLenClasses classes; the order within a class is arbitrary), keys[pos]
+        // = the item's number in the chunk.
+        for (uint32_t k = tid; k < (uint32_t)kSfLenClasses; k += kSfThreads) jhist[k] = 0;
+        __syncthreads();
+        uint32_t cls[kSfItems / kSfThreads], rank[kSfItems / kSfThreads];
 #pragma unroll
         for (int u = 0; u < kSfItems / kSfThreads; u++) {
             const uint32_t it = u * kSfThreads + tid;
-            if (it < p2) {
+            if (it < n) {
                 irow[it] = rr[u];
-                keys[it] = it < n ? (((seq - 1 - rr[u] % seq) << 16) | it) : 0xFFFFFFFFu;
+                cls[u] = (seq - 1 - rr[u] % seq) >> jsh;
+                rank[u] = atomicAdd(&jhist[cls[u]], 1u);
             }
         }
         __syncthreads();
-        for (uint32_t k = 2; k <= p2; k <<= 1) {
-            for (uint32_t jj = k >> 1; jj > 0; jj >>= 1) {
-                for (uint32_t i = tid; i < p2; i += kSfThreads) {
-                    const uint32_t ixj = i ^ jj;
-                    if (ixj > i) {
-                        const uint32_t a = keys[i], c = keys[ixj];
-                        if (((i & k) == 0) == (a > c)) {
-                            keys[i] = c;
-                            keys[ixj] = a;
-                        }
-                    }
-                }
-                __syncthreads();
+        if (wave == 0) {  // exclusive scan of the class counts
+            constexpr int kPerLane = kSfLenClasses / kWave;
+            uint32_t c[kPerLane], sum = 0;
+#pragma unroll
+            for (int k = 0; k < kPerLane; k++) {
+                c[k] = jhist[lane * kPerLane + k];
+                sum += c[k];
             }
+            uint32_t inc = sum;
+#pragma unroll
+            for (int o = 1; o < kWave; o <<= 1) {
+                const uint32_t y = __shfl_up(inc, o, kWave);
+                if (lane >= (uint32_t)o) inc += y;
+            }
+            uint32_t run = inc - sum;
+#pragma unroll
+            for (int k = 0; k < kPerLane; k++) {
+                jhist[lane * kPerLane + k] = run;
+                run += c[k];
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < kSfItems / kSfThreads; u++) {
+            const uint32_t it = u * kSfThreads + tid;
+            if (it < n) keys[jhist[cls[u]] + rank[u]] = it;
         }
         if (tid == 0) next_item = 0;
         __syncthreads();
