@@ -1574,17 +1574,18 @@ __global__ __launch_bounds__(kBlock) void k_zero64(double *__restrict__ p, uint6
 constexpr int kSeqWgThreads = 1024;
 constexpr int kSeqWgRowsMax = 4096;      // sub-table rows 2^(Nc+Npe)
 // LDS: 32 KiB of row counts and cursors, 52 KiB of u8 entries, 49 KiB of
-// gradient rows, 19 KiB of index tables: 195 items of 255 earlier positions
+// gradient rows, 19 KiB of index tables: 195 items of 255 earlier positions (and
+// the pads of 1024 rows)
 // and 64 columns fit one batch, so a (table, Q) bucket of up to 195 items --
 // every bucket of 2^6 Q values over 8192 (b, s) rows in practice -- is summed
-// and written in one pass.  A row's bucket of entries is padded to an even
-// size (the pad names the zero row), so the walk reads entries in pairs.
+// and written in one pass.  A row's bucket of entries is padded to a multiple
+// of four (pads name the zero row), so the walk reads entries four at a time.
 constexpr int kSeqWgEntries = 53248;     // entries per batch (u8 item numbers), pads included
 constexpr int kSeqWgGvWords = 12544;     // batch gradient rows (items x C) and the zero row
 constexpr int kSeqWgKeys = 8192;         // K indices of up to 8192 (b, s) rows at a time
 constexpr int kSeqWgPe = 1024;
 constexpr int kSeqWgItems = 256;         // u8 entries: at most 256 items a batch
-constexpr int kQuadStep = 2;             // entries a turn of the 16-byte row loop (one u16 pair)
+constexpr int kQuadStep = 4;             // entries a turn of the 16-byte row loop (one u32 read)
 constexpr int kSeqWgClasses = 64;        // row length classes (turns of kQuadStep entries, the last open)
 
 template <bool INT_MODE, bool OVERWRITE>
@@ -1596,7 +1597,7 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
     uint32_t cols, uint32_t n_slices, uint32_t items_per_batch, double int_rescaler, bool quad) {
     __shared__ uint32_t cnt[kSeqWgRowsMax];
     __shared__ uint32_t cur[kSeqWgRowsMax];
-    __shared__ __attribute__((aligned(4))) uint8_t ent[kSeqWgEntries + 2];  // + the walk's read-ahead
+    __shared__ __attribute__((aligned(4))) uint8_t ent[kSeqWgEntries + kQuadStep];  // + the walk's read-ahead
     __shared__ uint32_t gv[kSeqWgGvWords];
     __shared__ uint16_t ktab[kSeqWgKeys];
     __shared__ uint16_t ptab[kSeqWgPe];
@@ -1655,7 +1656,7 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
             uint32_t carry = 0;
             for (uint32_t base = 0; base < sub_rows; base += kSeqWgThreads) {
                 const uint32_t r = base + tid;
-                const uint32_t v = r < sub_rows ? (cnt[r] + 1u) & ~1u : 0u;  // buckets of even size
+                const uint32_t v = r < sub_rows ? (cnt[r] + kQuadStep - 1u) & ~(kQuadStep - 1u) : 0u;  // whole turns
                 uint32_t incl = v;
 #pragma unroll
                 for (int o = 1; o < kWave; o <<= 1) {
@@ -1690,8 +1691,8 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
             // is the k-th row of the walk, cnt[k] & 0xFFFF row k's count.
             if (quad) {
                 __syncthreads();
-                for (uint32_t r = tid; r < sub_rows; r += kSeqWgThreads)
-                    if (cnt[r] & 1u) ent[cur[r]] = (uint8_t)nb;  // the pad of an odd bucket: the zero row
+                for (uint32_t r = tid; r < sub_rows; r += kSeqWgThreads)  // pads: the zero row
+                    for (uint32_t k = cur[r]; k & (kQuadStep - 1u); k++) ent[k] = (uint8_t)nb;
                 for (uint32_t c = tid; c < (uint32_t)kSeqWgClasses; c += kSeqWgThreads) lhist[c] = 0u;
                 __syncthreads();
                 auto row_class = [&](uint32_t r) -> uint32_t {
@@ -1755,33 +1756,33 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
                 if (quad) {
                     // 64-column slices, lane k of a group holding columns 4k .. 4k+3:
                     // one 16-byte LDS read per entry.  Wavefront w takes the rows at
-                    // walk positions 4 (w + 16 m) .. + 3, one per group, and adds an
-                    // entry pair (one u16 read, the next pair's read in flight) a turn
-                    // (a pad or entries past a shorter row's end read the zero row,
-                    // adding +0, which leaves a sum that starts at +0 unchanged); the
-                    // group then writes its row.
-                    static_assert(kQuadStep == 2, "the walk reads entry pairs");
+                    // walk positions 4 (w + 16 m) .. + 3, one per group, and adds four
+                    // entries (one u32 read, the next four's read in flight) a turn
+                    // (pads read the zero row, adding +0, which leaves a sum that
+                    // starts at +0 unchanged); the group then writes its row.
+                    static_assert(kQuadStep == 4, "the walk reads entry quads");
                     const uint32_t c4 = (tid & 15u) * 4u;
                     const uint32_t cq = col0 + c4;
                     const uint32_t gw = (tid >> 4) & 3u;
-                    const uint16_t *ent2 = reinterpret_cast<const uint16_t *>(ent);
+                    const uint32_t *ent4 = reinterpret_cast<const uint32_t *>(ent);
                     for (uint32_t k4 = wave * 4u; k4 < sub_rows; k4 += kSeqWgThreads / 16u) {
                         const uint32_t pos = k4 + gw;
                         const bool have = pos < sub_rows;
                         const uint32_t row = have ? cnt[pos] >> 16 : 0u;
                         const uint32_t n = have ? cnt[row] & 0xFFFFu : 0u;
-                        const uint32_t e0 = have ? cur[row] - n : 0u;  // even
-                        const uint32_t np = (n + 1u) / 2u;              // entry pairs
+                        const uint32_t e0 = have ? cur[row] - n : 0u;  // a multiple of 4
+                        const uint32_t np = (n + 3u) / 4u;              // entry quads
                         float af[4] = {0.f, 0.f, 0.f, 0.f};
                         uint32_t ai[4] = {0u, 0u, 0u, 0u};
-                        uint32_t pr = ent2[e0 / 2u];
+                        uint32_t pr = ent4[e0 / 4u];
                         for (uint32_t k = 0; k < np; k++) {
-                            const uint32_t npr = ent2[e0 / 2u + k + 1u];  // next pair (read-ahead)
-                            u32x4 g[2];
-                            g[0] = *reinterpret_cast<const u32x4 *>(gv + (pr & 0xFFu) * 64u + c4);
-                            g[1] = *reinterpret_cast<const u32x4 *>(gv + (pr >> 8) * 64u + c4);
+                            const uint32_t npr = ent4[e0 / 4u + k + 1u];  // next quad (read-ahead)
+                            u32x4 g[4];
 #pragma unroll
-                            for (int u = 0; u < 2; u++)
+                            for (int u = 0; u < 4; u++)
+                                g[u] = *reinterpret_cast<const u32x4 *>(gv + ((pr >> (8 * u)) & 0xFFu) * 64u + c4);
+#pragma unroll
+                            for (int u = 0; u < 4; u++)
 #pragma unroll
                                 for (int c = 0; c < 4; c++) {
                                     if (INT_MODE) ai[c] += g[u][c];
@@ -1964,7 +1965,7 @@ uint32_t seq_fill_cols(const SeqShape &s) {
 uint32_t seq_wg_cols(const SeqShape &s) {
     const uint64_t sub_rows = 1ull << (s.n_anchors + s.pe_dim);
     if (sub_rows > (uint64_t)kSeqWgRowsMax || s.seq > (uint32_t)kSeqWgKeys ||
-        s.seq - 1 > (uint32_t)kSeqWgPe || s.seq - 1 + sub_rows > (uint64_t)kSeqWgEntries)
+        s.seq - 1 > (uint32_t)kSeqWgPe || s.seq - 1 + (kQuadStep - 1) * sub_rows > (uint64_t)kSeqWgEntries)
         return 0;
     uint32_t cols = 64;
     while (cols > 1 && cols / 2 >= s.n_outputs) cols /= 2;
@@ -1974,7 +1975,7 @@ uint32_t seq_wg_cols(const SeqShape &s) {
 // Items per batch: their entries (< seq each) and gradient rows must fit.
 uint32_t seq_wg_items(const SeqShape &s, uint32_t cols) {
     const uint32_t sub_rows = 1u << (s.n_anchors + s.pe_dim);
-    uint32_t n = ((uint32_t)kSeqWgEntries - sub_rows) / std::max<uint32_t>(1, s.seq - 1);  // and a pad a row
+    uint32_t n = ((uint32_t)kSeqWgEntries - (kQuadStep - 1) * sub_rows) / std::max<uint32_t>(1, s.seq - 1);  // and pads
     n = std::min<uint32_t>(n, (uint32_t)kSeqWgGvWords / cols - 1);  // and the zero row
     return std::min<uint32_t>(n, (uint32_t)kSeqWgItems);
 }
