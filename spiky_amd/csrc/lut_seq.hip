@@ -1628,9 +1628,24 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
     for (uint32_t r0 = 0; r0 < n_rows && k0 < end; r0 += rows_per_chunk) {
         const uint32_t r1 = min(r0 + rows_per_chunk, n_rows);
         __syncthreads();
-        for (uint32_t r = r0 + tid; r < r1; r += kSeqWgThreads) ktab[r - r0] = (uint16_t)rec_idx(kp[r]);
-        // first bucket position at or past row r1 (uniform binary search)
+        // the chunk's K indices, eight loads in flight a thread
+        for (uint32_t r = r0 + tid; r < r1; r += 8 * kSeqWgThreads) {
+            uint32_t kv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const uint32_t rr = r + u * kSeqWgThreads;
+                kv[u] = rr < r1 ? kp[rr].y : 0u;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const uint32_t rr = r + u * kSeqWgThreads;
+                if (rr < r1) ktab[rr - r0] = (uint16_t)rec_idx(make_uint2(0u, kv[u]));
+            }
+        }
+        // first bucket position at or past row r1 (uniform binary search; the
+        // bucket's end when the chunk reaches the last row)
         int32_t lo = k0, hi = end;
+        if (r1 >= n_rows) lo = end;
         while (lo < hi) {
             const int32_t mid = lo + (hi - lo) / 2;
             if ((uint32_t)smp[mid] < r1) lo = mid + 1; else hi = mid;
@@ -1683,6 +1698,30 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
                     ent[atomicAdd(&cur[row], 1u)] = (uint8_t)it;  // the item's gv row is it * cols
                 }
             }
+            // The quad path's gradient rows of a slice: thread tid loads columns
+            // col0 + 4 (tid & 15) .. + 3 of items (tid >> 4) + 64 u, one slice
+            // ahead (the loads run while the previous slice is walked); item nb
+            // is the zero row.
+            constexpr int kGvPasses = (kSeqWgGvWords / 64 + 63) / 64;
+            u32x4 pre[kGvPasses];
+            auto gv_load = [&](uint32_t col0) {
+                const uint32_t cq = col0 + (tid & 15u) * 4u;
+#pragma unroll
+                for (int u = 0; u < kGvPasses; u++) {
+                    const uint32_t it = (tid >> 4) + 64u * u;
+                    pre[u] = u32x4{0u, 0u, 0u, 0u};
+                    if (it < nb && cq < n_outputs)
+                        pre[u] = *reinterpret_cast<const u32x4 *>(cv + (size_t)bitems[it] * n_outputs + cq);
+                }
+            };
+            auto gv_store = [&]() {
+#pragma unroll
+                for (int u = 0; u < kGvPasses; u++) {
+                    const uint32_t it = (tid >> 4) + 64u * u;
+                    if (it <= nb) *reinterpret_cast<u32x4 *>(gv + it * 64u + (tid & 15u) * 4u) = pre[u];
+                }
+            };
+            if (quad) gv_load(0);
             // cur[row] is now the end of the row's bucket, cur - cnt its start.
             // The quad path walks rows four to a wavefront, one to each 16-lane
             // group; rows of equal length (in turns) go together, so the groups
@@ -1729,12 +1768,17 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
                 const uint32_t col0 = sl * cols;
                 __syncthreads();  // scatter done / the previous slice is done with gv
                 // the batch's gradient rows, then a zero row (item nb) that the
-                // quad path reads for entries past a row's end
-                for (uint32_t e = tid; e < (nb + 1) * cols; e += kSeqWgThreads) {
-                    const uint32_t it = e / cols, cc = col0 + e % cols;
-                    gv[e] = (it < nb && cc < n_outputs) ? cv[(size_t)bitems[it] * n_outputs + cc] : 0u;
+                // quad path reads for pads
+                if (quad) {
+                    gv_store();
+                } else {
+                    for (uint32_t e = tid; e < (nb + 1) * cols; e += kSeqWgThreads) {
+                        const uint32_t it = e / cols, cc = col0 + e % cols;
+                        gv[e] = (it < nb && cc < n_outputs) ? cv[(size_t)bitems[it] * n_outputs + cc] : 0u;
+                    }
                 }
                 __syncthreads();
+                if (quad && sl + 1 < n_slices) gv_load(col0 + cols);
                 // lane group g (cols lanes, or 16 lanes of 4 columns on the quad
                 // path) takes the rows whose entries start in [g E / G, (g + 1) E / G):
                 // about equal work whatever the row sizes
