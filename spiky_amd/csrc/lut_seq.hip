@@ -1050,6 +1050,16 @@ __device__ __forceinline__ int32_t grp_code(uint32_t e, int at) {
     return __builtin_amdgcn_sbfe((int32_t)e, at, 2);
 }
 
+// lanes below this one whose bit is set in a ballot
+__device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// v with its sign flipped when bit 0 of s is set
+__device__ __forceinline__ double signed_by(double v, uint32_t s) {
+    return __longlong_as_double(__double_as_longlong(v) ^ ((long long)(s & 1u) << 63));
+}
+
 // a list slot past the end: i = 0xFFFF is >= every j
 __device__ __forceinline__ uint2 grp_none() { return make_uint2(0u, 0xFFFFu); }
 
@@ -1268,8 +1278,9 @@ __global__ __launch_bounds__(kGrpThreads) void k_propagate_seq_grp(
                         if (__builtin_amdgcn_ballot_w64(pushes)) {
                             if (pushes && s8 == 0) {
                                 const int32_t ci = grp_code(e, kCoI), cd = grp_code(e, kCoD);
-                                if (ci) atomicAdd(&ca[grp_lane(e)], (double)ci * tot);
-                                if (cd) atomicAdd(&dsum[(e >> kEntD) & 0x3FFu], (double)cd * tot);
+                                // a share is +-tot: the code's high bit is the sign
+                                if (ci) atomicAdd(&ca[grp_lane(e)], signed_by(tot, e >> (kCoI + 1)));
+                                if (cd) atomicAdd(&dsum[(e >> kEntD) & 0x3FFu], signed_by(tot, e >> (kCoD + 1)));
                             }
                         }
                     }
@@ -1330,7 +1341,7 @@ __global__ __launch_bounds__(kGrpThreads) void k_propagate_seq_grp(
                         const uint64_t b1 = __ballot(n_rd >= 1);
                         const uint64_t b2 = kMain ? __ballot(n_rd >= 2) : 0ull;
                         const uint64_t b3 = kMain ? __ballot(n_rd >= 3) : 0ull;
-                        const uint32_t pos = qt + __popcll(b1 & below) + __popcll(b2 & below) + __popcll(b3 & below);
+                        const uint32_t pos = qt + lanes_below(b1) + (kMain ? lanes_below(b2) + lanes_below(b3) : 0u);
                         if (n_rd >= 1) q[pos & (kGrpQueue - 1)] = e_a;
                         if (kMain && n_rd >= 2) q[(pos + 1) & (kGrpQueue - 1)] = e_b;
                         if (kMain && n_rd >= 3) q[(pos + 2) & (kGrpQueue - 1)] = e_c;
