@@ -12,8 +12,9 @@
 //                          fp32 result is bit-identical to it (no atomics).
 //   k_fill_sparse_atomic   one thread per (b, t, group): the reference's own
 //                          decomposition with fp32/int32 atomics (any topology).
-//   k_propagate_sparse     one thread per (b, t, group): main/alt group dots in
-//                          fp64 and the min-margin anchor update.
+//   k_propagate_sparse     eight lanes (one for int32 sums) per (b, t, group):
+//                          main/alt group dots in fp64 and the min-margin anchor
+//                          update.
 //   k_wgrad_sparse_rowsum  one thread per synapse: sums lr*g over the samples
 //                          bucketed on its lookup neuron, ascending (bit-identical
 //                          to the reference CPU path), and writes it once.
@@ -55,6 +56,9 @@ __global__ __launch_bounds__(kBlock) void k_fill_sparse_uniform(
     float acc = out[item];
     int32_t iacc = __float_as_int(acc);
     const uint32_t emask = n_entries - 1;
+    // unrolled so that several pairs' dependent loads (index, neuron offset,
+    // weight) are in flight at once; the adds stay in ascending pair order
+#pragma unroll 8
     for (int64_t p = in_offsets[j]; p < in_offsets[j + 1]; p++) {
         const int2 tk = in_pairs[p];
         const uint32_t n = (uint32_t)tk.x * n_entries + ((uint32_t)ib[tk.x] & emask);
@@ -98,7 +102,40 @@ __global__ __launch_bounds__(kBlock) void k_fill_sparse_atomic(
 }
 
 // propagate_through_detectors_non_seq_sparse_logic (proto:1303-1419) with
-// accumulate_grad_sum_sparse (proto:315-395).
+// accumulate_grad_sum_sparse (proto:315-395).  fp32 summation: eight lanes per
+// (b, t, group): lane l takes the group's synapses l, l + 8, .. of the main and
+// of the alternative neuron (fp64 sums of the exact products w * g), the eight
+// partial sums are joined by DPP (a tree of depth 3), and lane 0 applies the
+// min-margin anchor update; the eight lanes of an item share its early exits.
+// int32 summation keeps one lane per item and the synapses' serial order, so
+// the fp64 dot, and with it the truncated payload, is the reference's.
+template <bool INT_MODE>
+constexpr int sp_lanes() { return INT_MODE ? 1 : 8; }
+
+__device__ __forceinline__ double sp_dpp_f64(double v, int ctrl_sel) {
+    const long long u = __double_as_longlong(v);
+    int lo = (int)(uint32_t)u, hi = (int)(uint32_t)((unsigned long long)u >> 32);
+    if (ctrl_sel == 0) {
+        lo = __builtin_amdgcn_mov_dpp(lo, 0xB1, 0xF, 0xF, true);  // quad_perm xor 1
+        hi = __builtin_amdgcn_mov_dpp(hi, 0xB1, 0xF, 0xF, true);
+    } else if (ctrl_sel == 1) {
+        lo = __builtin_amdgcn_mov_dpp(lo, 0x4E, 0xF, 0xF, true);  // quad_perm xor 2
+        hi = __builtin_amdgcn_mov_dpp(hi, 0x4E, 0xF, 0xF, true);
+    } else {
+        lo = __builtin_amdgcn_mov_dpp(lo, 0x141, 0xF, 0xF, true);  // half-row mirror (8 lanes)
+        hi = __builtin_amdgcn_mov_dpp(hi, 0x141, 0xF, 0xF, true);
+    }
+    return __longlong_as_double((long long)(((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo));
+}
+
+// sum over the 8 lanes of a group, every lane gets it
+__device__ __forceinline__ double sp_sum8(double v) {
+    v += sp_dpp_f64(v, 0);
+    v += sp_dpp_f64(v, 1);
+    v += sp_dpp_f64(v, 2);
+    return v;
+}
+
 template <bool INT_MODE>
 __global__ __launch_bounds__(kBlock) void k_propagate_sparse(
     const float *__restrict__ w, const float *__restrict__ g, const int32_t *__restrict__ idx,
@@ -107,8 +144,11 @@ __global__ __launch_bounds__(kBlock) void k_propagate_sparse(
     float *__restrict__ x_grad, uint32_t n_inputs, uint32_t n_outputs, uint32_t n_detectors,
     uint32_t n_anchors, uint32_t n_entries, uint32_t ogs, uint32_t max_groups, uint64_t n_items,
     double int_rescaler) {
-    const uint64_t item = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
-    if (item >= n_items) return;
+    constexpr int kSpLanes = sp_lanes<INT_MODE>();
+    const uint64_t gid = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+    const uint64_t item = gid / kSpLanes;
+    const uint32_t l = (uint32_t)(gid % kSpLanes);
+    if (item >= n_items) return;  // whole lane groups (kBlock % 8 == 0)
     const uint32_t grp = (uint32_t)(item % max_groups);
     const uint64_t bt = item / max_groups;
     const uint32_t t = (uint32_t)(bt % n_detectors);
@@ -123,7 +163,7 @@ __global__ __launch_bounds__(kBlock) void k_propagate_sparse(
     {
         const int64_t s0 = syn_offsets[nm] + (int64_t)grp * ogs;
         const int64_t s1 = min(s0 + (int64_t)ogs, syn_offsets[nm + 1]);
-        for (int64_t s = s0; s < s1; s++) {
+        for (int64_t s = s0 + l; s < s1; s += kSpLanes) {
             const uint32_t tg = (uint32_t)syn_targets[s];
             if (tg < n_outputs) ms += (double)w[s] * (double)gb[tg];
         }
@@ -131,10 +171,15 @@ __global__ __launch_bounds__(kBlock) void k_propagate_sparse(
     {
         const int64_t s0 = syn_offsets[na] + (int64_t)grp * ogs;
         const int64_t s1 = min(s0 + (int64_t)ogs, syn_offsets[na + 1]);
-        for (int64_t s = s0; s < s1; s++) {
+        for (int64_t s = s0 + l; s < s1; s += kSpLanes) {
             const uint32_t tg = (uint32_t)syn_targets[s];
             if (tg < n_outputs) as += (double)w[s] * (double)gb[tg];
         }
+    }
+    if (kSpLanes == 8) {
+        ms = sp_sum8(ms);
+        as = sp_sum8(as);
+        if (l != 0) return;
     }
     const double du = du_of_margin(md[bt]) * (ms - as);
     if (!(fabs(du) > kEps)) return;
@@ -184,6 +229,8 @@ __global__ __launch_bounds__(kBlock) void k_wgrad_sparse_rowsum(
     const int32_t *smp = samples + (size_t)t * batch;
     float acc = target[s];
     int32_t iacc = __float_as_int(acc);
+    // unrolled: several samples' g loads in flight, the adds in ascending order
+#pragma unroll 4
     for (int32_t k = beg; k < end; k++) {
         const double gg = (double)g[(size_t)smp[k] * n_outputs + tg];
         if (!(fabs(gg) > kEps)) continue;
@@ -248,14 +295,16 @@ hipError_t launch_propagate_sparse(const SparseShape &s, const float *w, const f
     const uint64_t n_items = (uint64_t)s.fc.batch * s.fc.n_detectors * s.max_groups;
     if (n_items == 0) return hipSuccess;
     const int2 *ap = reinterpret_cast<const int2 *>(anchors);
+    const uint64_t n_threads = n_items * (int_mode ? sp_lanes<true>() : sp_lanes<false>());
+    if ((n_threads + kBlock - 1) / kBlock > 0x7fffffffull) return hipErrorInvalidConfiguration;
     if (int_mode)
-        hipLaunchKernelGGL(k_propagate_sparse<true>, dim3(blocks_for(n_items)), dim3(kBlock), 0,
+        hipLaunchKernelGGL(k_propagate_sparse<true>, dim3(blocks_for(n_threads)), dim3(kBlock), 0,
                            st, w, g, idx, min_deltas, min_idx, ap, syn_offsets, syn_targets,
                            x_grad, s.fc.n_inputs, s.fc.n_outputs, s.fc.n_detectors,
                            s.fc.n_anchors, s.fc.n_entries, s.fc.ogs, s.max_groups, n_items,
                            int_rescaler);
     else
-        hipLaunchKernelGGL(k_propagate_sparse<false>, dim3(blocks_for(n_items)), dim3(kBlock), 0,
+        hipLaunchKernelGGL(k_propagate_sparse<false>, dim3(blocks_for(n_threads)), dim3(kBlock), 0,
                            st, w, g, idx, min_deltas, min_idx, ap, syn_offsets, syn_targets,
                            x_grad, s.fc.n_inputs, s.fc.n_outputs, s.fc.n_detectors,
                            s.fc.n_anchors, s.fc.n_entries, s.fc.ogs, s.max_groups, n_items,
