@@ -98,6 +98,43 @@ def test_int8_e256_chunks_and_folds(oracle, cuda_device, B, dgs):
     assert np.array_equal(out.cpu().numpy(), rout)
 
 
+
+@pytest.mark.parametrize("ordered", [True, False])
+def test_int8_e256_fp32_sums_partial_slice(oracle, cuda_device, ordered):
+    """int8 tables at E = 256 with fp32 summation (LUTDataManagerF): two
+    ragged 1024-sample chunks and 112 outputs, so the last 32-column slice is
+    half past the row (its loads clamp, its stores are skipped).  Ordered sums
+    commit every 32-table block in order, as the reference; folded ones form
+    one fp64 sum over the unit's blocks, which is the oracle with blocks of
+    that many tables.  Bit for bit either way."""
+    from test_gpu_layers import fold_blocks
+    from spiky_amd import LUTDataManagerF
+    dev = cuda_device
+    B, I, T, Nc, O = 1500, 300, 8192, 8, 112
+    E = 1 << Nc
+    g = torch.Generator().manual_seed(77)
+    x = torch.randn(B * I, generator=g)
+    anchors = torch.stack([torch.randperm(I, generator=g)[:2] for _ in range(T * Nc)]).to(torch.int32).flatten()
+    q = torch.randint(-128, 128, (T * E * O,), generator=g, dtype=torch.int8)
+    sc = torch.rand(T, generator=g) * 0.009 + 0.001
+    dm = LUTDataManagerF(I, O, T, Nc, 1, 0, 0, 32, 32)
+    dm.register_synapse_meta(1.0, -1.0, 1.0, 0.0, 0.0)
+    dm.initialize_neurons(True)
+    dm.to_device(0)
+    dm.set_ordered_sums(ordered)
+    fold = 1 if ordered else fold_blocks(B, T, O)
+    assert ordered or fold == 2
+    out = torch.zeros(B * O, device=dev)
+    idx = torch.empty(B * T, dtype=torch.int32, device=dev)
+    print(f"[int8 fp32 sums] ordered={ordered} fold={fold}", flush=True)
+    dm.forward_step_i8(q.to(dev), sc.to(dev), B, x.to(dev), anchors.to(dev), out, idx)
+    torch.cuda.synchronize()
+    ridx = oracle.check_detectors(x.numpy(), anchors.numpy(), B, I, T, Nc, train=False)
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    rout = oracle.fill_outputs_fc(None, ridx, B, O, T, E, dgs=32 * fold, q8=q.numpy(), scales=sc.numpy())
+    assert np.array_equal(out.cpu().numpy(), rout)
+
+
 def test_config2_projection_stack(oracle, cuda_device):
     """BASELINE config 2 as the bench builds it (bench.build_projection_stack):
     two sparse ProjectionLUTLayers and the 800 -> 10 dense head at batch 128,
