@@ -186,19 +186,23 @@ __global__ __launch_bounds__(kPrThreads) void k_prod_pairs(
 // row segment.  Pushes into rows i and distances j-i-1 are LDS atomics on
 // consecutive words; pushes into the shared row j are summed over the wave
 // first (one atomic per slot), since up to 64 lanes would hit one word.
+// fp32 pushes are summed in fp64 LDS words: on gfx950 ds_add_f64 sustains
+// about 7.5 lanes a clock per CU on consecutive words, ds_add_f32 0.33.
 // Pushes reach HBM as one atomic per (row, slot) per workgroup.
 constexpr uint32_t kTbThreads = 1024;
-constexpr uint32_t kPtBudget = 64 * 1024;
+constexpr uint32_t kPtBudget = 80 * 1024;  // two workgroups a CU
 
 struct TableLayout {
     uint32_t jb;  // positions per workgroup; 0 = does not fit
     uint32_t bytes;
 };
 
-TableLayout table_layout(const ProductShape &s, bool bwd) {
+// LDS: anchor codes (8 B each), the packed histogram (rounded up to 8 B), the
+// slot values (4 B), and in the backward the push sums (acc_bytes each).
+TableLayout table_layout(const ProductShape &s, bool bwd, uint32_t acc_bytes) {
     const uint64_t E = 1ull << s.n_anchors;
     const uint64_t NS = 2ull * s.n_anchors;
-    const uint64_t fixed = (uint64_t)s.n_anchors * 8 + 4 + (uint64_t)s.seq_len * NS * 4 * (bwd ? 2 : 1);
+    const uint64_t fixed = (uint64_t)s.n_anchors * 8 + 4 + (uint64_t)s.seq_len * NS * (4 + (bwd ? acc_bytes : 0));
     const uint64_t per_j = E * 2;
     if (fixed + per_j > kPtBudget || NS * s.seq_len >= (1ull << 28)) return {0, 0};
     uint64_t jb = (kPtBudget - fixed) / per_j;
@@ -252,13 +256,15 @@ __global__ __launch_bounds__(kTbThreads) __attribute__((amdgpu_waves_per_eu(8)))
     float cmp_eps, double int_rescaler, uint32_t JB, uint32_t n_jblocks) {
     // int32 payloads are summed as uint32 (wrapping, as the reference's int sums)
     typedef typename std::conditional<INT_MODE, uint32_t, float>::type push_t;
+    // and the workgroup's sums of fp32 pushes are fp64
+    typedef typename std::conditional<INT_MODE, uint32_t, double>::type acc_t;
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t E = 1u << n_anchors;
     const uint32_t NS = 2 * n_anchors;
     int2 *code = reinterpret_cast<int2 *>(smem);
     uint32_t *hist = reinterpret_cast<uint32_t *>(code + n_anchors);
     const uint32_t hist_words = (JB * E + 1) / 2;
-    float *xs = reinterpret_cast<float *>(hist + hist_words);
+    float *xs = reinterpret_cast<float *>(hist + ((hist_words + 1) & ~1u));  // 8-byte aligned
     const uint32_t tid = threadIdx.x;
     const uint32_t jblk = blockIdx.x % n_jblocks;
     const uint32_t bt = blockIdx.x / n_jblocks;
@@ -266,7 +272,7 @@ __global__ __launch_bounds__(kTbThreads) __attribute__((amdgpu_waves_per_eu(8)))
     const uint32_t j0 = jblk * JB;
     const uint32_t j_end = min(S, j0 + JB);
     const uint32_t R = j_end;  // rows 0 .. j_end-1 (i, j and distances all below j_end)
-    push_t *acc = reinterpret_cast<push_t *>(xs + (size_t)R * NS);  // BWD only
+    acc_t *acc = reinterpret_cast<acc_t *>(xs + (size_t)R * NS);  // BWD only (NS is even)
     if (tid < n_anchors) {
         const int2 ap = anchors[(size_t)t * n_anchors + tid];
         int2 c = make_int2(-1, -1);
@@ -366,7 +372,7 @@ __global__ __launch_bounds__(kTbThreads) __attribute__((amdgpu_waves_per_eu(8)))
                             if (hh == 0) { ps0 = cc & 0xFFFFFFF; pv0 = pv; }
                             else { ps1 = cc & 0xFFFFFFF; pv1 = pv; }
                         } else {
-                            atomicAdd(acc + (sr == 0 ? B0 : B2) + (cc & 0xFFFFFFF), pv);
+                            atomicAdd(acc + (sr == 0 ? B0 : B2) + (cc & 0xFFFFFFF), (acc_t)pv);
                         }
                     }
                 }
@@ -378,8 +384,8 @@ __global__ __launch_bounds__(kTbThreads) __attribute__((amdgpu_waves_per_eu(8)))
             const uint32_t jw = (uint32_t)__builtin_amdgcn_readlane((int)j, (int)first);
             const bool uniform = __ballot(active && j != jw) == 0;
             if (!uniform) {
-                if (ps0 >= 0) atomicAdd(acc + ps0 + j, pv0);
-                if (ps1 >= 0) atomicAdd(acc + ps1 + j, pv1);
+                if (ps0 >= 0) atomicAdd(acc + ps0 + j, (acc_t)pv0);
+                if (ps1 >= 0) atomicAdd(acc + ps1 + j, (acc_t)pv1);
             } else if (__ballot(ps0 >= 0 || ps1 >= 0) != 0) {
 #pragma unroll
                 for (int a = 0; a < NCMAX; a++) {
@@ -391,7 +397,7 @@ __global__ __launch_bounds__(kTbThreads) __attribute__((amdgpu_waves_per_eu(8)))
                         const push_t mine = (ps0 == sb ? pv0 : (push_t)0) + (ps1 == sb ? pv1 : (push_t)0);
                         if (__ballot(mine != (push_t)0) == 0) continue;
                         const push_t tot = wave_sum64(mine);
-                        if (lane == first) atomicAdd(acc + sb + jw, tot);
+                        if (lane == first) atomicAdd(acc + sb + jw, (acc_t)tot);
                     }
                 }
             }
@@ -412,8 +418,8 @@ __global__ __launch_bounds__(kTbThreads) __attribute__((amdgpu_waves_per_eu(8)))
     if (BWD) {
         for (uint32_t e = tid; e < R * NS; e += kTbThreads) {
             const uint32_t sidx = e / R, r = e - sidx * R;
-            const int32_t iv = reinterpret_cast<const int32_t *>(acc)[e];
-            if (iv == 0) continue;  // +0.0f, or a zero int32 sum (a -0.0f sum adds nothing either)
+            const acc_t av = acc[e];
+            if (av == (acc_t)0) continue;  // a zero sum (of either sign) adds nothing
             const int2 ap = anchors[(size_t)t * n_anchors + sidx / 2];
             int32_t src;
             uint32_t k;
@@ -421,8 +427,8 @@ __global__ __launch_bounds__(kTbThreads) __attribute__((amdgpu_waves_per_eu(8)))
             float *dst = src == 0 ? x1_grad + ((size_t)b * S + r) * n1 + k
                                   : (src == 1 ? x2_grad + ((size_t)b * S + r) * n2 + k
                                               : pe_grad + ((size_t)r * T + t) * pd + k);
-            if (INT_MODE) atomicAdd(reinterpret_cast<int32_t *>(dst), iv);
-            else atomicAdd(dst, reinterpret_cast<const float *>(acc)[e]);
+            if (INT_MODE) atomicAdd(reinterpret_cast<int32_t *>(dst), (int32_t)av);
+            else atomicAdd(dst, (float)av);
         }
     }
 }
@@ -846,7 +852,7 @@ hipError_t launch_forward_product(const ProductShape &s, const float *w, const f
     if (BS == 0) return hipSuccess;
     float *cnt = reinterpret_cast<float *>(scratch);
     const int2 *anc = reinterpret_cast<const int2 *>(anchors);
-    const TableLayout lay = table_grid_ok(s, table_layout(s, false));
+    const TableLayout lay = table_grid_ok(s, table_layout(s, false, 0));
     const uint32_t njb = lay.jb ? (s.seq_len + lay.jb - 1) / lay.jb : 0;
 #define SPIKY_PT(IM, NCM)                                                                         \
     hipLaunchKernelGGL((k_prod_pairs_tbl<false, IM, NCM>), dim3(s.batch * s.n_detectors * njb),   \
@@ -896,7 +902,7 @@ hipError_t launch_backward_product(const ProductShape &s, const float *w, const 
                                                 s.n_outputs, 0.0, nullptr, st);
     if (e != hipSuccess) return e;
     const int2 *anc = reinterpret_cast<const int2 *>(anchors);
-    const TableLayout lay = table_grid_ok(s, table_layout(s, true));
+    const TableLayout lay = table_grid_ok(s, table_layout(s, true, int_mode ? 4 : 8));
     const uint32_t njb = lay.jb ? (s.seq_len + lay.jb - 1) / lay.jb : 0;
 #define SPIKY_BT(IM, NCM)                                                                         \
     hipLaunchKernelGGL((k_prod_pairs_tbl<true, IM, NCM>), dim3(s.batch * s.n_detectors * njb),    \

@@ -1005,17 +1005,18 @@ __global__ __launch_bounds__(256) void k_propagate_reduce(const float *__restric
 // samples; their input-gradient rows are accumulated in LDS and added to HBM
 // once.
 constexpr int kScatterThreads = 1024;
-constexpr int kScatterLds = 64 * 1024;
+constexpr int kScatterLds = 128 * 1024;
 
 __global__ __launch_bounds__(kScatterThreads) void k_propagate_scatter(
     const float *__restrict__ du_in, const int32_t *__restrict__ mi,
     const int2 *__restrict__ anchors, float *__restrict__ x_grad, uint32_t batch,
     uint32_t n_inputs, uint32_t n_detectors, uint32_t n_anchors, uint32_t samples_per_group) {
-    __shared__ float xg[kScatterLds / 4];
+    // fp64 sums: on gfx950 ds_add_f64 sustains ~20x the lanes a clock of ds_add_f32
+    __shared__ double xg[kScatterLds / 8];
     const uint32_t b0 = blockIdx.x * samples_per_group;
     const uint32_t nb = min(samples_per_group, batch - b0);
     const uint32_t n_el = nb * n_inputs;
-    for (uint32_t i = threadIdx.x; i < n_el; i += kScatterThreads) xg[i] = 0.0f;
+    for (uint32_t i = threadIdx.x; i < n_el; i += kScatterThreads) xg[i] = 0.0;
     __syncthreads();
     const uint64_t n_pairs = (uint64_t)nb * n_detectors;
     const size_t base = (size_t)b0 * n_detectors;
@@ -1028,12 +1029,12 @@ __global__ __launch_bounds__(kScatterThreads) void k_propagate_scatter(
         if (m < 0 || (uint32_t)m >= n_anchors) continue;
         const int2 a = anchors[(size_t)t * n_anchors + m];
         if ((uint32_t)a.x >= n_inputs || (uint32_t)a.y >= n_inputs) continue;
-        atomicAdd(&xg[bl * n_inputs + a.x], du);
-        atomicAdd(&xg[bl * n_inputs + a.y], -du);
+        atomicAdd(&xg[bl * n_inputs + a.x], (double)du);
+        atomicAdd(&xg[bl * n_inputs + a.y], -(double)du);
     }
     __syncthreads();
     float *dst = x_grad + (size_t)b0 * n_inputs;
-    for (uint32_t i = threadIdx.x; i < n_el; i += kScatterThreads) dst[i] += xg[i];
+    for (uint32_t i = threadIdx.x; i < n_el; i += kScatterThreads) dst[i] += (float)xg[i];
 }
 
 // keys_t[t][b] = idx[b][t] (u8), through a 64x64 LDS tile.
@@ -1247,7 +1248,7 @@ hipError_t launch_block_commit(const uint32_t *part, float *out, uint64_t n, uin
 bool tm_propagate_applies(const FcShape &s) {
     const uint64_t n_slices = (s.n_outputs + kTmCols - 1) / kTmCols;
     return s.batch >= 256 && s.n_entries <= (uint32_t)kTmMaxEntries && s.n_outputs % 4 == 0 &&
-           s.n_outputs >= 64 && s.n_inputs * 4 <= (uint32_t)kScatterLds &&
+           s.n_outputs >= 64 && s.n_inputs * 8 <= (uint32_t)kScatterLds &&
            n_slices * s.batch * s.n_detectors * 4 <= (4ull << 30);
 }
 
@@ -1369,7 +1370,7 @@ static hipError_t launch_propagate_finish(const FcShape &s, float *dpart, uint32
 // x_grad from du [B][T]
 static hipError_t launch_propagate_scatter(const FcShape &s, const float *du, const int32_t *min_idx,
                                            const int32_t *anchors, float *x_grad, hipStream_t st) {
-    const uint32_t spg = std::max<uint32_t>(1, std::min<uint32_t>(16, kScatterLds / 4 / s.n_inputs));
+    const uint32_t spg = std::max<uint32_t>(1, std::min<uint32_t>(16, kScatterLds / 8 / s.n_inputs));
     const uint32_t groups = (s.batch + spg - 1) / spg;
     hipLaunchKernelGGL(k_propagate_scatter, dim3(groups), dim3(kScatterThreads), 0, st, du,
                        min_idx, reinterpret_cast<const int2 *>(anchors), x_grad, s.batch,
