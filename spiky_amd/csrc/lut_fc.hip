@@ -573,11 +573,29 @@ __global__ __launch_bounds__(kWave) void k_bucket_samples(
     auto key_of = [&](uint32_t b) -> uint32_t {
         return kt ? (((kt[b] & 0xFFFFu) >> key_shift) & emask) : ((uint32_t)idx[(size_t)b * n_detectors + t] & emask);
     };
+    // up to kBsCache keys a lane stay in registers for both passes, all loaded
+    // up front (a batch of at most 64 * kBsCache samples)
+    constexpr int kBsCache = 16;
+    const bool cached = batch <= (uint32_t)(kWave * kBsCache);
+    uint32_t kc[kBsCache];
+    if (cached) {
+#pragma unroll
+        for (int u = 0; u < kBsCache; u++) {
+            const uint32_t b = u * kWave + lane;
+            kc[u] = b < batch ? key_of(b) : 0u;
+        }
+    }
     for (uint32_t e = lane; e < n_entries; e += kWave) cnt[e] = 0;
     __syncthreads();
-    for (uint32_t base = 0; base < batch; base += kWave) {
-        const uint32_t b = base + lane;
-        if (b < batch) atomicAdd(&cnt[key_of(b)], 1);
+    if (cached) {
+#pragma unroll
+        for (int u = 0; u < kBsCache; u++)
+            if (u * kWave + lane < batch) atomicAdd(&cnt[kc[u]], 1);
+    } else {
+        for (uint32_t base = 0; base < batch; base += kWave) {
+            const uint32_t b = base + lane;
+            if (b < batch) atomicAdd(&cnt[key_of(b)], 1);
+        }
     }
     __syncthreads();
     // exclusive scan of cnt[0..E) by one wavefront: each lane sums a contiguous run
@@ -604,10 +622,10 @@ __global__ __launch_bounds__(kWave) void k_bucket_samples(
     if (lane == kWave - 1) off_t[n_entries] = incl;
     __syncthreads();
     int32_t *smp_t = samples + (size_t)t * batch;
-    for (uint32_t base = 0; base < batch; base += kWave) {
+    // samples base .. base + 63 in order: ballot-ranked among equal keys
+    auto scatter = [&](uint32_t base, uint32_t key) {
         const uint32_t b = base + lane;
         const bool valid = b < batch;
-        const uint32_t key = valid ? key_of(b) : 0u;
         uint64_t peers = __ballot(valid);
         for (uint32_t bit = 0; bit < n_bits; bit++) {
             const bool kb = (key >> bit) & 1u;
@@ -625,6 +643,16 @@ __global__ __launch_bounds__(kWave) void k_bucket_samples(
             if (lane == leader) cnt[key] = pos + 1;
         }
         __syncthreads();
+    };
+    if (cached) {
+#pragma unroll
+        for (int u = 0; u < kBsCache; u++) {
+            if ((uint32_t)u * kWave >= batch) break;  // uniform
+            scatter((uint32_t)u * kWave, kc[u]);
+        }
+    } else {
+        for (uint32_t base = 0; base < batch; base += kWave)
+            scatter(base, base + lane < batch ? key_of(base + lane) : 0u);
     }
 }
 
