@@ -1102,6 +1102,68 @@ __global__ __launch_bounds__(256) void k_transpose_keys(const int32_t *__restric
     }
 }
 
+// The same transpose with 16-byte accesses both ways (n_detectors % 4 == 0,
+// pitch % 4 == 0): a thread reads four tables of a sample row and writes four
+// samples of a table row.
+__global__ __launch_bounds__(256) void k_transpose_keys4(const int32_t *__restrict__ idx,
+                                                         const int32_t *__restrict__ mi,
+                                                         const float *__restrict__ md,
+                                                         uint32_t *__restrict__ key_t,
+                                                         float *__restrict__ du_t,
+                                                         uint32_t batch, uint32_t pitch,
+                                                         uint32_t n_detectors, uint32_t n_anchors,
+                                                         uint32_t n_entries, uint32_t row_shift) {
+    __shared__ uint32_t tile[64][65];
+    __shared__ float dtile[64][65];
+    const uint32_t tb = blockIdx.x * 64;
+    const uint32_t bb = blockIdx.y * 64;
+    const uint32_t c4 = (threadIdx.x & 15) * 4;
+    const uint32_t r0 = threadIdx.x >> 4;
+#pragma unroll
+    for (uint32_t r = r0; r < 64; r += 16) {
+        const uint32_t b = bb + r, t = tb + c4;
+        uint32_t k[4] = {0u, 0u, 0u, 0u};
+        float dv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (b < batch && t < n_detectors) {
+            const size_t bt = (size_t)b * n_detectors + t;
+            const int4 iv = *reinterpret_cast<const int4 *>(idx + bt);
+            const int4 mv = *reinterpret_cast<const int4 *>(mi + bt);
+            const int ia[4] = {iv.x, iv.y, iv.z, iv.w}, ma[4] = {mv.x, mv.y, mv.z, mv.w};
+            float da[4] = {0.f, 0.f, 0.f, 0.f};
+            if (du_t) {
+                const float4 dd = *reinterpret_cast<const float4 *>(md + bt);
+                da[0] = dd.x; da[1] = dd.y; da[2] = dd.z; da[3] = dd.w;
+            }
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const uint32_t rm = (uint32_t)ia[c] & (n_entries - 1);
+                const int32_t m = ma[c];
+                const bool used = m >= 0 && (uint32_t)m < n_anchors;
+                const uint32_t ra = used ? (rm ^ (1u << m)) : rm;
+                k[c] = (rm << row_shift) | (ra << (row_shift + 16));
+                if (du_t) dv[c] = used ? (float)du_of_margin(da[c]) : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            tile[r][c4 + c] = k[c];
+            dtile[r][c4 + c] = dv[c];
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t r = r0; r < 64; r += 16) {
+        const uint32_t t = tb + r, b = bb + c4;
+        if (b < pitch && t < n_detectors) {
+            *reinterpret_cast<uint4 *>(key_t + (size_t)t * pitch + b) =
+                make_uint4(tile[c4][r], tile[c4 + 1][r], tile[c4 + 2][r], tile[c4 + 3][r]);
+            if (du_t)
+                *reinterpret_cast<float4 *>(du_t + (size_t)t * pitch + b) =
+                    make_float4(dtile[c4][r], dtile[c4 + 1][r], dtile[c4 + 2][r], dtile[c4 + 3][r]);
+        }
+    }
+}
+
 constexpr uint64_t kFoldUnits = 1024;
 
 uint32_t tm_spt(uint32_t batch) {
@@ -1297,9 +1359,14 @@ hipError_t launch_propagate_tm(const FcShape &s, const float *w, const float *g,
     float *du_t = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(scratch) + keys);
     float *dpart = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(scratch) + 2 * keys);
     const bool wide = tm_propagate_wide(s);
-    hipLaunchKernelGGL(k_transpose_keys, dim3((s.n_detectors + 63) / 64, (pitch + 63) / 64),
-                       dim3(256), 0, st, idx, min_idx, min_deltas, key_t, wide ? du_t : nullptr,
-                       s.batch, pitch, s.n_detectors, s.n_anchors, s.n_entries, wide ? 8u : 7u);
+    if (s.n_detectors % 4 == 0 && pitch % 4 == 0)
+        hipLaunchKernelGGL(k_transpose_keys4, dim3((s.n_detectors + 63) / 64, (pitch + 63) / 64),
+                           dim3(256), 0, st, idx, min_idx, min_deltas, key_t, wide ? du_t : nullptr,
+                           s.batch, pitch, s.n_detectors, s.n_anchors, s.n_entries, wide ? 8u : 7u);
+    else
+        hipLaunchKernelGGL(k_transpose_keys, dim3((s.n_detectors + 63) / 64, (pitch + 63) / 64),
+                           dim3(256), 0, st, idx, min_idx, min_deltas, key_t, wide ? du_t : nullptr,
+                           s.batch, pitch, s.n_detectors, s.n_anchors, s.n_entries, wide ? 8u : 7u);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const uint32_t n_slices = (s.n_outputs + kTmCols - 1) / kTmCols;
