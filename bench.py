@@ -282,6 +282,8 @@ def bench_projection(args):
         for k, (cnt, tot) in d.get_kernel_times(reset=True).items():
             ktimes[f"{name}.{k}"] = tot / max(cnt, 1)
     log(f"{ms:.3f} ms/step; kernels {ktimes}")
+    graph_ms = projection_graph_ms(step, args.steps)
+    log(f"graph replay: {graph_ms:.3f} ms/step")
     roofline = projection_roofline(l1, l2, head, x.detach(), B, ktimes)
     cpu = None
     if not args.no_cpu_baseline:
@@ -298,10 +300,38 @@ def bench_projection(args):
                    "layer1": "28x28 -> 48x48, 144 groups x 32 tables, 5 pairs, 5x5 fields, 16 targets",
                    "layer2": "48x48 -> 20x40, 25 groups x 64 tables, 6 pairs, 12x12 fields, 32 targets",
                    "head": "800 -> 10, 128 tables, 6 pairs", "parallelism": "single GPU"},
+        "graph_replay": {"ms_per_step": round(graph_ms, 4), "value": round(B / (graph_ms / 1e3), 1),
+                         "unit": "samples/s",
+                         "note": "the same step captured once in a HIP graph (torch.cuda.CUDAGraph) and "
+                                 "replayed: the same kernels without the host's per-launch work"},
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)
+
+
+def projection_graph_ms(step, steps):
+    """Milliseconds per step of `step` captured in a HIP graph and replayed
+    (warmed up on a side stream first, as graph capture requires)."""
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
 
 
 def projection_roofline(l1, l2, head, x, B, ktimes):
@@ -313,19 +343,18 @@ def projection_roofline(l1, l2, head, x, B, ktimes):
     synapse weight (forward and propagate families) or weight-gradient word
     (weight-gradient family) once, plus the activations."""
     import numpy as np
-    import oracle
-    layers = {"layer1": (l1, 784, 2304, 5), "layer2": (l2, 2304, 800, 6)}
-    acts = {"layer1": x.cpu().numpy().reshape(-1)}
     import torch
+    layers = {"layer1": (l1, 784, 2304, 5), "layer2": (l2, 2304, 800, 6)}
+    # the lookup indices of this input, from the layers' own forward
     with torch.no_grad():
-        acts["layer2"] = l1(x).cpu().numpy().reshape(-1)
+        r1 = l1.forward_step(x.reshape(B, 1, 28, 28))
+        r2 = l2.forward_step(r1[0].reshape(B, 1, 48, 48))
+    idxs = {"layer1": r1[1].cpu().numpy(), "layer2": r2[1].cpu().numpy()}
     fams = {}
     for name, (layer, I, O, Nc) in layers.items():
         offs, tg = layer._lut_dm.lookup_connectivity()
         T = layer.n_detectors()
-        idx = oracle.check_detectors(acts[name], layer._detector_anchors.cpu().numpy(), B, I, T, Nc,
-                                     train=False)
-        neuron = (np.arange(T)[None, :] * (1 << Nc) + idx.reshape(B, T)).reshape(-1)
+        neuron = (np.arange(T)[None, :] * (1 << Nc) + idxs[name].reshape(B, T)).reshape(-1)
         hits = int(np.sum(offs[neuron + 1] - offs[neuron]))
         n_syn = int(tg.size)
         side = B * I * 4 + B * O * 4 + B * T * 12

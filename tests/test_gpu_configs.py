@@ -195,6 +195,66 @@ def test_config2_projection_stack(oracle, cuda_device):
     sparse_check(l1, np_(x), y1, np_(y1.grad), x.grad, 784, 2304, 5)
 
 
+def test_config2_graph_replay(cuda_device):
+    """The config-2 step captured in a HIP graph (as bench.py --config 2 times
+    it) and replayed four times, with eager work and a synchronisation before
+    each replay.  Every replay must give the eager step's results: the output
+    and the head's and layer 2's weight gradients bit for bit; layer 1's weight
+    gradient and the input gradient within 1e-5 of each row's largest value
+    (their upstream gradients come from fp32 atomics, whose order varies from
+    run to run, eager or replayed)."""
+    from bench import build_projection_stack
+    dev = cuda_device
+    B = 128
+    l1, l2, head = build_projection_stack(dev)
+    gen = torch.Generator(device=dev).manual_seed(3)
+    with torch.no_grad():
+        for layer in (l1, l2, head):
+            layer._weights.normal_(0.0, 0.01, generator=gen)
+    gx = torch.Generator(device=dev).manual_seed(1)
+    x = torch.rand(B, 1, 28, 28, device=dev, generator=gx)
+    x = (x * (torch.rand(B, 1, 28, 28, device=dev, generator=gx) > 0.8)).requires_grad_(True)
+    g = torch.randn(B, 1, 10, device=dev, generator=gx)
+    params = [l1._weights, l2._weights, head._weights]
+    res = {}
+
+    def step():
+        for p_ in params:
+            p_.grad = None
+        x.grad = None
+        out = head(l2(l1(x).reshape(B, 1, 48, 48)).reshape(B, 1, 800))
+        out.backward(g)
+        res["out"] = out
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    ref_out = res["out"].detach().clone()
+    ref_w = [p_.grad.detach().clone() for p_ in params]
+    ref_x = x.grad.detach().clone()
+    print("[config2 graph] capture", flush=True)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    gout, gw, gxg = res["out"], [p_.grad for p_ in params], x.grad
+    for rep in range(4):
+        with torch.no_grad():
+            torch.randn(1 << 20, device=dev).mul_(2.0)  # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        print(f"[config2 graph] replay {rep}", flush=True)
+        assert torch.equal(gout, ref_out)
+        assert torch.equal(gw[1], ref_w[1]) and torch.equal(gw[2], ref_w[2])
+        w1, r1 = gw[0].cpu().numpy(), ref_w[0].cpu().numpy()
+        assert np.all(np.abs(w1 - r1) <= 1e-5 * np.abs(r1).max())
+        _xg_close(gxg.cpu().numpy(), ref_x.cpu().numpy(), B, 784)
+
+
 @pytest.mark.parametrize("B", [8, 300])
 def test_nan_inputs(oracle, cuda_device, B):
     """NaN inputs through the detector check (the LDS-staged kernel at B = 300,
