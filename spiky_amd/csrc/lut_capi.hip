@@ -430,6 +430,8 @@ int spiky_lut_set_sparse_connectivity(spiky_lut_manager *m, const int64_t *syn_o
                     uniform = false;
             }
         }
+        // the output-major index addresses synapses with 32-bit offsets
+        if (n_synapses >= (1ull << 31)) uniform = false;
         m->uniform = uniform;
         m->in_offsets.clear();
         m->in_pairs.clear();
@@ -441,14 +443,19 @@ int spiky_lut_set_sparse_connectivity(spiky_lut_manager *m, const int64_t *syn_o
             }
             for (uint32_t j = 0; j < m->n_outputs; j++) cnt[j + 1] += cnt[j];
             m->in_offsets = cnt;
-            m->in_pairs.assign((size_t)cnt[m->n_outputs] * 2, 0);
+            // entry p: {t, offset of synapse k of the detector's row 0, synapses a row, 0}; the
+            // neurons of a detector have equal lengths, so row e's synapse k is at
+            // offset + e * length
+            m->in_pairs.assign((size_t)cnt[m->n_outputs] * 4, 0);
             std::vector<int64_t> pos(cnt.begin(), cnt.end() - 1);
             for (uint32_t t = 0; t < m->n_detectors; t++) {
                 const uint64_t n0 = (uint64_t)t * E;
+                const int64_t len0 = syn_offsets[n0 + 1] - syn_offsets[n0];
                 for (int64_t s = syn_offsets[n0]; s < syn_offsets[n0 + 1]; s++) {
                     const int64_t p = pos[syn_targets[s]]++;
-                    m->in_pairs[2 * p] = (int32_t)t;
-                    m->in_pairs[2 * p + 1] = (int32_t)(s - syn_offsets[n0]);
+                    m->in_pairs[4 * p] = (int32_t)t;
+                    m->in_pairs[4 * p + 1] = (int32_t)s;
+                    m->in_pairs[4 * p + 2] = (int32_t)len0;
                 }
             }
         }

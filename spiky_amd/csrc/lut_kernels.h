@@ -149,8 +149,10 @@ struct SparseShape {
 
 // Output-major index for the exact forward, valid when every lookup neuron of
 // a detector has the same target list ("uniform" topology, ProjectionLUTLayer):
-// for output j, in_pairs[in_offsets[j] .. in_offsets[j+1]) are (t, k) pairs in
-// ascending (t, k): synapse k of detector t's neurons targets j.
+// for output j, in_pairs[in_offsets[j] .. in_offsets[j+1]) are 4-int entries
+// {t, o, len, 0} in ascending (t, k): synapse k of detector t's neurons targets
+// j, o = syn_offsets[t * E] + k and len the synapses a neuron of t (row e's
+// synapse k is at o + e * len; total synapses below 2^31).
 hipError_t launch_fill_sparse_uniform(const SparseShape &s, const float *w, const int32_t *idx,
                                       const int64_t *syn_offsets, const int64_t *in_offsets,
                                       const int32_t *in_pairs, float *out, bool int_mode,

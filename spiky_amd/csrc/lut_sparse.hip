@@ -46,7 +46,7 @@ template <bool INT_MODE>
 __global__ __launch_bounds__(kBlock) void k_fill_sparse_uniform(
     const float *__restrict__ w, const int32_t *__restrict__ idx,
     const int64_t *__restrict__ syn_offsets, const int64_t *__restrict__ in_offsets,
-    const int2 *__restrict__ in_pairs, float *__restrict__ out, uint32_t batch,
+    const int4 *__restrict__ in_pairs, float *__restrict__ out, uint32_t batch,
     uint32_t n_outputs, uint32_t n_detectors, uint32_t n_entries, double int_rescaler) {
     const uint64_t item = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
     if (item >= (uint64_t)batch * n_outputs) return;
@@ -56,13 +56,15 @@ __global__ __launch_bounds__(kBlock) void k_fill_sparse_uniform(
     float acc = out[item];
     int32_t iacc = __float_as_int(acc);
     const uint32_t emask = n_entries - 1;
-    // unrolled so that several pairs' dependent loads (index, neuron offset,
-    // weight) are in flight at once; the adds stay in ascending pair order
+    // unrolled so that several pairs' dependent loads (entry, index, weight)
+    // are in flight at once; the adds stay in ascending pair order.  An entry
+    // holds the synapse's offset in the detector's row 0 and the row length,
+    // so the weight's address needs no neuron offset load.
 #pragma unroll 8
     for (int64_t p = in_offsets[j]; p < in_offsets[j + 1]; p++) {
-        const int2 tk = in_pairs[p];
-        const uint32_t n = (uint32_t)tk.x * n_entries + ((uint32_t)ib[tk.x] & emask);
-        const double wt = (double)w[syn_offsets[n] + tk.y];
+        const int4 tk = in_pairs[p];
+        const uint32_t e = (uint32_t)ib[tk.x] & emask;
+        const double wt = (double)w[(uint32_t)tk.y + e * (uint32_t)tk.z];
         if (INT_MODE)
             iacc = wrap_add(iacc, (int32_t)(wt * kDenom32 * int_rescaler));
         else
@@ -253,7 +255,7 @@ hipError_t launch_fill_sparse_uniform(const SparseShape &s, const float *w, cons
                                       double int_rescaler, hipStream_t st) {
     const uint64_t n = (uint64_t)s.fc.batch * s.fc.n_outputs;
     if (n == 0) return hipSuccess;
-    const int2 *pairs = reinterpret_cast<const int2 *>(in_pairs);
+    const int4 *pairs = reinterpret_cast<const int4 *>(in_pairs);
     if (int_mode)
         hipLaunchKernelGGL(k_fill_sparse_uniform<true>, dim3(blocks_for(n)), dim3(kBlock), 0, st,
                            w, idx, syn_offsets, in_offsets, pairs, out, s.fc.batch, s.fc.n_outputs,
