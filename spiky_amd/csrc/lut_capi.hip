@@ -128,11 +128,12 @@ struct spiky_lut_manager {
     bool has_connectivity = false;
     std::vector<int64_t> syn_offsets;
     std::vector<int32_t> syn_targets;
+    std::vector<int32_t> syn_neuron;  // lookup neuron of each synapse
     std::vector<int64_t> in_offsets;
     std::vector<int32_t> in_pairs;
     bool uniform = false;
     uint32_t max_groups = 0;
-    DeviceBuffer d_syn_offsets, d_syn_targets, d_in_offsets, d_in_pairs;
+    DeviceBuffer d_syn_offsets, d_syn_targets, d_syn_neuron, d_in_offsets, d_in_pairs;
     bool dirty = true;
 
     // forward and backward keep separate scratch so that calls issued on
@@ -217,6 +218,7 @@ struct spiky_lut_manager {
     void sync_connectivity() {
         d_syn_offsets.upload(syn_offsets.data(), syn_offsets.size() * sizeof(int64_t), dirty);
         d_syn_targets.upload(syn_targets.data(), syn_targets.size() * sizeof(int32_t), dirty);
+        d_syn_neuron.upload(syn_neuron.data(), syn_neuron.size() * sizeof(int32_t), dirty);
         if (uniform) {
             d_in_offsets.upload(in_offsets.data(), in_offsets.size() * sizeof(int64_t), dirty);
             d_in_pairs.upload(in_pairs.data(), in_pairs.size() * sizeof(int32_t), dirty);
@@ -325,6 +327,7 @@ void spiky_lut_destroy(spiky_lut_manager *m) {
     m->scratch_fwd.release();
     m->d_syn_offsets.release();
     m->d_syn_targets.release();
+    m->d_syn_neuron.release();
     m->d_in_offsets.release();
     m->d_in_pairs.release();
     delete m;
@@ -415,6 +418,9 @@ int spiky_lut_set_sparse_connectivity(spiky_lut_manager *m, const int64_t *syn_o
                 throw ValueError("synapse target out of range");
         m->syn_offsets.assign(syn_offsets, syn_offsets + nl + 1);
         m->syn_targets.assign(syn_targets, syn_targets + n_synapses);
+        m->syn_neuron.assign(n_synapses, 0);
+        for (uint64_t n = 0; n < nl; n++)
+            for (int64_t s = syn_offsets[n]; s < syn_offsets[n + 1]; s++) m->syn_neuron[s] = (int32_t)n;
         m->max_groups = max_groups;
         // uniform topology: all lookup neurons of a detector share one ordered target list
         const uint32_t E = (uint32_t)(m->n_lookup / m->n_detectors);  // rows of a table
@@ -693,11 +699,12 @@ int spiky_lut_backward_backprop(spiky_lut_manager *m, float *weights, uint32_t b
                           "convert_integers_to_floats");
             if (target) {
                 const uint64_t n_syn = m->syn_targets.size();
-                if (overwrite) check_hip(spiky::launch_zero(target, n_syn, st), "zero w_grad");
                 void *scr = m->scratch.ensure(spiky::wgrad_sparse_scratch_bytes(ss));
                 m->timed("gather_w_gradients_sparse", st, [&] {
-                    check_hip(spiky::launch_wgrad_sparse(ss, output_grad, lookup_indices, off, tg, target,
-                                                         lr, m->int_mode, m->int_rescaler, scr, n_syn, st),
+                    check_hip(spiky::launch_wgrad_sparse(ss, output_grad, lookup_indices, off, tg,
+                                                         (const int32_t *)m->d_syn_neuron.ptr, target,
+                                                         lr, overwrite, m->int_mode, m->int_rescaler, scr,
+                                                         n_syn, st),
                               "gather_w_gradients_sparse");
                 });
             }

@@ -174,10 +174,13 @@ hipError_t launch_propagate_sparse(const SparseShape &s, const float *w, const f
 // Scratch: the same bucket arrays as the FC path.
 size_t wgrad_sparse_scratch_bytes(const SparseShape &s);
 
+// syn_neuron[s] = the lookup neuron of synapse s.  overwrite: target starts
+// from zero (it is not read).
 hipError_t launch_wgrad_sparse(const SparseShape &s, const float *g, const int32_t *idx,
                                const int64_t *syn_offsets, const int32_t *syn_targets,
-                               float *target, double lr, bool int_mode, double int_rescaler,
-                               void *scratch, uint64_t n_synapses, hipStream_t st);
+                               const int32_t *syn_neuron, float *target, double lr, bool overwrite,
+                               bool int_mode, double int_rescaler, void *scratch,
+                               uint64_t n_synapses, hipStream_t st);
 
 // ---- product mode (concatenation_product == False, lut_product.hip) ---------
 // Sequence-concat over sparse connectivity (lut_seq_sparse.hip).  The lookup

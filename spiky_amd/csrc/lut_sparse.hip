@@ -16,8 +16,9 @@
 //                          main/alt group dots in fp64 and the min-margin anchor
 //                          update.
 //   k_wgrad_sparse_rowsum  one thread per synapse: sums lr*g over the samples
-//                          bucketed on its lookup neuron, ascending (bit-identical
-//                          to the reference CPU path), and writes it once.
+//                          bucketed on its lookup neuron (read from a per-synapse
+//                          neuron index), ascending (bit-identical to the
+//                          reference CPU path), and writes it once.
 #include "lut_kernels.h"
 
 #include <algorithm>
@@ -200,36 +201,34 @@ __global__ __launch_bounds__(kBlock) void k_propagate_sparse(
 
 // gather_w_gradients_non_seq_sparse_logic (proto:1501-1545) with
 // gather_weight_gradients_sparse (proto:584-714), one thread per synapse.
-// The neuron of synapse s is found by binary search in syn_offsets.
-template <bool INT_MODE>
+// The neuron of synapse s is syn_neuron[s].  With OVERWRITE the target starts
+// from zero and is not read (the caller need not clear it).
+template <bool INT_MODE, bool OVERWRITE>
 __global__ __launch_bounds__(kBlock) void k_wgrad_sparse_rowsum(
     const float *__restrict__ g, const int32_t *__restrict__ offsets,
-    const int32_t *__restrict__ samples, const int64_t *__restrict__ syn_offsets,
+    const int32_t *__restrict__ samples, const int32_t *__restrict__ syn_neuron,
     const int32_t *__restrict__ syn_targets, float *__restrict__ target, uint32_t batch,
-    uint32_t n_outputs, uint32_t n_entries, uint64_t n_lookup, uint64_t n_synapses, double lr,
-    double int_rescaler) {
+    uint32_t n_outputs, uint32_t n_entries, uint64_t n_synapses, double lr, double int_rescaler) {
     const uint64_t s = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
     if (s >= n_synapses) return;
-    // largest n with syn_offsets[n] <= s
-    uint64_t lo = 0, hi = n_lookup;
-    while (hi - lo > 1) {
-        const uint64_t mid = (lo + hi) / 2;
-        if ((uint64_t)syn_offsets[mid] <= s) lo = mid; else hi = mid;
-    }
-    const uint32_t t = (uint32_t)(lo / n_entries);
-    const uint32_t e = (uint32_t)(lo % n_entries);
+    const uint32_t n = (uint32_t)syn_neuron[s];
+    const uint32_t t = n / n_entries;
+    const uint32_t e = n % n_entries;
     const int32_t *off_t = offsets + (size_t)t * (n_entries + 1);
     const int32_t beg = off_t[e], end = off_t[e + 1];
     const uint32_t tg = (uint32_t)syn_targets[s];
+    const float init = OVERWRITE ? 0.0f : target[s];
     if (beg == end || tg >= n_outputs) {
         if (INT_MODE) {
-            const double y = (double)__float_as_int(target[s]) * kDenom32Reciproc;
+            const double y = (double)__float_as_int(init) * kDenom32Reciproc;
             target[s] = (float)(y / int_rescaler);
+        } else if (OVERWRITE) {
+            target[s] = 0.0f;
         }
         return;
     }
     const int32_t *smp = samples + (size_t)t * batch;
-    float acc = target[s];
+    float acc = init;
     int32_t iacc = __float_as_int(acc);
     // unrolled: several samples' g loads in flight, the adds in ascending order
 #pragma unroll 4
@@ -321,24 +320,25 @@ size_t wgrad_sparse_scratch_bytes(const SparseShape &s) {
 
 hipError_t launch_wgrad_sparse(const SparseShape &s, const float *g, const int32_t *idx,
                                const int64_t *syn_offsets, const int32_t *syn_targets,
-                               float *target, double lr, bool int_mode, double int_rescaler,
-                               void *scratch, uint64_t n_synapses, hipStream_t st) {
+                               const int32_t *syn_neuron, float *target, double lr, bool overwrite,
+                               bool int_mode, double int_rescaler, void *scratch,
+                               uint64_t n_synapses, hipStream_t st) {
+    (void)syn_offsets;
     if (n_synapses == 0) return hipSuccess;
     int32_t *offsets = reinterpret_cast<int32_t *>(scratch);
     int32_t *samples = offsets + (size_t)s.fc.n_detectors * (s.fc.n_entries + 1);
     hipError_t e = launch_bucket_samples(s.fc, idx, offsets, samples, st);
     if (e != hipSuccess) return e;
-    const uint64_t n_lookup = (uint64_t)s.fc.n_detectors * s.fc.n_entries;
-    if (int_mode)
-        hipLaunchKernelGGL(k_wgrad_sparse_rowsum<true>, dim3(blocks_for(n_synapses)), dim3(kBlock),
-                           0, st, g, offsets, samples, syn_offsets, syn_targets, target,
-                           s.fc.batch, s.fc.n_outputs, s.fc.n_entries, n_lookup, n_synapses, lr,
-                           int_rescaler);
-    else
-        hipLaunchKernelGGL(k_wgrad_sparse_rowsum<false>, dim3(blocks_for(n_synapses)),
-                           dim3(kBlock), 0, st, g, offsets, samples, syn_offsets, syn_targets,
-                           target, s.fc.batch, s.fc.n_outputs, s.fc.n_entries, n_lookup,
-                           n_synapses, lr, int_rescaler);
+#define SPIKY_WS(IM, OW)                                                                          \
+    hipLaunchKernelGGL((k_wgrad_sparse_rowsum<IM, OW>), dim3(blocks_for(n_synapses)), dim3(kBlock), \
+                       0, st, g, offsets, samples, syn_neuron, syn_targets, target, s.fc.batch,   \
+                       s.fc.n_outputs, s.fc.n_entries, n_synapses, lr, int_rescaler)
+    if (int_mode) {
+        if (overwrite) SPIKY_WS(true, true); else SPIKY_WS(true, false);
+    } else {
+        if (overwrite) SPIKY_WS(false, true); else SPIKY_WS(false, false);
+    }
+#undef SPIKY_WS
     return hipGetLastError();
 }
 
