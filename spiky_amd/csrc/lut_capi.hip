@@ -511,7 +511,7 @@ int spiky_lut_forward_step(spiky_lut_manager *m, const float *weights, uint32_t 
             }
         } else {
             m->sync_connectivity();
-            spiky::SparseShape ss{s, m->max_groups};
+            spiky::SparseShape ss{s, m->max_groups, m->uniform};
             const int64_t *off = (const int64_t *)m->d_syn_offsets.ptr;
             if (m->uniform) {
                 m->timed("fill_outputs_sparse", st, [&] {
@@ -684,7 +684,7 @@ int spiky_lut_backward_backprop(spiky_lut_manager *m, float *weights, uint32_t b
             }
         } else {
             m->sync_connectivity();
-            spiky::SparseShape ss{s, m->max_groups};
+            spiky::SparseShape ss{s, m->max_groups, m->uniform};
             const int64_t *off = (const int64_t *)m->d_syn_offsets.ptr;
             const int32_t *tg = (const int32_t *)m->d_syn_targets.ptr;
             m->timed("propagate_sparse", st, [&] {

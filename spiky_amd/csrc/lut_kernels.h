@@ -145,6 +145,7 @@ hipError_t launch_zero(float *buf, uint64_t n, hipStream_t st);
 struct SparseShape {
     FcShape fc;            // n_outputs, n_detectors, n_entries ... as above
     uint32_t max_groups;   // max forward groups (of fc.ogs synapses) per lookup neuron
+    bool uniform = false;  // every lookup neuron of a detector has the same synapse count
 };
 
 // Output-major index for the exact forward, valid when every lookup neuron of

@@ -146,7 +146,7 @@ __global__ __launch_bounds__(kBlock) void k_propagate_sparse(
     const int64_t *__restrict__ syn_offsets, const int32_t *__restrict__ syn_targets,
     float *__restrict__ x_grad, uint32_t n_inputs, uint32_t n_outputs, uint32_t n_detectors,
     uint32_t n_anchors, uint32_t n_entries, uint32_t ogs, uint32_t max_groups, uint64_t n_items,
-    double int_rescaler) {
+    double int_rescaler, bool uniform) {
     constexpr int kSpLanes = sp_lanes<INT_MODE>();
     const uint64_t gid = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
     const uint64_t item = gid / kSpLanes;
@@ -156,24 +156,32 @@ __global__ __launch_bounds__(kBlock) void k_propagate_sparse(
     const uint64_t bt = item / max_groups;
     const uint32_t t = (uint32_t)(bt % n_detectors);
     const uint32_t b = (uint32_t)(bt / n_detectors);
+    // uniform rows: row e of detector t starts at o0 + e * len, read beside the
+    // index instead of after it
+    const int64_t o0 = uniform ? syn_offsets[(size_t)t * n_entries] : 0;
+    const int64_t len = uniform ? syn_offsets[(size_t)t * n_entries + 1] - o0 : 0;
     const int32_t m = mi[bt];
     if (m < 0 || (uint32_t)m >= n_anchors) return;
     const uint32_t r = (uint32_t)idx[bt] & (n_entries - 1);
     const uint32_t nm = t * n_entries + r;
     const uint32_t na = t * n_entries + (r ^ (1u << m));
+    const int64_t bm = uniform ? o0 + (int64_t)r * len : syn_offsets[nm];
+    const int64_t em = uniform ? bm + len : syn_offsets[nm + 1];
+    const int64_t ba = uniform ? o0 + (int64_t)(r ^ (1u << m)) * len : syn_offsets[na];
+    const int64_t ea = uniform ? ba + len : syn_offsets[na + 1];
     const float *gb = g + (size_t)b * n_outputs;
     double ms = 0.0, as = 0.0;
     {
-        const int64_t s0 = syn_offsets[nm] + (int64_t)grp * ogs;
-        const int64_t s1 = min(s0 + (int64_t)ogs, syn_offsets[nm + 1]);
+        const int64_t s0 = bm + (int64_t)grp * ogs;
+        const int64_t s1 = min(s0 + (int64_t)ogs, em);
         for (int64_t s = s0 + l; s < s1; s += kSpLanes) {
             const uint32_t tg = (uint32_t)syn_targets[s];
             if (tg < n_outputs) ms += (double)w[s] * (double)gb[tg];
         }
     }
     {
-        const int64_t s0 = syn_offsets[na] + (int64_t)grp * ogs;
-        const int64_t s1 = min(s0 + (int64_t)ogs, syn_offsets[na + 1]);
+        const int64_t s0 = ba + (int64_t)grp * ogs;
+        const int64_t s1 = min(s0 + (int64_t)ogs, ea);
         for (int64_t s = s0 + l; s < s1; s += kSpLanes) {
             const uint32_t tg = (uint32_t)syn_targets[s];
             if (tg < n_outputs) as += (double)w[s] * (double)gb[tg];
@@ -303,13 +311,13 @@ hipError_t launch_propagate_sparse(const SparseShape &s, const float *w, const f
                            st, w, g, idx, min_deltas, min_idx, ap, syn_offsets, syn_targets,
                            x_grad, s.fc.n_inputs, s.fc.n_outputs, s.fc.n_detectors,
                            s.fc.n_anchors, s.fc.n_entries, s.fc.ogs, s.max_groups, n_items,
-                           int_rescaler);
+                           int_rescaler, s.uniform);
     else
         hipLaunchKernelGGL(k_propagate_sparse<false>, dim3(blocks_for(n_threads)), dim3(kBlock), 0,
                            st, w, g, idx, min_deltas, min_idx, ap, syn_offsets, syn_targets,
                            x_grad, s.fc.n_inputs, s.fc.n_outputs, s.fc.n_detectors,
                            s.fc.n_anchors, s.fc.n_entries, s.fc.ogs, s.max_groups, n_items,
-                           int_rescaler);
+                           int_rescaler, s.uniform);
     return hipGetLastError();
 }
 
