@@ -272,9 +272,47 @@ __global__ __launch_bounds__(kBlock) void k_fill_seq(
 // every sum unchanged.
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+// A workgroup barrier that orders LDS only: this wave's LDS accesses are complete
+// before it, while its vector-memory loads (an LDS DMA) may still be in flight.
+// __syncthreads' fence would wait for those as well.
+__device__ __forceinline__ void lds_barrier() {
+    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+}
+
+// LDS byte address of a __shared__ location
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p;
+}
+// A 16-byte LDS DMA per lane: global g -> LDS byte address lds + 16 * lane (lds
+// is the wavefront's base).  Issued as an instruction the compiler does not see
+// into: with the builtin, every later LDS access of the kernel waits for the
+// DMA, since the compiler cannot tell the destination apart from the other LDS
+// arrays.  The caller waits for it with an explicit vmcnt before reading the
+// destination.  M0 is restored, so the compiler's own use of it is unaffected.
+// For a load issued before it and used after it, the compiler's vmcnt wait
+// counts too few loads behind that one: the wait is only stricter (in order).
+__device__ __forceinline__ void dma16_unseen(const void *g, uint32_t lds) {
+    const uint32_t a = __builtin_amdgcn_readfirstlane(lds);
+    uint32_t keep;
+    __asm__ volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %2, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(keep)
+        : "s"(a), "v"(g)
+        : "memory");
+}
+
 constexpr int kSfThreads = 1024;
 constexpr int kSfTabFloats = 32768;   // 128 KiB sub-table slice
 constexpr int kSfItems = 1024;        // items sorted per chunk of a bucket
+static_assert(kSfItems % kSfThreads == 0, "whole item rows per thread");
 constexpr int kSfPe = 2048;           // distances S - 1
 constexpr int kSfLenClasses = 256;    // item length classes of the longest-first order
 
@@ -348,55 +386,75 @@ __global__ __launch_bounds__(kSfThreads) void k_fill_seq_lds(
         const uint32_t it = u * kSfThreads + tid;
         rr[u] = (int32_t)it < end - beg ? (uint32_t)smp[beg + it] : 0u;
     }
-    // stage the slice: C / 4 lanes per row, 16-byte loads (O % 4 == 0)
-    for (uint32_t e0 = 0; e0 < n_e; e0 += 8 * kSfThreads) {
-        f32x4 v[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const uint32_t e = e0 + u * kSfThreads + tid;
-            const uint32_t r = e / (C / 4), c4 = (e % (C / 4)) * 4;
-            v[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (e < n_e && c0 + c4 < n_outputs)
-                v[u] = *reinterpret_cast<const f32x4 *>(sub + (size_t)r * n_outputs + c4);
-        }
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const uint32_t e = e0 + u * kSfThreads + tid;
-            if (e < n_e) *reinterpret_cast<f32x4 *>(tab + (e / (C / 4)) * C + (e % (C / 4)) * 4) = v[u];
-        }
-    }
+    // the positional indices first: their loads are waited for before the
+    // table's are issued
     for (uint32_t d = tid; d + 1 < seq; d += kSfThreads)
         ptab[d] = (uint16_t)(rec_idx(ppack[(size_t)t * (seq - 1) + d]) & pmask);
     if (tid < (uint32_t)C) tab[sub_rows * C + tid] = 0.0f;
+    // the first chunk's item rows, in LDS before the table's loads are issued
+    // (stored by every lane, 0 past the chunk's end: no load is left pending
+    // on any path, which would make the compiler wait for the DMA as well)
+#pragma unroll
+    for (int u = 0; u < kSfItems / kSfThreads; u++) irow[u * kSfThreads + tid] = rr[u];
+    // stage the slice: C / 4 lanes per row, 16-byte pieces (O % 4 == 0), piece e
+    // at byte 16 e of the [row][C] image.  A slice inside the row goes by LDS DMA,
+    // so the first chunk's counting sort runs while it lands (the walk waits for
+    // it); a slice past the row's end, through registers with zeros past it.
+    const bool slice_dma = c0 + C <= n_outputs;  // uniform
+    if (slice_dma) {
+        const uint32_t tab_lds = lds_addr(tab);
+        for (uint32_t e0 = 0; e0 < n_e; e0 += kSfThreads) {
+            const uint32_t e = e0 + tid;
+            if (e < n_e) {
+                const uint32_t r = e / (C / 4), c4 = (e % (C / 4)) * 4;
+                dma16_unseen(sub + (size_t)r * n_outputs + c4, tab_lds + (e0 + wave * kWave) * 16);
+            }
+        }
+    } else {
+        for (uint32_t e0 = 0; e0 < n_e; e0 += 8 * kSfThreads) {
+            f32x4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const uint32_t e = e0 + u * kSfThreads + tid;
+                const uint32_t r = e / (C / 4), c4 = (e % (C / 4)) * 4;
+                v[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+                if (e < n_e && c0 + c4 < n_outputs)
+                    v[u] = *reinterpret_cast<const f32x4 *>(sub + (size_t)r * n_outputs + c4);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const uint32_t e = e0 + u * kSfThreads + tid;
+                if (e < n_e) *reinterpret_cast<f32x4 *>(tab + (e / (C / 4)) * C + (e % (C / 4)) * 4) = v[u];
+            }
+        }
+        // vmcnt(0), as the compiler's own wait: no load of this branch stays
+        // pending where it joins the DMA branch
+        __builtin_amdgcn_s_waitcnt(0xF70);
+    }
 
     // key record words of positions i (.y words)
     const uint32_t *kw = reinterpret_cast<const uint32_t *>(kp) + 1;
-    for (int32_t k0 = beg; k0 < end; k0 += kSfItems) {
-        const uint32_t n = (uint32_t)min((int32_t)kSfItems, end - k0);
-        if (k0 != beg) {
-#pragma unroll
-            for (int u = 0; u < kSfItems / kSfThreads; u++) {
-                const uint32_t it = u * kSfThreads + tid;
-                rr[u] = it < n ? (uint32_t)smp[k0 + it] : 0u;
-            }
-        }
-        __syncthreads();  // staging done / the previous chunk is done with keys and irow
+    // One chunk of the bucket's items, whose rows are in irow: the longest-first
+    // sort and the walk.  The first chunk runs outside the loop that loads the
+    // later chunks' rows, so nothing but the table DMA is in flight before the
+    // walk's wait for it, and the sort overlaps the DMA.
+    auto run_chunk = [&](int32_t k0, uint32_t n) {
+        lds_barrier();  // the chunk's item rows in irow
         // Longest first: a counting sort of the items on (S - 1 - j) >> jsh (at most
         // kSfLenClasses classes; the order within a class is arbitrary), keys[pos]
         // = the item's number in the chunk.
         for (uint32_t k = tid; k < (uint32_t)kSfLenClasses; k += kSfThreads) jhist[k] = 0;
-        __syncthreads();
+        lds_barrier();
         uint32_t cls[kSfItems / kSfThreads], rank[kSfItems / kSfThreads];
 #pragma unroll
         for (int u = 0; u < kSfItems / kSfThreads; u++) {
             const uint32_t it = u * kSfThreads + tid;
             if (it < n) {
-                irow[it] = rr[u];
-                cls[u] = (seq - 1 - rr[u] % seq) >> jsh;
+                cls[u] = (seq - 1 - irow[it] % seq) >> jsh;
                 rank[u] = atomicAdd(&jhist[cls[u]], 1u);
             }
         }
-        __syncthreads();
+        lds_barrier();
         if (wave == 0) {  // exclusive scan of the class counts
             constexpr int kPerLane = kSfLenClasses / kWave;
             uint32_t c[kPerLane], sum = 0;
@@ -418,13 +476,15 @@ __global__ __launch_bounds__(kSfThreads) void k_fill_seq_lds(
                 run += c[k];
             }
         }
-        __syncthreads();
+        lds_barrier();
 #pragma unroll
         for (int u = 0; u < kSfItems / kSfThreads; u++) {
             const uint32_t it = u * kSfThreads + tid;
             if (it < n) keys[jhist[cls[u]] + rank[u]] = it;
         }
         if (tid == 0) next_item = 0;
+        // the table slice has landed (this wave's DMA; the barrier, everyone's)
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         // items are taken kSlots at a time, longest first; the next group's rows
         // and first key records are fetched while the current group runs
@@ -514,6 +574,19 @@ __global__ __launch_bounds__(kSfThreads) void k_fill_seq_lds(
 #pragma unroll
             for (int k = 0; k < kPer; k++) rec[k] = nrec[k];
         }
+    };
+    run_chunk(beg, (uint32_t)min((int32_t)kSfItems, end - beg));
+    for (int32_t k0 = beg + kSfItems; k0 < end; k0 += kSfItems) {
+        const uint32_t n = (uint32_t)min((int32_t)kSfItems, end - k0);
+#pragma unroll
+        for (int u = 0; u < kSfItems / kSfThreads; u++) {
+            const uint32_t it = u * kSfThreads + tid;
+            rr[u] = it < n ? (uint32_t)smp[k0 + it] : 0u;
+        }
+        __syncthreads();  // the previous chunk is done with keys and irow
+#pragma unroll
+        for (int u = 0; u < kSfItems / kSfThreads; u++) irow[u * kSfThreads + tid] = rr[u];
+        run_chunk(k0, n);
     }
 }
 
@@ -980,7 +1053,6 @@ __global__ __launch_bounds__(kBlock) void k_seq_tri_reduce(
 // once.
 // Position s then takes du(minDelta_s) * M[b][t][s] (k_seq_xgrad), the same
 // total the pair triangles gave: qsum_main - qsum_alt + the K-flip column sum.
-typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kGrpThreads = 1024;
 constexpr int kGrpWaves = kGrpThreads / kWave;
