@@ -828,17 +828,22 @@ __global__ __launch_bounds__(kTmThreads) void k_propagate_units(
 #pragma unroll
     for (int j = 0; j < TPU; j++) acc[j] = 0.0f;
     f32x4 g0[SPT], g1[SPT];
+    // g by buffer loads with 32-bit byte offsets: the lane's two 16-byte pieces
+    // in VGPRs, the sample pass and the slice in the scalar offset (64-bit
+    // addresses per sample pass would not fit beside g without spilling).
+    // Samples past the batch lie beyond the resource and read as zeros; the
+    // launcher keeps every offset below 2^31.
+    const __amdgpu_buffer_rsrc_t g_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)g, (short)0, (int)(batch * n_outputs * 4u), 0x00020000);
+    const uint32_t g_lane = ((b_base + s_loc0) * n_outputs + q * 8) * 4u;
+    const uint32_t g_v0 = g_lane + sw, g_v1 = g_lane + 16 - sw;
     const uint32_t n_st = ntab * n_slices;
     auto issue = [&](uint32_t si) {
         const uint32_t sl = si / ntab, t = t0 + si % ntab;
         uint8_t *stage = smem + (si & 1) * kStage;
         const float *wt = w + (size_t)t * kTmMaxEntries * n_outputs + sl * 64;
-#pragma unroll
-        for (int h = 0; h < kRowLoads; h++) {
-            const uint32_t c = (uint32_t)h * kTmThreads + tid;  // row c / 16, quad c % 16
-            dma16<kNonTemporal>(wt + (c >> 4) * n_outputs + (c & 15) * 4,
-                                stage + ((uint32_t)h * kTmThreads + wave * kWave) * 16);
-        }
+        // keys and du first: should their address come back from a register
+        // spill, the wait for that reload then finds no row load in flight
         if (wave < 2 * kKeyWaves) {
             // waves 0 .. kKeyWaves-1 load the keys, the next kKeyWaves the du values
             const bool is_du = wave >= kKeyWaves;
@@ -849,6 +854,12 @@ __global__ __launch_bounds__(kTmThreads) void k_propagate_units(
             if (byte < (uint32_t)kKeyBytes)
                 dma16(src + byte, stage + kTm64Rows + (is_du ? kKeyBytes : 0) + wk * kWave * 16);
         }
+#pragma unroll
+        for (int h = 0; h < kRowLoads; h++) {
+            const uint32_t c = (uint32_t)h * kTmThreads + tid;  // row c / 16, quad c % 16
+            dma16<kNonTemporal>(wt + (c >> 4) * n_outputs + (c & 15) * 4,
+                                stage + ((uint32_t)h * kTmThreads + wave * kWave) * 16);
+        }
     };
 
     issue(0);
@@ -858,10 +869,9 @@ __global__ __launch_bounds__(kTmThreads) void k_propagate_units(
             // this slice's g columns, in the lane's read order
 #pragma unroll
             for (int i = 0; i < SPT; i++) {
-                const uint32_t b = min(b_base + s_loc0 + kUnitPass * i, batch - 1);
-                const float *gp = g + (size_t)b * n_outputs + sl * 64 + q * 8;
-                g0[i] = *reinterpret_cast<const f32x4 *>(gp + (sw >> 2));
-                g1[i] = *reinterpret_cast<const f32x4 *>(gp + 4 - (sw >> 2));
+                const uint32_t so = (kUnitPass * (uint32_t)i * n_outputs + sl * 64) * 4u;
+                g0[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(g_rsrc, g_v0, so, 0));
+                g1[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(g_rsrc, g_v1, so, 0));
             }
         }
         // stage si (and the g columns) have landed; every wave is done with
@@ -1322,7 +1332,10 @@ static hipError_t launch_propagate_scatter(const FcShape &s, const float *du, co
 
 // the 64-column propagate: whole 256-row fp32 tables, 64-column slices
 static bool tm_propagate_wide(const FcShape &s) {
-    return s.n_entries == (uint32_t)kTmMaxEntries && s.n_outputs % 64 == 0 && s.batch >= 256;
+    // k_propagate_units reads g with 32-bit byte offsets, up to a whole chunk
+    // past the batch
+    return s.n_entries == (uint32_t)kTmMaxEntries && s.n_outputs % 64 == 0 && s.batch >= 256 &&
+           (uint64_t)(s.batch + 8 * kUnitPass) * s.n_outputs * 4 <= 0x7fffffffu;
 }
 
 uint32_t tm_key_row_shift(const FcShape &s) { return tm_propagate_wide(s) ? 8u : 7u; }
