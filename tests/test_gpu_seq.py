@@ -203,6 +203,16 @@ def test_seq_one_bucket_chunks(oracle, cuda_device):
     run_seq(oracle, B, S, I, T, Nc, Npe, O, seed=12, inputs=(x, anchors, W, pe, go))
 
 
+def test_seq_one_bucket_chunks_partial_slice(oracle, cuda_device):
+    # one Q bucket of 10240 items (ten sorted chunks of the forward) with 96
+    # outputs: the first 64-column slice is staged by LDS DMA, the second runs
+    # past the row's end and is staged through registers with zeros past it
+    B, S, I, T, Nc, Npe, O = 160, 64, 16, 2, 3, 2, 96
+    x, anchors, W, pe, go = seq_inputs(19, B, S, I, T, Nc, Npe, O)
+    x.zero_()
+    run_seq(oracle, B, S, I, T, Nc, Npe, O, seed=19, inputs=(x, anchors, W, pe, go))
+
+
 def test_seq_many_rows_few_tables(oracle, cuda_device):
     # B*S >= 2048 rows over a few tables: the bucket sorts run a workgroup per
     # table (per-wave runs of the rows, scanned in (bucket, wave) order)
