@@ -1387,10 +1387,12 @@ hipError_t launch_propagate_tm(const FcShape &s, const float *w, const float *g,
     const uint32_t n_units = (s.n_detectors + tpu - 1) / tpu;
     if (wide) {
         // whole tables, every 64-column slice in one unit: du[b][t] directly
-        // 16 tables a unit: g is read once per unit and slice, so twice the
-        // tables of 8 halve its reads (config 3: 1.56 against 1.59 ms; 12
-        // leaves a partial last round of units, 1.75 ms)
-        constexpr uint32_t kTpu = 16;
+        // 8 tables a unit.  g is read once per unit and slice, so 16 tables
+        // halve its reads and ran 1.56 against 1.59 ms at config 3, but their
+        // keys and du (8 KiB a table, read again for every slice) then
+        // overflow an XCD's L2 and the kernel fetches 9.73 instead of 8.80 GB;
+        // 12 leaves a partial last round of units (1.75 ms)
+        constexpr uint32_t kTpu = 8;
         const uint32_t spt = tm_units_spt(s.batch);
         const uint32_t n_chunks = (s.batch + kUnitPass * spt - 1) / (kUnitPass * spt);
         const uint64_t grid = (uint64_t)((s.n_detectors + kTpu - 1) / kTpu) * n_chunks;
