@@ -103,8 +103,11 @@ int spiky_lut_forward_step(spiky_lut_manager *m, const float *weights, uint32_t 
  * scratch is a library-owned static device array of
  * SPIKY_NOALLOC_SCRATCH_BYTES, one copy per device, held until the process
  * ends; shapes that need more return SPIKY_VALUE_ERROR without launching.
- * Every call on one device shares that device's array, so calls that
- * overlap on one device (different streams, threads or managers) race. */
+ * Every call on one device shares that device's array.  Eager calls are
+ * chained on the device: each waits (hipStreamWaitEvent, on the caller's
+ * stream) for the previous call's last kernel, whatever its stream, thread or
+ * manager.  Calls captured into a HIP graph are not chained this way: graphs
+ * replayed so that they overlap on one device race on the array. */
 #define SPIKY_NOALLOC_SCRATCH_BYTES (64ull << 20)
 int spiky_lut_forward_step_noalloc(spiky_lut_manager *m, const float *weights,
                                    uint32_t batch_size, const float *input, const int32_t *anchors,

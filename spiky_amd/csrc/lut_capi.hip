@@ -238,19 +238,30 @@ static __device__ __align__(256) uint8_t scratch[SPIKY_NOALLOC_SCRATCH_BYTES];
 
 constexpr int kMaxDevices = 64;
 std::mutex g_noalloc_mutex;
-void *g_noalloc_ptr[kMaxDevices] = {};
+// Per device: the address of its copy of `scratch`, and an event recorded
+// after the last eager call's final kernel, so that the next call (on any
+// stream) starts only once that call has finished with the array.
+struct NoallocDevice {
+    void *ptr = nullptr;
+    hipEvent_t done = nullptr;
+    bool recorded = false;
+};
+NoallocDevice g_noalloc[kMaxDevices];
 
-void *noalloc_scratch() {
+// Resolves the current device's array and event once (with that device
+// current); the caller holds g_noalloc_mutex.
+NoallocDevice &noalloc_device() {
     int dev = 0;
     check_hip(hipGetDevice(&dev), "hipGetDevice");
     if (dev < 0 || dev >= kMaxDevices) throw std::runtime_error("device id out of range");
-    std::lock_guard<std::mutex> lock(g_noalloc_mutex);
-    if (!g_noalloc_ptr[dev]) {
+    NoallocDevice &d = g_noalloc[dev];
+    if (!d.ptr) {
         void *p = nullptr;
         check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
-        g_noalloc_ptr[dev] = p;
+        check_hip(hipEventCreateWithFlags(&d.done, hipEventDisableTiming), "hipEventCreate(noalloc)");
+        d.ptr = p;
     }
-    return g_noalloc_ptr[dev];
+    return d;
 }
 
 void require_manager(const spiky_lut_manager *m) {
@@ -557,20 +568,34 @@ int spiky_lut_forward_step_noalloc(spiky_lut_manager *m, const float *weights,
                              " bytes of scratch, more than the " +
                              std::to_string(SPIKY_NOALLOC_SCRATCH_BYTES) +
                              " the allocation-free path holds; use forward_step");
-        void *scr = tm ? noalloc_scratch() : nullptr;
         m->context_active = true;
         const hipStream_t st = as_stream(stream);
         check_hip(spiky::launch_check_detectors(s, input, anchors, cmp_eps, lookup_indices, min_deltas,
                                                 min_delta_indices, st),
                   "check_detectors");
-        if (tm)
-            check_hip(spiky::launch_fill_tm(s, weights, lookup_indices, output, m->int_mode,
-                                            m->int_rescaler, scr, st),
-                      "fill_outputs_fc");
-        else
+        if (!tm) {
             check_hip(spiky::launch_fill_fc_f32(s, weights, lookup_indices, output, m->int_mode,
                                                 m->int_rescaler, st),
                       "fill_outputs_fc");
+            return;
+        }
+        // Eager calls on one device are chained through the device's event, so a
+        // call on another stream waits for the previous call's kernels to finish
+        // with the shared array.  Under stream capture the caller's graph orders
+        // its nodes, and an event recorded outside the capture cannot be waited on.
+        std::lock_guard<std::mutex> lock(g_noalloc_mutex);
+        NoallocDevice &d = noalloc_device();
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        check_hip(hipStreamIsCapturing(st, &cs), "hipStreamIsCapturing");
+        const bool eager = cs == hipStreamCaptureStatusNone;
+        if (eager && d.recorded) check_hip(hipStreamWaitEvent(st, d.done, 0), "hipStreamWaitEvent(noalloc)");
+        check_hip(spiky::launch_fill_tm(s, weights, lookup_indices, output, m->int_mode,
+                                        m->int_rescaler, d.ptr, st),
+                  "fill_outputs_fc");
+        if (eager) {
+            check_hip(hipEventRecord(d.done, st), "hipEventRecord(noalloc)");
+            d.recorded = true;
+        }
     });
 }
 

@@ -300,32 +300,38 @@ class LUTLayerBasic(nn.Module):
                                     _backward_group_size)
         self._synapse_metas = synapse_metas
         for i, sm in enumerate(synapse_metas):
-            assert self._lut_dm.register_synapse_meta(
+            m_id = self._lut_dm.register_synapse_meta(
                 learning_rate=sm.learning_rate, min_synaptic_weight=sm.min_weight,
                 max_synaptic_weight=sm.max_weight, initial_noise_level=sm.initial_noise_level,
-                initial_weight=sm.initial_weight) == i
+                initial_weight=sm.initial_weight)
+            assert m_id == i
         self._lut_dm.initialize_neurons(is_fully_connected)
         self._n_lookup_neurons = self._lut_dm.get_number_of_lookup_neurons()
+        # neuron ids (reference LUTLayer.py:342-357): inputs (the virtual row in
+        # product mode) first, then the detectors; lookup neurons (one per table
+        # row) first, then the outputs.  They follow the layer across devices.
+        n_virtual = topo.n_virtual
+        self._input_neuron_ids = torch.arange(n_virtual, dtype=torch.int32)
+        self._detector_neuron_ids = torch.arange(n_virtual, n_virtual + n_detectors, dtype=torch.int32)
+        self._lookup_neuron_ids = torch.arange(self._n_lookup_neurons, dtype=torch.int32)
+        self._output_neuron_ids = torch.arange(self._n_lookup_neurons, self._n_lookup_neurons + n_outputs,
+                                               dtype=torch.int32)
         self._weights = None
         self._lookup_indices_callback = None
         self.register_buffer("_detector_anchors", None)
 
     # ---------------------------------------------------------------- neuron ids
-    # Inputs (the virtual row in product mode) come first, then the detectors;
-    # lookup neurons (one per table row) first, then the outputs.
     def get_input_neuron_ids(self):
-        return torch.arange(self._topology.n_virtual, dtype=torch.int32)
+        return self._input_neuron_ids
 
     def get_detector_neuron_ids(self):
-        first = self._topology.n_virtual
-        return torch.arange(first, first + self._n_detectors, dtype=torch.int32)
+        return self._detector_neuron_ids
 
     def get_lookup_neuron_ids(self):
-        return torch.arange(self._n_lookup_neurons, dtype=torch.int32)
+        return self._lookup_neuron_ids
 
     def get_output_neuron_ids(self):
-        return torch.arange(self._n_lookup_neurons, self._n_lookup_neurons + self._n_outputs,
-                            dtype=torch.int32)
+        return self._output_neuron_ids
 
     # ---------------------------------------------------------------- build time
     def add_detector_connections(self, chunk_of_connections: ChunkOfConnections, ids_shift=0,
@@ -746,6 +752,8 @@ class LUTLayerBasic(nn.Module):
         super().to(*args, **kwargs)
         target = kwargs.get("device", args[0] if args else None)
         self.device = _resolve_device(target)
+        for name in ("_input_neuron_ids", "_detector_neuron_ids", "_lookup_neuron_ids", "_output_neuron_ids"):
+            setattr(self, name, getattr(self, name).to(device=self.device))
         self._lut_dm.to_device(_device_index(self.device))
         if self._own_shared_context:
             self._shared_context.to_device(self.device)
@@ -981,8 +989,19 @@ class Conv2DLUTLayer(LUTLayerBasic):
     def _wire_detectors(self, geo, explicit_anchors, seed, whole_input):
         """Anchors: the caller's, or drawn over each detector's window."""
         if explicit_anchors is not None:
-            self._detector_anchors = explicit_anchors.to(device=self.device, dtype=torch.int32) \
-                .flatten().contiguous()
+            anchors = explicit_anchors.to(dtype=torch.int32).flatten().contiguous()
+            # the kernels read x at every anchor id: an id outside the detectors'
+            # inputs would read past the sample's row, so it is refused here once
+            # (-1, the reference's UINT32_MAX, marks an unused pair)
+            expected = self._n_detectors * self._n_anchors_per_detector * 2
+            if anchors.numel() != expected:
+                raise ValueError(f"_explicit_anchors has {anchors.numel()} ids, expected "
+                                 f"n_detectors * n_anchors_per_detector * 2 = {expected}")
+            n_virtual = self._topology.n_virtual
+            if anchors.numel() and (int(anchors.min()) < -1 or int(anchors.max()) >= n_virtual):
+                raise ValueError(f"_explicit_anchors must lie in [0, {n_virtual}) (or be -1 for an "
+                                 f"unused pair); got [{int(anchors.min())}, {int(anchors.max())}]")
+            self._detector_anchors = anchors.to(device=self.device)
             return
         if whole_input:
             self._set_full_detector_connectivity()

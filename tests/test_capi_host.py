@@ -215,6 +215,42 @@ def test_fc_layer_anchors_are_the_reference_compact_draw():
     assert layer._detector_anchors.tolist() == expect
 
 
+def test_explicit_anchors_are_range_checked():
+    """Explicit anchors are kept as given when every id is an input of the
+    layer (or -1, an unused pair), and refused with ValueError otherwise: the
+    kernels would read x past the sample's row."""
+    from spiky_amd import LUTLayer
+    I, T, Nc = 10, 3, 2
+    good = torch.tensor([[0, 9], [1, -1], [5, 4], [8, 2], [3, 7], [6, 0]], dtype=torch.int32)
+    layer = LUTLayer(I, Nc, T, 4, _explicit_anchors=good)
+    assert layer._detector_anchors.tolist() == good.flatten().tolist()
+    for bad in ([[0, 10]], [[-2, 3]]):
+        a = good.clone()
+        a[1] = torch.tensor(bad[0], dtype=torch.int32)
+        with pytest.raises(ValueError, match="_explicit_anchors must lie in"):
+            LUTLayer(I, Nc, T, 4, _explicit_anchors=a)
+    with pytest.raises(ValueError, match="expected n_detectors"):
+        LUTLayer(I, Nc, T, 4, _explicit_anchors=good[:4])
+    # product mode: the virtual row [x1 | x2 | pe] has 2 * I + pd inputs
+    pl = LUTLayer(I, Nc, T, 4, sequence_length=4, positional_dim=1, concatenation_product=False,
+                  _explicit_anchors=torch.full((T * Nc * 2,), 2 * I, dtype=torch.int32))
+    assert int(pl._detector_anchors.max()) == 2 * I
+
+
+def test_neuron_ids_are_kept_and_follow_the_layer():
+    """The four id ranges are stored once (reference LUTLayer.py:342-357) and
+    returned as the same tensors, not rebuilt per call."""
+    from spiky_amd import LUTLayer
+    layer = LUTLayer(12, 3, 5, 7, random_seed=1)
+    assert layer.get_input_neuron_ids() is layer.get_input_neuron_ids()
+    assert layer.get_input_neuron_ids().tolist() == list(range(12))
+    assert layer.get_detector_neuron_ids().tolist() == list(range(12, 17))
+    n_lookup = 5 * 8
+    assert layer.get_lookup_neuron_ids().tolist() == list(range(n_lookup))
+    assert layer.get_output_neuron_ids().tolist() == list(range(n_lookup, n_lookup + 7))
+    assert all(t.dtype == torch.int32 for t in (layer.get_input_neuron_ids(), layer.get_output_neuron_ids()))
+
+
 def test_chunk_roundtrip():
     from spiky_amd.util.chunk_of_connections import (build_connections, parse_connections,
                                                      repeat_connections_incrementing_source)
