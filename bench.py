@@ -143,6 +143,18 @@ def load_traffic(kernel, config):
     return value, digest
 
 
+def traffic_fields(key, config, ms):
+    """roofline.traffic and its rate: measured HBM bytes per launch of family
+    `key` (or per step, key "step") from profiles/hbm_traffic_config<N>.txt,
+    null when that summary was taken at other kernel sources."""
+    traffic, digest = load_traffic(key, config)
+    stale = traffic is not None and digest != source_digest()
+    if stale:
+        traffic = None
+    return {"traffic": traffic, "traffic_source_digest": digest, "traffic_stale": stale,
+            "traffic_gbs": round(traffic / (ms * 1e-3) / 1e9, 1) if traffic else None}
+
+
 def calibrate_copy(mib):
     """A plain device-to-device copy of `mib` MiB, five times: the known-size
     kernel the FETCH_SIZE / WRITE_SIZE counters are scaled against."""
@@ -420,6 +432,15 @@ def cpu_projection(l1, l2, head, x, g, B, reps):
 INT8 = dict(B=4096, I=4096, T=8192, Nc=8, O=1024, int_rescaler=0.001, cpu_B=2048)
 
 
+def int8_unique_bytes(B, I, T, Nc, O):
+    """Unique bytes per family of the int8 forward: the detector check reads
+    x and the anchors and writes the indices; the gather-sum reads the int8
+    tables and scales once and the indices, and updates the output."""
+    E = 1 << Nc
+    return {"check_detectors": B * I * 4 + T * Nc * 8 + B * T * 4,
+            "fill_outputs_fc_i8": T * E * O + T * 4 + B * T * 4 + 2 * B * O * 4}
+
+
 def bench_int8(args):
     """the config-3 layer with int8 tables (uniform in
     [-127, 127]) and one fp32 scale per table (uniform [0.001, 0.01]),
@@ -467,9 +488,7 @@ def bench_int8(args):
     log(f"{ms:.3f} ms/step; kernels {ktimes}")
     gb = {"check_detectors": B * I * 4 + T * Nc * 8 + B * T * 4,
           "fill_outputs_fc_i8": B * T * O * 1 + T * 4 + B * O * 4}
-    # unique bytes: the int8 tables and scales once, the indices, the output once
-    ub = {"check_detectors": B * I * 4 + T * Nc * 8 + B * T * 4,
-          "fill_outputs_fc_i8": T * E * O + T * 4 + B * T * 4 + 2 * B * O * 4}
+    ub = int8_unique_bytes(B, I, T, Nc, O)
     dom = max(ktimes.items(), key=lambda kv: kv[1][1])[0]
     dom_ms = ktimes[dom][1] / ktimes[dom][0]
     achieved = ub[dom] / (dom_ms * 1e-3) / 1e9
@@ -509,7 +528,7 @@ def bench_int8(args):
                    "n_inputs": I, "n_tables": T, "anchors_per_table": Nc, "n_outputs": O,
                    "table_bytes": T * E * O, "int_rescaler": c["int_rescaler"], "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), **traffic_fields(dom, 4, dom_ms),
                      "algorithmic_bytes_per_launch": ub[dom], "ms_per_launch": round(dom_ms, 4),
                      "g_model": {"bytes_per_launch": gb[dom],
                                  "frac": round(gb[dom] / (dom_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
@@ -682,7 +701,7 @@ def bench_transformer(args):
         "config": {"workload": "BASELINE config 5: LUTTransformer block stack fwd+bwd", "batch": B, **cfg},
         "roofline": {"bound": "hbm", "achieved": round(u / (ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(u / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                     "traffic": None, "algorithmic_bytes_per_step": u,
+                     **traffic_fields("step", 5, ms), "algorithmic_bytes_per_step": u,
                      "scope": "whole step, unique bytes (every table read forward and backward, every "
                               "weight gradient written once, activations)",
                      "g_model": {"bytes_per_step": g, "frac": round(g / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}},
@@ -845,6 +864,155 @@ def bench_densify(args):
     print(json.dumps(out), flush=True)
 
 
+# Kernels of each C-ABI launch family (one call = these kernels in order), by
+# configuration: the trace and counter summaries sum them per family.
+FAMILIES = {
+    3: {"check_detectors": ["k_check_detectors_lds"],
+        "fill_outputs_fc": ["k_transpose_idx", "k_fill_tm_dma", "k_fill_commit"],
+        "propagate_fc": ["k_transpose_keys4", "k_propagate_units", "k_propagate_scatter"],
+        "gather_w_gradients_fc": ["k_wgrad_commit_values", "k_bucket_samples", "k_wgrad_slices"]},
+    4: {"check_detectors": ["k_check_detectors_lds"],
+        "fill_outputs_fc_i8": ["k_transpose_idx", "k_fill_tm", "k_fill_commit"]},
+}
+
+
+def family_unique_bytes(config):
+    """Unique bytes per launch of each family of a configuration (the figures
+    the bench line's roofline divides by the family's launch time)."""
+    if config == 3:
+        B, I, T, Nc, O, _, _ = CONFIGS[3]
+        return unique_bytes(B, I, T, Nc, O)
+    if config == 4:
+        c = INT8
+        B, I, T, Nc, O = c["B"], c["I"], c["T"], c["Nc"], c["O"]
+        return int8_unique_bytes(B, I, T, Nc, O)
+    return {}
+
+
+def _profile_rows(path):
+    import csv
+    with open(path, newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def _timed_rows(rows, warmup, steps):
+    """The dispatches of the timed steps: everything from the first dispatch
+    of step warmup + 1 on.  A step starts with the first LUT kernel the run
+    launches (the earliest dispatch named k_*), which launches the same number
+    of times in every step.  Returns (rows, dispatches of that kernel a step,
+    its name)."""
+    rows = sorted(rows, key=lambda r: (int(r["Start_Timestamp"]), int(r["Dispatch_Id"])))
+    marker = next(r["Kernel_Name"] for r in rows if r["Kernel_Name"].startswith("k_"))
+    ids = sorted({int(r["Dispatch_Id"]) for r in rows if r["Kernel_Name"] == marker})
+    if len(ids) % (warmup + steps):
+        raise SystemExit(f"{marker} ran {len(ids)} times, not a multiple of {warmup + steps} steps")
+    per_step = len(ids) // (warmup + steps)
+    first = ids[warmup * per_step]
+    first_ts = min(int(r["Start_Timestamp"]) for r in rows if int(r["Dispatch_Id"]) == first)
+    return [r for r in rows if int(r["Start_Timestamp"]) >= first_ts], per_step, marker
+
+
+def summarize_trace(args):
+    """Summary of a rocprofv3 --kernel-trace CSV (run_kernel_trace.csv) over
+    the timed steps of a bench.py run: per kernel its launches a step and its
+    mean, min and max duration; per launch family the sum of its kernels'
+    means; and the dominant family's roofline fraction recomputed from them."""
+    import statistics
+    rows, per_step, marker = _timed_rows(_profile_rows(args.trace_summary), args.warmup, args.steps)
+    by = {}
+    for r in rows:
+        by.setdefault(r["Kernel_Name"], []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-6)
+    total = sum(sum(v) for v in by.values())
+    out = [f"# timed steps only: {args.steps} steps after {args.warmup} warm-up steps (from the first "
+           f"dispatch of step {args.warmup + 1} of {marker}); times in ms",
+           f"{'kernel':<36}{'per_step':>9}{'avg_ms':>10}{'min_ms':>10}{'max_ms':>10}{'ms/step':>10}{'share':>8}"]
+    for name, v in sorted(by.items(), key=lambda kv: -sum(kv[1])):
+        out.append(f"{name[:35]:<36}{len(v) / args.steps:>9.2f}{statistics.fmean(v):>10.4f}{min(v):>10.4f}"
+                   f"{max(v):>10.4f}{sum(v) / args.steps:>10.4f}{100 * sum(v) / total:>7.1f}%")
+    out.append(f"kernel time per step: {total / args.steps:.4f} ms")
+    fams = FAMILIES.get(args.config)
+    if fams:
+        ub = family_unique_bytes(args.config)
+        out.append("")
+        out.append("# per launch family: the sum of its kernels' mean durations (bench.py times the family "
+                   "with HIP events around the same kernels)")
+        fam_ms = {}
+        for fam, kernels in fams.items():
+            if all(k in by for k in kernels):
+                fam_ms[fam] = sum(statistics.fmean(by[k]) for k in kernels)
+                out.append(f"{fam:<24}{fam_ms[fam]:>10.4f} ms  = " + " + ".join(kernels))
+        if fam_ms:
+            dom = max(fam_ms, key=fam_ms.get)
+            gbs = ub[dom] / (fam_ms[dom] * 1e-3) / 1e9
+            out.append(f"# dominant family {dom}: {ub[dom]} unique bytes / {fam_ms[dom]:.4f} ms = "
+                       f"{gbs:.1f} GB/s = {gbs / PEAK_HBM_GBS:.4f} of {PEAK_HBM_GBS:.0f} GB/s")
+    print("\n".join(out))
+
+
+def summarize_counters(args):
+    """Summary of rocprofv3 --pmc CSVs (run_counter_collection.csv) over the
+    timed steps of a bench.py run: per kernel the mean of each counter per
+    dispatch.  FETCH_SIZE and WRITE_SIZE (KiB) become bytes scaled by the
+    calibration factors a plain copy of known size gives (--calibration
+    FETCH,WRITE); LDS bank-conflict cycles are also given as a fraction of
+    the LDS-active cycles.  With --traffic-out, the families' FETCH + WRITE
+    bytes per launch (configs 3 and 4) or the whole step's (other configs) go
+    to that file, which bench.py reads for roofline.traffic."""
+    import statistics
+    f_fetch, f_write = (float(v) for v in args.calibration.split(","))
+    per = {}
+    counters = []
+    for path in args.counter_summary:
+        rows, per_step, marker = _timed_rows(_profile_rows(path), args.warmup, args.steps)
+        for r in rows:
+            c = r["Counter_Name"]
+            if c not in counters:
+                counters.append(c)
+            v = float(r["Counter_Value"])
+            if c == "FETCH_SIZE":
+                v *= 1024 * f_fetch
+            elif c == "WRITE_SIZE":
+                v *= 1024 * f_write
+            per.setdefault(r["Kernel_Name"], {}).setdefault(c, {}).setdefault(r["Dispatch_Id"], 0.0)
+            # counters of one dispatch may come as several rows (one per agent block): sum them
+            per[r["Kernel_Name"]][c][r["Dispatch_Id"]] += v
+    cols = counters + (["conflict_frac"] if {"SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE"} <= set(counters) else [])
+    out = [f"# timed steps only: {args.steps} steps after {args.warmup} warm-up steps; mean per dispatch; "
+           f"FETCH_SIZE / WRITE_SIZE in bytes (KiB x 1024 x factor {f_fetch:g} / {f_write:g})",
+           f"{'kernel':<30}{'per_step':>9}" + "".join(f"{c[:20]:>22}" for c in cols)]
+    means = {}
+    order = sorted(per, key=lambda k: -max((statistics.fmean(d.values()) * len(d)
+                                            for c, d in per[k].items() if c in ("FETCH_SIZE", "WRITE_SIZE")),
+                                           default=0.0))
+    for k in order:
+        means[k] = {c: statistics.fmean(d.values()) for c, d in per[k].items()}
+        n = max(len(d) for d in per[k].values())
+        line = f"{k[:29]:<30}{n / args.steps:>9.2f}"
+        for c in counters:
+            line += f"{means[k].get(c, float('nan')):>22.6g}"
+        if "conflict_frac" in cols:
+            line += f"{means[k]['SQ_LDS_BANK_CONFLICT'] / max(means[k]['SQ_LDS_IDX_ACTIVE'], 1.0):>22.4f}"
+        out.append(line)
+    print("\n".join(out))
+    if args.traffic_out:
+        if not {"FETCH_SIZE", "WRITE_SIZE"} <= set(counters):
+            raise SystemExit("--traffic-out needs FETCH_SIZE and WRITE_SIZE runs")
+        lines = [f"# HBM bytes (FETCH_SIZE + WRITE_SIZE, calibrated) from: " + " ".join(args.counter_summary),
+                 f"# sources {source_digest()}"]
+        fams = FAMILIES.get(args.config)
+        if fams:
+            for fam, kernels in fams.items():
+                if all(k in means for k in kernels):
+                    b = sum(means[k]["FETCH_SIZE"] + means[k]["WRITE_SIZE"] for k in kernels)
+                    lines.append(f"{fam} {b:.0f}")
+        else:
+            step = sum(sum(per[k][c].values()) for k in per for c in ("FETCH_SIZE", "WRITE_SIZE")
+                       if c in per[k]) / args.steps
+            lines.append(f"step {step:.0f}")
+        with open(args.traffic_out, "w") as f:
+            f.write("\n".join(lines) + "\n")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -861,9 +1029,25 @@ def main():
                     help="time the dense -> sparse gradient converter instead of a LUT config")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="only run a plain copy of this many MiB (counter calibration) and exit")
+    ap.add_argument("--trace-summary", metavar="CSV",
+                    help="summarise a rocprofv3 kernel trace of a bench.py run with the same --config, "
+                         "--steps and --warmup over its timed steps, and exit")
+    ap.add_argument("--counter-summary", metavar="CSV", nargs="+",
+                    help="summarise rocprofv3 --pmc CSVs of a bench.py run with the same --config, "
+                         "--steps and --warmup over its timed steps, and exit")
+    ap.add_argument("--calibration", default="2,1",
+                    help="FETCH_SIZE,WRITE_SIZE scale factors from a copy of known size")
+    ap.add_argument("--traffic-out", metavar="FILE",
+                    help="with --counter-summary: write the HBM bytes per family (or per step) here")
     args = ap.parse_args()
     if args.calibrate_copy_mib:
         calibrate_copy(args.calibrate_copy_mib)
+        return
+    if args.trace_summary:
+        summarize_trace(args)
+        return
+    if args.counter_summary:
+        summarize_counters(args)
         return
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build's LUT path runs on a single MI355X "

@@ -252,6 +252,28 @@ void spiky_lut_reset_profiler(spiky_lut_manager *m);
 int spiky_lut_set_kernel_timing(spiky_lut_manager *m, int enable);
 int spiky_lut_kernel_times(spiky_lut_manager *m, char *buf, uint64_t buf_len, int reset);
 
+/* Scratch sizing, computed on the host without touching a device (no
+ * reference counterpart: the reference allocates its buffers per call).  For
+ * the entry point named by `op` on this manager and batch, *needed gets the
+ * bytes of device scratch that entry point grows its buffer to -- the
+ * layouts its launchers lay out -- and every launcher's layout is checked
+ * against its region of a buffer of `capacity` bytes (UINT64_MAX: no limit);
+ * a layout that does not fit returns SPIKY_VALUE_ERROR naming the launcher
+ * and the bytes it needs.  The entry points themselves refuse such a layout
+ * before launching anything.  sequence_length, n_inputs_1, n_inputs_2 and
+ * sliced_mode are read by the product-mode codes only. */
+#define SPIKY_OP_FORWARD 0           /* spiky_lut_forward_step (and _noalloc) */
+#define SPIKY_OP_FORWARD_I8 1        /* spiky_lut_forward_step_i8 */
+#define SPIKY_OP_BACKWARD 2          /* spiky_lut_backward_backprop, weight gradient or Internal update */
+#define SPIKY_OP_BACKWARD_NO_WGRAD 3 /* spiky_lut_backward_backprop without a weight gradient */
+#define SPIKY_OP_FORWARD_CONCAT 4    /* spiky_lut_forward_step_concat */
+#define SPIKY_OP_BACKWARD_CONCAT 5   /* spiky_lut_backward_backprop_concat */
+#define SPIKY_OP_FORWARD_PRODUCT 6   /* spiky_lut_forward_step_product */
+#define SPIKY_OP_BACKWARD_PRODUCT 7  /* spiky_lut_backward_backprop_product */
+int spiky_lut_scratch_plan(spiky_lut_manager *m, int op, uint32_t batch_size, uint32_t sequence_length,
+                           uint32_t n_inputs_1, uint32_t n_inputs_2, int sliced_mode, uint64_t capacity,
+                           uint64_t *needed);
+
 /* ---- dense -> sparse converter --------------------------------------------
  * Replaces DenseToSparseConverterNative (spiky_cuda/torch_utils/torch_utils.cu:
  * 11-339; Python side spiky/util/torch_utils.py:7-125).  A 32-bit word of the

@@ -48,6 +48,7 @@ _SIGNATURES = {
     "spiky_lut_reset_profiler": ([_vp], None),
     "spiky_lut_set_kernel_timing": ([_vp, _i32], _i32),
     "spiky_lut_kernel_times": ([_vp, ctypes.c_char_p, _u64, _i32], _i32),
+    "spiky_lut_scratch_plan": ([_vp, _i32, _u32, _u32, _u32, _u32, _i32, _u64, _vp], _i32),
     "spiky_grow_cuboid": ([_u32, _vp, _vp, _u32, _vp, _vp, _vp, _f32, _u64, _u32, _vp, _vp, _u64,
                            ctypes.POINTER(_u64)], _i32),
     "spiky_densify32_workspace_bytes": ([_u64], _u64),

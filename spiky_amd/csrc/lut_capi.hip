@@ -29,6 +29,29 @@ void check_hip(hipError_t e, const char *what) {
     }
 }
 
+// A launch's status; a refused scratch layout names the launcher and the
+// bytes it needed.
+void check_launch(hipError_t e, const char *what) {
+    std::string &why = spiky::scratch_refusal();
+    if (e != hipSuccess && !why.empty()) {
+        const std::string msg = std::string(what) + ": " + why;
+        why.clear();
+        throw std::runtime_error(msg);
+    }
+    check_hip(e, what);
+}
+
+// The bytes a launcher's scratch layout needs: the launcher run as a plan,
+// which launches nothing.
+template <typename F>
+size_t planned_bytes(F &&launch, const char *what) {
+    spiky::Scratch p = spiky::scratch_plan();
+    check_launch(launch(p), what);
+    return p.needed;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
 template <typename F>
 int guarded(F &&f) {
     try {
@@ -71,6 +94,12 @@ struct DeviceBuffer {
         bytes = need;
         device = cur;
         return ptr;
+    }
+    // This buffer, grown to the bytes `launch` lays out, as its scratch.
+    template <typename F>
+    spiky::Scratch scratch_for(F &&launch, const char *what) {
+        void *p = ensure(planned_bytes(launch, what));
+        return spiky::scratch_run(p, p ? bytes : 0);
     }
     // Upload host data (re-uploads when the current device changed).
     void *upload(const void *host, size_t n, bool force) {
@@ -275,6 +304,79 @@ void require_initialized(const spiky_lut_manager *m) {
 }
 
 hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---- scratch layouts --------------------------------------------------------
+// Each entry point's scratch launchers called with null pointers.  Run as a
+// Plan or a Check a launcher reads no pointer and launches nothing, so these
+// give exactly the layouts the entry points lay out: the entry points size
+// their buffers with them, and spiky_lut_scratch_plan reports them.
+hipError_t layout_fill_tm(const spiky_lut_manager *m, const spiky::FcShape &s, spiky::Scratch &x) {
+    return spiky::launch_fill_tm(s, nullptr, nullptr, nullptr, m->int_mode, m->int_rescaler, x, nullptr);
+}
+
+hipError_t layout_fill_tm_i8(const spiky_lut_manager *m, const spiky::FcShape &s, spiky::Scratch &x) {
+    return spiky::launch_fill_tm_i8(s, nullptr, nullptr, nullptr, nullptr, m->int_mode, m->int_rescaler, x,
+                                    nullptr);
+}
+
+hipError_t layout_propagate_tm(const spiky::FcShape &s, spiky::Scratch &x) {
+    return spiky::launch_propagate_tm(s, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, x,
+                                      nullptr);
+}
+
+hipError_t layout_wgrad_fc(const spiky_lut_manager *m, const spiky::FcShape &s, spiky::Scratch &x) {
+    return spiky::launch_wgrad_fc(s, nullptr, nullptr, nullptr, 1.0, m->int_mode, m->int_rescaler, true, x,
+                                  nullptr);
+}
+
+hipError_t layout_wgrad_sparse(const spiky_lut_manager *m, const spiky::SparseShape &s, spiky::Scratch &x) {
+    return spiky::launch_wgrad_sparse(s, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 1.0, true,
+                                      m->int_mode, m->int_rescaler, x, m->syn_targets.size(), nullptr);
+}
+
+hipError_t layout_forward_seq(const spiky_lut_manager *m, const spiky::SeqShape &s, spiky::Scratch &x) {
+    return spiky::launch_forward_seq(s, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                     nullptr, nullptr, nullptr, 0.0f, m->int_mode, m->int_rescaler, x, nullptr);
+}
+
+hipError_t layout_backward_seq(const spiky_lut_manager *m, const spiky::SeqShape &s, spiky::Scratch &x) {
+    return spiky::launch_backward_seq(s, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                      nullptr, nullptr, nullptr, nullptr, nullptr, 1.0, true, m->int_mode,
+                                      m->int_rescaler, x, nullptr);
+}
+
+hipError_t layout_forward_product(const spiky_lut_manager *m, const spiky::ProductShape &s, spiky::Scratch &x) {
+    return spiky::launch_forward_product(s, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, m->int_mode,
+                                         m->int_rescaler, x, nullptr);
+}
+
+hipError_t layout_backward_product(const spiky_lut_manager *m, const spiky::ProductShape &s, spiky::Scratch &x) {
+    return spiky::launch_backward_product(s, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                          nullptr, nullptr, nullptr, 1.0, m->int_mode,
+                                          m->int_rescaler, x, nullptr);
+}
+
+// The fully connected backward's one scratch buffer, used in stream order:
+// the table-major propagate's layout first, then the weight gradient's (whose
+// bucket sort reads the transposed keys the propagate leaves at the start of
+// its region).
+struct FcBackwardRegions {
+    bool tm = false;        // the table-major propagate runs
+    size_t prop_bytes = 0;  // its region, a 256-byte multiple
+    size_t wg_bytes = 0;    // the weight gradient's region after it
+};
+
+FcBackwardRegions fc_backward_regions(const spiky_lut_manager *m, const spiky::FcShape &s, bool with_wgrad) {
+    FcBackwardRegions r;
+    r.tm = !m->int_mode && spiky::tm_propagate_applies(s);
+    if (r.tm)
+        r.prop_bytes = align256(planned_bytes([&](spiky::Scratch &x) { return layout_propagate_tm(s, x); },
+                                              "propagate_through_detectors_fc"));
+    if (with_wgrad)
+        r.wg_bytes = planned_bytes([&](spiky::Scratch &x) { return layout_wgrad_fc(m, s, x); },
+                                   "gather_w_gradients_fc");
+    return r;
+}
 
 }  // namespace
 
@@ -507,11 +609,12 @@ int spiky_lut_forward_step(spiky_lut_manager *m, const float *weights, uint32_t 
         });
         if (m->fully_connected == 1) {
             if (spiky::tm_fill_applies(s, m->int_mode)) {
-                void *scr = m->scratch_fwd.ensure(spiky::tm_fill_scratch_bytes(s, m->int_mode));
+                spiky::Scratch scr = m->scratch_fwd.scratch_for(
+                    [&](spiky::Scratch &x) { return layout_fill_tm(m, s, x); }, "fill_outputs_fc");
                 m->timed("fill_outputs_fc", st, [&] {
-                    check_hip(spiky::launch_fill_tm(s, weights, lookup_indices, output, m->int_mode,
-                                                    m->int_rescaler, scr, st),
-                              "fill_outputs_fc");
+                    check_launch(spiky::launch_fill_tm(s, weights, lookup_indices, output, m->int_mode,
+                                                       m->int_rescaler, scr, st),
+                                 "fill_outputs_fc");
                 });
             } else {
                 m->timed("fill_outputs_fc", st, [&] {
@@ -562,14 +665,15 @@ int spiky_lut_forward_step_noalloc(spiky_lut_manager *m, const float *weights,
             throw ValueError("w_min_anchor_deltas and w_min_anchor_delta_indices must be given together");
         const spiky::FcShape s = m->shape(batch_size);
         const bool tm = spiky::tm_fill_applies(s, m->int_mode);
-        const size_t need = tm ? spiky::tm_fill_scratch_bytes(s, m->int_mode) : 0;
+        const hipStream_t st = as_stream(stream);
+        const size_t need =
+            tm ? planned_bytes([&](spiky::Scratch &x) { return layout_fill_tm(m, s, x); }, "fill_outputs_fc") : 0;
         if (need > SPIKY_NOALLOC_SCRATCH_BYTES)
             throw ValueError("forward_step_noalloc: this shape needs " + std::to_string(need) +
                              " bytes of scratch, more than the " +
                              std::to_string(SPIKY_NOALLOC_SCRATCH_BYTES) +
                              " the allocation-free path holds; use forward_step");
         m->context_active = true;
-        const hipStream_t st = as_stream(stream);
         check_hip(spiky::launch_check_detectors(s, input, anchors, cmp_eps, lookup_indices, min_deltas,
                                                 min_delta_indices, st),
                   "check_detectors");
@@ -589,9 +693,10 @@ int spiky_lut_forward_step_noalloc(spiky_lut_manager *m, const float *weights,
         check_hip(hipStreamIsCapturing(st, &cs), "hipStreamIsCapturing");
         const bool eager = cs == hipStreamCaptureStatusNone;
         if (eager && d.recorded) check_hip(hipStreamWaitEvent(st, d.done, 0), "hipStreamWaitEvent(noalloc)");
-        check_hip(spiky::launch_fill_tm(s, weights, lookup_indices, output, m->int_mode,
-                                        m->int_rescaler, d.ptr, st),
-                  "fill_outputs_fc");
+        spiky::Scratch scr = spiky::scratch_run(d.ptr, SPIKY_NOALLOC_SCRATCH_BYTES);
+        check_launch(spiky::launch_fill_tm(s, weights, lookup_indices, output, m->int_mode, m->int_rescaler,
+                                           scr, st),
+                     "fill_outputs_fc");
         if (eager) {
             check_hip(hipEventRecord(d.done, st), "hipEventRecord(noalloc)");
             d.recorded = true;
@@ -624,11 +729,12 @@ int spiky_lut_forward_step_i8(spiky_lut_manager *m, const int8_t *q8, const floa
                       "check_detectors");
         });
         if (spiky::tm_fill_applies(s, m->int_mode)) {
-            void *scr = m->scratch_fwd.ensure(spiky::tm_fill_scratch_bytes(s, m->int_mode));
+            spiky::Scratch scr = m->scratch_fwd.scratch_for(
+                [&](spiky::Scratch &x) { return layout_fill_tm_i8(m, s, x); }, "fill_outputs_fc_i8");
             m->timed("fill_outputs_fc_i8", st, [&] {
-                check_hip(spiky::launch_fill_tm_i8(s, q8, scales, lookup_indices, output, m->int_mode,
-                                                   m->int_rescaler, scr, st),
-                          "fill_outputs_fc_i8");
+                check_launch(spiky::launch_fill_tm_i8(s, q8, scales, lookup_indices, output, m->int_mode,
+                                                      m->int_rescaler, scr, st),
+                             "fill_outputs_fc_i8");
             });
         } else {
             m->timed("fill_outputs_fc_i8", st, [&] {
@@ -671,20 +777,18 @@ int spiky_lut_backward_backprop(spiky_lut_manager *m, float *weights, uint32_t b
         float *target = (ext >= 0.0f) ? weights : weight_grad;
         const bool overwrite = overwrite_weight_grad != 0 && target == weight_grad;
         if (m->fully_connected == 1) {
-            // one scratch: [propagate partials | weight-gradient buckets], used in stream order
-            const bool tm = !m->int_mode && spiky::tm_propagate_applies(s);
-            const size_t prop_bytes =
-                tm ? ((spiky::tm_propagate_scratch_bytes(s) + 255) & ~(size_t)255) : 0;
-            const size_t wg_bytes = target ? spiky::wgrad_fc_scratch_bytes(s) : 0;
-            uint8_t *scr_all = (prop_bytes + wg_bytes)
-                                   ? reinterpret_cast<uint8_t *>(m->scratch.ensure(prop_bytes + wg_bytes))
-                                   : nullptr;
+            const FcBackwardRegions r = fc_backward_regions(m, s, target != nullptr);
+            const bool tm = r.tm;
+            uint8_t *base = reinterpret_cast<uint8_t *>(m->scratch.ensure(r.prop_bytes + r.wg_bytes));
+            const size_t cap = base ? m->scratch.bytes : 0;
+            spiky::Scratch prop_scr = spiky::scratch_run(base, r.prop_bytes);
+            spiky::Scratch wg_scr = spiky::scratch_run(base ? base + r.prop_bytes : nullptr, cap - r.prop_bytes);
             m->timed("propagate_fc", st, [&] {
                 if (tm)
-                    check_hip(spiky::launch_propagate_tm(s, weights, output_grad, lookup_indices,
-                                                         min_deltas, min_delta_indices, anchors,
-                                                         input_grad, scr_all, st),
-                              "propagate_through_detectors_fc");
+                    check_launch(spiky::launch_propagate_tm(s, weights, output_grad, lookup_indices,
+                                                            min_deltas, min_delta_indices, anchors,
+                                                            input_grad, prop_scr, st),
+                                 "propagate_through_detectors_fc");
                 else
                     check_hip(spiky::launch_propagate_fc(s, weights, output_grad, lookup_indices,
                                                          min_deltas, min_delta_indices, anchors,
@@ -696,15 +800,14 @@ int spiky_lut_backward_backprop(spiky_lut_manager *m, float *weights, uint32_t b
                                                     m->int_rescaler, st),
                           "convert_integers_to_floats");
             if (target) {
-                void *scr = wg_bytes ? scr_all + prop_bytes : nullptr;
                 m->timed("gather_w_gradients_fc", st, [&] {
                     // the table-major propagate left the transposed keys at its scratch start
-                    const uint32_t *key_t = tm ? reinterpret_cast<const uint32_t *>(scr_all) : nullptr;
-                    check_hip(spiky::launch_wgrad_fc(s, output_grad, lookup_indices, target, lr,
-                                                     m->int_mode, m->int_rescaler, overwrite, scr, st,
-                                                     key_t, spiky::tm_key_pitch(s.batch),
-                                                     spiky::tm_key_row_shift(s)),
-                              "gather_w_gradients_fc");
+                    const uint32_t *key_t = tm ? reinterpret_cast<const uint32_t *>(base) : nullptr;
+                    check_launch(spiky::launch_wgrad_fc(s, output_grad, lookup_indices, target, lr,
+                                                        m->int_mode, m->int_rescaler, overwrite, wg_scr, st,
+                                                        key_t, spiky::tm_key_pitch(s.batch),
+                                                        spiky::tm_key_row_shift(s)),
+                                 "gather_w_gradients_fc");
                 });
             }
         } else {
@@ -724,13 +827,14 @@ int spiky_lut_backward_backprop(spiky_lut_manager *m, float *weights, uint32_t b
                           "convert_integers_to_floats");
             if (target) {
                 const uint64_t n_syn = m->syn_targets.size();
-                void *scr = m->scratch.ensure(spiky::wgrad_sparse_scratch_bytes(ss));
+                spiky::Scratch scr = m->scratch.scratch_for(
+                    [&](spiky::Scratch &x) { return layout_wgrad_sparse(m, ss, x); }, "gather_w_gradients_sparse");
                 m->timed("gather_w_gradients_sparse", st, [&] {
-                    check_hip(spiky::launch_wgrad_sparse(ss, output_grad, lookup_indices, off, tg,
-                                                         (const int32_t *)m->d_syn_neuron.ptr, target,
-                                                         lr, overwrite, m->int_mode, m->int_rescaler, scr,
-                                                         n_syn, st),
-                              "gather_w_gradients_sparse");
+                    check_launch(spiky::launch_wgrad_sparse(ss, output_grad, lookup_indices, off, tg,
+                                                            (const int32_t *)m->d_syn_neuron.ptr, target,
+                                                            lr, overwrite, m->int_mode, m->int_rescaler, scr,
+                                                            n_syn, st),
+                                 "gather_w_gradients_sparse");
                 });
             }
         }
@@ -812,9 +916,10 @@ int spiky_lut_forward_step_concat(spiky_lut_manager *m, const float *weights, ui
             });
             return;
         }
-        void *scr = m->scratch_fwd.ensure(spiky::seq_scratch_bytes(s, false));
+        spiky::Scratch scr = m->scratch_fwd.scratch_for(
+            [&](spiky::Scratch &x) { return layout_forward_seq(m, s, x); }, "forward_step_concat");
         m->timed("fill_outputs_seq", st, [&] {
-            check_hip(spiky::launch_forward_seq(s, weights, input, anchors, positional_embeddings,
+            check_launch(spiky::launch_forward_seq(s, weights, input, anchors, positional_embeddings,
                                                 output, lookup_indices, positional_lookup_indices,
                                                 min_deltas, min_delta_indices, positional_min_deltas,
                                                 positional_min_delta_indices, cmp_eps, m->int_mode,
@@ -874,9 +979,10 @@ int spiky_lut_backward_backprop_concat(spiky_lut_manager *m, float *weights, uin
             });
             return;
         }
-        void *scr = m->scratch.ensure(spiky::seq_scratch_bytes(s, true));
+        spiky::Scratch scr = m->scratch.scratch_for(
+            [&](spiky::Scratch &x) { return layout_backward_seq(m, s, x); }, "backward_backprop_concat");
         m->timed("backward_seq", st, [&] {
-            check_hip(spiky::launch_backward_seq(s, weights, output_grad, anchors, lookup_indices,
+            check_launch(spiky::launch_backward_seq(s, weights, output_grad, anchors, lookup_indices,
                                                  min_deltas, min_delta_indices,
                                                  positional_lookup_indices, positional_min_deltas,
                                                  positional_min_delta_indices, input_grad,
@@ -938,9 +1044,10 @@ int spiky_lut_forward_step_product(spiky_lut_manager *m, const float *weights, u
         m->context_active = true;
         const hipStream_t st = as_stream(stream);
         if (m->fully_connected == 1) {
-            void *scr = m->scratch_fwd.ensure(spiky::product_scratch_bytes(s, false));
+            spiky::Scratch scr = m->scratch_fwd.scratch_for(
+                [&](spiky::Scratch &x) { return layout_forward_product(m, s, x); }, "forward_step_product");
             m->timed("fill_outputs_product", st, [&] {
-                check_hip(spiky::launch_forward_product(s, weights, input_1, input_2,
+                check_launch(spiky::launch_forward_product(s, weights, input_1, input_2,
                                                         positional_embeddings, anchors, output,
                                                         m->int_mode, m->int_rescaler, scr, st),
                           "forward_step_product");
@@ -995,9 +1102,10 @@ int spiky_lut_backward_backprop_product(spiky_lut_manager *m, float *weights, ui
         if (external_lr >= 0.0) lr *= -external_lr;
         float *target = (external_lr >= 0.0) ? weights : weight_grad;
         if (m->fully_connected == 1) {
-            void *scr = m->scratch.ensure(spiky::product_scratch_bytes(s, true));
+            spiky::Scratch scr = m->scratch.scratch_for(
+                [&](spiky::Scratch &x) { return layout_backward_product(m, s, x); }, "backward_backprop_product");
             m->timed("backward_product", st, [&] {
-                check_hip(spiky::launch_backward_product(s, weights, input_1, input_2,
+                check_launch(spiky::launch_backward_product(s, weights, input_1, input_2,
                                                          positional_embeddings, anchors, output_grad,
                                                          input_grad_1, input_grad_2, positional_grad,
                                                          target, lr, m->int_mode, m->int_rescaler, scr,
@@ -1126,6 +1234,105 @@ int spiky_lut_profiling_stats(const spiky_lut_manager *m, char *buf, uint64_t bu
 
 void spiky_lut_reset_profiler(spiky_lut_manager *m) {
     if (m) m->stats.clear();
+}
+
+int spiky_lut_scratch_plan(spiky_lut_manager *m, int op, uint32_t batch_size, uint32_t sequence_length,
+                           uint32_t n_inputs_1, uint32_t n_inputs_2, int sliced_mode, uint64_t capacity,
+                           uint64_t *needed) {
+    return guarded([&] {
+        require_manager(m);
+        if (!needed) throw ValueError("null output pointer");
+        *needed = 0;
+        if (batch_size == 0) throw ValueError("batch_size == 0");
+        require_initialized(m);
+        const bool fc = m->fully_connected == 1;
+        // a launcher's layout checked against its region [offset, capacity) of
+        // the entry point's buffer (Check mode launches nothing)
+        auto check_region = [&](auto &&layout, uint64_t offset, uint64_t region, const char *what) {
+            spiky::Scratch x;
+            x.mode = spiky::Scratch::Check;
+            x.bytes = capacity > offset ? std::min<uint64_t>(capacity - offset, region) : 0;
+            if (layout(x) != hipSuccess) {
+                std::string why = spiky::scratch_refusal();
+                spiky::scratch_refusal().clear();
+                throw ValueError(why.empty() ? std::string(what) + ": layout refused" : why);
+            }
+        };
+        auto single = [&](auto &&layout, const char *what) {
+            *needed = planned_bytes(layout, what);
+            check_region(layout, 0, UINT64_MAX, what);
+        };
+        switch (op) {
+            case SPIKY_OP_FORWARD:
+            case SPIKY_OP_FORWARD_I8: {
+                if (m->sequence_length != 1)
+                    throw ValueError("forward_step should only be called when sequence_length == 1");
+                if (op == SPIKY_OP_FORWARD_I8 && !fc) throw ValueError("int8 tables need a fully connected manager");
+                const spiky::FcShape s = m->shape(batch_size);
+                if (fc && spiky::tm_fill_applies(s, m->int_mode)) {
+                    if (op == SPIKY_OP_FORWARD)
+                        single([&](spiky::Scratch &x) { return layout_fill_tm(m, s, x); }, "fill_outputs_fc");
+                    else
+                        single([&](spiky::Scratch &x) { return layout_fill_tm_i8(m, s, x); }, "fill_outputs_fc_i8");
+                }
+                break;
+            }
+            case SPIKY_OP_BACKWARD:
+            case SPIKY_OP_BACKWARD_NO_WGRAD: {
+                if (m->sequence_length != 1)
+                    throw ValueError("backward_backprop should only be called when sequence_length == 1");
+                const bool wg = op == SPIKY_OP_BACKWARD;
+                const spiky::FcShape s = m->shape(batch_size);
+                if (fc) {
+                    const FcBackwardRegions r = fc_backward_regions(m, s, wg);
+                    *needed = r.prop_bytes + r.wg_bytes;
+                    if (r.tm)
+                        check_region([&](spiky::Scratch &x) { return layout_propagate_tm(s, x); }, 0, r.prop_bytes,
+                                     "propagate_through_detectors_fc");
+                    if (wg)
+                        check_region([&](spiky::Scratch &x) { return layout_wgrad_fc(m, s, x); }, r.prop_bytes,
+                                     UINT64_MAX, "gather_w_gradients_fc");
+                } else if (wg) {
+                    const spiky::SparseShape ss{s, m->max_groups, m->uniform};
+                    single([&](spiky::Scratch &x) { return layout_wgrad_sparse(m, ss, x); },
+                           "gather_w_gradients_sparse");
+                }
+                break;
+            }
+            case SPIKY_OP_FORWARD_CONCAT:
+            case SPIKY_OP_BACKWARD_CONCAT: {
+                const bool fwd = op == SPIKY_OP_FORWARD_CONCAT;
+                require_seq(m, batch_size, fwd ? "forward_step_concat" : "backward_backprop_concat");
+                const spiky::SeqShape s = seq_shape(m, batch_size);
+                if (fc) {
+                    if (fwd)
+                        single([&](spiky::Scratch &x) { return layout_forward_seq(m, s, x); }, "forward_step_concat");
+                    else
+                        single([&](spiky::Scratch &x) { return layout_backward_seq(m, s, x); },
+                               "backward_backprop_concat");
+                }
+                break;
+            }
+            case SPIKY_OP_FORWARD_PRODUCT:
+            case SPIKY_OP_BACKWARD_PRODUCT: {
+                const bool fwd = op == SPIKY_OP_FORWARD_PRODUCT;
+                const spiky::ProductShape s =
+                    product_shape(m, batch_size, sequence_length, n_inputs_1, n_inputs_2, sliced_mode, 0.0f,
+                                  fwd ? "forward_step_product" : "backward_backprop_product");
+                if (fc) {
+                    if (fwd)
+                        single([&](spiky::Scratch &x) { return layout_forward_product(m, s, x); },
+                               "forward_step_product");
+                    else
+                        single([&](spiky::Scratch &x) { return layout_backward_product(m, s, x); },
+                               "backward_backprop_product");
+                }
+                break;
+            }
+            default:
+                throw ValueError("unknown operation code " + std::to_string(op));
+        }
+    });
 }
 
 int spiky_lut_set_kernel_timing(spiky_lut_manager *m, int enable) {

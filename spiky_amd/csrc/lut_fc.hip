@@ -1093,22 +1093,21 @@ hipError_t launch_propagate_fc(const FcShape &s, const float *w, const float *g,
     return hipGetLastError();
 }
 
-// scratch: bucket offsets [T][E+1] | sorted samples [T][B] | commit values [B][O]
-size_t wgrad_fc_scratch_bytes(const FcShape &s) {
-    if (!rowsum_applies(s)) return 0;
-    return ((size_t)s.n_detectors * (s.n_entries + 1) + (size_t)s.n_detectors * s.batch +
-            (size_t)s.batch * s.n_outputs) *
-           sizeof(int32_t);
-}
-
+// scratch (bucketed path): bucket offsets [T][E+1] | sorted samples [T][B] |
+// commit values [B][O]; the atomic fallback takes none
 hipError_t launch_wgrad_fc(const FcShape &s, const float *g, const int32_t *idx, float *target,
                            double lr, bool int_mode, double int_rescaler, bool overwrite,
-                           void *scratch, hipStream_t st, const uint32_t *key_t,
+                           Scratch &scratch, hipStream_t st, const uint32_t *key_t,
                            uint32_t key_pitch, uint32_t key_shift) {
-    if (rowsum_applies(s) && scratch != nullptr) {
-        int32_t *offsets = reinterpret_cast<int32_t *>(scratch);
-        int32_t *samples = offsets + (size_t)s.n_detectors * (s.n_entries + 1);
-        hipError_t e = launch_bucket_samples(s, idx, offsets, samples, st,
+    const bool rowsum = rowsum_applies(s);
+    ScratchLayout lay(scratch);
+    int32_t *offsets = rowsum ? lay.take<int32_t>((size_t)s.n_detectors * (s.n_entries + 1) * 4) : nullptr;
+    int32_t *samples = rowsum ? lay.take<int32_t>((size_t)s.n_detectors * s.batch * 4) : nullptr;
+    uint32_t *cv = rowsum ? lay.take<uint32_t>((size_t)s.batch * s.n_outputs * 4) : nullptr;
+    hipError_t e;
+    if (lay.stop(&e, "gather_w_gradients_fc")) return e;
+    if (rowsum) {
+        e = launch_bucket_samples(s, idx, offsets, samples, st,
                                              s.n_entries <= 256 ? key_t : nullptr, key_pitch,
                                              key_shift);
         if (e != hipSuccess) return e;
@@ -1119,7 +1118,6 @@ hipError_t launch_wgrad_fc(const FcShape &s, const float *g, const int32_t *idx,
         const uint64_t units = (uint64_t)s.n_detectors * (s.n_entries / rpw);
         const uint64_t grid = (uint64_t)n_slices * ((units + kWPB - 1) / kWPB);
         if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
-        uint32_t *cv = reinterpret_cast<uint32_t *>(samples + (size_t)s.n_detectors * s.batch);
         const uint64_t n_cv = (uint64_t)s.batch * s.n_outputs;
         if (int_mode)
             hipLaunchKernelGGL(k_wgrad_commit_values<true>, dim3(blocks_for(n_cv)), dim3(kBlock), 0,
@@ -1152,7 +1150,7 @@ hipError_t launch_wgrad_fc(const FcShape &s, const float *g, const int32_t *idx,
     const uint64_t n_items = (uint64_t)s.batch * s.n_detectors * s.n_outputs;
     if (n_items == 0) return hipSuccess;
     if (overwrite) {
-        hipError_t e = launch_zero(target, (uint64_t)s.n_detectors * s.n_entries * s.n_outputs, st);
+        e = launch_zero(target, (uint64_t)s.n_detectors * s.n_entries * s.n_outputs, st);
         if (e != hipSuccess) return e;
     }
     if (int_mode)
@@ -1163,7 +1161,7 @@ hipError_t launch_wgrad_fc(const FcShape &s, const float *g, const int32_t *idx,
         hipLaunchKernelGGL(k_wgrad_fc_atomic<false>, dim3(blocks_for(n_items)), dim3(kBlock), 0,
                            st, g, idx, target, s.n_outputs, s.n_detectors, s.n_entries, n_items,
                            lr, int_rescaler);
-    hipError_t e = hipGetLastError();
+    e = hipGetLastError();
     if (e != hipSuccess || !int_mode) return e;
     return launch_convert_i2f(target, (uint64_t)s.n_detectors * s.n_entries * s.n_outputs,
                               int_rescaler, st);

@@ -7,7 +7,77 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <string>
+
 namespace spiky {
+
+// ---- scratch ---------------------------------------------------------------
+// Device memory beyond a launcher's inputs and outputs (partials, keys,
+// buckets) comes in a caller-owned buffer described by a Scratch.  A launcher
+// lays its regions out with a ScratchLayout before it launches anything, so
+// the bytes it asks for and the bytes it addresses come from one layout:
+//   Plan  -- record the layout's end in `needed`, launch nothing;
+//   Check -- also refuse a layout that ends past `bytes`, launch nothing;
+//   Run   -- refuse such a layout (hipErrorInvalidValue, nothing launched),
+//            else launch.
+// In Plan and Check modes no pointer argument is read: they may be null.
+struct Scratch {
+    enum Mode { Plan, Check, Run };
+    void *ptr = nullptr;
+    size_t bytes = 0;
+    Mode mode = Run;
+    size_t needed = 0;  // set by the launcher
+};
+
+inline Scratch scratch_plan() {
+    Scratch s;
+    s.mode = Scratch::Plan;
+    return s;
+}
+
+inline Scratch scratch_run(void *ptr, size_t bytes) {
+    Scratch s;
+    s.ptr = ptr;
+    s.bytes = bytes;
+    return s;
+}
+
+// Why the last launcher on this thread refused its scratch (empty if none).
+inline std::string &scratch_refusal() {
+    thread_local std::string why;
+    return why;
+}
+
+class ScratchLayout {
+  public:
+    explicit ScratchLayout(Scratch &s) : s_(s) {}
+    // The next region: n bytes at a 256-byte boundary.
+    template <typename T>
+    T *take(size_t n) {
+        off_ = (off_ + 255) & ~(size_t)255;
+        T *p = reinterpret_cast<T *>(reinterpret_cast<uintptr_t>(s_.ptr) + off_);
+        off_ += n;
+        return p;
+    }
+    size_t end() const { return off_; }
+    // After the last take(): true when the launcher returns *err now, without
+    // launching (Plan or Check mode, or a layout past the buffer's end).
+    bool stop(hipError_t *err, const char *who) {
+        s_.needed = off_;
+        *err = hipSuccess;
+        if (s_.mode != Scratch::Plan && off_ > s_.bytes) {
+            scratch_refusal() = std::string(who) + ": its scratch layout needs " + std::to_string(off_) +
+                                " bytes, " + std::to_string(s_.bytes) + " given";
+            *err = hipErrorInvalidValue;
+            return true;
+        }
+        return s_.mode != Scratch::Run;
+    }
+
+  private:
+    Scratch &s_;
+    size_t off_ = 0;
+};
 
 // spiky_cuda/misc/misc.h:90 (EPS) and misc.h:98-99 (DENOMINATOR32 and its reciprocal)
 constexpr double kEps = 0.00000000000000001;
@@ -49,16 +119,14 @@ hipError_t launch_propagate_fc(const FcShape &s, const float *w, const float *g,
                                const int32_t *min_idx, const int32_t *anchors, float *x_grad,
                                bool int_mode, double int_rescaler, hipStream_t st);
 
-// Scratch bytes the bucketed weight-gradient path needs (0 if it does not apply).
-size_t wgrad_fc_scratch_bytes(const FcShape &s);
-
 // Table-row gradient: target[row, o] += lr * g[b, o] for every sample b hitting row.
-// scratch may be null when wgrad_fc_scratch_bytes() is 0.  key_t, when given,
-// holds the transposed keys [T][key_pitch] (lookup index << key_shift in the low
-// 16 bits) that launch_propagate_tm leaves at the start of its scratch.
+// The bucketed path lays out its buckets and commit values in scratch (none for
+// the atomic fallback).  key_t, when given, holds the transposed keys
+// [T][key_pitch] (lookup index << key_shift in the low 16 bits) that
+// launch_propagate_tm leaves at the start of its scratch.
 hipError_t launch_wgrad_fc(const FcShape &s, const float *g, const int32_t *idx, float *target,
                            double lr, bool int_mode, double int_rescaler, bool overwrite,
-                           void *scratch, hipStream_t st, const uint32_t *key_t = nullptr,
+                           Scratch &scratch, hipStream_t st, const uint32_t *key_t = nullptr,
                            uint32_t key_pitch = 0, uint32_t key_shift = 7);
 
 // int32 fixed point -> fp32, in place.
@@ -78,13 +146,12 @@ hipError_t launch_bucket_samples(const FcShape &s, const int32_t *idx, int32_t *
 // blocks, committed in ascending order.  Applies to fp32 tables with E <= 256
 // and O % 4 == 0.
 bool tm_fill_applies(const FcShape &s, bool int_mode);
-size_t tm_fill_scratch_bytes(const FcShape &s, bool int_mode);
 hipError_t launch_fill_tm(const FcShape &s, const float *w, const int32_t *idx, float *out,
-                          bool int_mode, double int_rescaler, void *scratch, hipStream_t st);
+                          bool int_mode, double int_rescaler, Scratch &scratch, hipStream_t st);
 // The same with int8 tables and one fp32 scale per table (weight = scale * q).
 hipError_t launch_fill_tm_i8(const FcShape &s, const int8_t *q8, const float *scales,
                              const int32_t *idx, float *out, bool int_mode, double int_rescaler,
-                             void *scratch, hipStream_t st);
+                             Scratch &scratch, hipStream_t st);
 
 // fp32-summation min-margin input gradient through per-slice partial dots.
 // out[i] (+)= sum over k of part[k][i] in ascending k (fp32, or wrapping int32
@@ -96,11 +163,10 @@ bool tm_propagate_applies(const FcShape &s);
 // propagate writes.
 uint32_t tm_key_pitch(uint32_t batch);
 uint32_t tm_key_row_shift(const FcShape &s);
-size_t tm_propagate_scratch_bytes(const FcShape &s);
 hipError_t launch_propagate_tm(const FcShape &s, const float *w, const float *g,
                                const int32_t *idx, const float *min_deltas,
                                const int32_t *min_idx, const int32_t *anchors, float *x_grad,
-                               void *scratch, hipStream_t st);
+                               Scratch &scratch, hipStream_t st);
 
 // Commit values of the weight gradient for every (row, output) of g
 // (lut_fc.hip k_wgrad_commit_values).
@@ -119,13 +185,12 @@ struct SeqShape {
     uint32_t dgs;
     uint32_t ogs;
 };
-size_t seq_scratch_bytes(const SeqShape &s, bool backward);
 // check_detectors_seq(_eval) + check_positional_embeddings(_eval) +
 // fill_outputs_fully_connected_seq; md == null selects eval mode.
 hipError_t launch_forward_seq(const SeqShape &s, const float *w, const float *x,
                               const int32_t *anchors, const float *pe, float *out, int32_t *idx,
                               int32_t *pidx, float *md, int32_t *mi, float *pmd, int32_t *pmi,
-                              float cmp_eps, bool int_mode, double int_rescaler, void *scratch,
+                              float cmp_eps, bool int_mode, double int_rescaler, Scratch &scratch,
                               hipStream_t st);
 // propagate_through_detectors_seq_fc + gather_w_gradients_seq_fc; target is the
 // weight gradient (or the weights for the Internal policy, lr folded in), or null.
@@ -133,7 +198,7 @@ hipError_t launch_backward_seq(const SeqShape &s, float *w, const float *g, cons
                                const int32_t *idx, const float *md, const int32_t *mi,
                                const int32_t *pidx, const float *pmd, const int32_t *pmi,
                                float *x_grad, float *pe_grad, float *target, double lr,
-                               bool overwrite, bool int_mode, double int_rescaler, void *scratch,
+                               bool overwrite, bool int_mode, double int_rescaler, Scratch &scratch,
                                hipStream_t st);
 
 // Zero n floats with a kernel (graph-capture safe, unlike hipMemsetAsync).
@@ -172,15 +237,12 @@ hipError_t launch_propagate_sparse(const SparseShape &s, const float *w, const f
                                    float *x_grad, bool int_mode, double int_rescaler,
                                    hipStream_t st);
 
-// Scratch: the same bucket arrays as the FC path.
-size_t wgrad_sparse_scratch_bytes(const SparseShape &s);
-
 // syn_neuron[s] = the lookup neuron of synapse s.  overwrite: target starts
-// from zero (it is not read).
+// from zero (it is not read).  Scratch: the FC path's bucket arrays.
 hipError_t launch_wgrad_sparse(const SparseShape &s, const float *g, const int32_t *idx,
                                const int64_t *syn_offsets, const int32_t *syn_targets,
                                const int32_t *syn_neuron, float *target, double lr, bool overwrite,
-                               bool int_mode, double int_rescaler, void *scratch,
+                               bool int_mode, double int_rescaler, Scratch &scratch,
                                uint64_t n_synapses, hipStream_t st);
 
 // ---- product mode (concatenation_product == False, lut_product.hip) ---------
@@ -214,12 +276,11 @@ struct ProductShape {
     float cmp_eps;
 };
 bool product_applies(const ProductShape &s);
-size_t product_scratch_bytes(const ProductShape &s, bool backward);
 // out (+)= sum over pairs i < j and tables of W[t][lookup]; int32 payloads
 // when int_mode (the caller converts).
 hipError_t launch_forward_product(const ProductShape &s, const float *w, const float *x1,
                                   const float *x2, const float *pe, const int32_t *anchors,
-                                  float *out, bool int_mode, double int_rescaler, void *scratch,
+                                  float *out, bool int_mode, double int_rescaler, Scratch &scratch,
                                   hipStream_t st);
 // Input, positional and (target != null) weight gradients; x1_grad may alias
 // x2_grad.  target gets lr * g terms (weight gradient, or the weights
@@ -241,7 +302,7 @@ hipError_t launch_backward_product(const ProductShape &s, const float *w, const 
                                    const float *x2, const float *pe, const int32_t *anchors,
                                    const float *g, float *x1_grad, float *x2_grad, float *pe_grad,
                                    float *target, double lr, bool int_mode, double int_rescaler,
-                                   void *scratch, hipStream_t st);
+                                   Scratch &scratch, hipStream_t st);
 
 // ---- dense -> sparse compaction of 32-bit words (lut_densify.hip) ---------
 // Workspace (tile counts, then offsets) for a source of n words (n % 4 == 0).

@@ -825,32 +825,20 @@ bool product_applies(const ProductShape &s) {
 // scratch: Cnt [B*S][T*E] f32 | P [B*S][T*E] f64 (backward) | split-K partials
 // of the product that sums over the longest dimension (forward: Cnt . W over
 // T*E; backward: Cnt^T . g' over B*S)
-static size_t cnt_bytes(const ProductShape &s) {
-    const uint64_t TE = (uint64_t)s.n_detectors << s.n_anchors;
-    return ((uint64_t)s.batch * s.seq_len * TE * 4 + 255) & ~(size_t)255;
-}
-
-static size_t p_bytes(const ProductShape &s) {
-    const uint64_t TE = (uint64_t)s.n_detectors << s.n_anchors;
-    return ((uint64_t)s.batch * s.seq_len * TE * 8 + 255) & ~(size_t)255;
-}
-
-size_t product_scratch_bytes(const ProductShape &s, bool backward) {
-    const uint32_t TE = s.n_detectors << s.n_anchors;
-    const uint32_t BS = s.batch * s.seq_len;
-    if (!backward) return cnt_bytes(s) + splitk_bytes(BS, s.n_outputs, TE);
-    return cnt_bytes(s) + p_bytes(s) + splitk_bytes(TE, s.n_outputs, BS);
-}
 
 hipError_t launch_forward_product(const ProductShape &s, const float *w, const float *x1,
                                   const float *x2, const float *pe, const int32_t *anchors,
-                                  float *out, bool int_mode, double int_rescaler, void *scratch,
+                                  float *out, bool int_mode, double int_rescaler, Scratch &scratch,
                                   hipStream_t st) {
     const uint32_t E = 1u << s.n_anchors;
     const uint32_t TE = s.n_detectors * E;
     const uint32_t BS = s.batch * s.seq_len;
+    ScratchLayout sl(scratch);
+    float *cnt = sl.take<float>((size_t)BS * TE * 4);
+    double *part = sl.take<double>(splitk_bytes(BS, s.n_outputs, TE));
+    hipError_t e;
+    if (sl.stop(&e, "forward_step_product")) return e;
     if (BS == 0) return hipSuccess;
-    float *cnt = reinterpret_cast<float *>(scratch);
     const int2 *anc = reinterpret_cast<const int2 *>(anchors);
     const TableLayout lay = table_grid_ok(s, table_layout(s, false, 0));
     const uint32_t njb = lay.jb ? (s.seq_len + lay.jb - 1) / lay.jb : 0;
@@ -873,13 +861,12 @@ hipError_t launch_forward_product(const ProductShape &s, const float *w, const f
     if (int_mode) { SPIKY_PP(true); } else { SPIKY_PP(false); }
 #undef SPIKY_PP
 #undef SPIKY_PT
-    hipError_t e = hipGetLastError();
+    e = hipGetLastError();
     if (e != hipSuccess) return e;
     // out[bj][o] (+)= sum_k cnt[bj][k] * W[k][o]
     if (int_mode)
         return gemm<false, false, 1, 1>(cnt, TE, w, s.n_outputs, out, BS, s.n_outputs, TE, 0.0,
                                         int_rescaler, st);
-    double *part = reinterpret_cast<double *>(reinterpret_cast<uint8_t *>(scratch) + cnt_bytes(s));
     return gemm_mfma<false, false, 0, 0>(cnt, TE, w, s.n_outputs, out, BS, s.n_outputs, TE, 0.0, part,
                                          st);
 }
@@ -888,17 +875,19 @@ hipError_t launch_backward_product(const ProductShape &s, const float *w, const 
                                    const float *x2, const float *pe, const int32_t *anchors,
                                    const float *g, float *x1_grad, float *x2_grad, float *pe_grad,
                                    float *target, double lr, bool int_mode, double int_rescaler,
-                                   void *scratch, hipStream_t st) {
+                                   Scratch &scratch, hipStream_t st) {
     const uint32_t E = 1u << s.n_anchors;
     const uint32_t TE = s.n_detectors * E;
     const uint32_t BS = s.batch * s.seq_len;
+    ScratchLayout sl(scratch);
+    float *cnt = sl.take<float>((size_t)BS * TE * 4);
+    double *P = sl.take<double>((size_t)BS * TE * 8);
+    double *part = sl.take<double>(splitk_bytes(TE, s.n_outputs, BS));
+    hipError_t e;
+    if (sl.stop(&e, "backward_backprop_product")) return e;
     if (BS == 0) return hipSuccess;
-    float *cnt = reinterpret_cast<float *>(scratch);
-    double *P = reinterpret_cast<double *>(reinterpret_cast<uint8_t *>(scratch) + cnt_bytes(s));
-    double *part = reinterpret_cast<double *>(reinterpret_cast<uint8_t *>(scratch) + cnt_bytes(s) +
-                                              p_bytes(s));
     // P[bj][k] = sum_o g[bj][o] * W[k][o]  (fp64; no split: B*S x T*E tiles fill the chip)
-    hipError_t e = gemm_mfma<false, true, 0, 2>(g, s.n_outputs, w, s.n_outputs, P, BS, TE,
+    e = gemm_mfma<false, true, 0, 2>(g, s.n_outputs, w, s.n_outputs, P, BS, TE,
                                                 s.n_outputs, 0.0, nullptr, st);
     if (e != hipSuccess) return e;
     const int2 *anc = reinterpret_cast<const int2 *>(anchors);

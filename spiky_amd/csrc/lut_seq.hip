@@ -2034,8 +2034,6 @@ __global__ __launch_bounds__(kBlock) void k_wgrad_seq_atomic(
 
 uint32_t blocks_for(uint64_t n) { return (uint32_t)((n + kBlock - 1) / kBlock); }
 
-uint64_t align256_u64(uint64_t x) { return (x + 255) & ~(uint64_t)255; }
-
 uint32_t seq_vec(uint32_t n_outputs) {
     if (n_outputs % 4 == 0 && n_outputs >= 64u * 4u * 4u) return 4;
     if (n_outputs % 2 == 0 && n_outputs >= 64u * 2u * 4u) return 2;
@@ -2062,14 +2060,6 @@ int seq_grp_bits(const SeqShape &s) {
     while ((kGrpTabBytes >> (lr + 1)) >= (int)(s.n_outputs * 4)) lr++;
     if (s.pe_dim > lr) return -1;
     return (int)std::min<uint32_t>(s.n_anchors, lr - s.pe_dim);
-}
-
-// Bytes of the grouped pass's position lists: two [T][B][S] entry arrays and
-// two [T][B][groups + 1] offset arrays.
-uint64_t seq_grp_list_bytes(const SeqShape &s, int gb) {
-    const uint64_t tb = (uint64_t)s.n_detectors * s.batch;
-    const uint64_t ng = 1ull << (s.n_anchors - gb);
-    return 2 * align256_u64(tb * s.seq * 8) + 2 * align256_u64(tb * (ng + 1) * 4);
 }
 
 // Columns of a forward slice for k_fill_seq_lds (0: it does not apply): the
@@ -2109,40 +2099,6 @@ uint32_t seq_wg_items(const SeqShape &s, uint32_t cols) {
 
 }  // namespace
 
-// scratch: pack [T][B*S] | ppack [T][S-1] | dq, dk [B][T][S] f64 | dpe [(S-1)][T][Npe] f64 |
-//          bucket offsets [T][2^Nc+1] | samples [T][B*S] | commit values [B*S][O]
-static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
-
-// forward scratch: pack | ppack | [bucket offsets | samples | partials [T][B*S][O]]
-size_t seq_scratch_bytes(const SeqShape &s, bool backward) {
-    const size_t rows = (size_t)s.batch * s.seq;
-    size_t n = align256(rows * s.n_detectors * 8) + align256((size_t)s.n_detectors * (s.seq - 1) * 8);
-    if (!backward) {
-        if (seq_fill_cols(s) == 0) return n;
-        n += align256((size_t)s.n_detectors * ((1u << s.n_anchors) + 1) * 4);
-        n += align256((size_t)s.n_detectors * rows * 4);
-        n += align256((size_t)s.n_detectors * rows * s.n_outputs * 4);
-        return n;
-    }
-    n += 3 * align256(rows * s.n_detectors * 8);
-    n += align256((size_t)(s.seq - 1) * s.n_detectors * std::max<uint32_t>(s.pe_dim, 1) * 8);
-    n += align256((size_t)s.n_detectors * ((1u << s.n_anchors) + 1) * 4);
-    n += align256((size_t)s.n_detectors * rows * 4);
-    n += align256(rows * s.n_outputs * 4);
-    // Q-flip pass: keys [B*S][T], offsets [T][2^(Nc+1)+1], samples [T][B*S]
-    n += align256(rows * s.n_detectors * 4);
-    n += align256((size_t)s.n_detectors * ((2u << s.n_anchors) + 1) * 4);
-    n += align256((size_t)s.n_detectors * rows * 4);
-    // position lists of the grouped pass, else the pair triangles of the
-    // pair-parallel main pass
-    const int gb = seq_grp_bits(s);
-    if (gb >= 0)
-        n += seq_grp_list_bytes(s, gb);
-    else if (seq_pairs_applies(s))
-        n += 2 * align256(seq_tri_bytes(s));
-    return n;
-}
-
 hipError_t launch_seq_indices(const SeqShape &s, const float *x, const int32_t *anchors,
                               const float *pe, int32_t *idx, int32_t *pidx, float *md, int32_t *mi,
                               float *pmd, int32_t *pmi, float cmp_eps, hipStream_t st) {
@@ -2173,9 +2129,25 @@ hipError_t launch_seq_indices(const SeqShape &s, const float *x, const int32_t *
 hipError_t launch_forward_seq(const SeqShape &s, const float *w, const float *x,
                               const int32_t *anchors, const float *pe, float *out, int32_t *idx,
                               int32_t *pidx, float *md, int32_t *mi, float *pmd, int32_t *pmi,
-                              float cmp_eps, bool int_mode, double int_rescaler, void *scratch,
+                              float cmp_eps, bool int_mode, double int_rescaler, Scratch &scratch,
                               hipStream_t st) {
     const uint32_t rows = s.batch * s.seq;
+    const uint32_t fcols = seq_fill_cols(s);
+    // scratch: packed keys [T][B*S] | positional keys [T][S-1] | and for the
+    // LDS-sliced forward: bucket offsets [T][2^Nc+1] | samples [T][B*S] |
+    // per-table partials [T][B*S][O]
+    ScratchLayout lay(scratch);
+    uint2 *pack = lay.take<uint2>((size_t)rows * s.n_detectors * 8);
+    uint2 *ppack = lay.take<uint2>((size_t)s.n_detectors * (s.seq - 1) * 8);
+    int32_t *offsets = nullptr, *samples = nullptr;
+    uint32_t *part = nullptr;
+    if (fcols > 0) {
+        offsets = lay.take<int32_t>((size_t)s.n_detectors * ((1u << s.n_anchors) + 1) * 4);
+        samples = lay.take<int32_t>((size_t)s.n_detectors * rows * 4);
+        part = lay.take<uint32_t>((size_t)s.n_detectors * rows * s.n_outputs * 4);
+    }
+    hipError_t e;
+    if (lay.stop(&e, "forward_step_concat")) return e;
     FcShape fs{};
     fs.batch = rows;
     fs.n_inputs = s.n_inputs;
@@ -2185,12 +2157,9 @@ hipError_t launch_forward_seq(const SeqShape &s, const float *w, const float *x,
     fs.n_entries = 1u << s.n_anchors;
     fs.dgs = s.dgs;
     fs.ogs = s.ogs;
-    hipError_t e = launch_seq_indices(s, x, anchors, pe, idx, pidx, md, mi, pmd, pmi, cmp_eps, st);
+    e = launch_seq_indices(s, x, anchors, pe, idx, pidx, md, mi, pmd, pmi, cmp_eps, st);
     if (e != hipSuccess) return e;
     const uint32_t n_pe = (s.seq - 1) * s.n_detectors;
-    uint8_t *sp = reinterpret_cast<uint8_t *>(scratch);
-    uint2 *pack = reinterpret_cast<uint2 *>(sp);
-    uint2 *ppack = reinterpret_cast<uint2 *>(sp + align256((size_t)rows * s.n_detectors * 8));
     hipLaunchKernelGGL(k_seq_pack, dim3((s.n_detectors + 63) / 64, (rows + 63) / 64), dim3(kBlock),
                        0, st, idx, (const float *)nullptr, (const int32_t *)nullptr, pack, rows,
                        s.n_detectors);
@@ -2199,14 +2168,7 @@ hipError_t launch_forward_seq(const SeqShape &s, const float *w, const float *x,
                        (const int32_t *)nullptr, ppack, s.seq - 1, s.n_detectors);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const uint32_t fcols = seq_fill_cols(s);
     if (fcols > 0) {
-        size_t off = align256((size_t)rows * s.n_detectors * 8) + align256((size_t)s.n_detectors * (s.seq - 1) * 8);
-        int32_t *offsets = reinterpret_cast<int32_t *>(sp + off);
-        off += align256((size_t)s.n_detectors * ((1u << s.n_anchors) + 1) * 4);
-        int32_t *samples = reinterpret_cast<int32_t *>(sp + off);
-        off += align256((size_t)s.n_detectors * rows * 4);
-        uint32_t *part = reinterpret_cast<uint32_t *>(sp + off);
         FcShape fs2 = fs;
         e = launch_bucket_samples(fs2, idx, offsets, samples, st);
         if (e != hipSuccess) return e;
@@ -2261,62 +2223,53 @@ hipError_t launch_backward_seq(const SeqShape &s, float *w, const float *g, cons
                                const int32_t *idx, const float *md, const int32_t *mi,
                                const int32_t *pidx, const float *pmd, const int32_t *pmi,
                                float *x_grad, float *pe_grad, float *target, double lr,
-                               bool overwrite, bool int_mode, double int_rescaler, void *scratch,
+                               bool overwrite, bool int_mode, double int_rescaler, Scratch &scratch,
                                hipStream_t st) {
     const uint32_t rows = s.batch * s.seq;
     const uint32_t n_pe = (s.seq - 1) * s.n_detectors;
-    uint8_t *sp = reinterpret_cast<uint8_t *>(scratch);
-    size_t off = 0;
-    uint2 *pack = reinterpret_cast<uint2 *>(sp + off);
-    off += align256((size_t)rows * s.n_detectors * 8);
-    uint2 *ppack = reinterpret_cast<uint2 *>(sp + off);
-    off += align256((size_t)s.n_detectors * (s.seq - 1) * 8);
-    double *dq = reinterpret_cast<double *>(sp + off);
-    off += align256((size_t)rows * s.n_detectors * 8);
-    double *dq_alt = reinterpret_cast<double *>(sp + off);
-    off += align256((size_t)rows * s.n_detectors * 8);
-    double *dk = reinterpret_cast<double *>(sp + off);
-    off += align256((size_t)rows * s.n_detectors * 8);
-    double *dpe = reinterpret_cast<double *>(sp + off);
     const size_t n_dpe = (size_t)n_pe * std::max<uint32_t>(s.pe_dim, 1);
-    off += align256(n_dpe * 8);
-    int32_t *offsets = reinterpret_cast<int32_t *>(sp + off);
-    off += align256((size_t)s.n_detectors * ((1u << s.n_anchors) + 1) * 4);
-    int32_t *samples = reinterpret_cast<int32_t *>(sp + off);
-    off += align256((size_t)s.n_detectors * rows * 4);
-    uint32_t *cv = reinterpret_cast<uint32_t *>(sp + off);
-    off += align256((size_t)rows * s.n_outputs * 4);
-    int32_t *alt_keys = reinterpret_cast<int32_t *>(sp + off);
-    off += align256((size_t)rows * s.n_detectors * 4);
-    int32_t *offsets2 = reinterpret_cast<int32_t *>(sp + off);
-    off += align256((size_t)s.n_detectors * ((2u << s.n_anchors) + 1) * 4);
-    int32_t *samples2 = reinterpret_cast<int32_t *>(sp + off);
-    off += align256((size_t)s.n_detectors * rows * 4);
     const int gb = int_mode ? -1 : seq_grp_bits(s);
     const bool pairs = gb < 0 && seq_pairs_applies(s);
-    double *tk = pairs ? reinterpret_cast<double *>(sp + off) : nullptr;
-    if (pairs) off += align256(seq_tri_bytes(s));
-    double *tp = pairs ? reinterpret_cast<double *>(sp + off) : nullptr;
+    // scratch: packed keys [T][B*S] | positional keys [T][S-1] | dq, dq_alt,
+    // dk [B*S][T] f64 | dpe [(S-1)][T][Npe] f64 | bucket offsets [T][2^Nc+1] |
+    // samples [T][B*S] | commit values [B*S][O] | Q-flipped keys [B*S][T] |
+    // their bucket offsets [T][2^(Nc+1)+1] and samples [T][B*S] | then the
+    // pair triangles of the pair-parallel pass, or the position lists of the
+    // grouped pass
+    ScratchLayout lay(scratch);
+    uint2 *pack = lay.take<uint2>((size_t)rows * s.n_detectors * 8);
+    uint2 *ppack = lay.take<uint2>((size_t)s.n_detectors * (s.seq - 1) * 8);
+    double *dq = lay.take<double>((size_t)rows * s.n_detectors * 8);
+    double *dq_alt = lay.take<double>((size_t)rows * s.n_detectors * 8);
+    double *dk = lay.take<double>((size_t)rows * s.n_detectors * 8);
+    double *dpe = lay.take<double>(n_dpe * 8);
+    int32_t *offsets = lay.take<int32_t>((size_t)s.n_detectors * ((1u << s.n_anchors) + 1) * 4);
+    int32_t *samples = lay.take<int32_t>((size_t)s.n_detectors * rows * 4);
+    uint32_t *cv = lay.take<uint32_t>((size_t)rows * s.n_outputs * 4);
+    int32_t *alt_keys = lay.take<int32_t>((size_t)rows * s.n_detectors * 4);
+    int32_t *offsets2 = lay.take<int32_t>((size_t)s.n_detectors * ((2u << s.n_anchors) + 1) * 4);
+    int32_t *samples2 = lay.take<int32_t>((size_t)s.n_detectors * rows * 4);
+    double *tk = pairs ? lay.take<double>(seq_tri_bytes(s)) : nullptr;
+    double *tp = pairs ? lay.take<double>(seq_tri_bytes(s)) : nullptr;
     uint2 *list_a = nullptr, *list_b = nullptr;
     uint32_t *off_a = nullptr, *off_b = nullptr;
     if (gb >= 0) {
         const uint64_t tb = (uint64_t)s.n_detectors * s.batch;
         const uint64_t ng = 1ull << (s.n_anchors - gb);
-        list_a = reinterpret_cast<uint2 *>(sp + off);
-        off += align256_u64(tb * s.seq * 8);
-        list_b = reinterpret_cast<uint2 *>(sp + off);
-        off += align256_u64(tb * s.seq * 8);
-        off_a = reinterpret_cast<uint32_t *>(sp + off);
-        off += align256_u64(tb * (ng + 1) * 4);
-        off_b = reinterpret_cast<uint32_t *>(sp + off);
+        list_a = lay.take<uint2>(tb * s.seq * 8);
+        list_b = lay.take<uint2>(tb * s.seq * 8);
+        off_a = lay.take<uint32_t>(tb * (ng + 1) * 4);
+        off_b = lay.take<uint32_t>(tb * (ng + 1) * 4);
     }
+    hipError_t e;
+    if (lay.stop(&e, "backward_backprop_concat")) return e;
 
     hipLaunchKernelGGL(k_seq_pack, dim3((s.n_detectors + 63) / 64, (rows + 63) / 64), dim3(kBlock),
                        0, st, idx, md, mi, pack, rows, s.n_detectors);
     hipLaunchKernelGGL(k_seq_pack_pe, dim3(blocks_for(n_pe)), dim3(kBlock), 0, st,
                        s.pe_dim > 0 ? pidx : (const int32_t *)nullptr, pmd, pmi, ppack, s.seq - 1,
                        s.n_detectors);
-    hipError_t e = hipGetLastError();
+    e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int2 *ap = reinterpret_cast<const int2 *>(anchors);
 

@@ -321,21 +321,20 @@ hipError_t launch_propagate_sparse(const SparseShape &s, const float *w, const f
     return hipGetLastError();
 }
 
-size_t wgrad_sparse_scratch_bytes(const SparseShape &s) {
-    return ((size_t)s.fc.n_detectors * (s.fc.n_entries + 1) +
-            (size_t)s.fc.n_detectors * s.fc.batch) * sizeof(int32_t);
-}
-
+// scratch: bucket offsets [T][E+1] | sorted samples [T][B]
 hipError_t launch_wgrad_sparse(const SparseShape &s, const float *g, const int32_t *idx,
                                const int64_t *syn_offsets, const int32_t *syn_targets,
                                const int32_t *syn_neuron, float *target, double lr, bool overwrite,
-                               bool int_mode, double int_rescaler, void *scratch,
+                               bool int_mode, double int_rescaler, Scratch &scratch,
                                uint64_t n_synapses, hipStream_t st) {
     (void)syn_offsets;
+    ScratchLayout lay(scratch);
+    int32_t *offsets = lay.take<int32_t>((size_t)s.fc.n_detectors * (s.fc.n_entries + 1) * 4);
+    int32_t *samples = lay.take<int32_t>((size_t)s.fc.n_detectors * s.fc.batch * 4);
+    hipError_t e;
+    if (lay.stop(&e, "gather_w_gradients_sparse")) return e;
     if (n_synapses == 0) return hipSuccess;
-    int32_t *offsets = reinterpret_cast<int32_t *>(scratch);
-    int32_t *samples = offsets + (size_t)s.fc.n_detectors * (s.fc.n_entries + 1);
-    hipError_t e = launch_bucket_samples(s.fc, idx, offsets, samples, st);
+    e = launch_bucket_samples(s.fc, idx, offsets, samples, st);
     if (e != hipSuccess) return e;
 #define SPIKY_WS(IM, OW)                                                                          \
     hipLaunchKernelGGL((k_wgrad_sparse_rowsum<IM, OW>), dim3(blocks_for(n_synapses)), dim3(kBlock), \

@@ -1219,36 +1219,33 @@ static uint32_t tm_fill_pitch(const FcShape &s) {
     return n_chunks * kTmPass * spt;
 }
 
-size_t tm_fill_scratch_bytes(const FcShape &s, bool int_mode) {
-    const uint64_t n_blocks = (s.n_detectors + s.dgs - 1) / s.dgs;
-    const uint64_t bpu = tm_fill_bpu(s, int_mode);
-    const size_t keys = ((size_t)s.n_detectors * tm_fill_pitch(s) + 255) & ~(size_t)255;
-    return keys + (size_t)((n_blocks + bpu - 1) / bpu) * s.batch * s.n_outputs * 4;
-}
-
+// scratch: u8 lookup indices transposed [T][pitch] | partials [n_parts][B][O]
+// (fp32 commits, or wrapping int32 sums)
 template <typename WT>
 static hipError_t launch_fill_tm_impl(const FcShape &s, const WT *w, const float *scales,
                                       const int32_t *idx, float *out, bool int_mode,
-                                      double int_rescaler, void *scratch, hipStream_t st) {
-    uint8_t *idx_t = reinterpret_cast<uint8_t *>(scratch);
+                                      double int_rescaler, Scratch &scratch, hipStream_t st) {
     const uint32_t pitch = tm_fill_pitch(s);
-    const size_t keys = ((size_t)s.n_detectors * pitch + 255) & ~(size_t)255;
-    uint32_t *part = reinterpret_cast<uint32_t *>(reinterpret_cast<uint8_t *>(scratch) + keys);
-    // the DMA form reads whole 16-byte key pieces: pad the rows with zeros
-    const bool dma = std::is_same<WT, float>::value && s.n_entries == (uint32_t)kTmMaxEntries;
-    const uint32_t ipitch = dma ? pitch : s.batch;
-    hipLaunchKernelGGL(k_transpose_idx, dim3((s.n_detectors + 63) / 64, (ipitch + 63) / 64),
-                       dim3(256), 0, st, idx, idx_t, s.batch, s.n_detectors, ipitch);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
     const uint32_t spt = tm_spt(s.batch);
     const uint32_t n_chunks = (s.batch + kTmPass * spt - 1) / (kTmPass * spt);
     const uint32_t n_slices = (s.n_outputs + kTmCols - 1) / kTmCols;
     const uint32_t n_blocks = (s.n_detectors + s.dgs - 1) / s.dgs;
     const uint32_t bpu = tm_fill_bpu(s, int_mode);
     const uint32_t n_parts = (n_blocks + bpu - 1) / bpu;
+    ScratchLayout lay(scratch);
+    uint8_t *idx_t = lay.take<uint8_t>((size_t)s.n_detectors * pitch);
+    uint32_t *part = lay.take<uint32_t>((size_t)n_parts * s.batch * s.n_outputs * 4);
+    hipError_t e;
+    if (lay.stop(&e, "fill_outputs_fc (table-major)")) return e;
+    // the DMA form reads whole 16-byte key pieces: pad the rows with zeros
+    const bool dma = std::is_same<WT, float>::value && s.n_entries == (uint32_t)kTmMaxEntries;
+    const uint32_t ipitch = dma ? pitch : s.batch;
     const uint64_t grid = (uint64_t)n_parts * n_chunks * n_slices;
     if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL(k_transpose_idx, dim3((s.n_detectors + 63) / 64, (ipitch + 63) / 64),
+                       dim3(256), 0, st, idx, idx_t, s.batch, s.n_detectors, ipitch);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
     if (dma) {
         const float *wf = reinterpret_cast<const float *>(w);
         // a 4-stage ring, one workgroup per CU.  (A 2-stage ring with chunks of
@@ -1292,13 +1289,13 @@ static hipError_t launch_fill_tm_impl(const FcShape &s, const WT *w, const float
 }
 
 hipError_t launch_fill_tm(const FcShape &s, const float *w, const int32_t *idx, float *out,
-                          bool int_mode, double int_rescaler, void *scratch, hipStream_t st) {
+                          bool int_mode, double int_rescaler, Scratch &scratch, hipStream_t st) {
     return launch_fill_tm_impl<float>(s, w, nullptr, idx, out, int_mode, int_rescaler, scratch, st);
 }
 
 hipError_t launch_fill_tm_i8(const FcShape &s, const int8_t *q8, const float *scales,
                              const int32_t *idx, float *out, bool int_mode, double int_rescaler,
-                             void *scratch, hipStream_t st) {
+                             Scratch &scratch, hipStream_t st) {
     return launch_fill_tm_impl<int8_t>(s, q8, scales, idx, out, int_mode, int_rescaler, scratch, st);
 }
 
@@ -1354,24 +1351,21 @@ uint32_t tm_key_pitch(uint32_t batch) {
 
 // scratch: keys [T][pitch] u32 | du_t [T][pitch] f32 | then, for the
 // whole-table propagate, du [B][T] f32; for the slice propagate, partial dots
-// [slices][T][B] f32 | du [B][T] f32
-size_t tm_propagate_scratch_bytes(const FcShape &s) {
-    const uint64_t n_slices = (s.n_outputs + kTmCols - 1) / kTmCols;
-    const size_t keys = ((size_t)s.n_detectors * tm_key_pitch(s.batch) * 4 + 255) & ~(size_t)255;
-    if (tm_propagate_wide(s)) return 2 * keys + (size_t)s.batch * s.n_detectors * 4;
-    return 2 * keys + (size_t)(n_slices + 1) * s.batch * s.n_detectors * 4;
-}
-
+// [slices][T][B] f32 and du [B][T] f32 after them
 hipError_t launch_propagate_tm(const FcShape &s, const float *w, const float *g,
                                const int32_t *idx, const float *min_deltas,
                                const int32_t *min_idx, const int32_t *anchors, float *x_grad,
-                               void *scratch, hipStream_t st) {
-    uint32_t *key_t = reinterpret_cast<uint32_t *>(scratch);
+                               Scratch &scratch, hipStream_t st) {
     const uint32_t pitch = tm_key_pitch(s.batch);
-    const size_t keys = ((size_t)s.n_detectors * pitch * 4 + 255) & ~(size_t)255;
-    float *du_t = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(scratch) + keys);
-    float *dpart = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(scratch) + 2 * keys);
     const bool wide = tm_propagate_wide(s);
+    const uint32_t n_slices = (s.n_outputs + kTmCols - 1) / kTmCols;
+    ScratchLayout lay(scratch);
+    uint32_t *key_t = lay.take<uint32_t>((size_t)s.n_detectors * pitch * 4);
+    float *du_t = lay.take<float>((size_t)s.n_detectors * pitch * 4);
+    // wide: du [B][T]; else the slice partials and du after them
+    float *dpart = lay.take<float>((size_t)(wide ? 1 : n_slices + 1) * s.batch * s.n_detectors * 4);
+    hipError_t e;
+    if (lay.stop(&e, "propagate_through_detectors_fc (table-major)")) return e;
     if (s.n_detectors % 4 == 0 && pitch % 4 == 0)
         hipLaunchKernelGGL(k_transpose_keys4, dim3((s.n_detectors + 63) / 64, (pitch + 63) / 64),
                            dim3(256), 0, st, idx, min_idx, min_deltas, key_t, wide ? du_t : nullptr,
@@ -1380,9 +1374,8 @@ hipError_t launch_propagate_tm(const FcShape &s, const float *w, const float *g,
         hipLaunchKernelGGL(k_transpose_keys, dim3((s.n_detectors + 63) / 64, (pitch + 63) / 64),
                            dim3(256), 0, st, idx, min_idx, min_deltas, key_t, wide ? du_t : nullptr,
                            s.batch, pitch, s.n_detectors, s.n_anchors, s.n_entries, wide ? 8u : 7u);
-    hipError_t e = hipGetLastError();
+    e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const uint32_t n_slices = (s.n_outputs + kTmCols - 1) / kTmCols;
     const uint32_t tpu = 32;
     const uint32_t n_units = (s.n_detectors + tpu - 1) / tpu;
     if (wide) {
@@ -1397,7 +1390,7 @@ hipError_t launch_propagate_tm(const FcShape &s, const float *w, const float *g,
         const uint32_t n_chunks = (s.batch + kUnitPass * spt - 1) / (kUnitPass * spt);
         const uint64_t grid = (uint64_t)((s.n_detectors + kTpu - 1) / kTpu) * n_chunks;
         if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
-        float *du = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(scratch) + 2 * keys);
+        float *du = dpart;
         if (spt == 4)
             hipLaunchKernelGGL((k_propagate_units<4, kTpu>), dim3((uint32_t)grid), dim3(kTmThreads), 0, st,
                                w, g, key_t, du_t, du, s.batch, pitch, s.n_outputs, s.n_detectors, n_chunks,
