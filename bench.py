@@ -977,9 +977,10 @@ def summarize_counters(args):
             # counters of one dispatch may come as several rows (one per agent block): sum them
             per[r["Kernel_Name"]][c][r["Dispatch_Id"]] += v
     cols = counters + (["conflict_frac"] if {"SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE"} <= set(counters) else [])
+    gb = {"FETCH_SIZE", "WRITE_SIZE"}
     out = [f"# timed steps only: {args.steps} steps after {args.warmup} warm-up steps; mean per dispatch; "
-           f"FETCH_SIZE / WRITE_SIZE in bytes (KiB x 1024 x factor {f_fetch:g} / {f_write:g})",
-           f"{'kernel':<30}{'per_step':>9}" + "".join(f"{c[:20]:>22}" for c in cols)]
+           f"FETCH_SIZE / WRITE_SIZE in GB (KiB x 1024 x factor {f_fetch:g} / {f_write:g})",
+           f"{'kernel':<30}{'per_step':>9}" + "".join(f"{(c + '_GB' if c in gb else c)[:21]:>22}" for c in cols)]
     means = {}
     order = sorted(per, key=lambda k: -max((statistics.fmean(d.values()) * len(d)
                                             for c, d in per[k].items() if c in ("FETCH_SIZE", "WRITE_SIZE")),
@@ -989,7 +990,8 @@ def summarize_counters(args):
         n = max(len(d) for d in per[k].values())
         line = f"{k[:29]:<30}{n / args.steps:>9.2f}"
         for c in counters:
-            line += f"{means[k].get(c, float('nan')):>22.6g}"
+            v = means[k].get(c, float("nan"))
+            line += f"{v / 1e9:>22.4f}" if c in gb else f"{v:>22.0f}"
         if "conflict_frac" in cols:
             line += f"{means[k]['SQ_LDS_BANK_CONFLICT'] / max(means[k]['SQ_LDS_IDX_ACTIVE'], 1.0):>22.4f}"
         out.append(line)
