@@ -115,9 +115,17 @@ template <bool TRAIN, int NA>
 __global__ __launch_bounds__(1024) void k_check_detectors_lds(
     const float *__restrict__ x, const int2 *__restrict__ anchors, uint32_t batch,
     uint32_t n_inputs, uint32_t n_detectors, uint32_t n_anchors, uint32_t spb, float cmp_eps,
-    int32_t *__restrict__ idx, float *__restrict__ md, int32_t *__restrict__ mi) {
+    int32_t *__restrict__ idx, float *__restrict__ md, int32_t *__restrict__ mi, uint32_t gx,
+    uint32_t gy) {
     extern __shared__ float xs[];
-    const uint32_t b0 = blockIdx.y * spb;
+    // the gx table blocks of one sample group run on one XCD (workgroup i runs
+    // on XCD i % 8, consecutively there), so the group's x rows are fetched from
+    // HBM once and then served by that XCD's L2
+    const uint32_t wl = blockIdx.x;
+    const uint32_t gyb = (wl % 8u) + 8u * (wl / (8u * gx));
+    const uint32_t gxb = (wl / 8u) % gx;
+    if (gyb >= gy) return;  // uniform over the workgroup
+    const uint32_t b0 = gyb * spb;
     const uint32_t nb = min(spb, batch - b0);
     const uint32_t n_el = nb * n_inputs;
     const float *src = x + (size_t)b0 * n_inputs;
@@ -129,7 +137,7 @@ __global__ __launch_bounds__(1024) void k_check_detectors_lds(
         for (uint32_t i = threadIdx.x; i < n_el; i += blockDim.x) xs[i] = src[i];
     }
     __syncthreads();
-    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t t = gxb * blockDim.x + threadIdx.x;
     if (t >= n_detectors) return;
     // the table's pairs in registers (fully unrolled, compile-time indices);
     // pairs past n_anchors or with an input id outside [0, n_inputs) are
@@ -979,20 +987,21 @@ hipError_t launch_check_detectors(const FcShape &s, const float *x, const int32_
     const int2 *ap = reinterpret_cast<const int2 *>(anchors);
     const uint32_t spb_lds = kCheckLdsBytes / 4 / std::max<uint32_t>(s.n_inputs, 1);
     if (s.n_anchors <= (uint32_t)kCheckMaxAnchors && spb_lds >= 1 &&
-        (s.batch + std::min<uint32_t>(spb_lds, 16) - 1) / std::min<uint32_t>(spb_lds, 16) <= 65535u) {
+        (uint64_t)(s.batch + 7) * ((s.n_detectors + 63) / 64) <= 0x7fffffffull) {
         // one thread per table, x rows of spb samples in LDS; spb is lowered so
         // that the grid still holds ~512 workgroups where the batch allows it
         const uint32_t threads = std::min<uint32_t>(1024, (s.n_detectors + 63) / 64 * 64);
         const uint32_t gx = (s.n_detectors + threads - 1) / threads;
         const uint64_t want = std::max<uint64_t>(1, (uint64_t)s.batch * gx / 512);
-        uint32_t spb = (uint32_t)std::min<uint64_t>({(uint64_t)spb_lds, want, 16});
-        while ((s.batch + spb - 1) / spb > 65535u) spb++;
+        const uint32_t spb = (uint32_t)std::min<uint64_t>({(uint64_t)spb_lds, want, 16});
         const uint32_t gy = (s.batch + spb - 1) / spb;
+        const uint64_t grid = 8ull * gx * ((gy + 7) / 8);
+        if (grid > 0x7fffffffull) return hipErrorInvalidConfiguration;
         const size_t lds = (size_t)spb * s.n_inputs * sizeof(float);
 #define SPIKY_CHK(TR, NA)                                                                       \
-    hipLaunchKernelGGL((k_check_detectors_lds<TR, NA>), dim3(gx, gy), dim3(threads), lds, st, x, ap, \
-                       s.batch, s.n_inputs, s.n_detectors, s.n_anchors, spb, cmp_eps, idx,       \
-                       min_deltas, min_idx)
+    hipLaunchKernelGGL((k_check_detectors_lds<TR, NA>), dim3((uint32_t)grid), dim3(threads), lds, st, x, \
+                       ap, s.batch, s.n_inputs, s.n_detectors, s.n_anchors, spb, cmp_eps, idx,   \
+                       min_deltas, min_idx, gx, gy)
         if (min_deltas) {
             if (s.n_anchors <= 8) SPIKY_CHK(true, 8); else SPIKY_CHK(true, 16);
         } else {

@@ -1028,19 +1028,34 @@ __global__ __launch_bounds__(kScatterThreads) void k_propagate_scatter(
     const uint32_t n_el = nb * n_inputs;
     for (uint32_t i = threadIdx.x; i < n_el; i += kScatterThreads) xg[i] = 0.0;
     __syncthreads();
-    const uint64_t n_pairs = (uint64_t)nb * n_detectors;
+    const uint32_t n_pairs = nb * n_detectors;
     const size_t base = (size_t)b0 * n_detectors;
-    for (uint64_t p = threadIdx.x; p < n_pairs; p += kScatterThreads) {
-        const float du = du_in[base + p];
-        if (du == 0.0f) continue;
-        const int32_t m = mi[base + p];
-        const uint32_t t = (uint32_t)(p % n_detectors);
-        const uint32_t bl = (uint32_t)(p / n_detectors);
-        if (m < 0 || (uint32_t)m >= n_anchors) continue;
-        const int2 a = anchors[(size_t)t * n_anchors + m];
-        if ((uint32_t)a.x >= n_inputs || (uint32_t)a.y >= n_inputs) continue;
-        atomicAdd(&xg[bl * n_inputs + a.x], (double)du);
-        atomicAdd(&xg[bl * n_inputs + a.y], -(double)du);
+    // eight (sample, table) items a thread at a time: their du and margin index
+    // loads, then their anchor loads, each batch in flight together
+    constexpr int kU = 8;
+    for (uint32_t p0 = threadIdx.x; p0 < n_pairs; p0 += kU * kScatterThreads) {
+        float du[kU];
+        int32_t m[kU];
+#pragma unroll
+        for (int u = 0; u < kU; u++) {
+            const uint32_t p = p0 + u * kScatterThreads;
+            du[u] = p < n_pairs ? du_in[base + p] : 0.0f;
+            m[u] = p < n_pairs ? mi[base + p] : -1;
+        }
+        int2 a[kU];
+#pragma unroll
+        for (int u = 0; u < kU; u++) {
+            const uint32_t t = (p0 + u * kScatterThreads) % n_detectors;
+            const bool on = du[u] != 0.0f && m[u] >= 0 && (uint32_t)m[u] < n_anchors;
+            a[u] = on ? anchors[(size_t)t * n_anchors + m[u]] : make_int2(-1, -1);
+        }
+#pragma unroll
+        for (int u = 0; u < kU; u++) {
+            if ((uint32_t)a[u].x >= n_inputs || (uint32_t)a[u].y >= n_inputs) continue;
+            const uint32_t bl = (p0 + u * kScatterThreads) / n_detectors;
+            atomicAdd(&xg[bl * n_inputs + a[u].x], (double)du[u]);
+            atomicAdd(&xg[bl * n_inputs + a[u].y], -(double)du[u]);
+        }
     }
     __syncthreads();
     float *dst = x_grad + (size_t)b0 * n_inputs;

@@ -334,3 +334,40 @@ def test_errors_on_device(cuda_device):
     with pytest.raises(ValueError, match="batch_size == 0"):
         dm.forward_step(W, 0, torch.zeros(8, device=dev), torch.zeros(16, dtype=torch.int32, device=dev),
                         torch.zeros(4, device=dev), torch.zeros(4, dtype=torch.int32, device=dev))
+
+
+def test_forward_batch_dependence(cuda_device):
+    """The fold of the default fp32 forward is chosen from the shape and the
+    batch (enough blocks to leave about 1024 work units), so the same sample's
+    output bits can differ between batch sizes: here 8 blocks a partial at
+    B = 4096 and 2 at B = 1024, and the ordered 32-table commits of the
+    small-batch kernel at B = 200.  Every pair stays within 1e-5 of the row's
+    largest output; with ordered sums the three are bit-identical."""
+    from test_gpu_layers import fold_blocks
+    dev = cuda_device
+    I, T, Nc, O = 128, 8192, 8, 256
+    assert (fold_blocks(4096, T, O), fold_blocks(1024, T, O)) == (8, 2)
+    x, anchors, W, _ = make_inputs(23, 4096, I, T, Nc, O, x_normal=True)
+    Wd, xd, ad = W.to(dev), x.to(dev), anchors.to(dev)
+    outs = {}
+    for ordered in (False, True):
+        dm = make_dm(I, O, T, Nc)
+        dm.set_ordered_sums(ordered)
+        for B in (4096, 1024, 200):
+            print(f"[batch dependence] ordered={ordered} B={B}", flush=True)
+            out = torch.zeros(B * O, device=dev)
+            idx = torch.empty(B * T, dtype=torch.int32, device=dev)
+            dm.forward_step(Wd, B, xd[:B * I], ad, out, idx)
+            torch.cuda.synchronize()
+            outs[ordered, B] = out.view(B, O)[:200].cpu()
+    for ordered in (False, True):
+        a, b, c = (outs[ordered, B] for B in (4096, 1024, 200))
+        if ordered:
+            assert torch.equal(a.view(torch.int32), c.view(torch.int32))
+            assert torch.equal(b.view(torch.int32), c.view(torch.int32))
+        else:
+            scale = c.abs().max(dim=1, keepdim=True).values
+            for got in (a, b):
+                assert torch.all((got - c).abs() <= 1e-5 * scale)
+            assert not torch.equal(a, c), "the folded forward is expected to round differently somewhere"
+    assert torch.equal(outs[True, 200], outs[False, 200])
