@@ -146,6 +146,14 @@ def test_table_major_wide_slices(oracle, cuda_device, B, O):
     run_fc(oracle, B, 300, 40, 8, O, seed=16)
 
 
+@pytest.mark.parametrize("int_rescaler", [None, 0.5])
+def test_table_major_dma_forward_two_chunks(oracle, cuda_device, int_rescaler):
+    # 256-entry tables and more than 1024 samples: the LDS-DMA forward over two
+    # sample chunks (the second of 76 samples) and two units of 32 and 8
+    # tables, fp32 and int32 summation
+    run_fc(oracle, 1100, 300, 40, 8, 128, seed=17, int_rescaler=int_rescaler)
+
+
 def test_many_samples_few_tables(oracle, cuda_device):
     # 4100 samples over 6 tables: the weight gradient's bucket sort runs a
     # workgroup per table, with a ragged last 64-sample group
