@@ -1207,7 +1207,6 @@ __global__ __launch_bounds__(kGrpThreads) void k_propagate_seq_grp(
     const uint32_t p = lane >> 3, s8 = lane & 7;
     const uint32_t podd = p & 1;
     const uint32_t pmask = (1u << pe_dim) - 1, gmask = (1u << gb) - 1;
-    const uint64_t below = (1ull << lane) - 1;
     uint32_t *q = queue[wave];
     for (uint32_t k = lane; k < kGrpQueue; k += kWave) q[k] = 0;  // a slot past n reads a valid row
     // Position-i shares are summed in LDS per candidate lane (cacc) while a turn

@@ -70,7 +70,6 @@ __device__ __forceinline__ double dpp_f64(double v) {
 constexpr int kDppHalfMirror = 0x141;  // lane l of 8 <-> 7 - l
 constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]
-constexpr int kDppRowRor8 = 0x128;     // lane l of 16 <- lane (l + 8) % 16
 
 // One reduce-scatter step over a lane pairing: the pair sums its N items and
 // each lane keeps half of them (the lane with `upper` set keeps the upper
