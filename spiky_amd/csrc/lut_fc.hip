@@ -1123,7 +1123,10 @@ hipError_t launch_wgrad_fc(const FcShape &s, const float *g, const int32_t *idx,
         // 4 columns per lane once that still leaves 4 slices (two XCDs per slice)
         const uint32_t vec = (s.n_outputs % 4 == 0 && s.n_outputs >= 1024) ? 4 : pick_vec(s.n_outputs);
         const uint32_t n_slices = (s.n_outputs + kWave * vec - 1) / (kWave * vec);
-        const uint32_t rpw = std::min<uint32_t>(s.n_entries, 32);
+        // rows a wavefront: 32, or fewer where few tables would leave the grid
+        // short of 16 wavefronts a CU (a feed-forward layer's 16 tables)
+        uint32_t rpw = std::min<uint32_t>(s.n_entries, 32);
+        while (rpw > 4 && (uint64_t)n_slices * s.n_detectors * (s.n_entries / rpw) < 4096) rpw /= 2;
         const uint64_t units = (uint64_t)s.n_detectors * (s.n_entries / rpw);
         const uint64_t grid = (uint64_t)n_slices * ((units + kWPB - 1) / kWPB);
         if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;

@@ -1399,20 +1399,34 @@ hipError_t launch_propagate_tm(const FcShape &s, const float *w, const float *g,
         // keys and du (8 KiB a table, read again for every slice) then
         // overflow an XCD's L2 and the kernel fetches 9.73 instead of 8.80 GB;
         // 12 leaves a partial last round of units (1.75 ms)
-        constexpr uint32_t kTpu = 8;
+        // Few tables over many samples (a transformer's feed-forward layer: 16
+        // tables, 8192 rows) would leave most CUs idle at 8 tables a unit: fewer
+        // tables a unit then, down to one, until the grid covers the 256 CUs.
         const uint32_t spt = tm_units_spt(s.batch);
         const uint32_t n_chunks = (s.batch + kUnitPass * spt - 1) / (kUnitPass * spt);
-        const uint64_t grid = (uint64_t)((s.n_detectors + kTpu - 1) / kTpu) * n_chunks;
+        uint32_t tpu = 8;
+        while (tpu > 1 && (uint64_t)((s.n_detectors + tpu - 1) / tpu) * n_chunks < 256) tpu /= 2;
+        const uint64_t grid = (uint64_t)((s.n_detectors + tpu - 1) / tpu) * n_chunks;
         if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
         float *du = dpart;
-        if (spt == 4)
-            hipLaunchKernelGGL((k_propagate_units<4, kTpu>), dim3((uint32_t)grid), dim3(kTmThreads), 0, st,
-                               w, g, key_t, du_t, du, s.batch, pitch, s.n_outputs, s.n_detectors, n_chunks,
-                               s.ogs == (uint32_t)kTmCols);
-        else
-            hipLaunchKernelGGL((k_propagate_units<8, kTpu>), dim3((uint32_t)grid), dim3(kTmThreads), 0, st,
-                               w, g, key_t, du_t, du, s.batch, pitch, s.n_outputs, s.n_detectors, n_chunks,
-                               s.ogs == (uint32_t)kTmCols);
+#define SPIKY_PU(SPT, TPU)                                                                          \
+    hipLaunchKernelGGL((k_propagate_units<SPT, TPU>), dim3((uint32_t)grid), dim3(kTmThreads), 0, st, w, g, \
+                       key_t, du_t, du, s.batch, pitch, s.n_outputs, s.n_detectors, n_chunks,            \
+                       s.ogs == (uint32_t)kTmCols)
+#define SPIKY_PU_T(SPT)                    \
+    switch (tpu) {                         \
+        case 1: SPIKY_PU(SPT, 1); break;   \
+        case 2: SPIKY_PU(SPT, 2); break;   \
+        case 4: SPIKY_PU(SPT, 4); break;   \
+        default: SPIKY_PU(SPT, 8); break;  \
+    }
+        if (spt == 4) {
+            SPIKY_PU_T(4)
+        } else {
+            SPIKY_PU_T(8)
+        }
+#undef SPIKY_PU_T
+#undef SPIKY_PU
         e = hipGetLastError();
         if (e != hipSuccess) return e;
         return launch_propagate_scatter(s, du, min_idx, anchors, x_grad, st);
