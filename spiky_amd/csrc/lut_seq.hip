@@ -1677,9 +1677,9 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
     const uint2 *__restrict__ ppack, float *__restrict__ target, uint32_t batch, uint32_t seq,
     uint32_t n_outputs, uint32_t n_detectors, uint32_t n_anchors, uint32_t pe_dim,
     uint32_t cols, uint32_t n_slices, uint32_t items_per_batch, double int_rescaler, bool quad) {
-    __shared__ uint32_t cnt[kSeqWgRowsMax];
+    __shared__ uint32_t cnt[kSeqWgRowsMax + 1];  // counts, then (quad path) the walk's words and its end
     __shared__ uint32_t cur[kSeqWgRowsMax];
-    __shared__ __attribute__((aligned(4))) uint8_t ent[kSeqWgEntries + kQuadStep];  // + the walk's read-ahead
+    __shared__ __attribute__((aligned(4))) uint8_t ent[kSeqWgEntries + 2 * kQuadStep];  // + the walk's read-ahead
     __shared__ uint32_t gv[kSeqWgGvWords];
     __shared__ uint16_t ktab[kSeqWgKeys];
     __shared__ uint16_t ptab[kSeqWgPe];
@@ -1749,11 +1749,54 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
                     atomicAdd(&cnt[(((uint32_t)kt[i] << pe_dim) | ptab[j - i - 1]) & (sub_rows - 1)], 1u);
             }
             __syncthreads();
-            // exclusive scan of the counts into cur (one pass per 1024 rows)
+            // Bucket starts, padded to whole turns of kQuadStep entries.  The quad
+            // path lays the buckets out in its walk order (rows by length class,
+            // longest first, so the four 16-lane groups of a wavefront reach
+            // their rows' ends on the same turn): a walk position's bucket then
+            // runs from its start to the next position's, and the walk reads one
+            // packed word a position, cnt[pos] = row | start / 4 << 12 (written
+            // over the counts once they are read; cnt[sub_rows] = the end).  The
+            // other path keeps row order.  cur[row] = the row's start, the
+            // scatter's cursor.
+            constexpr int kRowPasses = kSeqWgRowsMax / kSeqWgThreads;
+            auto row_class = [&](uint32_t r) -> uint32_t {
+                const uint32_t turns = (cnt[r] + kQuadStep - 1) / kQuadStep;
+                return (uint32_t)kSeqWgClasses - 1u - min(turns, (uint32_t)kSeqWgClasses - 1u);
+            };
+            if (quad) {
+                for (uint32_t c = tid; c < (uint32_t)kSeqWgClasses; c += kSeqWgThreads) lhist[c] = 0u;
+                __syncthreads();
+                for (uint32_t r = tid; r < sub_rows; r += kSeqWgThreads) atomicAdd(&lhist[row_class(r)], 1u);
+                __syncthreads();
+                if (wave == 0) {
+                    const uint32_t v = lane < (uint32_t)kSeqWgClasses ? lhist[lane] : 0u;
+                    uint32_t incl = v;
+#pragma unroll
+                    for (int o = 1; o < kWave; o <<= 1) {
+                        const uint32_t y = __shfl_up(incl, o, kWave);
+                        if ((int)lane >= o) incl += y;
+                    }
+                    if (lane < (uint32_t)kSeqWgClasses) lhist[lane] = incl - v;
+                }
+                __syncthreads();
+                // cur[pos] = the row at walk position pos (until the starts replace it)
+                for (uint32_t r = tid; r < sub_rows; r += kSeqWgThreads) cur[atomicAdd(&lhist[row_class(r)], 1u)] = r;
+                __syncthreads();
+            }
+            uint32_t prow[kRowPasses], pv[kRowPasses];
+#pragma unroll
+            for (int u = 0; u < kRowPasses; u++) {
+                const uint32_t pos = u * kSeqWgThreads + tid;
+                prow[u] = pos < sub_rows ? (quad ? cur[pos] : pos) : 0u;
+                pv[u] = pos < sub_rows ? (cnt[prow[u]] + kQuadStep - 1u) & ~(kQuadStep - 1u) : 0u;  // whole turns
+            }
+            __syncthreads();  // every row and count read before cur and cnt are rewritten
             uint32_t carry = 0;
-            for (uint32_t base = 0; base < sub_rows; base += kSeqWgThreads) {
-                const uint32_t r = base + tid;
-                const uint32_t v = r < sub_rows ? (cnt[r] + kQuadStep - 1u) & ~(kQuadStep - 1u) : 0u;  // whole turns
+#pragma unroll
+            for (int u = 0; u < kRowPasses; u++) {
+                if ((uint32_t)u * kSeqWgThreads >= sub_rows) break;  // uniform
+                const uint32_t pos = u * kSeqWgThreads + tid;
+                const uint32_t v = pv[u];
                 uint32_t incl = v;
 #pragma unroll
                 for (int o = 1; o < kWave; o <<= 1) {
@@ -1766,10 +1809,15 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
                 for (uint32_t w = 0; w < wave; w++) wprefix += wsum[w];
                 uint32_t total = 0;
                 for (uint32_t w = 0; w < kSeqWgThreads / kWave; w++) total += wsum[w];
-                if (r < sub_rows) cur[r] = carry + wprefix + incl - v;
+                const uint32_t start = carry + wprefix + incl - v;
+                if (pos < sub_rows) {
+                    cur[prow[u]] = start;
+                    if (quad) cnt[pos] = prow[u] | (start / kQuadStep) << 12;
+                }
                 carry += total;
                 __syncthreads();
             }
+            if (quad && tid == 0) cnt[sub_rows] = (carry / kQuadStep) << 12;
             // scatter the entries' item numbers into their rows' buckets
             for (uint32_t it = wave; it < nb; it += kSeqWgThreads / kWave) {
                 const uint32_t r = bitems[it];
@@ -1804,47 +1852,14 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
                 }
             };
             if (quad) gv_load(0);
-            // cur[row] is now the end of the row's bucket, cur - cnt its start.
-            // The quad path walks rows four to a wavefront, one to each 16-lane
-            // group; rows of equal length (in turns) go together, so the groups
-            // of a wavefront reach their rows' ends on the same turn.  The order
-            // (longest class first) goes into the high half of cnt: cnt[k] >> 16
-            // is the k-th row of the walk, cnt[k] & 0xFFFF row k's count.
+            // cur[row] is now the end of the row's entries.  The quad path pads
+            // each bucket to whole turns with the zero row (item nb), and the two
+            // words past the last turn too (the walk's read-ahead)
             if (quad) {
                 __syncthreads();
-                for (uint32_t r = tid; r < sub_rows; r += kSeqWgThreads)  // pads: the zero row
+                for (uint32_t r = tid; r < sub_rows; r += kSeqWgThreads)
                     for (uint32_t k = cur[r]; k & (kQuadStep - 1u); k++) ent[k] = (uint8_t)nb;
-                for (uint32_t c = tid; c < (uint32_t)kSeqWgClasses; c += kSeqWgThreads) lhist[c] = 0u;
-                __syncthreads();
-                auto row_class = [&](uint32_t r) -> uint32_t {
-                    const uint32_t turns = (cnt[r] + kQuadStep - 1) / kQuadStep;
-                    return (uint32_t)kSeqWgClasses - 1u - min(turns, (uint32_t)kSeqWgClasses - 1u);
-                };
-                for (uint32_t r = tid; r < sub_rows; r += kSeqWgThreads) atomicAdd(&lhist[row_class(r)], 1u);
-                __syncthreads();
-                if (wave == 0) {
-                    const uint32_t v = lane < (uint32_t)kSeqWgClasses ? lhist[lane] : 0u;
-                    uint32_t incl = v;
-#pragma unroll
-                    for (int o = 1; o < kWave; o <<= 1) {
-                        const uint32_t y = __shfl_up(incl, o, kWave);
-                        if ((int)lane >= o) incl += y;
-                    }
-                    if (lane < (uint32_t)kSeqWgClasses) lhist[lane] = incl - v;
-                }
-                __syncthreads();
-                uint32_t rowc[kSeqWgRowsMax / kSeqWgThreads];
-#pragma unroll
-                for (int u = 0; u < kSeqWgRowsMax / kSeqWgThreads; u++) {
-                    const uint32_t r = u * kSeqWgThreads + tid;
-                    rowc[u] = r < sub_rows ? atomicAdd(&lhist[row_class(r)], 1u) : 0u;
-                }
-                __syncthreads();  // every class read before the high halves are written
-#pragma unroll
-                for (int u = 0; u < kSeqWgRowsMax / kSeqWgThreads; u++) {
-                    const uint32_t r = u * kSeqWgThreads + tid;
-                    if (r < sub_rows) atomicOr(&cnt[rowc[u]], r << 16);
-                }
+                if (tid < 2u * kQuadStep) ent[carry + tid] = (uint8_t)nb;
             }
             for (uint32_t sl = 0; sl < n_slices; sl++) {
                 const uint32_t col0 = sl * cols;
@@ -1861,62 +1876,62 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
                 }
                 __syncthreads();
                 if (quad && sl + 1 < n_slices) gv_load(col0 + cols);
-                // lane group g (cols lanes, or 16 lanes of 4 columns on the quad
-                // path) takes the rows whose entries start in [g E / G, (g + 1) E / G):
-                // about equal work whatever the row sizes
-                const uint32_t lanes = quad ? 16u : cols;
-                const uint32_t n_groups = kSeqWgThreads / lanes, grp = tid / lanes;
-                const uint32_t total = cur[sub_rows - 1];  // entries of the batch
-                auto first_row = [&](uint32_t gi) -> uint32_t {
-                    if (gi >= n_groups) return sub_rows;
-                    const uint32_t tgt = (uint32_t)(((uint64_t)total * gi + n_groups - 1) / n_groups);
-                    uint32_t lo = 0, hi = sub_rows;  // first row r with start(r) >= tgt
-                    while (lo < hi) {
-                        const uint32_t mid = (lo + hi) / 2;
-                        if (cur[mid] - (cnt[mid] & 0xFFFFu) < tgt) lo = mid + 1; else hi = mid;
-                    }
-                    return gi == 0 ? 0u : lo;
-                };
-                const uint32_t rs = first_row(grp), re = first_row(grp + 1);
                 const bool store = first && OVERWRITE;
                 if (quad) {
                     // 64-column slices, lane k of a group holding columns 4k .. 4k+3:
-                    // one 16-byte LDS read per entry.  Wavefront w takes the rows at
-                    // walk positions 4 (w + 16 m) .. + 3, one per group, and adds four
-                    // entries (one u32 read, the next four's read in flight) a turn
-                    // (pads read the zero row, adding +0, which leaves a sum that
-                    // starts at +0 unchanged); the group then writes its row.
+                    // one 16-byte LDS read per entry.  Wavefront w takes walk
+                    // positions 4 (w + 16 m) .. + 3, one per group, and adds four
+                    // entries (one u32 of item numbers) a turn, the next turn's
+                    // rows loading while this turn's are added (pads read the zero
+                    // row, adding +0, which leaves a sum that starts at +0
+                    // unchanged); the group then writes its row.  An entry's LDS
+                    // address is item * 256 + the lane's byte offset (< 256): one
+                    // byte permute builds it.
                     static_assert(kQuadStep == 4, "the walk reads entry quads");
                     const uint32_t c4 = (tid & 15u) * 4u;
                     const uint32_t cq = col0 + c4;
                     const uint32_t gw = (tid >> 4) & 3u;
+                    const uint32_t lane_b = c4 * 4u;
                     const uint32_t *ent4 = reinterpret_cast<const uint32_t *>(ent);
+                    const uint8_t *gvb = reinterpret_cast<const uint8_t *>(gv);
                     for (uint32_t k4 = wave * 4u; k4 < sub_rows; k4 += kSeqWgThreads / 16u) {
                         const uint32_t pos = k4 + gw;
                         const bool have = pos < sub_rows;
-                        const uint32_t row = have ? cnt[pos] >> 16 : 0u;
-                        const uint32_t n = have ? cnt[row] & 0xFFFFu : 0u;
-                        const uint32_t e0 = have ? cur[row] - n : 0u;  // a multiple of 4
-                        const uint32_t np = (n + 3u) / 4u;              // entry quads
+                        const uint32_t ps = min(pos, sub_rows - 1u);
+                        const uint32_t w0 = cnt[ps], w1 = cnt[ps + 1u];
+                        const uint32_t row = w0 & 0xFFFu;
+                        const uint32_t e0q = w0 >> 12;
+                        const uint32_t np = have ? (w1 >> 12) - e0q : 0u;  // turns
                         float af[4] = {0.f, 0.f, 0.f, 0.f};
                         uint32_t ai[4] = {0u, 0u, 0u, 0u};
-                        uint32_t pr = ent4[e0 / 4u];
-                        for (uint32_t k = 0; k < np; k++) {
-                            const uint32_t npr = ent4[e0 / 4u + k + 1u];  // next quad (read-ahead)
-                            u32x4 g[4];
+                        u32x4 ga[4], gb[4];
+                        auto rows = [&](u32x4 (&gg)[4], uint32_t pr) {
 #pragma unroll
                             for (int u = 0; u < 4; u++)
-                                g[u] = *reinterpret_cast<const u32x4 *>(gv + ((pr >> (8 * u)) & 0xFFu) * 64u + c4);
+                                gg[u] = *reinterpret_cast<const u32x4 *>(
+                                    gvb + __builtin_amdgcn_perm(pr, lane_b, 0x0C0C0000u | ((4u + u) << 8)));
+                        };
+                        auto add = [&](const u32x4 (&gg)[4]) {
 #pragma unroll
                             for (int u = 0; u < 4; u++)
 #pragma unroll
                                 for (int c = 0; c < 4; c++) {
-                                    if (INT_MODE) ai[c] += g[u][c];
-                                    else af[c] += __uint_as_float(g[u][c]);
+                                    if (INT_MODE) ai[c] += gg[u][c];
+                                    else af[c] += __uint_as_float(gg[u][c]);
                                 }
-                            pr = npr;
+                        };
+                        uint32_t pn = ent4[e0q + 1u];
+                        rows(ga, ent4[e0q]);
+                        for (uint32_t k = 0; k < np; k += 2) {
+                            const uint32_t p2 = ent4[e0q + k + 2u];
+                            rows(gb, pn);
+                            add(ga);
+                            if (k + 1u >= np) break;
+                            pn = ent4[e0q + k + 3u];
+                            rows(ga, p2);
+                            add(gb);
                         }
-                        if (have && (store || n > 0) && cq < n_outputs) {
+                        if (have && (store || np > 0) && cq < n_outputs) {
                             u32x4 *p = reinterpret_cast<u32x4 *>(dst + (size_t)row * n_outputs + cq);
                             u32x4 o;
                             if (store) {
@@ -1934,6 +1949,22 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
                     }
                     continue;
                 }
+                // lane group g (cols lanes) takes the rows whose entries start in
+                // [g E / G, (g + 1) E / G): about equal work whatever the row sizes
+                const uint32_t lanes = cols;
+                const uint32_t n_groups = kSeqWgThreads / lanes, grp = tid / lanes;
+                const uint32_t total = cur[sub_rows - 1];  // entries of the batch
+                auto first_row = [&](uint32_t gi) -> uint32_t {
+                    if (gi >= n_groups) return sub_rows;
+                    const uint32_t tgt = (uint32_t)(((uint64_t)total * gi + n_groups - 1) / n_groups);
+                    uint32_t lo = 0, hi = sub_rows;  // first row r with start(r) >= tgt
+                    while (lo < hi) {
+                        const uint32_t mid = (lo + hi) / 2;
+                        if (cur[mid] - cnt[mid] < tgt) lo = mid + 1; else hi = mid;
+                    }
+                    return gi == 0 ? 0u : lo;
+                };
+                const uint32_t rs = first_row(grp), re = first_row(grp + 1);
                 const uint32_t cc = col0 + my_col;
                 for (uint32_t row = rs; row < re; row++) {
                     const uint32_t e1 = cur[row];
