@@ -36,6 +36,7 @@
 
 #include <algorithm>
 #include <type_traits>
+#include <utility>
 
 namespace spiky {
 namespace {
@@ -330,6 +331,47 @@ __device__ __forceinline__ void lds_cols(const uint8_t *p, float (&v)[VW]) {
     }
 }
 
+// v from lane M of this lane's 16-lane row (DPP row_newbcast); folded into the
+// add that uses it
+template <int M>
+__device__ __forceinline__ uint32_t row_bcast(uint32_t v) {
+    return __builtin_amdgcn_update_dpp(0u, v, 0x150 + M, 0xF, 0xF, false);
+}
+
+// Pairs of a chunk of 16 n pairs whose LDS row offsets lie one per lane of the
+// item's 16-lane row (pair M in lane M % 16, register M / 16): sixteen pairs'
+// VW columns read (all in flight), then added to the fp64 sums in ascending M.
+template <int M>
+struct SeqPairs16 {
+    template <int VW, int KP>
+    __device__ __forceinline__ static void read(const uint8_t *tb, const uint32_t (&off)[KP], float (&v)[16][VW]) {
+        SeqPairs16<M - 1>::template read<VW, KP>(tb, off, v);
+        lds_cols<VW>(tb + row_bcast<(M - 1) % 16>(off[(M - 1) / 16]), v[(M - 1) % 16]);
+    }
+};
+template <>
+struct SeqPairs16<0> {
+    template <int VW, int KP>
+    __device__ __forceinline__ static void read(const uint8_t *, const uint32_t (&)[KP], float (&)[16][VW]) {}
+};
+template <int VW, int KP, int M0>
+__device__ __forceinline__ void seq_group_add(const uint8_t *tb, const uint32_t (&off)[KP], double (&acc)[VW]) {
+    float v[16][VW];
+    // offsets of pairs M0 .. M0 + 15: register M0 / 16, lanes 0 .. 15
+    const uint32_t (&o)[KP] = off;
+    uint32_t one[1] = {o[M0 / 16]};
+    SeqPairs16<16>::template read<VW, 1>(tb, one, v);
+#pragma unroll
+    for (int m = 0; m < 16; m++)
+#pragma unroll
+        for (int c = 0; c < VW; c++) acc[c] += (double)v[m][c];  // ascending pairs: ascending i
+}
+template <int VW, int KP, int... Gs>
+__device__ __forceinline__ void seq_chunk_add(const uint8_t *tb, const uint32_t (&off)[KP], double (&acc)[VW],
+                                              std::integer_sequence<int, Gs...>) {
+    (seq_group_add<VW, KP, 16 * Gs>(tb, off, acc), ...);
+}
+
 // C / VW lanes own an item, lane l of it holding columns VW l .. VW l + VW-1 of
 // the slice (VW = 4 at 64-column slices, 2 at 32, 1 below): 16 lanes an item,
 // so a bucket of ~128 items makes ~32 item groups for the 16 wavefronts and
@@ -525,6 +567,24 @@ __global__ __launch_bounds__(kSfThreads) void k_fill_seq_lds(
             double acc[VW];
 #pragma unroll
             for (int c = 0; c < VW; c++) acc[c] = 0.0;
+            if constexpr (L == 16) {
+                // 16 lanes an item, one DPP row: each lane forms kPer of the chunk's
+                // row offsets, and every pair's address add takes its offset from
+                // the lane that formed it
+                for (uint32_t i0 = 0; i0 < jw; i0 += C) {
+                    uint32_t off[kPer];
+#pragma unroll
+                    for (int k = 0; k < kPer; k++) {
+                        const uint32_t i = i0 + cl + L * k;
+                        asm volatile("" : "+v"(rec[k]));
+                        const uint32_t d = i < j ? j - i - 1 : 0u;
+                        off[k] = i < j ? (((((rec[k] & 0xFFFFu) << pe_dim) | ptab[d]) & (sub_rows - 1)) * C) * 4u
+                                       : zero_off;
+                        rec[k] = kw[2 * (brow + min(i + C, j > 0 ? j - 1 : 0u))];  // next chunk, in flight meanwhile
+                    }
+                    seq_chunk_add<VW>(tab_b, off, acc, std::make_integer_sequence<int, C / 16>());
+                }
+            } else
             for (uint32_t i0 = 0; i0 < jw; i0 += C) {
                 // this chunk's C row offsets (bytes), kPer per lane
 #pragma unroll
