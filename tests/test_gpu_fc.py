@@ -160,6 +160,16 @@ def test_many_samples_few_tables(oracle, cuda_device):
     run_fc(oracle, 4100, 64, 6, 4, 64, seed=19)
 
 
+@pytest.mark.parametrize("T,B,O", [(192, 8192, 64), (64, 8192, 128)])
+def test_few_tables_many_samples_unit_sizes(oracle, cuda_device, T, B, O):
+    # few 256-entry tables over many samples, a transformer feed-forward layer's
+    # shape: so that the grid still covers the CUs, the whole-table propagate
+    # takes 4 (T 192) or 2 (T 64) tables a unit over 8 sample chunks, and the
+    # weight gradient 8 or 4 rows a wavefront.  Every sum and its order are
+    # unchanged, so the usual bars hold (1 table a unit is the config-5 test's)
+    run_fc(oracle, B, 256, T, 8, O, seed=21)
+
+
 def test_large_batch_int32_summation(oracle, cuda_device):
     run_fc(oracle, 530, 64, 20, 4, 512, seed=14, int_rescaler=0.5)
 
