@@ -1729,20 +1729,31 @@ constexpr int kSeqWgPe = 1024;
 constexpr int kSeqWgItems = 256;         // u8 entries: at most 256 items a batch
 constexpr int kQuadStep = 4;             // entries a turn of the 16-byte row loop (one u32 read)
 constexpr int kSeqWgClasses = 64;        // row length classes (turns of kQuadStep entries, the last open)
+// The wide walk (128 columns a pass, two 64-column planes of gradient rows) fits
+// LDS for sub-tables of up to 1024 rows: its second plane shares its array with
+// the K and positional index tables, which a batch's walk does not read.
+constexpr int kSeqWgWideRows = 1024;
+static_assert(kSeqWgGvWords * 4 >= (kSeqWgKeys + kSeqWgPe) * 2, "the index tables fit the second plane");
 
-template <bool INT_MODE, bool OVERWRITE>
+template <bool INT_MODE, bool OVERWRITE, bool WIDE>
 __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
     const uint32_t *__restrict__ cv, const int32_t *__restrict__ offsets,
     const int32_t *__restrict__ samples, const uint2 *__restrict__ pack,
     const uint2 *__restrict__ ppack, float *__restrict__ target, uint32_t batch, uint32_t seq,
     uint32_t n_outputs, uint32_t n_detectors, uint32_t n_anchors, uint32_t pe_dim,
     uint32_t cols, uint32_t n_slices, uint32_t items_per_batch, double int_rescaler, bool quad) {
-    __shared__ uint32_t cnt[kSeqWgRowsMax + 1];  // counts, then (quad path) the walk's words and its end
-    __shared__ uint32_t cur[kSeqWgRowsMax];
+    constexpr int kRowsCap = WIDE ? kSeqWgWideRows : kSeqWgRowsMax;
+    __shared__ uint32_t cnt[kRowsCap + 1];  // counts, then (quad path) the walk's words and its end
+    __shared__ uint32_t cur[kRowsCap];
     __shared__ __attribute__((aligned(4))) uint8_t ent[kSeqWgEntries + 2 * kQuadStep];  // + the walk's read-ahead
-    __shared__ uint32_t gv[kSeqWgGvWords];
-    __shared__ uint16_t ktab[kSeqWgKeys];
-    __shared__ uint16_t ptab[kSeqWgPe];
+    __shared__ __attribute__((aligned(16))) uint32_t gv[kSeqWgGvWords];
+    // the wide walk's second column plane, which also holds the index tables
+    // while a batch is sorted
+    __shared__ __attribute__((aligned(16))) uint32_t gv_hi[WIDE ? kSeqWgGvWords : 1];
+    __shared__ uint16_t ktab_own[WIDE ? 1 : kSeqWgKeys];
+    __shared__ uint16_t ptab_own[WIDE ? 1 : kSeqWgPe];
+    uint16_t *const ktab = WIDE ? reinterpret_cast<uint16_t *>(gv_hi) : ktab_own;
+    uint16_t *const ptab = WIDE ? reinterpret_cast<uint16_t *>(gv_hi) + kSeqWgKeys : ptab_own;
     __shared__ uint32_t bitems[kSeqWgItems];  // row ids of the batch's items
     __shared__ uint32_t wsum[kSeqWgThreads / kWave];
     __shared__ uint32_t lhist[kSeqWgClasses];  // rows per length class (quad path)
@@ -1756,8 +1767,11 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
     const uint32_t n_rows = batch * seq;
     const uint32_t my_col = tid % cols;  // cols divides the 1024 threads
 
-    for (uint32_t d = tid; d + 1 < seq; d += kSeqWgThreads)
-        ptab[d] = (uint16_t)(rec_idx(ppack[(size_t)t * (seq - 1) + d]) & pmask);
+    auto load_ptab = [&]() {
+        for (uint32_t d = tid; d + 1 < seq; d += kSeqWgThreads)
+            ptab[d] = (uint16_t)(rec_idx(ppack[(size_t)t * (seq - 1) + d]) & pmask);
+    };
+    if (!WIDE) load_ptab();
     const int32_t *off_t = offsets + (size_t)t * (n_q + 1);
     const int32_t beg = off_t[q], end = off_t[q + 1];
     const int32_t *smp = samples + (size_t)t * n_rows;
@@ -1771,19 +1785,22 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
         const uint32_t r1 = min(r0 + rows_per_chunk, n_rows);
         __syncthreads();
         // the chunk's K indices, eight loads in flight a thread
-        for (uint32_t r = r0 + tid; r < r1; r += 8 * kSeqWgThreads) {
-            uint32_t kv[8];
+        auto load_ktab = [&]() {
+            for (uint32_t r = r0 + tid; r < r1; r += 8 * kSeqWgThreads) {
+                uint32_t kv[8];
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const uint32_t rr = r + u * kSeqWgThreads;
-                kv[u] = rr < r1 ? kp[rr].y : 0u;
-            }
+                for (int u = 0; u < 8; u++) {
+                    const uint32_t rr = r + u * kSeqWgThreads;
+                    kv[u] = rr < r1 ? kp[rr].y : 0u;
+                }
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const uint32_t rr = r + u * kSeqWgThreads;
-                if (rr < r1) ktab[rr - r0] = (uint16_t)rec_idx(make_uint2(0u, kv[u]));
+                for (int u = 0; u < 8; u++) {
+                    const uint32_t rr = r + u * kSeqWgThreads;
+                    if (rr < r1) ktab[rr - r0] = (uint16_t)rec_idx(make_uint2(0u, kv[u]));
+                }
             }
-        }
+        };
+        if (!WIDE) load_ktab();
         // first bucket position at or past row r1 (uniform binary search; the
         // bucket's end when the chunk reaches the last row)
         int32_t lo = k0, hi = end;
@@ -1796,7 +1813,12 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
         for (int32_t kb = k0; kb < k1; kb += (int32_t)items_per_batch) {
             const uint32_t nb = (uint32_t)min((int32_t)items_per_batch, k1 - kb);
             __syncthreads();
-            // the batch's items; zero counts
+            // the batch's items; zero counts; (wide walk) the index tables, which
+            // the previous batch's walk overwrote
+            if (WIDE) {
+                load_ptab();
+                load_ktab();
+            }
             for (uint32_t it = tid; it < nb; it += kSeqWgThreads) bitems[it] = (uint32_t)smp[kb + it];
             for (uint32_t r = tid; r < sub_rows; r += kSeqWgThreads) cnt[r] = 0u;
             __syncthreads();
@@ -1911,7 +1933,26 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
                     if (it <= nb) *reinterpret_cast<u32x4 *>(gv + it * 64u + (tid & 15u) * 4u) = pre[u];
                 }
             };
-            if (quad) gv_load(0);
+            if (quad && !WIDE) gv_load(0);
+            // The wide walk's pass of 128 columns: both planes' loads in flight
+            // before their stores; the first pass's loads are issued here, to
+            // land while the buckets are padded
+            u32x4 wlo[kGvPasses], whi[kGvPasses];
+            auto wide_load = [&](uint32_t col0) {
+                const uint32_t cq = col0 + (tid & 15u) * 4u;
+#pragma unroll
+                for (int u = 0; u < kGvPasses; u++) {
+                    const uint32_t it = (tid >> 4) + 64u * u;
+                    wlo[u] = u32x4{0u, 0u, 0u, 0u};
+                    whi[u] = u32x4{0u, 0u, 0u, 0u};
+                    if (it < nb) {
+                        const uint32_t *src = cv + (size_t)bitems[it] * n_outputs + cq;
+                        if (cq < n_outputs) wlo[u] = *reinterpret_cast<const u32x4 *>(src);
+                        if (cq + 64u < n_outputs) whi[u] = *reinterpret_cast<const u32x4 *>(src + 64);
+                    }
+                }
+            };
+            if (WIDE) wide_load(0);
             // cur[row] is now the end of the row's entries.  The quad path pads
             // each bucket to whole turns with the zero row (item nb), and the two
             // words past the last turn too (the walk's read-ahead)
@@ -1921,12 +1962,28 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
                     for (uint32_t k = cur[r]; k & (kQuadStep - 1u); k++) ent[k] = (uint8_t)nb;
                 if (tid < 2u * kQuadStep) ent[carry + tid] = (uint8_t)nb;
             }
-            for (uint32_t sl = 0; sl < n_slices; sl++) {
-                const uint32_t col0 = sl * cols;
+            // the wide walk takes two 64-column slices a pass
+            const uint32_t n_pass = WIDE ? (n_slices + 1) / 2 : n_slices;
+            for (uint32_t sl = 0; sl < n_pass; sl++) {
+                const uint32_t col0 = sl * cols * (WIDE ? 2u : 1u);
                 __syncthreads();  // scatter done / the previous slice is done with gv
                 // the batch's gradient rows, then a zero row (item nb) that the
                 // quad path reads for pads
-                if (quad) {
+                if (WIDE) {
+                    if (sl > 0) wide_load(col0);
+#pragma unroll
+                    for (int u = 0; u < kGvPasses; u++) {
+                        const uint32_t it = (tid >> 4) + 64u * u;
+                        if (it <= nb) {
+                            *reinterpret_cast<u32x4 *>(gv + it * 64u + (tid & 15u) * 4u) = wlo[u];
+                            *reinterpret_cast<u32x4 *>(gv_hi + it * 64u + (tid & 15u) * 4u) = whi[u];
+                        }
+                        // dead until the next pass loads them: constants, so the
+                        // walk holds no registers for them
+                        wlo[u] = u32x4{0u, 0u, 0u, 0u};
+                        whi[u] = u32x4{0u, 0u, 0u, 0u};
+                    }
+                } else if (quad) {
                     gv_store();
                 } else {
                     for (uint32_t e = tid; e < (nb + 1) * cols; e += kSeqWgThreads) {
@@ -1935,7 +1992,7 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
                     }
                 }
                 __syncthreads();
-                if (quad && sl + 1 < n_slices) gv_load(col0 + cols);
+                if (quad && !WIDE && sl + 1 < n_slices) gv_load(col0 + cols);
                 const bool store = first && OVERWRITE;
                 if (quad) {
                     // 64-column slices, lane k of a group holding columns 4k .. 4k+3:
@@ -1962,6 +2019,58 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
                         const uint32_t row = w0 & 0xFFFu;
                         const uint32_t e0q = w0 >> 12;
                         const uint32_t np = have ? (w1 >> 12) - e0q : 0u;  // turns
+                        if constexpr (WIDE) {
+                            // a pass of 128 columns: the same LDS offset in both
+                            // 64-column planes, so one permute serves two reads
+                            const uint8_t *gvh = reinterpret_cast<const uint8_t *>(gv_hi);
+                            float af[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+                            uint32_t ai[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+                            uint32_t pn = ent4[e0q];
+                            for (uint32_t k = 0; k < np; k++) {
+                                const uint32_t p2 = ent4[e0q + k + 1u];  // the next turn's entries
+                                u32x4 gg[8];
+#pragma unroll
+                                for (int u = 0; u < 4; u++) {
+                                    const uint32_t a = __builtin_amdgcn_perm(pn, lane_b, 0x0C0C0000u | ((4u + u) << 8));
+                                    gg[u] = *reinterpret_cast<const u32x4 *>(gvb + a);
+                                    gg[u + 4] = *reinterpret_cast<const u32x4 *>(gvh + a);
+                                }
+#pragma unroll
+                                for (int u = 0; u < 4; u++)
+#pragma unroll
+                                    for (int c = 0; c < 4; c++) {
+                                        if (INT_MODE) {
+                                            ai[c] += gg[u][c];
+                                            ai[c + 4] += gg[u + 4][c];
+                                        } else {
+                                            af[c] += __uint_as_float(gg[u][c]);
+                                            af[c + 4] += __uint_as_float(gg[u + 4][c]);
+                                        }
+                                    }
+                                pn = p2;
+                            }
+                            if (have && (store || np > 0)) {
+#pragma unroll
+                                for (int h = 0; h < 2; h++) {
+                                    if (cq + 64u * h >= n_outputs) continue;
+                                    u32x4 *p = reinterpret_cast<u32x4 *>(dst + (size_t)row * n_outputs + cq + 64u * h);
+                                    u32x4 o;
+                                    if (store) {
+#pragma unroll
+                                        for (int c = 0; c < 4; c++)
+                                            o[c] = INT_MODE ? ai[4 * h + c] : __float_as_uint(af[4 * h + c]);
+                                    } else {
+                                        const u32x4 old = *p;
+#pragma unroll
+                                        for (int c = 0; c < 4; c++)
+                                            o[c] = INT_MODE ? (uint32_t)wrap_add((int32_t)ai[4 * h + c], (int32_t)old[c])
+                                                            : __float_as_uint(__uint_as_float(old[c]) + af[4 * h + c]);
+                                    }
+                                    *p = o;
+                                }
+                            }
+                            continue;
+                        }
                         float af[4] = {0.f, 0.f, 0.f, 0.f};
                         uint32_t ai[4] = {0u, 0u, 0u, 0u};
                         u32x4 ga[4], gb[4];
@@ -2493,15 +2602,23 @@ hipError_t launch_backward_seq(const SeqShape &s, float *w, const float *g, cons
         const uint32_t ipb = seq_wg_items(s, cols);
         // 16-byte row pieces: 64-column slices of whole quads, 16-byte aligned rows
         const bool quad = cols == 64 && s.n_outputs % 4 == 0 && ((uintptr_t)target & 15) == 0;
-#define SPIKY_WSEQ(IM, OW)                                                                             \
-    hipLaunchKernelGGL((k_wgrad_seq_sort<IM, OW>), dim3((uint32_t)grid), dim3(kSeqWgThreads), 0, st, cv, \
-                       offsets, samples, pack, ppack, target, s.batch, s.seq, s.n_outputs,             \
+        // two 64-column slices a pass where the sub-table's row arrays leave LDS room
+        const bool wide = quad && (1u << (s.n_anchors + s.pe_dim)) <= (uint32_t)kSeqWgWideRows;
+#define SPIKY_WSEQ(IM, OW, WD)                                                                              \
+    hipLaunchKernelGGL((k_wgrad_seq_sort<IM, OW, WD>), dim3((uint32_t)grid), dim3(kSeqWgThreads), 0, st, cv, \
+                       offsets, samples, pack, ppack, target, s.batch, s.seq, s.n_outputs,                  \
                        s.n_detectors, s.n_anchors, s.pe_dim, cols, n_slices, ipb, int_rescaler, quad)
+#define SPIKY_WSEQ_W(IM, OW)           \
+    if (wide)                          \
+        SPIKY_WSEQ(IM, OW, true);      \
+    else                               \
+        SPIKY_WSEQ(IM, OW, false);
         if (int_mode) {
-            if (overwrite) SPIKY_WSEQ(true, true); else SPIKY_WSEQ(true, false);
+            if (overwrite) { SPIKY_WSEQ_W(true, true) } else { SPIKY_WSEQ_W(true, false) }
         } else {
-            if (overwrite) SPIKY_WSEQ(false, true); else SPIKY_WSEQ(false, false);
+            if (overwrite) { SPIKY_WSEQ_W(false, true) } else { SPIKY_WSEQ_W(false, false) }
         }
+#undef SPIKY_WSEQ_W
 #undef SPIKY_WSEQ
         return hipGetLastError();
     }
