@@ -1735,13 +1735,47 @@ constexpr int kSeqWgClasses = 64;        // row length classes (turns of kQuadSt
 constexpr int kSeqWgWideRows = 1024;
 static_assert(kSeqWgGvWords * 4 >= (kSeqWgKeys + kSeqWgPe) * 2, "the index tables fit the second plane");
 
+// The order in which the weight gradient's workgroups take the (table, Q)
+// buckets: largest first (classes of 32 items), so that the longest workgroups
+// -- buckets past one batch, where an input's few values concentrate its Q --
+// start first instead of trailing the grid.  One workgroup.
+constexpr int kOrderClasses = 64;
+__global__ __launch_bounds__(kSeqWgThreads) void k_bucket_order(const int32_t *__restrict__ offsets,
+                                                              uint32_t n_q, uint32_t n_buckets,
+                                                              uint32_t *__restrict__ order) {
+    __shared__ uint32_t hist[kOrderClasses];
+    const uint32_t tid = threadIdx.x;
+    auto cls = [&](uint32_t b) -> uint32_t {
+        const int32_t *o = offsets + (size_t)(b / n_q) * (n_q + 1) + b % n_q;
+        const uint32_t n = (uint32_t)(o[1] - o[0]);
+        return (uint32_t)kOrderClasses - 1u - min(n / 32u, (uint32_t)kOrderClasses - 1u);
+    };
+    if (tid < (uint32_t)kOrderClasses) hist[tid] = 0u;
+    __syncthreads();
+    for (uint32_t b = tid; b < n_buckets; b += kSeqWgThreads) atomicAdd(&hist[cls(b)], 1u);
+    __syncthreads();
+    if (tid < (uint32_t)kWave) {  // exclusive scan of the class counts
+        const uint32_t v = tid < (uint32_t)kOrderClasses ? hist[tid] : 0u;
+        uint32_t incl = v;
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) {
+            const uint32_t y = __shfl_up(incl, o, kWave);
+            if ((int)tid >= o) incl += y;
+        }
+        if (tid < (uint32_t)kOrderClasses) hist[tid] = incl - v;
+    }
+    __syncthreads();
+    for (uint32_t b = tid; b < n_buckets; b += kSeqWgThreads) order[atomicAdd(&hist[cls(b)], 1u)] = b;
+}
+
 template <bool INT_MODE, bool OVERWRITE, bool WIDE>
 __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
     const uint32_t *__restrict__ cv, const int32_t *__restrict__ offsets,
     const int32_t *__restrict__ samples, const uint2 *__restrict__ pack,
-    const uint2 *__restrict__ ppack, float *__restrict__ target, uint32_t batch, uint32_t seq,
-    uint32_t n_outputs, uint32_t n_detectors, uint32_t n_anchors, uint32_t pe_dim,
-    uint32_t cols, uint32_t n_slices, uint32_t items_per_batch, double int_rescaler, bool quad) {
+    const uint2 *__restrict__ ppack, const uint32_t *__restrict__ order, float *__restrict__ target,
+    uint32_t batch, uint32_t seq, uint32_t n_outputs, uint32_t n_detectors, uint32_t n_anchors,
+    uint32_t pe_dim, uint32_t cols, uint32_t n_slices, uint32_t items_per_batch, double int_rescaler,
+    bool quad) {
     constexpr int kRowsCap = WIDE ? kSeqWgWideRows : kSeqWgRowsMax;
     __shared__ uint32_t cnt[kRowsCap + 1];  // counts, then (quad path) the walk's words and its end
     __shared__ uint32_t cur[kRowsCap];
@@ -1761,7 +1795,8 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
     const uint32_t lane = tid & (kWave - 1);
     const uint32_t wave = tid / kWave;
     const uint32_t n_q = 1u << n_anchors;
-    const uint32_t t = blockIdx.x / n_q, q = blockIdx.x % n_q;
+    const uint32_t bq = order[blockIdx.x];  // the bucket (t, q), largest first
+    const uint32_t t = bq / n_q, q = bq % n_q;
     const uint32_t sub_rows = 1u << (n_anchors + pe_dim);
     const uint32_t pmask = (1u << pe_dim) - 1;
     const uint32_t n_rows = batch * seq;
@@ -1936,7 +1971,8 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
             if (quad && !WIDE) gv_load(0);
             // The wide walk's pass of 128 columns: both planes' loads in flight
             // before their stores; the first pass's loads are issued here, to
-            // land while the buckets are padded
+            // land while the buckets are padded, a later pass's at the end of the
+            // pass before
             u32x4 wlo[kGvPasses], whi[kGvPasses];
             auto wide_load = [&](uint32_t col0) {
                 const uint32_t cq = col0 + (tid & 15u) * 4u;
@@ -1970,7 +2006,6 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
                 // the batch's gradient rows, then a zero row (item nb) that the
                 // quad path reads for pads
                 if (WIDE) {
-                    if (sl > 0) wide_load(col0);
 #pragma unroll
                     for (int u = 0; u < kGvPasses; u++) {
                         const uint32_t it = (tid >> 4) + 64u * u;
@@ -2116,6 +2151,9 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
                             *p = o;
                         }
                     }
+                    // the wide walk's next pass: each wave issues its share of the
+                    // loads once its rows are done, to land while others walk
+                    if (WIDE && sl + 1 < n_pass) wide_load(col0 + 2 * cols);
                     continue;
                 }
                 // lane group g (cols lanes) takes the rows whose entries start in
@@ -2450,6 +2488,7 @@ hipError_t launch_backward_seq(const SeqShape &s, float *w, const float *g, cons
     int32_t *samples2 = lay.take<int32_t>((size_t)s.n_detectors * rows * 4);
     double *tk = pairs ? lay.take<double>(seq_tri_bytes(s)) : nullptr;
     double *tp = pairs ? lay.take<double>(seq_tri_bytes(s)) : nullptr;
+    uint32_t *wg_order = lay.take<uint32_t>((size_t)s.n_detectors * (1u << s.n_anchors) * 4);
     uint2 *list_a = nullptr, *list_b = nullptr;
     uint32_t *off_a = nullptr, *off_b = nullptr;
     if (gb >= 0) {
@@ -2604,9 +2643,11 @@ hipError_t launch_backward_seq(const SeqShape &s, float *w, const float *g, cons
         const bool quad = cols == 64 && s.n_outputs % 4 == 0 && ((uintptr_t)target & 15) == 0;
         // two 64-column slices a pass where the sub-table's row arrays leave LDS room
         const bool wide = quad && (1u << (s.n_anchors + s.pe_dim)) <= (uint32_t)kSeqWgWideRows;
+        hipLaunchKernelGGL(k_bucket_order, dim3(1), dim3(kSeqWgThreads), 0, st, offsets, 1u << s.n_anchors,
+                           (uint32_t)grid, wg_order);
 #define SPIKY_WSEQ(IM, OW, WD)                                                                              \
     hipLaunchKernelGGL((k_wgrad_seq_sort<IM, OW, WD>), dim3((uint32_t)grid), dim3(kSeqWgThreads), 0, st, cv, \
-                       offsets, samples, pack, ppack, target, s.batch, s.seq, s.n_outputs,                  \
+                       offsets, samples, pack, ppack, wg_order, target, s.batch, s.seq, s.n_outputs,        \
                        s.n_detectors, s.n_anchors, s.pe_dim, cols, n_slices, ipb, int_rescaler, quad)
 #define SPIKY_WSEQ_W(IM, OW)           \
     if (wide)                          \
