@@ -381,8 +381,8 @@ template <int C, bool INT_MODE>
 __global__ __launch_bounds__(kSfThreads) void k_fill_seq_lds(
     const float *__restrict__ w, const uint2 *__restrict__ pack, const uint2 *__restrict__ ppack,
     const int32_t *__restrict__ offsets, const int32_t *__restrict__ samples,
-    uint32_t *__restrict__ part, uint32_t batch, uint32_t seq, uint32_t n_outputs,
-    uint32_t n_anchors, uint32_t pe_dim, uint32_t n_slices, double int_rescaler) {
+    const uint32_t *__restrict__ order, uint32_t *__restrict__ part, uint32_t batch, uint32_t seq,
+    uint32_t n_outputs, uint32_t n_anchors, uint32_t pe_dim, uint32_t n_slices, double int_rescaler) {
     constexpr int VW = C >= 64 ? 4 : (C >= 32 ? 2 : 1);  // columns per lane
     constexpr int L = C / VW;          // lanes per item
     constexpr int kSlots = kWave / L;  // items per wavefront
@@ -402,7 +402,7 @@ __global__ __launch_bounds__(kSfThreads) void k_fill_seq_lds(
     const uint32_t half = lane / L, cl = lane % L;
     uint32_t *my_rows = rowtab + (wave * kSlots + half) * C;
     const uint32_t slice = blockIdx.x % n_slices;
-    const uint32_t tq = blockIdx.x / n_slices;
+    const uint32_t tq = order[blockIdx.x / n_slices];  // the bucket (t, q), largest first
     const uint32_t n_q = 1u << n_anchors;
     const uint32_t t = tq / n_q, q = tq % n_q;
     const uint32_t sub_rows = 1u << (n_anchors + pe_dim);
@@ -2377,11 +2377,12 @@ hipError_t launch_forward_seq(const SeqShape &s, const float *w, const float *x,
     uint2 *pack = lay.take<uint2>((size_t)rows * s.n_detectors * 8);
     uint2 *ppack = lay.take<uint2>((size_t)s.n_detectors * (s.seq - 1) * 8);
     int32_t *offsets = nullptr, *samples = nullptr;
-    uint32_t *part = nullptr;
+    uint32_t *part = nullptr, *order = nullptr;
     if (fcols > 0) {
         offsets = lay.take<int32_t>((size_t)s.n_detectors * ((1u << s.n_anchors) + 1) * 4);
         samples = lay.take<int32_t>((size_t)s.n_detectors * rows * 4);
         part = lay.take<uint32_t>((size_t)s.n_detectors * rows * s.n_outputs * 4);
+        order = lay.take<uint32_t>((size_t)s.n_detectors * (1u << s.n_anchors) * 4);
     }
     hipError_t e;
     if (lay.stop(&e, "forward_step_concat")) return e;
@@ -2412,9 +2413,13 @@ hipError_t launch_forward_seq(const SeqShape &s, const float *w, const float *x,
         const uint32_t n_slices = (s.n_outputs + fcols - 1) / fcols;
         const uint64_t grid = (uint64_t)s.n_detectors * (1u << s.n_anchors) * n_slices;
         if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
+        // workgroups take the buckets largest first (an input with few distinct
+        // rows, such as a token embedding, concentrates its Q values)
+        hipLaunchKernelGGL(k_bucket_order, dim3(1), dim3(kSeqWgThreads), 0, st, offsets, 1u << s.n_anchors,
+                           s.n_detectors * (1u << s.n_anchors), order);
 #define SPIKY_FLDS(C, IM)                                                                          \
     hipLaunchKernelGGL((k_fill_seq_lds<C, IM>), dim3((uint32_t)grid), dim3(kSfThreads), 0, st, w,    \
-                       pack, ppack, offsets, samples, part, s.batch, s.seq, s.n_outputs,            \
+                       pack, ppack, offsets, samples, order, part, s.batch, s.seq, s.n_outputs,     \
                        s.n_anchors, s.pe_dim, n_slices, int_rescaler)
         switch (fcols) {
             case 64: if (int_mode) SPIKY_FLDS(64, true); else SPIKY_FLDS(64, false); break;
