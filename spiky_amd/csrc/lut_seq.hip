@@ -2292,7 +2292,7 @@ bool seq_pairs_applies(const SeqShape &s) {
 int seq_grp_bits(const SeqShape &s) {
     if (s.n_outputs != 64 && s.n_outputs != 128 && s.n_outputs != 256) return -1;
     if (s.n_anchors > 10 || s.seq < 2 || s.seq - 1 > (uint32_t)kGrpMaxDist) return -1;
-    if ((uint64_t)s.batch * s.seq > 0x7fffffffull) return -1;
+    if ((uint64_t)s.batch * s.seq >= (1ull << 27)) return -1;  // rows in 27 bits of the item metadata
     uint32_t lr = 0;
     while ((kGrpTabBytes >> (lr + 1)) >= (int)(s.n_outputs * 4)) lr++;
     if (s.pe_dim > lr) return -1;
