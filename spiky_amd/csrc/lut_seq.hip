@@ -402,7 +402,7 @@ __global__ __launch_bounds__(kSfThreads) void k_fill_seq_lds(
     const uint32_t half = lane / L, cl = lane % L;
     uint32_t *my_rows = rowtab + (wave * kSlots + half) * C;
     const uint32_t slice = blockIdx.x % n_slices;
-    const uint32_t tq = order[blockIdx.x / n_slices];  // the bucket (t, q), largest first
+    const uint32_t tq = order ? order[blockIdx.x / n_slices] : blockIdx.x / n_slices;  // largest first
     const uint32_t n_q = 1u << n_anchors;
     const uint32_t t = tq / n_q, q = tq % n_q;
     const uint32_t sub_rows = 1u << (n_anchors + pe_dim);
@@ -1740,6 +1740,7 @@ static_assert(kSeqWgGvWords * 4 >= (kSeqWgKeys + kSeqWgPe) * 2, "the index table
 // -- buckets past one batch, where an input's few values concentrate its Q --
 // start first instead of trailing the grid.  One workgroup.
 constexpr int kOrderClasses = 64;
+constexpr uint32_t kOrderMaxBuckets = 65536;  // beyond: table order (one workgroup sorts)
 __global__ __launch_bounds__(kSeqWgThreads) void k_bucket_order(const int32_t *__restrict__ offsets,
                                                               uint32_t n_q, uint32_t n_buckets,
                                                               uint32_t *__restrict__ order) {
@@ -1795,7 +1796,7 @@ __global__ __launch_bounds__(kSeqWgThreads) void k_wgrad_seq_sort(
     const uint32_t lane = tid & (kWave - 1);
     const uint32_t wave = tid / kWave;
     const uint32_t n_q = 1u << n_anchors;
-    const uint32_t bq = order[blockIdx.x];  // the bucket (t, q), largest first
+    const uint32_t bq = order ? order[blockIdx.x] : blockIdx.x;  // the bucket (t, q), largest first
     const uint32_t t = bq / n_q, q = bq % n_q;
     const uint32_t sub_rows = 1u << (n_anchors + pe_dim);
     const uint32_t pmask = (1u << pe_dim) - 1;
@@ -2415,8 +2416,12 @@ hipError_t launch_forward_seq(const SeqShape &s, const float *w, const float *x,
         if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
         // workgroups take the buckets largest first (an input with few distinct
         // rows, such as a token embedding, concentrates its Q values)
-        hipLaunchKernelGGL(k_bucket_order, dim3(1), dim3(kSeqWgThreads), 0, st, offsets, 1u << s.n_anchors,
-                           s.n_detectors * (1u << s.n_anchors), order);
+        const uint32_t n_buckets = s.n_detectors * (1u << s.n_anchors);
+        if (n_buckets <= kOrderMaxBuckets)
+            hipLaunchKernelGGL(k_bucket_order, dim3(1), dim3(kSeqWgThreads), 0, st, offsets,
+                               1u << s.n_anchors, n_buckets, order);
+        else
+            order = nullptr;
 #define SPIKY_FLDS(C, IM)                                                                          \
     hipLaunchKernelGGL((k_fill_seq_lds<C, IM>), dim3((uint32_t)grid), dim3(kSfThreads), 0, st, w,    \
                        pack, ppack, offsets, samples, order, part, s.batch, s.seq, s.n_outputs,     \
@@ -2648,8 +2653,11 @@ hipError_t launch_backward_seq(const SeqShape &s, float *w, const float *g, cons
         const bool quad = cols == 64 && s.n_outputs % 4 == 0 && ((uintptr_t)target & 15) == 0;
         // two 64-column slices a pass where the sub-table's row arrays leave LDS room
         const bool wide = quad && (1u << (s.n_anchors + s.pe_dim)) <= (uint32_t)kSeqWgWideRows;
-        hipLaunchKernelGGL(k_bucket_order, dim3(1), dim3(kSeqWgThreads), 0, st, offsets, 1u << s.n_anchors,
-                           (uint32_t)grid, wg_order);
+        if (grid <= kOrderMaxBuckets)
+            hipLaunchKernelGGL(k_bucket_order, dim3(1), dim3(kSeqWgThreads), 0, st, offsets,
+                               1u << s.n_anchors, (uint32_t)grid, wg_order);
+        else
+            wg_order = nullptr;
 #define SPIKY_WSEQ(IM, OW, WD)                                                                              \
     hipLaunchKernelGGL((k_wgrad_seq_sort<IM, OW, WD>), dim3((uint32_t)grid), dim3(kSeqWgThreads), 0, st, cv, \
                        offsets, samples, pack, ppack, wg_order, target, s.batch, s.seq, s.n_outputs,        \

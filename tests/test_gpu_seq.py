@@ -230,6 +230,13 @@ def test_seq_grouped_input_gradient(oracle, cuda_device, shape):
     run_seq(oracle, B, S, I, T, Nc, Npe, O, seed=30 + Nc)
 
 
+def test_seq_many_buckets_table_order(oracle, cuda_device):
+    # more (table, Q) buckets than the largest-first order sorts in its one
+    # workgroup (4100 x 16 > 65536): the forward and the weight gradient then
+    # take them in table order, 64-column slices (the weight gradient's wide pass)
+    run_seq(oracle, 2, 8, 16, 4100, 4, 0, 64, seed=40)
+
+
 def test_seq_attention_layer_shape_int32(oracle, cuda_device):
     run_seq(oracle, 2, 256, 64, 4, 6, 4, 256, seed=13, int_rescaler=0.25)
 
