@@ -160,9 +160,11 @@ struct spiky_lut_manager {
     std::vector<int32_t> syn_neuron;  // lookup neuron of each synapse
     std::vector<int64_t> in_offsets;
     std::vector<int32_t> in_pairs;
+    std::vector<uint32_t> in_order;  // outputs by descending list length, ties in output order
+    uint32_t n_in_nonempty = 0;      // outputs with a non-empty list (the head of in_order)
     bool uniform = false;
     uint32_t max_groups = 0;
-    DeviceBuffer d_syn_offsets, d_syn_targets, d_syn_neuron, d_in_offsets, d_in_pairs;
+    DeviceBuffer d_syn_offsets, d_syn_targets, d_syn_neuron, d_in_offsets, d_in_pairs, d_in_order;
     bool dirty = true;
 
     // forward and backward keep separate scratch so that calls issued on
@@ -251,6 +253,7 @@ struct spiky_lut_manager {
         if (uniform) {
             d_in_offsets.upload(in_offsets.data(), in_offsets.size() * sizeof(int64_t), dirty);
             d_in_pairs.upload(in_pairs.data(), in_pairs.size() * sizeof(int32_t), dirty);
+            d_in_order.upload(in_order.data(), in_order.size() * sizeof(uint32_t), dirty);
         }
         dirty = false;
     }
@@ -327,6 +330,17 @@ hipError_t layout_propagate_tm(const spiky::FcShape &s, spiky::Scratch &x) {
 hipError_t layout_wgrad_fc(const spiky_lut_manager *m, const spiky::FcShape &s, spiky::Scratch &x) {
     return spiky::launch_wgrad_fc(s, nullptr, nullptr, nullptr, 1.0, m->int_mode, m->int_rescaler, true, x,
                                   nullptr);
+}
+
+// fp32 sums leave the outputs with empty lists as they are; int32 sums convert every output
+uint32_t fill_sparse_order_len(const spiky_lut_manager *m) {
+    return m->int_mode ? m->n_outputs : m->n_in_nonempty;
+}
+
+hipError_t layout_fill_sparse(const spiky_lut_manager *m, const spiky::SparseShape &s, spiky::Scratch &x) {
+    return spiky::launch_fill_sparse_uniform(s, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                             fill_sparse_order_len(m), nullptr, m->int_mode, m->int_rescaler, x,
+                                             nullptr);
 }
 
 hipError_t layout_wgrad_sparse(const spiky_lut_manager *m, const spiky::SparseShape &s, spiky::Scratch &x) {
@@ -443,6 +457,7 @@ void spiky_lut_destroy(spiky_lut_manager *m) {
     m->d_syn_neuron.release();
     m->d_in_offsets.release();
     m->d_in_pairs.release();
+    m->d_in_order.release();
     delete m;
 }
 
@@ -554,6 +569,8 @@ int spiky_lut_set_sparse_connectivity(spiky_lut_manager *m, const int64_t *syn_o
         m->uniform = uniform;
         m->in_offsets.clear();
         m->in_pairs.clear();
+        m->in_order.clear();
+        m->n_in_nonempty = 0;
         if (uniform) {
             std::vector<int64_t> cnt(m->n_outputs + 1, 0);
             for (uint32_t t = 0; t < m->n_detectors; t++) {
@@ -577,6 +594,13 @@ int spiky_lut_set_sparse_connectivity(spiky_lut_manager *m, const int64_t *syn_o
                     m->in_pairs[4 * p + 2] = (int32_t)len0;
                 }
             }
+            // the sample-lane forward's order: longest lists first
+            m->in_order.resize(m->n_outputs);
+            for (uint32_t j = 0; j < m->n_outputs; j++) m->in_order[j] = j;
+            std::stable_sort(m->in_order.begin(), m->in_order.end(), [&](uint32_t a, uint32_t b) {
+                return cnt[a + 1] - cnt[a] > cnt[b + 1] - cnt[b];
+            });
+            for (uint32_t j = 0; j < m->n_outputs; j++) m->n_in_nonempty += cnt[j + 1] > cnt[j] ? 1u : 0u;
         }
         m->has_connectivity = true;
         m->dirty = true;
@@ -628,12 +652,14 @@ int spiky_lut_forward_step(spiky_lut_manager *m, const float *weights, uint32_t 
             spiky::SparseShape ss{s, m->max_groups, m->uniform};
             const int64_t *off = (const int64_t *)m->d_syn_offsets.ptr;
             if (m->uniform) {
+                spiky::Scratch scr = m->scratch_fwd.scratch_for(
+                    [&](spiky::Scratch &x) { return layout_fill_sparse(m, ss, x); }, "fill_outputs_sparse");
                 m->timed("fill_outputs_sparse", st, [&] {
-                    check_hip(spiky::launch_fill_sparse_uniform(
-                                  ss, weights, lookup_indices, off, (const int64_t *)m->d_in_offsets.ptr,
-                                  (const int32_t *)m->d_in_pairs.ptr, output, m->int_mode,
-                                  m->int_rescaler, st),
-                              "fill_outputs_sparse");
+                    check_launch(spiky::launch_fill_sparse_uniform(
+                                     ss, weights, lookup_indices, off, (const int64_t *)m->d_in_offsets.ptr,
+                                     (const int32_t *)m->d_in_pairs.ptr, (const uint32_t *)m->d_in_order.ptr,
+                                     fill_sparse_order_len(m), output, m->int_mode, m->int_rescaler, scr, st),
+                                 "fill_outputs_sparse");
                 });
             } else {
                 m->timed("fill_outputs_sparse", st, [&] {
@@ -1274,6 +1300,9 @@ int spiky_lut_scratch_plan(spiky_lut_manager *m, int op, uint32_t batch_size, ui
                         single([&](spiky::Scratch &x) { return layout_fill_tm(m, s, x); }, "fill_outputs_fc");
                     else
                         single([&](spiky::Scratch &x) { return layout_fill_tm_i8(m, s, x); }, "fill_outputs_fc_i8");
+                } else if (!fc && m->uniform) {
+                    const spiky::SparseShape ss{s, m->max_groups, m->uniform};
+                    single([&](spiky::Scratch &x) { return layout_fill_sparse(m, ss, x); }, "fill_outputs_sparse");
                 }
                 break;
             }

@@ -218,11 +218,19 @@ struct SparseShape {
 // for output j, in_pairs[in_offsets[j] .. in_offsets[j+1]) are 4-int entries
 // {t, o, len, 0} in ascending (t, k): synapse k of detector t's neurons targets
 // j, o = syn_offsets[t * E] + k and len the synapses a neuron of t (row e's
-// synapse k is at o + e * len; total synapses below 2^31).
+// synapse k is at o + e * len; total synapses below 2^31).  order[0 .. n_order)
+// lists outputs by descending list length (ties in output order); fp32 sums
+// may leave out the outputs with empty lists (their sums are the output's own
+// value), int32 sums must list every output (the conversion rewrites it).
+// With sparse_fill_by_sample(s) the launcher lays out the lookup indices
+// table-major in `scr` (T * batch bytes, two a key past 256 rows); otherwise it
+// takes no scratch and ignores the order.
+bool sparse_fill_by_sample(const SparseShape &s);
 hipError_t launch_fill_sparse_uniform(const SparseShape &s, const float *w, const int32_t *idx,
                                       const int64_t *syn_offsets, const int64_t *in_offsets,
-                                      const int32_t *in_pairs, float *out, bool int_mode,
-                                      double int_rescaler, hipStream_t st);
+                                      const int32_t *in_pairs, const uint32_t *order, uint32_t n_order,
+                                      float *out, bool int_mode, double int_rescaler, Scratch &scr,
+                                      hipStream_t st);
 
 // Generic forward: one thread per (b, t, group), fp32 (or int32) atomics.
 hipError_t launch_fill_sparse_atomic(const SparseShape &s, const float *w, const int32_t *idx,

@@ -10,6 +10,12 @@
 //                          incoming (detector, slot) pairs in ascending order,
 //                          which is the reference CPU path's commit order, so the
 //                          fp32 result is bit-identical to it (no atomics).
+//   k_keys_by_table        the lookup indices table-major, one byte (or two) a
+//                          key: keys_t[t][b] = idx[b][t].
+//   k_fill_sparse_by_sample the same sums with a wavefront per (output, 64
+//                          samples), outputs longest list first: the list is
+//                          read through scalar loads once per 64 samples and the
+//                          keys of 64 samples are 64 contiguous bytes.
 //   k_fill_sparse_atomic   one thread per (b, t, group): the reference's own
 //                          decomposition with fp32/int32 atomics (any topology).
 //   k_propagate_sparse     eight lanes (one for int32 sums) per (b, t, group):
@@ -75,6 +81,160 @@ __global__ __launch_bounds__(kBlock) void k_fill_sparse_uniform(
         out[item] = (float)(((double)iacc * kDenom32Reciproc) / int_rescaler);
     else
         out[item] = acc;
+}
+
+// Thread (t4, b): keys_t[t][b] = idx[b][t] for t = 4 t4 .. 4 t4 + 3, lanes
+// running over b (the 16-byte reads when rows are 16-byte aligned, `vec`).
+template <typename KT>
+__global__ __launch_bounds__(kBlock) void k_keys_by_table(const int32_t *__restrict__ idx, KT *__restrict__ keys_t,
+                                                          uint32_t batch, uint32_t n_detectors, bool vec) {
+    const uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+    const uint32_t n_t4 = (n_detectors + 3) / 4;
+    if (i >= (uint64_t)n_t4 * batch) return;
+    const uint32_t b = (uint32_t)(i % batch), t = (uint32_t)(i / batch) * 4;
+    const int32_t *src = idx + (size_t)b * n_detectors + t;
+    KT *dst = keys_t + (size_t)t * batch + b;
+    if (vec) {
+        const int4 v = *reinterpret_cast<const int4 *>(src);
+        dst[0] = (KT)v.x;
+        dst[batch] = (KT)v.y;
+        dst[2 * (size_t)batch] = (KT)v.z;
+        dst[3 * (size_t)batch] = (KT)v.w;
+    } else {
+        for (uint32_t k = 0; k < 4 && t + k < n_detectors; k++) dst[k * (size_t)batch] = (KT)src[k];
+    }
+}
+
+// The sums of k_fill_sparse_uniform, one wavefront (a workgroup) per (output
+// order[r], 64 samples), lane = sample.  The output's list is the same for
+// every lane, so it comes through scalar loads, and lane b's key of table t is
+// keys_t[t * batch + b]: 64 lanes read 64 (or 128) contiguous bytes.  The walk
+// runs three groups of kGrp entries deep -- the weights of group g, the keys of
+// group g + 1 and the entries of group g + 2 are in flight together -- and adds
+// in ascending entry order, so the result is bit-identical to the one-thread
+// walk.  Outputs come longest list first (order[]), so the longest walks start
+// first and the short ones fill in behind them.
+constexpr int kSparseGrp = 8;
+constexpr uint32_t kSparseLanesMinBatch = 48;
+
+template <bool INT_MODE, typename KT>
+__global__ __launch_bounds__(64) void k_fill_sparse_by_sample(
+    const float *__restrict__ w, const KT *__restrict__ keys_t, const int64_t *__restrict__ in_offsets,
+    const int4 *__restrict__ in_pairs, const uint32_t *__restrict__ order, float *__restrict__ out,
+    uint32_t batch, uint32_t n_outputs, uint32_t n_bblk, uint32_t emask, double int_rescaler) {
+    constexpr int G = kSparseGrp;
+    const uint32_t r = blockIdx.x / n_bblk;
+    const uint32_t j = __builtin_amdgcn_readfirstlane(order[r]);
+    const uint32_t b = (blockIdx.x % n_bblk) * 64u + threadIdx.x;
+    const bool on = b < batch;
+    const uint32_t bb = on ? b : batch - 1u;  // lanes past the batch walk a valid sample
+    const size_t o = (size_t)bb * n_outputs + j;
+    const KT *kb = keys_t + bb;
+    float acc = out[o];
+    int32_t iacc = __float_as_int(acc);
+    const int64_t p0 = in_offsets[j], p1 = in_offsets[j + 1];
+    const int64_t ng = (p1 - p0) / G;
+    int4 pa[G], pb[G];
+    uint32_t ea[G];
+#pragma unroll
+    for (int k = 0; k < G; k++) {
+        pa[k] = make_int4(0, 0, 0, 0);
+        pb[k] = pa[k];
+        ea[k] = 0;
+    }
+    if (ng > 0) {
+        const int64_t pn = ng > 1 ? p0 + G : p0;
+#pragma unroll
+        for (int k = 0; k < G; k++) {
+            pa[k] = in_pairs[p0 + k];
+            pb[k] = in_pairs[pn + k];
+        }
+#pragma unroll
+        for (int k = 0; k < G; k++) ea[k] = kb[(size_t)pa[k].x * batch];
+    }
+    // The values entering the loop pass through an xor with a zero the
+    // compiler cannot prove, so no loop-carried value is a phi of loads alone:
+    // the optimiser would turn such a phi into one load at the use, which
+    // undoes the three-deep walk.
+    const uint32_t z = emask >> 31;
+#pragma unroll
+    for (int k = 0; k < G; k++) {
+        pa[k].x ^= z; pa[k].y ^= z; pa[k].z ^= z;
+        pb[k].x ^= z; pb[k].y ^= z; pb[k].z ^= z;
+        ea[k] ^= z;
+    }
+    // past the last group the entry loads re-read group 0 (in bounds, unused):
+    // the loop has no branch, so its waits count the loads in flight exactly
+    for (int64_t g = 0; g < ng; g++) {
+        float wv[G];
+        uint32_t eb[G];
+        int4 pc[G];
+#pragma unroll
+        for (int k = 0; k < G; k++) wv[k] = w[(uint32_t)pa[k].y + (ea[k] & emask) * (uint32_t)pa[k].z];
+#pragma unroll
+        for (int k = 0; k < G; k++) eb[k] = kb[(size_t)pb[k].x * batch];
+        const int64_t pn = (g + 2 < ng) ? p0 + (g + 2) * G : p0;
+#pragma unroll
+        for (int k = 0; k < G; k++) pc[k] = in_pairs[pn + k];
+#pragma unroll
+        for (int k = 0; k < G; k++) {
+            const double wt = (double)wv[k];
+            if (INT_MODE)
+                iacc = wrap_add(iacc, (int32_t)(wt * kDenom32 * int_rescaler));
+            else
+                acc += (float)wt;
+        }
+#pragma unroll
+        for (int k = 0; k < G; k++) {
+            pa[k] = pb[k];
+            ea[k] = eb[k];
+            pb[k] = pc[k];
+        }
+    }
+#pragma unroll 8
+    for (int64_t p = p0 + ng * G; p < p1; p++) {
+        const int4 tk = in_pairs[p];
+        const uint32_t e = (uint32_t)kb[(size_t)tk.x * batch] & emask;
+        const double wt = (double)w[(uint32_t)tk.y + e * (uint32_t)tk.z];
+        if (INT_MODE)
+            iacc = wrap_add(iacc, (int32_t)(wt * kDenom32 * int_rescaler));
+        else
+            acc += (float)wt;
+    }
+    if (!on) return;
+    if (INT_MODE)
+        out[o] = (float)(((double)iacc * kDenom32Reciproc) / int_rescaler);
+    else
+        out[o] = acc;
+}
+
+template <typename KT>
+hipError_t launch_fill_by_sample(const SparseShape &s, const float *w, const int32_t *idx,
+                                 const int64_t *in_offsets, const int4 *pairs, const uint32_t *order,
+                                 uint32_t n_order, float *out, bool int_mode, double int_rescaler, Scratch &scr,
+                                 hipStream_t st) {
+    ScratchLayout lay(scr);
+    KT *keys_t = lay.take<KT>((size_t)s.fc.n_detectors * s.fc.batch * sizeof(KT));
+    hipError_t e;
+    if (lay.stop(&e, "fill_outputs_sparse")) return e;
+    const uint64_t n_keys = (uint64_t)((s.fc.n_detectors + 3) / 4) * s.fc.batch;
+    const uint32_t n_bblk = (s.fc.batch + 63) / 64;
+    const uint64_t grid = (uint64_t)n_order * n_bblk;
+    if (grid > 0x7fffffffu || (n_keys + kBlock - 1) / kBlock > 0x7fffffffu) return hipErrorInvalidConfiguration;
+    if (grid == 0) return hipSuccess;
+    const bool vec = s.fc.n_detectors % 4 == 0 && reinterpret_cast<uintptr_t>(idx) % 16 == 0;
+    hipLaunchKernelGGL(k_keys_by_table<KT>, dim3((uint32_t)((n_keys + kBlock - 1) / kBlock)), dim3(kBlock), 0, st,
+                       idx, keys_t, s.fc.batch, s.fc.n_detectors, vec);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const uint32_t emask = s.fc.n_entries - 1;
+    if (int_mode)
+        hipLaunchKernelGGL((k_fill_sparse_by_sample<true, KT>), dim3((uint32_t)grid), dim3(64), 0, st, w, keys_t,
+                           in_offsets, pairs, order, out, s.fc.batch, s.fc.n_outputs, n_bblk, emask, int_rescaler);
+    else
+        hipLaunchKernelGGL((k_fill_sparse_by_sample<false, KT>), dim3((uint32_t)grid), dim3(64), 0, st, w, keys_t,
+                           in_offsets, pairs, order, out, s.fc.batch, s.fc.n_outputs, n_bblk, emask, int_rescaler);
+    return hipGetLastError();
 }
 
 template <bool INT_MODE>
@@ -256,13 +416,25 @@ __global__ __launch_bounds__(kBlock) void k_wgrad_sparse_rowsum(
 
 }  // namespace
 
+bool sparse_fill_by_sample(const SparseShape &s) {
+    return s.fc.batch >= kSparseLanesMinBatch && s.fc.n_entries <= 65536;
+}
+
 hipError_t launch_fill_sparse_uniform(const SparseShape &s, const float *w, const int32_t *idx,
                                       const int64_t *syn_offsets, const int64_t *in_offsets,
-                                      const int32_t *in_pairs, float *out, bool int_mode,
-                                      double int_rescaler, hipStream_t st) {
+                                      const int32_t *in_pairs, const uint32_t *order, uint32_t n_order,
+                                      float *out, bool int_mode, double int_rescaler, Scratch &scr,
+                                      hipStream_t st) {
     const uint64_t n = (uint64_t)s.fc.batch * s.fc.n_outputs;
-    if (n == 0) return hipSuccess;
     const int4 *pairs = reinterpret_cast<const int4 *>(in_pairs);
+    if (sparse_fill_by_sample(s)) {
+        if (s.fc.n_entries <= 256)
+            return launch_fill_by_sample<uint8_t>(s, w, idx, in_offsets, pairs, order, n_order, out, int_mode,
+                                                  int_rescaler, scr, st);
+        return launch_fill_by_sample<uint16_t>(s, w, idx, in_offsets, pairs, order, n_order, out, int_mode,
+                                               int_rescaler, scr, st);
+    }
+    if (scr.mode != Scratch::Run || n == 0) return hipSuccess;
     if (int_mode)
         hipLaunchKernelGGL(k_fill_sparse_uniform<true>, dim3(blocks_for(n)), dim3(kBlock), 0, st,
                            w, idx, syn_offsets, in_offsets, pairs, out, s.fc.batch, s.fc.n_outputs,

@@ -104,6 +104,37 @@ def test_projection_layer_sparse_parity(oracle, cuda_device):
     assert np.array_equal(layer._weights.grad.cpu().numpy(), rwg)
 
 
+@pytest.mark.parametrize("B", [48, 70, 130])
+@pytest.mark.parametrize("int_sums", [False, True])
+@pytest.mark.parametrize("Nc", [5, 9])
+def test_projection_layer_sparse_forward_wide_batches(oracle, cuda_device, B, int_sums, Nc):
+    """The sparse forward at batches of 48 and more (a wavefront per output and
+    64 samples over table-major keys: one byte a key at 32 rows, two at 512),
+    with partly filled wavefronts and outputs no synapse reaches, in fp32 and
+    int32 sums: bit-exact against the CPU restatement."""
+    dev = cuda_device
+    kw = dict(summation_dtype=torch.int32, _int_rescaler=0.37) if int_sums else {}
+    layer = ProjectionLUTLayer((20, 20), (16, 16), Nc, 20, 6, (5, 5), (4, 4), random_seed=11, **kw).to(dev)
+    with torch.no_grad():
+        layer._weights.normal_(0.0, 0.05)
+    T, I, O = layer.n_detectors(), 400, 256
+    E = 1 << Nc
+    x = torch.rand(B, 1, 20, 20, device=dev)
+    layer.eval()
+    with torch.no_grad():
+        y = layer(x)
+    offs, tg = layer._lut_dm.lookup_connectivity()
+    assert np.bincount(np.asarray(tg), minlength=O).min() == 0    # some outputs have empty lists
+    ridx, _, _ = oracle.check_detectors(x.cpu().numpy().reshape(-1), layer._detector_anchors.cpu().numpy(),
+                                        B, I, T, Nc)
+    Wn = layer._weights.detach().cpu().numpy()
+    rout = oracle.fill_outputs_sparse(Wn, ridx, offs, tg, B, O, T, E, int_mode=int_sums,
+                                      int_rescaler=0.37 if int_sums else 1.0)
+    if int_sums:
+        oracle.convert_int_to_float(rout, 0.37)    # the restatement leaves the int32 payloads
+    assert np.array_equal(y.cpu().numpy().reshape(-1), rout)
+
+
 def test_projection_layer_built_on_device(cuda_device):
     """A ProjectionLUTLayer constructed with device=cuda grows its connectivity
     on the host and gives the same layer as one built on the host and moved."""

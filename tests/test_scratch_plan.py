@@ -112,6 +112,26 @@ def test_sparse_layouts():
     assert walk(dm, "BACKWARD_NO_WGRAD", 100) == 0
 
 
+@pytest.mark.parametrize("Nc,key_bytes", [(3, 1), (9, 2)])
+def test_uniform_sparse_forward_layout(Nc, key_bytes):
+    # every lookup neuron of a detector sharing its target list: from a batch of
+    # 48 the forward lays the lookup indices out table-major, one byte a key for
+    # up to 256 rows and two beyond
+    import numpy as np
+    T, O = 5, 12
+    dm = manager(20, O, T, Nc, fc=False)
+    E = 1 << Nc
+    row = [np.array([(3 * t + k) % O for k in range(3 + t % 2)], np.int32) for t in range(T)]
+    tg = np.concatenate([np.tile(row[t], E) for t in range(T)]).astype(np.int32)
+    lens = np.repeat([len(r) for r in row], E)
+    offs = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    _native.check(_native.lib().spiky_lut_set_sparse_connectivity(
+        dm._h, offs.ctypes.data_as(ctypes.c_void_p), tg.ctypes.data_as(ctypes.c_void_p), tg.size))
+    assert walk(dm, "FORWARD", 47) == 0
+    assert walk(dm, "FORWARD", 48) == T * 48 * key_bytes
+    assert walk(dm, "FORWARD", 1000) == T * 1000 * key_bytes
+
+
 def test_config3_sizes():
     """Config 3's scratch: the forward's transposed u8 indices [T][B] and one
     fp32 partial [B][O] per unit of eight folded 32-table blocks; the
