@@ -164,6 +164,8 @@ struct spiky_lut_manager {
     uint32_t n_in_nonempty = 0;      // outputs with a non-empty list (the head of in_order)
     bool uniform = false;
     uint32_t max_groups = 0;
+    uint32_t max_row = 0;  // most synapses of one lookup neuron
+    uint32_t typ_row = 0;  // the median synapse count of the lookup neurons that have any
     DeviceBuffer d_syn_offsets, d_syn_targets, d_syn_neuron, d_in_offsets, d_in_pairs, d_in_order;
     bool dirty = true;
 
@@ -535,11 +537,13 @@ int spiky_lut_set_sparse_connectivity(spiky_lut_manager *m, const int64_t *syn_o
         if (syn_offsets[0] != 0 || (uint64_t)syn_offsets[nl] != n_synapses)
             throw ValueError("syn_offsets must start at 0 and end at n_synapses");
         uint32_t max_groups = 0;
+        int64_t max_row = 0;
         for (uint64_t n = 0; n < nl; n++) {
             const int64_t len = syn_offsets[n + 1] - syn_offsets[n];
             if (len < 0) throw ValueError("syn_offsets must be non-decreasing");
             max_groups = std::max<uint32_t>(
                 max_groups, (uint32_t)((len + m->forward_group_size - 1) / m->forward_group_size));
+            max_row = std::max(max_row, len);
         }
         for (uint64_t s = 0; s < n_synapses; s++)
             if (syn_targets[s] < 0 || (uint32_t)syn_targets[s] >= m->n_outputs)
@@ -550,6 +554,19 @@ int spiky_lut_set_sparse_connectivity(spiky_lut_manager *m, const int64_t *syn_o
         for (uint64_t n = 0; n < nl; n++)
             for (int64_t s = syn_offsets[n]; s < syn_offsets[n + 1]; s++) m->syn_neuron[s] = (int32_t)n;
         m->max_groups = max_groups;
+        m->max_row = (uint32_t)std::min<int64_t>(max_row, UINT32_MAX);
+        {
+            std::vector<int64_t> lens;
+            lens.reserve(nl);
+            for (uint64_t n = 0; n < nl; n++)
+                if (syn_offsets[n + 1] > syn_offsets[n]) lens.push_back(syn_offsets[n + 1] - syn_offsets[n]);
+            int64_t typ = 0;
+            if (!lens.empty()) {
+                std::nth_element(lens.begin(), lens.begin() + lens.size() / 2, lens.end());
+                typ = lens[lens.size() / 2];
+            }
+            m->typ_row = (uint32_t)std::min<int64_t>(typ, UINT32_MAX);
+        }
         // uniform topology: all lookup neurons of a detector share one ordered target list
         const uint32_t E = (uint32_t)(m->n_lookup / m->n_detectors);  // rows of a table
         bool uniform = true;
@@ -649,7 +666,7 @@ int spiky_lut_forward_step(spiky_lut_manager *m, const float *weights, uint32_t 
             }
         } else {
             m->sync_connectivity();
-            spiky::SparseShape ss{s, m->max_groups, m->uniform};
+            spiky::SparseShape ss{s, m->max_groups, m->uniform, m->max_row, m->typ_row};
             const int64_t *off = (const int64_t *)m->d_syn_offsets.ptr;
             if (m->uniform) {
                 spiky::Scratch scr = m->scratch_fwd.scratch_for(
@@ -838,7 +855,7 @@ int spiky_lut_backward_backprop(spiky_lut_manager *m, float *weights, uint32_t b
             }
         } else {
             m->sync_connectivity();
-            spiky::SparseShape ss{s, m->max_groups, m->uniform};
+            spiky::SparseShape ss{s, m->max_groups, m->uniform, m->max_row, m->typ_row};
             const int64_t *off = (const int64_t *)m->d_syn_offsets.ptr;
             const int32_t *tg = (const int32_t *)m->d_syn_targets.ptr;
             m->timed("propagate_sparse", st, [&] {
@@ -1301,7 +1318,7 @@ int spiky_lut_scratch_plan(spiky_lut_manager *m, int op, uint32_t batch_size, ui
                     else
                         single([&](spiky::Scratch &x) { return layout_fill_tm_i8(m, s, x); }, "fill_outputs_fc_i8");
                 } else if (!fc && m->uniform) {
-                    const spiky::SparseShape ss{s, m->max_groups, m->uniform};
+                    const spiky::SparseShape ss{s, m->max_groups, m->uniform, m->max_row, m->typ_row};
                     single([&](spiky::Scratch &x) { return layout_fill_sparse(m, ss, x); }, "fill_outputs_sparse");
                 }
                 break;
@@ -1322,7 +1339,7 @@ int spiky_lut_scratch_plan(spiky_lut_manager *m, int op, uint32_t batch_size, ui
                         check_region([&](spiky::Scratch &x) { return layout_wgrad_fc(m, s, x); }, r.prop_bytes,
                                      UINT64_MAX, "gather_w_gradients_fc");
                 } else if (wg) {
-                    const spiky::SparseShape ss{s, m->max_groups, m->uniform};
+                    const spiky::SparseShape ss{s, m->max_groups, m->uniform, m->max_row, m->typ_row};
                     single([&](spiky::Scratch &x) { return layout_wgrad_sparse(m, ss, x); },
                            "gather_w_gradients_sparse");
                 }

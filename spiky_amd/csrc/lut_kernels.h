@@ -211,6 +211,8 @@ struct SparseShape {
     FcShape fc;            // n_outputs, n_detectors, n_entries ... as above
     uint32_t max_groups;   // max forward groups (of fc.ogs synapses) per lookup neuron
     bool uniform = false;  // every lookup neuron of a detector has the same synapse count
+    uint32_t max_row = 0;  // most synapses of one lookup neuron
+    uint32_t typ_row = 0;  // the median synapse count of the lookup neurons that have any
 };
 
 // Output-major index for the exact forward, valid when every lookup neuron of

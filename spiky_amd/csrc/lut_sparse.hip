@@ -21,6 +21,11 @@
 //   k_propagate_sparse     eight lanes (one for int32 sums) per (b, t, group):
 //                          main/alt group dots in fp64 and the min-margin anchor
 //                          update.
+//   k_propagate_sparse_rows the same for fp32 sums over uniform rows: four lanes
+//                          per (b, t, group), each with a fixed number of entry
+//                          slots, the row's targets read once for both rows,
+//                          three rounds of loads, none behind a branch, and the
+//                          input-gradient adds summed in LDS where inputs are few.
 //   k_wgrad_sparse_rowsum  one thread per synapse: sums lr*g over the samples
 //                          bucketed on its lookup neuron (read from a per-synapse
 //                          neuron index), ascending (bit-identical to the
@@ -292,6 +297,12 @@ __device__ __forceinline__ double sp_dpp_f64(double v, int ctrl_sel) {
 }
 
 // sum over the 8 lanes of a group, every lane gets it
+__device__ __forceinline__ double sp_sum4(double v) {
+    v += sp_dpp_f64(v, 0);
+    v += sp_dpp_f64(v, 1);
+    return v;
+}
+
 __device__ __forceinline__ double sp_sum8(double v) {
     v += sp_dpp_f64(v, 0);
     v += sp_dpp_f64(v, 1);
@@ -362,6 +373,109 @@ __global__ __launch_bounds__(kBlock) void k_propagate_sparse(
         atomicAdd(reinterpret_cast<int32_t *>(xg + a.x), d);
         atomicAdd(reinterpret_cast<int32_t *>(xg + a.y), (int32_t)(0u - (uint32_t)d));
     } else {
+        unsafeAtomicAdd(xg + a.x, (float)du);
+        unsafeAtomicAdd(xg + a.y, (float)(-du));
+    }
+}
+
+// k_propagate_sparse for fp32 sums when every lookup neuron of a detector has
+// the same target list: kRowLanes lanes per (b, t, group), P entry slots a
+// lane per pass over the group, grid (items, batch).  The rows of a detector
+// share their targets, so the main and the alternative row read one target
+// and one output gradient per entry.  The loads go out in three rounds --
+// (offsets, key, min-margin index), then (margin, anchors, targets, both
+// rows' weights), then the output gradients -- with no branch between them
+// for groups of at most P * kRowLanes entries; slots past the group read
+// synapse 0 (in bounds) and add nothing.  With RED the workgroup (one sample)
+// first sums its input-gradient adds in LDS and then adds each non-zero input
+// once: where many tables share few inputs, that takes most of the same-address
+// atomics off the L2.
+constexpr int kRowLanes = 4;
+constexpr uint32_t kRowRedInputs = 4096;  // the LDS sum's inputs (16 KiB)
+
+template <int P, bool RED>
+__global__ __launch_bounds__(kBlock) void k_propagate_sparse_rows(
+    const float *__restrict__ w, const float *__restrict__ g, const int32_t *__restrict__ idx,
+    const float *__restrict__ md, const int32_t *__restrict__ mi, const int2 *__restrict__ anchors,
+    const int64_t *__restrict__ syn_offsets, const int32_t *__restrict__ syn_targets,
+    float *__restrict__ x_grad, uint32_t n_inputs, uint32_t n_outputs, uint32_t n_detectors,
+    uint32_t n_anchors, uint32_t n_entries, uint32_t ogs, uint32_t max_groups, uint32_t n_items) {
+    constexpr int L = kRowLanes;
+    __shared__ float red[RED ? kRowRedInputs : 1];
+    if (RED) {
+        for (uint32_t i = threadIdx.x; i < n_inputs; i += kBlock) red[i] = 0.0f;
+        __syncthreads();
+    }
+    const uint32_t xi = blockIdx.x * kBlock + threadIdx.x;
+    const uint32_t l = xi % L;
+    const uint32_t item0 = xi / L;  // t * max_groups + group
+    if (!RED && item0 >= n_items) return;  // whole lane groups (kBlock % L == 0)
+    const bool live = item0 < n_items;
+    const uint32_t item = live ? item0 : 0u;  // past the end: item 0's loads, no adds
+    const uint32_t b = blockIdx.y;
+    const uint32_t grp = max_groups == 1 ? 0 : item % max_groups;
+    const uint32_t t = max_groups == 1 ? item : item / max_groups;
+    const size_t bt = (size_t)b * n_detectors + t;
+    const int64_t o0 = syn_offsets[(size_t)t * n_entries];
+    const int64_t o1 = syn_offsets[(size_t)t * n_entries + 1];
+    const int32_t m = mi[bt];
+    const uint32_t r = (uint32_t)idx[bt] & (n_entries - 1);
+    const float mdv = md[bt];
+    // the 64-bit length keeps both halves of the offsets' load live, so no
+    // register of it is reused (and waited for) before the other loads go out
+    const int64_t len64 = o1 - o0;
+    const uint32_t len = (uint32_t)len64;
+    const uint32_t k0 = grp * ogs;
+    const uint32_t k1 = min(k0 + ogs, len);
+    const bool act = m >= 0 && (uint32_t)m < n_anchors;
+    const uint32_t mm = act ? (uint32_t)m : 0u;
+    const int2 a = anchors[(size_t)t * n_anchors + mm];
+    const int64_t om = o0 + (int64_t)r * len64, oa = o0 + (int64_t)(r ^ (1u << mm)) * len64;
+    const float *gb = g + (size_t)b * n_outputs;
+    double ms = 0.0, as = 0.0;
+    for (uint32_t c0 = k0; c0 < k1; c0 += (uint32_t)(L * P)) {
+        uint32_t tgv[P];
+        float wmv[P], wav[P];
+        bool ok[P];
+#pragma unroll
+        for (int i = 0; i < P; i++) {
+            const uint32_t k = c0 + l + (uint32_t)i * L;
+            ok[i] = k < k1;
+            tgv[i] = (uint32_t)syn_targets[ok[i] ? o0 + k : 0];
+            wmv[i] = w[ok[i] ? om + k : 0];
+            wav[i] = w[ok[i] ? oa + k : 0];
+        }
+        double gv[P];
+#pragma unroll
+        for (int i = 0; i < P; i++) gv[i] = (double)gb[tgv[i]];
+#pragma unroll
+        for (int i = 0; i < P; i++) {
+            const double pm = ms + (double)wmv[i] * gv[i], pa = as + (double)wav[i] * gv[i];
+            ms = ok[i] ? pm : ms;
+            as = ok[i] ? pa : as;
+        }
+    }
+    // The margin and the anchors are used in this block, so their loads stay up
+    // front instead of sinking below a branch; dmg == 0 gives du == 0, which
+    // never fires, so testing it changes nothing.
+    const double dmg = du_of_margin(mdv);
+    const bool fire = live && act && (uint32_t)a.x < n_inputs && (uint32_t)a.y < n_inputs && dmg != 0.0;
+    ms = sp_sum4(ms);
+    as = sp_sum4(as);
+    const double du = dmg * (ms - as);
+    const bool add = l == 0 && fire && fabs(du) > kEps;
+    float *xg = x_grad + (size_t)b * n_inputs;
+    if (RED) {
+        if (add) {
+            atomicAdd(&red[a.x], (float)du);
+            atomicAdd(&red[a.y], (float)(-du));
+        }
+        __syncthreads();
+        for (uint32_t i = threadIdx.x; i < n_inputs; i += kBlock) {
+            const float v = red[i];
+            if (v != 0.0f) unsafeAtomicAdd(xg + i, v);
+        }
+    } else if (add) {
         unsafeAtomicAdd(xg + a.x, (float)du);
         unsafeAtomicAdd(xg + a.y, (float)(-du));
     }
@@ -476,6 +590,41 @@ hipError_t launch_propagate_sparse(const SparseShape &s, const float *w, const f
     const uint64_t n_items = (uint64_t)s.fc.batch * s.fc.n_detectors * s.max_groups;
     if (n_items == 0) return hipSuccess;
     const int2 *ap = reinterpret_cast<const int2 *>(anchors);
+    // fp32 sums over uniform rows: slots for the typical group (a median row, at
+    // most ogs entries), longer groups take more passes
+    const uint32_t span = std::min(s.fc.ogs, s.typ_row);
+    const uint64_t n_rows_items = (uint64_t)s.fc.n_detectors * s.max_groups;
+    if (!int_mode && s.uniform && s.max_row > 0 && span > 0 && s.fc.batch <= 65535 &&
+        n_rows_items * kRowLanes <= 0x7fffffffull) {
+        const uint32_t n_x = (uint32_t)n_rows_items;
+        const dim3 grid((uint32_t)((n_rows_items * kRowLanes + kBlock - 1) / kBlock), s.fc.batch);
+        const uint32_t slots = (span + kRowLanes - 1) / kRowLanes;
+        // the LDS sum pays where a sample's adds (two a table and group) come to
+        // four or more per input
+        const bool red = s.fc.n_inputs <= kRowRedInputs && n_rows_items * 2 >= 4ull * s.fc.n_inputs;
+#define SPIKY_PROP_ROWS(P)                                                                                           \
+    do {                                                                                                             \
+        if (red)                                                                                                     \
+            hipLaunchKernelGGL((k_propagate_sparse_rows<P, true>), grid, dim3(kBlock), 0, st, w, g, idx, min_deltas, \
+                               min_idx, ap, syn_offsets, syn_targets, x_grad, s.fc.n_inputs, s.fc.n_outputs,         \
+                               s.fc.n_detectors, s.fc.n_anchors, s.fc.n_entries, s.fc.ogs, s.max_groups, n_x);       \
+        else                                                                                                         \
+            hipLaunchKernelGGL((k_propagate_sparse_rows<P, false>), grid, dim3(kBlock), 0, st, w, g, idx,            \
+                               min_deltas, min_idx, ap, syn_offsets, syn_targets, x_grad, s.fc.n_inputs,             \
+                               s.fc.n_outputs, s.fc.n_detectors, s.fc.n_anchors, s.fc.n_entries, s.fc.ogs,           \
+                               s.max_groups, n_x);                                                                   \
+    } while (0)
+        if (slots <= 1)
+            SPIKY_PROP_ROWS(1);
+        else if (slots <= 2)
+            SPIKY_PROP_ROWS(2);
+        else if (slots <= 4)
+            SPIKY_PROP_ROWS(4);
+        else
+            SPIKY_PROP_ROWS(8);
+#undef SPIKY_PROP_ROWS
+        return hipGetLastError();
+    }
     const uint64_t n_threads = n_items * (int_mode ? sp_lanes<true>() : sp_lanes<false>());
     if ((n_threads + kBlock - 1) / kBlock > 0x7fffffffull) return hipErrorInvalidConfiguration;
     if (int_mode)

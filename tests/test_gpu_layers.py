@@ -104,6 +104,51 @@ def test_projection_layer_sparse_parity(oracle, cuda_device):
     assert np.array_equal(layer._weights.grad.cpu().numpy(), rwg)
 
 
+@pytest.mark.parametrize("geo", [
+    # many tables on few inputs: the input-gradient adds summed in LDS first;
+    # 6x6 projections give rows of 36 entries, two forward groups
+    dict(inp=(12, 12), out=(24, 24), groups=64, tables=16, field=(5, 5), proj=(6, 6), B=40),
+    # rows of 1..4 entries (one slot a lane), inputs outnumbering the adds
+    dict(inp=(32, 32), out=(16, 16), groups=9, tables=8, field=(7, 7), proj=(2, 2), B=24),
+    # forward groups of 64 entries, rows of 12..36 (median 24: 8 slots a lane),
+    # so the longest rows take two passes
+    dict(inp=(16, 16), out=(10, 10), groups=25, tables=12, field=(5, 5), proj=(6, 6), B=17, fgs=64),
+])
+def test_projection_layer_sparse_backward_shapes(oracle, cuda_device, geo):
+    """The fp32 input gradient over uniform rows (four lanes per table and
+    group, entry slots for a median row, LDS-summed adds where inputs are few)
+    against the CPU restatement, with the weight gradient bit-exact."""
+    dev = cuda_device
+    torch.manual_seed(3)
+    fgs = geo.get("fgs", 32)
+    layer = ProjectionLUTLayer(geo["inp"], geo["out"], 5, geo["groups"], geo["tables"], geo["field"], geo["proj"],
+                               random_seed=9, _forward_group_size=fgs).to(dev)
+    with torch.no_grad():
+        layer._weights.normal_(0.0, 0.01)
+    B = geo["B"]
+    T, Nc = layer.n_detectors(), 5
+    I, O = geo["inp"][0] * geo["inp"][1], geo["out"][0] * geo["out"][1]
+    E = 1 << Nc
+    x = torch.rand(B, 1, *geo["inp"], device=dev)
+    x = (x * (torch.rand_like(x) > 0.5)).requires_grad_(True)
+    y = layer(x)
+    g = torch.randn_like(y)
+    y.backward(g)
+    offs, tg = layer._lut_dm.lookup_connectivity()
+    an = layer._detector_anchors.cpu().numpy()
+    Wn = layer._weights.detach().cpu().numpy()
+    xn = x.detach().cpu().numpy().reshape(-1)
+    gn = g.cpu().numpy().reshape(-1)
+    ridx, rmd, rmi = oracle.check_detectors(xn, an, B, I, T, Nc)
+    maxg = layer._lut_dm.get_max_forward_groups_per_neuron()
+    rxg = oracle.propagate_sparse(Wn, gn, ridx, rmd, rmi, an, offs, tg, B, I, O, T, Nc, E, fgs, maxg)
+    rwg = np.zeros(Wn.size, np.float32)
+    oracle.gather_wgrad_sparse(gn, ridx, offs, tg, rwg, B, O, T, E)
+    assert np.array_equal(y.detach().cpu().numpy().reshape(-1), oracle.fill_outputs_sparse(Wn, ridx, offs, tg, B, O, T, E))
+    _xg_close(x.grad.cpu().numpy(), rxg, B, I)
+    assert np.array_equal(layer._weights.grad.cpu().numpy(), rwg)
+
+
 @pytest.mark.parametrize("B", [48, 70, 130])
 @pytest.mark.parametrize("int_sums", [False, True])
 @pytest.mark.parametrize("Nc", [5, 9])
