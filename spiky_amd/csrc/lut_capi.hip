@@ -161,12 +161,14 @@ struct spiky_lut_manager {
     std::vector<int64_t> in_offsets;
     std::vector<int32_t> in_pairs;
     std::vector<uint32_t> in_order;  // outputs by descending list length, ties in output order
+    std::vector<int32_t> row_pairs;  // (t, k) for synapse k of detector t's rows (uniform topology)
     uint32_t n_in_nonempty = 0;      // outputs with a non-empty list (the head of in_order)
     bool uniform = false;
     uint32_t max_groups = 0;
     uint32_t max_row = 0;  // most synapses of one lookup neuron
     uint32_t typ_row = 0;  // the median synapse count of the lookup neurons that have any
-    DeviceBuffer d_syn_offsets, d_syn_targets, d_syn_neuron, d_in_offsets, d_in_pairs, d_in_order;
+    DeviceBuffer d_syn_offsets, d_syn_targets, d_syn_neuron, d_in_offsets, d_in_pairs, d_in_order,
+        d_row_pairs;
     bool dirty = true;
 
     // forward and backward keep separate scratch so that calls issued on
@@ -256,6 +258,7 @@ struct spiky_lut_manager {
             d_in_offsets.upload(in_offsets.data(), in_offsets.size() * sizeof(int64_t), dirty);
             d_in_pairs.upload(in_pairs.data(), in_pairs.size() * sizeof(int32_t), dirty);
             d_in_order.upload(in_order.data(), in_order.size() * sizeof(uint32_t), dirty);
+            d_row_pairs.upload(row_pairs.data(), row_pairs.size() * sizeof(int32_t), dirty);
         }
         dirty = false;
     }
@@ -346,8 +349,8 @@ hipError_t layout_fill_sparse(const spiky_lut_manager *m, const spiky::SparseSha
 }
 
 hipError_t layout_wgrad_sparse(const spiky_lut_manager *m, const spiky::SparseShape &s, spiky::Scratch &x) {
-    return spiky::launch_wgrad_sparse(s, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 1.0, true,
-                                      m->int_mode, m->int_rescaler, x, m->syn_targets.size(), nullptr);
+    return spiky::launch_wgrad_sparse(s, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0, nullptr, 1.0,
+                                      true, m->int_mode, m->int_rescaler, x, m->syn_targets.size(), nullptr);
 }
 
 hipError_t layout_forward_seq(const spiky_lut_manager *m, const spiky::SeqShape &s, spiky::Scratch &x) {
@@ -460,6 +463,7 @@ void spiky_lut_destroy(spiky_lut_manager *m) {
     m->d_in_offsets.release();
     m->d_in_pairs.release();
     m->d_in_order.release();
+    m->d_row_pairs.release();
     delete m;
 }
 
@@ -587,6 +591,7 @@ int spiky_lut_set_sparse_connectivity(spiky_lut_manager *m, const int64_t *syn_o
         m->in_offsets.clear();
         m->in_pairs.clear();
         m->in_order.clear();
+        m->row_pairs.clear();
         m->n_in_nonempty = 0;
         if (uniform) {
             std::vector<int64_t> cnt(m->n_outputs + 1, 0);
@@ -618,6 +623,14 @@ int spiky_lut_set_sparse_connectivity(spiky_lut_manager *m, const int64_t *syn_o
                 return cnt[a + 1] - cnt[a] > cnt[b + 1] - cnt[b];
             });
             for (uint32_t j = 0; j < m->n_outputs; j++) m->n_in_nonempty += cnt[j + 1] > cnt[j] ? 1u : 0u;
+            // the weight gradient's threads: synapse k of each detector's rows
+            for (uint32_t t = 0; t < m->n_detectors; t++) {
+                const uint64_t n0 = (uint64_t)t * E;
+                for (int64_t k = 0; k < syn_offsets[n0 + 1] - syn_offsets[n0]; k++) {
+                    m->row_pairs.push_back((int32_t)t);
+                    m->row_pairs.push_back((int32_t)k);
+                }
+            }
         }
         m->has_connectivity = true;
         m->dirty = true;
@@ -874,9 +887,11 @@ int spiky_lut_backward_backprop(spiky_lut_manager *m, float *weights, uint32_t b
                     [&](spiky::Scratch &x) { return layout_wgrad_sparse(m, ss, x); }, "gather_w_gradients_sparse");
                 m->timed("gather_w_gradients_sparse", st, [&] {
                     check_launch(spiky::launch_wgrad_sparse(ss, output_grad, lookup_indices, off, tg,
-                                                            (const int32_t *)m->d_syn_neuron.ptr, target,
-                                                            lr, overwrite, m->int_mode, m->int_rescaler, scr,
-                                                            n_syn, st),
+                                                            (const int32_t *)m->d_syn_neuron.ptr,
+                                                            (const int32_t *)m->d_row_pairs.ptr,
+                                                            (uint32_t)(m->row_pairs.size() / 2), target, lr,
+                                                            overwrite, m->int_mode, m->int_rescaler, scr, n_syn,
+                                                            st),
                                  "gather_w_gradients_sparse");
                 });
             }

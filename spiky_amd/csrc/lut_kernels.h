@@ -248,12 +248,15 @@ hipError_t launch_propagate_sparse(const SparseShape &s, const float *w, const f
                                    hipStream_t st);
 
 // syn_neuron[s] = the lookup neuron of synapse s.  overwrite: target starts
-// from zero (it is not read).  Scratch: the FC path's bucket arrays.
+// from zero (it is not read).  Scratch: the FC path's bucket arrays.  On a
+// uniform topology row_pairs lists (t, k) int pairs, one for synapse k of each
+// detector's rows (n_row_pairs = synapses / E); given, the gradient walks a
+// detector's samples once per k instead of once per synapse.
 hipError_t launch_wgrad_sparse(const SparseShape &s, const float *g, const int32_t *idx,
                                const int64_t *syn_offsets, const int32_t *syn_targets,
-                               const int32_t *syn_neuron, float *target, double lr, bool overwrite,
-                               bool int_mode, double int_rescaler, Scratch &scratch,
-                               uint64_t n_synapses, hipStream_t st);
+                               const int32_t *syn_neuron, const int32_t *row_pairs, uint32_t n_row_pairs,
+                               float *target, double lr, bool overwrite, bool int_mode, double int_rescaler,
+                               Scratch &scratch, uint64_t n_synapses, hipStream_t st);
 
 // ---- product mode (concatenation_product == False, lut_product.hip) ---------
 // Sequence-concat over sparse connectivity (lut_seq_sparse.hip).  The lookup

@@ -180,6 +180,51 @@ def test_projection_layer_sparse_forward_wide_batches(oracle, cuda_device, B, in
     assert np.array_equal(y.cpu().numpy().reshape(-1), rout)
 
 
+@pytest.mark.parametrize("int_sums", [False, True])
+@pytest.mark.parametrize("overwrite", [False, True])
+@pytest.mark.parametrize("B", [70, 100])
+def test_projection_sparse_wgrad_modes(oracle, cuda_device, int_sums, overwrite, B):
+    """The sparse weight gradient over uniform rows through the data manager --
+    a thread per synapse (70 samples over 32 rows) or per synapse slot of four
+    rows walking their samples in bucket order (100 samples) -- written over or
+    added to a buffer holding other values, in fp32 and int32 sums (where the
+    buffer holds int32 payloads and each row ends converted), bit-exact against
+    the CPU restatement."""
+    dev = cuda_device
+    R = 0.37
+    kw = dict(summation_dtype=torch.int32, _int_rescaler=R) if int_sums else {}
+    layer = ProjectionLUTLayer((16, 16), (12, 12), 5, 16, 8, (5, 5), (4, 4), random_seed=4, **kw).to(dev)
+    with torch.no_grad():
+        layer._weights.normal_(0.0, 0.05)
+    dm = layer._lut_dm
+    T, I, O, E = layer.n_detectors(), 256, 144, 32
+    torch.manual_seed(6)
+    x = torch.rand(B * I, device=dev)
+    out = torch.zeros(B * O, device=dev)
+    li = torch.zeros(B * T, dtype=torch.int32, device=dev)
+    md = torch.zeros(B * T, device=dev)
+    mi = torch.zeros(B * T, dtype=torch.int32, device=dev)
+    dm.forward_step(layer._weights, B, x, layer._detector_anchors, out, li, 0.0,
+                    w_min_anchor_deltas=md, w_min_anchor_delta_indices=mi)
+    g = torch.randn(B * O, device=dev)
+    xg = torch.zeros(B * I, device=dev)
+    W = layer._weights.numel()
+    if int_sums:
+        init = torch.randint(-5000, 5000, (W,), dtype=torch.int32).view(torch.float32)
+    else:
+        init = torch.randn(W)
+    wg = init.clone().to(dev)
+    dm.backward_backprop(layer._weights, B, g, layer._detector_anchors, li, md, mi, xg, -1.0, wg,
+                         overwrite_weights_gradients=overwrite)
+    offs, tg = dm.lookup_connectivity()
+    rt = np.zeros(W, np.float32) if overwrite else init.numpy().copy()
+    oracle.gather_wgrad_sparse(g.cpu().numpy(), li.cpu().numpy(), offs, tg, rt, B, O, T, E,
+                               int_mode=int_sums, int_rescaler=R)
+    if int_sums:
+        oracle.convert_int_to_float(rt, R)
+    assert np.array_equal(wg.cpu().numpy().view(np.int32), rt.view(np.int32))
+
+
 def test_projection_layer_built_on_device(cuda_device):
     """A ProjectionLUTLayer constructed with device=cuda grows its connectivity
     on the host and gives the same layer as one built on the host and moved."""
