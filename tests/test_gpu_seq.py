@@ -189,7 +189,8 @@ def test_seq_two_tiles_wide_rows(oracle, cuda_device):
 def test_seq_attention_layer_shape(oracle, cuda_device):
     # the config-5 attention layer's per-table shape (S = 256, Nc = 6, Npe = 4,
     # 2^10-row sub-tables, O = 256) at a batch and table count the oracle
-    # finishes in seconds: LDS-sliced forward, pair-parallel backward
+    # finishes in seconds: LDS-sliced forward, the grouped backward (one
+    # workgroup per (table, Q, group of 8 K values), k_propagate_seq_grp)
     run_seq(oracle, 2, 256, 64, 4, 6, 4, 256, seed=11)
 
 
