@@ -325,7 +325,6 @@ __global__ __launch_bounds__(kTmThreads) void k_fill_tm(
     const uint32_t col0 = slice * kTmCols;
     const uint32_t q = lane & 7;
     const uint32_t col = col0 + q * 4;
-    const uint32_t emask = n_entries - 1;
     const uint32_t s_loc0 = wave * 8 + (lane >> 3);
 
     double acc[SPT][4];
@@ -361,7 +360,7 @@ __global__ __launch_bounds__(kTmThreads) void k_fill_tm(
             const uint8_t *keys = tb + kTmMaxEntries * 128;
 #pragma unroll
             for (int i = 0; i < SPT; i++) {
-                const uint32_t r = (uint32_t)keys[s_loc0 + kTmPass * i] & emask;
+                const uint32_t r = (uint32_t)keys[s_loc0 + kTmPass * i];  // masked by k_transpose_idx
                 const f32x4 v = *reinterpret_cast<const f32x4 *>(tb + r * 128 + q * 16);
                 acc[i][0] += (double)v.x;
                 acc[i][1] += (double)v.y;
@@ -1061,12 +1060,13 @@ __global__ __launch_bounds__(kScatterThreads) void k_propagate_scatter(
     for (uint32_t i = threadIdx.x; i < n_el; i += kScatterThreads) dst[i] += (float)xg[i];
 }
 
-// keys_t[t][b] = idx[b][t] (u8), through a 64x64 LDS tile.
+// keys_t[t][b] = idx[b][t] & emask (u8), through a 64x64 LDS tile: the rows the
+// forward reads, masked here once instead of once per column slice.
 // idx_t[t][b] (row pitch `pitch` >= batch; samples past the batch get 0).
 __global__ __launch_bounds__(256) void k_transpose_idx(const int32_t *__restrict__ idx,
                                                        uint8_t *__restrict__ idx_t,
                                                        uint32_t batch, uint32_t n_detectors,
-                                                       uint32_t pitch) {
+                                                       uint32_t pitch, uint32_t emask) {
     __shared__ uint8_t tile[64][65];
     const uint32_t tb = blockIdx.x * 64;  // table tile
     const uint32_t bb = blockIdx.y * 64;  // sample tile
@@ -1074,7 +1074,7 @@ __global__ __launch_bounds__(256) void k_transpose_idx(const int32_t *__restrict
     const uint32_t ty = threadIdx.x >> 6;
     for (uint32_t r = ty; r < 64; r += 4) {
         const uint32_t b = bb + r, t = tb + tx;
-        tile[r][tx] = (b < batch && t < n_detectors) ? (uint8_t)idx[(size_t)b * n_detectors + t] : 0;
+        tile[r][tx] = (b < batch && t < n_detectors) ? (uint8_t)((uint32_t)idx[(size_t)b * n_detectors + t] & emask) : 0;
     }
     __syncthreads();
     for (uint32_t r = ty; r < 64; r += 4) {
@@ -1257,7 +1257,7 @@ static hipError_t launch_fill_tm_impl(const FcShape &s, const WT *w, const float
     const uint64_t grid = (uint64_t)n_parts * n_chunks * n_slices;
     if (grid > 0x7fffffffu) return hipErrorInvalidConfiguration;
     hipLaunchKernelGGL(k_transpose_idx, dim3((s.n_detectors + 63) / 64, (ipitch + 63) / 64),
-                       dim3(256), 0, st, idx, idx_t, s.batch, s.n_detectors, ipitch);
+                       dim3(256), 0, st, idx, idx_t, s.batch, s.n_detectors, ipitch, s.n_entries - 1);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (dma) {
