@@ -279,6 +279,18 @@ def bench_projection(args):
         step()
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    # the same eager step with the backward run on the calling thread instead
+    # of the device's autograd worker thread (a PyTorch switch; same kernels)
+    with torch.autograd.set_multithreading_enabled(False):
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        ms_one_thread = (time.perf_counter() - t0) * 1e3 / args.steps
+    log(f"backward on the calling thread: {ms_one_thread:.3f} ms/step")
     # per-family times in a separate pass: the events around each of the
     # stack's 15 launches would otherwise weigh on a sub-millisecond step
     dms = [l1._lut_dm, l2._lut_dm, head._lut_dm]
@@ -312,6 +324,11 @@ def bench_projection(args):
                    "layer1": "28x28 -> 48x48, 144 groups x 32 tables, 5 pairs, 5x5 fields, 16 targets",
                    "layer2": "48x48 -> 20x40, 25 groups x 64 tables, 6 pairs, 12x12 fields, 32 targets",
                    "head": "800 -> 10, 128 tables, 6 pairs", "parallelism": "single GPU"},
+        "eager_backward_on_calling_thread": {
+            "ms_per_step": round(ms_one_thread, 4), "value": round(B / (ms_one_thread / 1e3), 1),
+            "unit": "samples/s",
+            "note": "the eager step under torch.autograd.set_multithreading_enabled(False): the host-bound "
+                    "step saves the hand-over to the device's autograd thread"},
         "graph_replay": {"ms_per_step": round(graph_ms, 4), "value": round(B / (graph_ms / 1e3), 1),
                          "unit": "samples/s",
                          "note": "the same step captured once in a HIP graph (torch.cuda.CUDAGraph) and "

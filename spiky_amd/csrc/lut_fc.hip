@@ -107,7 +107,9 @@ __global__ __launch_bounds__(kBlock) void k_check_detectors(
 // A thread owns one table: it loads the table's anchor pairs once and
 // evaluates them for every staged sample, so the anchor reads are shared by
 // spb samples and the 2 * n_anchors input reads per (sample, table) are LDS
-// reads instead of dependent global loads.
+// reads instead of dependent global loads.  A workgroup walks `rounds`
+// consecutive sample groups with the same anchors in registers, staging each
+// group's rows in turn.
 constexpr int kCheckMaxAnchors = 16;
 constexpr uint32_t kCheckLdsBytes = 64 * 1024;
 
@@ -116,34 +118,23 @@ __global__ __launch_bounds__(1024) void k_check_detectors_lds(
     const float *__restrict__ x, const int2 *__restrict__ anchors, uint32_t batch,
     uint32_t n_inputs, uint32_t n_detectors, uint32_t n_anchors, uint32_t spb, float cmp_eps,
     int32_t *__restrict__ idx, float *__restrict__ md, int32_t *__restrict__ mi, uint32_t gx,
-    uint32_t gy) {
+    uint32_t gy, uint32_t rounds) {
     extern __shared__ float xs[];
-    // the gx table blocks of one sample group run on one XCD (workgroup i runs
-    // on XCD i % 8, consecutively there), so the group's x rows are fetched from
-    // HBM once and then served by that XCD's L2
+    // the gx table blocks of one run of sample groups run on one XCD
+    // (workgroup i runs on XCD i % 8, consecutively there), so each group's x
+    // rows are fetched from HBM once and then served by that XCD's L2
     const uint32_t wl = blockIdx.x;
-    const uint32_t gyb = (wl % 8u) + 8u * (wl / (8u * gx));
+    const uint32_t run = (wl % 8u) + 8u * (wl / (8u * gx));
     const uint32_t gxb = (wl / 8u) % gx;
-    if (gyb >= gy) return;  // uniform over the workgroup
-    const uint32_t b0 = gyb * spb;
-    const uint32_t nb = min(spb, batch - b0);
-    const uint32_t n_el = nb * n_inputs;
-    const float *src = x + (size_t)b0 * n_inputs;
-    if ((n_el & 3u) == 0 && (reinterpret_cast<uintptr_t>(src) & 15u) == 0) {
-        const float4 *s4 = reinterpret_cast<const float4 *>(src);
-        float4 *d4 = reinterpret_cast<float4 *>(xs);
-        for (uint32_t i = threadIdx.x; i < n_el / 4; i += blockDim.x) d4[i] = s4[i];
-    } else {
-        for (uint32_t i = threadIdx.x; i < n_el; i += blockDim.x) xs[i] = src[i];
-    }
-    __syncthreads();
+    const uint32_t g0 = run * rounds;
+    if (g0 >= gy) return;  // uniform over the workgroup
     const uint32_t t = gxb * blockDim.x + threadIdx.x;
-    if (t >= n_detectors) return;
+    const bool active = t < n_detectors;
     // the table's pairs in registers (fully unrolled, compile-time indices);
     // pairs past n_anchors or with an input id outside [0, n_inputs) are
     // skipped, marked by x = -1
     int2 a[NA];
-    const int2 *ap = anchors + (size_t)t * n_anchors;
+    const int2 *ap = anchors + (size_t)(active ? t : 0) * n_anchors;
 #pragma unroll
     for (int k = 0; k < NA; k++) {
         int2 v = make_int2(-1, -1);
@@ -151,29 +142,47 @@ __global__ __launch_bounds__(1024) void k_check_detectors_lds(
         if ((uint32_t)v.x >= n_inputs || (uint32_t)v.y >= n_inputs) v = make_int2(-1, -1);
         a[k] = v;
     }
-    for (uint32_t sl = 0; sl < nb; sl++) {
-        const float *xr = xs + sl * n_inputs;
-        int32_t li = 0;
-        float mind = 0.0f;
-        int32_t mink = -1;
+    const uint32_t g1 = min(g0 + rounds, gy);
+    for (uint32_t gyb = g0; gyb < g1; gyb++) {
+        const uint32_t b0 = gyb * spb;
+        const uint32_t nb = min(spb, batch - b0);
+        const uint32_t n_el = nb * n_inputs;
+        const float *src = x + (size_t)b0 * n_inputs;
+        // every thread is done with the previous group's rows
+        if (gyb != g0) __syncthreads();
+        if ((n_el & 3u) == 0 && (reinterpret_cast<uintptr_t>(src) & 15u) == 0) {
+            const float4 *s4 = reinterpret_cast<const float4 *>(src);
+            float4 *d4 = reinterpret_cast<float4 *>(xs);
+            for (uint32_t i = threadIdx.x; i < n_el / 4; i += blockDim.x) d4[i] = s4[i];
+        } else {
+            for (uint32_t i = threadIdx.x; i < n_el; i += blockDim.x) xs[i] = src[i];
+        }
+        __syncthreads();
+        if (!active) continue;
+        for (uint32_t sl = 0; sl < nb; sl++) {
+            const float *xr = xs + sl * n_inputs;
+            int32_t li = 0;
+            float mind = 0.0f;
+            int32_t mink = -1;
 #pragma unroll
-        for (int k = 0; k < NA; k++) {
-            if (a[k].x >= 0) {
-                const float d = xr[a[k].x] - xr[a[k].y];
-                if (rounded_greater0(d, cmp_eps)) li |= (1 << k);
-                if (TRAIN) {
-                    if (mink == -1 || fabsf(d) < fabsf(mind)) {
-                        mind = d;
-                        mink = (int32_t)k;
+            for (int k = 0; k < NA; k++) {
+                if (a[k].x >= 0) {
+                    const float d = xr[a[k].x] - xr[a[k].y];
+                    if (rounded_greater0(d, cmp_eps)) li |= (1 << k);
+                    if (TRAIN) {
+                        if (mink == -1 || fabsf(d) < fabsf(mind)) {
+                            mind = d;
+                            mink = (int32_t)k;
+                        }
                     }
                 }
             }
-        }
-        const size_t o = (size_t)(b0 + sl) * n_detectors + t;
-        idx[o] = li;
-        if (TRAIN) {
-            md[o] = mind;
-            mi[o] = mink;
+            const size_t o = (size_t)(b0 + sl) * n_detectors + t;
+            idx[o] = li;
+            if (TRAIN) {
+                md[o] = mind;
+                mi[o] = mink;
+            }
         }
     }
 }
@@ -995,13 +1004,16 @@ hipError_t launch_check_detectors(const FcShape &s, const float *x, const int32_
         const uint64_t want = std::max<uint64_t>(1, (uint64_t)s.batch * gx / 512);
         const uint32_t spb = (uint32_t)std::min<uint64_t>({(uint64_t)spb_lds, want, 16});
         const uint32_t gy = (s.batch + spb - 1) / spb;
-        const uint64_t grid = 8ull * gx * ((gy + 7) / 8);
+        // sample groups a workgroup walks: enough to leave ~512 workgroups
+        const uint32_t rounds = (uint32_t)std::max<uint64_t>(1, (uint64_t)gy * gx / 512);
+        const uint32_t runs = (gy + rounds - 1) / rounds;
+        const uint64_t grid = 8ull * gx * ((runs + 7) / 8);
         if (grid > 0x7fffffffull) return hipErrorInvalidConfiguration;
         const size_t lds = (size_t)spb * s.n_inputs * sizeof(float);
 #define SPIKY_CHK(TR, NA)                                                                       \
     hipLaunchKernelGGL((k_check_detectors_lds<TR, NA>), dim3((uint32_t)grid), dim3(threads), lds, st, x, \
                        ap, s.batch, s.n_inputs, s.n_detectors, s.n_anchors, spb, cmp_eps, idx,   \
-                       min_deltas, min_idx, gx, gy)
+                       min_deltas, min_idx, gx, gy, rounds)
         if (min_deltas) {
             if (s.n_anchors <= 8) SPIKY_CHK(true, 8); else SPIKY_CHK(true, 16);
         } else {
