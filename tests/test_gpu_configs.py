@@ -289,3 +289,37 @@ def test_nan_inputs(oracle, cuda_device, B):
     assert np.array_equal(gmd[~np.isnan(rmd)], rmd[~np.isnan(rmd)])
     assert np.array_equal(mi.cpu().numpy(), rmi)
     assert np.array_equal(out.cpu().numpy(), oracle.fill_outputs_fc(W.numpy(), ridx, B, O, T, 1 << Nc))
+
+
+@pytest.mark.parametrize("Nc,train", [(8, True), (12, False)])
+def test_check_runs_of_sample_groups(oracle, cuda_device, Nc, train):
+    """The detector check's workgroups each walk a run of sample groups (here
+    4-sample groups, two a run, 750 groups): a partial last group (B = 2999),
+    runs past the last group that do nothing, both anchor-register widths, in
+    training (margins and their indices) and in evaluation.  Indices, margins
+    and margin indices bit-exact against the oracle."""
+    from spiky_amd import LUTDataManagerF
+    dev = cuda_device
+    B, I, T, O = 2999, 4096, 2048, 32
+    E = 1 << Nc
+    g = torch.Generator().manual_seed(23)
+    x = torch.randn(B * I, generator=g)
+    anchors = torch.stack([torch.randperm(I, generator=g)[:2] for _ in range(T * Nc)]).to(torch.int32).flatten()
+    dm = LUTDataManagerF(I, O, T, Nc, 1, 0, 0, 32, 32)
+    dm.register_synapse_meta(1.0, -1.0, 1.0, 0.0, 0.0)
+    dm.initialize_neurons(True)
+    dm.to_device(0)
+    W = torch.zeros(T * E * O, device=dev)
+    out = torch.zeros(B * O, device=dev)
+    idx = torch.empty(B * T, dtype=torch.int32, device=dev)
+    md = torch.empty(B * T, device=dev) if train else None
+    mi = torch.empty(B * T, dtype=torch.int32, device=dev) if train else None
+    print(f"[check runs] B={B} I={I} T={T} Nc={Nc} train={train}", flush=True)
+    dm.forward_step(W, B, x.to(dev), anchors.to(dev), out, idx, 0.0, None, md, mi)
+    torch.cuda.synchronize()
+    res = oracle.check_detectors(x.numpy(), anchors.numpy(), B, I, T, Nc, train=train)
+    ridx = res[0] if train else res
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    if train:
+        assert np.array_equal(md.cpu().numpy(), res[1])
+        assert np.array_equal(mi.cpu().numpy(), res[2])
