@@ -55,7 +55,7 @@ def xg_close(gpu, cpu, B, I, T=8192, n_ob=32):
 
 
 def run_fc(oracle, B, I, T, Nc, O, fgs=32, bgs=32, cmp_eps=0.0, seed=0, int_rescaler=None, lr=1.0,
-           edit_grad=None):
+           edit_grad=None, wg_exact=True):
     dev = torch.device("cuda:0")
     E = 1 << Nc
     int_mode = int_rescaler is not None
@@ -105,8 +105,18 @@ def run_fc(oracle, B, I, T, Nc, O, fgs=32, bgs=32, cmp_eps=0.0, seed=0, int_resc
     else:
         xg_close(xg.cpu().numpy(), rxg, B, I, T, n_ob)
         xg_close(xg2.cpu().numpy(), rxg, B, I, T, n_ob)
-    assert np.array_equal(wg.cpu().numpy(), rwg)
-    assert np.array_equal(wg_acc.cpu().numpy(), rwg)
+    if wg_exact:
+        assert np.array_equal(wg.cpu().numpy(), rwg)
+        assert np.array_equal(wg_acc.cpu().numpy(), rwg)
+    else:
+        # fp32 sums committed with atomics in any order: within B * 2^-24 of
+        # the sum of the terms' magnitudes (the oracle's own sum of |g * lr|)
+        rabs = np.zeros(T * E * O, np.float32)
+        oracle.gather_wgrad_fc(np.abs(gn), ridx, rabs, B, O, T, E, ogs=fgs, first_meta_lr=lr)
+        bound = B * 2.0 ** -24 * rabs.astype(np.float64) * 1.01
+        for got in (wg, wg_acc):
+            err = np.abs(got.cpu().numpy().astype(np.float64) - rwg)
+            assert np.all(err <= bound), f"max excess {np.max(err - bound)}"
 
 
 def test_config1_full(oracle, cuda_device):
@@ -197,6 +207,16 @@ def test_unusual_group_sizes(oracle, cuda_device):
 
 def test_wide_outputs_and_eps(oracle, cuda_device):
     run_fc(oracle, 5, 64, 40, 3, 1536, seed=3, cmp_eps=0.05)
+
+
+@pytest.mark.parametrize("Nc,int_rescaler", [(10, None), (10, 0.5), (13, None), (13, 0.5)])
+def test_many_entries(oracle, cuda_device, Nc, int_rescaler):
+    """Tables of 2^10 and 2^13 rows (16-pair anchor registers in the check, the
+    per-sample forward).  Up to 4096 rows the weight gradient is the bucketed
+    walk (bit-exact); past it, the atomic form, whose fp32 sums are order-free
+    as the reference GPU path's are (int32 sums stay bit-exact)."""
+    run_fc(oracle, 70, 200, 6, Nc, 48, seed=31, int_rescaler=int_rescaler,
+           wg_exact=Nc <= 12 or int_rescaler is not None)
 
 
 def test_single_sample_single_table(oracle, cuda_device):
