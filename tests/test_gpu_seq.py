@@ -330,3 +330,17 @@ def test_seq_layer_autograd(oracle, cuda_device):
     rwg = np.zeros(Wn.size, np.float32)
     oracle.gather_wgrad_seq(gn, ridx, rpli, rwg, B, O, T, S, Nc, Npe)
     assert np.array_equal(layer._weights.grad.cpu().numpy(), rwg)
+
+
+def test_seq_degenerate_anchors_int32(oracle, cuda_device):
+    """Explicit anchors drawn with repetition, a quarter comparing an input with
+    itself (Δ = 0 on both sides of the concatenation: bit 0, and the two pushes
+    of the min-margin pair cancel), in int32 summation, where every output and
+    gradient is bit-exact whatever the order of the pushes."""
+    B, S, I, T, Nc, Npe, O = 2, 20, 12, 4, 3, 2, 32
+    x, anchors, W, pe, go = seq_inputs(51, B, S, I, T, Nc, Npe, O)
+    g = torch.Generator().manual_seed(52)
+    a = torch.randint(0, I, (T * Nc, 2), generator=g, dtype=torch.int32)
+    a[::4, 1] = a[::4, 0]
+    run_seq(oracle, B, S, I, T, Nc, Npe, O, int_rescaler=0.5,
+            inputs=(x, a.flatten().contiguous(), W, pe, go))
