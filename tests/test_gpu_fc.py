@@ -244,6 +244,15 @@ def test_degenerate_anchor_pairs(oracle, cuda_device, int_rescaler):
                xg_extra=2 * 40 * 40 * 2.0 ** -24)
 
 
+def test_check_without_lds_staging(oracle, cuda_device):
+    """The detector check's other kernel: rows past 16384 inputs (no four-sample
+    group fits the LDS) and tables past 16 pairs (2^17 rows; their weight
+    gradient is the atomic form)."""
+    run_fc(oracle, 5, 20000, 3, 4, 8, seed=61)
+    run_fc(oracle, 6, 64, 2, 17, 4, seed=62, wg_exact=False)
+    run_fc(oracle, 6, 64, 2, 17, 4, seed=63, int_rescaler=0.5)
+
+
 def test_single_sample_single_table(oracle, cuda_device):
     run_fc(oracle, 1, 2, 1, 1, 1, seed=4)
 
