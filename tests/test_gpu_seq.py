@@ -344,3 +344,16 @@ def test_seq_degenerate_anchors_int32(oracle, cuda_device):
     a[::4, 1] = a[::4, 0]
     run_seq(oracle, B, S, I, T, Nc, Npe, O, int_rescaler=0.5,
             inputs=(x, a.flatten().contiguous(), W, pe, go))
+
+
+@pytest.mark.parametrize("int_rescaler", [None, 0.5])
+def test_seq_shortest_sequences(oracle, cuda_device, int_rescaler):
+    """S = 2 and 3: one and three causal pairs a sequence, a single distance."""
+    run_seq(oracle, 4, 2, 8, 3, 2, 1, 16, seed=70, int_rescaler=int_rescaler)
+    run_seq(oracle, 3, 3, 8, 3, 2, 1, 64, seed=71, int_rescaler=int_rescaler)
+
+
+def test_seq_past_the_grouped_propagate(oracle, cuda_device):
+    """S = 520, past the 513 positions the grouped input-gradient pass takes:
+    the pair-parallel form, with its Q-flip pass and triangle reduction."""
+    run_seq(oracle, 1, 520, 16, 2, 3, 3, 64, seed=72)
