@@ -253,6 +253,15 @@ def test_check_without_lds_staging(oracle, cuda_device):
     run_fc(oracle, 6, 64, 2, 17, 4, seed=63, int_rescaler=0.5)
 
 
+@pytest.mark.parametrize("int_rescaler", [None, 0.5])
+def test_large_batch_odd_outputs(oracle, cuda_device, int_rescaler):
+    """A batch past 256 with 10 and 66 outputs (not whole 4-column pieces: the
+    table-major kernels do not take it) and a batch of exactly 256 with 64."""
+    run_fc(oracle, 300, 50, 30, 5, 10, seed=81, int_rescaler=int_rescaler)
+    run_fc(oracle, 260, 50, 30, 5, 66, seed=82, int_rescaler=int_rescaler)
+    run_fc(oracle, 256, 50, 30, 5, 64, seed=83, int_rescaler=int_rescaler)
+
+
 def test_single_sample_single_table(oracle, cuda_device):
     run_fc(oracle, 1, 2, 1, 1, 1, seed=4)
 
