@@ -316,7 +316,7 @@ def test_internal_policy_sgd(oracle, cuda_device):
     assert np.array_equal(Wd.cpu().numpy(), rW)
 
 
-@pytest.mark.parametrize("B,O", [(12, 128), (517, 1024)])
+@pytest.mark.parametrize("B,O", [(12, 128), (517, 1024), (300, 100), (300, 66)])
 def test_int8_tables(oracle, cuda_device, B, O):
     dev = cuda_device
     I, T, Nc = 256, 96, 6
